@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""bench.py -- measure quantibbler-kernels' hot paths on one MI355X.
+
+Headline (BASELINE.json metric, configs[0] shape): the binary-factor linear
+decode GEMV, y = s1 . (Ub (Vb^T (s2 . x))), m = n = 4096, r = 1024, batch 1,
+bf16 x and y, f32 accumulation, over a rotation of distinct layers (default
+512, 562 MB of weights: larger than the 256 MB Infinity Cache, so HBM is what
+is measured).  One step = one decode of every layer in the set: two
+launches (stage 1: t = bf16(Vb^T bf16(s2*x)); stage 2: y = bf16(bf16(Ub t)*s1)).
+
+value = algorithmic bytes of all layers / step time, with the BASELINE.md
+per-layer count 1,097,728 B (U 512 KiB + V 512 KiB + x 8 KiB + y 8 KiB + s1,
+s2 32 KiB); each stage kernel accounts for half (548,864 B per layer).
+Stage durations come from HIP events recorded on the launch stream around
+each launch inside the timed region.
+
+Extras (same JSON line): single-layer decode latency; prefill GEMM TFLOP/s at
+B in {16, 128, 512, 2048}; block-scaled SageAttention prefill at
+B=1, H=32, S=4096, d=128, causal; and the CPU baseline: the
+oracle's C restatement of the reference fast face (fast.rs, f64, OpenMP over
+64-row blocks) timed on the host on a bounded sample of the decode workload.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--layers 512]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12          # B/s
+BF16_PEAK = 2.5e15         # dense FLOP/s
+INT8_PEAK = 5.0e15         # dense OP/s
+LAYER_BYTES = 1_097_728    # BASELINE.md config 1, per layer
+STAGE_BYTES = LAYER_BYTES // 2
+M = N = 4096
+R = 1024
+METRIC = "factor-linear GB/s & %HBM peak (B=1); GEMM+SageAttn TFLOP/s & %MFMA peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_layers(qa, ctx, np, count, seed):
+    rng = np.random.default_rng(seed)
+    layers, host = [], []
+    for i in range(count):
+        ub = rng.integers(0, 256, (M, R // 8), dtype=np.uint8)
+        vt = rng.integers(0, 256, (R, N // 8), dtype=np.uint8)
+        s1 = np.exp(0.5 * rng.standard_normal(M)).astype(np.float32)
+        s2 = np.exp(0.5 * rng.standard_normal(N)).astype(np.float32)
+        layers.append(qa.FactorLayer.from_rows(ctx, M, N, R, ub, vt, s1, s2, None))
+        if i < 16:
+            host.append((ub, vt, s1, s2))
+        if (i + 1) % 128 == 0:
+            log(f"  uploaded {i + 1}/{count} layers")
+    return layers, host
+
+
+def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
+    S = qa.FactorSet(ctx, layers)
+    L = len(layers)
+    rng = np.random.default_rng(7)
+    xh = rng.standard_normal((L, N)).astype(np.float32)
+    x = torch.from_numpy(xh).to("cuda").to(torch.bfloat16)
+    y = torch.empty((L, M), dtype=torch.bfloat16, device="cuda")
+    ws_n = S.workspace_size()
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream()
+    for _ in range(warmup):
+        S.stage_dev(1, x, y, ws, ws_n, st)
+        S.stage_dev(2, x, y, ws, ws_n, st)
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(st)
+    for k in range(steps):
+        ev[k][0].record(st)
+        S.stage_dev(1, x, y, ws, ws_n, st)
+        ev[k][1].record(st)
+        S.stage_dev(2, x, y, ws, ws_n, st)
+        ev[k][2].record(st)
+    end.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(end) / steps
+    s1 = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    s2 = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    return dict(ms_per_step=ms_step, stage1_ms=s1, stage2_ms=s2, wall_s=wall, set=S)
+
+
+def bench_single_latency(torch, np, layer, iters=200):
+    x = torch.randn((1, N), device="cuda").to(torch.bfloat16)
+    y = torch.empty((1, M), dtype=torch.bfloat16, device="cuda")
+    ws_n = layer.workspace_size(1)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream()
+    for _ in range(20):
+        layer.linear_dev(x, 1, y, "bfloat16", ws, ws_n, st)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(iters):
+        layer.linear_dev(x, 1, y, "bfloat16", ws, ws_n, st)
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters * 1e3  # us
+
+
+def bench_gemm(torch, np, layer, batches=(16, 128, 512, 2048), iters=20):
+    out = {}
+    st = torch.cuda.current_stream()
+    for B in batches:
+        x = torch.randn((B, N), device="cuda").to(torch.bfloat16)
+        y = torch.empty((B, M), dtype=torch.bfloat16, device="cuda")
+        ws_n = layer.workspace_size(B)
+        ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+        for _ in range(3):
+            layer.linear_dev(x, B, y, "bfloat16", ws, ws_n, st)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(iters):
+            layer.linear_dev(x, B, y, "bfloat16", ws, ws_n, st)
+        b.record(st)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / iters
+        flop = 2.0 * B * R * (M + N)
+        tf = flop / (ms * 1e-3) / 1e12
+        out[str(B)] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_bf16_peak": round(tf * 1e12 / BF16_PEAK, 4)}
+        log(f"  gemm B={B}: {ms:.3f} ms  {tf:.1f} TFLOP/s")
+    return out
+
+
+def bench_sage(qa, ctx, torch, np, iters=10):
+    B, H, S, D = 1, 32, 4096, 128
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn((B, H, S, D), device="cuda", generator=g).to(torch.bfloat16)
+    k = (torch.randn((B, H, S, D), device="cuda", generator=g)
+         + 2.0 * torch.randn((B, H, 1, D), device="cuda", generator=g)).to(torch.bfloat16)
+    v = torch.randn((B, H, S, D), device="cuda", generator=g).to(torch.bfloat16)
+    o = torch.empty((B, H, S, D), dtype=torch.bfloat16, device="cuda")
+    shape = qa.AttentionShape(B, H, H, S, S, D, D)
+    ws_n = ctx.sage_blk_workspace_size(shape)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream()
+    for _ in range(3):
+        ctx.attention_sage_blk_dev(shape, q, k, v, True, o, ws, ws_n, st)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(iters):
+        ctx.attention_sage_blk_dev(shape, q, k, v, True, o, ws, ws_n, st)
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / iters
+    qk_ops = 2.0 * H * S * S * D / 2      # causal lower triangle, int8
+    pv_flops = 2.0 * H * S * S * D / 2    # fp16
+    blended_peak = (qk_ops + pv_flops) / (qk_ops / INT8_PEAK + pv_flops / BF16_PEAK)
+    tops = (qk_ops + pv_flops) / (ms * 1e-3)
+    log(f"  sage blk cfg4: {ms:.3f} ms  {tops / 1e12:.1f} TOPS blended")
+    return {"ms": round(ms, 4), "tops_blended": round(tops / 1e12, 2),
+            "frac_blended_peak": round(tops / blended_peak, 4),
+            "blended_peak_tops": round(blended_peak / 1e12, 1),
+            "shape": "B=1 H=32 S=4096 d=128 causal, bf16 in/out, includes the quantisation pre-pass"}
+
+
+def bench_cpu(np, host, budget_s=10.0):
+    from oracle import oracle as orc
+
+    orc.build()
+    threads = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(N).astype(np.float32)
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        ub, vt, s1, s2 = host[calls % len(host)]
+        orc.factor_apply("fp32", M, N, R, ub, vt, s1, s2, None, x, fast=True, threads=threads)
+        calls += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(calls * LAYER_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{calls} decode calls of config-1 layers (m=n=4096, r=1024, B=1) cycling "
+                      f"{len(host)} distinct layers in {dt:.1f} s: the oracle's C restatement of the "
+                      "reference fast face (fast.rs:28-110, f64, 64-row blocks, OpenMP) inside "
+                      "PackedLayer::apply (engine/mod.rs:393-437)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=512)
+    ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path's multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import quantibbler_amd as qa
+
+    ctx = qa.GpuContext(0)
+    log(f"building {args.layers} config-1 layers ...")
+    layers, host = make_layers(qa, ctx, np, args.layers, seed=1)
+    log("decode sweep ...")
+    d = bench_decode(qa, ctx, torch, np, layers, args.steps, args.warmup)
+    total_bytes = args.layers * LAYER_BYTES
+    value = total_bytes / (d["ms_per_step"] * 1e-3) / 1e9
+    dom = 1 if d["stage1_ms"] >= d["stage2_ms"] else 2
+    dom_ms = d["stage1_ms"] if dom == 1 else d["stage2_ms"]
+    achieved = args.layers * STAGE_BYTES / (dom_ms * 1e-3) / 1e9
+    log(f"  decode: {d['ms_per_step']:.3f} ms/step, {value:.1f} GB/s; stage1 {d['stage1_ms']:.3f} ms, "
+        f"stage2 {d['stage2_ms']:.3f} ms")
+    extra = {"decode_stage_ms": {"stage1": round(d["stage1_ms"], 4), "stage2": round(d["stage2_ms"], 4)}}
+    if not args.no_extra:
+        log("single-layer latency ...")
+        extra["decode_single_layer_us"] = round(bench_single_latency(torch, np, layers[0]), 2)
+        log("prefill GEMM ...")
+        extra["prefill_gemm"] = bench_gemm(torch, np, layers[0])
+        log("sage attention ...")
+        extra["sage_blk"] = bench_sage(qa, ctx, torch, np)
+    log("cpu baseline ...")
+    cpu = bench_cpu(np, host, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"decode GEMV (batch 1) over {args.layers} distinct config-1 factor layers "
+                        "(m=n=4096, r=1024, +-1 Bernoulli(0.5) signs, lognormal(0,0.5) fp32 scales, "
+                        "bf16 N(0,1) x), one launch per stage for the whole set",
+            "layers": args.layers, "m": M, "n": N, "r": R, "batch": 1,
+            "weight_bytes": args.layers * (M * R + N * R) // 8,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": None,
+            "kernel": f"gemv_kernel<{dom},false> (stage {dom})",
+            "bytes_per_launch": args.layers * STAGE_BYTES, "avg_launch_ms": round(dom_ms, 4),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

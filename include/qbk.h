@@ -1,0 +1,198 @@
+/*
+ * qbk.h -- C ABI of libqbk, the MI355X (gfx950) implementation of the two
+ * quantibbler-kernels hot paths:
+ *
+ *   1. the binary latent-factor linear  y = s1 . (Ub (Vb^T (s2 . x))) + b
+ *      over 1-bit sign matrices (decode GEMV and prefill GEMM), and
+ *   2. SageAttention (INT8 Q.K^T, online softmax, tiled P.V).
+ *
+ * Every entry point names the reference interface it replaces
+ * (donicrosby/quantibbler, file:line).  Plain pointers and sizes only.
+ *
+ * Conventions
+ *   - Return value: QBK_OK (0) or a QBK_ERR_* code.  On error nothing is
+ *     written to the outputs and qbk_last_error() returns the message; for
+ *     validation errors that text is the reference's KernelError text
+ *     (core.rs, gpu.rs, gpu_attention.rs) verbatim.
+ *   - "host" entry points take host buffers and block until the result is in
+ *     the output buffer (GpuContext semantics: copy in, launch, copy out).
+ *   - "_dev" entry points take device pointers, enqueue on `stream` (a
+ *     hipStream_t, NULL = the null stream) and return without waiting.
+ *   - bf16 values cross as uint16_t bit patterns (lib.rs:245-261).
+ *   - A qbk_ctx may be shared by threads; calls are independent (each host
+ *     call uses its own stream and buffers; device calls use the caller's).
+ */
+#ifndef QBK_H
+#define QBK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    QBK_OK = 0,
+    QBK_ERR_VALIDATION = 1, /* core::KernelError from input validation      */
+    QBK_ERR_DEVICE = 2,     /* a HIP call failed (per-call device error)     */
+    QBK_ERR_INIT = 3        /* no usable device (gpu.rs GPU_INIT_HINT)       */
+};
+
+/* Dense operand dtype tag: dtype.rs:93-130 Dtype {F64, F32, Bf16}. */
+enum { QBK_F64 = 0, QBK_F32 = 1, QBK_BF16 = 2 };
+
+typedef struct qbk_ctx qbk_ctx;
+typedef struct qbk_factor qbk_factor;
+
+/* ---- meta ---------------------------------------------------------------- */
+
+/* lib.rs:94-97 backend_version() */
+const char *qbk_backend_version(void);
+/* Message of the calling thread's last failed call (core.rs:31 KernelError). */
+const char *qbk_last_error(void);
+/* dtype.rs:110-119 Dtype::from_name: "float64" | "float32" | "bfloat16";
+ * an unknown name is refused, naming the value. */
+int qbk_dtype_from_name(const char *name, int *dtype_out);
+
+/* ---- host-side bit layout (core.rs) --------------------------------------- */
+
+/* core.rs:129-162 pack_bits: +-1 factor (n_rows x n_cols, row-major) ->
+ * n_rows x ceil(n_cols/8) bytes, LSB-first, +1 -> 1, pad bits 0. */
+int qbk_pack_bits(const int8_t *factor, size_t factor_len, size_t n_rows, size_t n_cols,
+                  uint8_t *out);
+/* core.rs:166-189 unpack_bits: pad bits ignored. */
+int qbk_unpack_bits(const uint8_t *packed, size_t packed_len, size_t n_rows, size_t n_bits,
+                    int8_t *out);
+/* core.rs:223-240 validate_packed; *n_words = ceil(n_bits/8). */
+int qbk_validate_packed(size_t packed_len, size_t n_rows, size_t n_bits, size_t *n_words);
+/* core.rs sign_estimate: x >= 0 (incl. -0.0) -> +1, else -1. */
+void qbk_sign_estimate(const double *x, size_t n, int8_t *out);
+
+/* ---- device context (gpu.rs:76-189 GpuContext) --------------------------- */
+
+/* gpu.rs:85-101 GpuContext::init_at(device_index); failure -> QBK_ERR_INIT
+ * with the GPU_INIT_HINT-style message. */
+int qbk_ctx_create(int device_index, qbk_ctx **out);
+void qbk_ctx_destroy(qbk_ctx *ctx);
+/* gpu.rs:187-189 gpu_available() */
+int qbk_gpu_available(void);
+
+/* ---- packed products ------------------------------------------------------ */
+
+/* gpu.rs:116-185 GpuContext::packed_matvec generalised to the three dtypes of
+ * dispatch.rs:81-92 packed_matvec_dyn.  out[i] = sum_k s(i,k) vec[k] in the
+ * dtype's accumulator (f64, f32, f32 for bf16), summed in element order, so
+ * results are bit-identical to core::packed_matvec. */
+int qbk_packed_matvec(qbk_ctx *ctx, int dtype, const uint8_t *packed, size_t packed_len,
+                      size_t n_rows, size_t n_bits, const void *vec, size_t vec_len, void *out);
+/* dispatch.rs:95-109 packed_matmul_dyn / core.rs:288-317: output n_rows x k,
+ * k = mat_len / max(n_bits,1), element (i,j) = sum_t s(i,t) mat[t*n_cols + j]
+ * in element order.  An n_cols that would index past mat_len is a
+ * validation error (the reference would panic). */
+int qbk_packed_matmul(qbk_ctx *ctx, int dtype, const uint8_t *packed, size_t packed_len,
+                      size_t n_rows, size_t n_bits, const void *mat, size_t mat_len,
+                      size_t n_cols, void *out);
+/* Device-pointer forms of the two above (same arithmetic); k_cols = output
+ * width.  packed is n_rows x ceil(n_bits/8) bytes. */
+int qbk_packed_matvec_dev(qbk_ctx *ctx, int dtype, const uint8_t *packed, size_t n_rows,
+                          size_t n_bits, const void *vec, void *out, void *stream);
+int qbk_packed_matmul_dev(qbk_ctx *ctx, int dtype, const uint8_t *packed, size_t n_rows,
+                          size_t n_bits, const void *mat, size_t k_cols, size_t n_cols, void *out,
+                          void *stream);
+
+/* ---- binary factor linear (engine/mod.rs:313-481 PackedLayer) ------------ */
+
+/* Upload one qpk1 layer stream (quantibbler-qpk1 lib.rs:229-320 parse; v1 or
+ * v2, f16 or f32 scales) and repack it once into the device layout
+ * (engine/mod.rs:342-381 PackedLayer::from_layer).  Parse errors carry the
+ * reference's text. */
+int qbk_factor_from_qpk1(qbk_ctx *ctx, const uint8_t *stream, size_t len, qbk_factor **out);
+/* Same, from the engine's per-row bitplanes (engine/mod.rs:313-340 fields):
+ * ub_rows = dout x ceil(r/8), vb_t_rows = r x ceil(din/8); bias may be NULL
+ * (a legacy v1 layer: the zero map). */
+int qbk_factor_from_rows(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const uint8_t *ub_rows,
+                         const uint8_t *vb_t_rows, const float *s1, const float *s2,
+                         const float *bias, qbk_factor **out);
+void qbk_factor_destroy(qbk_factor *layer);
+int qbk_factor_dims(const qbk_factor *layer, size_t *dout, size_t *din, size_t *r);
+/* Bytes of device workspace qbk_factor_linear_dev needs at this batch. */
+size_t qbk_factor_workspace_size(const qbk_factor *layer, size_t batch);
+/* Device factor linear over `batch` tokens (the bf16 serving composite,
+ * engine/mod.rs:449-460 apply_bf16, batched):
+ *   z = bf16(s2*x); t = bf16(Vb^T z); u = bf16(Ub t); y = f32(u)*s1 + b
+ * x: bf16 [batch][din] (token-major); y: [batch][dout] as f32 (y_dtype
+ * QBK_F32) or bf16 (QBK_BF16, one more RNE).  batch == 1 runs the decode
+ * GEMV, larger batches the MFMA GEMM.  Accumulation is f32. */
+int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *layer, const uint16_t *x, size_t batch,
+                          void *y, int y_dtype, void *workspace, size_t workspace_size,
+                          void *stream);
+/* Host form of PackedLayer::apply / apply_bf16 (engine/mod.rs:393-460) on
+ * the device: x f32 [batch][din] -> y f32 [batch][dout].  serving QBK_BF16 is
+ * apply_bf16's composite; serving QBK_F32 is apply's (f64 matvecs). */
+int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *layer, int serving, const float *x,
+                     size_t batch, float *y);
+
+/* A set of layers of one shape decoded together, one launch per stage for
+ * the whole set (independent projections such as q/k/v, or every layer of
+ * a bandwidth sweep).  The set keeps device descriptor tables; the layers
+ * must outlive it and share (dout, din, r). */
+typedef struct qbk_factor_set qbk_factor_set;
+int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t n_layers,
+                          qbk_factor_set **out);
+void qbk_factor_set_destroy(qbk_factor_set *set);
+size_t qbk_factor_set_workspace_size(const qbk_factor_set *set);
+/* y_i = layer_i(x_i) at batch 1 for every layer i of the set:
+ * x bf16 [n_layers][din], y bf16 [n_layers][dout] (device pointers). */
+int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *set, const uint16_t *x,
+                              uint16_t *y, void *workspace, size_t workspace_size, void *stream);
+/* One of the two launches of qbk_factor_set_decode_dev: stage 1 writes
+ * t = bf16(Vb^T bf16(s2*x)) for every layer into the workspace, stage 2
+ * reads it and writes y (for callers that interleave work or time stages). */
+int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *set, int stage,
+                             const uint16_t *x, uint16_t *y, void *workspace,
+                             size_t workspace_size, void *stream);
+
+/* ---- attention (gpu_attention.rs) ----------------------------------------- */
+
+/* gpu_attention.rs:402-411 AttentionShape */
+typedef struct {
+    size_t batch, n_heads, n_kv_heads, seq_q, seq_kv, head_dim, val_dim;
+} qbk_attn_shape;
+
+/* gpu_attention.rs:589-756 GpuContext::attention_sage: the [SA] s4 reference
+ * scheme (per-token INT8 Q with 1/sqrt(d) folded, per-K-block mean, per-token
+ * INT8 K, P at the static 1/127 scale, per-channel INT8 V per tile), f32
+ * q (B,H,S,d), k (B,Hkv,S,d), v (B,Hkv,S,dv) -> out (B,H,S,dv), same
+ * validation and messages.  Both INT8 products run on INT8 MFMA. */
+int qbk_attention_sage(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, size_t q_len,
+                       const float *k, size_t k_len, const float *v, size_t v_len, int causal,
+                       size_t block_size, float *out);
+/* Device-pointer form of qbk_attention_sage. */
+int qbk_attention_sage_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q,
+                           const float *k, const float *v, int causal, size_t block_size,
+                           float *out, void *stream);
+
+/* Block-scaled SageAttention prefill (no reference symbol: the scheme the
+ * north_star names).  bf16 q (B,H,S,d), k (B,Hkv,S,d), v (B,Hkv,S,dv),
+ * d == 128, dv == 128, seq_q == seq_kv:
+ *   K smoothed by its whole-sequence channel mean; Q (1/sqrt(d) folded) and K
+ *   INT8 with one scale per 64-token block per head; Q.K^T on INT8 MFMA;
+ *   base-2 online softmax in f32; P and V in fp16 on fp16 MFMA.
+ * out is bf16 (B,H,S,dv).  workspace >= qbk_sage_blk_workspace_size(). */
+size_t qbk_sage_blk_workspace_size(const qbk_attn_shape *shape);
+int qbk_attention_sage_blk_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const uint16_t *q,
+                               const uint16_t *k, const uint16_t *v, int causal, uint16_t *out,
+                               void *workspace, size_t workspace_size, void *stream);
+/* The quantisation pre-pass alone, exporting its stages (for parity checks):
+ * qhat i8 (B,H,S,d), qscale f32 (B,H,ceil(S/64)), khat i8 (B,Hkv,S,d),
+ * kscale f32 (B,Hkv,ceil(S/64)), kmean f32 (B,Hkv,d), vh fp16 (B,Hkv,S,dv). */
+int qbk_sage_blk_quantize_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const uint16_t *q,
+                              const uint16_t *k, const uint16_t *v, int8_t *qhat, float *qscale,
+                              int8_t *khat, float *kscale, float *kmean, uint16_t *vh,
+                              void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QBK_H */

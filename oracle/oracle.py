@@ -1,0 +1,355 @@
+"""ctypes face of the C oracle (oracle/qbk_oracle.c) — TEST INFRASTRUCTURE ONLY.
+
+NumPy in, NumPy out.  Each wrapper names the reference function whose
+arithmetic the C code restates; see qbk_oracle.c for the citations and for
+what pins each function.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "_build", "liborc.so")
+_lib = None
+
+
+class OracleError(ValueError):
+    """A validation error raised by the oracle, carrying the reference's text."""
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with its Makefile (gcc); returns the .so path."""
+    if force or not os.path.exists(_SO):
+        subprocess.run(["make", "-s", "-C", _HERE] + (["-B"] if force else []), check=True)
+    return _SO
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_SO):
+            build()
+        _lib = C.CDLL(_SO)
+        _declare(_lib)
+    return _lib
+
+
+class AttnShape(C.Structure):
+    _fields_ = [(n, C.c_size_t) for n in
+                ("batch", "n_heads", "n_kv_heads", "seq", "head_dim", "val_dim")]
+
+
+class Qpk1Header(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("dtype_tag", C.c_uint32)] + [
+        (n, C.c_size_t) for n in
+        ("dout", "din", "r", "s1_off", "s2_off", "bias_off", "ub_off", "vb_off")]
+
+
+_P = C.c_void_p
+_Z = C.c_size_t
+
+
+def _declare(L):
+    sig = {
+        "orc_pack_bits": (C.c_int, [_P, _Z, _Z, _Z, _P, C.c_char_p, _Z]),
+        "orc_unpack_bits": (C.c_int, [_P, _Z, _Z, _Z, _P, C.c_char_p, _Z]),
+        "orc_validate_packed": (C.c_int, [_Z, _Z, _Z, _P, C.c_char_p, _Z]),
+        "orc_sign_estimate": (None, [_P, _Z, _P]),
+        "orc_f32_to_bf16": (C.c_uint16, [C.c_float]),
+        "orc_bf16_to_f32": (C.c_float, [C.c_uint16]),
+        "orc_packed_matvec": (C.c_int, [C.c_int, _P, _Z, _Z, _Z, _P, _Z, _P, C.c_char_p, _Z]),
+        "orc_packed_matmul": (C.c_int, [C.c_int, _P, _Z, _Z, _Z, _P, _Z, _Z, _P, C.c_char_p, _Z]),
+        "orc_fast_packed_matvec_f64": (C.c_int, [_P, _Z, _Z, _Z, _P, _Z, _P, C.c_int, C.c_char_p, _Z]),
+        "orc_fast_packed_matmul_f64": (C.c_int, [_P, _Z, _Z, _Z, _P, _Z, _Z, _P, C.c_int, C.c_char_p, _Z]),
+        "orc_qpk1_parse": (C.c_int, [_P, _Z, C.POINTER(Qpk1Header), _P, _P, _P, C.c_char_p, _Z]),
+        "orc_qpk1_expected_size": (_Z, [_Z, _Z, _Z, C.c_int, C.c_int]),
+        "orc_container_to_rows": (None, [_P, _Z, _Z, _P]),
+        "orc_container_to_rows_transposed": (None, [_P, _Z, _Z, _P]),
+        "orc_factor_apply": (C.c_int, [C.c_int, _Z, _Z, _Z, _P, _P, _P, _P, _P, _P, _P, C.c_int, C.c_int]),
+        "orc_factor_apply_bf16_batch": (None, [_Z, _Z, _Z, _P, _P, _P, _P, _P, _P, _Z, _P, _P, C.c_int]),
+        "orc_attention_tiled_f64": (C.c_int, [C.POINTER(AttnShape), _P, _P, _P, C.c_int, _Z, _P, _P]),
+        "orc_attention_sage_np_f64": (C.c_int, [C.POINTER(AttnShape), _P, _P, _P, C.c_int, _Z, _P]),
+        "orc_attention_sage_dev_f32": (C.c_int, [C.POINTER(AttnShape), _P, _P, _P, C.c_int, _Z, _P, _P, _P, C.c_int]),
+        "orc_expf": (C.c_float, [C.c_float]),
+        "orc_attention_sage_blk": (C.c_int, [C.POINTER(AttnShape), _P, _P, _P, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _err():
+    return C.create_string_buffer(512)
+
+
+def _check(rc, err):
+    if rc != 0:
+        raise OracleError(err.value.decode())
+
+
+def _threads(threads):
+    return threads if threads else (os.cpu_count() or 1)
+
+
+# ---- bit layout (core.rs:129-240) ------------------------------------------
+
+def pack_bits(factor) -> np.ndarray:
+    f = np.ascontiguousarray(factor, dtype=np.int8)
+    rows = int(np.prod(f.shape[:-1], dtype=np.int64)) if f.ndim > 1 else 1
+    cols = f.shape[-1]
+    out = np.zeros((rows, (cols + 7) // 8), dtype=np.uint8)
+    e = _err()
+    _check(lib().orc_pack_bits(_ptr(f), f.size, rows, cols, _ptr(out), e, 512), e)
+    return out
+
+
+def unpack_bits(packed, n_bits: int, n_rows=None) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    rows = n_rows if n_rows is not None else (p.shape[0] if p.ndim == 2 else 1)
+    out = np.zeros((rows, n_bits), dtype=np.int8)
+    e = _err()
+    _check(lib().orc_unpack_bits(_ptr(p), p.size, rows, n_bits, _ptr(out), e, 512), e)
+    return out
+
+
+def validate_packed(packed_len: int, n_rows: int, n_bits: int) -> int:
+    w = C.c_size_t(0)
+    e = _err()
+    _check(lib().orc_validate_packed(packed_len, n_rows, n_bits, C.byref(w), e, 512), e)
+    return w.value
+
+
+def sign_estimate(x) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=np.float64).ravel()
+    out = np.zeros(a.size, dtype=np.int8)
+    lib().orc_sign_estimate(_ptr(a), a.size, _ptr(out))
+    return out
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    f = lib().orc_f32_to_bf16
+    return np.array([f(float(v)) for v in a.ravel()], dtype=np.uint16).reshape(a.shape)
+
+
+def f32_to_bf16_fast(x) -> np.ndarray:
+    """Vectorised RNE (same rule as orc_f32_to_bf16 for non-NaN input)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (u >> np.uint64(16)) & np.uint64(1)
+    return (((u + np.uint64(0x7FFF) + lsb) >> np.uint64(16)) & np.uint64(0xFFFF)).astype(np.uint16)
+
+
+def bf16_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+# ---- products (core.rs:202-317; fast.rs:28-158) ------------------------------
+
+_DT = {"float64": (0, np.float64), "float32": (1, np.float32), "bfloat16": (2, np.uint16)}
+
+
+def packed_matvec(packed, n_rows: int, n_bits: int, vec, dtype: str = "float64"):
+    code, npdt = _DT[dtype]
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    v = np.ascontiguousarray(vec, dtype=npdt).ravel()
+    out = np.zeros(n_rows, dtype=npdt)
+    e = _err()
+    _check(lib().orc_packed_matvec(code, _ptr(p), p.size, n_rows, n_bits, _ptr(v), v.size,
+                                   _ptr(out), e, 512), e)
+    return out
+
+
+def packed_matmul(packed, n_rows: int, n_bits: int, mat, n_cols: int, dtype: str = "float64"):
+    code, npdt = _DT[dtype]
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    m = np.ascontiguousarray(mat, dtype=npdt).ravel()
+    kc = m.size // max(n_bits, 1)
+    out = np.zeros(n_rows * kc, dtype=npdt)
+    e = _err()
+    _check(lib().orc_packed_matmul(code, _ptr(p), p.size, n_rows, n_bits, _ptr(m), m.size,
+                                   n_cols, _ptr(out), e, 512), e)
+    return out.reshape(n_rows, kc)
+
+
+def fast_packed_matvec(packed, n_rows: int, n_bits: int, vec, threads: int = 0):
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    v = np.ascontiguousarray(vec, dtype=np.float64).ravel()
+    out = np.zeros(n_rows, dtype=np.float64)
+    e = _err()
+    _check(lib().orc_fast_packed_matvec_f64(_ptr(p), p.size, n_rows, n_bits, _ptr(v), v.size,
+                                            _ptr(out), _threads(threads), e, 512), e)
+    return out
+
+
+def fast_packed_matmul(packed, n_rows: int, n_bits: int, mat, n_cols: int, threads: int = 0):
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    m = np.ascontiguousarray(mat, dtype=np.float64).ravel()
+    kc = m.size // max(n_bits, 1)
+    out = np.zeros(n_rows * kc, dtype=np.float64)
+    e = _err()
+    _check(lib().orc_fast_packed_matmul_f64(_ptr(p), p.size, n_rows, n_bits, _ptr(m), m.size,
+                                            n_cols, _ptr(out), _threads(threads), e, 512), e)
+    return out.reshape(n_rows, kc)
+
+
+# ---- qpk1 + engine layout (qpk1 lib.rs:152-320; engine/mod.rs:258-481) ------
+
+def qpk1_parse(stream: bytes) -> dict:
+    b = np.frombuffer(stream, dtype=np.uint8).copy()
+    hdr = Qpk1Header()
+    e = _err()
+    _check(lib().orc_qpk1_parse(_ptr(b), b.size, C.byref(hdr), None, None, None, e, 512), e)
+    s1 = np.zeros(hdr.dout, np.float64)
+    s2 = np.zeros(hdr.din, np.float64)
+    bias = np.zeros(hdr.dout, np.float64)
+    _check(lib().orc_qpk1_parse(_ptr(b), b.size, C.byref(hdr), _ptr(s1), _ptr(s2), _ptr(bias),
+                                e, 512), e)
+    ub_len = (hdr.dout * hdr.r + 7) // 8
+    vb_len = (hdr.din * hdr.r + 7) // 8
+    return {
+        "version": hdr.version, "dtype_tag": hdr.dtype_tag, "dout": hdr.dout, "din": hdr.din,
+        "r": hdr.r, "s1": s1, "s2": s2, "bias": bias if hdr.version >= 2 else np.zeros(0),
+        "ub_packed": b[hdr.ub_off:hdr.ub_off + ub_len].copy(),
+        "vb_packed": b[hdr.vb_off:hdr.vb_off + vb_len].copy(),
+    }
+
+
+def qpk1_expected_size(dout, din, r, itemsize, with_bias) -> int:
+    return lib().orc_qpk1_expected_size(dout, din, r, itemsize, int(with_bias))
+
+
+def container_to_rows(packed, n_rows: int, r: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.zeros(n_rows * ((r + 7) // 8), np.uint8)
+    lib().orc_container_to_rows(_ptr(p), n_rows, r, _ptr(out))
+    return out
+
+
+def container_to_rows_transposed(packed, din: int, r: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.zeros(r * ((din + 7) // 8), np.uint8)
+    lib().orc_container_to_rows_transposed(_ptr(p), din, r, _ptr(out))
+    return out
+
+
+def factor_apply(serving: str, dout, din, r, ub_rows, vb_t_rows, s1, s2, bias, x,
+                 fast: bool = False, threads: int = 0) -> np.ndarray:
+    """engine/mod.rs:393-481 PackedLayer::apply ("fp32") / apply_bf16 ("bf16")."""
+    ub = np.ascontiguousarray(ub_rows, np.uint8)
+    vt = np.ascontiguousarray(vb_t_rows, np.uint8)
+    a1 = np.ascontiguousarray(s1, np.float32)
+    a2 = np.ascontiguousarray(s2, np.float32)
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    xx = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(dout, np.float32)
+    rc = lib().orc_factor_apply(0 if serving == "fp32" else 1, dout, din, r, _ptr(ub), _ptr(vt),
+                                _ptr(a1), _ptr(a2), _ptr(bb), _ptr(xx), _ptr(y), int(fast),
+                                _threads(threads))
+    if rc:
+        raise OracleError("factor_apply failed")
+    return y
+
+
+def factor_apply_bf16_batch(dout, din, r, ub_rows, vb_t_rows, s1, s2, bias, x_bf16,
+                            threads: int = 0, want_t: bool = False):
+    """Token-major batched apply_bf16; returns y f32 [batch, dout] (and t bf16)."""
+    ub = np.ascontiguousarray(ub_rows, np.uint8)
+    vt = np.ascontiguousarray(vb_t_rows, np.uint8)
+    a1 = np.ascontiguousarray(s1, np.float32)
+    a2 = np.ascontiguousarray(s2, np.float32)
+    bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    batch = x.size // din
+    y = np.zeros((batch, dout), np.float32)
+    t = np.zeros((batch, r), np.uint16) if want_t else None
+    lib().orc_factor_apply_bf16_batch(dout, din, r, _ptr(ub), _ptr(vt), _ptr(a1), _ptr(a2),
+                                      _ptr(bb), _ptr(x), batch, _ptr(y), _ptr(t),
+                                      _threads(threads))
+    return (y, t) if want_t else y
+
+
+# ---- attention --------------------------------------------------------------
+
+def _shape(q, k, v):
+    b, h, s, d = q.shape
+    return AttnShape(b, h, k.shape[1], s, d, v.shape[3])
+
+
+def attention_tiled(q, k, v, causal=False, block_size=64, return_lse=False):
+    """attention_tiled.py:76-180 (exact, f64)."""
+    q = np.ascontiguousarray(q, np.float64)
+    k = np.ascontiguousarray(k, np.float64)
+    v = np.ascontiguousarray(v, np.float64)
+    sh = _shape(q, k, v)
+    out = np.zeros(q.shape[:3] + (v.shape[3],), np.float64)
+    lse = np.zeros(q.shape[:3], np.float64)
+    lib().orc_attention_tiled_f64(C.byref(sh), _ptr(q), _ptr(k), _ptr(v), int(causal),
+                                  block_size, _ptr(out), _ptr(lse))
+    return (out, lse) if return_lse else out
+
+
+def attention_sage_np(q, k, v, causal=False, block_size=64):
+    """attention_sage.py:206-350 (f64 NumPy semantics)."""
+    q = np.ascontiguousarray(q, np.float64)
+    k = np.ascontiguousarray(k, np.float64)
+    v = np.ascontiguousarray(v, np.float64)
+    sh = _shape(q, k, v)
+    out = np.zeros(q.shape[:3] + (v.shape[3],), np.float64)
+    lib().orc_attention_sage_np_f64(C.byref(sh), _ptr(q), _ptr(k), _ptr(v), int(causal),
+                                    block_size, _ptr(out))
+    return out
+
+
+def attention_sage_dev(q, k, v, causal=False, block_size=64, threads=0, stages=False):
+    """gpu_attention.rs:89-396 (f32 device semantics, orc_expf)."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    sh = _shape(q, k, v)
+    out = np.zeros(q.shape[:3] + (v.shape[3],), np.float32)
+    qhat = np.zeros(q.shape, np.int8) if stages else None
+    qd = np.zeros(q.shape[:3], np.float32) if stages else None
+    lib().orc_attention_sage_dev_f32(C.byref(sh), _ptr(q), _ptr(k), _ptr(v), int(causal),
+                                     block_size, _ptr(out), _ptr(qhat), _ptr(qd),
+                                     _threads(threads))
+    return (out, qhat, qd) if stages else out
+
+
+def expf(x: float) -> float:
+    return lib().orc_expf(float(x))
+
+
+def attention_sage_blk(q_bf16, k_bf16, v_bf16, causal=True, threads=0, stages=False):
+    """Block-scaled Sage variant (north_star scheme).  Inputs are bf16 bit
+    patterns (uint16) shaped (B,H,S,d)/(B,Hkv,S,d)/(B,Hkv,S,dv)."""
+    q = np.ascontiguousarray(q_bf16, np.uint16)
+    k = np.ascontiguousarray(k_bf16, np.uint16)
+    v = np.ascontiguousarray(v_bf16, np.uint16)
+    sh = _shape(q, k, v)
+    B, H, S, d = q.shape
+    Hk = k.shape[1]
+    nblk = (S + 63) // 64
+    out = np.zeros(q.shape[:3] + (v.shape[3],), np.float32)
+    st = None
+    if stages:
+        st = {
+            "qhat": np.zeros(q.shape, np.int8), "qscale": np.zeros((B, H, nblk), np.float32),
+            "khat": np.zeros(k.shape, np.int8), "kscale": np.zeros((B, Hk, nblk), np.float32),
+            "kmean": np.zeros((B, Hk, d), np.float32),
+        }
+    g = (lambda n: _ptr(st[n])) if stages else (lambda n: None)
+    rc = lib().orc_attention_sage_blk(C.byref(sh), _ptr(q), _ptr(k), _ptr(v), int(causal),
+                                      _ptr(out), g("qhat"), g("qscale"), g("khat"),
+                                      g("kscale"), g("kmean"), _threads(threads))
+    if rc:
+        raise OracleError("attention_sage_blk: bad shape")
+    return (out, st) if stages else out

@@ -1,0 +1,100 @@
+// qbk_internal.h -- shared internals of libqbk (gfx950 / CDNA4).
+//
+// Error plumbing (thread-local last error, reference message texts), the
+// device context, and small device helpers (bf16 RNE, wave reductions).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/qbk.h"
+
+namespace qbk {
+
+// ---- errors --------------------------------------------------------------
+
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+std::string fmt(const char *f, ...) __attribute__((format(printf, 1, 2)));
+
+// HIP call that maps a failure to QBK_ERR_DEVICE with the call's text.
+#define QBK_HIP(call)                                                                  \
+    do {                                                                               \
+        hipError_t e_ = (call);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return ::qbk::fail(QBK_ERR_DEVICE, ::qbk::fmt("%s failed: %s", #call,      \
+                                                          hipGetErrorString(e_)));     \
+    } while (0)
+
+// ---- context -------------------------------------------------------------
+
+}  // namespace qbk
+
+struct qbk_ctx {
+    int device;
+    int num_cus;
+    hipDeviceProp_t props;
+};
+
+namespace qbk {
+
+// Makes ctx->device current for the calling thread.
+int bind(qbk_ctx *ctx);
+
+// Scoped device buffer for the host-pointer entry points.
+struct DevBuf {
+    void *p = nullptr;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    int alloc(size_t n) {
+        if (n == 0) n = 16;
+        hipError_t e = hipMalloc(&p, n);
+        if (e != hipSuccess) {
+            p = nullptr;
+            return fail(QBK_ERR_DEVICE, fmt("hipMalloc(%zu) failed: %s", n, hipGetErrorString(e)));
+        }
+        return QBK_OK;
+    }
+};
+
+// Scoped non-default stream for a blocking host call.
+struct CallStream {
+    hipStream_t s = nullptr;
+    ~CallStream() {
+        if (s) (void)hipStreamDestroy(s);
+    }
+    int create() {
+        hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            s = nullptr;
+            return fail(QBK_ERR_DEVICE, fmt("hipStreamCreate failed: %s", hipGetErrorString(e)));
+        }
+        return QBK_OK;
+    }
+};
+
+// validate_packed (core.rs:223-240) with the reference's messages.
+int validate_packed(size_t packed_len, size_t n_rows, size_t n_bits, size_t *n_words);
+
+static inline size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
+static inline size_t round_up(size_t a, size_t b) { return div_ceil(a, b) * b; }
+
+// ---- device helpers -------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+    return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// half 2.7.1 bf16::from_f32 (round to nearest even; NaN stays quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t lsb = (u >> 16) & 1u;
+    return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+
+}  // namespace qbk

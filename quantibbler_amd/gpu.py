@@ -1,0 +1,274 @@
+"""Device face: GpuContext, FactorLayer, FactorSet, AttentionShape.
+
+Mirrors crates/quantibbler-kernels/src/gpu.rs (GpuContext::init / init_at /
+packed_matvec, gpu_available) and gpu_attention.rs (AttentionShape,
+attention_sage), plus the device-resident factor linear of the engine's
+PackedLayer (crates/quantibbler-server/src/engine/mod.rs:313-481).
+
+Host-buffer methods take and return NumPy arrays (copy in, launch, copy
+out, like the reference).  ``*_dev`` methods take device pointers (ints, or
+objects with ``data_ptr()`` such as torch tensors) and a stream handle, and
+return without waiting.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import AttnShape, check
+
+_DTYPES = {"float64": (_lib.QBK_F64, np.float64), "float32": (_lib.QBK_F32, np.float32),
+           "bfloat16": (_lib.QBK_BF16, np.uint16)}
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    raise TypeError(f"cannot take a pointer of {type(x)!r}")
+
+
+def _stream(s):
+    if s is None:
+        return None
+    if isinstance(s, int):
+        return s
+    if hasattr(s, "cuda_stream"):
+        return s.cuda_stream
+    raise TypeError(f"cannot take a stream handle of {type(s)!r}")
+
+
+def gpu_available() -> bool:
+    """gpu.rs:187-189."""
+    return bool(_lib.load().qbk_gpu_available())
+
+
+@dataclass(frozen=True)
+class AttentionShape:
+    """gpu_attention.rs:402-411."""
+    batch: int
+    n_heads: int
+    n_kv_heads: int
+    seq_q: int
+    seq_kv: int
+    head_dim: int
+    val_dim: int
+
+    def c(self) -> AttnShape:
+        return AttnShape(self.batch, self.n_heads, self.n_kv_heads, self.seq_q, self.seq_kv,
+                         self.head_dim, self.val_dim)
+
+
+class GpuContext:
+    """gpu.rs:76-185: a live context on one gfx950 device (fail-closed init)."""
+
+    def __init__(self, device_index: int = 0):
+        lib = _lib.load()
+        h = C.c_void_p()
+        check(lib.qbk_ctx_create(int(device_index), C.byref(h)))
+        self._h = h
+        self.device_index = int(device_index)
+
+    @classmethod
+    def init(cls) -> "GpuContext":
+        return cls(0)
+
+    @classmethod
+    def init_at(cls, device_index: int) -> "GpuContext":
+        return cls(device_index)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.load().qbk_ctx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- packed products (gpu.rs:116-185, dispatch.rs:81-109) -------------
+
+    def packed_matvec(self, packed, n_rows: int, n_bits: int, vec, dtype: str = "float64"):
+        code, npdt = _DTYPES[dtype]
+        p = np.ascontiguousarray(packed, dtype=np.uint8).ravel()
+        v = np.ascontiguousarray(vec, dtype=npdt).ravel()
+        out = np.zeros(n_rows, dtype=npdt)
+        check(_lib.load().qbk_packed_matvec(self._h, code, _ptr(p), p.size, n_rows, n_bits,
+                                            _ptr(v), v.size, _ptr(out)))
+        return out
+
+    def packed_matmul(self, packed, n_rows: int, n_bits: int, mat, n_cols: int,
+                      dtype: str = "float64"):
+        code, npdt = _DTYPES[dtype]
+        p = np.ascontiguousarray(packed, dtype=np.uint8).ravel()
+        m = np.ascontiguousarray(mat, dtype=npdt).ravel()
+        k = m.size // max(n_bits, 1)
+        out = np.zeros(n_rows * k, dtype=npdt)
+        check(_lib.load().qbk_packed_matmul(self._h, code, _ptr(p), p.size, n_rows, n_bits,
+                                            _ptr(m), m.size, n_cols, _ptr(out)))
+        return out.reshape(n_rows, k)
+
+    # ---- attention (gpu_attention.rs:589-756) -----------------------------
+
+    def attention_sage(self, shape: AttentionShape, query, key, value, causal: bool,
+                       block_size: int):
+        q = np.ascontiguousarray(query, dtype=np.float32).ravel()
+        k = np.ascontiguousarray(key, dtype=np.float32).ravel()
+        v = np.ascontiguousarray(value, dtype=np.float32).ravel()
+        out = np.zeros(shape.batch * shape.n_heads * shape.seq_q * shape.val_dim, np.float32)
+        sh = shape.c()
+        check(_lib.load().qbk_attention_sage(self._h, C.byref(sh), _ptr(q), q.size, _ptr(k),
+                                             k.size, _ptr(v), v.size, int(bool(causal)),
+                                             int(block_size), _ptr(out)))
+        return out
+
+    def attention_sage_dev(self, shape: AttentionShape, q, k, v, causal: bool, block_size: int,
+                           out, stream=None):
+        sh = shape.c()
+        check(_lib.load().qbk_attention_sage_dev(self._h, C.byref(sh), _ptr(q), _ptr(k), _ptr(v),
+                                                 int(bool(causal)), int(block_size), _ptr(out),
+                                                 _stream(stream)))
+
+    def sage_blk_workspace_size(self, shape: AttentionShape) -> int:
+        sh = shape.c()
+        return int(_lib.load().qbk_sage_blk_workspace_size(C.byref(sh)))
+
+    def attention_sage_blk_dev(self, shape: AttentionShape, q, k, v, causal: bool, out,
+                               workspace, workspace_size: int, stream=None):
+        sh = shape.c()
+        check(_lib.load().qbk_attention_sage_blk_dev(self._h, C.byref(sh), _ptr(q), _ptr(k),
+                                                     _ptr(v), int(bool(causal)), _ptr(out),
+                                                     _ptr(workspace), int(workspace_size),
+                                                     _stream(stream)))
+
+    def sage_blk_quantize_dev(self, shape: AttentionShape, q, k, v, qhat, qscale, khat, kscale,
+                              kmean, vh, stream=None):
+        sh = shape.c()
+        check(_lib.load().qbk_sage_blk_quantize_dev(self._h, C.byref(sh), _ptr(q), _ptr(k),
+                                                    _ptr(v), _ptr(qhat), _ptr(qscale),
+                                                    _ptr(khat), _ptr(kscale), _ptr(kmean),
+                                                    _ptr(vh), _stream(stream)))
+
+
+class FactorLayer:
+    """Device-resident binary factor linear (engine/mod.rs:313-481 PackedLayer)."""
+
+    def __init__(self, ctx: GpuContext, handle):
+        self.ctx = ctx
+        self._h = handle
+        d = [C.c_size_t() for _ in range(3)]
+        check(_lib.load().qbk_factor_dims(handle, *[C.byref(x) for x in d]))
+        self.dout, self.din, self.r = (x.value for x in d)
+
+    @classmethod
+    def from_qpk1(cls, ctx: GpuContext, stream: bytes) -> "FactorLayer":
+        b = np.frombuffer(bytes(stream), dtype=np.uint8)
+        h = C.c_void_p()
+        check(_lib.load().qbk_factor_from_qpk1(ctx.handle, _ptr(b), b.size, C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def from_rows(cls, ctx: GpuContext, dout: int, din: int, r: int, ub_rows, vb_t_rows, s1, s2,
+                  bias=None) -> "FactorLayer":
+        ub = np.ascontiguousarray(ub_rows, np.uint8)
+        vt = np.ascontiguousarray(vb_t_rows, np.uint8)
+        a1 = np.ascontiguousarray(s1, np.float32)
+        a2 = np.ascontiguousarray(s2, np.float32)
+        bb = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        if ub.size != dout * ((r + 7) // 8) or vt.size != r * ((din + 7) // 8):
+            raise _lib.KernelError("bitplane length mismatch after repack")
+        if a1.size != dout or a2.size != din or (bb is not None and bb.size != dout):
+            raise _lib.KernelError(
+                f"scale/bias lengths ({a1.size}, {a2.size}, {None if bb is None else bb.size}) "
+                f"do not match (dout={dout}, din={din})")
+        h = C.c_void_p()
+        check(_lib.load().qbk_factor_from_rows(ctx.handle, dout, din, r, _ptr(ub), _ptr(vt),
+                                               _ptr(a1), _ptr(a2), _ptr(bb), C.byref(h)))
+        return cls(ctx, h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def workspace_size(self, batch: int) -> int:
+        return int(_lib.load().qbk_factor_workspace_size(self._h, batch))
+
+    def linear_dev(self, x, batch: int, y, y_dtype: str, workspace, workspace_size: int,
+                   stream=None):
+        code = _DTYPES[y_dtype][0]
+        check(_lib.load().qbk_factor_linear_dev(self.ctx.handle, self._h, _ptr(x), batch,
+                                                _ptr(y), code, _ptr(workspace),
+                                                int(workspace_size), _stream(stream)))
+
+    def apply(self, x, serving: str = "bfloat16") -> np.ndarray:
+        """PackedLayer::apply ("float32": f64 matvecs) / apply_bf16 ("bfloat16")."""
+        code = _DTYPES[serving][0]
+        xx = np.ascontiguousarray(x, np.float32)
+        batch = xx.size // self.din
+        if batch * self.din != xx.size:
+            raise _lib.KernelError(f"layer expects input dim {self.din}, got {xx.shape[-1]}")
+        y = np.zeros((batch, self.dout), np.float32)
+        check(_lib.load().qbk_factor_apply(self.ctx.handle, self._h, code, _ptr(xx), batch,
+                                           _ptr(y)))
+        return y if xx.ndim > 1 else y[0]
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.load().qbk_factor_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class FactorSet:
+    """Layers of one shape decoded together, one launch per stage."""
+
+    def __init__(self, ctx: GpuContext, layers):
+        self.ctx = ctx
+        self.layers = list(layers)
+        arr = (C.c_void_p * len(self.layers))(*[l.handle.value for l in self.layers])
+        h = C.c_void_p()
+        check(_lib.load().qbk_factor_set_create(ctx.handle, arr, len(self.layers), C.byref(h)))
+        self._h = h
+
+    def workspace_size(self) -> int:
+        return int(_lib.load().qbk_factor_set_workspace_size(self._h))
+
+    def decode_dev(self, x, y, workspace, workspace_size: int, stream=None):
+        check(_lib.load().qbk_factor_set_decode_dev(self.ctx.handle, self._h, _ptr(x), _ptr(y),
+                                                    _ptr(workspace), int(workspace_size),
+                                                    _stream(stream)))
+
+    def stage_dev(self, stage: int, x, y, workspace, workspace_size: int, stream=None):
+        check(_lib.load().qbk_factor_set_stage_dev(self.ctx.handle, self._h, int(stage), _ptr(x),
+                                                   _ptr(y), _ptr(workspace), int(workspace_size),
+                                                   _stream(stream)))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.load().qbk_factor_set_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,113 @@
+"""C-ABI checks that need no GPU: libqbk.so loads, exports every symbol
+include/qbk.h declares, its host-side functions agree with the oracle and the
+reference's error texts, and device init fails closed with the hint when no
+device is visible (gpu.rs:85-101)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from quantibbler_amd import _lib
+
+    return _lib.load()
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "qbk.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qbk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_symbols()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), f"libqbk.so does not export {n}"
+    from quantibbler_amd import _lib
+
+    assert set(_lib.EXPORTED) <= set(names) | {"qbk_backend_version", "qbk_last_error"}
+
+
+def test_library_is_gfx950_code_object():
+    so = os.path.join(ROOT, "quantibbler_amd", "libqbk.so")
+    blob = open(so, "rb").read()
+    assert b"gfx950" in blob
+
+
+def test_host_bit_layout_matches_oracle(orc):
+    from quantibbler_amd import kernels as K
+
+    rng = np.random.default_rng(2)
+    for rows, cols in [(5, 11), (3, 64), (7, 1), (1, 129)]:
+        f = rng.choice([-1, 1], (rows, cols)).astype(np.int8)
+        p = K.pack_bits(f)
+        assert p.tobytes() == orc.pack_bits(f).tobytes()
+        assert K.unpack_bits(p, cols, "int8").tobytes() == f.tobytes()
+        assert K.unpack_bits(p, cols, "float64").tolist() == f.astype(np.float64).tolist()
+    x = np.array([0.0, -0.0, 1.5, -2.5, -1e-9, 1e-300])
+    assert K.sign_estimate(x).tolist() == orc.sign_estimate(x).tolist()
+
+
+def test_host_error_texts():
+    from quantibbler_amd import KernelError
+    from quantibbler_amd import kernels as K
+
+    with pytest.raises(KernelError, match=r"pack_bits expects values in \{-1, \+1\}; got 0.5"):
+        K.pack_bits(np.array([[1.0, 0.5]]))
+    with pytest.raises(KernelError, match=r"n_bits=17 exceeds the packed width 2 \(16 bits\)"):
+        K.unpack_bits(np.zeros((1, 2), np.uint8), 17, "int8")
+    with pytest.raises(KernelError, match="packed length 2 does not match 1 rows x 1 bitplanes"):
+        K.unpack_bits(np.zeros((1, 2), np.uint8), 8, "int8")
+    with pytest.raises(KernelError, match="unpack_bits dtype must be 'int8' or 'float64', got \"float32\""):
+        K.unpack_bits(np.zeros((1, 1), np.uint8), 8, "float32")
+    with pytest.raises(KernelError, match=r'unknown kernel dtype "float16"; expected one of "float64", "float32", "bfloat16"'):
+        K.packed_matvec_dtype(np.zeros((1, 1), np.uint8), 8, np.zeros(8), "float16")
+
+
+def test_validation_precedes_device_use(lib):
+    # shape errors are reported before any device is touched (gpu.rs:123-137)
+    from quantibbler_amd import KernelError
+    from quantibbler_amd._lib import check
+
+    packed, vec, out = np.zeros(2, np.uint8), np.zeros(8), np.zeros(1)
+    with pytest.raises(KernelError, match="vec must have length 9, got 8"):
+        check(lib.qbk_packed_matvec(None, 0, packed.ctypes.data, 2, 1, 9, vec.ctypes.data, 8,
+                                    out.ctypes.data))
+    with pytest.raises(KernelError, match="packed length 2 does not match 3 rows x 2 bitplanes"):
+        check(lib.qbk_packed_matvec(None, 0, packed.ctypes.data, 2, 3, 9, vec.ctypes.data, 9,
+                                    out.ctypes.data))
+    with pytest.raises(KernelError, match="sage attention requires a positive block_size"):
+        from quantibbler_amd._lib import AttnShape
+
+        sh = AttnShape(1, 2, 1, 8, 8, 4, 4)
+        check(lib.qbk_attention_sage(None, C.byref(sh), None, 64, None, 32, None, 32, 1, 0, None))
+    with pytest.raises(KernelError, match=r"n_kv_heads must divide n_heads: n_heads=3, n_kv_heads=2"):
+        sh = AttnShape(1, 3, 2, 8, 8, 4, 4)
+        check(lib.qbk_attention_sage(None, C.byref(sh), None, 0, None, 0, None, 0, 1, 4, None))
+    with pytest.raises(KernelError, match=r"query must hold 64 values for AttentionShape \{ batch: 1, "
+                       r"n_heads: 2, n_kv_heads: 1, seq_q: 8, seq_kv: 8, head_dim: 4, val_dim: 4 \}, got 63"):
+        sh = AttnShape(1, 2, 1, 8, 8, 4, 4)
+        check(lib.qbk_attention_sage(None, C.byref(sh), None, 63, None, 32, None, 32, 1, 4, None))
+
+
+def test_init_fails_closed_without_device(lib):
+    try:
+        import torch
+
+        has_gpu = torch.cuda.is_available()
+    except Exception:
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a device is visible; the fail-closed path is exercised on CPU hosts")
+    from quantibbler_amd import GpuContext, InitError, gpu_available
+
+    assert gpu_available() is False
+    with pytest.raises(InitError, match="no usable HIP/ROCm device"):
+        GpuContext(0)

@@ -1,0 +1,218 @@
+"""GPU parity: the binary factor linear (engine/mod.rs:393-481) through the C
+ABI against the oracle.
+
+* Integer-exact inputs (small-integer z, so every f32 sum is exact and every
+  bf16 rounding is decided by the exact value): the device composite must be
+  bit-identical to the oracle's -- a single misplaced bit anywhere in the
+  repacked layouts would change an output.
+* Config-distribution inputs: each stage within the reference's bf16 backward
+  bound (1e-2 of the row term scale, parity.rs:797-806 and
+  engine/mod.rs:1897-1949), and within one bf16 ulp of the oracle's stage
+  output (the two differ only by f32 reassociation).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from quantibbler_amd import GpuContext
+
+    return GpuContext(0)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def make_layer(orc, rng, dout, din, r, integer=False):
+    ubs = rng.choice([-1, 1], (dout, r)).astype(np.int8)
+    vts = rng.choice([-1, 1], (r, din)).astype(np.int8)
+    if integer:
+        s2 = np.ones(din, np.float32)
+    else:
+        s2 = np.exp(0.5 * rng.standard_normal(din)).astype(np.float32)
+    s1 = np.exp(0.5 * rng.standard_normal(dout)).astype(np.float32)
+    bias = rng.standard_normal(dout).astype(np.float32)
+    return dict(dout=dout, din=din, r=r, ub=orc.pack_bits(ubs), vt=orc.pack_bits(vts), s1=s1,
+                s2=s2, bias=bias, ubs=ubs, vts=vts)
+
+
+def upload(ctx, L):
+    from quantibbler_amd import FactorLayer
+
+    return FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"],
+                                 L["s2"], L["bias"])
+
+
+def run_dev(layer, x_bf16, y_dtype="float32"):
+    batch = x_bf16.shape[0]
+    x = torch.from_numpy(x_bf16.view(np.int16)).cuda()
+    y = torch.empty((batch, layer.dout), dtype=torch.float32 if y_dtype == "float32" else torch.int16,
+                    device="cuda")
+    ws_n = layer.workspace_size(batch)
+    ws = torch.zeros(ws_n, dtype=torch.uint8, device="cuda")
+    layer.linear_dev(x, batch, y, y_dtype, ws, ws_n, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    yy = y.cpu().numpy()
+    if y_dtype == "bfloat16":
+        yy = yy.view(np.uint16)
+    return yy, ws.cpu().numpy()
+
+
+SHAPES = [(256, 512, 128), (300, 200, 37), (1024, 4096, 1102), (4096, 4096, 1024)]
+
+
+@pytest.mark.parametrize("dout,din,r", SHAPES)
+@pytest.mark.parametrize("batch", [1, 2, 16, 33, 128])
+def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
+    if dout * r > 2_000_000 and batch not in (1, 16, 128):
+        pytest.skip("covered by the smaller shapes")
+    say("factor integer-exact", dout, din, r, "batch", batch)
+    rng = np.random.default_rng(dout + din + r + batch)
+    L = make_layer(orc, rng, dout, din, r, integer=True)
+    layer = upload(ctx, L)
+    x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (batch, din)).astype(np.float32))
+    want = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
+    got, _ = run_dev(layer, x)
+    assert got.tobytes() == want.tobytes()
+    got_b, _ = run_dev(layer, x, "bfloat16")
+    assert got_b.tobytes() == orc.f32_to_bf16_fast(want).tobytes()
+
+
+def gpu_t(layer, ws, batch):
+    """The device's t (bf16) read back from the documented workspace layout."""
+    r, rp = layer.r, -(-layer.r // 128) * 128
+    if batch == 1:
+        return ws[: rp * 2].view(np.uint16)[:r][None, :]
+    parts = ws[: (ws.size // 4) * 4].view(np.float32)
+    nsplit = None
+    for s in (1, 2, 4, 8):
+        if s * batch * rp * 4 + 256 == ws.size:
+            nsplit = s
+    assert nsplit is not None
+    p = parts[: nsplit * batch * rp].reshape(nsplit, batch, rp)
+    tot = p[0].copy()
+    for s in range(1, nsplit):
+        tot = (tot + p[s]).astype(np.float32)
+    from oracle import oracle as orc
+
+    return orc.f32_to_bf16_fast(tot[:, :r])
+
+
+@pytest.mark.parametrize("dout,din,r", SHAPES)
+@pytest.mark.parametrize("batch", [1, 16, 128])
+def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
+    say("factor stage bounds", dout, din, r, "batch", batch)
+    rng = np.random.default_rng(1000 + dout + r + batch)
+    L = make_layer(orc, rng, dout, din, r)
+    layer = upload(ctx, L)
+    x = orc.f32_to_bf16_fast(rng.standard_normal((batch, din)).astype(np.float32))
+    y, ws = run_dev(layer, x)
+    y2, _ = run_dev(layer, x)
+    assert y.tobytes() == y2.tobytes(), "device result not repeatable"
+    t = gpu_t(layer, ws, batch)
+    tf = orc.bf16_to_f32(t).astype(np.float64)
+    z = orc.bf16_to_f32(orc.f32_to_bf16_fast(L["s2"] * orc.bf16_to_f32(x))).astype(np.float64)
+    t_exact = z @ L["vts"].T.astype(np.float64)
+    assert np.all(np.abs(tf - t_exact) <= 1e-2 * np.abs(z).sum(axis=1, keepdims=True))
+    _, t_orc = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"],
+                                           L["bias"], x, want_t=True)
+    tof = orc.bf16_to_f32(t_orc).astype(np.float64)
+    ulp = np.spacing(np.abs(tof).astype(np.float32)).astype(np.float64) * 2 ** 16
+    assert np.all(np.abs(tf - tof) <= ulp + 1e-6 * np.abs(z).sum(axis=1, keepdims=True))
+    # stage 2 from the device's own t
+    u_exact = tf @ L["ubs"].T.astype(np.float64)
+    y_exact = u_exact * L["s1"] + L["bias"]
+    bound = np.abs(L["s1"]) * (1e-2 * np.abs(tf).sum(axis=1, keepdims=True)) + 1e-5 * np.abs(y_exact)
+    assert np.all(np.abs(y - y_exact) <= bound)
+    u_or = np.stack([orc.bf16_to_f32(orc.packed_matvec(L["ub"], dout, r, t[i], "bfloat16")) for i in range(batch)])
+    y_or = (u_or * L["s1"] + L["bias"]).astype(np.float32)
+    # one bf16 ulp of u, plus the f32 reassociation term (the device sums in a
+    # different order; under cancellation that can move u across several ulps)
+    uulp = np.spacing(np.abs(u_or).astype(np.float32)) * 2 ** 16
+    reassoc = 1e-6 * np.abs(tf).sum(axis=1, keepdims=True)
+    assert np.all(np.abs(y - y_or) <= np.abs(L["s1"]) * (uulp * 1.01 + reassoc) + 1e-6 * np.abs(y_or))
+
+
+def test_set_decode_matches_single_layers(ctx, orc):
+    from quantibbler_amd import FactorSet
+
+    say("factor set decode")
+    rng = np.random.default_rng(77)
+    Ls = [make_layer(orc, rng, 512, 1024, 200) for _ in range(5)]
+    layers = [upload(ctx, L) for L in Ls]
+    S = FactorSet(ctx, layers)
+    x = orc.f32_to_bf16_fast(rng.standard_normal((5, 1024)).astype(np.float32))
+    xd = torch.from_numpy(x.view(np.int16)).cuda()
+    yd = torch.empty((5, 512), dtype=torch.int16, device="cuda")
+    ws = torch.zeros(S.workspace_size(), dtype=torch.uint8, device="cuda")
+    S.decode_dev(xd, yd, ws, ws.numel(), torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    ys = yd.cpu().numpy().view(np.uint16)
+    for i, layer in enumerate(layers):
+        yi, _ = run_dev(layer, x[i:i + 1], "bfloat16")
+        assert ys[i].tobytes() == yi[0].tobytes()
+
+
+def test_apply_host_faces(ctx, orc):
+    say("factor apply host faces")
+    rng = np.random.default_rng(5)
+    L = make_layer(orc, rng, 96, 160, 40)
+    layer = upload(ctx, L)
+    x = rng.standard_normal(160).astype(np.float32)
+    # fp32 serving: f64 matvecs in element order -> bit-identical (BS-3.1)
+    got = layer.apply(x, "float32")
+    want = orc.factor_apply("fp32", 96, 160, 40, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
+    assert got.tobytes() == want.tobytes()
+    # bf16 serving with an f32 x: z = bf16(s2*x) as apply_bf16 does
+    got_b = layer.apply(x, "bfloat16")
+    want_b = orc.factor_apply("bf16", 96, 160, 40, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
+    z = orc.bf16_to_f32(orc.f32_to_bf16_fast(L["s2"] * x)).astype(np.float64)
+    tf = np.abs(z).sum() * 2  # loose scale for the two-stage bound
+    assert np.all(np.abs(got_b - want_b) <= np.abs(L["s1"]) * 1e-2 * tf)
+
+
+def qpk1_stream(L, orc):
+    dout, din, r = L["dout"], L["din"], L["r"]
+    ub_bits = np.zeros((dout * r + 7) // 8, np.uint8)
+    vb_bits = np.zeros((din * r + 7) // 8, np.uint8)
+    for i in range(dout):
+        for j in range(r):
+            if L["ubs"][i, j] == 1:
+                b = i * r + j
+                ub_bits[b >> 3] |= 1 << (b & 7)
+    vb = L["vts"].T  # (din, r)
+    for i in range(din):
+        for j in range(r):
+            if vb[i, j] == 1:
+                b = i * r + j
+                vb_bits[b >> 3] |= 1 << (b & 7)
+    head = b"QPK1" + b"".join(int(v).to_bytes(4, "little") for v in (2, 1, dout, din, r))
+    f16 = lambda a: np.asarray(a, np.float16).tobytes()
+    return head + f16(L["s1"]) + f16(L["s2"]) + f16(L["bias"]) + ub_bits.tobytes() + vb_bits.tobytes()
+
+
+def test_from_qpk1_matches_from_rows(ctx, orc):
+    from quantibbler_amd import FactorLayer, KernelError
+
+    say("factor from qpk1")
+    rng = np.random.default_rng(6)
+    L = make_layer(orc, rng, 40, 24, 13)
+    L["s1"] = L["s1"].astype(np.float16).astype(np.float32)
+    L["s2"] = L["s2"].astype(np.float16).astype(np.float32)
+    L["bias"] = L["bias"].astype(np.float16).astype(np.float32)
+    stream = qpk1_stream(L, orc)
+    parsed = orc.qpk1_parse(stream)
+    assert np.array_equal(orc.container_to_rows(parsed["ub_packed"], 40, 13), L["ub"].ravel())
+    assert np.array_equal(orc.container_to_rows_transposed(parsed["vb_packed"], 24, 13), L["vt"].ravel())
+    a = FactorLayer.from_qpk1(ctx, stream)
+    b = upload(ctx, L)
+    x = orc.f32_to_bf16_fast(rng.standard_normal((3, 24)).astype(np.float32))
+    assert run_dev(a, x)[0].tobytes() == run_dev(b, x)[0].tobytes()
+    with pytest.raises(KernelError, match="trailing garbage"):
+        FactorLayer.from_qpk1(ctx, stream + b"\0")

@@ -1,0 +1,152 @@
+"""GPU parity: SageAttention through the C ABI.
+
+Reference scheme (gpu_attention.rs:589-756): on every attention_sage.json
+case the device output is bit-identical to the oracle's f32 restatement of
+the reference kernel, passes the reference's device gate against the f64
+quantized reference (gpu_attention_sage.rs:35-46), and stays inside its
+measured quality envelope against exact attention.
+
+Block-scaled scheme: INT8 codes and scales bit-identical to the oracle's
+pre-pass; outputs within 1 bf16 ulp-scale tolerance of the oracle; quality
+against exact attention at cos >= 0.999, relL1 <= 0.02.
+"""
+import numpy as np
+import pytest
+
+from conftest import load_golden
+from test_oracle_attention import COS_MIN, RL1_MAX, SLACK, dense_attention, metrics, shaped, two_part_gate
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from quantibbler_amd import GpuContext
+
+    return GpuContext(0)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def shape_of(q, k, v):
+    from quantibbler_amd import AttentionShape
+
+    b, h, s, d = q.shape
+    return AttentionShape(b, h, k.shape[1], s, s, d, v.shape[3])
+
+
+def test_reference_scheme_fixture_battery(ctx, orc):
+    for rec in load_golden("attention_sage.json"):
+        q, k, v = (shaped(rec, n, t) for n, t in (("query", "q"), ("key", "k"), ("value", "v")))
+        say("sage ref fixture", rec["seed"], rec["shape"], rec["causal"], rec["block_size"])
+        out = ctx.attention_sage(shape_of(q, k, v), q, k, v, rec["causal"], rec["block_size"])
+        want = orc.attention_sage_dev(q, k, v, rec["causal"], rec["block_size"])
+        assert out.tobytes() == want.ravel().tobytes()
+        two_part_gate(out, rec["faces"]["quantized-reference"]["out"], rec["shape"]["val_dim"])
+        cos, rl1 = metrics(out, rec["faces"]["exact"]["out"])
+        ref = rec["reference_metrics"]
+        assert cos >= COS_MIN and rl1 <= RL1_MAX
+        assert cos >= ref["cosine"] - SLACK and rl1 <= ref["relative_l1"] + SLACK
+
+
+@pytest.mark.parametrize("b,h,hk,s,d,dv,causal,block", [
+    (1, 4, 2, 200, 64, 64, True, 64),
+    (2, 2, 1, 130, 128, 128, True, 64),
+    (1, 2, 2, 96, 32, 48, False, 16),
+    (1, 2, 1, 150, 16, 16, True, 100),   # blocks wider than one LDS chunk
+    (1, 1, 1, 70, 8, 8, False, 70),
+])
+def test_reference_scheme_random_bit_identical(ctx, orc, b, h, hk, s, d, dv, causal, block):
+    say("sage ref random", b, h, hk, s, d, dv, causal, block)
+    rng = np.random.default_rng(s + d + block)
+    q = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    k = (rng.standard_normal((b, hk, s, d)) + 2 * rng.standard_normal((b, hk, 1, d))).astype(np.float32)
+    v = rng.standard_normal((b, hk, s, dv)).astype(np.float32)
+    out = ctx.attention_sage(shape_of(q, k, v), q, k, v, causal, block)
+    want = orc.attention_sage_dev(q, k, v, causal, block)
+    assert out.tobytes() == want.ravel().tobytes()
+    npref = orc.attention_sage_np(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), causal, block)
+    two_part_gate(out, npref, dv)
+
+
+def test_reference_scheme_device_pointer_form(ctx, orc):
+    say("sage ref dev form")
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((1, 2, 64, 32)).astype(np.float32)
+    k = rng.standard_normal((1, 1, 64, 32)).astype(np.float32)
+    v = rng.standard_normal((1, 1, 64, 32)).astype(np.float32)
+    sh = shape_of(q, k, v)
+    qd, kd, vd = (torch.from_numpy(a).cuda() for a in (q, k, v))
+    od = torch.empty((1, 2, 64, 32), dtype=torch.float32, device="cuda")
+    ctx.attention_sage_dev(sh, qd, kd, vd, True, 8, od, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert od.cpu().numpy().tobytes() == orc.attention_sage_dev(q, k, v, True, 8).tobytes()
+
+
+def run_blk(ctx, qb, kb, vb, causal):
+    sh = shape_of(qb, kb, vb)
+    qd, kd, vd = (torch.from_numpy(a.view(np.int16)).cuda() for a in (qb, kb, vb))
+    od = torch.empty(qb.shape[:3] + (vb.shape[3],), dtype=torch.int16, device="cuda")
+    ws_n = ctx.sage_blk_workspace_size(sh)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    ctx.attention_sage_blk_dev(sh, qd, kd, vd, causal, od, ws, ws_n, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    return od.cpu().numpy().view(np.uint16)
+
+
+def blk_inputs(orc, rng, b, h, hk, s):
+    q = rng.standard_normal((b, h, s, 128)).astype(np.float32)
+    k = (rng.standard_normal((b, hk, s, 128)) + 2 * rng.standard_normal((b, hk, 1, 128))).astype(np.float32)
+    v = rng.standard_normal((b, hk, s, 128)).astype(np.float32)
+    return tuple(orc.f32_to_bf16_fast(a) for a in (q, k, v))
+
+
+@pytest.mark.parametrize("b,h,hk,s", [(1, 2, 2, 64), (1, 4, 2, 200), (2, 2, 1, 333), (1, 2, 1, 1024)])
+def test_blk_prepass_codes_bit_identical(ctx, orc, b, h, hk, s):
+    say("sage blk prepass", b, h, hk, s)
+    rng = np.random.default_rng(b * 100 + s)
+    qb, kb, vb = blk_inputs(orc, rng, b, h, hk, s)
+    _, st = orc.attention_sage_blk(qb, kb, vb, causal=True, stages=True)
+    sh = shape_of(qb, kb, vb)
+    nblk = (s + 63) // 64
+    qd, kd, vd = (torch.from_numpy(a.view(np.int16)).cuda() for a in (qb, kb, vb))
+    qh = torch.empty((b, h, s, 128), dtype=torch.int8, device="cuda")
+    kh = torch.empty((b, hk, s, 128), dtype=torch.int8, device="cuda")
+    qs = torch.empty((b, h, nblk), dtype=torch.float32, device="cuda")
+    ks = torch.empty((b, hk, nblk), dtype=torch.float32, device="cuda")
+    km = torch.empty((b, hk, 128), dtype=torch.float32, device="cuda")
+    vh = torch.empty((b, hk, s, 128), dtype=torch.int16, device="cuda")
+    ctx.sage_blk_quantize_dev(sh, qd, kd, vd, qh, qs, kh, ks, km, vh, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(qh.cpu().numpy(), st["qhat"])
+    assert np.array_equal(kh.cpu().numpy(), st["khat"])
+    assert qs.cpu().numpy().tobytes() == st["qscale"].tobytes()
+    assert ks.cpu().numpy().tobytes() == st["kscale"].tobytes()
+    assert km.cpu().numpy().tobytes() == st["kmean"].tobytes()
+    vf = orc.bf16_to_f32(vb)
+    assert np.array_equal(vh.cpu().numpy().view(np.float16).astype(np.float32), vf.astype(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("b,h,hk,s,causal", [
+    (1, 2, 2, 64, True), (1, 4, 2, 200, True), (2, 2, 1, 333, False), (1, 2, 1, 1024, True),
+    (1, 2, 2, 128, False),
+])
+def test_blk_attention_against_oracle_and_exact(ctx, orc, b, h, hk, s, causal):
+    say("sage blk attention", b, h, hk, s, causal)
+    rng = np.random.default_rng(b * 1000 + s + causal)
+    qb, kb, vb = blk_inputs(orc, rng, b, h, hk, s)
+    got = orc.bf16_to_f32(run_blk(ctx, qb, kb, vb, causal)).astype(np.float64)
+    want = orc.attention_sage_blk(qb, kb, vb, causal=causal).astype(np.float64)
+    # outputs are bf16: allow 2 bf16 ulps of each value plus a row-scale floor
+    rowmax = np.abs(want).max(axis=-1, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 2e-3 * rowmax)
+    c, r = metrics(got, want)
+    assert c > 0.99999 and r < 4e-3
+    exact = dense_attention(*(orc.bf16_to_f32(a).astype(np.float64) for a in (qb, kb, vb)), causal)
+    c, r = metrics(got, exact)
+    assert c >= COS_MIN and r <= RL1_MAX, (c, r)
+    again = orc.bf16_to_f32(run_blk(ctx, qb, kb, vb, causal)).astype(np.float64)
+    assert again.tobytes() == got.tobytes()
