@@ -68,8 +68,15 @@ def test_reference_scheme_random_bit_identical(ctx, orc, b, h, hk, s, d, dv, cau
     out = ctx.attention_sage(shape_of(q, k, v), q, k, v, causal, block)
     want = orc.attention_sage_dev(q, k, v, causal, block)
     assert out.tobytes() == want.ravel().tobytes()
+    # Against the f64 NumPy semantics the f32 scheme differs wherever an INT8
+    # code lands on the other side of a rounding boundary (the reference's
+    # 1e-4 gate is pinned on its fixture battery only), so the f64 form is a
+    # quality comparison here, as is exact attention.
     npref = orc.attention_sage_np(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), causal, block)
-    two_part_gate(out, npref, dv)
+    c, r = metrics(out, npref)
+    assert c > 0.99999 and r < 2e-3, (c, r)
+    c, r = metrics(out, dense_attention(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64), causal))
+    assert c >= COS_MIN and r <= RL1_MAX, (c, r)
 
 
 def test_reference_scheme_device_pointer_form(ctx, orc):
