@@ -35,7 +35,6 @@ HBM_PEAK = 8.0e12          # B/s
 BF16_PEAK = 2.5e15         # dense FLOP/s
 INT8_PEAK = 5.0e15         # dense OP/s
 LAYER_BYTES = 1_097_728    # BASELINE.md config 1, per layer
-STAGE_BYTES = LAYER_BYTES // 2
 M = N = 4096
 R = 1024
 METRIC = "factor-linear GB/s & %HBM peak (B=1); GEMM+SageAttn TFLOP/s & %MFMA peak"
@@ -72,26 +71,24 @@ def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
     ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
     st = torch.cuda.current_stream()
     for _ in range(warmup):
-        S.stage_dev(1, x, y, ws, ws_n, st)
-        S.stage_dev(2, x, y, ws, ws_n, st)
+        S.decode_dev(x, y, ws, ws_n, st)
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    # one event before each of the four phases and one after the last
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(st)
     for k in range(steps):
-        ev[k][0].record(st)
-        S.stage_dev(1, x, y, ws, ws_n, st)
-        ev[k][1].record(st)
-        S.stage_dev(2, x, y, ws, ws_n, st)
-        ev[k][2].record(st)
+        for ph in range(1, 5):
+            ev[k][ph - 1].record(st)
+            S.stage_dev(ph, x, y, ws, ws_n, st)
+        ev[k][4].record(st)
     end.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / steps
-    s1 = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
-    s2 = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
-    return dict(ms_per_step=ms_step, stage1_ms=s1, stage2_ms=s2, wall_s=wall, set=S)
+    phase_ms = [sum(e[p].elapsed_time(e[p + 1]) for e in ev) / steps for p in range(4)]
+    return dict(ms_per_step=ms_step, phase_ms=phase_ms, wall_s=wall, set=S)
 
 
 def bench_single_latency(torch, np, layer, iters=200):
@@ -217,12 +214,17 @@ def main():
     d = bench_decode(qa, ctx, torch, np, layers, args.steps, args.warmup)
     total_bytes = args.layers * LAYER_BYTES
     value = total_bytes / (d["ms_per_step"] * 1e-3) / 1e9
-    dom = 1 if d["stage1_ms"] >= d["stage2_ms"] else 2
-    dom_ms = d["stage1_ms"] if dom == 1 else d["stage2_ms"]
-    achieved = args.layers * STAGE_BYTES / (dom_ms * 1e-3) / 1e9
-    log(f"  decode: {d['ms_per_step']:.3f} ms/step, {value:.1f} GB/s; stage1 {d['stage1_ms']:.3f} ms, "
-        f"stage2 {d['stage2_ms']:.3f} ms")
-    extra = {"decode_stage_ms": {"stage1": round(d["stage1_ms"], 4), "stage2": round(d["stage2_ms"], 4)}}
+    ph = d["phase_ms"]
+    # algorithmic bytes per layer of each GEMV kernel (the preps carry x, s2)
+    gemv_bytes = {1: M * R // 8, 2: N * R // 8 + 4 * M + 2 * M}
+    dom = 1 if ph[1] >= ph[3] else 2
+    dom_ms = ph[1] if dom == 1 else ph[3]
+    bytes_launch = args.layers * gemv_bytes[dom]
+    achieved = bytes_launch / (dom_ms * 1e-3) / 1e9
+    log(f"  decode: {d['ms_per_step']:.3f} ms/step, {value:.1f} GB/s; phases (prep x, gemv 1, "
+        f"prep t, gemv 2) = {', '.join(f'{p:.4f}' for p in ph)} ms")
+    extra = {"decode_phase_ms": {"prep_x": round(ph[0], 4), "gemv_stage1": round(ph[1], 4),
+                                 "prep_t": round(ph[2], 4), "gemv_stage2": round(ph[3], 4)}}
     if not args.no_extra:
         log("single-layer latency ...")
         extra["decode_single_layer_us"] = round(bench_single_latency(torch, np, layers[0]), 2)
@@ -255,8 +257,8 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": None,
-            "kernel": f"gemv_kernel<{dom},false> (stage {dom})",
-            "bytes_per_launch": args.layers * STAGE_BYTES, "avg_launch_ms": round(dom_ms, 4),
+            "kernel": f"q4_gemv_kernel<{dom},*> (decode stage {dom}, fp4 x fp8 scaled MFMA)",
+            "bytes_per_launch": bytes_launch, "avg_launch_ms": round(dom_ms, 4),
         },
         "cpu_baseline": cpu,
         "extra": extra,

@@ -37,6 +37,14 @@ struct GemvLayer {
     const float *bias;      // stage 2: bias [rows]
 };
 
+// The same for the fp4-MFMA decode (bits in the fp4 decode layout).
+struct Q4Layer {
+    const uint32_t *bits;
+    const float *s_in;
+    const float *s_out;
+    const float *bias;
+};
+
 }  // namespace qbk
 
 struct qbk_factor {
@@ -47,8 +55,11 @@ struct qbk_factor {
     uint8_t *ub_rows, *vbt_rows;      // reference per-row bitplanes
     uint32_t *vt_gemv, *u_gemv;       // [r_p][din_w], [dout_p][r_w]
     uint32_t *vt_frag, *u_frag;       // [r_p/64][din_p/32][64], [dout_p/64][r_p/32][64]
+    size_t din_q, r_q;                // K of the fp4 decode layout: multiples of 128
+    uint32_t *vt_q4, *u_q4;           // [r_p/64][din_q/128][64][4], [dout_p/64][r_q/128][64][4]
     float *s1, *s2, *bias;            // dout, din, dout (zeros when absent)
     qbk::GemvLayer *gemv_tab;  // device: [0] stage 1, [1] stage 2
+    void *q4_tab;              // device Q4Layer[2]: [0] stage 1, [1] stage 2
     std::vector<void *> allocs;
 };
 
@@ -99,6 +110,36 @@ static void repack_frag(const uint8_t *rows, size_t n_rows, size_t n_bits, size_
                 }
                 out[(g * ns + s) * 64 + l] = w;
             }
+}
+
+// fp4 decode layout.  The scaled 16x16x128 MFMA with an fp4 A operand gives
+// lane group g = l/16 the 32 elements k = kq4(g, e) of a 128-k slice, and an
+// fp8 B operand gives group g the elements 32g .. 32g+31 (measured pairing).
+__host__ __device__ inline int kq4(int g, int e) {
+    return 16 * (g >> 1) + 64 * (g & 1) + (e & 15) + 32 * (e >> 4);
+}
+// Word for (row group rg, slice s, lane l, row tile rt): element e of row
+// 64rg + 16rt + l%16 is stored at bit 4*(e%8) + e/8, set when the sign is -1,
+// so VGPR v of the fp4 operand is one v_bfi of (word << (3 - v)) into
+// 0x22222222 (fp4 e2m1 +1.0 = 0x2, -1.0 = 0xA).
+static void repack_q4(const uint8_t *rows, size_t n_rows, size_t n_bits, size_t rows_p,
+                      size_t bits_q, uint32_t *out) {
+    size_t rw = div_ceil(n_bits, 8);
+    size_t ns = bits_q / 128, ng = rows_p / 64;
+    memset(out, 0, ng * ns * 64 * 4 * 4);
+    for (size_t rg = 0; rg < ng; rg++)
+        for (size_t s = 0; s < ns; s++)
+            for (int l = 0; l < 64; l++)
+                for (int rt = 0; rt < 4; rt++) {
+                    size_t i = 64 * rg + 16 * rt + (l & 15);
+                    if (i >= n_rows) continue;
+                    uint32_t w = 0;
+                    for (int e = 0; e < 32; e++) {
+                        size_t k = 128 * s + kq4(l >> 4, e);
+                        if (k < n_bits && !rbit(rows, rw, i, k)) w |= 1u << (4 * (e & 7) + (e >> 3));
+                    }
+                    out[((rg * ns + s) * 64 + l) * 4 + rt] = w;
+                }
 }
 
 // engine/mod.rs:258-289 container_to_rows / container_to_rows_transposed.
@@ -164,6 +205,11 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
     std::vector<uint32_t> vf(L->r_p / 64 * L->din_p / 32 * 64), uf(L->dout_p / 64 * L->r_p / 32 * 64);
     repack_frag(vbt_rows, r, din, L->r_p, L->din_p, vf.data());
     repack_frag(ub_rows, dout, r, L->dout_p, L->r_p, uf.data());
+    L->din_q = round_up(din, 128);
+    L->r_q = round_up(r, 128);
+    std::vector<uint32_t> vq(L->r_p / 64 * L->din_q / 128 * 256), uq(L->dout_p / 64 * L->r_q / 128 * 256);
+    repack_q4(vbt_rows, r, din, L->r_p, L->din_q, vq.data());
+    repack_q4(ub_rows, dout, r, L->dout_p, L->r_q, uq.data());
     std::vector<float> zb(dout, 0.0f);
     void *p;
 #define UP(field, src, n)                                                  \
@@ -178,11 +224,15 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
     UP(u_gemv, ug.data(), ug.size() * 4);
     UP(vt_frag, vf.data(), vf.size() * 4);
     UP(u_frag, uf.data(), uf.size() * 4);
+    UP(vt_q4, vq.data(), vq.size() * 4);
+    UP(u_q4, uq.data(), uq.size() * 4);
     UP(s1, s1, dout * 4);
     UP(s2, s2, din * 4);
     UP(bias, bias ? bias : zb.data(), dout * 4);
     GemvLayer tab[2] = {{L->vt_gemv, L->s2, nullptr, nullptr}, {L->u_gemv, nullptr, L->s1, L->bias}};
     UP(gemv_tab, tab, sizeof tab);
+    Q4Layer qtab[2] = {{L->vt_q4, L->s2, nullptr, nullptr}, {L->u_q4, nullptr, L->s1, L->bias}};
+    UP(q4_tab, qtab, sizeof qtab);
 #undef UP
     *out = L;
     return QBK_OK;
@@ -329,10 +379,10 @@ struct GemmArgs {
     const void *x;          // [N][ldx] bf16 or f32
     size_t ldx;
     const float *s2;
-    // stage 2 source: partials [nsplit][N][ldp] f32
-    const float *part_in;
-    int nsplit_in;
-    size_t ldp;
+    int vec_ok;             // x rows and s2 allow 16-byte loads
+    // stage 2 source: t bf16 [N][ldt], zero for k >= r
+    const uint16_t *t_in;
+    size_t ldt;
     // outputs
     float *part_out;        // stage 1: [split][N][M_p]
     void *y_out;            // stage 2: [N][ldy]
@@ -382,35 +432,54 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs A) {
             if (ci >= CHUNKS) break;
             int nn = ci / (GBK / 8), kk = (ci % (GBK / 8)) * 8;
             size_t n = n0 + nn, k = k0 + kk;
-            uint16_t v[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = 0;
-            if (n < A.N) {
-                if (STAGE == 1) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        size_t kk2 = k + e;
-                        if (kk2 < A.k_valid) {
-                            float xv = XF32 ? ((const float *)A.x)[n * A.ldx + kk2]
-                                            : bf16_to_f32(((const uint16_t *)A.x)[n * A.ldx + kk2]);
-                            v[e] = f32_to_bf16(A.s2[kk2] * xv);
-                        }
-                    }
+            if (n >= A.N) {
+                breg[c][0] = breg[c][1] = breg[c][2] = breg[c][3] = 0;
+                continue;
+            }
+            if (STAGE == 2) {
+                // t (bf16, zero beyond r) written by the split-K reduction
+                uint4 tv = *(const uint4 *)(A.t_in + n * A.ldt + k);
+                breg[c][0] = tv.x;
+                breg[c][1] = tv.y;
+                breg[c][2] = tv.z;
+                breg[c][3] = tv.w;
+                continue;
+            }
+            float xv[8], sv[8];
+            if (A.vec_ok && k + 8 <= A.k_valid) {
+                if (XF32) {
+                    const float4 *xp = (const float4 *)((const float *)A.x + n * A.ldx + k);
+                    float4 a0 = xp[0], a1 = xp[1];
+                    xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
+                    xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
                 } else {
+                    uint4 xb = *(const uint4 *)((const uint16_t *)A.x + n * A.ldx + k);
+                    uint32_t w4[4] = {xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        size_t kk2 = k + e;
-                        if (kk2 < A.k_valid) {
-                            float s = 0.0f;
-                            for (int sp = 0; sp < A.nsplit_in; sp++)
-                                s += A.part_in[((size_t)sp * A.N + n) * A.ldp + kk2];
-                            v[e] = f32_to_bf16(s);
-                        }
+                    for (int e = 0; e < 4; e++) {
+                        xv[2 * e] = __uint_as_float(w4[e] << 16);
+                        xv[2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
                     }
+                }
+                const float4 *sp = (const float4 *)(A.s2 + k);
+                float4 b0 = sp[0], b1 = sp[1];
+                sv[0] = b0.x; sv[1] = b0.y; sv[2] = b0.z; sv[3] = b0.w;
+                sv[4] = b1.x; sv[5] = b1.y; sv[6] = b1.z; sv[7] = b1.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    size_t kk2 = k + e;
+                    bool ok = kk2 < A.k_valid;
+                    xv[e] = !ok ? 0.0f
+                                : XF32 ? ((const float *)A.x)[n * A.ldx + kk2]
+                                       : bf16_to_f32(((const uint16_t *)A.x)[n * A.ldx + kk2]);
+                    sv[e] = ok ? A.s2[kk2] : 0.0f;
                 }
             }
 #pragma unroll
-            for (int e = 0; e < 4; e++) breg[c][e] = (uint32_t)v[2 * e] | ((uint32_t)v[2 * e + 1] << 16);
+            for (int e = 0; e < 4; e++)
+                breg[c][e] = (uint32_t)f32_to_bf16(sv[2 * e] * xv[2 * e]) |
+                             ((uint32_t)f32_to_bf16(sv[2 * e + 1] * xv[2 * e + 1]) << 16);
         }
     };
     auto store_b = [&](int buf) {
@@ -507,6 +576,216 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs A) {
 }
 
 // ------------------------------------------------------------------------
+// decode GEMV on the scaled fp4 x fp8 MFMA (batch 1..8)
+// ------------------------------------------------------------------------
+//
+// out[i] = sum_k s(i,k) a_k as C = A.B with v_mfma_scale_f32_16x16x128_f8f6f4:
+// A = the +-1 signs as fp4 e2m1 (exact), built from the bits with one shift
+// and one v_bfi per 8 weights; B = the activations split exactly into two
+// fp8 e4m3 columns, a = hi*2^e_hi + lo*2^e_lo, with one E8M0 scale per
+// 32-element block and column (a bf16 value has 8 significant bits: hi keeps
+// the top 4, lo the rest).  Token b of a decode batch uses columns 2b, 2b+1;
+// the product sums exactly-represented terms in f32, and out = C[.,2b] +
+// C[.,2b+1].  Each 128-k slice of a 16-row tile is one MFMA over 256 bytes
+// of packed signs.
+
+#define Q4_MAXB 8
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+// B operand of one (layer, slice, lane group, column): 32 fp8 bytes + scale.
+struct Q4Args {
+    const Q4Layer *layers;
+    size_t rows_p, rows_valid, k_valid, ns;  // ns = K_q / 128
+    int batch, ncol;                          // ncol = 2 * batch
+    const void *act;                          // stage 1: x bf16 [layer][batch][ldx]; stage 2: t bf16
+    size_t act_ld, act_layer;                 // elements per token row, per layer
+    uint8_t *bop;                             // [layer][ns][4][ncol][32]
+    uint8_t *bsc;                             // [layer][ns][4][ncol]
+    void *out;                                // stage 1: t bf16 [layer][batch][out_ld]; stage 2: y
+    size_t out_ld, out_layer;
+    int y_bf16;
+};
+
+__device__ __forceinline__ int e8m0_of(float amax) {
+    // exponent so that amax * 2^-e lies in [128, 256): e = floor(log2 amax) - 7
+    int ex = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
+    int e = ex - 7;
+    return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+__device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+// One thread per (layer, token, slice, lane group): the 32 activations of
+// that k block become the hi and lo fp8 columns of the token.
+template <int STAGE, bool XF32>
+__global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a, size_t n_items) {
+    size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (it >= n_items) return;
+    const int g = it & 3;
+    size_t rest = it >> 2;
+    const size_t s = rest % a.ns;
+    rest /= a.ns;
+    const int b = (int)(rest % a.batch);
+    const size_t li = rest / a.batch;
+    const Q4Layer L = a.layers[li];
+    const size_t off = li * a.act_layer + (size_t)b * a.act_ld;
+    const uint16_t *src = (const uint16_t *)a.act + off;
+    const float *srcf = (const float *)a.act + off;
+    // The E8M0 scale given by lane group g covers the activations
+    // k = 128s + kq4(g, e) (measured): two 16-element runs, held in B lane
+    // groups 2(g&1) and 2(g&1)+1 at byte offset 16(g>>1).
+    const size_t k0 = 128 * s + 16 * (g >> 1) + 64 * (g & 1);
+    float z[32];
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; e++) {
+        size_t k = k0 + (e & 15) + 32 * (e >> 4);
+        float v = 0.0f;
+        if (k < a.k_valid) {
+            if (STAGE == 1)
+                v = bf16_to_f32(f32_to_bf16(L.s_in[k] * (XF32 ? srcf[k] : bf16_to_f32(src[k]))));
+            else
+                v = bf16_to_f32(src[k]);
+        }
+        z[e] = v;
+        amax = fmaxf(amax, fabsf(v));
+    }
+    const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+    const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+    uint32_t hw[8];
+    float rmax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
+        hw[q] = (uint32_t)w;
+        const float back[4] = {__builtin_amdgcn_cvt_f32_fp8(w, 0), __builtin_amdgcn_cvt_f32_fp8(w, 1),
+                               __builtin_amdgcn_cvt_f32_fp8(w, 2), __builtin_amdgcn_cvt_f32_fp8(w, 3)};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            z[4 * q + u] = z[4 * q + u] - back[u] * sc_hi;  // exact residual
+            rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
+        }
+    }
+    const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+    const float inv_lo = pow2f(-e_lo);
+    uint32_t lw[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
+        lw[q] = (uint32_t)w;
+    }
+    // bytes of elements e < 16 go to B lane group gb, e >= 16 to gb + 1
+    const size_t gb = 2 * (g & 1), boff = 16 * (g >> 1);
+    const size_t slot0 = ((li * a.ns + s) * 4 + gb) * a.ncol + 2 * b;      // (group gb, hi column)
+    const size_t slot1 = ((li * a.ns + s) * 4 + gb + 1) * a.ncol + 2 * b;  // (group gb+1, hi column)
+    *(uint4 *)(a.bop + slot0 * 32 + boff) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(a.bop + slot1 * 32 + boff) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    *(uint4 *)(a.bop + (slot0 + 1) * 32 + boff) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    *(uint4 *)(a.bop + (slot1 + 1) * 32 + boff) = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    const size_t sc = ((li * a.ns + s) * 4 + g) * a.ncol + 2 * b;
+    a.bsc[sc] = (uint8_t)(e_hi + 127);
+    a.bsc[sc + 1] = (uint8_t)(e_lo + 127);
+}
+
+// Workgroup = 4 waves; KSPLIT waves share a 64-row group and split its
+// slices, 4/KSPLIT row groups per workgroup.  Lane l loads the 16 bytes of
+// its four row tiles' sign words per slice (1 KiB per wave, contiguous).
+template <int STAGE, int KSPLIT>
+__global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
+    __shared__ f32x4_t red[KSPLIT > 1 ? 4 : 1][4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t li = blockIdx.y;
+    const Q4Layer L = a.layers[li];
+    constexpr int RG_PER_WG = 4 / KSPLIT;
+    const size_t rg = (size_t)blockIdx.x * RG_PER_WG + wave / KSPLIT;
+    const int ks = wave % KSPLIT;
+    const size_t n_rg = a.rows_p / 64;
+    const size_t per = (a.ns + KSPLIT - 1) / KSPLIT;
+    const size_t s0 = ks * per, s1 = s0 + per < a.ns ? s0 + per : a.ns;
+    const int col = lane & 15, g = lane >> 4;
+    const bool bcol = col < a.ncol;
+
+    f32x4_t acc[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
+    if (rg < n_rg) {
+        const uint4 *wp = (const uint4 *)L.bits + (rg * a.ns) * 64 + lane;
+        const uint8_t *bp = a.bop + (li * a.ns * 4 + g) * a.ncol * 32 + col * 32;
+        const uint8_t *sp = a.bsc + (li * a.ns * 4 + g) * a.ncol + col;
+        const size_t bstride = 4 * a.ncol * 32, sstride = 4 * a.ncol;
+        for (size_t s = s0; s < s1; s++) {
+            uint4 w4 = wp[s * 64];
+            i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
+            int bs = 127;
+            if (bcol) {
+                const uint4 *bq = (const uint4 *)(bp + s * bstride);
+                uint4 b0 = bq[0], b1 = bq[1];
+                bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                             (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+                bs = sp[s * sstride];
+            }
+            uint32_t wr[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int rt = 0; rt < 4; rt++) {
+                const uint32_t w = wr[rt];
+                i32x8_t av;
+                av[0] = (int)(((w << 3) & 0x88888888u) | 0x22222222u);
+                av[1] = (int)(((w << 2) & 0x88888888u) | 0x22222222u);
+                av[2] = (int)(((w << 1) & 0x88888888u) | 0x22222222u);
+                av[3] = (int)((w & 0x88888888u) | 0x22222222u);
+                av[4] = av[5] = av[6] = av[7] = 0;
+                acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[rt], 4, 0, 0, 127,
+                                                                          0, bs);
+            }
+        }
+    }
+    if (KSPLIT > 1) {
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) red[wave][rt][lane] = acc[rt];
+        __syncthreads();
+        if (ks != 0) return;
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) {
+            f32x4_t v = red[wave][rt][lane];
+            for (int q = 1; q < KSPLIT; q++) v += red[wave + q][rt][lane];
+            acc[rt] = v;
+        }
+    }
+    if (rg >= n_rg) return;
+    // hi + lo: lane col 2b holds hi, col 2b+1 holds lo for rows 4g+i
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) {
+        f32x4_t v = acc[rt];
+        f32x4_t lo;
+#pragma unroll
+        for (int i = 0; i < 4; i++) lo[i] = __shfl_down(v[i], 1, 64);
+        if ((col & 1) == 0 && col < a.ncol) {
+            const int b = col >> 1;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const size_t row = rg * 64 + 16 * rt + 4 * g + i;
+                const float sum = v[i] + lo[i];
+                if (STAGE == 1) {
+                    ((uint16_t *)a.out)[li * a.out_layer + (size_t)b * a.out_ld + row] =
+                        row < a.rows_valid ? f32_to_bf16(sum) : (uint16_t)0;
+                } else if (row < a.rows_valid) {
+                    float u = bf16_to_f32(f32_to_bf16(sum));
+                    float y = u * L.s_out[row] + L.bias[row];
+                    size_t o = li * a.out_layer + (size_t)b * a.out_ld + row;
+                    if (a.y_bf16)
+                        ((uint16_t *)a.out)[o] = f32_to_bf16(y);
+                    else
+                        ((float *)a.out)[o] = y;
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------
 // host orchestration
 // ------------------------------------------------------------------------
 
@@ -518,9 +797,44 @@ static int splitk_for(const qbk_factor *L, size_t batch, int num_cus) {
     return s;
 }
 
+// batch 1: t bf16 [r_p].  batch > 1: f32 partials [split][batch][r_p], then
+// t bf16 [batch][r_p].
+static size_t q4_ws(const qbk_factor *L, size_t n_layers, size_t batch);
+
+// batch <= Q4_MAXB: the fp4 decode's operand buffers (q4_plan).  Larger
+// batches: f32 partials [split][batch][r_p], then t bf16 [batch][r_p].
 static size_t ws_bytes(const qbk_factor *L, size_t batch, int split) {
-    if (batch <= 1) return L->r_p * 2 + 256;
-    return (size_t)split * batch * L->r_p * 4 + 256;
+    if (batch <= Q4_MAXB) return q4_ws(L, 1, batch);
+    return round_up((size_t)split * batch * L->r_p * 4, 256) + batch * L->r_p * 2 + 256;
+}
+
+// Sum the split-K partials in split order, round to bf16, zero k >= r.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float *__restrict__ part,
+                                                            int split, size_t stride,
+                                                            size_t ld, size_t r,
+                                                            uint16_t *__restrict__ t,
+                                                            size_t chunks) {
+    size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    size_t e0 = c * 8, k0 = e0 % ld;
+    float v[8];
+    const float4 *p0 = (const float4 *)(part + e0);
+    float4 a = p0[0], b = p0[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    for (int s = 1; s < split; s++) {
+        const float4 *ps = (const float4 *)(part + (size_t)s * stride + e0);
+        float4 c0 = ps[0], c1 = ps[1];
+        v[0] += c0.x; v[1] += c0.y; v[2] += c0.z; v[3] += c0.w;
+        v[4] += c1.x; v[5] += c1.y; v[6] += c1.z; v[7] += c1.w;
+    }
+    uint32_t w[4];
+    for (int e = 0; e < 4; e++) {
+        uint32_t lo = k0 + 2 * e < r ? f32_to_bf16(v[2 * e]) : 0;
+        uint32_t hi = k0 + 2 * e + 1 < r ? f32_to_bf16(v[2 * e + 1]) : 0;
+        w[e] = lo | (hi << 16);
+    }
+    *(uint4 *)(t + e0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // One GEMV stage over n_layers layers of one shape (table entries
@@ -566,6 +880,119 @@ static int run_gemv(const qbk_factor *L, const void *x, bool xf32, void *y, bool
     return launch_gemv_stage(2, false, L, L->gemv_tab + 1, 1, ws, 0, y, 0, ybf16, s);
 }
 
+// Workspace of the fp4 decode for n_layers layers of L's shape at `batch`:
+// [bop1 | bsc1 | t | bop2 | bsc2], each region 256-byte aligned.
+struct Q4Plan {
+    size_t ns1, ns2, ncol;
+    size_t o_bop1, o_bsc1, o_t, o_bop2, o_bsc2, bytes;
+};
+
+static Q4Plan q4_plan(const qbk_factor *L, size_t n_layers, size_t batch) {
+    Q4Plan p{};
+    p.ns1 = L->din_q / 128;
+    p.ns2 = L->r_q / 128;
+    p.ncol = 2 * batch;
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        size_t o = off;
+        off += round_up(n, 256);
+        return o;
+    };
+    p.o_bop1 = take(n_layers * p.ns1 * 4 * p.ncol * 32);
+    p.o_bsc1 = take(n_layers * p.ns1 * 4 * p.ncol);
+    p.o_t = take(n_layers * batch * L->r_p * 2);
+    p.o_bop2 = take(n_layers * p.ns2 * 4 * p.ncol * 32);
+    p.o_bsc2 = take(n_layers * p.ns2 * 4 * p.ncol);
+    p.bytes = off;
+    return p;
+}
+
+static size_t q4_ws(const qbk_factor *L, size_t n_layers, size_t batch) {
+    return q4_plan(L, n_layers, batch).bytes;
+}
+
+static int q4_ksplit(size_t ns) { return ns >= 16 ? 4 : (ns >= 8 ? 2 : 1); }
+
+// phase 1: x -> fp8 B operands; 2: stage-1 MFMA GEMV -> t; 3: t -> B
+// operands; 4: stage-2 MFMA GEMV -> y.  x: [n][batch][din] (bf16, or f32 when
+// xf32), y: [n][batch][dout].
+static int q4_phase(int phase, const qbk_factor *L, const Q4Layer *tab, size_t n_layers,
+                    size_t batch, const void *x, bool xf32, void *y, bool ybf16, void *ws,
+                    hipStream_t s) {
+    Q4Plan p = q4_plan(L, n_layers, batch);
+    char *w = (char *)ws;
+    Q4Args a{};
+    a.batch = (int)batch;
+    a.ncol = (int)p.ncol;
+    a.y_bf16 = ybf16;
+    if (phase <= 2) {
+        a.layers = tab;
+        a.rows_p = L->r_p;
+        a.rows_valid = L->r;
+        a.k_valid = L->din;
+        a.ns = p.ns1;
+        a.act = x;
+        a.act_ld = L->din;
+        a.act_layer = batch * L->din;
+        a.bop = (uint8_t *)(w + p.o_bop1);
+        a.bsc = (uint8_t *)(w + p.o_bsc1);
+        a.out = w + p.o_t;
+        a.out_ld = L->r_p;
+        a.out_layer = batch * L->r_p;
+    } else {
+        a.layers = tab + n_layers;
+        a.rows_p = L->dout_p;
+        a.rows_valid = L->dout;
+        a.k_valid = L->r;
+        a.ns = p.ns2;
+        a.act = w + p.o_t;
+        a.act_ld = L->r_p;
+        a.act_layer = batch * L->r_p;
+        a.bop = (uint8_t *)(w + p.o_bop2);
+        a.bsc = (uint8_t *)(w + p.o_bsc2);
+        a.out = y;
+        a.out_ld = L->dout;
+        a.out_layer = batch * L->dout;
+    }
+    if (phase == 1 || phase == 3) {
+        size_t items = n_layers * batch * a.ns * 4;
+        dim3 g((unsigned)div_ceil(items, 256));
+        if (phase == 1 && xf32)
+            hipLaunchKernelGGL((q4_prep_kernel<1, true>), g, dim3(256), 0, s, a, items);
+        else if (phase == 1)
+            hipLaunchKernelGGL((q4_prep_kernel<1, false>), g, dim3(256), 0, s, a, items);
+        else
+            hipLaunchKernelGGL((q4_prep_kernel<2, false>), g, dim3(256), 0, s, a, items);
+    } else {
+        const int ksplit = q4_ksplit(a.ns);
+        const size_t n_rg = a.rows_p / 64, rg_per_wg = 4 / ksplit;
+        dim3 g((unsigned)div_ceil(n_rg, rg_per_wg), (unsigned)n_layers);
+#define Q4_LAUNCH(ST)                                                                          \
+    if (ksplit == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, 4>), g, dim3(256), 0, s, a);       \
+    else if (ksplit == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, 2>), g, dim3(256), 0, s, a);  \
+    else hipLaunchKernelGGL((q4_gemv_kernel<ST, 1>), g, dim3(256), 0, s, a);
+        if (phase == 2) {
+            Q4_LAUNCH(1)
+        } else {
+            Q4_LAUNCH(2)
+        }
+#undef Q4_LAUNCH
+    }
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+static int run_q4(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y,
+                  bool ybf16, void *ws, hipStream_t s) {
+    // a single layer's table is {stage 1, stage 2}: tab + n_layers is stage 2
+    const Q4Layer *tab = (const Q4Layer *)L->q4_tab;
+    for (int ph = 1; ph <= 4; ph++) {
+        int rc = q4_phase(ph, L, tab, 1, batch, x, xf32, y, ybf16, ws, s);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
+
 template <int STAGE, bool XF32>
 static void launch_gemm_cfg(const GemmArgs &a, size_t N, int split, hipStream_t s) {
     if (N <= 32) {
@@ -591,6 +1018,7 @@ static int run_gemm(const qbk_factor *L, const void *x, bool xf32, size_t N, voi
     a.x = x;
     a.ldx = L->din;
     a.s2 = L->s2;
+    a.vec_ok = (L->din % 8) == 0;
     a.part_out = (float *)ws;
     a.k_per_split = round_up(div_ceil(L->din_p, split), GBK);
     bool small = N <= 32;
@@ -606,6 +1034,12 @@ static int run_gemm(const qbk_factor *L, const void *x, bool xf32, size_t N, voi
             hipLaunchKernelGGL((gemm_kernel<1, false, 2, 2, 128>), g, dim3(256), 0, s, a);
     }
     QBK_HIP(hipGetLastError());
+    // t = bf16(sum of the split partials), zero for k >= r
+    uint16_t *tb = (uint16_t *)((char *)ws + round_up((size_t)split * N * L->r_p * 4, 256));
+    size_t chunks = N * L->r_p / 8;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)div_ceil(chunks, 256)), dim3(256), 0, s,
+                       (const float *)ws, split, N * L->r_p, L->r_p, L->r, tb, chunks);
+    QBK_HIP(hipGetLastError());
     GemmArgs b{};
     b.frag = L->u_frag;
     b.M_p = L->dout_p;
@@ -613,9 +1047,8 @@ static int run_gemm(const qbk_factor *L, const void *x, bool xf32, size_t N, voi
     b.M_valid = L->dout;
     b.N = N;
     b.k_valid = L->r;
-    b.part_in = (const float *)ws;
-    b.nsplit_in = split;
-    b.ldp = L->r_p;
+    b.t_in = tb;
+    b.ldt = L->r_p;
     b.y_out = y;
     b.ldy = L->dout;
     b.s1 = L->s1;
@@ -638,7 +1071,7 @@ using namespace qbk;
 struct qbk_factor_set {
     int device;
     size_t n, dout, din, r, r_p;
-    GemvLayer *d1, *d2;  // device tables: stage 1 entries, stage 2 entries
+    Q4Layer *d1, *d2;  // device table: [0, n) stage 1 entries, [n, 2n) stage 2 (d2 = d1 + n)
     const qbk_factor *first;
 };
 
@@ -769,7 +1202,7 @@ int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *L, const uint16_t *x, 
                     fmt("workspace of %zu bytes is smaller than the %zu this call needs",
                         workspace_size, need));
     hipStream_t s = (hipStream_t)stream;
-    if (batch == 1) return run_gemv(L, x, false, y, y_dtype == QBK_BF16, workspace, s);
+    if (batch <= Q4_MAXB) return run_q4(L, batch, x, false, y, y_dtype == QBK_BF16, workspace, s);
     return run_gemm(L, x, false, batch, y, y_dtype == QBK_BF16, workspace, split, s);
 }
 
@@ -816,8 +1249,8 @@ int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *L, int serving, const float
         (rc = dws.alloc(ws_bytes(L, batch, split))))
         return rc;
     QBK_HIP(hipMemcpyAsync(dx.p, x, batch * L->din * 4, hipMemcpyHostToDevice, cs.s));
-    if (batch == 1)
-        rc = run_gemv(L, dx.p, true, dy.p, false, dws.p, cs.s);
+    if (batch <= Q4_MAXB)
+        rc = run_q4(L, batch, dx.p, true, dy.p, false, dws.p, cs.s);
     else
         rc = run_gemm(L, dx.p, true, batch, dy.p, false, dws.p, split, cs.s);
     if (rc) return rc;
@@ -840,13 +1273,13 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
                             i, f->dout, f->din, f->r));
     }
     if ((rc = bind(ctx))) return rc;
-    std::vector<GemvLayer> h(2 * n);
+    std::vector<Q4Layer> h(2 * n);
     for (size_t i = 0; i < n; i++) {
         const qbk_factor *L = layers[i];
         if (L->device != ctx->device)
             return fail(QBK_ERR_VALIDATION, fmt("layer %zu lives on another device", i));
-        h[i] = GemvLayer{L->vt_gemv, L->s2, nullptr, nullptr};
-        h[n + i] = GemvLayer{L->u_gemv, nullptr, L->s1, L->bias};
+        h[i] = Q4Layer{L->vt_q4, L->s2, nullptr, nullptr};
+        h[n + i] = Q4Layer{L->u_q4, nullptr, L->s1, L->bias};
     }
     qbk_factor_set *S = new qbk_factor_set();
     S->device = ctx->device;
@@ -856,13 +1289,13 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
     S->r = f->r;
     S->r_p = f->r_p;
     S->first = f;
-    hipError_t e1 = hipMalloc((void **)&S->d1, 2 * n * sizeof(GemvLayer));
+    hipError_t e1 = hipMalloc((void **)&S->d1, 2 * n * sizeof(Q4Layer));
     if (e1 != hipSuccess) {
         delete S;
         return fail(QBK_ERR_DEVICE, fmt("hipMalloc failed: %s", hipGetErrorString(e1)));
     }
     S->d2 = S->d1 + n;
-    e1 = hipMemcpy(S->d1, h.data(), 2 * n * sizeof(GemvLayer), hipMemcpyHostToDevice);
+    e1 = hipMemcpy(S->d1, h.data(), 2 * n * sizeof(Q4Layer), hipMemcpyHostToDevice);
     if (e1 != hipSuccess) {
         (void)hipFree(S->d1);
         delete S;
@@ -883,7 +1316,7 @@ void qbk_factor_set_destroy(qbk_factor_set *S) {
 }
 
 size_t qbk_factor_set_workspace_size(const qbk_factor_set *S) {
-    return S ? S->n * (S->r_p * 2) + 256 : 0;
+    return S ? q4_ws(S->first, S->n, 1) : 0;
 }
 
 // x [n][din] bf16 -> t (workspace, [n][r_p] bf16) -> y [n][dout] bf16.
@@ -891,25 +1324,24 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, c
                              uint16_t *y, void *workspace, size_t workspace_size, void *stream) {
     int rc;
     if (!S) return fail(QBK_ERR_VALIDATION, "null layer set");
-    if (stage != 1 && stage != 2) return fail(QBK_ERR_VALIDATION, fmt("stage must be 1 or 2, got %d", stage));
+    if (stage < 1 || stage > 4)
+        return fail(QBK_ERR_VALIDATION, fmt("stage must be 1..4, got %d", stage));
     if ((rc = bind(ctx))) return rc;
     if (workspace_size < qbk_factor_set_workspace_size(S))
         return fail(QBK_ERR_VALIDATION,
                     fmt("workspace of %zu bytes is smaller than the %zu this call needs",
                         workspace_size, qbk_factor_set_workspace_size(S)));
-    hipStream_t s = (hipStream_t)stream;
-    if (stage == 1)
-        return launch_gemv_stage(1, false, S->first, S->d1, S->n, x, S->din, workspace, S->r_p,
-                                 false, s);
-    return launch_gemv_stage(2, false, S->first, S->d2, S->n, workspace, S->r_p, y, S->dout, true,
-                             s);
+    return q4_phase(stage, S->first, (const Q4Layer *)S->d1, S->n, 1, x, false, y, true, workspace,
+                    (hipStream_t)stream);
 }
 
 int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *S, const uint16_t *x,
                               uint16_t *y, void *workspace, size_t workspace_size, void *stream) {
-    int rc = qbk_factor_set_stage_dev(ctx, S, 1, x, y, workspace, workspace_size, stream);
-    if (rc) return rc;
-    return qbk_factor_set_stage_dev(ctx, S, 2, x, y, workspace, workspace_size, stream);
+    for (int ph = 1; ph <= 4; ph++) {
+        int rc = qbk_factor_set_stage_dev(ctx, S, ph, x, y, workspace, workspace_size, stream);
+        if (rc) return rc;
+    }
+    return QBK_OK;
 }
 
 }  // extern "C"

@@ -474,6 +474,8 @@ static int run_ref(const qbk_attn_shape *s, const float *q, const float *k, cons
 #define BQ 128   // query rows per workgroup (4 waves x 32)
 #define HD 128   // head_dim == val_dim
 #define LOG2E_F 1.44269504088896341f
+#define KS_PITCH 144  // bytes per K^ row in LDS (128 + 16 pad)
+#define VS_PITCH 72   // fp16 per V^T row in LDS (64 + 8 pad)
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -607,8 +609,10 @@ __global__ void __launch_bounds__(256) blk_qquant(BlkArgs a) {
 //                  4*(l/16)+e of key tile 2c (e<4) or 16 + 4*(l/16)+(e-4)
 //                  of key tile 2c+1, and V^T is read with the same map.
 __global__ void __launch_bounds__(256) blk_attn(BlkArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t ks[2][BLK * HD];
-    __shared__ __attribute__((aligned(16))) uint16_t vs[2][HD * BLK];
+    // LDS rows padded to 144 bytes: the 16 lanes of a fragment read rows
+    // 144 B apart, which lands them on disjoint bank groups.
+    __shared__ __attribute__((aligned(16))) int8_t ks[2][BLK * KS_PITCH];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[2][HD * VS_PITCH];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
     const size_t bk = b * a.Hk + h / (a.H / a.Hk);
@@ -641,20 +645,35 @@ __global__ void __launch_bounds__(256) blk_attn(BlkArgs a) {
     size_t wlast = qw + 31 < a.S - 1 ? qw + 31 : a.S - 1;
     const size_t wave_kb_end = a.causal ? wlast / BLK + 1 : a.nblk;
 
-    auto load_tile = [&](int buf, size_t kb) {
+    // Next tile staged in registers: the global loads are issued before the
+    // block's math and written to LDS after it, so their latency overlaps
+    // the MFMA/softmax work.  K^ tile: 512 x 16 B chunks (2 per thread),
+    // V^T tile: 1024 x 16 B chunks (4 per thread).
+    uint4 kreg[2], vreg[4];
+    auto fetch_tile = [&](size_t kb) {
         const uint4 *ksrc = (const uint4 *)(a.khat + (bk * a.Sp + kb * BLK) * HD);
-        uint4 *kdst = (uint4 *)ks[buf];
-        for (int x = tid; x < BLK * HD / 16; x += 256) kdst[x] = ksrc[x];
+        for (int u = 0; u < 2; u++) kreg[u] = ksrc[tid + 256 * u];
         const uint4 *vsrc = (const uint4 *)(a.vt + (bk * a.nblk + kb) * HD * BLK);
-        uint4 *vdst = (uint4 *)vs[buf];
-        for (int x = tid; x < HD * BLK * 2 / 16; x += 256) vdst[x] = vsrc[x];
+        for (int u = 0; u < 4; u++) vreg[u] = vsrc[tid + 256 * u];
+    };
+    auto store_tile = [&](int buf) {
+        for (int u = 0; u < 2; u++) {
+            int x = tid + 256 * u;  // row x/8 (128 B = 8 chunks), chunk x%8
+            *(uint4 *)&ks[buf][(x >> 3) * KS_PITCH + (x & 7) * 16] = kreg[u];
+        }
+        for (int u = 0; u < 4; u++) {
+            int x = tid + 256 * u;  // row x/8 (64 fp16 = 8 chunks), chunk x%8
+            *(uint4 *)&vs[buf][(x >> 3) * VS_PITCH + (x & 7) * 8] = vreg[u];
+        }
     };
 
-    load_tile(0, 0);
+    fetch_tile(0);
+    store_tile(0);
     __syncthreads();
     for (size_t kb = 0; kb < kb_end; kb++) {
         const int buf = kb & 1;
-        if (kb + 1 < kb_end) load_tile(buf ^ 1, kb + 1);
+        const bool more = kb + 1 < kb_end;
+        if (more) fetch_tile(kb + 1);
         if (wave_live && kb < wave_kb_end) {
             const float cs = (qsc * a.kscale[bk * a.nblk + kb]) * LOG2E_F;
             // ---- S^T = K^ Q^T
@@ -663,7 +682,7 @@ __global__ void __launch_bounds__(256) blk_attn(BlkArgs a) {
                 for (int qt = 0; qt < 2; qt++) st[kt][qt] = i32x4_t{0, 0, 0, 0};
             for (int kt = 0; kt < 4; kt++)
                 for (int dc = 0; dc < 2; dc++) {
-                    i32x4_t kf = *(const i32x4_t *)&ks[buf][(16 * kt + col) * HD + dc * 64 + 16 * g];
+                    i32x4_t kf = *(const i32x4_t *)&ks[buf][(16 * kt + col) * KS_PITCH + dc * 64 + 16 * g];
                     for (int qt = 0; qt < 2; qt++)
                         st[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[qt][dc], st[kt][qt], 0, 0, 0);
                 }
@@ -709,7 +728,7 @@ __global__ void __launch_bounds__(256) blk_attn(BlkArgs a) {
             // ---- O^T += V^T P^T
             for (int ct = 0; ct < 8; ct++)
                 for (int kc = 0; kc < 2; kc++) {
-                    const uint16_t *vrow = &vs[buf][(16 * ct + col) * BLK + 32 * kc];
+                    const uint16_t *vrow = &vs[buf][(16 * ct + col) * VS_PITCH + 32 * kc];
                     uint2 lo = *(const uint2 *)(vrow + 4 * g);
                     uint2 hi = *(const uint2 *)(vrow + 16 + 4 * g);
                     uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
@@ -718,6 +737,7 @@ __global__ void __launch_bounds__(256) blk_attn(BlkArgs a) {
                         o[qt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[qt][kc], o[qt][ct], 0, 0, 0);
                 }
         }
+        if (more) store_tile(buf ^ 1);
         __syncthreads();
     }
     if (!wave_live) return;

@@ -13,6 +13,8 @@ ABI against the oracle.
 import numpy as np
 import pytest
 
+from conftest import same
+
 pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
@@ -68,9 +70,9 @@ SHAPES = [(256, 512, 128), (300, 200, 37), (1024, 4096, 1102), (4096, 4096, 1024
 
 
 @pytest.mark.parametrize("dout,din,r", SHAPES)
-@pytest.mark.parametrize("batch", [1, 2, 16, 33, 128])
+@pytest.mark.parametrize("batch", [1, 2, 8, 9, 16, 33, 128])
 def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
-    if dout * r > 2_000_000 and batch not in (1, 16, 128):
+    if dout * r > 2_000_000 and batch not in (1, 8, 16, 128):
         pytest.skip("covered by the smaller shapes")
     say("factor integer-exact", dout, din, r, "batch", batch)
     rng = np.random.default_rng(dout + din + r + batch)
@@ -79,33 +81,41 @@ def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
     x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (batch, din)).astype(np.float32))
     want = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
     got, _ = run_dev(layer, x)
-    assert got.tobytes() == want.tobytes()
+    same(got, want)
     got_b, _ = run_dev(layer, x, "bfloat16")
-    assert got_b.tobytes() == orc.f32_to_bf16_fast(want).tobytes()
+    same(got_b, orc.f32_to_bf16_fast(want))
 
 
 def gpu_t(layer, ws, batch):
     """The device's t (bf16) read back from the documented workspace layout."""
     r, rp = layer.r, -(-layer.r // 128) * 128
-    if batch == 1:
-        return ws[: rp * 2].view(np.uint16)[:r][None, :]
-    parts = ws[: (ws.size // 4) * 4].view(np.float32)
-    nsplit = None
+    rnd = lambda n: -(-n // 256) * 256
+    if batch <= 8:
+        # fp4 decode: [B operands 1 | scales 1 | t bf16 [batch][r_p] | ...]
+        ns1, ncol = -(-layer.din // 128), 2 * batch
+        off = rnd(ns1 * 4 * ncol * 32) + rnd(ns1 * 4 * ncol)
+        t = ws[off: off + batch * rp * 2].view(np.uint16).reshape(batch, rp)
+        assert not t[:, r:].any()
+        return t[:, :r]
+    # [split][batch][r_p] f32 partials, then t bf16 [batch][r_p]
     for s in (1, 2, 4, 8):
-        if s * batch * rp * 4 + 256 == ws.size:
-            nsplit = s
-    assert nsplit is not None
-    p = parts[: nsplit * batch * rp].reshape(nsplit, batch, rp)
-    tot = p[0].copy()
-    for s in range(1, nsplit):
-        tot = (tot + p[s]).astype(np.float32)
-    from oracle import oracle as orc
+        off = rnd(s * batch * rp * 4)
+        if off + batch * rp * 2 + 256 == ws.size:
+            t = ws[off: off + batch * rp * 2].view(np.uint16).reshape(batch, rp)
+            assert not t[:, r:].any()
+            parts = ws[: s * batch * rp * 4].view(np.float32).reshape(s, batch, rp)
+            tot = parts[0].copy()
+            for i in range(1, s):
+                tot = (tot + parts[i]).astype(np.float32)
+            from oracle import oracle as orc
 
-    return orc.f32_to_bf16_fast(tot[:, :r])
+            assert np.array_equal(orc.f32_to_bf16_fast(tot[:, :r]), t[:, :r])
+            return t[:, :r]
+    raise AssertionError("unexpected workspace size")
 
 
 @pytest.mark.parametrize("dout,din,r", SHAPES)
-@pytest.mark.parametrize("batch", [1, 16, 128])
+@pytest.mark.parametrize("batch", [1, 4, 16, 128])
 def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
     say("factor stage bounds", dout, din, r, "batch", batch)
     rng = np.random.default_rng(1000 + dout + r + batch)
@@ -114,7 +124,7 @@ def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
     x = orc.f32_to_bf16_fast(rng.standard_normal((batch, din)).astype(np.float32))
     y, ws = run_dev(layer, x)
     y2, _ = run_dev(layer, x)
-    assert y.tobytes() == y2.tobytes(), "device result not repeatable"
+    same(y, y2, "device result not repeatable")
     t = gpu_t(layer, ws, batch)
     tf = orc.bf16_to_f32(t).astype(np.float64)
     z = orc.bf16_to_f32(orc.f32_to_bf16_fast(L["s2"] * orc.bf16_to_f32(x))).astype(np.float64)
@@ -156,7 +166,7 @@ def test_set_decode_matches_single_layers(ctx, orc):
     ys = yd.cpu().numpy().view(np.uint16)
     for i, layer in enumerate(layers):
         yi, _ = run_dev(layer, x[i:i + 1], "bfloat16")
-        assert ys[i].tobytes() == yi[0].tobytes()
+        same(ys[i], yi[0])
 
 
 def test_apply_host_faces(ctx, orc):
@@ -168,7 +178,7 @@ def test_apply_host_faces(ctx, orc):
     # fp32 serving: f64 matvecs in element order -> bit-identical (BS-3.1)
     got = layer.apply(x, "float32")
     want = orc.factor_apply("fp32", 96, 160, 40, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
-    assert got.tobytes() == want.tobytes()
+    same(got, want)
     # bf16 serving with an f32 x: z = bf16(s2*x) as apply_bf16 does
     got_b = layer.apply(x, "bfloat16")
     want_b = orc.factor_apply("bf16", 96, 160, 40, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
@@ -213,6 +223,6 @@ def test_from_qpk1_matches_from_rows(ctx, orc):
     a = FactorLayer.from_qpk1(ctx, stream)
     b = upload(ctx, L)
     x = orc.f32_to_bf16_fast(rng.standard_normal((3, 24)).astype(np.float32))
-    assert run_dev(a, x)[0].tobytes() == run_dev(b, x)[0].tobytes()
+    same(run_dev(a, x)[0], run_dev(b, x)[0])
     with pytest.raises(KernelError, match="trailing garbage"):
         FactorLayer.from_qpk1(ctx, stream + b"\0")

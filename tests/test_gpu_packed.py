@@ -5,7 +5,7 @@ and run-to-run bit identity for f64)."""
 import numpy as np
 import pytest
 
-from conftest import load_golden
+from conftest import load_golden, same
 
 pytestmark = pytest.mark.gpu
 
@@ -27,17 +27,17 @@ def test_fixtures_bit_identical(ctx, orc):
         v = np.array(rec["inputs"]["vec"], np.float64)
         say("packed_matvec fixture", rec["scenario"])
         got = ctx.packed_matvec(p, p.shape[0], rec["dtypes"]["n_bits"], v)
-        assert got.tobytes() == np.array(rec["faces"]["numpy-reference"]["result"]).tobytes()
+        same(got, np.array(rec["faces"]["numpy-reference"]["result"]))
         if "packed_dirty" in rec["inputs"]:
             pd = np.array(rec["inputs"]["packed_dirty"], np.uint8)
             got = ctx.packed_matvec(pd, p.shape[0], rec["dtypes"]["n_bits"], v)
-            assert got.tobytes() == np.array(rec["faces"]["numpy-reference"]["result_dirty"]).tobytes()
+            same(got, np.array(rec["faces"]["numpy-reference"]["result_dirty"]))
     for rec in load_golden("packed_matmul.json"):
         p = np.array(rec["inputs"]["packed"], np.uint8)
         m = np.array(rec["inputs"]["mat"], np.float64)
         say("packed_matmul fixture", rec["scenario"])
         got = ctx.packed_matmul(p, p.shape[0], m.shape[0], m, m.shape[1])
-        assert got.tobytes() == np.array(rec["faces"]["numpy-reference"]["result"]).tobytes()
+        same(got, np.array(rec["faces"]["numpy-reference"]["result"]))
     for rec in load_golden("dtype_parity.json"):
         dt = rec["dtypes"]["operand"]
         npd = {"float32": np.float32, "bfloat16": np.uint16}[dt]
@@ -50,7 +50,7 @@ def test_fixtures_bit_identical(ctx, orc):
         else:
             m = np.array(rec["inputs"]["mat"], npd)
             got = ctx.packed_matmul(p, p.shape[0], nb, m, m.shape[1], dt)
-        assert got.tobytes() == exp.reshape(got.shape).tobytes()
+        same(got, exp.reshape(got.shape))
 
 
 @pytest.mark.parametrize("dtype", ["float64", "float32", "bfloat16"])
@@ -65,12 +65,12 @@ def test_random_bit_identical_and_repeatable(ctx, orc, dtype, n_rows, n_bits):
     want = orc.packed_matvec(packed, n_rows, n_bits, v, dtype)
     g1 = ctx.packed_matvec(packed, n_rows, n_bits, v, dtype)
     g2 = ctx.packed_matvec(packed, n_rows, n_bits, v, dtype)
-    assert g1.tobytes() == g2.tobytes()
-    assert g1.tobytes() == want.tobytes()
+    same(g1, g2)
+    same(g1, want)
     if n_rows * n_bits <= 300000:
         wm = orc.packed_matmul(packed, n_rows, n_bits, op, 3, dtype)
         gm = ctx.packed_matmul(packed, n_rows, n_bits, op, 3, dtype)
-        assert gm.tobytes() == wm.tobytes()
+        same(gm, wm)
 
 
 def test_degenerate_shapes_and_errors(ctx, orc):
@@ -96,9 +96,8 @@ def test_pyo3_face_on_gpu(orc):
     f = rng.choice([-1, 1], (6, 13)).astype(np.int8)
     p = K.pack_bits(f)
     v = rng.standard_normal(13)
-    assert K.packed_matvec(p, 13, v).tobytes() == orc.packed_matvec(p, 6, 13, v).tobytes()
+    same(K.packed_matvec(p, 13, v), orc.packed_matvec(p, 6, 13, v))
     m = rng.standard_normal((13, 4))
-    assert K.packed_matmul(p, 13, m).tobytes() == orc.packed_matmul(p, 6, 13, m, 4).tobytes()
+    same(K.packed_matmul(p, 13, m), orc.packed_matmul(p, 6, 13, m, 4))
     vb = orc.f32_to_bf16_fast(v.astype(np.float32))
-    assert K.packed_matvec_dtype(p, 13, vb, "bfloat16").tobytes() == \
-        orc.packed_matvec(p, 6, 13, vb, "bfloat16").tobytes()
+    same(K.packed_matvec_dtype(p, 13, vb, "bfloat16"), orc.packed_matvec(p, 6, 13, vb, "bfloat16"))

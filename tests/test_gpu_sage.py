@@ -13,7 +13,7 @@ against exact attention at cos >= 0.999, relL1 <= 0.02.
 import numpy as np
 import pytest
 
-from conftest import load_golden
+from conftest import load_golden, same
 from test_oracle_attention import COS_MIN, RL1_MAX, SLACK, dense_attention, metrics, shaped, two_part_gate
 
 pytestmark = pytest.mark.gpu
@@ -44,7 +44,7 @@ def test_reference_scheme_fixture_battery(ctx, orc):
         say("sage ref fixture", rec["seed"], rec["shape"], rec["causal"], rec["block_size"])
         out = ctx.attention_sage(shape_of(q, k, v), q, k, v, rec["causal"], rec["block_size"])
         want = orc.attention_sage_dev(q, k, v, rec["causal"], rec["block_size"])
-        assert out.tobytes() == want.ravel().tobytes()
+        same(out, want.ravel())
         two_part_gate(out, rec["faces"]["quantized-reference"]["out"], rec["shape"]["val_dim"])
         cos, rl1 = metrics(out, rec["faces"]["exact"]["out"])
         ref = rec["reference_metrics"]
@@ -59,6 +59,8 @@ def test_reference_scheme_fixture_battery(ctx, orc):
     (1, 2, 1, 150, 16, 16, True, 100),   # blocks wider than one LDS chunk
     (1, 1, 1, 70, 8, 8, False, 70),
 ])
+
+
 def test_reference_scheme_random_bit_identical(ctx, orc, b, h, hk, s, d, dv, causal, block):
     say("sage ref random", b, h, hk, s, d, dv, causal, block)
     rng = np.random.default_rng(s + d + block)
@@ -67,7 +69,7 @@ def test_reference_scheme_random_bit_identical(ctx, orc, b, h, hk, s, d, dv, cau
     v = rng.standard_normal((b, hk, s, dv)).astype(np.float32)
     out = ctx.attention_sage(shape_of(q, k, v), q, k, v, causal, block)
     want = orc.attention_sage_dev(q, k, v, causal, block)
-    assert out.tobytes() == want.ravel().tobytes()
+    same(out, want.ravel())
     # Against the f64 NumPy semantics the f32 scheme differs wherever an INT8
     # code lands on the other side of a rounding boundary (the reference's
     # 1e-4 gate is pinned on its fixture battery only), so the f64 form is a
@@ -90,7 +92,7 @@ def test_reference_scheme_device_pointer_form(ctx, orc):
     od = torch.empty((1, 2, 64, 32), dtype=torch.float32, device="cuda")
     ctx.attention_sage_dev(sh, qd, kd, vd, True, 8, od, torch.cuda.current_stream())
     torch.cuda.synchronize()
-    assert od.cpu().numpy().tobytes() == orc.attention_sage_dev(q, k, v, True, 8).tobytes()
+    same(od.cpu().numpy(), orc.attention_sage_dev(q, k, v, True, 8))
 
 
 def run_blk(ctx, qb, kb, vb, causal):
@@ -130,9 +132,9 @@ def test_blk_prepass_codes_bit_identical(ctx, orc, b, h, hk, s):
     torch.cuda.synchronize()
     assert np.array_equal(qh.cpu().numpy(), st["qhat"])
     assert np.array_equal(kh.cpu().numpy(), st["khat"])
-    assert qs.cpu().numpy().tobytes() == st["qscale"].tobytes()
-    assert ks.cpu().numpy().tobytes() == st["kscale"].tobytes()
-    assert km.cpu().numpy().tobytes() == st["kmean"].tobytes()
+    same(qs.cpu().numpy(), st["qscale"])
+    same(ks.cpu().numpy(), st["kscale"])
+    same(km.cpu().numpy(), st["kmean"])
     vf = orc.bf16_to_f32(vb)
     assert np.array_equal(vh.cpu().numpy().view(np.float16).astype(np.float32), vf.astype(np.float16).astype(np.float32))
 
@@ -141,6 +143,8 @@ def test_blk_prepass_codes_bit_identical(ctx, orc, b, h, hk, s):
     (1, 2, 2, 64, True), (1, 4, 2, 200, True), (2, 2, 1, 333, False), (1, 2, 1, 1024, True),
     (1, 2, 2, 128, False),
 ])
+
+
 def test_blk_attention_against_oracle_and_exact(ctx, orc, b, h, hk, s, causal):
     say("sage blk attention", b, h, hk, s, causal)
     rng = np.random.default_rng(b * 1000 + s + causal)
@@ -156,4 +160,4 @@ def test_blk_attention_against_oracle_and_exact(ctx, orc, b, h, hk, s, causal):
     c, r = metrics(got, exact)
     assert c >= COS_MIN and r <= RL1_MAX, (c, r)
     again = orc.bf16_to_f32(run_blk(ctx, qb, kb, vb, causal)).astype(np.float64)
-    assert again.tobytes() == got.tobytes()
+    same(again, got)
