@@ -73,21 +73,21 @@ def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
     for _ in range(warmup):
         S.decode_dev(x, y, ws, ws_n, st)
     torch.cuda.synchronize()
-    # one event before each of the four phases and one after the last
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    # one event before each of the three phases and one after the last
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(st)
     for k in range(steps):
-        for ph in range(1, 5):
+        for ph in range(1, 4):
             ev[k][ph - 1].record(st)
             S.stage_dev(ph, x, y, ws, ws_n, st)
-        ev[k][4].record(st)
+        ev[k][3].record(st)
     end.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / steps
-    phase_ms = [sum(e[p].elapsed_time(e[p + 1]) for e in ev) / steps for p in range(4)]
+    phase_ms = [sum(e[p].elapsed_time(e[p + 1]) for e in ev) / steps for p in range(3)]
     return dict(ms_per_step=ms_step, phase_ms=phase_ms, wall_s=wall, set=S)
 
 
@@ -215,16 +215,18 @@ def main():
     total_bytes = args.layers * LAYER_BYTES
     value = total_bytes / (d["ms_per_step"] * 1e-3) / 1e9
     ph = d["phase_ms"]
-    # algorithmic bytes per layer of each GEMV kernel (the preps carry x, s2)
-    gemv_bytes = {1: M * R // 8, 2: N * R // 8 + 4 * M + 2 * M}
-    dom = 1 if ph[1] >= ph[3] else 2
-    dom_ms = ph[1] if dom == 1 else ph[3]
+    # algorithmic bytes per layer of each GEMV kernel: stage 1 streams Vb
+    # (r x n bits; the prep carries x and s2), stage 2 streams Ub (m x r bits)
+    # and reads s1, writes y
+    gemv_bytes = {1: N * R // 8, 2: M * R // 8 + 4 * M + 2 * M}
+    dom = 1 if ph[1] >= ph[2] else 2
+    dom_ms = ph[1] if dom == 1 else ph[2]
     bytes_launch = args.layers * gemv_bytes[dom]
     achieved = bytes_launch / (dom_ms * 1e-3) / 1e9
-    log(f"  decode: {d['ms_per_step']:.3f} ms/step, {value:.1f} GB/s; phases (prep x, gemv 1, "
-        f"prep t, gemv 2) = {', '.join(f'{p:.4f}' for p in ph)} ms")
+    log(f"  decode: {d['ms_per_step']:.3f} ms/step, {value:.1f} GB/s; phases (prep x, gemv 1 + "
+        f"t operand, gemv 2) = {', '.join(f'{p:.4f}' for p in ph)} ms")
     extra = {"decode_phase_ms": {"prep_x": round(ph[0], 4), "gemv_stage1": round(ph[1], 4),
-                                 "prep_t": round(ph[2], 4), "gemv_stage2": round(ph[3], 4)}}
+                                 "gemv_stage2": round(ph[2], 4)}}
     if not args.no_extra:
         log("single-layer latency ...")
         extra["decode_single_layer_us"] = round(bench_single_latency(torch, np, layers[0]), 2)
@@ -257,7 +259,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": None,
-            "kernel": f"q4_gemv_kernel<{dom},*> (decode stage {dom}, fp4 x fp8 scaled MFMA)",
+            "kernel": f"q4_stream_kernel<{dom},2,4> (decode stage {dom}, fp4 x fp8 scaled MFMA, persistent)",
             "bytes_per_launch": bytes_launch, "avg_launch_ms": round(dom_ms, 4),
         },
         "cpu_baseline": cpu,

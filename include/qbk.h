@@ -146,12 +146,22 @@ size_t qbk_factor_set_workspace_size(const qbk_factor_set *set);
  * x bf16 [n_layers][din], y bf16 [n_layers][dout] (device pointers). */
 int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *set, const uint16_t *x,
                               uint16_t *y, void *workspace, size_t workspace_size, void *stream);
-/* One of the two launches of qbk_factor_set_decode_dev: stage 1 writes
- * t = bf16(Vb^T bf16(s2*x)) for every layer into the workspace, stage 2
- * reads it and writes y (for callers that interleave work or time stages). */
+/* One of the three launches of qbk_factor_set_decode_dev (for callers that
+ * interleave work or time phases): phase 1 turns every x into stage 1's fp8
+ * operand in the workspace; phase 2 runs stage 1 and writes
+ * t = bf16(Vb^T bf16(s2*x)) as stage 2's fp8 operand; phase 3 runs stage 2
+ * and writes y.  No counterpart in the reference (its apply is one call). */
 int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *set, int stage,
                              const uint16_t *x, uint16_t *y, void *workspace,
                              size_t workspace_size, void *stream);
+
+/* Tuning knobs of this implementation; no counterpart in the reference.
+ * QBK_TUNE_STREAM_MIN_TASKS: a decode stage (batch 1-2) runs the persistent
+ * streaming GEMV once it has at least `value` 64-row tasks; -1 restores the
+ * library's own threshold.  Returns the previous value (-2: unknown knob).
+ * Process-wide; set it while no decode call is in flight. */
+#define QBK_TUNE_STREAM_MIN_TASKS 1
+long long qbk_tune(int knob, long long value);
 
 /* ---- attention (gpu_attention.rs) ----------------------------------------- */
 

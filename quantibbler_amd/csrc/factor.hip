@@ -590,8 +590,22 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs A) {
 // of packed signs.
 
 #define Q4_MAXB 8
+#define Q4_U 8  // slices whose sign loads a wave issues together
+#define Q4_PHASES 3  // prep x, stage 1 (+ stage 2's operand), stage 2
+#define Q4_SU 4      // slices per unit of the stream kernel
+#define Q4_LDS_MAX (40 * 1024)  // largest per-layer operand staged in LDS
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Pointers read from a layer table are generic to the compiler; loading
+// through an address_space(1) pointer keeps them global loads (flat loads
+// count against both vmcnt and lgkmcnt and defeat per-load waits).
+typedef __attribute__((address_space(1))) const u32x4_t gu32x4_t;
+typedef __attribute__((address_space(1))) const float gf32_t;
+// The layer tables are never written by a kernel: reading them through the
+// constant address space lets the compiler use scalar loads even after the
+// kernel's own stores (a vector load of a pointer would wait on vmcnt).
+typedef __attribute__((address_space(4))) const Q4Layer cq4layer_t;
 
 // B operand of one (layer, slice, lane group, column): 32 fp8 bytes + scale.
 struct Q4Args {
@@ -602,9 +616,13 @@ struct Q4Args {
     size_t act_ld, act_layer;                 // elements per token row, per layer
     uint8_t *bop;                             // [layer][ns][4][ncol][32]
     uint8_t *bsc;                             // [layer][ns][4][ncol]
-    void *out;                                // stage 1: t bf16 [layer][batch][out_ld]; stage 2: y
+    void *out;                                // stage 2: y [layer][batch][out_ld]
     size_t out_ld, out_layer;
     int y_bf16;
+    int vec_ok;                               // act rows allow 4-element vector loads
+    uint32_t m8, c2;                          // 0x88888888, 0x22222222 (fp4 sign build)
+    uint8_t *tb_op, *tb_sc;                   // stage 1: stage 2's operand and scales
+    size_t tb_ns;                             // stage 2's slices per layer
 };
 
 __device__ __forceinline__ int e8m0_of(float amax) {
@@ -616,87 +634,245 @@ __device__ __forceinline__ int e8m0_of(float amax) {
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
-// One thread per (layer, token, slice, lane group): the 32 activations of
-// that k block become the hi and lo fp8 columns of the token.
+// Eight threads per (layer, token, slice, scale group g), four activations
+// each.  The E8M0 scale given by lane group g covers the activations
+// k = 128s + kq4(g, e) (measured on gfx950): two runs of 16, at k offsets
+// 16(g>>1) + 64(g&1) and that + 32, whose fp8 bytes sit in B lane groups
+// 2(g&1) and 2(g&1)+1 at byte offset 16(g>>1).  Thread j < 4 takes 4j..4j+3
+// of the first run, j >= 4 the second.
 template <int STAGE, bool XF32>
 __global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a, size_t n_items) {
-    size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (it >= n_items) return;
-    const int g = it & 3;
-    size_t rest = it >> 2;
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t it = tid >> 3;
+    const int j = (int)(tid & 7);
+    const bool live = it < n_items;  // dead threads still join the shuffles
+    const size_t itc = live ? it : 0;
+    const int g = itc & 3;
+    size_t rest = itc >> 2;
     const size_t s = rest % a.ns;
     rest /= a.ns;
     const int b = (int)(rest % a.batch);
     const size_t li = rest / a.batch;
-    const Q4Layer L = a.layers[li];
-    const size_t off = li * a.act_layer + (size_t)b * a.act_ld;
-    const uint16_t *src = (const uint16_t *)a.act + off;
-    const float *srcf = (const float *)a.act + off;
-    // The E8M0 scale given by lane group g covers the activations
-    // k = 128s + kq4(g, e) (measured): two 16-element runs, held in B lane
-    // groups 2(g&1) and 2(g&1)+1 at byte offset 16(g>>1).
-    const size_t k0 = 128 * s + 16 * (g >> 1) + 64 * (g & 1);
-    float z[32];
-    float amax = 0.0f;
+    const size_t k0 = 128 * s + 16 * (g >> 1) + 64 * (g & 1) + 4 * (j & 3) + 32 * (j >> 2);
+    float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+        const size_t off = li * a.act_layer + (size_t)b * a.act_ld;
+        const uint16_t *src = (const uint16_t *)a.act + off;
+        const float *srcf = (const float *)a.act + off;
+        if (a.vec_ok && k0 + 3 < a.k_valid) {
+            float v[4];
+            if (XF32) {
+                float4 q = *(const float4 *)(srcf + k0);
+                v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+            } else {
+                uint2 q = *(const uint2 *)(src + k0);
+                v[0] = bf16_to_f32(q.x & 0xffff); v[1] = bf16_to_f32(q.x >> 16);
+                v[2] = bf16_to_f32(q.y & 0xffff); v[3] = bf16_to_f32(q.y >> 16);
+            }
+            if (STAGE == 1) {
+                float4 sv = *(const float4 *)(a.layers[li].s_in + k0);
+                v[0] = bf16_to_f32(f32_to_bf16(sv.x * v[0]));
+                v[1] = bf16_to_f32(f32_to_bf16(sv.y * v[1]));
+                v[2] = bf16_to_f32(f32_to_bf16(sv.z * v[2]));
+                v[3] = bf16_to_f32(f32_to_bf16(sv.w * v[3]));
+            }
 #pragma unroll
-    for (int e = 0; e < 32; e++) {
-        size_t k = k0 + (e & 15) + 32 * (e >> 4);
-        float v = 0.0f;
-        if (k < a.k_valid) {
-            if (STAGE == 1)
-                v = bf16_to_f32(f32_to_bf16(L.s_in[k] * (XF32 ? srcf[k] : bf16_to_f32(src[k]))));
-            else
-                v = bf16_to_f32(src[k]);
+            for (int e = 0; e < 4; e++) z[e] = v[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const size_t k = k0 + e;
+                if (k >= a.k_valid) continue;
+                float v = XF32 ? srcf[k] : bf16_to_f32(src[k]);
+                z[e] = STAGE == 1 ? bf16_to_f32(f32_to_bf16(a.layers[li].s_in[k] * v)) : v;
+            }
         }
-        z[e] = v;
-        amax = fmaxf(amax, fabsf(v));
     }
+    float amax = fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
     const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
     const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
-    uint32_t hw[8];
-    float rmax = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
-        hw[q] = (uint32_t)w;
-        const float back[4] = {__builtin_amdgcn_cvt_f32_fp8(w, 0), __builtin_amdgcn_cvt_f32_fp8(w, 1),
-                               __builtin_amdgcn_cvt_f32_fp8(w, 2), __builtin_amdgcn_cvt_f32_fp8(w, 3)};
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            z[4 * q + u] = z[4 * q + u] - back[u] * sc_hi;  // exact residual
-            rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
-        }
-    }
+    int hw = __builtin_amdgcn_cvt_pk_fp8_f32(z[0] * inv_hi, z[1] * inv_hi, 0, false);
+    hw = __builtin_amdgcn_cvt_pk_fp8_f32(z[2] * inv_hi, z[3] * inv_hi, hw, true);
+    // exact residual: each bf16 value keeps at most 4 significant bits for lo
+    z[0] -= __builtin_amdgcn_cvt_f32_fp8(hw, 0) * sc_hi;
+    z[1] -= __builtin_amdgcn_cvt_f32_fp8(hw, 1) * sc_hi;
+    z[2] -= __builtin_amdgcn_cvt_f32_fp8(hw, 2) * sc_hi;
+    z[3] -= __builtin_amdgcn_cvt_f32_fp8(hw, 3) * sc_hi;
+    float rmax = fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3])));
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 64));
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 4, 64));
     const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
     const float inv_lo = pow2f(-e_lo);
-    uint32_t lw[8];
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
-        lw[q] = (uint32_t)w;
+    int lw = __builtin_amdgcn_cvt_pk_fp8_f32(z[0] * inv_lo, z[1] * inv_lo, 0, false);
+    lw = __builtin_amdgcn_cvt_pk_fp8_f32(z[2] * inv_lo, z[3] * inv_lo, lw, true);
+    if (!live) return;
+    const size_t gb = 2 * (g & 1) + (j >> 2);
+    const size_t slot = ((li * a.ns + s) * 4 + gb) * a.ncol + 2 * b;  // hi column; lo is slot + 1
+    const size_t byte = 16 * (g >> 1) + 4 * (j & 3);
+    *(uint32_t *)(a.bop + slot * 32 + byte) = (uint32_t)hw;
+    *(uint32_t *)(a.bop + (slot + 1) * 32 + byte) = (uint32_t)lw;
+    if (j == 0) {
+        const size_t sc = ((li * a.ns + s) * 4 + g) * a.ncol + 2 * b;
+        a.bsc[sc] = (uint8_t)(e_hi + 127);
+        a.bsc[sc + 1] = (uint8_t)(e_lo + 127);
     }
-    // bytes of elements e < 16 go to B lane group gb, e >= 16 to gb + 1
-    const size_t gb = 2 * (g & 1), boff = 16 * (g >> 1);
-    const size_t slot0 = ((li * a.ns + s) * 4 + gb) * a.ncol + 2 * b;      // (group gb, hi column)
-    const size_t slot1 = ((li * a.ns + s) * 4 + gb + 1) * a.ncol + 2 * b;  // (group gb+1, hi column)
-    *(uint4 *)(a.bop + slot0 * 32 + boff) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    *(uint4 *)(a.bop + slot1 * 32 + boff) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-    *(uint4 *)(a.bop + (slot0 + 1) * 32 + boff) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    *(uint4 *)(a.bop + (slot1 + 1) * 32 + boff) = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-    const size_t sc = ((li * a.ns + s) * 4 + g) * a.ncol + 2 * b;
-    a.bsc[sc] = (uint8_t)(e_hi + 127);
-    a.bsc[sc + 1] = (uint8_t)(e_lo + 127);
+}
+
+// Signs of one 16-row tile as fp4 e2m1 +-1 (0x2 / 0xA): nibble e of VGPR j
+// carries bit 4e + 3 - j of the word, moved to the nibble's sign bit.  7 VALU
+// ops per MFMA: m8 arrives as a kernel argument (an SGPR) and c2 sits in a
+// VGPR so that the compiler fuses and-or (gfx9 VOP3 takes one scalar operand
+// and no literal).
+__device__ __forceinline__ i32x8_t q4_signs(uint32_t w, uint32_t m8, uint32_t c2) {
+    i32x8_t av;
+    av[0] = (int)(((w << 3) & m8) | c2);
+    av[1] = (int)(((w << 2) & m8) | c2);
+    av[2] = (int)(((w << 1) & m8) | c2);
+    av[3] = (int)((w & m8) | c2);
+    av[4] = av[5] = av[6] = av[7] = 0;
+    return av;
+}
+
+// One 128-k slice of a 64-row group: the four row tiles' MFMAs against the
+// fp8 operand held in LDS at byte offset bo (scale byte at so).
+__device__ __forceinline__ void q4_slice_lds(f32x4_t acc[4], const uint4 &w4, const uint8_t *lds,
+                                             uint32_t bo, uint32_t so, uint32_t m8, uint32_t c2) {
+    const uint4 *bq = (const uint4 *)(lds + bo);
+    const uint4 b0 = bq[0], b1 = bq[1];
+    const i32x8_t bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                        (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    const int bs = lds[so];
+    const uint32_t wr[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++)
+        acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], m8, c2), bv, acc[rt],
+                                                                  4, 0, 0, 127, 0, bs);
+}
+
+// Stage-1 epilogue: t = bf16(hi + lo) for the 64 rows of group rg, written
+// straight into stage 2's fp8 operand (the prep's split, done in registers).
+// Rows 16rt + 4g + i of the group sit in lane (col 2b, g); the group is half
+// of stage-2 slice rg/2, and its rows 16rt + 4g + i belong to scale group
+// G = 2(rt&1) + (rg&1), B lane group 2(rg&1) + (rt>>1), byte 16(rt&1) + 4g + i.
+// Rows >= rows_valid are zero.  Every lane joins the shuffles.
+__device__ __forceinline__ void q4_emit_t(const f32x4_t acc[4], const Q4Args &a, size_t li,
+                                          size_t rg, int lane) {
+    const int col = lane & 15, g = lane >> 4;
+    float t[4][4];
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float lo = __shfl_down(acc[rt][i], 1, 64);
+            const size_t row = rg * 64 + 16 * rt + 4 * g + i;
+            t[rt][i] = row < a.rows_valid ? bf16_to_f32(f32_to_bf16(acc[rt][i] + lo)) : 0.0f;
+        }
+    const bool writer = (col & 1) == 0 && col < a.ncol;
+    const size_t b = col >> 1;
+    const size_t base = (li * a.tb_ns + (rg >> 1)) * 4;
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        // scale group G = 2q + (rg&1): rows of tiles q and q+2
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) amax = fmaxf(amax, fmaxf(fabsf(t[q][i]), fabsf(t[q + 2][i])));
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+        const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+        int hw[2], lw[2];
+        float r[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float *v = t[q + 2 * h];
+            int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv_hi, v[1] * inv_hi, 0, false);
+            w = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv_hi, v[3] * inv_hi, w, true);
+            hw[h] = w;
+            r[h][0] = v[0] - __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;
+            r[h][1] = v[1] - __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
+            r[h][2] = v[2] - __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
+            r[h][3] = v[3] - __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+        }
+        float rmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) rmax = fmaxf(rmax, fmaxf(fabsf(r[0][i]), fabsf(r[1][i])));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 16, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+        const float inv_lo = pow2f(-e_lo);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int w = __builtin_amdgcn_cvt_pk_fp8_f32(r[h][0] * inv_lo, r[h][1] * inv_lo, 0, false);
+            lw[h] = __builtin_amdgcn_cvt_pk_fp8_f32(r[h][2] * inv_lo, r[h][3] * inv_lo, w, true);
+        }
+        if (writer) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const size_t slot = (base + 2 * (rg & 1) + h) * a.ncol + 2 * b;  // hi column; lo = +1
+                const size_t byte = 16 * q + 4 * g;
+                *(uint32_t *)(a.tb_op + slot * 32 + byte) = (uint32_t)hw[h];
+                *(uint32_t *)(a.tb_op + (slot + 1) * 32 + byte) = (uint32_t)lw[h];
+            }
+            if (g == 0) {
+                const size_t sc = (base + 2 * q + (rg & 1)) * a.ncol + 2 * b;
+                a.tb_sc[sc] = (uint8_t)(e_hi + 127);
+                a.tb_sc[sc + 1] = (uint8_t)(e_lo + 127);
+            }
+        }
+    }
+}
+
+// Stage-2 epilogue: y = bf16(hi + lo) * s1 + bias for the 64 rows of group
+// rg; so / bi are this lane's row (rg*64 + lane) of s1 and bias.
+__device__ __forceinline__ void q4_emit_y(const f32x4_t acc[4], const Q4Args &a, size_t li, size_t rg,
+                                          int lane, float so, float bi) {
+    const int col = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) {
+        f32x4_t lo, sov, biv;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = __shfl_down(acc[rt][i], 1, 64);
+            sov[i] = __shfl(so, 16 * rt + 4 * g + i, 64);
+            biv[i] = __shfl(bi, 16 * rt + 4 * g + i, 64);
+        }
+        if ((col & 1) == 0 && col < a.ncol) {
+            const size_t b = col >> 1;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const size_t row = rg * 64 + 16 * rt + 4 * g + i;
+                if (row >= a.rows_valid) continue;
+                const float u = bf16_to_f32(f32_to_bf16(acc[rt][i] + lo[i]));
+                const float y = u * sov[i] + biv[i];
+                const size_t o = li * a.out_layer + b * a.out_ld + row;
+                if (a.y_bf16)
+                    ((uint16_t *)a.out)[o] = f32_to_bf16(y);
+                else
+                    ((float *)a.out)[o] = y;
+            }
+        }
+    }
 }
 
 // Workgroup = 4 waves; KSPLIT waves share a 64-row group and split its
-// slices, 4/KSPLIT row groups per workgroup.  Lane l loads the 16 bytes of
-// its four row tiles' sign words per slice (1 KiB per wave, contiguous).
-template <int STAGE, int KSPLIT>
+// slices, 4/KSPLIT row groups per workgroup, so a workgroup covers every
+// slice of its layer.  Lane l loads the 16 bytes of its four row tiles' sign
+// words per slice (1 KiB per wave per slice, contiguous over the slices).
+// Used for small launches (a single layer) and batches above 2; many-layer
+// decode at batch 1-2 takes q4_stream_kernel.
+//
+// BLDS: the layer's fp8 operand and scales are copied to LDS once per
+// workgroup before the sign loads are issued.  Otherwise (operands larger
+// than Q4_LDS_MAX) each slice's operand is read from global memory.
+template <int STAGE, int KSPLIT, bool BLDS>
 __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
-    __shared__ f32x4_t red[KSPLIT > 1 ? 4 : 1][4][64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const size_t li = blockIdx.y;
     const Q4Layer L = a.layers[li];
     constexpr int RG_PER_WG = 4 / KSPLIT;
@@ -704,83 +880,277 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
     const int ks = wave % KSPLIT;
     const size_t n_rg = a.rows_p / 64;
     const size_t per = (a.ns + KSPLIT - 1) / KSPLIT;
-    const size_t s0 = ks * per, s1 = s0 + per < a.ns ? s0 + per : a.ns;
+    const size_t s0 = ks * per < a.ns ? ks * per : a.ns;
+    const size_t s1 = s0 + per < a.ns ? s0 + per : a.ns;
     const int col = lane & 15, g = lane >> 4;
     const bool bcol = col < a.ncol;
+    const bool live = rg < n_rg;
+    const uint32_t bbytes = (uint32_t)(a.ns * 4 * a.ncol * 32), sbytes = (uint32_t)(a.ns * 4 * a.ncol);
+    const uint8_t *gb = a.bop + li * bbytes;
+    const uint8_t *gs = a.bsc + li * sbytes;
+    const uint32_t m8 = a.m8;
+    uint32_t c2;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(c2) : "s"(a.c2));
+
+    // fp8 operand of slice s for this lane: LDS offsets (BLDS) or global
+    const uint32_t zslot = (bbytes + sbytes + 15) & ~15u;  // 32 zero bytes, then scale 127
+    const uint32_t slot0 = (uint32_t)(g * a.ncol + col);
+    const uint32_t bo0 = bcol ? slot0 * 32 : zslot, bstep = bcol ? 4 * a.ncol * 32 : 0;
+    const uint32_t so0 = bcol ? bbytes + slot0 : zslot + 32, sstep = bcol ? 4 * a.ncol : 0;
+    if (BLDS) {
+        for (uint32_t o = tid * 16; o < bbytes; o += 256 * 16)
+            *(uint4 *)(q4_lds + o) = *(const uint4 *)(gb + o);
+        for (uint32_t o = tid * 8; o < sbytes; o += 256 * 8)
+            *(uint2 *)(q4_lds + bbytes + o) = *(const uint2 *)(gs + o);
+        if (tid < 2) *(uint4 *)(q4_lds + zslot + 16 * tid) = make_uint4(0, 0, 0, 0);
+        if (tid == 2) q4_lds[zslot + 32] = 127;
+    }
+
+    // Sign loads are unconditional (indices clamped into the layer) so that
+    // the compiler's wait counts stay exact: each slice's MFMAs start as soon
+    // as its own load lands.
+    const size_t rgc = live ? rg : n_rg - 1;
+    const size_t slast = s1 > s0 ? s1 - 1 : (s0 < a.ns ? s0 : a.ns - 1);
+    const uint4 *wp = (const uint4 *)L.bits + (rgc * a.ns) * 64 + lane;
+    uint4 w4[Q4_U];
+    auto load_signs = [&](size_t sb) {
+#pragma unroll
+        for (int u = 0; u < Q4_U; u++) {
+            const size_t sl = sb + u < slast ? sb + u : slast;
+            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64));
+            w4[u] = make_uint4(q[0], q[1], q[2], q[3]);
+        }
+    };
+    load_signs(s0);
+    // stage 2: this lane's row of the group, for the epilogue
+    float so = 0.0f, bi = 0.0f;
+    if (STAGE == 2) {
+        const size_t row = rgc * 64 + lane;
+        const size_t rc = row < a.rows_valid ? row : a.rows_valid - 1;
+        so = ((gf32_t *)L.s_out)[rc];
+        bi = ((gf32_t *)L.bias)[rc];
+    }
+    if (BLDS) __syncthreads();
 
     f32x4_t acc[4];
 #pragma unroll
     for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
-    if (rg < n_rg) {
-        const uint4 *wp = (const uint4 *)L.bits + (rg * a.ns) * 64 + lane;
-        const uint8_t *bp = a.bop + (li * a.ns * 4 + g) * a.ncol * 32 + col * 32;
-        const uint8_t *sp = a.bsc + (li * a.ns * 4 + g) * a.ncol + col;
-        const size_t bstride = 4 * a.ncol * 32, sstride = 4 * a.ncol;
-        for (size_t s = s0; s < s1; s++) {
-            uint4 w4 = wp[s * 64];
-            i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
-            int bs = 127;
-            if (bcol) {
-                const uint4 *bq = (const uint4 *)(bp + s * bstride);
-                uint4 b0 = bq[0], b1 = bq[1];
-                bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
-                             (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-                bs = sp[s * sstride];
-            }
-            uint32_t wr[4] = {w4.x, w4.y, w4.z, w4.w};
+    auto step = [&](const uint4 &w4u, size_t s) {
+        if (BLDS) {
+            q4_slice_lds(acc, w4u, q4_lds, bo0 + (uint32_t)s * bstep, so0 + (uint32_t)s * sstep, m8, c2);
+            return;
+        }
+        i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
+        int bs = 127;
+        if (bcol) {
+            const size_t slot = (s * 4 + g) * a.ncol + col;
+            const uint4 *bq = (const uint4 *)(gb + slot * 32);
+            const uint4 b0 = bq[0], b1 = bq[1];
+            bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                         (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+            bs = gs[slot];
+        }
+        const uint32_t wr[4] = {w4u.x, w4u.y, w4u.z, w4u.w};
 #pragma unroll
-            for (int rt = 0; rt < 4; rt++) {
-                const uint32_t w = wr[rt];
-                i32x8_t av;
-                av[0] = (int)(((w << 3) & 0x88888888u) | 0x22222222u);
-                av[1] = (int)(((w << 2) & 0x88888888u) | 0x22222222u);
-                av[2] = (int)(((w << 1) & 0x88888888u) | 0x22222222u);
-                av[3] = (int)((w & 0x88888888u) | 0x22222222u);
-                av[4] = av[5] = av[6] = av[7] = 0;
-                acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[rt], 4, 0, 0, 127,
-                                                                          0, bs);
-            }
+        for (int rt = 0; rt < 4; rt++)
+            acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], m8, c2), bv,
+                                                                      acc[rt], 4, 0, 0, 127, 0, bs);
+    };
+    auto batch = [&](size_t sb) {
+        if (sb + Q4_U <= s1) {
+#pragma unroll
+            for (int u = 0; u < Q4_U; u++) step(w4[u], sb + u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < Q4_U; u++)
+                if (sb + u < s1) step(w4[u], sb + u);
+        }
+    };
+    if (live) {
+        // The first batch's loads were issued before the barrier; later
+        // batches load at the top of their step, so that within a batch the
+        // waits stay per slice.
+        batch(s0);
+        for (size_t sb = s0 + Q4_U; sb < s1; sb += Q4_U) {
+            load_signs(sb);
+            batch(sb);
         }
     }
     if (KSPLIT > 1) {
+        // the operand region is reused for the cross-wave sums
+        f32x4_t *red = (f32x4_t *)q4_lds;  // [4 waves][4 tiles][64 lanes]
+        if (BLDS) __syncthreads();
 #pragma unroll
-        for (int rt = 0; rt < 4; rt++) red[wave][rt][lane] = acc[rt];
+        for (int rt = 0; rt < 4; rt++) red[(wave * 4 + rt) * 64 + lane] = acc[rt];
         __syncthreads();
         if (ks != 0) return;
 #pragma unroll
         for (int rt = 0; rt < 4; rt++) {
-            f32x4_t v = red[wave][rt][lane];
-            for (int q = 1; q < KSPLIT; q++) v += red[wave + q][rt][lane];
+            f32x4_t v = red[(wave * 4 + rt) * 64 + lane];
+            for (int q = 1; q < KSPLIT; q++) v += red[((wave + q) * 4 + rt) * 64 + lane];
             acc[rt] = v;
         }
     }
-    if (rg >= n_rg) return;
-    // hi + lo: lane col 2b holds hi, col 2b+1 holds lo for rows 4g+i
+    if (!live) return;
+    if (STAGE == 1)
+        q4_emit_t(acc, a, li, rg, lane);
+    else
+        q4_emit_y(acc, a, li, rg, lane, so, bi);
+}
+
+// Persistent decode GEMV for many layers at batch 1-2 (NCOL = 2 * batch
+// fp8 columns).  A task is one 64-row group of one layer; a unit is Q4_U
+// slices of a task.  Each wave walks its tasks unit by unit with the next
+// unit's loads in flight while it computes the current one: two register
+// sets of signs (Q4_U KiB each), and the fp8 operand of the unit staged
+// through registers into a wave-private double buffer in LDS (no barriers).
+// Tasks are split into 8 contiguous ranges, one per XCD (workgroup i runs
+// on XCD i mod 8), so that one layer's operand is fetched into one L2.
+//
+// Issue order inside a unit -- operand staging loads, then signs, then (stage
+// 2) the scale/bias of the row -- keeps every wait exact: the operand is
+// written to LDS with the signs still in flight, and the epilogue's stores
+// come after that write.
+template <int STAGE, int NCOL, int U>
+__global__ void __launch_bounds__(256) q4_stream_kernel(Q4Args a, uint32_t n_tasks) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
+    static_assert(U * 4 * NCOL <= 256, "scale staging is one dword per lane");
+    constexpr uint32_t OPB = U * 4 * NCOL * 32;  // operand bytes of a unit
+    constexpr uint32_t NSTG = OPB / 1024;        // operand uint4 per lane
+    constexpr uint32_t SCB = U * 4 * NCOL;       // scale bytes of a unit
+    constexpr uint32_t BUF = OPB + 256;          // + one staged dword per lane
+    constexpr uint32_t REGION = 2 * BUF + 48;    // two buffers + zero slot
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t *rl = q4_lds + wave * REGION;
+    const uint32_t zs = 2 * BUF;
+    if (lane < 2) *(uint4 *)(rl + zs + 16 * lane) = make_uint4(0, 0, 0, 0);
+    if (lane == 2) rl[zs + 32] = 127;
+
+    const uint32_t nx = 8, xcd = blockIdx.x % nx, wgx = blockIdx.x / nx;
+    const uint32_t n_wg_x = (gridDim.x - xcd + nx - 1) / nx;
+    const uint32_t t0 = (uint32_t)((uint64_t)n_tasks * xcd / nx);
+    const uint32_t t1 = (uint32_t)((uint64_t)n_tasks * (xcd + 1) / nx);
+    const uint32_t wv = wgx * 4 + wave, nw = n_wg_x * 4;
+    if (t0 + wv >= t1) return;
+    const uint32_t ntask = (t1 - t0 - wv + nw - 1) / nw;
+    const uint32_t ns = (uint32_t)a.ns, cpt = (ns + U - 1) / U;
+    const uint32_t n_units = ntask * cpt;
+    const uint32_t n_rg = (uint32_t)(a.rows_p / 64);
+    const int col = lane & 15, g = lane >> 4;
+    const bool bcol = col < NCOL;
+    const uint32_t m8 = a.m8;
+    uint32_t c2;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(c2) : "s"(a.c2));
+    // per-lane LDS offsets of slice j within a buffer
+    const uint32_t slot0 = g * NCOL + col;
+    const uint32_t bo0 = bcol ? slot0 * 32 : zs, bstep = bcol ? 4 * NCOL * 32 : 0;
+    const uint32_t so0 = bcol ? OPB + slot0 : zs + 32, sstep = bcol ? 4 * NCOL : 0;
+
+    uint4 wA[U], wB[U], stg[NSTG];
+    uint32_t stgs = 0;
+    float soA = 0.0f, biA = 0.0f, soB = 0.0f, biB = 0.0f;
+    f32x4_t acc[4];
+
+    auto where = [&](uint32_t u, uint32_t &li, uint32_t &rg, uint32_t &c) {
+        const uint32_t k = u / cpt;
+        c = u - k * cpt;
+        const uint32_t t = t0 + wv + k * nw;
+        li = t / n_rg;
+        rg = t - li * n_rg;
+    };
+    auto issue = [&](uint32_t u, uint4 (&w)[U], float &so_, float &bi_) {
+        uint32_t li, rg, c;
+        where(u, li, rg, c);
+        const uint32_t nsl = ns - U * c < U ? ns - U * c : U;
+        // operand staging: NSTG uint4 + one dword of scales per lane
+        const uint8_t *gb = a.bop + ((size_t)li * ns + U * c) * 4 * NCOL * 32;
+        const uint8_t *gs = a.bsc + ((size_t)li * ns + U * c) * 4 * NCOL;
+        const uint32_t ob_valid = nsl * 4 * NCOL * 32, os_valid = nsl * 4 * NCOL;
 #pragma unroll
-    for (int rt = 0; rt < 4; rt++) {
-        f32x4_t v = acc[rt];
-        f32x4_t lo;
+        for (int q = 0; q < (int)NSTG; q++) {
+            uint32_t o = (lane + 64 * q) * 16;
+            o = o < ob_valid ? o : ob_valid - 16;
+            stg[q] = *(const uint4 *)(gb + o);
+        }
+        {
+            uint32_t o = lane * 4;
+            o = o < os_valid ? o : os_valid - 4;
+            stgs = *(const uint32_t *)(gs + o);
+        }
+        const cq4layer_t *lp = (const cq4layer_t *)a.layers + li;
+        const Q4Layer L = {lp->bits, lp->s_in, lp->s_out, lp->bias};
+        const uint4 *wp = (const uint4 *)L.bits + ((size_t)rg * ns + U * c) * 64 + lane;
 #pragma unroll
-        for (int i = 0; i < 4; i++) lo[i] = __shfl_down(v[i], 1, 64);
-        if ((col & 1) == 0 && col < a.ncol) {
-            const int b = col >> 1;
+        for (int j = 0; j < U; j++) {
+            const uint32_t jj = j < (int)nsl ? j : nsl - 1;
+            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + jj * 64));
+            w[j] = make_uint4(q[0], q[1], q[2], q[3]);
+        }
+        if (STAGE == 2) {
+            const size_t row = (size_t)rg * 64 + lane;
+            const size_t rc = row < a.rows_valid ? row : a.rows_valid - 1;
+            so_ = ((gf32_t *)L.s_out)[rc];
+            bi_ = ((gf32_t *)L.bias)[rc];
+        }
+    };
+    auto stage_write = [&](uint32_t buf) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const size_t row = rg * 64 + 16 * rt + 4 * g + i;
-                const float sum = v[i] + lo[i];
-                if (STAGE == 1) {
-                    ((uint16_t *)a.out)[li * a.out_layer + (size_t)b * a.out_ld + row] =
-                        row < a.rows_valid ? f32_to_bf16(sum) : (uint16_t)0;
-                } else if (row < a.rows_valid) {
-                    float u = bf16_to_f32(f32_to_bf16(sum));
-                    float y = u * L.s_out[row] + L.bias[row];
-                    size_t o = li * a.out_layer + (size_t)b * a.out_ld + row;
-                    if (a.y_bf16)
-                        ((uint16_t *)a.out)[o] = f32_to_bf16(y);
-                    else
-                        ((float *)a.out)[o] = y;
-                }
-            }
+        for (int q = 0; q < (int)NSTG; q++) *(uint4 *)(rl + buf + (lane + 64 * q) * 16) = stg[q];
+        *(uint32_t *)(rl + buf + OPB + lane * 4) = stgs;  // lanes past SCB fill the padding
+    };
+    auto mfmas = [&](uint32_t u, const uint4 (&w)[U], uint32_t buf) {
+        uint32_t li, rg, c;
+        where(u, li, rg, c);
+        const uint32_t nsl = ns - U * c < U ? ns - U * c : U;
+        const uint32_t bo = bcol ? buf + bo0 : bo0, so = bcol ? buf + so0 : so0;
+        if (nsl == U) {
+#pragma unroll
+            for (int j = 0; j < U; j++) q4_slice_lds(acc, w[j], rl, bo + j * bstep, so + j * sstep, m8, c2);
+        } else {
+#pragma unroll
+            for (int j = 0; j < U; j++)
+                if (j < (int)nsl) q4_slice_lds(acc, w[j], rl, bo + j * bstep, so + j * sstep, m8, c2);
+        }
+    };
+    auto tail = [&](uint32_t u, float so_, float bi_) {
+        uint32_t li, rg, c;
+        where(u, li, rg, c);
+        if (c != cpt - 1) return;
+        if (STAGE == 1)
+            q4_emit_t(acc, a, li, rg, lane);
+        else
+            q4_emit_y(acc, a, li, rg, lane, so_, bi_);
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
+    };
+
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
+    issue(0, wA, soA, biA);
+    stage_write(0);
+    for (uint32_t u = 0;;) {
+        if (u + 1 < n_units) {
+            issue(u + 1, wB, soB, biB);
+            mfmas(u, wA, 0);
+            stage_write(BUF);
+            tail(u, soA, biA);
+            u++;
+        } else {
+            mfmas(u, wA, 0);
+            tail(u, soA, biA);
+            break;
+        }
+        if (u + 1 < n_units) {
+            issue(u + 1, wA, soA, biA);
+            mfmas(u, wB, BUF);
+            stage_write(0);
+            tail(u, soB, biB);
+            u++;
+        } else {
+            mfmas(u, wB, BUF);
+            tail(u, soB, biB);
+            break;
         }
     }
 }
@@ -880,11 +1250,14 @@ static int run_gemv(const qbk_factor *L, const void *x, bool xf32, void *y, bool
     return launch_gemv_stage(2, false, L, L->gemv_tab + 1, 1, ws, 0, y, 0, ybf16, s);
 }
 
+static long long g_stream_min_tasks = -1;  // qbk_tune(QBK_TUNE_STREAM_MIN_TASKS)
+
 // Workspace of the fp4 decode for n_layers layers of L's shape at `batch`:
-// [bop1 | bsc1 | t | bop2 | bsc2], each region 256-byte aligned.
+// [bop1 | bsc1 | bop2 | bsc2] (the fp8 operands and E8M0 scales of the two
+// stages), each region 256-byte aligned.
 struct Q4Plan {
     size_t ns1, ns2, ncol;
-    size_t o_bop1, o_bsc1, o_t, o_bop2, o_bsc2, bytes;
+    size_t o_bop1, o_bsc1, o_bop2, o_bsc2, bytes;
 };
 
 static Q4Plan q4_plan(const qbk_factor *L, size_t n_layers, size_t batch) {
@@ -900,7 +1273,6 @@ static Q4Plan q4_plan(const qbk_factor *L, size_t n_layers, size_t batch) {
     };
     p.o_bop1 = take(n_layers * p.ns1 * 4 * p.ncol * 32);
     p.o_bsc1 = take(n_layers * p.ns1 * 4 * p.ncol);
-    p.o_t = take(n_layers * batch * L->r_p * 2);
     p.o_bop2 = take(n_layers * p.ns2 * 4 * p.ncol * 32);
     p.o_bsc2 = take(n_layers * p.ns2 * 4 * p.ncol);
     p.bytes = off;
@@ -911,17 +1283,57 @@ static size_t q4_ws(const qbk_factor *L, size_t n_layers, size_t batch) {
     return q4_plan(L, n_layers, batch).bytes;
 }
 
-static int q4_ksplit(size_t ns) { return ns >= 16 ? 4 : (ns >= 8 ? 2 : 1); }
+// Waves that share a 64-row group split its slices: about 8 slices a wave
+// (two load steps), more splits while the launch is too small to fill the
+// chip (a single layer).
+static int q4_ksplit(size_t ns, size_t n_rg_total, int num_cus) {
+    int k = ns >= 32 ? 4 : (ns >= 16 ? 2 : 1);
+    while (k < 4 && ns >= (size_t)(2 * k) && n_rg_total * k < (size_t)num_cus * 8) k *= 2;
+    return k;
+}
 
-// phase 1: x -> fp8 B operands; 2: stage-1 MFMA GEMV -> t; 3: t -> B
-// operands; 4: stage-2 MFMA GEMV -> y.  x: [n][batch][din] (bf16, or f32 when
-// xf32), y: [n][batch][dout].
+// Workgroups per CU of the stream kernel at this LDS size (cached per variant).
+// Resident workgroups per CU of a stream-kernel variant (its LDS is fixed;
+// computed once per process).
+template <int STAGE, int NCOL, int U>
+static int q4_stream_occupancy(size_t lds) {
+    static int cached = 0;
+    if (!cached) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q4_stream_kernel<STAGE, NCOL, U>, 256, lds) !=
+                hipSuccess || n < 1)
+            n = 1;
+        cached = n;
+    }
+    return cached;
+}
+
+template <int STAGE, int NCOL>
+static void q4_launch_stream(const Q4Args &a, uint32_t n_tasks, int num_cus, hipStream_t s) {
+    constexpr int U = Q4_SU;
+    constexpr size_t BUF = U * 4 * NCOL * 32 + 256;
+    const size_t lds = 4 * (2 * BUF + 48);
+    const int per_cu = q4_stream_occupancy<STAGE, NCOL, U>(lds);
+    size_t grid = (size_t)num_cus * per_cu;
+    // at least one task per wave, but never fewer than 8 workgroups: task
+    // range x belongs to the workgroups with blockIdx % 8 == x
+    const size_t need = round_up(div_ceil(n_tasks, 4), 8);
+    if (grid > need) grid = need;
+    hipLaunchKernelGGL((q4_stream_kernel<STAGE, NCOL, U>), dim3((unsigned)grid), dim3(256), lds, s, a,
+                       n_tasks);
+}
+
+// phase 1: x -> stage 1's fp8 operand; 2: stage-1 MFMA GEMV, whose epilogue
+// writes t = bf16(Vb^T z) as stage 2's fp8 operand; 3: stage-2 MFMA GEMV -> y.
+// x: [n][batch][din] (bf16, or f32 when xf32), y: [n][batch][dout].
 static int q4_phase(int phase, const qbk_factor *L, const Q4Layer *tab, size_t n_layers,
                     size_t batch, const void *x, bool xf32, void *y, bool ybf16, void *ws,
                     hipStream_t s) {
     Q4Plan p = q4_plan(L, n_layers, batch);
     char *w = (char *)ws;
     Q4Args a{};
+    a.m8 = 0x88888888u;
+    a.c2 = 0x22222222u;
     a.batch = (int)batch;
     a.ncol = (int)p.ncol;
     a.y_bf16 = ybf16;
@@ -936,48 +1348,68 @@ static int q4_phase(int phase, const qbk_factor *L, const Q4Layer *tab, size_t n
         a.act_layer = batch * L->din;
         a.bop = (uint8_t *)(w + p.o_bop1);
         a.bsc = (uint8_t *)(w + p.o_bsc1);
-        a.out = w + p.o_t;
-        a.out_ld = L->r_p;
-        a.out_layer = batch * L->r_p;
+        a.tb_op = (uint8_t *)(w + p.o_bop2);
+        a.tb_sc = (uint8_t *)(w + p.o_bsc2);
+        a.tb_ns = p.ns2;
     } else {
         a.layers = tab + n_layers;
         a.rows_p = L->dout_p;
         a.rows_valid = L->dout;
         a.k_valid = L->r;
         a.ns = p.ns2;
-        a.act = w + p.o_t;
-        a.act_ld = L->r_p;
-        a.act_layer = batch * L->r_p;
         a.bop = (uint8_t *)(w + p.o_bop2);
         a.bsc = (uint8_t *)(w + p.o_bsc2);
         a.out = y;
         a.out_ld = L->dout;
         a.out_layer = batch * L->dout;
     }
-    if (phase == 1 || phase == 3) {
+    if (phase == 1) {
+        const size_t elem = xf32 ? 4 : 2;
+        a.vec_ok = a.act_ld % 4 == 0 && (uintptr_t)a.act % (4 * elem) == 0;
         size_t items = n_layers * batch * a.ns * 4;
-        dim3 g((unsigned)div_ceil(items, 256));
-        if (phase == 1 && xf32)
+        dim3 g((unsigned)div_ceil(items * 8, 256));
+        if (xf32)
             hipLaunchKernelGGL((q4_prep_kernel<1, true>), g, dim3(256), 0, s, a, items);
-        else if (phase == 1)
-            hipLaunchKernelGGL((q4_prep_kernel<1, false>), g, dim3(256), 0, s, a, items);
         else
-            hipLaunchKernelGGL((q4_prep_kernel<2, false>), g, dim3(256), 0, s, a, items);
-    } else {
-        const int ksplit = q4_ksplit(a.ns);
-        const size_t n_rg = a.rows_p / 64, rg_per_wg = 4 / ksplit;
-        dim3 g((unsigned)div_ceil(n_rg, rg_per_wg), (unsigned)n_layers);
-#define Q4_LAUNCH(ST)                                                                          \
-    if (ksplit == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, 4>), g, dim3(256), 0, s, a);       \
-    else if (ksplit == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, 2>), g, dim3(256), 0, s, a);  \
-    else hipLaunchKernelGGL((q4_gemv_kernel<ST, 1>), g, dim3(256), 0, s, a);
-        if (phase == 2) {
-            Q4_LAUNCH(1)
-        } else {
-            Q4_LAUNCH(2)
-        }
-#undef Q4_LAUNCH
+            hipLaunchKernelGGL((q4_prep_kernel<1, false>), g, dim3(256), 0, s, a, items);
+        QBK_HIP(hipGetLastError());
+        return QBK_OK;
     }
+    const size_t n_rg = a.rows_p / 64;
+    const size_t n_tasks = n_layers * n_rg;
+    // the persistent kernel once a stage has enough 64-row tasks to keep
+    // every resident wave busy (or from the tuned threshold)
+    const long long min_tasks = g_stream_min_tasks >= 0 ? g_stream_min_tasks : (long long)L->num_cus * 8;
+    if (batch <= 2 && (long long)n_tasks >= min_tasks && n_tasks < (1ull << 31)) {
+        if (phase == 2 && batch == 1) q4_launch_stream<1, 2>(a, (uint32_t)n_tasks, L->num_cus, s);
+        else if (phase == 2) q4_launch_stream<1, 4>(a, (uint32_t)n_tasks, L->num_cus, s);
+        else if (batch == 1) q4_launch_stream<2, 2>(a, (uint32_t)n_tasks, L->num_cus, s);
+        else q4_launch_stream<2, 4>(a, (uint32_t)n_tasks, L->num_cus, s);
+        QBK_HIP(hipGetLastError());
+        return QBK_OK;
+    }
+    const int ksplit = q4_ksplit(a.ns, n_tasks, L->num_cus);
+    const size_t rg_per_wg = 4 / ksplit;
+    dim3 g((unsigned)div_ceil(n_rg, rg_per_wg), (unsigned)n_layers);
+    // operand + scales of one layer in LDS when they fit Q4_LDS_MAX
+    const size_t opnd = round_up(a.ns * 4 * p.ncol * 33, 16) + 48;  // + zero slot
+    const bool blds = opnd <= Q4_LDS_MAX;
+    const size_t red = ksplit > 1 ? 4 * 4 * 64 * 16 : 0;
+    const size_t lds = blds ? (opnd > red ? opnd : red) : red;
+#define Q4_LAUNCH(ST, KS)                                                                      \
+    if (blds) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, true>), g, dim3(256), lds, s, a);     \
+    else hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, false>), g, dim3(256), lds, s, a);
+#define Q4_LAUNCH_KS(ST)                                                                       \
+    if (ksplit == 4) { Q4_LAUNCH(ST, 4) }                                                      \
+    else if (ksplit == 2) { Q4_LAUNCH(ST, 2) }                                                 \
+    else { Q4_LAUNCH(ST, 1) }
+    if (phase == 2) {
+        Q4_LAUNCH_KS(1)
+    } else {
+        Q4_LAUNCH_KS(2)
+    }
+#undef Q4_LAUNCH_KS
+#undef Q4_LAUNCH
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }
@@ -986,7 +1418,7 @@ static int run_q4(const qbk_factor *L, size_t batch, const void *x, bool xf32, v
                   bool ybf16, void *ws, hipStream_t s) {
     // a single layer's table is {stage 1, stage 2}: tab + n_layers is stage 2
     const Q4Layer *tab = (const Q4Layer *)L->q4_tab;
-    for (int ph = 1; ph <= 4; ph++) {
+    for (int ph = 1; ph <= Q4_PHASES; ph++) {
         int rc = q4_phase(ph, L, tab, 1, batch, x, xf32, y, ybf16, ws, s);
         if (rc) return rc;
     }
@@ -1319,13 +1751,13 @@ size_t qbk_factor_set_workspace_size(const qbk_factor_set *S) {
     return S ? q4_ws(S->first, S->n, 1) : 0;
 }
 
-// x [n][din] bf16 -> t (workspace, [n][r_p] bf16) -> y [n][dout] bf16.
+// x [n][din] bf16 -> y [n][dout] bf16 in three phases (see q4_phase).
 int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, const uint16_t *x,
                              uint16_t *y, void *workspace, size_t workspace_size, void *stream) {
     int rc;
     if (!S) return fail(QBK_ERR_VALIDATION, "null layer set");
-    if (stage < 1 || stage > 4)
-        return fail(QBK_ERR_VALIDATION, fmt("stage must be 1..4, got %d", stage));
+    if (stage < 1 || stage > Q4_PHASES)
+        return fail(QBK_ERR_VALIDATION, fmt("stage must be 1..%d, got %d", Q4_PHASES, stage));
     if ((rc = bind(ctx))) return rc;
     if (workspace_size < qbk_factor_set_workspace_size(S))
         return fail(QBK_ERR_VALIDATION,
@@ -1335,9 +1767,18 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, c
                     (hipStream_t)stream);
 }
 
+long long qbk_tune(int knob, long long value) {
+    if (knob == QBK_TUNE_STREAM_MIN_TASKS) {
+        const long long prev = g_stream_min_tasks;
+        g_stream_min_tasks = value < 0 ? -1 : value;
+        return prev;
+    }
+    return -2;
+}
+
 int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *S, const uint16_t *x,
                               uint16_t *y, void *workspace, size_t workspace_size, void *stream) {
-    for (int ph = 1; ph <= 4; ph++) {
+    for (int ph = 1; ph <= Q4_PHASES; ph++) {
         int rc = qbk_factor_set_stage_dev(ctx, S, ph, x, y, workspace, workspace_size, stream);
         if (rc) return rc;
     }

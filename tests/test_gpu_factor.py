@@ -86,17 +86,45 @@ def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
     same(got_b, orc.f32_to_bf16_fast(want))
 
 
+def e4m3(b):
+    """OCP fp8 e4m3 bytes -> float64 (bias 7, subnormals, no infinities)."""
+    b = np.asarray(b, np.uint8).astype(np.int64)
+    e, m = (b >> 3) & 0xF, b & 7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7))
+    return np.where(b & 0x80, -v, v)
+
+
+def kq4(g, e):
+    """k offset within a 128-slice of fp4 element e of lane group g (gfx950
+    scaled MFMA, measured): two runs of 16."""
+    return 16 * (g >> 1) + 64 * (g & 1) + (e & 15) + 32 * (e >> 4)
+
+
 def gpu_t(layer, ws, batch):
     """The device's t (bf16) read back from the documented workspace layout."""
     r, rp = layer.r, -(-layer.r // 128) * 128
     rnd = lambda n: -(-n // 256) * 256
     if batch <= 8:
-        # fp4 decode: [B operands 1 | scales 1 | t bf16 [batch][r_p] | ...]
-        ns1, ncol = -(-layer.din // 128), 2 * batch
-        off = rnd(ns1 * 4 * ncol * 32) + rnd(ns1 * 4 * ncol)
-        t = ws[off: off + batch * rp * 2].view(np.uint16).reshape(batch, rp)
-        assert not t[:, r:].any()
-        return t[:, :r]
+        # fp4 decode: [op1 | sc1 | op2 [slice][4][ncol][32] | sc2 [slice][4][ncol]]:
+        # t is stage 2's operand, hi (column 2b) + lo (2b+1), E8M0 scales
+        ns1, ns2, ncol = -(-layer.din // 128), rp // 128, 2 * batch
+        o2 = rnd(ns1 * 4 * ncol * 32) + rnd(ns1 * 4 * ncol)
+        op = ws[o2: o2 + ns2 * 4 * ncol * 32].reshape(ns2, 4, ncol, 32)
+        sc = ws[o2 + rnd(ns2 * 4 * ncol * 32):][: ns2 * 4 * ncol].reshape(ns2, 4, ncol).astype(np.int64)
+        t = np.zeros((batch, rp))
+        for g in range(4):
+            for e in range(32):
+                gb, byte, k = 2 * (g & 1) + (e >> 4), 16 * (g >> 1) + (e & 15), kq4(g, e)
+                for b in range(batch):
+                    hi = e4m3(op[:, gb, 2 * b, byte]) * 2.0 ** (sc[:, g, 2 * b] - 127)
+                    lo = e4m3(op[:, gb, 2 * b + 1, byte]) * 2.0 ** (sc[:, g, 2 * b + 1] - 127)
+                    t[b, np.arange(ns2) * 128 + k] = hi + lo
+        from oracle import oracle as orc
+
+        tb = orc.f32_to_bf16_fast(t.astype(np.float32))
+        assert np.array_equal(orc.bf16_to_f32(tb).astype(np.float64), t), "operand is not a bf16 t"
+        assert not tb[:, r:].any()
+        return tb[:, :r]
     # [split][batch][r_p] f32 partials, then t bf16 [batch][r_p]
     for s in (1, 2, 4, 8):
         off = rnd(s * batch * rp * 4)
@@ -149,24 +177,71 @@ def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
     assert np.all(np.abs(y - y_or) <= np.abs(L["s1"]) * (uulp * 1.01 + reassoc) + 1e-6 * np.abs(y_or))
 
 
-def test_set_decode_matches_single_layers(ctx, orc):
-    from quantibbler_amd import FactorSet
-
-    say("factor set decode")
-    rng = np.random.default_rng(77)
-    Ls = [make_layer(orc, rng, 512, 1024, 200) for _ in range(5)]
-    layers = [upload(ctx, L) for L in Ls]
-    S = FactorSet(ctx, layers)
-    x = orc.f32_to_bf16_fast(rng.standard_normal((5, 1024)).astype(np.float32))
+def set_decode(S, x, dout):
     xd = torch.from_numpy(x.view(np.int16)).cuda()
-    yd = torch.empty((5, 512), dtype=torch.int16, device="cuda")
+    yd = torch.empty((x.shape[0], dout), dtype=torch.int16, device="cuda")
     ws = torch.zeros(S.workspace_size(), dtype=torch.uint8, device="cuda")
     S.decode_dev(xd, yd, ws, ws.numel(), torch.cuda.current_stream())
     torch.cuda.synchronize()
-    ys = yd.cpu().numpy().view(np.uint16)
-    for i, layer in enumerate(layers):
+    return yd.cpu().numpy().view(np.uint16)
+
+
+@pytest.fixture
+def stream_forced():
+    """Run the persistent streaming GEMV on every decode stage."""
+    from quantibbler_amd import tune_stream_min_tasks
+
+    prev = tune_stream_min_tasks(0)
+    yield
+    tune_stream_min_tasks(prev)
+
+
+@pytest.mark.parametrize("dout,din,r,n", [(512, 1024, 200, 5), (300, 640, 200, 7), (96, 128, 64, 3)])
+def test_set_decode_matches_single_layers(ctx, orc, dout, din, r, n):
+    """Integer-exact set decode: bit-identical to the oracle and to the
+    single-layer path, on the default kernels and on the streaming kernel
+    (forced; partial units where din/128 or r_p/128 is not a multiple of 4)."""
+    from quantibbler_amd import FactorSet, tune_stream_min_tasks
+
+    say("factor set decode", dout, din, r, n)
+    rng = np.random.default_rng(77 + din)
+    Ls = [make_layer(orc, rng, dout, din, r, integer=True) for _ in range(n)]
+    layers = [upload(ctx, L) for L in Ls]
+    S = FactorSet(ctx, layers)
+    x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (n, din)).astype(np.float32))
+    ys = set_decode(S, x, dout)
+    prev = tune_stream_min_tasks(0)
+    try:
+        ys_stream = set_decode(S, x, dout)
+    finally:
+        tune_stream_min_tasks(prev)
+    for i, (L, layer) in enumerate(zip(Ls, layers)):
+        want = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"],
+                                           x[i:i + 1])
+        wb = orc.f32_to_bf16_fast(want)[0]
+        same(ys[i], wb, f"set decode, layer {i}")
+        same(ys_stream[i], wb, f"streaming set decode, layer {i}")
         yi, _ = run_dev(layer, x[i:i + 1], "bfloat16")
         same(ys[i], yi[0])
+
+
+@pytest.mark.parametrize("dout,din,r", [(256, 512, 128), (300, 200, 37), (1024, 4096, 1102)])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_stream_kernel_single_layer(ctx, orc, stream_forced, dout, din, r, batch):
+    """The streaming GEMV (forced) on one layer at batch 1 and 2: integer-exact
+    bit identity with the oracle, and the stage bounds on config inputs."""
+    say("factor streaming kernel", dout, din, r, "batch", batch)
+    rng = np.random.default_rng(3 * dout + din + r + batch)
+    L = make_layer(orc, rng, dout, din, r, integer=True)
+    layer = upload(ctx, L)
+    x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (batch, din)).astype(np.float32))
+    want = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
+    got, ws = run_dev(layer, x)
+    same(got, want)
+    t = gpu_t(layer, ws, batch)
+    _, t_orc = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"],
+                                           L["bias"], x, want_t=True)
+    same(t, t_orc)
 
 
 def test_apply_host_faces(ctx, orc):
