@@ -3,16 +3,18 @@
 
 Headline (BASELINE.json metric, configs[0] shape): the binary-factor linear
 decode GEMV, y = s1 . (Ub (Vb^T (s2 . x))), m = n = 4096, r = 1024, batch 1,
-bf16 x and y, f32 accumulation, over a rotation of distinct layers (default
-512, 562 MB of weights: larger than the 256 MB Infinity Cache, so HBM is what
-is measured).  One step = one decode of every layer in the set: two
-launches (stage 1: t = bf16(Vb^T bf16(s2*x)); stage 2: y = bf16(bf16(Ub t)*s1)).
+bf16 x and y, f32 accumulation, over a set of distinct layers (default 512,
+537 MB of signs: larger than the 256 MB Infinity Cache, so HBM is what is
+measured).  One step = one decode of every layer in the set: three launches
+(the fp8 split of x; stage 1, t = bf16(Vb^T bf16(s2*x)), written as stage 2's
+fp8 operand; stage 2, y = bf16(bf16(Ub t)*s1)).
 
 value = algorithmic bytes of all layers / step time, with the BASELINE.md
 per-layer count 1,097,728 B (U 512 KiB + V 512 KiB + x 8 KiB + y 8 KiB + s1,
-s2 32 KiB); each stage kernel accounts for half (548,864 B per layer).
-Stage durations come from HIP events recorded on the launch stream around
-each launch inside the timed region.
+s2 32 KiB).  The timed region holds only the steps between two events.  The
+roofline's kernel duration: that phase alone, launched `steps` times back to
+back between two events on the launch stream (rocprofv3 --kernel-trace
+--stats of the same command agrees; profiles/).
 
 Extras (same JSON line): single-layer decode latency; prefill GEMM TFLOP/s at
 B in {16, 128, 512, 2048}; block-scaled SageAttention prefill at
@@ -61,6 +63,10 @@ def make_layers(qa, ctx, np, count, seed):
 
 
 def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
+    """The timed region: `steps` decodes of the whole set (three launches
+    each), bracketed by two events and nothing else.  Then each phase alone,
+    `steps` launches back to back between two events, for its average
+    launch duration (the roofline's denominator)."""
     S = qa.FactorSet(ctx, layers)
     L = len(layers)
     rng = np.random.default_rng(7)
@@ -73,21 +79,24 @@ def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
     for _ in range(warmup):
         S.decode_dev(x, y, ws, ws_n, st)
     torch.cuda.synchronize()
-    # one event before each of the three phases and one after the last
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(st)
-    for k in range(steps):
-        for ph in range(1, 4):
-            ev[k][ph - 1].record(st)
-            S.stage_dev(ph, x, y, ws, ws_n, st)
-        ev[k][3].record(st)
+    for _ in range(steps):
+        S.decode_dev(x, y, ws, ws_n, st)
     end.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / steps
-    phase_ms = [sum(e[p].elapsed_time(e[p + 1]) for e in ev) / steps for p in range(3)]
+    phase_ms = []
+    for ph in range(1, 4):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(steps):
+            S.stage_dev(ph, x, y, ws, ws_n, st)
+        b.record(st)
+        torch.cuda.synchronize()
+        phase_ms.append(a.elapsed_time(b) / steps)
     return dict(ms_per_step=ms_step, phase_ms=phase_ms, wall_s=wall, set=S)
 
 
@@ -196,6 +205,9 @@ def main():
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-traffic", action="store_true",
+                    help="first run an elementwise kernel of known traffic (256 MiB read, 256 MiB "
+                         "written) that rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs scale by")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -208,6 +220,13 @@ def main():
     import quantibbler_amd as qa
 
     ctx = qa.GpuContext(0)
+    if args.calibrate_traffic:
+        a = torch.ones(1 << 26, dtype=torch.int32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        del a, b
     log(f"building {args.layers} config-1 layers ...")
     layers, host = make_layers(qa, ctx, np, args.layers, seed=1)
     log("decode sweep ...")
@@ -259,7 +278,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": None,
-            "kernel": f"q4_stream_kernel<{dom},2,4> (decode stage {dom}, fp4 x fp8 scaled MFMA, persistent)",
+            "kernel": f"q4_gemv_kernel<{dom},*,2> (decode stage {dom}, fp4 x fp8 scaled MFMA)",
             "bytes_per_launch": bytes_launch, "avg_launch_ms": round(dom_ms, 4),
         },
         "cpu_baseline": cpu,

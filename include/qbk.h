@@ -155,13 +155,6 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *set, int stage,
                              const uint16_t *x, uint16_t *y, void *workspace,
                              size_t workspace_size, void *stream);
 
-/* Tuning knobs of this implementation; no counterpart in the reference.
- * QBK_TUNE_STREAM_MIN_TASKS: a decode stage (batch 1-2) runs the persistent
- * streaming GEMV once it has at least `value` 64-row tasks; -1 restores the
- * library's own threshold.  Returns the previous value (-2: unknown knob).
- * Process-wide; set it while no decode call is in flight. */
-#define QBK_TUNE_STREAM_MIN_TASKS 1
-long long qbk_tune(int knob, long long value);
 
 /* ---- attention (gpu_attention.rs) ----------------------------------------- */
 

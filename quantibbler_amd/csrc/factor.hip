@@ -592,8 +592,6 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs A) {
 #define Q4_MAXB 8
 #define Q4_U 8  // slices whose sign loads a wave issues together
 #define Q4_PHASES 3  // prep x, stage 1 (+ stage 2's operand), stage 2
-#define Q4_SU 4      // slices per unit of the stream kernel
-#define Q4_LDS_MAX (40 * 1024)  // largest per-layer operand staged in LDS
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -620,7 +618,7 @@ struct Q4Args {
     size_t out_ld, out_layer;
     int y_bf16;
     int vec_ok;                               // act rows allow 4-element vector loads
-    uint32_t m8, c2;                          // 0x88888888, 0x22222222 (fp4 sign build)
+    uint32_t c7;                              // 0x77777777 (fp4 sign build)
     uint8_t *tb_op, *tb_sc;                   // stage 1: stage 2's operand and scales
     size_t tb_ns;                             // stage 2's slices per layer
 };
@@ -722,17 +720,21 @@ __global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a, size_t n_items) 
     }
 }
 
-// Signs of one 16-row tile as fp4 e2m1 +-1 (0x2 / 0xA): nibble e of VGPR j
-// carries bit 4e + 3 - j of the word, moved to the nibble's sign bit.  7 VALU
-// ops per MFMA: m8 arrives as a kernel argument (an SGPR) and c2 sits in a
-// VGPR so that the compiler fuses and-or (gfx9 VOP3 takes one scalar operand
-// and no literal).
-__device__ __forceinline__ i32x8_t q4_signs(uint32_t w, uint32_t m8, uint32_t c2) {
+// Signs of one 16-row tile as fp4 e2m1: nibble e of VGPR j carries bit
+// 4e + 3 - j of the word in its sign bit, and OR-ing 0x7 into every nibble
+// forces the other three bits to 1 whatever the shift brought in, so each
+// element is exactly +-6 (e2m1 0111 = 1.5 * 2^2).  One VALU op per VGPR
+// (v_lshl_or_b32 with c7 = 0x77777777 in an SGPR; v_or_b32 for j = 3).  The
+// MFMA's A scale 2^-2 (E8M0 125) makes the elements +-1.5, and the epilogue
+// divides by 1.5: exact whenever the f32 sum is (1.5 * sum then needs one
+// more significant bit).
+#define Q4_SCALE_A 125
+__device__ __forceinline__ i32x8_t q4_signs(uint32_t w, uint32_t c7) {
     i32x8_t av;
-    av[0] = (int)(((w << 3) & m8) | c2);
-    av[1] = (int)(((w << 2) & m8) | c2);
-    av[2] = (int)(((w << 1) & m8) | c2);
-    av[3] = (int)((w & m8) | c2);
+    av[0] = (int)((w << 3) | c7);
+    av[1] = (int)((w << 2) | c7);
+    av[2] = (int)((w << 1) | c7);
+    av[3] = (int)(w | c7);
     av[4] = av[5] = av[6] = av[7] = 0;
     return av;
 }
@@ -740,7 +742,7 @@ __device__ __forceinline__ i32x8_t q4_signs(uint32_t w, uint32_t m8, uint32_t c2
 // One 128-k slice of a 64-row group: the four row tiles' MFMAs against the
 // fp8 operand held in LDS at byte offset bo (scale byte at so).
 __device__ __forceinline__ void q4_slice_lds(f32x4_t acc[4], const uint4 &w4, const uint8_t *lds,
-                                             uint32_t bo, uint32_t so, uint32_t m8, uint32_t c2) {
+                                             uint32_t bo, uint32_t so, uint32_t c7) {
     const uint4 *bq = (const uint4 *)(lds + bo);
     const uint4 b0 = bq[0], b1 = bq[1];
     const i32x8_t bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
@@ -749,132 +751,136 @@ __device__ __forceinline__ void q4_slice_lds(f32x4_t acc[4], const uint4 &w4, co
     const uint32_t wr[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
     for (int rt = 0; rt < 4; rt++)
-        acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], m8, c2), bv, acc[rt],
-                                                                  4, 0, 0, 127, 0, bs);
+        acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], c7), bv, acc[rt],
+                                                                  4, 0, 0, Q4_SCALE_A, 0, bs);
 }
 
-// Stage-1 epilogue: t = bf16(hi + lo) for the 64 rows of group rg, written
-// straight into stage 2's fp8 operand (the prep's split, done in registers).
-// Rows 16rt + 4g + i of the group sit in lane (col 2b, g); the group is half
-// of stage-2 slice rg/2, and its rows 16rt + 4g + i belong to scale group
-// G = 2(rt&1) + (rg&1), B lane group 2(rg&1) + (rt>>1), byte 16(rt&1) + 4g + i.
-// Rows >= rows_valid are zero.  Every lane joins the shuffles.
-__device__ __forceinline__ void q4_emit_t(const f32x4_t acc[4], const Q4Args &a, size_t li,
-                                          size_t rg, int lane) {
+// Epilogue of one 64-row group, one row per lane: the accumulators are
+// transposed through the wave's LDS region T [ncol][64] (lane (col, g) holds
+// rows 16rt + 4g + i of column col), then lane l finishes row rg*64 + l of
+// every token: v = (hi + lo) / 1.5 (the A scale of q4_signs).
+//
+// Stage 1 writes t = bf16(v) (0 past rows_valid) as stage 2's fp8 operand:
+// row l of the group is element e = (l & 15) + 16 (l >> 5) of scale group
+// G = 2((l >> 4) & 1) + (rg & 1) of stage-2 slice rg/2 (the 32 rows sharing
+// G differ in lane bits 0-3 and 5, so the block max is five xor shuffles);
+// its bytes go to B lane group 2(rg & 1) + (l >> 5), byte 16((l >> 4) & 1) +
+// (l & 15), hi to column 2b and lo to 2b + 1.
+//
+// Stage 2 writes y = bf16(v) * s1 + bias (so / bi: this lane's row).
+template <int STAGE>
+__device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, const Q4Args &a, int ncol,
+                                            size_t li, size_t rg, int lane, float so, float bi) {
     const int col = lane & 15, g = lane >> 4;
-    float t[4][4];
+    if (col < ncol) {
 #pragma unroll
-    for (int rt = 0; rt < 4; rt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float lo = __shfl_down(acc[rt][i], 1, 64);
-            const size_t row = rg * 64 + 16 * rt + 4 * g + i;
-            t[rt][i] = row < a.rows_valid ? bf16_to_f32(f32_to_bf16(acc[rt][i] + lo)) : 0.0f;
-        }
-    const bool writer = (col & 1) == 0 && col < a.ncol;
-    const size_t b = col >> 1;
-    const size_t base = (li * a.tb_ns + (rg >> 1)) * 4;
-#pragma unroll
-    for (int q = 0; q < 2; q++) {
-        // scale group G = 2q + (rg&1): rows of tiles q and q+2
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) amax = fmaxf(amax, fmaxf(fabsf(t[q][i]), fabsf(t[q + 2][i])));
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-        const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
-        const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
-        int hw[2], lw[2];
-        float r[2][4];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const float *v = t[q + 2 * h];
-            int w = __builtin_amdgcn_cvt_pk_fp8_f32(v[0] * inv_hi, v[1] * inv_hi, 0, false);
-            w = __builtin_amdgcn_cvt_pk_fp8_f32(v[2] * inv_hi, v[3] * inv_hi, w, true);
-            hw[h] = w;
-            r[h][0] = v[0] - __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;
-            r[h][1] = v[1] - __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
-            r[h][2] = v[2] - __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
-            r[h][3] = v[3] - __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
-        }
-        float rmax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) rmax = fmaxf(rmax, fmaxf(fabsf(r[0][i]), fabsf(r[1][i])));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 16, 64));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
-        const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
-        const float inv_lo = pow2f(-e_lo);
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int w = __builtin_amdgcn_cvt_pk_fp8_f32(r[h][0] * inv_lo, r[h][1] * inv_lo, 0, false);
-            lw[h] = __builtin_amdgcn_cvt_pk_fp8_f32(r[h][2] * inv_lo, r[h][3] * inv_lo, w, true);
-        }
-        if (writer) {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const size_t slot = (base + 2 * (rg & 1) + h) * a.ncol + 2 * b;  // hi column; lo = +1
-                const size_t byte = 16 * q + 4 * g;
-                *(uint32_t *)(a.tb_op + slot * 32 + byte) = (uint32_t)hw[h];
-                *(uint32_t *)(a.tb_op + (slot + 1) * 32 + byte) = (uint32_t)lw[h];
-            }
-            if (g == 0) {
-                const size_t sc = (base + 2 * q + (rg & 1)) * a.ncol + 2 * b;
-                a.tb_sc[sc] = (uint8_t)(e_hi + 127);
-                a.tb_sc[sc + 1] = (uint8_t)(e_lo + 127);
-            }
-        }
+        for (int rt = 0; rt < 4; rt++) *(f32x4_t *)(T + col * 64 + 16 * rt + 4 * g) = acc[rt];
     }
-}
-
-// Stage-2 epilogue: y = bf16(hi + lo) * s1 + bias for the 64 rows of group
-// rg; so / bi are this lane's row (rg*64 + lane) of s1 and bias.
-__device__ __forceinline__ void q4_emit_y(const f32x4_t acc[4], const Q4Args &a, size_t li, size_t rg,
-                                          int lane, float so, float bi) {
-    const int col = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int rt = 0; rt < 4; rt++) {
-        f32x4_t lo, sov, biv;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            lo[i] = __shfl_down(acc[rt][i], 1, 64);
-            sov[i] = __shfl(so, 16 * rt + 4 * g + i, 64);
-            biv[i] = __shfl(bi, 16 * rt + 4 * g + i, 64);
-        }
-        if ((col & 1) == 0 && col < a.ncol) {
-            const size_t b = col >> 1;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const size_t row = rg * 64 + 16 * rt + 4 * g + i;
-                if (row >= a.rows_valid) continue;
-                const float u = bf16_to_f32(f32_to_bf16(acc[rt][i] + lo[i]));
-                const float y = u * sov[i] + biv[i];
-                const size_t o = li * a.out_layer + b * a.out_ld + row;
+    __builtin_amdgcn_wave_barrier();
+    const size_t row = rg * 64 + lane;
+    const bool valid = row < a.rows_valid;
+    for (int b = 0; b < (ncol >> 1); b++) {
+        const float v = (T[(2 * b) * 64 + lane] + T[(2 * b + 1) * 64 + lane]) / 1.5f;
+        const float t = valid ? bf16_to_f32(f32_to_bf16(v)) : 0.0f;
+        if (STAGE == 2) {
+            if (valid) {
+                const float y = t * so + bi;
+                const size_t o = li * a.out_layer + (size_t)b * a.out_ld + row;
                 if (a.y_bf16)
                     ((uint16_t *)a.out)[o] = f32_to_bf16(y);
                 else
                     ((float *)a.out)[o] = y;
             }
+            continue;
+        }
+        float amax = fabsf(t);
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+        const int hw = __builtin_amdgcn_cvt_pk_fp8_f32(t * pow2f(-e_hi), 0.0f, 0, false);
+        const float r = t - __builtin_amdgcn_cvt_f32_fp8(hw, 0) * pow2f(e_hi);  // exact residual
+        float rmax = fabsf(r);
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 4, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 8, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+        const int lw = __builtin_amdgcn_cvt_pk_fp8_f32(r * pow2f(-e_lo), 0.0f, 0, false);
+        const int q = (lane >> 4) & 1, h = lane >> 5;
+        const size_t base = (li * a.tb_ns + (rg >> 1)) * 4;
+        const size_t slot = (base + 2 * (rg & 1) + h) * ncol + 2 * b;  // hi column; lo = +1
+        const size_t byte = 16 * q + (lane & 15);
+        a.tb_op[slot * 32 + byte] = (uint8_t)hw;
+        a.tb_op[(slot + 1) * 32 + byte] = (uint8_t)lw;
+        if ((lane & 47) == 0) {  // lanes 0 and 16: scale groups 2q + (rg & 1)
+            const size_t sc = (base + 2 * q + (rg & 1)) * ncol + 2 * b;
+            a.tb_sc[sc] = (uint8_t)(e_hi + 127);
+            a.tb_sc[sc + 1] = (uint8_t)(e_lo + 127);
         }
     }
 }
 
-// Workgroup = 4 waves; KSPLIT waves share a 64-row group and split its
-// slices, 4/KSPLIT row groups per workgroup, so a workgroup covers every
-// slice of its layer.  Lane l loads the 16 bytes of its four row tiles' sign
-// words per slice (1 KiB per wave per slice, contiguous over the slices).
-// Used for small launches (a single layer) and batches above 2; many-layer
-// decode at batch 1-2 takes q4_stream_kernel.
+// Slice j of a step: the fp8 operand from the wave's staged LDS region
+// (NCOL > 0) or from global memory (NCOL == 0), then the four MFMAs.
+template <int NCOL>
+__device__ __forceinline__ void q4_step(f32x4_t acc[4], const uint4 &w4u, uint32_t j, const uint8_t *wl,
+                                        uint32_t bo0, uint32_t bstep, uint32_t so0, uint32_t sstep,
+                                        const uint8_t *gb, const uint8_t *gs, size_t sb, int g, int ncol,
+                                        int col, bool bcol, uint32_t c7) {
+    if (NCOL > 0) {
+        q4_slice_lds(acc, w4u, wl, bo0 + j * bstep, so0 + j * sstep, c7);
+        return;
+    }
+    i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
+    int bs = 127;
+    if (bcol) {
+        const size_t slot = ((sb + j) * 4 + g) * ncol + col;
+        const uint4 *bq = (const uint4 *)(gb + slot * 32);
+        const uint4 b0 = bq[0], b1 = bq[1];
+        bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        bs = gs[slot];
+    }
+    const uint32_t wr[4] = {w4u.x, w4u.y, w4u.z, w4u.w};
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++)
+        acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], c7), bv, acc[rt], 4, 0, 0,
+                                                                  Q4_SCALE_A, 0, bs);
+}
+
+// LDS bytes of one wave's region: the staged operand of Q4_U slices (NCOL
+// columns), their scales (one dword per lane), a zero slot, and room for the
+// epilogue's transpose.
+__host__ __device__ constexpr uint32_t q4_wave_lds(int ncol) {
+    return ncol > 0 ? (uint32_t)(Q4_U * 4 * ncol * 32 + 256 + 48) : 16 * 64 * 4;
+}
+
+// Decode GEMV.  Workgroup = 4 waves; KSPLIT waves share a 64-row group and
+// split its slices (4/KSPLIT row groups per workgroup).  Lane l loads the 16
+// bytes of its four row tiles' sign words per slice (1 KiB per wave per
+// slice, contiguous over the slices); Q4_U slices are loaded per step.
 //
-// BLDS: the layer's fp8 operand and scales are copied to LDS once per
-// workgroup before the sign loads are issued.  Otherwise (operands larger
-// than Q4_LDS_MAX) each slice's operand is read from global memory.
-template <int STAGE, int KSPLIT, bool BLDS>
+// NCOL > 0 (batch 1-2): each wave stages the fp8 operand of its own slices
+// through registers into its LDS region -- operand loads issued first, sign
+// loads right behind them, no workgroup barrier -- and reads it per slice;
+// lanes past the batch's columns read a zero slot.  NCOL == 0 (batch 3-8):
+// lanes read the operand of each slice from global memory (L2).
+//
+// Loads are unconditional (indices clamped into the layer; the MFMAs of
+// clamped slices are skipped) so that the compiler's wait counts stay exact:
+// each slice's MFMAs start as soon as its own load lands.
+template <int STAGE, int KSPLIT, int NCOL>
 __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
+    const int ncol = NCOL > 0 ? NCOL : a.ncol;
     const size_t li = blockIdx.y;
-    const Q4Layer L = a.layers[li];
+    const cq4layer_t *lp = (const cq4layer_t *)a.layers + li;
+    const Q4Layer L = {lp->bits, lp->s_in, lp->s_out, lp->bias};
     constexpr int RG_PER_WG = 4 / KSPLIT;
     const size_t rg = (size_t)blockIdx.x * RG_PER_WG + wave / KSPLIT;
     const int ks = wave % KSPLIT;
@@ -883,45 +889,27 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
     const size_t s0 = ks * per < a.ns ? ks * per : a.ns;
     const size_t s1 = s0 + per < a.ns ? s0 + per : a.ns;
     const int col = lane & 15, g = lane >> 4;
-    const bool bcol = col < a.ncol;
+    const bool bcol = col < ncol;
     const bool live = rg < n_rg;
-    const uint32_t bbytes = (uint32_t)(a.ns * 4 * a.ncol * 32), sbytes = (uint32_t)(a.ns * 4 * a.ncol);
-    const uint8_t *gb = a.bop + li * bbytes;
-    const uint8_t *gs = a.bsc + li * sbytes;
-    const uint32_t m8 = a.m8;
-    uint32_t c2;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(c2) : "s"(a.c2));
+    const size_t rgc = live ? rg : n_rg - 1;
+    const uint32_t c7 = a.c7;
+    const uint32_t wreg = q4_wave_lds(NCOL);  // the launch allocates 4 * this (+ red)
+    uint8_t *wl = q4_lds + wave * wreg;
+    const size_t opl = a.ns * 4 * ncol * 32, scl = a.ns * 4 * ncol;  // per layer
+    const uint8_t *gb = a.bop + li * opl;
+    const uint8_t *gs = a.bsc + li * scl;
 
-    // fp8 operand of slice s for this lane: LDS offsets (BLDS) or global
-    const uint32_t zslot = (bbytes + sbytes + 15) & ~15u;  // 32 zero bytes, then scale 127
-    const uint32_t slot0 = (uint32_t)(g * a.ncol + col);
-    const uint32_t bo0 = bcol ? slot0 * 32 : zslot, bstep = bcol ? 4 * a.ncol * 32 : 0;
-    const uint32_t so0 = bcol ? bbytes + slot0 : zslot + 32, sstep = bcol ? 4 * a.ncol : 0;
-    if (BLDS) {
-        for (uint32_t o = tid * 16; o < bbytes; o += 256 * 16)
-            *(uint4 *)(q4_lds + o) = *(const uint4 *)(gb + o);
-        for (uint32_t o = tid * 8; o < sbytes; o += 256 * 8)
-            *(uint2 *)(q4_lds + bbytes + o) = *(const uint2 *)(gs + o);
-        if (tid < 2) *(uint4 *)(q4_lds + zslot + 16 * tid) = make_uint4(0, 0, 0, 0);
-        if (tid == 2) q4_lds[zslot + 32] = 127;
+    // staged operand offsets within the wave's region (slice j of the step)
+    constexpr uint32_t OPB = NCOL > 0 ? Q4_U * 4 * NCOL * 32 : 0;
+    constexpr uint32_t ZS = OPB + 256;
+    const uint32_t slot0 = (uint32_t)(g * ncol + col);
+    const uint32_t bo0 = bcol ? slot0 * 32 : ZS, bstep = bcol ? 4 * ncol * 32 : 0;
+    const uint32_t so0 = bcol ? OPB + slot0 : ZS + 32, sstep = bcol ? 4 * ncol : 0;
+    if (NCOL > 0) {
+        if (lane < 2) *(uint4 *)(wl + ZS + 16 * lane) = make_uint4(0, 0, 0, 0);
+        if (lane == 2) wl[ZS + 32] = 127;
     }
 
-    // Sign loads are unconditional (indices clamped into the layer) so that
-    // the compiler's wait counts stay exact: each slice's MFMAs start as soon
-    // as its own load lands.
-    const size_t rgc = live ? rg : n_rg - 1;
-    const size_t slast = s1 > s0 ? s1 - 1 : (s0 < a.ns ? s0 : a.ns - 1);
-    const uint4 *wp = (const uint4 *)L.bits + (rgc * a.ns) * 64 + lane;
-    uint4 w4[Q4_U];
-    auto load_signs = [&](size_t sb) {
-#pragma unroll
-        for (int u = 0; u < Q4_U; u++) {
-            const size_t sl = sb + u < slast ? sb + u : slast;
-            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64));
-            w4[u] = make_uint4(q[0], q[1], q[2], q[3]);
-        }
-    };
-    load_signs(s0);
     // stage 2: this lane's row of the group, for the epilogue
     float so = 0.0f, bi = 0.0f;
     if (STAGE == 2) {
@@ -930,56 +918,56 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
         so = ((gf32_t *)L.s_out)[rc];
         bi = ((gf32_t *)L.bias)[rc];
     }
-    if (BLDS) __syncthreads();
 
+    const uint4 *wp = (const uint4 *)L.bits + (rgc * a.ns) * 64 + lane;
     f32x4_t acc[4];
 #pragma unroll
     for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
-    auto step = [&](const uint4 &w4u, size_t s) {
-        if (BLDS) {
-            q4_slice_lds(acc, w4u, q4_lds, bo0 + (uint32_t)s * bstep, so0 + (uint32_t)s * sstep, m8, c2);
-            return;
-        }
-        i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
-        int bs = 127;
-        if (bcol) {
-            const size_t slot = (s * 4 + g) * a.ncol + col;
-            const uint4 *bq = (const uint4 *)(gb + slot * 32);
-            const uint4 b0 = bq[0], b1 = bq[1];
-            bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
-                         (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-            bs = gs[slot];
-        }
-        const uint32_t wr[4] = {w4u.x, w4u.y, w4u.z, w4u.w};
+    for (size_t sb = s0; sb < s1; sb += Q4_U) {
+        const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
+        uint4 stg[NCOL > 0 ? NCOL : 1];
+        uint32_t stgs = 0;
+        if (NCOL > 0) {
+            // operand of slices sb..sb+nsl-1: NCOL uint4 + one dword of scales per lane
+            const uint32_t ob = nsl * 4 * NCOL * 32, os = nsl * 4 * NCOL;
+            const uint8_t *gbs = gb + sb * 4 * NCOL * 32, *gss = gs + sb * 4 * NCOL;
 #pragma unroll
-        for (int rt = 0; rt < 4; rt++)
-            acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], m8, c2), bv,
-                                                                      acc[rt], 4, 0, 0, 127, 0, bs);
-    };
-    auto batch = [&](size_t sb) {
-        if (sb + Q4_U <= s1) {
+            for (int q = 0; q < (NCOL > 0 ? NCOL : 1); q++) {
+                uint32_t o = (lane + 64 * q) * 16;
+                o = o < ob ? o : ob - 16;
+                stg[q] = *(const uint4 *)(gbs + o);
+            }
+            uint32_t o = lane * 4;
+            o = o < os ? o : os - 4;
+            stgs = *(const uint32_t *)(gss + o);
+        }
+        uint4 w4[Q4_U];
 #pragma unroll
-            for (int u = 0; u < Q4_U; u++) step(w4[u], sb + u);
+        for (int u = 0; u < Q4_U; u++) {
+            const size_t sl = sb + (u < (int)nsl ? u : nsl - 1);
+            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64));
+            w4[u] = make_uint4(q[0], q[1], q[2], q[3]);
+        }
+        if (NCOL > 0) {
+#pragma unroll
+            for (int q = 0; q < (NCOL > 0 ? NCOL : 1); q++) *(uint4 *)(wl + (lane + 64 * q) * 16) = stg[q];
+            *(uint32_t *)(wl + OPB + lane * 4) = stgs;  // lanes past the scales fill the padding
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (nsl == Q4_U) {
+#pragma unroll
+            for (int u = 0; u < Q4_U; u++)
+                q4_step<NCOL>(acc, w4[u], u, wl, bo0, bstep, so0, sstep, gb, gs, sb, g, ncol, col, bcol, c7);
         } else {
 #pragma unroll
             for (int u = 0; u < Q4_U; u++)
-                if (sb + u < s1) step(w4[u], sb + u);
+                if (u < (int)nsl)
+                    q4_step<NCOL>(acc, w4[u], u, wl, bo0, bstep, so0, sstep, gb, gs, sb, g, ncol, col, bcol, c7);
         }
-    };
-    if (live) {
-        // The first batch's loads were issued before the barrier; later
-        // batches load at the top of their step, so that within a batch the
-        // waits stay per slice.
-        batch(s0);
-        for (size_t sb = s0 + Q4_U; sb < s1; sb += Q4_U) {
-            load_signs(sb);
-            batch(sb);
-        }
+        if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
     }
     if (KSPLIT > 1) {
-        // the operand region is reused for the cross-wave sums
-        f32x4_t *red = (f32x4_t *)q4_lds;  // [4 waves][4 tiles][64 lanes]
-        if (BLDS) __syncthreads();
+        f32x4_t *red = (f32x4_t *)(q4_lds + 4 * wreg);  // [4 waves][4 tiles][64 lanes]
 #pragma unroll
         for (int rt = 0; rt < 4; rt++) red[(wave * 4 + rt) * 64 + lane] = acc[rt];
         __syncthreads();
@@ -992,167 +980,12 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
         }
     }
     if (!live) return;
-    if (STAGE == 1)
-        q4_emit_t(acc, a, li, rg, lane);
-    else
-        q4_emit_y(acc, a, li, rg, lane, so, bi);
+    q4_epilogue<STAGE>(acc, (float *)wl, a, ncol, li, rg, lane, so, bi);
 }
 
-// Persistent decode GEMV for many layers at batch 1-2 (NCOL = 2 * batch
-// fp8 columns).  A task is one 64-row group of one layer; a unit is Q4_U
-// slices of a task.  Each wave walks its tasks unit by unit with the next
-// unit's loads in flight while it computes the current one: two register
-// sets of signs (Q4_U KiB each), and the fp8 operand of the unit staged
-// through registers into a wave-private double buffer in LDS (no barriers).
-// Tasks are split into 8 contiguous ranges, one per XCD (workgroup i runs
-// on XCD i mod 8), so that one layer's operand is fetched into one L2.
-//
-// Issue order inside a unit -- operand staging loads, then signs, then (stage
-// 2) the scale/bias of the row -- keeps every wait exact: the operand is
-// written to LDS with the signs still in flight, and the epilogue's stores
-// come after that write.
-template <int STAGE, int NCOL, int U>
-__global__ void __launch_bounds__(256) q4_stream_kernel(Q4Args a, uint32_t n_tasks) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
-    static_assert(U * 4 * NCOL <= 256, "scale staging is one dword per lane");
-    constexpr uint32_t OPB = U * 4 * NCOL * 32;  // operand bytes of a unit
-    constexpr uint32_t NSTG = OPB / 1024;        // operand uint4 per lane
-    constexpr uint32_t SCB = U * 4 * NCOL;       // scale bytes of a unit
-    constexpr uint32_t BUF = OPB + 256;          // + one staged dword per lane
-    constexpr uint32_t REGION = 2 * BUF + 48;    // two buffers + zero slot
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    uint8_t *rl = q4_lds + wave * REGION;
-    const uint32_t zs = 2 * BUF;
-    if (lane < 2) *(uint4 *)(rl + zs + 16 * lane) = make_uint4(0, 0, 0, 0);
-    if (lane == 2) rl[zs + 32] = 127;
-
-    const uint32_t nx = 8, xcd = blockIdx.x % nx, wgx = blockIdx.x / nx;
-    const uint32_t n_wg_x = (gridDim.x - xcd + nx - 1) / nx;
-    const uint32_t t0 = (uint32_t)((uint64_t)n_tasks * xcd / nx);
-    const uint32_t t1 = (uint32_t)((uint64_t)n_tasks * (xcd + 1) / nx);
-    const uint32_t wv = wgx * 4 + wave, nw = n_wg_x * 4;
-    if (t0 + wv >= t1) return;
-    const uint32_t ntask = (t1 - t0 - wv + nw - 1) / nw;
-    const uint32_t ns = (uint32_t)a.ns, cpt = (ns + U - 1) / U;
-    const uint32_t n_units = ntask * cpt;
-    const uint32_t n_rg = (uint32_t)(a.rows_p / 64);
-    const int col = lane & 15, g = lane >> 4;
-    const bool bcol = col < NCOL;
-    const uint32_t m8 = a.m8;
-    uint32_t c2;
-    asm volatile("v_mov_b32 %0, %1" : "=v"(c2) : "s"(a.c2));
-    // per-lane LDS offsets of slice j within a buffer
-    const uint32_t slot0 = g * NCOL + col;
-    const uint32_t bo0 = bcol ? slot0 * 32 : zs, bstep = bcol ? 4 * NCOL * 32 : 0;
-    const uint32_t so0 = bcol ? OPB + slot0 : zs + 32, sstep = bcol ? 4 * NCOL : 0;
-
-    uint4 wA[U], wB[U], stg[NSTG];
-    uint32_t stgs = 0;
-    float soA = 0.0f, biA = 0.0f, soB = 0.0f, biB = 0.0f;
-    f32x4_t acc[4];
-
-    auto where = [&](uint32_t u, uint32_t &li, uint32_t &rg, uint32_t &c) {
-        const uint32_t k = u / cpt;
-        c = u - k * cpt;
-        const uint32_t t = t0 + wv + k * nw;
-        li = t / n_rg;
-        rg = t - li * n_rg;
-    };
-    auto issue = [&](uint32_t u, uint4 (&w)[U], float &so_, float &bi_) {
-        uint32_t li, rg, c;
-        where(u, li, rg, c);
-        const uint32_t nsl = ns - U * c < U ? ns - U * c : U;
-        // operand staging: NSTG uint4 + one dword of scales per lane
-        const uint8_t *gb = a.bop + ((size_t)li * ns + U * c) * 4 * NCOL * 32;
-        const uint8_t *gs = a.bsc + ((size_t)li * ns + U * c) * 4 * NCOL;
-        const uint32_t ob_valid = nsl * 4 * NCOL * 32, os_valid = nsl * 4 * NCOL;
-#pragma unroll
-        for (int q = 0; q < (int)NSTG; q++) {
-            uint32_t o = (lane + 64 * q) * 16;
-            o = o < ob_valid ? o : ob_valid - 16;
-            stg[q] = *(const uint4 *)(gb + o);
-        }
-        {
-            uint32_t o = lane * 4;
-            o = o < os_valid ? o : os_valid - 4;
-            stgs = *(const uint32_t *)(gs + o);
-        }
-        const cq4layer_t *lp = (const cq4layer_t *)a.layers + li;
-        const Q4Layer L = {lp->bits, lp->s_in, lp->s_out, lp->bias};
-        const uint4 *wp = (const uint4 *)L.bits + ((size_t)rg * ns + U * c) * 64 + lane;
-#pragma unroll
-        for (int j = 0; j < U; j++) {
-            const uint32_t jj = j < (int)nsl ? j : nsl - 1;
-            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + jj * 64));
-            w[j] = make_uint4(q[0], q[1], q[2], q[3]);
-        }
-        if (STAGE == 2) {
-            const size_t row = (size_t)rg * 64 + lane;
-            const size_t rc = row < a.rows_valid ? row : a.rows_valid - 1;
-            so_ = ((gf32_t *)L.s_out)[rc];
-            bi_ = ((gf32_t *)L.bias)[rc];
-        }
-    };
-    auto stage_write = [&](uint32_t buf) {
-#pragma unroll
-        for (int q = 0; q < (int)NSTG; q++) *(uint4 *)(rl + buf + (lane + 64 * q) * 16) = stg[q];
-        *(uint32_t *)(rl + buf + OPB + lane * 4) = stgs;  // lanes past SCB fill the padding
-    };
-    auto mfmas = [&](uint32_t u, const uint4 (&w)[U], uint32_t buf) {
-        uint32_t li, rg, c;
-        where(u, li, rg, c);
-        const uint32_t nsl = ns - U * c < U ? ns - U * c : U;
-        const uint32_t bo = bcol ? buf + bo0 : bo0, so = bcol ? buf + so0 : so0;
-        if (nsl == U) {
-#pragma unroll
-            for (int j = 0; j < U; j++) q4_slice_lds(acc, w[j], rl, bo + j * bstep, so + j * sstep, m8, c2);
-        } else {
-#pragma unroll
-            for (int j = 0; j < U; j++)
-                if (j < (int)nsl) q4_slice_lds(acc, w[j], rl, bo + j * bstep, so + j * sstep, m8, c2);
-        }
-    };
-    auto tail = [&](uint32_t u, float so_, float bi_) {
-        uint32_t li, rg, c;
-        where(u, li, rg, c);
-        if (c != cpt - 1) return;
-        if (STAGE == 1)
-            q4_emit_t(acc, a, li, rg, lane);
-        else
-            q4_emit_y(acc, a, li, rg, lane, so_, bi_);
-#pragma unroll
-        for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
-    };
-
-#pragma unroll
-    for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
-    issue(0, wA, soA, biA);
-    stage_write(0);
-    for (uint32_t u = 0;;) {
-        if (u + 1 < n_units) {
-            issue(u + 1, wB, soB, biB);
-            mfmas(u, wA, 0);
-            stage_write(BUF);
-            tail(u, soA, biA);
-            u++;
-        } else {
-            mfmas(u, wA, 0);
-            tail(u, soA, biA);
-            break;
-        }
-        if (u + 1 < n_units) {
-            issue(u + 1, wA, soA, biA);
-            mfmas(u, wB, BUF);
-            stage_write(0);
-            tail(u, soB, biB);
-            u++;
-        } else {
-            mfmas(u, wB, BUF);
-            tail(u, soB, biB);
-            break;
-        }
-    }
+// LDS bytes of a q4_gemv_kernel workgroup.
+static size_t q4_gemv_lds(int ncol_t, int ksplit) {
+    return 4 * (size_t)q4_wave_lds(ncol_t) + (ksplit > 1 ? 4 * 4 * 64 * 16 : 0);
 }
 
 // ------------------------------------------------------------------------
@@ -1250,8 +1083,6 @@ static int run_gemv(const qbk_factor *L, const void *x, bool xf32, void *y, bool
     return launch_gemv_stage(2, false, L, L->gemv_tab + 1, 1, ws, 0, y, 0, ybf16, s);
 }
 
-static long long g_stream_min_tasks = -1;  // qbk_tune(QBK_TUNE_STREAM_MIN_TASKS)
-
 // Workspace of the fp4 decode for n_layers layers of L's shape at `batch`:
 // [bop1 | bsc1 | bop2 | bsc2] (the fp8 operands and E8M0 scales of the two
 // stages), each region 256-byte aligned.
@@ -1283,46 +1114,16 @@ static size_t q4_ws(const qbk_factor *L, size_t n_layers, size_t batch) {
     return q4_plan(L, n_layers, batch).bytes;
 }
 
-// Waves that share a 64-row group split its slices: about 8 slices a wave
-// (two load steps), more splits while the launch is too small to fill the
-// chip (a single layer).
+// Waves that share a 64-row group split its slices only while the launch is
+// too small to fill the chip (a single layer): a whole group per wave needs
+// no cross-wave reduction or barrier.
 static int q4_ksplit(size_t ns, size_t n_rg_total, int num_cus) {
-    int k = ns >= 32 ? 4 : (ns >= 16 ? 2 : 1);
+    int k = 1;
     while (k < 4 && ns >= (size_t)(2 * k) && n_rg_total * k < (size_t)num_cus * 8) k *= 2;
     return k;
 }
 
 // Workgroups per CU of the stream kernel at this LDS size (cached per variant).
-// Resident workgroups per CU of a stream-kernel variant (its LDS is fixed;
-// computed once per process).
-template <int STAGE, int NCOL, int U>
-static int q4_stream_occupancy(size_t lds) {
-    static int cached = 0;
-    if (!cached) {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q4_stream_kernel<STAGE, NCOL, U>, 256, lds) !=
-                hipSuccess || n < 1)
-            n = 1;
-        cached = n;
-    }
-    return cached;
-}
-
-template <int STAGE, int NCOL>
-static void q4_launch_stream(const Q4Args &a, uint32_t n_tasks, int num_cus, hipStream_t s) {
-    constexpr int U = Q4_SU;
-    constexpr size_t BUF = U * 4 * NCOL * 32 + 256;
-    const size_t lds = 4 * (2 * BUF + 48);
-    const int per_cu = q4_stream_occupancy<STAGE, NCOL, U>(lds);
-    size_t grid = (size_t)num_cus * per_cu;
-    // at least one task per wave, but never fewer than 8 workgroups: task
-    // range x belongs to the workgroups with blockIdx % 8 == x
-    const size_t need = round_up(div_ceil(n_tasks, 4), 8);
-    if (grid > need) grid = need;
-    hipLaunchKernelGGL((q4_stream_kernel<STAGE, NCOL, U>), dim3((unsigned)grid), dim3(256), lds, s, a,
-                       n_tasks);
-}
-
 // phase 1: x -> stage 1's fp8 operand; 2: stage-1 MFMA GEMV, whose epilogue
 // writes t = bf16(Vb^T z) as stage 2's fp8 operand; 3: stage-2 MFMA GEMV -> y.
 // x: [n][batch][din] (bf16, or f32 when xf32), y: [n][batch][dout].
@@ -1332,8 +1133,7 @@ static int q4_phase(int phase, const qbk_factor *L, const Q4Layer *tab, size_t n
     Q4Plan p = q4_plan(L, n_layers, batch);
     char *w = (char *)ws;
     Q4Args a{};
-    a.m8 = 0x88888888u;
-    a.c2 = 0x22222222u;
+    a.c7 = 0x77777777u;
     a.batch = (int)batch;
     a.ncol = (int)p.ncol;
     a.y_bf16 = ybf16;
@@ -1376,32 +1176,18 @@ static int q4_phase(int phase, const qbk_factor *L, const Q4Layer *tab, size_t n
         return QBK_OK;
     }
     const size_t n_rg = a.rows_p / 64;
-    const size_t n_tasks = n_layers * n_rg;
-    // the persistent kernel once a stage has enough 64-row tasks to keep
-    // every resident wave busy (or from the tuned threshold)
-    const long long min_tasks = g_stream_min_tasks >= 0 ? g_stream_min_tasks : (long long)L->num_cus * 8;
-    if (batch <= 2 && (long long)n_tasks >= min_tasks && n_tasks < (1ull << 31)) {
-        if (phase == 2 && batch == 1) q4_launch_stream<1, 2>(a, (uint32_t)n_tasks, L->num_cus, s);
-        else if (phase == 2) q4_launch_stream<1, 4>(a, (uint32_t)n_tasks, L->num_cus, s);
-        else if (batch == 1) q4_launch_stream<2, 2>(a, (uint32_t)n_tasks, L->num_cus, s);
-        else q4_launch_stream<2, 4>(a, (uint32_t)n_tasks, L->num_cus, s);
-        QBK_HIP(hipGetLastError());
-        return QBK_OK;
-    }
-    const int ksplit = q4_ksplit(a.ns, n_tasks, L->num_cus);
+    const int ksplit = q4_ksplit(a.ns, n_layers * n_rg, L->num_cus);
     const size_t rg_per_wg = 4 / ksplit;
     dim3 g((unsigned)div_ceil(n_rg, rg_per_wg), (unsigned)n_layers);
-    // operand + scales of one layer in LDS when they fit Q4_LDS_MAX
-    const size_t opnd = round_up(a.ns * 4 * p.ncol * 33, 16) + 48;  // + zero slot
-    const bool blds = opnd <= Q4_LDS_MAX;
-    const size_t red = ksplit > 1 ? 4 * 4 * 64 * 16 : 0;
-    const size_t lds = blds ? (opnd > red ? opnd : red) : red;
-#define Q4_LAUNCH(ST, KS)                                                                      \
-    if (blds) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, true>), g, dim3(256), lds, s, a);     \
-    else hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, false>), g, dim3(256), lds, s, a);
-#define Q4_LAUNCH_KS(ST)                                                                       \
-    if (ksplit == 4) { Q4_LAUNCH(ST, 4) }                                                      \
-    else if (ksplit == 2) { Q4_LAUNCH(ST, 2) }                                                 \
+    const int ncol_t = batch <= 2 ? (int)p.ncol : 0;  // staged operand at batch 1-2
+    const size_t lds = q4_gemv_lds(ncol_t, ksplit);
+#define Q4_LAUNCH(ST, KS)                                                                        \
+    if (ncol_t == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 2>), g, dim3(256), lds, s, a);  \
+    else if (ncol_t == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 4>), g, dim3(256), lds, s, a); \
+    else hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0>), g, dim3(256), lds, s, a);
+#define Q4_LAUNCH_KS(ST)                                                                         \
+    if (ksplit == 4) { Q4_LAUNCH(ST, 4) }                                                        \
+    else if (ksplit == 2) { Q4_LAUNCH(ST, 2) }                                                   \
     else { Q4_LAUNCH(ST, 1) }
     if (phase == 2) {
         Q4_LAUNCH_KS(1)
@@ -1765,15 +1551,6 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, c
                         workspace_size, qbk_factor_set_workspace_size(S)));
     return q4_phase(stage, S->first, (const Q4Layer *)S->d1, S->n, 1, x, false, y, true, workspace,
                     (hipStream_t)stream);
-}
-
-long long qbk_tune(int knob, long long value) {
-    if (knob == QBK_TUNE_STREAM_MIN_TASKS) {
-        const long long prev = g_stream_min_tasks;
-        g_stream_min_tasks = value < 0 ? -1 : value;
-        return prev;
-    }
-    return -2;
 }
 
 int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *S, const uint16_t *x,

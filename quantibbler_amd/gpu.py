@@ -51,13 +51,6 @@ def gpu_available() -> bool:
     return bool(_lib.load().qbk_gpu_available())
 
 
-def tune_stream_min_tasks(value: int) -> int:
-    """Threshold (in 64-row tasks per stage) above which batch-1/2 decode
-    runs the persistent streaming GEMV; -1 restores the library default.
-    Returns the previous value.  Process-wide."""
-    return int(_lib.load().qbk_tune(1, int(value)))
-
-
 @dataclass(frozen=True)
 class AttentionShape:
     """gpu_attention.rs:402-411."""

@@ -186,22 +186,12 @@ def set_decode(S, x, dout):
     return yd.cpu().numpy().view(np.uint16)
 
 
-@pytest.fixture
-def stream_forced():
-    """Run the persistent streaming GEMV on every decode stage."""
-    from quantibbler_amd import tune_stream_min_tasks
-
-    prev = tune_stream_min_tasks(0)
-    yield
-    tune_stream_min_tasks(prev)
-
-
 @pytest.mark.parametrize("dout,din,r,n", [(512, 1024, 200, 5), (300, 640, 200, 7), (96, 128, 64, 3)])
 def test_set_decode_matches_single_layers(ctx, orc, dout, din, r, n):
     """Integer-exact set decode: bit-identical to the oracle and to the
-    single-layer path, on the default kernels and on the streaming kernel
-    (forced; partial units where din/128 or r_p/128 is not a multiple of 4)."""
-    from quantibbler_amd import FactorSet, tune_stream_min_tasks
+    single-layer path (steps of fewer than 8 slices where din/128 or r_p/128
+    is small)."""
+    from quantibbler_amd import FactorSet
 
     say("factor set decode", dout, din, r, n)
     rng = np.random.default_rng(77 + din)
@@ -210,38 +200,13 @@ def test_set_decode_matches_single_layers(ctx, orc, dout, din, r, n):
     S = FactorSet(ctx, layers)
     x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (n, din)).astype(np.float32))
     ys = set_decode(S, x, dout)
-    prev = tune_stream_min_tasks(0)
-    try:
-        ys_stream = set_decode(S, x, dout)
-    finally:
-        tune_stream_min_tasks(prev)
     for i, (L, layer) in enumerate(zip(Ls, layers)):
         want = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"],
                                            x[i:i + 1])
         wb = orc.f32_to_bf16_fast(want)[0]
         same(ys[i], wb, f"set decode, layer {i}")
-        same(ys_stream[i], wb, f"streaming set decode, layer {i}")
         yi, _ = run_dev(layer, x[i:i + 1], "bfloat16")
         same(ys[i], yi[0])
-
-
-@pytest.mark.parametrize("dout,din,r", [(256, 512, 128), (300, 200, 37), (1024, 4096, 1102)])
-@pytest.mark.parametrize("batch", [1, 2])
-def test_stream_kernel_single_layer(ctx, orc, stream_forced, dout, din, r, batch):
-    """The streaming GEMV (forced) on one layer at batch 1 and 2: integer-exact
-    bit identity with the oracle, and the stage bounds on config inputs."""
-    say("factor streaming kernel", dout, din, r, "batch", batch)
-    rng = np.random.default_rng(3 * dout + din + r + batch)
-    L = make_layer(orc, rng, dout, din, r, integer=True)
-    layer = upload(ctx, L)
-    x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (batch, din)).astype(np.float32))
-    want = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
-    got, ws = run_dev(layer, x)
-    same(got, want)
-    t = gpu_t(layer, ws, batch)
-    _, t_orc = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"],
-                                           L["bias"], x, want_t=True)
-    same(t, t_orc)
 
 
 def test_apply_host_faces(ctx, orc):
