@@ -46,6 +46,24 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_decode_config1_512layers.md")
+
+
+def measured_traffic(stage):
+    """HBM bytes per launch of a decode GEMV stage from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy
+    kernel of known traffic), or None when the summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic-per-launch:"):
+                    kv = dict(t.split("=") for t in line.split(":", 1)[1].split())
+                    return int(kv[f"stage{stage}"])
+    except (OSError, ValueError, KeyError):
+        pass
+    return None
+
+
 def make_layers(qa, ctx, np, count, seed):
     rng = np.random.default_rng(seed)
     layers, host = [], []
@@ -277,7 +295,8 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": None,
+            "frac": round(achieved / (HBM_PEAK / 1e9), 4), "traffic": measured_traffic(dom),
+            "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
             "kernel": f"q4_gemv_kernel<{dom},*,2> (decode stage {dom}, fp4 x fp8 scaled MFMA)",
             "bytes_per_launch": bytes_launch, "avg_launch_ms": round(dom_ms, 4),
         },

@@ -133,10 +133,11 @@ int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *layer, const uint16_t 
 int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *layer, int serving, const float *x,
                      size_t batch, float *y);
 
-/* A set of layers of one shape decoded together, one launch per stage for
- * the whole set (independent projections such as q/k/v, or every layer of
- * a bandwidth sweep).  The set keeps device descriptor tables; the layers
- * must outlive it and share (dout, din, r). */
+/* A set of layers of one shape decoded together, three launches for the
+ * whole set (independent projections such as q/k/v, or every layer of a
+ * bandwidth sweep).  The set keeps device descriptor tables; the layers
+ * must outlive it and share (dout, din, r).  No counterpart in the
+ * reference (its engine applies one layer per call). */
 typedef struct qbk_factor_set qbk_factor_set;
 int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t n_layers,
                           qbk_factor_set **out);

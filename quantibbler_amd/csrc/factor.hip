@@ -28,16 +28,9 @@
 #include "qbk_internal.h"
 
 namespace qbk {
-// Per-layer operands of one GEMV stage: an entry of a device-side table
-// indexed by blockIdx.y, so one launch covers any number of layers.
-struct GemvLayer {
-    const uint32_t *bits;   // [rows_p][words]
-    const float *s_in;      // stage 1: s2 [K]
-    const float *s_out;     // stage 2: s1 [rows]
-    const float *bias;      // stage 2: bias [rows]
-};
-
-// The same for the fp4-MFMA decode (bits in the fp4 decode layout).
+// Per-layer operands of one decode GEMV stage (bits in the fp4 decode
+// layout): an entry of a device-side table, so one launch covers any number
+// of layers of one shape.
 struct Q4Layer {
     const uint32_t *bits;
     const float *s_in;
@@ -51,14 +44,11 @@ struct qbk_factor {
     int device, num_cus;
     size_t dout, din, r;
     size_t din_p, r_p, dout_p;  // padded for the MFMA tiles (64 / 128 / 128)
-    size_t din_w, r_w;          // gemv row words: ceil(din/256)*8, ceil(r/256)*8
     uint8_t *ub_rows, *vbt_rows;      // reference per-row bitplanes
-    uint32_t *vt_gemv, *u_gemv;       // [r_p][din_w], [dout_p][r_w]
     uint32_t *vt_frag, *u_frag;       // [r_p/64][din_p/32][64], [dout_p/64][r_p/32][64]
     size_t din_q, r_q;                // K of the fp4 decode layout: multiples of 128
     uint32_t *vt_q4, *u_q4;           // [r_p/64][din_q/128][64][4], [dout_p/64][r_q/128][64][4]
     float *s1, *s2, *bias;            // dout, din, dout (zeros when absent)
-    qbk::GemvLayer *gemv_tab;  // device: [0] stage 1, [1] stage 2
     void *q4_tab;              // device Q4Layer[2]: [0] stage 1, [1] stage 2
     std::vector<void *> allocs;
 };
@@ -71,20 +61,6 @@ namespace qbk {
 
 static inline int rbit(const uint8_t *rows, size_t row_words, size_t i, size_t k) {
     return (rows[i * row_words + (k >> 3)] >> (k & 7)) & 1;
-}
-
-// gemv word: column c of a 32-column group sits at bit (c/2) + 16*(c%2), so
-// the pair (2m, 2m+1) occupies bits m and m+16.
-static void repack_gemv(const uint8_t *rows, size_t n_rows, size_t n_bits, size_t rows_p,
-                        size_t words, uint32_t *out) {
-    size_t rw = div_ceil(n_bits, 8);
-    memset(out, 0, rows_p * words * 4);
-    for (size_t i = 0; i < n_rows; i++)
-        for (size_t k = 0; k < n_bits; k++)
-            if (rbit(rows, rw, i, k)) {
-                size_t c = k & 31;
-                out[i * words + (k >> 5)] |= 1u << ((c >> 1) + 16 * (c & 1));
-            }
 }
 
 // mfma fragment word for (group g, slice s, lane l): rows 64g + 16*rt + l%16
@@ -197,11 +173,6 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
     L->din_p = round_up(din, 64);
     L->r_p = round_up(r, 128);
     L->dout_p = round_up(dout, 128);
-    L->din_w = div_ceil(din, 256) * 8;
-    L->r_w = div_ceil(r, 256) * 8;
-    std::vector<uint32_t> vg(L->r_p * L->din_w), ug(L->dout_p * L->r_w);
-    repack_gemv(vbt_rows, r, din, L->r_p, L->din_w, vg.data());
-    repack_gemv(ub_rows, dout, r, L->dout_p, L->r_w, ug.data());
     std::vector<uint32_t> vf(L->r_p / 64 * L->din_p / 32 * 64), uf(L->dout_p / 64 * L->r_p / 32 * 64);
     repack_frag(vbt_rows, r, din, L->r_p, L->din_p, vf.data());
     repack_frag(ub_rows, dout, r, L->dout_p, L->r_p, uf.data());
@@ -220,8 +191,6 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
     L->field = (decltype(L->field))p;
     UP(ub_rows, ub_rows, dout * div_ceil(r, 8));
     UP(vbt_rows, vbt_rows, r * div_ceil(din, 8));
-    UP(vt_gemv, vg.data(), vg.size() * 4);
-    UP(u_gemv, ug.data(), ug.size() * 4);
     UP(vt_frag, vf.data(), vf.size() * 4);
     UP(u_frag, uf.data(), uf.size() * 4);
     UP(vt_q4, vq.data(), vq.size() * 4);
@@ -229,124 +198,11 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
     UP(s1, s1, dout * 4);
     UP(s2, s2, din * 4);
     UP(bias, bias ? bias : zb.data(), dout * 4);
-    GemvLayer tab[2] = {{L->vt_gemv, L->s2, nullptr, nullptr}, {L->u_gemv, nullptr, L->s1, L->bias}};
-    UP(gemv_tab, tab, sizeof tab);
     Q4Layer qtab[2] = {{L->vt_q4, L->s2, nullptr, nullptr}, {L->u_q4, nullptr, L->s1, L->bias}};
     UP(q4_tab, qtab, sizeof qtab);
 #undef UP
     *out = L;
     return QBK_OK;
-}
-
-// ------------------------------------------------------------------------
-// decode GEMV (batch 1)
-// ------------------------------------------------------------------------
-//
-// out_row = sum_j s(row, j) a_j over a K-wide row of pair-permuted words.
-// A wave takes GEMV_R rows at a time; lane l reads word l, l+64, ... of each
-// row (coalesced), fetches the matching 16 bf16 pairs of `a` from LDS once
-// and applies them to all GEMV_R rows: per pair one shift + one v_bfi build
-// the +-1 bf16 pair and one v_dot2_f32_bf16 accumulates.  Rows are then
-// reduced across the wave with a fixed xor-butterfly (deterministic).
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-#define GEMV_WAVES 4
-#define GEMV_R 4
-
-__device__ __forceinline__ float dot_word(uint32_t w, const uint32_t *zp, float acc) {
-    uint32_t nw = ~w;  // bit set = -1
-#pragma unroll
-    for (int m = 0; m < 16; m++) {
-        uint32_t t = nw << (15 - m);
-        uint32_t sg = (t & 0x80008000u) | 0x3F803F80u;
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, zp[m]),
-                                              __builtin_bit_cast(bf16x2_t, sg), acc, false);
-    }
-    return acc;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-struct GemvArgs {
-    const GemvLayer *layers;
-    size_t rows_p, words, rows_valid, k_valid;
-    const void *act;        // stage 1: x (bf16 or f32) [K]; stage 2: t (bf16) [K]
-    size_t act_stride;      // elements between consecutive layers' act
-    void *out;              // stage 1: t (bf16) [rows_p]; stage 2: y [rows]
-    size_t out_stride;
-    int y_bf16;
-};
-
-// STAGE 1: act = bf16(s2*x) (XF32 selects an f32 x), out = bf16 t (zero for
-// padded rows).  STAGE 2: act = t, out = y = f32(bf16(u))*s1 + b.
-template <int STAGE, bool XF32>
-__global__ void __launch_bounds__(GEMV_WAVES * 64) gemv_kernel(GemvArgs a) {
-    extern __shared__ uint32_t zs[];  // bf16 pairs, words*16 entries
-    const GemvLayer L = a.layers[blockIdx.y];
-    const size_t words = a.words;
-    const size_t li = blockIdx.y;
-    // stage the activation pairs in LDS
-    for (size_t p = threadIdx.x; p < words * 16; p += blockDim.x) {
-        uint32_t pair = 0;
-        for (int h = 0; h < 2; h++) {
-            size_t j = 2 * p + h;
-            uint16_t zb = 0;
-            if (j < a.k_valid) {
-                if (STAGE == 1) {
-                    float xv = XF32 ? ((const float *)a.act)[li * a.act_stride + j]
-                                    : bf16_to_f32(((const uint16_t *)a.act)[li * a.act_stride + j]);
-                    zb = f32_to_bf16(L.s_in[j] * xv);
-                } else {
-                    zb = ((const uint16_t *)a.act)[li * a.act_stride + j];
-                }
-            }
-            pair |= (uint32_t)zb << (16 * h);
-        }
-        zs[p] = pair;
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    size_t row0 = ((size_t)blockIdx.x * GEMV_WAVES + wave) * GEMV_R;
-    if (row0 >= a.rows_p) return;
-    float acc[GEMV_R];
-#pragma unroll
-    for (int r = 0; r < GEMV_R; r++) acc[r] = 0.0f;
-    const uint32_t *base = L.bits + row0 * words;
-    for (size_t wi = lane; wi < words; wi += 64) {
-        uint32_t wv[GEMV_R];
-#pragma unroll
-        for (int r = 0; r < GEMV_R; r++) wv[r] = base[r * words + wi];
-        uint32_t zp[16];
-#pragma unroll
-        for (int m = 0; m < 16; m++) zp[m] = zs[wi * 16 + m];
-#pragma unroll
-        for (int r = 0; r < GEMV_R; r++) acc[r] = dot_word(wv[r], zp, acc[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < GEMV_R; r++) acc[r] = wave_sum(acc[r]);
-    if (lane < GEMV_R) {
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < GEMV_R; r++)
-            if (lane == r) v = acc[r];
-        size_t row = row0 + lane;
-        if (STAGE == 1) {
-            ((uint16_t *)a.out)[li * a.out_stride + row] =
-                row < a.rows_valid ? f32_to_bf16(v) : (uint16_t)0;
-        } else if (row < a.rows_valid) {
-            float u = bf16_to_f32(f32_to_bf16(v));
-            float y = u * L.s_out[row] + L.bias[row];
-            if (a.y_bf16)
-                ((uint16_t *)a.out)[li * a.out_stride + row] = f32_to_bf16(y);
-            else
-                ((float *)a.out)[li * a.out_stride + row] = y;
-        }
-    }
 }
 
 // ------------------------------------------------------------------------
@@ -621,6 +477,7 @@ struct Q4Args {
     uint32_t c7;                              // 0x77777777 (fp4 sign build)
     uint8_t *tb_op, *tb_sc;                   // stage 1: stage 2's operand and scales
     size_t tb_ns;                             // stage 2's slices per layer
+    uint32_t wg_per_layer, n_layers;          // GEMV grid: workgroups per layer, layers
 };
 
 __device__ __forceinline__ int e8m0_of(float amax) {
@@ -632,89 +489,109 @@ __device__ __forceinline__ int e8m0_of(float amax) {
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
-// Eight threads per (layer, token, slice, scale group g), four activations
-// each.  The E8M0 scale given by lane group g covers the activations
-// k = 128s + kq4(g, e) (measured on gfx950): two runs of 16, at k offsets
-// 16(g>>1) + 64(g&1) and that + 32, whose fp8 bytes sit in B lane groups
-// 2(g&1) and 2(g&1)+1 at byte offset 16(g>>1).  Thread j < 4 takes 4j..4j+3
-// of the first run, j >= 4 the second.
-template <int STAGE, bool XF32>
-__global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a, size_t n_items) {
-    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t it = tid >> 3;
-    const int j = (int)(tid & 7);
-    const bool live = it < n_items;  // dead threads still join the shuffles
+// x -> stage 1's fp8 operand.  One thread per run of 16 activations:
+// (layer, token, slice s, run r) covers k = 128s + 16r .. +15.  The E8M0
+// scale given by MFMA lane group G covers the activations k = 128s +
+// kq4(G, e) (measured on gfx950): the two runs 16(G>>1) + 64(G&1) + {0, 32},
+// i.e. runs r and r^2 with G = 2(r&1) + (r>>2), so the block max is one
+// shuffle away.  Run r's bytes go to B lane group 2(r>>2) + ((r>>1)&1) at
+// byte offset 16(r&1): one uint4 for hi (column 2b), one for lo (2b + 1).
+// z = bf16(s2 * x) splits exactly into hi + lo: each fp8 e4m3 part keeps 4
+// significant bits relative to the block max's exponent.
+template <bool XF32>
+__global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a, size_t n_runs) {
+    const size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = it < n_runs;  // dead threads still join the shuffle
     const size_t itc = live ? it : 0;
-    const int g = itc & 3;
-    size_t rest = itc >> 2;
+    const int r = (int)(itc & 7);
+    size_t rest = itc >> 3;
     const size_t s = rest % a.ns;
     rest /= a.ns;
     const int b = (int)(rest % a.batch);
     const size_t li = rest / a.batch;
-    const size_t k0 = 128 * s + 16 * (g >> 1) + 64 * (g & 1) + 4 * (j & 3) + 32 * (j >> 2);
-    float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const size_t k0 = 128 * s + 16 * r;
+    float z[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) z[e] = 0.0f;
     if (live) {
         const size_t off = li * a.act_layer + (size_t)b * a.act_ld;
         const uint16_t *src = (const uint16_t *)a.act + off;
         const float *srcf = (const float *)a.act + off;
-        if (a.vec_ok && k0 + 3 < a.k_valid) {
-            float v[4];
+        const float *s2 = ((const cq4layer_t *)a.layers + li)->s_in;
+        if (a.vec_ok && k0 + 15 < a.k_valid) {
+            float v[16];
             if (XF32) {
-                float4 q = *(const float4 *)(srcf + k0);
-                v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 f = *(const float4 *)(srcf + k0 + 4 * q);
+                    v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+                }
             } else {
-                uint2 q = *(const uint2 *)(src + k0);
-                v[0] = bf16_to_f32(q.x & 0xffff); v[1] = bf16_to_f32(q.x >> 16);
-                v[2] = bf16_to_f32(q.y & 0xffff); v[3] = bf16_to_f32(q.y >> 16);
-            }
-            if (STAGE == 1) {
-                float4 sv = *(const float4 *)(a.layers[li].s_in + k0);
-                v[0] = bf16_to_f32(f32_to_bf16(sv.x * v[0]));
-                v[1] = bf16_to_f32(f32_to_bf16(sv.y * v[1]));
-                v[2] = bf16_to_f32(f32_to_bf16(sv.z * v[2]));
-                v[3] = bf16_to_f32(f32_to_bf16(sv.w * v[3]));
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const uint4 u = *(const uint4 *)(src + k0 + 8 * q);
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int h = 0; h < 4; h++) {
+                        v[8 * q + 2 * h] = bf16_to_f32(w[h] & 0xffff);
+                        v[8 * q + 2 * h + 1] = bf16_to_f32(w[h] >> 16);
+                    }
+                }
             }
 #pragma unroll
-            for (int e = 0; e < 4; e++) z[e] = v[e];
+            for (int q = 0; q < 4; q++) {
+                const float4 f = *(const float4 *)(s2 + k0 + 4 * q);
+                z[4 * q] = bf16_to_f32(f32_to_bf16(f.x * v[4 * q]));
+                z[4 * q + 1] = bf16_to_f32(f32_to_bf16(f.y * v[4 * q + 1]));
+                z[4 * q + 2] = bf16_to_f32(f32_to_bf16(f.z * v[4 * q + 2]));
+                z[4 * q + 3] = bf16_to_f32(f32_to_bf16(f.w * v[4 * q + 3]));
+            }
         } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
+            for (int e = 0; e < 16; e++) {
                 const size_t k = k0 + e;
                 if (k >= a.k_valid) continue;
-                float v = XF32 ? srcf[k] : bf16_to_f32(src[k]);
-                z[e] = STAGE == 1 ? bf16_to_f32(f32_to_bf16(a.layers[li].s_in[k] * v)) : v;
+                const float v = XF32 ? srcf[k] : bf16_to_f32(src[k]);
+                z[e] = bf16_to_f32(f32_to_bf16(s2[k] * v));
             }
         }
     }
-    float amax = fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(z[e]));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
     const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
     const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
-    int hw = __builtin_amdgcn_cvt_pk_fp8_f32(z[0] * inv_hi, z[1] * inv_hi, 0, false);
-    hw = __builtin_amdgcn_cvt_pk_fp8_f32(z[2] * inv_hi, z[3] * inv_hi, hw, true);
-    // exact residual: each bf16 value keeps at most 4 significant bits for lo
-    z[0] -= __builtin_amdgcn_cvt_f32_fp8(hw, 0) * sc_hi;
-    z[1] -= __builtin_amdgcn_cvt_f32_fp8(hw, 1) * sc_hi;
-    z[2] -= __builtin_amdgcn_cvt_f32_fp8(hw, 2) * sc_hi;
-    z[3] -= __builtin_amdgcn_cvt_f32_fp8(hw, 3) * sc_hi;
-    float rmax = fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3])));
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 64));
+    uint32_t hw[4], lw[4];
+    float rmax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
+        hw[q] = (uint32_t)w;
+        z[4 * q] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
+        z[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
+        z[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
+        z[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+#pragma unroll
+        for (int u = 0; u < 4; u++) rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
+    }
     rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 4, 64));
     const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
     const float inv_lo = pow2f(-e_lo);
-    int lw = __builtin_amdgcn_cvt_pk_fp8_f32(z[0] * inv_lo, z[1] * inv_lo, 0, false);
-    lw = __builtin_amdgcn_cvt_pk_fp8_f32(z[2] * inv_lo, z[3] * inv_lo, lw, true);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
+        lw[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
+    }
     if (!live) return;
-    const size_t gb = 2 * (g & 1) + (j >> 2);
+    const size_t gb = 2 * (r >> 2) + ((r >> 1) & 1);
     const size_t slot = ((li * a.ns + s) * 4 + gb) * a.ncol + 2 * b;  // hi column; lo is slot + 1
-    const size_t byte = 16 * (g >> 1) + 4 * (j & 3);
-    *(uint32_t *)(a.bop + slot * 32 + byte) = (uint32_t)hw;
-    *(uint32_t *)(a.bop + (slot + 1) * 32 + byte) = (uint32_t)lw;
-    if (j == 0) {
-        const size_t sc = ((li * a.ns + s) * 4 + g) * a.ncol + 2 * b;
+    const size_t byte = 16 * (r & 1);
+    *(uint4 *)(a.bop + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(a.bop + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if ((r & 2) == 0) {
+        const size_t sc = ((li * a.ns + s) * 4 + 2 * (r & 1) + (r >> 2)) * a.ncol + 2 * b;
         a.bsc[sc] = (uint8_t)(e_hi + 127);
         a.bsc[sc + 1] = (uint8_t)(e_lo + 127);
     }
@@ -878,11 +755,17 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const int ncol = NCOL > 0 ? NCOL : a.ncol;
-    const size_t li = blockIdx.y;
+    // XCD-aware 1D grid: workgroup i runs on XCD i % 8; XCD x takes the
+    // contiguous workgroup range [x*per_x, (x+1)*per_x) of the (layer, row
+    // group) order, so that one layer's operand is fetched into one L2.
+    const uint32_t xcd = blockIdx.x & 7, per_x = gridDim.x >> 3;
+    const size_t wgi = (size_t)xcd * per_x + (blockIdx.x >> 3);
+    if (wgi >= (size_t)a.wg_per_layer * a.n_layers) return;  // padding workgroup
+    const size_t li = wgi / a.wg_per_layer;
     const cq4layer_t *lp = (const cq4layer_t *)a.layers + li;
     const Q4Layer L = {lp->bits, lp->s_in, lp->s_out, lp->bias};
     constexpr int RG_PER_WG = 4 / KSPLIT;
-    const size_t rg = (size_t)blockIdx.x * RG_PER_WG + wave / KSPLIT;
+    const size_t rg = (wgi - li * a.wg_per_layer) * RG_PER_WG + wave / KSPLIT;
     const int ks = wave % KSPLIT;
     const size_t n_rg = a.rows_p / 64;
     const size_t per = (a.ns + KSPLIT - 1) / KSPLIT;
@@ -1040,48 +923,6 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float *__restr
     *(uint4 *)(t + e0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// One GEMV stage over n_layers layers of one shape (table entries
-// tab[0..n_layers)); act/out advance by their strides per layer.
-static int launch_gemv_stage(int stage, bool xf32, const qbk_factor *L, const GemvLayer *tab,
-                             size_t n_layers, const void *act, size_t act_stride, void *out,
-                             size_t out_stride, bool ybf16, hipStream_t s) {
-    GemvArgs a{};
-    a.layers = tab;
-    a.act = act;
-    a.act_stride = act_stride;
-    a.out = out;
-    a.out_stride = out_stride;
-    a.y_bf16 = ybf16;
-    if (stage == 1) {
-        a.rows_p = L->r_p;
-        a.words = L->din_w;
-        a.rows_valid = L->r;
-        a.k_valid = L->din;
-    } else {
-        a.rows_p = L->dout_p;
-        a.words = L->r_w;
-        a.rows_valid = L->dout;
-        a.k_valid = L->r;
-    }
-    const size_t rows_per_block = GEMV_WAVES * GEMV_R;
-    dim3 g((unsigned)div_ceil(a.rows_p, rows_per_block), (unsigned)n_layers), blk(GEMV_WAVES * 64);
-    size_t lds = a.words * 16 * 4;
-    if (stage == 1 && xf32)
-        hipLaunchKernelGGL((gemv_kernel<1, true>), g, blk, lds, s, a);
-    else if (stage == 1)
-        hipLaunchKernelGGL((gemv_kernel<1, false>), g, blk, lds, s, a);
-    else
-        hipLaunchKernelGGL((gemv_kernel<2, false>), g, blk, lds, s, a);
-    QBK_HIP(hipGetLastError());
-    return QBK_OK;
-}
-
-static int run_gemv(const qbk_factor *L, const void *x, bool xf32, void *y, bool ybf16,
-                    void *ws, hipStream_t s) {
-    int rc = launch_gemv_stage(1, xf32, L, L->gemv_tab, 1, x, 0, ws, 0, false, s);
-    if (rc) return rc;
-    return launch_gemv_stage(2, false, L, L->gemv_tab + 1, 1, ws, 0, y, 0, ybf16, s);
-}
 
 // Workspace of the fp4 decode for n_layers layers of L's shape at `batch`:
 // [bop1 | bsc1 | bop2 | bsc2] (the fp8 operands and E8M0 scales of the two
@@ -1114,11 +955,12 @@ static size_t q4_ws(const qbk_factor *L, size_t n_layers, size_t batch) {
     return q4_plan(L, n_layers, batch).bytes;
 }
 
-// Waves that share a 64-row group split its slices only while the launch is
-// too small to fill the chip (a single layer): a whole group per wave needs
-// no cross-wave reduction or barrier.
+// Waves that share a 64-row group split its slices: one load step (Q4_U
+// slices) per wave where the group has more, and further while the launch is
+// too small to fill the chip (a single layer).
 static int q4_ksplit(size_t ns, size_t n_rg_total, int num_cus) {
     int k = 1;
+    while (k < 4 && ns > (size_t)(Q4_U * k)) k *= 2;
     while (k < 4 && ns >= (size_t)(2 * k) && n_rg_total * k < (size_t)num_cus * 8) k *= 2;
     return k;
 }
@@ -1164,21 +1006,23 @@ static int q4_phase(int phase, const qbk_factor *L, const Q4Layer *tab, size_t n
         a.out_layer = batch * L->dout;
     }
     if (phase == 1) {
-        const size_t elem = xf32 ? 4 : 2;
-        a.vec_ok = a.act_ld % 4 == 0 && (uintptr_t)a.act % (4 * elem) == 0;
-        size_t items = n_layers * batch * a.ns * 4;
-        dim3 g((unsigned)div_ceil(items * 8, 256));
+        // 16-element vector loads need 16-aligned rows (32 or 64 bytes)
+        a.vec_ok = a.act_ld % 16 == 0 && (uintptr_t)a.act % 16 == 0;
+        const size_t runs = n_layers * batch * a.ns * 8;
+        dim3 g((unsigned)div_ceil(runs, 256));
         if (xf32)
-            hipLaunchKernelGGL((q4_prep_kernel<1, true>), g, dim3(256), 0, s, a, items);
+            hipLaunchKernelGGL((q4_prep_kernel<true>), g, dim3(256), 0, s, a, runs);
         else
-            hipLaunchKernelGGL((q4_prep_kernel<1, false>), g, dim3(256), 0, s, a, items);
+            hipLaunchKernelGGL((q4_prep_kernel<false>), g, dim3(256), 0, s, a, runs);
         QBK_HIP(hipGetLastError());
         return QBK_OK;
     }
     const size_t n_rg = a.rows_p / 64;
     const int ksplit = q4_ksplit(a.ns, n_layers * n_rg, L->num_cus);
     const size_t rg_per_wg = 4 / ksplit;
-    dim3 g((unsigned)div_ceil(n_rg, rg_per_wg), (unsigned)n_layers);
+    a.wg_per_layer = (uint32_t)div_ceil(n_rg, rg_per_wg);
+    a.n_layers = (uint32_t)n_layers;
+    dim3 g((unsigned)round_up((size_t)a.wg_per_layer * n_layers, 8));  // a multiple of the 8 XCDs
     const int ncol_t = batch <= 2 ? (int)p.ncol : 0;  // staged operand at batch 1-2
     const size_t lds = q4_gemv_lds(ncol_t, ksplit);
 #define Q4_LAUNCH(ST, KS)                                                                        \
