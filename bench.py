@@ -194,6 +194,99 @@ def bench_sage(qa, ctx, torch, np, iters=10):
             "shape": "B=1 H=32 S=4096 d=128 causal, bf16 in/out, includes the quantisation pre-pass"}
 
 
+# the seven projections of a Llama-3-8B-shaped
+# decoder layer, ranks from the reference's planning rule at 0.55 bits/weight
+# (v2 stream, fp16 scales): (name, dout, din, r).
+CFG3 = [("q", 4096, 4096, 1102), ("k", 1024, 4096, 431), ("v", 1024, 4096, 431),
+        ("o", 4096, 4096, 1102), ("gate", 14336, 4096, 1724), ("up", 14336, 4096, 1724),
+        ("down", 4096, 14336, 1733)]
+
+
+def random_rows(np, rng, n_rows, n_bits):
+    """Random +-1 rows, packed LSB-first with zero pad bits."""
+    b = rng.integers(0, 256, (n_rows, (n_bits + 7) // 8), dtype=np.uint8)
+    if n_bits % 8:
+        b[:, -1] &= (1 << (n_bits % 8)) - 1
+    return b
+
+
+def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=20, prefill_b=2048):
+    """Decode (batch 1) of every projection of n_layers distinct decoder
+    layers -- 480 MB of signs, beyond the 256 MB MALL -- as one FactorSet
+    over all of them (three launches per token); then the prefill GEMM of
+    one layer's projections at B = prefill_b."""
+    rng = np.random.default_rng(33)
+    groups, ordered = {}, []
+    sign_bytes = act_bytes = 0
+    for li in range(n_layers):
+        for name, m, n, r in CFG3:
+            L = qa.FactorLayer.from_rows(ctx, m, n, r, random_rows(np, rng, m, r), random_rows(np, rng, r, n),
+                                         np.exp(0.5 * rng.standard_normal(m)).astype(np.float32),
+                                         np.exp(0.5 * rng.standard_normal(n)).astype(np.float32), None)
+            groups.setdefault((m, n, r), []).append(L)
+            ordered.append(L)
+            sign_bytes += (m * r + 7) // 8 + (n * r + 7) // 8
+            act_bytes += 2 * n + 2 * m + 4 * m + 4 * n  # x, y (bf16), s1, s2 (f32)
+        if (li + 1) % 8 == 0:
+            log(f"  cfg3: uploaded {li + 1}/{n_layers} decoder layers")
+    st = torch.cuda.current_stream()
+    # one set over every projection of every layer, in decoder-layer order
+    # (q, k, v, o, gate, up, down of layer 0, then layer 1, ...): three
+    # launches per token
+    all_layers = ordered
+    S = qa.FactorSet(ctx, all_layers)
+    n_in = sum(L.din for L in all_layers)
+    n_out = sum(L.dout for L in all_layers)
+    x = torch.randn(n_in, device="cuda").to(torch.bfloat16)
+    y = torch.empty(n_out, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(S.workspace_size(), dtype=torch.uint8, device="cuda")
+    def token():
+        S.decode_dev(x, y, ws, ws.numel(), st)
+    for _ in range(3):
+        token()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(steps):
+        token()
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    total = sign_bytes + act_bytes
+    out = {"decoder_layers": n_layers, "sign_bytes": sign_bytes, "bytes_per_token": total,
+           "ms_per_token": round(ms, 4), "GB/s": round(total / (ms * 1e-3) / 1e9, 1),
+           "frac_hbm_peak": round(total / (ms * 1e-3) / HBM_PEAK, 4),
+           "note": "f32 s1/s2 as stored here; the reference v2 stream (fp16 scales) counts 14,995,624 B per layer"}
+    log(f"  cfg3 decode: {ms:.3f} ms/token over {n_layers} layers, {out['GB/s']} GB/s")
+    # prefill: one decoder layer's seven projections at B = prefill_b
+    flop = 0
+    calls = []
+    for name, m, n, r in CFG3:
+        L = groups[(m, n, r)][0]
+        xb = torch.randn((prefill_b, n), device="cuda").to(torch.bfloat16)
+        yb = torch.empty((prefill_b, m), dtype=torch.bfloat16, device="cuda")
+        wn = L.workspace_size(prefill_b)
+        wsb = torch.empty(wn, dtype=torch.uint8, device="cuda")
+        calls.append((L, xb, yb, wsb, wn))
+        flop += 2.0 * prefill_b * r * (m + n)
+    def layer():
+        for L, xb, yb, wsb, wn in calls:
+            L.linear_dev(xb, prefill_b, yb, "bfloat16", wsb, wn, st)
+    layer()
+    torch.cuda.synchronize()
+    a.record(st)
+    for _ in range(5):
+        layer()
+    b.record(st)
+    torch.cuda.synchronize()
+    pms = a.elapsed_time(b) / 5
+    tf = flop / (pms * 1e-3) / 1e12
+    out["prefill"] = {"B": prefill_b, "ms_per_layer": round(pms, 3), "gflop": round(flop / 1e9, 1),
+                      "tflops": round(tf, 1), "frac_bf16_peak": round(tf * 1e12 / BF16_PEAK, 4)}
+    log(f"  cfg3 prefill B={prefill_b}: {pms:.3f} ms/layer, {tf:.1f} TFLOP/s")
+    return out
+
+
 def bench_cpu(np, host, budget_s=10.0):
     from oracle import oracle as orc
 
@@ -271,6 +364,8 @@ def main():
         extra["prefill_gemm"] = bench_gemm(torch, np, layers[0])
         log("sage attention ...")
         extra["sage_blk"] = bench_sage(qa, ctx, torch, np)
+        log("config 3 (8B decoder layer projections) ...")
+        extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")
     cpu = bench_cpu(np, host, args.cpu_seconds)
     line = {

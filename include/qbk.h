@@ -133,18 +133,19 @@ int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *layer, const uint16_t 
 int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *layer, int serving, const float *x,
                      size_t batch, float *y);
 
-/* A set of layers of one shape decoded together, three launches for the
- * whole set (independent projections such as q/k/v, or every layer of a
- * bandwidth sweep).  The set keeps device descriptor tables; the layers
- * must outlive it and share (dout, din, r).  No counterpart in the
- * reference (its engine applies one layer per call). */
+/* A set of layers (any shapes) decoded together at batch 1, three launches
+ * for the whole set: independent projections such as q/k/v/o/gate/up/down
+ * of one or many decoder layers.  The set keeps a device descriptor table;
+ * the layers must outlive it.  No counterpart in the reference (its engine
+ * applies one layer per call). */
 typedef struct qbk_factor_set qbk_factor_set;
 int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t n_layers,
                           qbk_factor_set **out);
 void qbk_factor_set_destroy(qbk_factor_set *set);
 size_t qbk_factor_set_workspace_size(const qbk_factor_set *set);
-/* y_i = layer_i(x_i) at batch 1 for every layer i of the set:
- * x bf16 [n_layers][din], y bf16 [n_layers][dout] (device pointers). */
+/* y_i = layer_i(x_i) at batch 1 for every layer i of the set (device
+ * pointers): x bf16 is the concatenation of the x_i (layer i's din values
+ * start after the din of layers 0..i-1), y bf16 likewise of the y_i. */
 int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *set, const uint16_t *x,
                               uint16_t *y, void *workspace, size_t workspace_size, void *stream);
 /* One of the three launches of qbk_factor_set_decode_dev (for callers that

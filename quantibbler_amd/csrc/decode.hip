@@ -1,0 +1,774 @@
+// decode.hip -- the factor linear's decode GEMV (batch 1..8) on gfx950.
+//
+//   t = bf16(Vb^T z), z = bf16(s2 * x);  y = bf16(Ub t) * s1 + bias
+//                                        (engine/mod.rs:449-460, apply_bf16)
+//
+// out[i] = sum_k s(i,k) a_k runs on v_mfma_scale_f32_16x16x128_f8f6f4:
+// A = the +-1 signs as fp4 e2m1, built in registers from the packed words;
+// B = the activations split into two fp8 e4m3 columns, a = hi*2^e_hi +
+// lo*2^e_lo, one E8M0 scale per 32-element block and column (a bf16 value
+// has 8 significant bits: hi keeps the top 4, lo the rest).  Token b of a
+// decode batch uses columns 2b, 2b+1.  Each 128-k slice of a 16-row tile is
+// one MFMA over 256 bytes of packed signs.
+//
+// A launch covers any set of layers (any shapes): each stage reads a device
+// table of Q4Layer entries (factor_internal.h) and finds its layer from the
+// workgroup index.  Three launches per decode:
+//   1. q4_prep_kernel: x -> stage 1's fp8 operand;
+//   2. q4_gemv_kernel<1>: t = bf16(Vb^T z), written by the epilogue straight
+//      into stage 2's fp8 operand;
+//   3. q4_gemv_kernel<2>: y = bf16(Ub t) * s1 + bias.
+#include <string.h>
+
+#include <vector>
+
+#include "factor_internal.h"
+
+namespace qbk {
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Pointers read from a layer table are generic to the compiler; loading
+// through an address_space(1) pointer keeps them global loads (flat loads
+// count against both vmcnt and lgkmcnt and defeat per-load waits).
+typedef __attribute__((address_space(1))) const u32x4_t gu32x4_t;
+typedef __attribute__((address_space(1))) const float gf32_t;
+// The layer tables are never written by a kernel: reading them through the
+// constant address space lets the compiler use scalar loads even after the
+// kernel's own stores (a vector load of a pointer would wait on vmcnt).
+typedef __attribute__((address_space(4))) const Q4Layer cq4layer_t;
+
+#define Q4_U 8       // slices whose sign loads a wave issues together
+#define Q4_PHASES 3  // prep x, stage 1 (+ stage 2's operand), stage 2
+
+// One launch over a set of layers.
+struct Q4Args {
+    const Q4Layer *layers;       // this stage's table entries
+    const uint32_t *wg_layer;    // GEMV: layer of each workgroup (null for one layer)
+    uint32_t n_layers, n_wg;     // layers; workgroups doing work (GEMV)
+    int batch, ncol;             // ncol = 2 * batch
+    const void *act;             // stage 1 prep: x (bf16, or f32)
+    void *out;                   // stage 2: y (bf16 or f32)
+    uint8_t *op, *sc;            // this stage's fp8 operand [slice][4][ncol][32] and scales [slice][4][ncol]
+    uint8_t *tb_op, *tb_sc;      // stage 1: stage 2's operand and scales
+    int y_bf16, vec_ok;          // vec_ok: x rows allow 16-element vector loads
+    uint32_t c7;                 // 0x77777777 (fp4 sign build)
+};
+
+// The table entry of layer li (scalar loads).
+__device__ __forceinline__ Q4Layer q4_entry(const Q4Args &a, uint32_t li) {
+    const cq4layer_t *lp = (const cq4layer_t *)a.layers + li;
+    Q4Layer L;
+    L.bits = lp->bits;
+    L.s_in = lp->s_in;
+    L.s_out = lp->s_out;
+    L.bias = lp->bias;
+    L.rows_p = lp->rows_p;
+    L.rows_valid = lp->rows_valid;
+    L.ns = lp->ns;
+    L.k_valid = lp->k_valid;
+    L.slice0 = lp->slice0;
+    L.tb_ns = lp->tb_ns;
+    L.tb_slice0 = lp->tb_slice0;
+    L.wg0 = lp->wg0;
+    L.act0 = lp->act0;
+    L.out0 = lp->out0;
+    return L;
+}
+
+// The layer of workgroup wgi: one scalar load from the per-workgroup table
+// (so that a workgroup's sign loads wait on two dependent scalar loads, not
+// on a search).
+__device__ __forceinline__ uint32_t q4_layer_of(const Q4Args &a, uint32_t wgi) {
+    if (a.n_layers == 1) return 0;
+    return ((__attribute__((address_space(4))) const uint32_t *)a.wg_layer)[wgi];
+}
+
+__device__ __forceinline__ int e8m0_of(float amax) {
+    // exponent so that amax * 2^-e lies in [128, 256): e = floor(log2 amax) - 7
+    int ex = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
+    int e = ex - 7;
+    return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+__device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+// x -> stage 1's fp8 operand.  Workgroup (x, layer); one thread per run of
+// 16 activations: (token b, slice s, run r) covers k = 128s + 16r .. +15.
+// The E8M0 scale given by MFMA lane group G covers the activations k =
+// 128s + kq4(G, e) (measured on gfx950): the two runs 16(G>>1) + 64(G&1) +
+// {0, 32}, i.e. runs r and r^2 with G = 2(r&1) + (r>>2), so the block max is
+// one shuffle away.  Run r's bytes go to B lane group 2(r>>2) + ((r>>1)&1)
+// at byte offset 16(r&1): one uint4 for hi (column 2b), one for lo (2b + 1).
+// z = bf16(s2 * x) splits exactly into hi + lo: each fp8 e4m3 part keeps 4
+// significant bits relative to the block max's exponent.
+template <bool XF32>
+__global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a) {
+    const uint32_t li = blockIdx.y;
+    const Q4Layer L = q4_entry(a, li);
+    const size_t n_runs = (size_t)a.batch * L.ns * 8;
+    const size_t it = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = it < n_runs;  // dead threads still join the shuffle
+    const size_t itc = live ? it : 0;
+    const int r = (int)(itc & 7);
+    const size_t s = (itc >> 3) % L.ns;
+    const int b = (int)((itc >> 3) / L.ns);
+    const size_t k0 = 128 * s + 16 * r;
+    float z[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) z[e] = 0.0f;
+    if (live) {
+        const size_t off = L.act0 + (size_t)b * L.k_valid;
+        const uint16_t *src = (const uint16_t *)a.act + off;
+        const float *srcf = (const float *)a.act + off;
+        const float *s2 = L.s_in;
+        if (a.vec_ok && k0 + 15 < L.k_valid) {
+            float v[16];
+            if (XF32) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 f = *(const float4 *)(srcf + k0 + 4 * q);
+                    v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const uint4 u = *(const uint4 *)(src + k0 + 8 * q);
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int h = 0; h < 4; h++) {
+                        v[8 * q + 2 * h] = bf16_to_f32(w[h] & 0xffff);
+                        v[8 * q + 2 * h + 1] = bf16_to_f32(w[h] >> 16);
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 f = *(const float4 *)(s2 + k0 + 4 * q);
+                z[4 * q] = bf16_to_f32(f32_to_bf16(f.x * v[4 * q]));
+                z[4 * q + 1] = bf16_to_f32(f32_to_bf16(f.y * v[4 * q + 1]));
+                z[4 * q + 2] = bf16_to_f32(f32_to_bf16(f.z * v[4 * q + 2]));
+                z[4 * q + 3] = bf16_to_f32(f32_to_bf16(f.w * v[4 * q + 3]));
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const size_t k = k0 + e;
+                if (k >= L.k_valid) continue;
+                const float v = XF32 ? srcf[k] : bf16_to_f32(src[k]);
+                z[e] = bf16_to_f32(f32_to_bf16(s2[k] * v));
+            }
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(z[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+    const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+    uint32_t hw[4], lw[4];
+    float rmax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
+        hw[q] = (uint32_t)w;
+        z[4 * q] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
+        z[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
+        z[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
+        z[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+#pragma unroll
+        for (int u = 0; u < 4; u++) rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
+    }
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
+    const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+    const float inv_lo = pow2f(-e_lo);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
+        lw[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
+    }
+    if (!live) return;
+    const size_t gb = 2 * (r >> 2) + ((r >> 1) & 1);
+    const size_t slot = ((L.slice0 + s) * 4 + gb) * a.ncol + 2 * b;  // hi column; lo is slot + 1
+    const size_t byte = 16 * (r & 1);
+    *(uint4 *)(a.op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(a.op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if ((r & 2) == 0) {
+        const size_t sc = ((L.slice0 + s) * 4 + 2 * (r & 1) + (r >> 2)) * a.ncol + 2 * b;
+        a.sc[sc] = (uint8_t)(e_hi + 127);
+        a.sc[sc + 1] = (uint8_t)(e_lo + 127);
+    }
+}
+
+// Signs of one 16-row tile as fp4 e2m1: nibble e of VGPR j carries bit
+// 4e + 3 - j of the word in its sign bit, and OR-ing 0x7 into every nibble
+// forces the other three bits to 1 whatever the shift brought in, so each
+// element is exactly +-6 (e2m1 0111 = 1.5 * 2^2).  One VALU op per VGPR
+// (v_lshl_or_b32 with c7 = 0x77777777 in an SGPR; v_or_b32 for j = 3).  The
+// MFMA's A scale 2^-2 (E8M0 125) makes the elements +-1.5, and the epilogue
+// divides by 1.5: exact whenever the f32 sum is (1.5 * sum then needs one
+// more significant bit).
+#define Q4_SCALE_A 125
+__device__ __forceinline__ i32x8_t q4_signs(uint32_t w, uint32_t c7) {
+    i32x8_t av;
+    av[0] = (int)((w << 3) | c7);
+    av[1] = (int)((w << 2) | c7);
+    av[2] = (int)((w << 1) | c7);
+    av[3] = (int)(w | c7);
+    av[4] = av[5] = av[6] = av[7] = 0;
+    return av;
+}
+
+// One 128-k slice of a 64-row group: the four row tiles' MFMAs against the
+// fp8 operand held in LDS at byte offset bo (scale byte at so).
+__device__ __forceinline__ void q4_slice_lds(f32x4_t acc[4], const uint4 &w4, const uint8_t *lds,
+                                             uint32_t bo, uint32_t so, uint32_t c7) {
+    const uint4 *bq = (const uint4 *)(lds + bo);
+    const uint4 b0 = bq[0], b1 = bq[1];
+    const i32x8_t bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+                        (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    const int bs = lds[so];
+    const uint32_t wr[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++)
+        acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], c7), bv, acc[rt],
+                                                                  4, 0, 0, Q4_SCALE_A, 0, bs);
+}
+
+// Slice j of a step: the fp8 operand from the wave's staged LDS region
+// (NCOL > 0) or from global memory (NCOL == 0; gb/gs point at the step's
+// first slice), then the four MFMAs.
+template <int NCOL>
+__device__ __forceinline__ void q4_step(f32x4_t acc[4], const uint4 &w4u, uint32_t j, const uint8_t *wl,
+                                        uint32_t bo0, uint32_t bstep, uint32_t so0, uint32_t sstep,
+                                        const uint8_t *gb, const uint8_t *gs, int g, int ncol, int col,
+                                        bool bcol, uint32_t c7) {
+    if (NCOL > 0) {
+        q4_slice_lds(acc, w4u, wl, bo0 + j * bstep, so0 + j * sstep, c7);
+        return;
+    }
+    i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
+    int bs = 127;
+    if (bcol) {
+        const size_t slot = ((size_t)j * 4 + g) * ncol + col;
+        const uint4 *bq = (const uint4 *)(gb + slot * 32);
+        const uint4 b0 = bq[0], b1 = bq[1];
+        bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+        bs = gs[slot];
+    }
+    const uint32_t wr[4] = {w4u.x, w4u.y, w4u.z, w4u.w};
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++)
+        acc[rt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4_signs(wr[rt], c7), bv, acc[rt], 4, 0, 0,
+                                                                  Q4_SCALE_A, 0, bs);
+}
+
+// Epilogue of one 64-row group, one row per lane: the accumulators are
+// transposed through the wave's LDS region T [ncol][64] (lane (col, g) holds
+// rows 16rt + 4g + i of column col), then lane l finishes row rg*64 + l of
+// every token: v = (hi + lo) / 1.5 (the A scale of q4_signs).
+//
+// Stage 1 writes t = bf16(v) (0 past rows_valid) as stage 2's fp8 operand:
+// row l of the group is element e = (l & 15) + 16 (l >> 5) of scale group
+// G = 2((l >> 4) & 1) + (rg & 1) of stage-2 slice rg/2 (the 32 rows sharing
+// G differ in lane bits 0-3 and 5, so the block max is five xor shuffles);
+// its bytes go to B lane group 2(rg & 1) + (l >> 5), byte 16((l >> 4) & 1) +
+// (l & 15), hi to column 2b and lo to 2b + 1.
+//
+// Stage 2 writes y = bf16(v) * s1 + bias (so / bi: this lane's row).
+template <int STAGE>
+__device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, const Q4Args &a,
+                                            const Q4Layer &L, int ncol, size_t rg, int lane, float so,
+                                            float bi) {
+    const int col = lane & 15, g = lane >> 4;
+    if (col < ncol) {
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) *(f32x4_t *)(T + col * 64 + 16 * rt + 4 * g) = acc[rt];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const size_t row = rg * 64 + lane;
+    const bool valid = row < L.rows_valid;
+    for (int b = 0; b < (ncol >> 1); b++) {
+        const float v = (T[(2 * b) * 64 + lane] + T[(2 * b + 1) * 64 + lane]) / 1.5f;
+        const float t = valid ? bf16_to_f32(f32_to_bf16(v)) : 0.0f;
+        if (STAGE == 2) {
+            if (valid) {
+                const float y = t * so + bi;
+                const size_t o = L.out0 + (size_t)b * L.rows_valid + row;
+                if (a.y_bf16)
+                    ((uint16_t *)a.out)[o] = f32_to_bf16(y);
+                else
+                    ((float *)a.out)[o] = y;
+            }
+            continue;
+        }
+        float amax = fabsf(t);
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+        const int hw = __builtin_amdgcn_cvt_pk_fp8_f32(t * pow2f(-e_hi), 0.0f, 0, false);
+        const float r = t - __builtin_amdgcn_cvt_f32_fp8(hw, 0) * pow2f(e_hi);  // exact residual
+        float rmax = fabsf(r);
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 4, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 8, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+        const int lw = __builtin_amdgcn_cvt_pk_fp8_f32(r * pow2f(-e_lo), 0.0f, 0, false);
+        const int q = (lane >> 4) & 1, h = lane >> 5;
+        const size_t base = ((size_t)L.tb_slice0 + (rg >> 1)) * 4;
+        const size_t slot = (base + 2 * (rg & 1) + h) * ncol + 2 * b;  // hi column; lo = +1
+        const size_t byte = 16 * q + (lane & 15);
+        a.tb_op[slot * 32 + byte] = (uint8_t)hw;
+        a.tb_op[(slot + 1) * 32 + byte] = (uint8_t)lw;
+        if ((lane & 47) == 0) {  // lanes 0 and 16: scale groups 2q + (rg & 1)
+            const size_t sc = (base + 2 * q + (rg & 1)) * ncol + 2 * b;
+            a.tb_sc[sc] = (uint8_t)(e_hi + 127);
+            a.tb_sc[sc + 1] = (uint8_t)(e_lo + 127);
+        }
+    }
+}
+
+// LDS bytes of one wave's region: the staged operand of Q4_U slices (NCOL
+// columns), their scales (one dword per lane), a zero slot, and room for the
+// epilogue's transpose.
+__host__ __device__ constexpr uint32_t q4_wave_lds(int ncol) {
+    return ncol > 0 ? (uint32_t)(Q4_U * 4 * ncol * 32 + 256 + 48) : 16 * 64 * 4;
+}
+
+// Decode GEMV.  Workgroup = 4 waves; KSPLIT waves share a 64-row group and
+// split its slices (4/KSPLIT row groups per workgroup).  Lane l loads the 16
+// bytes of its four row tiles' sign words per slice (1 KiB per wave per
+// slice, contiguous over the slices); Q4_U slices are loaded per step.
+//
+// NCOL > 0 (batch 1-2): each wave stages the fp8 operand of its own slices
+// through registers into its LDS region -- operand loads issued first, sign
+// loads right behind them, no workgroup barrier -- and reads it per slice;
+// lanes past the batch's columns read a zero slot.  NCOL == 0 (batch 3-8):
+// lanes read the operand of each slice from global memory (L2).
+//
+// Loads are unconditional (indices clamped into the layer; the MFMAs of
+// clamped slices are skipped) so that the compiler's wait counts stay exact:
+// each slice's MFMAs start as soon as its own load lands.
+//
+// XCD-aware 1-D grid: workgroup i runs on XCD i % 8; XCD x takes the
+// contiguous range [x*per_x, (x+1)*per_x) of the (layer, row group) work, so
+// that one layer's operand is fetched into one L2.
+template <int STAGE, int KSPLIT, int NCOL>
+__global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
+    const int ncol = NCOL > 0 ? NCOL : a.ncol;
+    const uint32_t xcd = blockIdx.x & 7, per_x = gridDim.x >> 3;
+    const uint32_t wgi = xcd * per_x + (blockIdx.x >> 3);
+    if (wgi >= a.n_wg) return;  // padding workgroup (the whole group leaves)
+    const uint32_t li = q4_layer_of(a, wgi);
+    const Q4Layer L = q4_entry(a, li);
+    constexpr int RG_PER_WG = 4 / KSPLIT;
+    const size_t rg = (size_t)(wgi - L.wg0) * RG_PER_WG + wave / KSPLIT;
+    const int ks = wave % KSPLIT;
+    const size_t n_rg = L.rows_p / 64, ns = L.ns;
+    const size_t per = (ns + KSPLIT - 1) / KSPLIT;
+    const size_t s0 = ks * per < ns ? ks * per : ns;
+    const size_t s1 = s0 + per < ns ? s0 + per : ns;
+    const int col = lane & 15, g = lane >> 4;
+    const bool bcol = col < ncol;
+    const bool live = rg < n_rg;
+    const size_t rgc = live ? rg : n_rg - 1;
+    const uint32_t c7 = a.c7;
+    const uint32_t wreg = q4_wave_lds(NCOL);  // the launch allocates 4 * this (+ red)
+    uint8_t *wl = q4_lds + wave * wreg;
+    const uint8_t *gb = a.op + (size_t)L.slice0 * 4 * ncol * 32;  // this layer's operand
+    const uint8_t *gs = a.sc + (size_t)L.slice0 * 4 * ncol;
+
+    // staged operand offsets within the wave's region (slice j of the step)
+    constexpr uint32_t OPB = NCOL > 0 ? Q4_U * 4 * NCOL * 32 : 0;
+    constexpr uint32_t ZS = OPB + 256;
+    const uint32_t slot0 = (uint32_t)(g * ncol + col);
+    const uint32_t bo0 = bcol ? slot0 * 32 : ZS, bstep = bcol ? 4 * ncol * 32 : 0;
+    const uint32_t so0 = bcol ? OPB + slot0 : ZS + 32, sstep = bcol ? 4 * ncol : 0;
+    if (NCOL > 0) {
+        if (lane < 2) *(uint4 *)(wl + ZS + 16 * lane) = make_uint4(0, 0, 0, 0);
+        if (lane == 2) wl[ZS + 32] = 127;
+    }
+
+    // stage 2: this lane's row of the group, for the epilogue
+    float so = 0.0f, bi = 0.0f;
+    if (STAGE == 2) {
+        const size_t row = rgc * 64 + lane;
+        const size_t rc = row < L.rows_valid ? row : L.rows_valid - 1;
+        so = ((gf32_t *)L.s_out)[rc];
+        bi = ((gf32_t *)L.bias)[rc];
+    }
+
+    const uint4 *wp = (const uint4 *)L.bits + (rgc * ns) * 64 + lane;
+    f32x4_t acc[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
+    for (size_t sb = s0; sb < s1; sb += Q4_U) {
+        const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
+        uint4 stg[NCOL > 0 ? NCOL : 1];
+        uint32_t stgs = 0;
+        if (NCOL > 0) {
+            // operand of slices sb..sb+nsl-1: NCOL uint4 + one dword of scales per lane
+            const uint32_t ob = nsl * 4 * NCOL * 32, os = nsl * 4 * NCOL;
+            const uint8_t *gbs = gb + sb * 4 * NCOL * 32, *gss = gs + sb * 4 * NCOL;
+#pragma unroll
+            for (int q = 0; q < (NCOL > 0 ? NCOL : 1); q++) {
+                uint32_t o = (lane + 64 * q) * 16;
+                o = o < ob ? o : ob - 16;
+                stg[q] = *(const uint4 *)(gbs + o);
+            }
+            uint32_t o = lane * 4;
+            o = o < os ? o : os - 4;
+            stgs = *(const uint32_t *)(gss + o);
+        }
+        uint4 w4[Q4_U];
+#pragma unroll
+        for (int u = 0; u < Q4_U; u++) {
+            const size_t sl = sb + (u < (int)nsl ? u : nsl - 1);
+            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64));
+            w4[u] = make_uint4(q[0], q[1], q[2], q[3]);
+        }
+        if (NCOL > 0) {
+#pragma unroll
+            for (int q = 0; q < (NCOL > 0 ? NCOL : 1); q++) *(uint4 *)(wl + (lane + 64 * q) * 16) = stg[q];
+            *(uint32_t *)(wl + OPB + lane * 4) = stgs;  // lanes past the scales fill the padding
+            __builtin_amdgcn_wave_barrier();
+        }
+        const uint8_t *gbs = gb + sb * 4 * ncol * 32, *gss = gs + sb * 4 * ncol;
+        if (nsl == Q4_U) {
+#pragma unroll
+            for (int u = 0; u < Q4_U; u++)
+                q4_step<NCOL>(acc, w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
+        } else {
+#pragma unroll
+            for (int u = 0; u < Q4_U; u++)
+                if (u < (int)nsl)
+                    q4_step<NCOL>(acc, w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
+        }
+        if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
+    }
+    if (KSPLIT > 1) {
+        f32x4_t *red = (f32x4_t *)(q4_lds + 4 * wreg);  // [4 waves][4 tiles][64 lanes]
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) red[(wave * 4 + rt) * 64 + lane] = acc[rt];
+        __syncthreads();
+        if (ks != 0) return;
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) {
+            f32x4_t v = red[(wave * 4 + rt) * 64 + lane];
+            for (int q = 1; q < KSPLIT; q++) v += red[((wave + q) * 4 + rt) * 64 + lane];
+            acc[rt] = v;
+        }
+    }
+    if (!live) return;
+    q4_epilogue<STAGE>(acc, (float *)wl, a, L, ncol, rg, lane, so, bi);
+}
+
+// ------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------
+
+// LDS bytes of a q4_gemv_kernel workgroup.
+static size_t q4_gemv_lds(int ncol_t, int ksplit) {
+    return 4 * (size_t)q4_wave_lds(ncol_t) + (ksplit > 1 ? 4 * 4 * 64 * 16 : 0);
+}
+
+// Waves that share a 64-row group split its slices: one load step (Q4_U
+// slices) per wave where the group has more, and further while the launch
+// is too small to fill the chip (a single layer).
+static int q4_ksplit(size_t max_ns, size_t min_ns, size_t n_rg_total, int num_cus) {
+    int k = 1;
+    while (k < 4 && max_ns > (size_t)(Q4_U * k)) k *= 2;
+    while (k < 4 && min_ns >= (size_t)(2 * k) && n_rg_total * k < (size_t)num_cus * 8) k *= 2;
+    return k;
+}
+
+// Launch geometry of one set of layers (or one layer) at a batch.
+struct Q4Geom {
+    size_t n_layers, batch, ncol;
+    size_t ns1_tot, ns2_tot, max_ns1;
+    bool din_mult8;  // every layer's din % 8 == 0: x blocks and rows start 16-byte aligned
+    int ks1, ks2;
+    uint32_t n_wg1, n_wg2;
+    size_t o_op1, o_sc1, o_op2, o_sc2, bytes;  // workspace regions
+};
+
+// Fill stage-1 / stage-2 entries (tab[i], tab[n + i]) for layers[0..n) and
+// the launch geometry; x and y of layer i start at the running sums of
+// batch * din and batch * dout.
+static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, int num_cus,
+                     Q4Layer *tab, Q4Geom &G) {
+    G = Q4Geom{};
+    G.n_layers = n;
+    G.batch = batch;
+    G.ncol = 2 * batch;
+    size_t max1 = 0, min1 = SIZE_MAX, max2 = 0, min2 = SIZE_MAX, rg1 = 0, rg2 = 0;
+    for (size_t i = 0; i < n; i++) {
+        const qbk_factor *L = layers[i];
+        const size_t ns1 = L->din_q / 128, ns2 = L->r_q / 128;
+        max1 = ns1 > max1 ? ns1 : max1;
+        min1 = ns1 < min1 ? ns1 : min1;
+        max2 = ns2 > max2 ? ns2 : max2;
+        min2 = ns2 < min2 ? ns2 : min2;
+        rg1 += L->r_p / 64;
+        rg2 += L->dout_p / 64;
+    }
+    G.max_ns1 = max1;
+    G.din_mult8 = true;
+    for (size_t i = 0; i < n; i++) G.din_mult8 = G.din_mult8 && layers[i]->din % 8 == 0;
+    G.ks1 = q4_ksplit(max1, min1, rg1, num_cus);
+    G.ks2 = q4_ksplit(max2, min2, rg2, num_cus);
+    const size_t rpw1 = 4 / G.ks1, rpw2 = 4 / G.ks2;
+    size_t s1 = 0, s2 = 0, wg1 = 0, wg2 = 0, act = 0, out = 0;
+    for (size_t i = 0; i < n; i++) {
+        const qbk_factor *L = layers[i];
+        const size_t ns1 = L->din_q / 128, ns2 = L->r_q / 128;
+        Q4Layer &a = tab[i];
+        Q4Layer &b = tab[n + i];
+        a = Q4Layer{};
+        b = Q4Layer{};
+        a.bits = L->vt_q4;
+        a.s_in = L->s2;
+        a.rows_p = (uint32_t)L->r_p;
+        a.rows_valid = (uint32_t)L->r;
+        a.ns = (uint32_t)ns1;
+        a.k_valid = (uint32_t)L->din;
+        a.slice0 = (uint32_t)s1;
+        a.tb_ns = (uint32_t)ns2;
+        a.tb_slice0 = (uint32_t)s2;
+        a.wg0 = (uint32_t)wg1;
+        a.act0 = act;
+        b.bits = L->u_q4;
+        b.s_out = L->s1;
+        b.bias = L->bias;
+        b.rows_p = (uint32_t)L->dout_p;
+        b.rows_valid = (uint32_t)L->dout;
+        b.ns = (uint32_t)ns2;
+        b.k_valid = (uint32_t)L->r;
+        b.slice0 = (uint32_t)s2;
+        b.wg0 = (uint32_t)wg2;
+        b.out0 = out;
+        s1 += ns1;
+        s2 += ns2;
+        wg1 += div_ceil(L->r_p / 64, rpw1);
+        wg2 += div_ceil(L->dout_p / 64, rpw2);
+        act += batch * L->din;
+        out += batch * L->dout;
+    }
+    G.ns1_tot = s1;
+    G.ns2_tot = s2;
+    G.n_wg1 = (uint32_t)wg1;
+    G.n_wg2 = (uint32_t)wg2;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off += round_up(bytes, 256);
+        return o;
+    };
+    G.o_op1 = take(s1 * 4 * G.ncol * 32);
+    G.o_sc1 = take(s1 * 4 * G.ncol);
+    G.o_op2 = take(s2 * 4 * G.ncol * 32);
+    G.o_sc2 = take(s2 * 4 * G.ncol);
+    G.bytes = off;
+}
+
+// One phase of a decode over the table `tab` (device; stage-1 entries
+// [0, n), stage-2 entries [n, 2n)) and, for several layers, the per-
+// workgroup layer tables wg1 (stage 1) and wg2.  Phase 1: x -> stage 1's
+// operand; 2: stage 1 (writes stage 2's operand); 3: stage 2 -> y.
+static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32_t *wg1,
+                    const uint32_t *wg2, const void *x, bool xf32, void *y, bool ybf16, void *ws,
+                    hipStream_t s) {
+    char *w = (char *)ws;
+    Q4Args a{};
+    a.c7 = 0x77777777u;
+    a.batch = (int)G.batch;
+    a.ncol = (int)G.ncol;
+    a.n_layers = (uint32_t)G.n_layers;
+    a.y_bf16 = ybf16;
+    if (phase <= 2) {
+        a.layers = tab;
+        a.act = x;
+        a.op = (uint8_t *)(w + G.o_op1);
+        a.sc = (uint8_t *)(w + G.o_sc1);
+        a.tb_op = (uint8_t *)(w + G.o_op2);
+        a.tb_sc = (uint8_t *)(w + G.o_sc2);
+        a.n_wg = G.n_wg1;
+        a.wg_layer = wg1;
+    } else {
+        a.layers = tab + G.n_layers;
+        a.op = (uint8_t *)(w + G.o_op2);
+        a.sc = (uint8_t *)(w + G.o_sc2);
+        a.out = y;
+        a.n_wg = G.n_wg2;
+        a.wg_layer = wg2;
+    }
+    if (phase == 1) {
+        // 16-byte vector loads of x: every layer's x block and token row
+        // start 16-byte aligned when x is and every din is a multiple of 8
+        a.vec_ok = G.din_mult8 && (uintptr_t)x % 16 == 0;
+        const size_t runs = G.batch * G.max_ns1 * 8;
+        dim3 g((unsigned)div_ceil(runs, 256), (unsigned)G.n_layers);
+        if (xf32)
+            hipLaunchKernelGGL((q4_prep_kernel<true>), g, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((q4_prep_kernel<false>), g, dim3(256), 0, s, a);
+        QBK_HIP(hipGetLastError());
+        return QBK_OK;
+    }
+    const int ksplit = phase == 2 ? G.ks1 : G.ks2;
+    const int ncol_t = G.batch <= 2 ? (int)G.ncol : 0;  // staged operand at batch 1-2
+    const size_t lds = q4_gemv_lds(ncol_t, ksplit);
+    dim3 g((unsigned)round_up((size_t)a.n_wg, 8));  // a multiple of the 8 XCDs
+#define Q4_LAUNCH(ST, KS)                                                                        \
+    if (ncol_t == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 2>), g, dim3(256), lds, s, a);  \
+    else if (ncol_t == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 4>), g, dim3(256), lds, s, a); \
+    else hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0>), g, dim3(256), lds, s, a);
+#define Q4_LAUNCH_KS(ST)                                                                         \
+    if (ksplit == 4) { Q4_LAUNCH(ST, 4) }                                                        \
+    else if (ksplit == 2) { Q4_LAUNCH(ST, 2) }                                                   \
+    else { Q4_LAUNCH(ST, 1) }
+    if (phase == 2) {
+        Q4_LAUNCH_KS(1)
+    } else {
+        Q4_LAUNCH_KS(2)
+    }
+#undef Q4_LAUNCH_KS
+#undef Q4_LAUNCH
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+void q4_layer_entries(const qbk_factor *L, Q4Layer out[2]) {
+    Q4Geom G;
+    q4_build(&L, 1, 1, L->num_cus, out, G);
+}
+
+size_t q4_workspace(const qbk_factor *L, size_t batch) {
+    Q4Layer tab[2];
+    Q4Geom G;
+    q4_build(&L, 1, batch, L->num_cus, tab, G);
+    return G.bytes;
+}
+
+int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y, bool ybf16, void *ws,
+           hipStream_t s) {
+    Q4Layer tab[2];
+    Q4Geom G;
+    q4_build(&L, 1, batch, L->num_cus, tab, G);  // geometry; the device table is L->q4_tab
+    for (int ph = 1; ph <= Q4_PHASES; ph++) {
+        int rc = q4_phase(ph, G, L->q4_tab, nullptr, nullptr, x, xf32, y, ybf16, ws, s);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
+
+}  // namespace qbk
+
+using namespace qbk;
+
+// A decode set: layers of any shapes, one table, three launches.
+struct qbk_factor_set {
+    int device;
+    size_t n;
+    Q4Layer *tab;          // device: [0, n) stage 1, [n, 2n) stage 2; then the
+    uint32_t *wg1, *wg2;   // per-workgroup layer tables (same allocation)
+    Q4Geom geom;           // batch 1
+    std::vector<const qbk_factor *> layers;
+};
+
+extern "C" {
+
+int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t n,
+                          qbk_factor_set **out) {
+    int rc;
+    if (!out || !layers || n == 0) return fail(QBK_ERR_VALIDATION, "empty layer set");
+    *out = nullptr;
+    if ((rc = bind(ctx))) return rc;
+    for (size_t i = 0; i < n; i++) {
+        if (!layers[i]) return fail(QBK_ERR_VALIDATION, fmt("layer %zu of the set is null", i));
+        if (layers[i]->device != ctx->device)
+            return fail(QBK_ERR_VALIDATION, fmt("layer %zu lives on another device", i));
+    }
+    std::vector<Q4Layer> h(2 * n);
+    qbk_factor_set *S = new qbk_factor_set();
+    S->device = ctx->device;
+    S->n = n;
+    S->layers.assign(layers, layers + n);
+    q4_build(layers, n, 1, ctx->num_cus, h.data(), S->geom);
+    if (S->geom.n_wg1 == 0 || S->geom.n_wg2 == 0 || S->geom.ns1_tot >= (1ull << 31)) {
+        delete S;
+        return fail(QBK_ERR_VALIDATION, "layer set too large for one decode launch");
+    }
+    // layer of every workgroup of the two GEMV launches
+    std::vector<uint32_t> wl(S->geom.n_wg1 + S->geom.n_wg2);
+    for (size_t i = 0; i < n; i++) {
+        const uint32_t e1 = i + 1 < n ? h[i + 1].wg0 : S->geom.n_wg1;
+        const uint32_t e2 = i + 1 < n ? h[n + i + 1].wg0 : S->geom.n_wg2;
+        for (uint32_t w = h[i].wg0; w < e1; w++) wl[w] = (uint32_t)i;
+        for (uint32_t w = h[n + i].wg0; w < e2; w++) wl[S->geom.n_wg1 + w] = (uint32_t)i;
+    }
+    const size_t tab_bytes = 2 * n * sizeof(Q4Layer);
+    hipError_t e1 = hipMalloc((void **)&S->tab, tab_bytes + wl.size() * 4);
+    if (e1 != hipSuccess) {
+        delete S;
+        return fail(QBK_ERR_DEVICE, fmt("hipMalloc failed: %s", hipGetErrorString(e1)));
+    }
+    S->wg1 = (uint32_t *)((char *)S->tab + tab_bytes);
+    S->wg2 = S->wg1 + S->geom.n_wg1;
+    e1 = hipMemcpy(S->tab, h.data(), tab_bytes, hipMemcpyHostToDevice);
+    if (e1 == hipSuccess) e1 = hipMemcpy(S->wg1, wl.data(), wl.size() * 4, hipMemcpyHostToDevice);
+    if (e1 != hipSuccess) {
+        (void)hipFree(S->tab);
+        delete S;
+        return fail(QBK_ERR_DEVICE, fmt("hipMemcpy failed: %s", hipGetErrorString(e1)));
+    }
+    *out = S;
+    return QBK_OK;
+}
+
+void qbk_factor_set_destroy(qbk_factor_set *S) {
+    if (!S) return;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(S->device);
+    (void)hipFree(S->tab);
+    (void)hipSetDevice(cur);
+    delete S;
+}
+
+size_t qbk_factor_set_workspace_size(const qbk_factor_set *S) { return S ? S->geom.bytes : 0; }
+
+int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, const uint16_t *x,
+                             uint16_t *y, void *workspace, size_t workspace_size, void *stream) {
+    int rc;
+    if (!S) return fail(QBK_ERR_VALIDATION, "null layer set");
+    if (stage < 1 || stage > Q4_PHASES)
+        return fail(QBK_ERR_VALIDATION, fmt("stage must be 1..%d, got %d", Q4_PHASES, stage));
+    if ((rc = bind(ctx))) return rc;
+    if (workspace_size < S->geom.bytes)
+        return fail(QBK_ERR_VALIDATION, fmt("workspace of %zu bytes is smaller than the %zu this call needs",
+                                            workspace_size, S->geom.bytes));
+    return q4_phase(stage, S->geom, S->tab, S->wg1, S->wg2, x, false, y, true, workspace,
+                    (hipStream_t)stream);
+}
+
+int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *S, const uint16_t *x, uint16_t *y,
+                              void *workspace, size_t workspace_size, void *stream) {
+    for (int ph = 1; ph <= Q4_PHASES; ph++) {
+        int rc = qbk_factor_set_stage_dev(ctx, S, ph, x, y, workspace, workspace_size, stream);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,62 @@
+// factor_internal.h -- the device-resident factor layer shared by the layer
+// upload / prefill GEMM (factor.hip) and the decode GEMV (decode.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "qbk_internal.h"
+
+namespace qbk {
+
+// One stage of one layer in a decode launch: an entry of a device-side
+// table, so that one launch covers any number of layers of any shapes.
+// Offsets count slices (128 k) and elements, so they do not depend on the
+// batch; the byte offsets follow from the launch's column count.
+struct Q4Layer {
+    const uint32_t *bits;        // this stage's signs in the fp4 decode layout
+    const float *s_in;           // stage 1: s2
+    const float *s_out, *bias;   // stage 2: s1, bias
+    uint32_t rows_p, rows_valid; // this stage's output rows: padded (to 128), valid
+    uint32_t ns, k_valid;        // this stage's 128-k slices, valid K
+    uint32_t slice0;             // slices of this stage held by the layers before this one
+    uint32_t tb_ns, tb_slice0;   // stage 1: stage 2's slices of this layer / before it
+    uint32_t wg0;                // first workgroup of this layer in its stage's launch
+    uint64_t act0, out0;         // element offsets of this layer's x (stage 1) / y (stage 2)
+};
+
+}  // namespace qbk
+
+struct qbk_factor {
+    int device, num_cus;
+    size_t dout, din, r;
+    size_t din_p, r_p, dout_p;  // padded for the MFMA tiles (64 / 128 / 128)
+    uint8_t *ub_rows, *vbt_rows;      // reference per-row bitplanes
+    uint32_t *vt_frag, *u_frag;       // [r_p/64][din_p/32][64], [dout_p/64][r_p/32][64]
+    size_t din_q, r_q;                // K of the fp4 decode layout: multiples of 128
+    uint32_t *vt_q4, *u_q4;           // [r_p/64][din_q/128][64][4], [dout_p/64][r_q/128][64][4]
+    float *s1, *s2, *bias;            // dout, din, dout (zeros when absent)
+    qbk::Q4Layer *q4_tab;             // device Q4Layer[2] of this layer alone: stage 1, stage 2
+    std::vector<void *> allocs;
+};
+
+namespace qbk {
+
+// decode.hip: the largest batch the fp4 decode GEMV serves.
+constexpr size_t Q4_MAXB = 8;
+
+// The two table entries of one layer decoded alone (offsets 0).
+void q4_layer_entries(const qbk_factor *L, Q4Layer out[2]);
+
+// Workspace bytes of a single-layer decode at `batch` (<= Q4_MAXB).
+size_t q4_workspace(const qbk_factor *L, size_t batch);
+
+// Single-layer decode: x [batch][din] (bf16, or f32 when xf32) ->
+// y [batch][dout] (bf16 when ybf16, else f32), three launches on s.
+int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y, bool ybf16,
+           void *ws, hipStream_t s);
+
+}  // namespace qbk

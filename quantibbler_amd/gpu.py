@@ -239,7 +239,8 @@ class FactorLayer:
 
 
 class FactorSet:
-    """Layers of one shape decoded together, one launch per stage."""
+    """Layers (any shapes) decoded together at batch 1 in three launches;
+    x and y are the concatenations of the layers' x_i and y_i."""
 
     def __init__(self, ctx: GpuContext, layers):
         self.ctx = ctx

@@ -209,6 +209,37 @@ def test_set_decode_matches_single_layers(ctx, orc, dout, din, r, n):
         same(ys[i], yi[0])
 
 
+def test_mixed_shape_set_decode(ctx, orc):
+    """One set over layers of different shapes (a decoder layer's q/k/v/o/
+    gate/up/down, scaled down, with ragged ranks and a din that is not a
+    multiple of 8): x and y are the concatenated per-layer vectors, every
+    layer's output bit-identical to the oracle on integer-exact inputs."""
+    from quantibbler_amd import FactorSet
+
+    say("factor mixed-shape set decode")
+    rng = np.random.default_rng(91)
+    shapes = [(512, 512, 138), (128, 512, 54), (128, 512, 54), (512, 512, 138), (1792, 512, 216),
+              (1792, 512, 216), (512, 1792, 217), (200, 300, 37)]
+    Ls = [make_layer(orc, rng, m, n, r, integer=True) for m, n, r in shapes]
+    layers = [upload(ctx, L) for L in Ls]
+    S = FactorSet(ctx, layers)
+    xs = [orc.f32_to_bf16_fast(rng.integers(-2, 3, n).astype(np.float32)) for _, n, _ in shapes]
+    x = np.concatenate(xs)
+    xd = torch.from_numpy(x.view(np.int16)).cuda()
+    yd = torch.empty(sum(m for m, _, _ in shapes), dtype=torch.int16, device="cuda")
+    ws = torch.zeros(S.workspace_size(), dtype=torch.uint8, device="cuda")
+    for rep in range(2):  # the workspace keeps the last call's contents: run twice
+        S.decode_dev(xd, yd, ws, ws.numel(), torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        y = yd.cpu().numpy().view(np.uint16)
+        off = 0
+        for i, ((m, n, r), L, xi) in enumerate(zip(shapes, Ls, xs)):
+            want = orc.factor_apply_bf16_batch(m, n, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"],
+                                               xi[None, :])
+            same(y[off:off + m], orc.f32_to_bf16_fast(want)[0], f"mixed set, layer {i} {(m, n, r)}")
+            off += m
+
+
 def test_apply_host_faces(ctx, orc):
     say("factor apply host faces")
     rng = np.random.default_rng(5)
