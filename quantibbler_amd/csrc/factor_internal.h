@@ -35,7 +35,7 @@ struct qbk_factor {
     size_t dout, din, r;
     size_t din_p, r_p, dout_p;  // padded for the MFMA tiles (64 / 128 / 128)
     uint8_t *ub_rows, *vbt_rows;      // reference per-row bitplanes
-    uint32_t *vt_frag, *u_frag;       // [r_p/64][din_p/32][64], [dout_p/64][r_p/32][64]
+    uint32_t *vt_g32, *u_g32;         // prefill layout: [r_p/128][din_p/64][64][4], [dout_p/128][r_p/64][64][4]
     size_t din_q, r_q;                // K of the fp4 decode layout: multiples of 128
     uint32_t *vt_q4, *u_q4;           // [r_p/64][din_q/128][64][4], [dout_p/64][r_q/128][64][4]
     float *s1, *s2, *bias;            // dout, din, dout (zeros when absent)
@@ -58,5 +58,14 @@ size_t q4_workspace(const qbk_factor *L, size_t batch);
 // y [batch][dout] (bf16 when ybf16, else f32), three launches on s.
 int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y, bool ybf16,
            void *ws, hipStream_t s);
+
+// prefill.hip: the sign layout of the prefill GEMM (rows_p a multiple of
+// 128, bits_p of 64), its workspace, and the two-stage GEMM for N tokens:
+// x [N][din] (bf16, or f32 when xf32) -> y [N][dout].
+void g32_repack(const uint8_t *rows, size_t n_rows, size_t n_bits, size_t rows_p, size_t bits_p,
+                uint32_t *out);
+size_t g32_workspace(const qbk_factor *L, size_t N);
+int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
+            hipStream_t s);
 
 }  // namespace qbk

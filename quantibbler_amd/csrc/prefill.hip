@@ -1,0 +1,440 @@
+// prefill.hip -- the factor linear's prefill GEMM (batch > 8) on gfx950.
+//
+//   t = bf16(Vb^T z), z = bf16(s2 * x);  y = bf16(Ub t) * s1 + bias
+//                              (engine/mod.rs:449-460, apply_bf16, per token)
+//
+// Both stages are C[M x N] = S[M x K] (+-1) . Act[K x N] with the
+// activations token-major (Act^T [N][K], bf16) and f32 accumulation on
+// v_mfma_f32_32x32x16_bf16:
+//   * workgroup tile 256 (rows) x 128 (tokens), 4 waves as 2 x 2, wave tile
+//     128 x 64 = 4 x 2 MFMA tiles;
+//   * A (signs): each wave loads one uint4 per lane per 64-k stage -- its
+//     128 rows x 64 k bits -- from the g32 layout (g32_repack) and expands a
+//     32x16 fragment with two VALU ops per VGPR, reused by both n-tiles;
+//   * B (activations): 128 tokens x 64 k staged through LDS, double
+//     buffered, rows padded to 144 bytes (the 32 lanes of a fragment read
+//     rows 144 B apart: conflict-free 16-byte reads);
+//   * stage 1 reads z = bf16(s2 * x) written once by g32_prep_kernel (zero
+//     past din), splits K to fill the chip and writes f32 partials that
+//     g32_reduce_kernel sums in split order into t bf16 (zero past r); with
+//     no split the epilogue writes t directly;
+//   * stage 2 reads t and writes y = bf16(u) * s1 + bias, u = bf16(acc).
+#include <string.h>
+
+#include "factor_internal.h"
+
+namespace qbk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+#define G_BM 256
+#define G_BN 128
+#define G_BK 64
+#define G_PITCH 72    // bf16 per LDS row of the activation tile: 64 + 8 of padding
+#define G_TPITCH 132  // f32 per token row of the epilogue transpose: 128 + 4
+#define G_LDS (4 * 32 * G_TPITCH * 4)  // >= 2 * G_BN * G_PITCH * 2
+
+// g32 sign layout: blocks of (128-row group g, 64-k slice s), 64 lanes x 4
+// words.  Word j of lane l holds row 128g + 32j + l%32 at
+// k = 64s + 16q + 8(l/32) + e for k16 step q (0..3) and element e (0..7):
+// element 2v at bit 4q + v, element 2v + 1 at bit 4q + v + 16, set when the
+// sign is -1 (0 in the rows' bitplanes).  Rows >= n_rows and k >= n_bits
+// hold +1 (0): padded k meets zero activations.
+void g32_repack(const uint8_t *rows, size_t n_rows, size_t n_bits, size_t rows_p, size_t bits_p,
+                uint32_t *out) {
+    const size_t rw = div_ceil(n_bits, 8);
+    const size_t ng = rows_p / 128, nsk = bits_p / 64;
+    memset(out, 0, ng * nsk * 64 * 4 * 4);
+    for (size_t g = 0; g < ng; g++)
+        for (size_t s = 0; s < nsk; s++)
+            for (int l = 0; l < 64; l++)
+                for (int j = 0; j < 4; j++) {
+                    const size_t i = 128 * g + 32 * j + (l & 31);
+                    if (i >= n_rows) continue;
+                    uint32_t w = 0;
+                    for (int q = 0; q < 4; q++)
+                        for (int e = 0; e < 8; e++) {
+                            const size_t k = 64 * s + 16 * q + 8 * (l >> 5) + e;
+                            if (k < n_bits && !((rows[i * rw + (k >> 3)] >> (k & 7)) & 1))
+                                w |= 1u << (4 * q + (e >> 1) + 16 * (e & 1));
+                        }
+                    out[((g * nsk + s) * 64 + l) * 4 + j] = w;
+                }
+}
+
+struct G32Args {
+    const uint32_t *sg;    // g32 layout [M_p/128][K_p/64][64][4]
+    size_t M_p, K_p, M_valid, N;
+    const uint16_t *act;   // bf16 [N][K_p] (z or t), zero for k past the valid K
+    // stage 1
+    float *part;           // [split][N][M_p] f32 (split > 1)
+    uint16_t *t_out;       // [N][M_p] bf16 (split == 1), zero for rows >= M_valid
+    size_t k_per_split;
+    int split;
+    // stage 2
+    void *y;               // [N][M_valid] bf16 or f32
+    const float *s1, *bias;
+    int y_bf16, vec_y;     // vec_y: y rows allow 16-byte stores (M_valid % 8 == 0, y aligned)
+};
+
+// Expand sign word w for k16 step q into the 32x16 A fragment: VGPR v holds
+// elements 2v, 2v + 1 as bf16 +-1 (0x3F80 | sign << 15).
+__device__ __forceinline__ bf16x8_t g32_frag(uint32_t w, int q) {
+    uint4 u;
+    u.x = ((w << (15 - (4 * q + 0))) & 0x80008000u) | 0x3F803F80u;
+    u.y = ((w << (15 - (4 * q + 1))) & 0x80008000u) | 0x3F803F80u;
+    u.z = ((w << (15 - (4 * q + 2))) & 0x80008000u) | 0x3F803F80u;
+    u.w = ((w << (15 - (4 * q + 3))) & 0x80008000u) | 0x3F803F80u;
+    return __builtin_bit_cast(bf16x8_t, u);
+}
+
+template <int STAGE>
+__global__ void __launch_bounds__(256) g32_kernel(G32Args a) {
+    // [2 tile buffers of G_BN x G_PITCH bf16] during the loop; [4 waves][32 x
+    // G_TPITCH f32] in the epilogue
+    extern __shared__ __attribute__((aligned(16))) uint8_t g32_lds[];
+    uint16_t(*bs)[G_BN * G_PITCH] = (uint16_t(*)[G_BN * G_PITCH])g32_lds;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const size_t n0 = (size_t)blockIdx.x * G_BN, m0 = (size_t)blockIdx.y * G_BM;
+    size_t kb = 0, ke = a.K_p;
+    if (STAGE == 1) {
+        kb = (size_t)blockIdx.z * a.k_per_split;
+        ke = kb + a.k_per_split < a.K_p ? kb + a.k_per_split : a.K_p;
+    }
+    const size_t ng = a.M_p / 128, nsk = a.K_p / G_BK;
+    const size_t g = m0 / 128 + wm;                 // this wave's 128-row group
+    const size_t gc = g < ng ? g : ng - 1;          // clamped: loads stay in bounds
+    const uint4 *sp = (const uint4 *)a.sg + (gc * nsk) * 64 + lane;
+
+    // B tile: 128 tokens x 64 k = 1024 chunks of 8 bf16, four per thread
+    uint4 breg[4];
+    auto load_b = [&](size_t k0) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int c = tid + 256 * u, nn = c >> 3, kk = (c & 7) * 8;
+            const size_t n = n0 + nn;
+            breg[u] = n < a.N ? *(const uint4 *)(a.act + n * a.K_p + k0 + kk) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_b = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int c = tid + 256 * u, nn = c >> 3, kk = (c & 7) * 8;
+            *(uint4 *)&bs[buf][nn * G_PITCH + kk] = breg[u];
+        }
+    };
+
+    f32x16_t acc[4][2];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[j][nt][i] = 0.0f;
+
+    uint4 aw = make_uint4(0, 0, 0, 0);
+    if (kb < ke) {
+        load_b(kb);
+        aw = sp[(kb / G_BK) * 64];
+        store_b(0);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (size_t k0 = kb; k0 < ke; k0 += G_BK) {
+        const bool more = k0 + G_BK < ke;
+        uint4 an = make_uint4(0, 0, 0, 0);
+        if (more) {
+            load_b(k0 + G_BK);
+            an = sp[((k0 + G_BK) / G_BK) * 64];
+        }
+        const uint32_t wv[4] = {aw.x, aw.y, aw.z, aw.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            bf16x8_t bf[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                const int nn = wn * 64 + nt * 32 + (lane & 31);
+                const uint4 bv = *(const uint4 *)&bs[buf][nn * G_PITCH + 16 * q + 8 * (lane >> 5)];
+                bf[nt] = __builtin_bit_cast(bf16x8_t, bv);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bf16x8_t af = g32_frag(wv[j], q);
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+                    acc[j][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[nt], acc[j][nt], 0, 0, 0);
+            }
+        }
+        if (more) {
+            store_b(buf ^ 1);
+            aw = an;
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+    // Epilogue, one 32-token n-tile at a time, through the wave's LDS region
+    // T [32 tokens][G_TPITCH] f32 (the tile buffers are free: the loop ended
+    // with a barrier): lanes write their accumulators -- acc[j][nt][4h + p]
+    // is row 32j + 8h + 4(l/32) + p of token l%32 -- then read whole
+    // token rows back, so that consecutive lanes store consecutive 16-byte
+    // pieces of one token's output row.
+    float *T = (float *)(g32_lds + wave * (32 * G_TPITCH * 4));
+    const bool gvalid = g < ng;
+    const size_t row0 = 128 * g;  // this wave's first row
+    // stage 2: s1 and bias of rows 8c .. 8c + 7 of the wave (c = lane % 16)
+    float s1v[8], biv[8];
+    if (STAGE == 2 && gvalid) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const size_t rr = row0 + 8 * (lane & 15) + e;
+            s1v[e] = rr < a.M_valid ? a.s1[rr] : 0.0f;
+            biv[e] = rr < a.M_valid ? a.bias[rr] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int h = 0; h < 4; h++)
+                *(float4 *)&T[(lane & 31) * G_TPITCH + 32 * j + 8 * h + 4 * (lane >> 5)] =
+                    make_float4(acc[j][nt][4 * h], acc[j][nt][4 * h + 1], acc[j][nt][4 * h + 2],
+                                acc[j][nt][4 * h + 3]);
+        __builtin_amdgcn_wave_barrier();
+        const size_t nb = n0 + wn * 64 + nt * 32;  // first token of the n-tile
+        if (gvalid) {
+            if (STAGE == 1 && a.split > 1) {
+                // f32 partials: 32 lanes per token (4 rows each), two tokens per store
+#pragma unroll 4
+                for (int k = 0; k < 16; k++) {
+                    const int tt = 2 * k + (lane >> 5), c = lane & 31;
+                    const size_t n = nb + tt;
+                    const float4 v = *(const float4 *)&T[tt * G_TPITCH + 4 * c];
+                    if (n < a.N) *(float4 *)(a.part + ((size_t)blockIdx.z * a.N + n) * a.M_p + row0 + 4 * c) = v;
+                }
+            } else {
+                // bf16 rows: 16 lanes per token (8 rows each), four tokens per store
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int tt = 4 * k + (lane >> 4), c = lane & 15;
+                    const size_t n = nb + tt;
+                    const float4 v0 = *(const float4 *)&T[tt * G_TPITCH + 8 * c];
+                    const float4 v1 = *(const float4 *)&T[tt * G_TPITCH + 8 * c + 4];
+                    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                    const size_t rb = row0 + 8 * c;
+                    if (n >= a.N) continue;
+                    if (STAGE == 1) {
+                        // t = bf16(acc), zero past r (split == 1)
+                        uint32_t w[4];
+#pragma unroll
+                        for (int p = 0; p < 4; p++) {
+                            const uint32_t lo = rb + 2 * p < a.M_valid ? f32_to_bf16(v[2 * p]) : 0;
+                            const uint32_t hi = rb + 2 * p + 1 < a.M_valid ? f32_to_bf16(v[2 * p + 1]) : 0;
+                            w[p] = lo | (hi << 16);
+                        }
+                        *(uint4 *)(a.t_out + n * a.M_p + rb) = make_uint4(w[0], w[1], w[2], w[3]);
+                    } else {
+                        float y[8];
+#pragma unroll
+                        for (int p = 0; p < 8; p++) y[p] = bf16_to_f32(f32_to_bf16(v[p])) * s1v[p] + biv[p];
+                        if (a.y_bf16 && a.vec_y && rb + 8 <= a.M_valid) {
+                            uint32_t w[4];
+#pragma unroll
+                            for (int p = 0; p < 4; p++)
+                                w[p] = (uint32_t)f32_to_bf16(y[2 * p]) | ((uint32_t)f32_to_bf16(y[2 * p + 1]) << 16);
+                            *(uint4 *)((uint16_t *)a.y + n * a.M_valid + rb) = make_uint4(w[0], w[1], w[2], w[3]);
+                        } else {
+#pragma unroll
+                            for (int p = 0; p < 8; p++) {
+                                if (rb + p >= a.M_valid) continue;
+                                if (a.y_bf16)
+                                    ((uint16_t *)a.y)[n * a.M_valid + rb + p] = f32_to_bf16(y[p]);
+                                else
+                                    ((float *)a.y)[n * a.M_valid + rb + p] = y[p];
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the next n-tile overwrites T
+    }
+}
+
+// z[n][k] = bf16(s2[k] * x[n][k]) for k < din, 0 for din <= k < K_p; eight
+// elements per thread.
+template <bool XF32>
+__global__ void __launch_bounds__(256) g32_prep_kernel(const void *x, const float *s2, size_t din,
+                                                        size_t K_p, size_t N, uint16_t *z, int vec_ok) {
+    const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t per_row = K_p / 8;
+    if (c >= N * per_row) return;
+    const size_t n = c / per_row, k0 = (c % per_row) * 8;
+    float v[8], sv[8];
+    if (vec_ok && k0 + 8 <= din) {
+        if (XF32) {
+            const float4 *xp = (const float4 *)((const float *)x + n * din + k0);
+            const float4 a0 = xp[0], a1 = xp[1];
+            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+        } else {
+            const uint4 xb = *(const uint4 *)((const uint16_t *)x + n * din + k0);
+            const uint32_t w[4] = {xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[2 * e] = bf16_to_f32(w[e] & 0xffff);
+                v[2 * e + 1] = bf16_to_f32(w[e] >> 16);
+            }
+        }
+        const float4 *sp = (const float4 *)(s2 + k0);
+        const float4 b0 = sp[0], b1 = sp[1];
+        sv[0] = b0.x; sv[1] = b0.y; sv[2] = b0.z; sv[3] = b0.w;
+        sv[4] = b1.x; sv[5] = b1.y; sv[6] = b1.z; sv[7] = b1.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const size_t k = k0 + e;
+            const bool ok = k < din;
+            v[e] = !ok ? 0.0f : XF32 ? ((const float *)x)[n * din + k] : bf16_to_f32(((const uint16_t *)x)[n * din + k]);
+            sv[e] = ok ? s2[k] : 0.0f;
+        }
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        w[e] = (uint32_t)f32_to_bf16(sv[2 * e] * v[2 * e]) | ((uint32_t)f32_to_bf16(sv[2 * e + 1] * v[2 * e + 1]) << 16);
+    *(uint4 *)(z + n * K_p + k0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// t = bf16(sum of the split partials in split order), zero for rows >= r;
+// eight rows per thread.
+__global__ void __launch_bounds__(256) g32_reduce_kernel(const float *__restrict__ part, int split,
+                                                          size_t stride, size_t ld, size_t r,
+                                                          uint16_t *__restrict__ t, size_t chunks) {
+    const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const size_t e0 = c * 8, k0 = e0 % ld;
+    float v[8];
+    const float4 *p0 = (const float4 *)(part + e0);
+    const float4 a0 = p0[0], a1 = p0[1];
+    v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+    v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+    for (int s = 1; s < split; s++) {
+        const float4 *ps = (const float4 *)(part + (size_t)s * stride + e0);
+        const float4 c0 = ps[0], c1 = ps[1];
+        v[0] += c0.x; v[1] += c0.y; v[2] += c0.z; v[3] += c0.w;
+        v[4] += c1.x; v[5] += c1.y; v[6] += c1.z; v[7] += c1.w;
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t lo = k0 + 2 * e < r ? f32_to_bf16(v[2 * e]) : 0;
+        const uint32_t hi = k0 + 2 * e + 1 < r ? f32_to_bf16(v[2 * e + 1]) : 0;
+        w[e] = lo | (hi << 16);
+    }
+    *(uint4 *)(t + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------
+
+// Stage-1 K split: enough workgroups to cover every CU, at least four
+// 64-k stages per split.
+static int g32_split(const qbk_factor *L, size_t N) {
+    const size_t tiles = div_ceil(N, G_BN) * div_ceil(L->r_p, G_BM);
+    int s = 1;
+    while (tiles * s < (size_t)L->num_cus && s < 8 && L->din_p / (G_BK * 2 * s) >= 4) s *= 2;
+    return s;
+}
+
+// Workspace: z bf16 [N][din_p] | partials f32 [split][N][r_p] | t bf16 [N][r_p].
+struct G32Plan {
+    int split;
+    size_t o_z, o_part, o_t, bytes;
+};
+
+static G32Plan g32_plan(const qbk_factor *L, size_t N) {
+    G32Plan p{};
+    p.split = g32_split(L, N);
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        size_t o = off;
+        off += round_up(n, 256);
+        return o;
+    };
+    p.o_z = take(N * L->din_p * 2);
+    p.o_part = take(p.split > 1 ? (size_t)p.split * N * L->r_p * 4 : 0);
+    p.o_t = take(N * L->r_p * 2);
+    p.bytes = off;
+    return p;
+}
+
+size_t g32_workspace(const qbk_factor *L, size_t N) { return g32_plan(L, N).bytes; }
+
+int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
+            hipStream_t s) {
+    const G32Plan p = g32_plan(L, N);
+    static bool lds_set = false;  // the epilogue's 66 KiB exceed the 64 KiB default
+    if (!lds_set) {
+        QBK_HIP(hipFuncSetAttribute((const void *)g32_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
+        QBK_HIP(hipFuncSetAttribute((const void *)g32_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
+        lds_set = true;
+    }
+    char *w = (char *)ws;
+    uint16_t *z = (uint16_t *)(w + p.o_z), *t = (uint16_t *)(w + p.o_t);
+    float *part = (float *)(w + p.o_part);
+    {
+        const size_t chunks = N * L->din_p / 8;
+        const int vec_ok = L->din % 8 == 0 && (uintptr_t)x % 16 == 0;
+        dim3 g((unsigned)div_ceil(chunks, 256));
+        if (xf32)
+            hipLaunchKernelGGL((g32_prep_kernel<true>), g, dim3(256), 0, s, x, (const float *)L->s2, L->din,
+                               L->din_p, N, z, vec_ok);
+        else
+            hipLaunchKernelGGL((g32_prep_kernel<false>), g, dim3(256), 0, s, x, (const float *)L->s2, L->din,
+                               L->din_p, N, z, vec_ok);
+        QBK_HIP(hipGetLastError());
+    }
+    G32Args a{};
+    a.sg = L->vt_g32;
+    a.M_p = L->r_p;
+    a.K_p = L->din_p;
+    a.M_valid = L->r;
+    a.N = N;
+    a.act = z;
+    a.split = p.split;
+    a.part = part;
+    a.t_out = t;
+    a.k_per_split = round_up(div_ceil(L->din_p, p.split), G_BK);
+    dim3 g1((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->r_p, G_BM), p.split);
+    hipLaunchKernelGGL((g32_kernel<1>), g1, dim3(256), G_LDS, s, a);
+    QBK_HIP(hipGetLastError());
+    if (p.split > 1) {
+        const size_t chunks = N * L->r_p / 8;
+        hipLaunchKernelGGL(g32_reduce_kernel, dim3((unsigned)div_ceil(chunks, 256)), dim3(256), 0, s,
+                           (const float *)part, p.split, N * L->r_p, L->r_p, L->r, t, chunks);
+        QBK_HIP(hipGetLastError());
+    }
+    G32Args b{};
+    b.sg = L->u_g32;
+    b.M_p = L->dout_p;
+    b.K_p = L->r_p;
+    b.M_valid = L->dout;
+    b.N = N;
+    b.act = t;
+    b.y = y;
+    b.s1 = L->s1;
+    b.bias = L->bias;
+    b.y_bf16 = ybf16;
+    b.vec_y = L->dout % 8 == 0 && (uintptr_t)y % 16 == 0;
+    dim3 g2((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->dout_p, G_BM), 1);
+    hipLaunchKernelGGL((g32_kernel<2>), g2, dim3(256), G_LDS, s, b);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+}  // namespace qbk

@@ -125,19 +125,22 @@ def gpu_t(layer, ws, batch):
         assert np.array_equal(orc.bf16_to_f32(tb).astype(np.float64), t), "operand is not a bf16 t"
         assert not tb[:, r:].any()
         return tb[:, :r]
-    # [split][batch][r_p] f32 partials, then t bf16 [batch][r_p]
-    for s in (1, 2, 4, 8):
-        off = rnd(s * batch * rp * 4)
-        if off + batch * rp * 2 + 256 == ws.size:
-            t = ws[off: off + batch * rp * 2].view(np.uint16).reshape(batch, rp)
-            assert not t[:, r:].any()
-            parts = ws[: s * batch * rp * 4].view(np.float32).reshape(s, batch, rp)
-            tot = parts[0].copy()
-            for i in range(1, s):
-                tot = (tot + parts[i]).astype(np.float32)
-            from oracle import oracle as orc
+    # prefill GEMM: [z bf16 [batch][din_p] | f32 partials [split][batch][r_p]
+    # (split > 1) | t bf16 [batch][r_p]]
+    from oracle import oracle as orc
 
-            assert np.array_equal(orc.f32_to_bf16_fast(tot[:, :r]), t[:, :r])
+    zb = rnd(batch * (-(-layer.din // 64) * 64) * 2)
+    for s in (1, 2, 4, 8):
+        pb = rnd(s * batch * rp * 4) if s > 1 else 0
+        if zb + pb + rnd(batch * rp * 2) == ws.size:
+            t = ws[zb + pb: zb + pb + batch * rp * 2].view(np.uint16).reshape(batch, rp)
+            assert not t[:, r:].any()
+            if s > 1:
+                parts = ws[zb: zb + s * batch * rp * 4].view(np.float32).reshape(s, batch, rp)
+                tot = parts[0].copy()
+                for i in range(1, s):
+                    tot = (tot + parts[i]).astype(np.float32)
+                assert np.array_equal(orc.f32_to_bf16_fast(tot[:, :r]), t[:, :r])
             return t[:, :r]
     raise AssertionError("unexpected workspace size")
 
