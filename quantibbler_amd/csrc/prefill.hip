@@ -6,10 +6,12 @@
 // Both stages are C[M x N] = S[M x K] (+-1) . Act[K x N] with the
 // activations token-major (Act^T [N][K], bf16) and f32 accumulation on
 // v_mfma_f32_32x32x16_bf16:
-//   * workgroup tile 256 (rows) x 128 (tokens), 4 waves as 2 x 2, wave tile
-//     128 x 64 = 4 x 2 MFMA tiles;
-//   * A (signs): each wave loads one uint4 per lane per 64-k stage -- its
-//     128 rows x 64 k bits -- from the g32 layout (g32_repack) and expands a
+//   * workgroup tile 256 (rows) x 128 (tokens), 8 waves as 4 (rows) x 2
+//     (tokens), wave tile 64 x 64 = 2 x 2 MFMA tiles: 64 accumulator
+//     registers, so two waves share each SIMD and one's LDS and barrier
+//     waits are covered by the other's MFMAs;
+//   * A (signs): each wave loads one uint2 per lane per 64-k stage -- its
+//     64 rows x 64 k bits -- from the g32 layout (g32_repack) and expands a
 //     32x16 fragment with two VALU ops per VGPR, reused by both n-tiles;
 //   * B (activations): 128 tokens x 64 k staged through LDS, double
 //     buffered, rows padded to 144 bytes (the 32 lanes of a fragment read
@@ -27,13 +29,14 @@ namespace qbk {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 #define G_BM 256
 #define G_BN 128
 #define G_BK 64
 #define G_PITCH 72    // bf16 per LDS row of the activation tile: 64 + 8 of padding
-#define G_TPITCH 132  // f32 per token row of the epilogue transpose: 128 + 4
-#define G_LDS (4 * 32 * G_TPITCH * 4)  // >= 2 * G_BN * G_PITCH * 2
+#define G_TPITCH 68   // f32 per token row of the epilogue transpose: 64 + 4
+#define G_LDS (8 * 32 * G_TPITCH * 4)  // >= 2 * G_BN * G_PITCH * 2
 
 // g32 sign layout: blocks of (128-row group g, 64-k slice s), 64 lanes x 4
 // words.  Word j of lane l holds row 128g + 32j + l%32 at
@@ -76,28 +79,31 @@ struct G32Args {
     void *y;               // [N][M_valid] bf16 or f32
     const float *s1, *bias;
     int y_bf16, vec_y;     // vec_y: y rows allow 16-byte stores (M_valid % 8 == 0, y aligned)
+    uint32_t sign_mask, one_pair;  // 0x80008000, 0x3F803F80 (see g32_frag)
 };
 
 // Expand sign word w for k16 step q into the 32x16 A fragment: VGPR v holds
-// elements 2v, 2v + 1 as bf16 +-1 (0x3F80 | sign << 15).
-__device__ __forceinline__ bf16x8_t g32_frag(uint32_t w, int q) {
-    uint4 u;
-    u.x = ((w << (15 - (4 * q + 0))) & 0x80008000u) | 0x3F803F80u;
-    u.y = ((w << (15 - (4 * q + 1))) & 0x80008000u) | 0x3F803F80u;
-    u.z = ((w << (15 - (4 * q + 2))) & 0x80008000u) | 0x3F803F80u;
-    u.w = ((w << (15 - (4 * q + 3))) & 0x80008000u) | 0x3F803F80u;
+// elements 2v, 2v + 1 as bf16 +-1 (0x3F80 | sign << 15).  The mask and the
+// +1 pair come in as registers (m = 0x80008000, one = 0x3F803F80) so that
+// each VGPR costs a shift and one v_and_or_b32 (VOP3 takes no literal).
+__device__ __forceinline__ bf16x8_t g32_frag(uint32_t w, int q, uint32_t m, uint32_t one) {
+    u32x4_t u;
+    u.x = ((w << (15 - (4 * q + 0))) & m) | one;
+    u.y = ((w << (15 - (4 * q + 1))) & m) | one;
+    u.z = ((w << (15 - (4 * q + 2))) & m) | one;
+    u.w = ((w << (15 - (4 * q + 3))) & m) | one;
     return __builtin_bit_cast(bf16x8_t, u);
 }
 
 template <int STAGE>
-__global__ void __launch_bounds__(256) g32_kernel(G32Args a) {
-    // [2 tile buffers of G_BN x G_PITCH bf16] during the loop; [4 waves][32 x
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) g32_kernel(G32Args a) {
+    // [2 tile buffers of G_BN x G_PITCH bf16] during the loop; [8 waves][32 x
     // G_TPITCH f32] in the epilogue
     extern __shared__ __attribute__((aligned(16))) uint8_t g32_lds[];
     uint16_t(*bs)[G_BN * G_PITCH] = (uint16_t(*)[G_BN * G_PITCH])g32_lds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wr = wave & 3, wc = wave >> 2;  // 64-row block, 64-token half
     const size_t n0 = (size_t)blockIdx.x * G_BN, m0 = (size_t)blockIdx.y * G_BM;
     size_t kb = 0, ke = a.K_p;
     if (STAGE == 1) {
@@ -105,76 +111,105 @@ __global__ void __launch_bounds__(256) g32_kernel(G32Args a) {
         ke = kb + a.k_per_split < a.K_p ? kb + a.k_per_split : a.K_p;
     }
     const size_t ng = a.M_p / 128, nsk = a.K_p / G_BK;
-    const size_t g = m0 / 128 + wm;                 // this wave's 128-row group
+    const size_t g = m0 / 128 + (wr >> 1);          // this wave's 128-row group
     const size_t gc = g < ng ? g : ng - 1;          // clamped: loads stay in bounds
-    const uint4 *sp = (const uint4 *)a.sg + (gc * nsk) * 64 + lane;
+    // words 2h, 2h + 1 of each lane's record: this wave's 64 rows
+    const uint2 *sp = (const uint2 *)a.sg + ((gc * nsk) * 64 + lane) * 2 + (wr & 1);
+    // the +1 pair in a VGPR, the mask in an SGPR: one v_and_or_b32 can read both
+    const uint32_t m_sign = a.sign_mask;
+    uint32_t one;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(a.one_pair));
 
-    // B tile: 128 tokens x 64 k = 1024 chunks of 8 bf16, four per thread
-    uint4 breg[4];
-    auto load_b = [&](size_t k0) {
+    // B tile: 128 tokens x 64 k = 1024 chunks of 8 bf16, two per thread
+    // (tokens tid/8 + 64u, k chunk tid%8).  Every load is issued
+    // unconditionally -- tokens past N are clamped to N - 1 and only feed
+    // output columns the epilogue does not store -- so that the wait for the
+    // prefetch can be a counted one at the LDS store.
+    const uint16_t *brow[2];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int c = tid + 256 * u, nn = c >> 3, kk = (c & 7) * 8;
-            const size_t n = n0 + nn;
-            breg[u] = n < a.N ? *(const uint4 *)(a.act + n * a.K_p + k0 + kk) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_b = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int c = tid + 256 * u, nn = c >> 3, kk = (c & 7) * 8;
-            *(uint4 *)&bs[buf][nn * G_PITCH + kk] = breg[u];
-        }
-    };
+    for (int u = 0; u < 2; u++) {
+        const size_t n = n0 + (tid >> 3) + 64 * u;
+        brow[u] = a.act + (n < a.N ? n : a.N - 1) * a.K_p + (tid & 7) * 8;
+    }
+    u32x4_t breg[2];
 
-    f32x16_t acc[4][2];
+    f32x16_t acc[2][2];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int nt = 0; nt < 2; nt++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[j][nt][i] = 0.0f;
 
-    uint4 aw = make_uint4(0, 0, 0, 0);
-    if (kb < ke) {
-        load_b(kb);
-        aw = sp[(kb / G_BK) * 64];
-        store_b(0);
+    // Three-stage pipeline over the 64-k stages i.  Activations: stage
+    // i + 2's tile is in flight from global memory, stage i + 1's sits in
+    // registers until it is stored to LDS at the top of stage i and read
+    // back (after the barrier) under stage i's MFMAs.  Signs: stage i + 2's
+    // words load during stage i and stage i + 1's fragments are expanded
+    // between stage i's MFMAs, so that no MFMA waits on a VALU result or an
+    // LDS read of its own stage.  Stages past the end reload the last one (in
+    // bounds, never used).  The loop is unrolled by two so that words,
+    // fragments and tiles alternate between two register sets (a copy of a
+    // value still in flight would wait for it).
+    const size_t k_last = ke > kb ? ke - G_BK : kb;
+    uint2 awA = make_uint2(0, 0), awB = make_uint2(0, 0);
+    bf16x8_t afA[4][2], afB[4][2], bfA[4][2], bfB[4][2];
+#define G32_READ_FRAGS(B, F)                                                                    \
+    _Pragma("unroll") for (int q = 0; q < 4; q++)                                               \
+    _Pragma("unroll") for (int nt = 0; nt < 2; nt++)                                            \
+        F[q][nt] = __builtin_bit_cast(                                                          \
+            bf16x8_t, *(const u32x4_t *)&bs[B][(wc * 64 + nt * 32 + (lane & 31)) * G_PITCH +    \
+                                              16 * q + 8 * (lane >> 5)]);
+    // one stage: K0 its first k, B its LDS buffer, AFC/BFC its sign and
+    // activation fragments, AFN/BFN the next stage's, AWU the next stage's
+    // sign words, AWL the register set for stage i + 2's
+#define G32_STAGE(K0, B, AFC, AFN, BFC, BFN, AWU, AWL)                                          \
+    {                                                                                           \
+        _Pragma("unroll") for (int u = 0; u < 2; u++)                                           \
+            *(u32x4_t *)&bs[(B) ^ 1][((tid >> 3) + 64 * u) * G_PITCH + (tid & 7) * 8] = breg[u];\
+        const size_t k2 = (K0) + 2 * G_BK < ke ? (K0) + 2 * G_BK : k_last;                      \
+        AWL = sp[(k2 / G_BK) * 128];                                                            \
+        _Pragma("unroll") for (int u = 0; u < 2; u++) breg[u] = *(const u32x4_t *)(brow[u] + k2);\
+        __builtin_amdgcn_sched_barrier(0);                                                      \
+        __syncthreads();                                                                        \
+        __builtin_amdgcn_sched_barrier(0);                                                      \
+        G32_READ_FRAGS((B) ^ 1, BFN)                                                            \
+        __builtin_amdgcn_sched_barrier(0);                                                      \
+        _Pragma("unroll") for (int q = 0; q < 4; q++) {                                         \
+            AFN[q][0] = g32_frag(AWU.x, q, m_sign, one);                                        \
+            AFN[q][1] = g32_frag(AWU.y, q, m_sign, one);                                        \
+            _Pragma("unroll") for (int j = 0; j < 2; j++)                                       \
+            _Pragma("unroll") for (int nt = 0; nt < 2; nt++)                                    \
+                acc[j][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AFC[q][j], BFC[q][nt], acc[j][nt], 0, 0, 0);\
+        }                                                                                       \
     }
-    __syncthreads();
-    int buf = 0;
-    for (size_t k0 = kb; k0 < ke; k0 += G_BK) {
-        const bool more = k0 + G_BK < ke;
-        uint4 an = make_uint4(0, 0, 0, 0);
-        if (more) {
-            load_b(k0 + G_BK);
-            an = sp[((k0 + G_BK) / G_BK) * 64];
-        }
-        const uint32_t wv[4] = {aw.x, aw.y, aw.z, aw.w};
+    if (kb < ke) {
+        const size_t k1 = kb + G_BK < ke ? kb + G_BK : k_last;
+#pragma unroll
+        for (int u = 0; u < 2; u++) breg[u] = *(const u32x4_t *)(brow[u] + kb);
+        const uint2 aw0 = sp[(kb / G_BK) * 128];
+        awB = sp[(k1 / G_BK) * 128];
+#pragma unroll
+        for (int u = 0; u < 2; u++) *(u32x4_t *)&bs[0][((tid >> 3) + 64 * u) * G_PITCH + (tid & 7) * 8] = breg[u];
+#pragma unroll
+        for (int u = 0; u < 2; u++) breg[u] = *(const u32x4_t *)(brow[u] + k1);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            bf16x8_t bf[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                const int nn = wn * 64 + nt * 32 + (lane & 31);
-                const uint4 bv = *(const uint4 *)&bs[buf][nn * G_PITCH + 16 * q + 8 * (lane >> 5)];
-                bf[nt] = __builtin_bit_cast(bf16x8_t, bv);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const bf16x8_t af = g32_frag(wv[j], q);
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-                    acc[j][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[nt], acc[j][nt], 0, 0, 0);
-            }
+            afA[q][0] = g32_frag(aw0.x, q, m_sign, one);
+            afA[q][1] = g32_frag(aw0.y, q, m_sign, one);
         }
-        if (more) {
-            store_b(buf ^ 1);
-            aw = an;
-        }
-        __syncthreads();
-        buf ^= 1;
     }
+    __syncthreads();
+    G32_READ_FRAGS(0, bfA)
+    size_t k0 = kb;
+    for (; k0 + G_BK < ke; k0 += 2 * G_BK) {
+        G32_STAGE(k0, 0, afA, afB, bfA, bfB, awB, awA)
+        G32_STAGE(k0 + G_BK, 1, afB, afA, bfB, bfA, awA, awB)
+    }
+    if (k0 < ke) G32_STAGE(k0, 0, afA, afB, bfA, bfB, awB, awA)  // an odd stage count's last
+#undef G32_STAGE
+#undef G32_READ_FRAGS
+    __syncthreads();  // the epilogue reuses the tile buffers
     // Epilogue, one 32-token n-tile at a time, through the wave's LDS region
     // T [32 tokens][G_TPITCH] f32 (the tile buffers are free: the loop ended
     // with a barrier): lanes write their accumulators -- acc[j][nt][4h + p]
@@ -183,13 +218,13 @@ __global__ void __launch_bounds__(256) g32_kernel(G32Args a) {
     // pieces of one token's output row.
     float *T = (float *)(g32_lds + wave * (32 * G_TPITCH * 4));
     const bool gvalid = g < ng;
-    const size_t row0 = 128 * g;  // this wave's first row
-    // stage 2: s1 and bias of rows 8c .. 8c + 7 of the wave (c = lane % 16)
+    const size_t row0 = m0 + 64 * wr;  // this wave's first row
+    // stage 2: s1 and bias of rows 8c .. 8c + 7 of the wave (c = lane % 8)
     float s1v[8], biv[8];
     if (STAGE == 2 && gvalid) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const size_t rr = row0 + 8 * (lane & 15) + e;
+            const size_t rr = row0 + 8 * (lane & 7) + e;
             s1v[e] = rr < a.M_valid ? a.s1[rr] : 0.0f;
             biv[e] = rr < a.M_valid ? a.bias[rr] : 0.0f;
         }
@@ -197,29 +232,29 @@ __global__ void __launch_bounds__(256) g32_kernel(G32Args a) {
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int h = 0; h < 4; h++)
                 *(float4 *)&T[(lane & 31) * G_TPITCH + 32 * j + 8 * h + 4 * (lane >> 5)] =
                     make_float4(acc[j][nt][4 * h], acc[j][nt][4 * h + 1], acc[j][nt][4 * h + 2],
                                 acc[j][nt][4 * h + 3]);
         __builtin_amdgcn_wave_barrier();
-        const size_t nb = n0 + wn * 64 + nt * 32;  // first token of the n-tile
+        const size_t nb = n0 + wc * 64 + nt * 32;  // first token of the n-tile
         if (gvalid) {
             if (STAGE == 1 && a.split > 1) {
-                // f32 partials: 32 lanes per token (4 rows each), two tokens per store
+                // f32 partials: 16 lanes per token (4 rows each), four tokens per store
 #pragma unroll 4
-                for (int k = 0; k < 16; k++) {
-                    const int tt = 2 * k + (lane >> 5), c = lane & 31;
+                for (int k = 0; k < 8; k++) {
+                    const int tt = 4 * k + (lane >> 4), c = lane & 15;
                     const size_t n = nb + tt;
                     const float4 v = *(const float4 *)&T[tt * G_TPITCH + 4 * c];
                     if (n < a.N) *(float4 *)(a.part + ((size_t)blockIdx.z * a.N + n) * a.M_p + row0 + 4 * c) = v;
                 }
             } else {
-                // bf16 rows: 16 lanes per token (8 rows each), four tokens per store
+                // bf16 rows: 8 lanes per token (8 rows each), eight tokens per store
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const int tt = 4 * k + (lane >> 4), c = lane & 15;
+                for (int k = 0; k < 4; k++) {
+                    const int tt = 8 * k + (lane >> 3), c = lane & 7;
                     const size_t n = nb + tt;
                     const float4 v0 = *(const float4 *)&T[tt * G_TPITCH + 8 * c];
                     const float4 v1 = *(const float4 *)&T[tt * G_TPITCH + 8 * c + 4];
@@ -231,20 +266,23 @@ __global__ void __launch_bounds__(256) g32_kernel(G32Args a) {
                         uint32_t w[4];
 #pragma unroll
                         for (int p = 0; p < 4; p++) {
-                            const uint32_t lo = rb + 2 * p < a.M_valid ? f32_to_bf16(v[2 * p]) : 0;
-                            const uint32_t hi = rb + 2 * p + 1 < a.M_valid ? f32_to_bf16(v[2 * p + 1]) : 0;
-                            w[p] = lo | (hi << 16);
+                            w[p] = f32x2_to_bf16x2(v[2 * p], v[2 * p + 1]);
+                            if (rb + 2 * p >= a.M_valid) w[p] &= 0xffff0000u;
+                            if (rb + 2 * p + 1 >= a.M_valid) w[p] &= 0x0000ffffu;
                         }
                         *(uint4 *)(a.t_out + n * a.M_p + rb) = make_uint4(w[0], w[1], w[2], w[3]);
                     } else {
                         float y[8];
 #pragma unroll
-                        for (int p = 0; p < 8; p++) y[p] = bf16_to_f32(f32_to_bf16(v[p])) * s1v[p] + biv[p];
+                        for (int p = 0; p < 4; p++) {
+                            const uint32_t u = f32x2_to_bf16x2(v[2 * p], v[2 * p + 1]);
+                            y[2 * p] = __uint_as_float(u << 16) * s1v[2 * p] + biv[2 * p];
+                            y[2 * p + 1] = __uint_as_float(u & 0xffff0000u) * s1v[2 * p + 1] + biv[2 * p + 1];
+                        }
                         if (a.y_bf16 && a.vec_y && rb + 8 <= a.M_valid) {
                             uint32_t w[4];
 #pragma unroll
-                            for (int p = 0; p < 4; p++)
-                                w[p] = (uint32_t)f32_to_bf16(y[2 * p]) | ((uint32_t)f32_to_bf16(y[2 * p + 1]) << 16);
+                            for (int p = 0; p < 4; p++) w[p] = f32x2_to_bf16x2(y[2 * p], y[2 * p + 1]);
                             *(uint4 *)((uint16_t *)a.y + n * a.M_valid + rb) = make_uint4(w[0], w[1], w[2], w[3]);
                         } else {
 #pragma unroll
@@ -305,7 +343,7 @@ __global__ void __launch_bounds__(256) g32_prep_kernel(const void *x, const floa
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; e++)
-        w[e] = (uint32_t)f32_to_bf16(sv[2 * e] * v[2 * e]) | ((uint32_t)f32_to_bf16(sv[2 * e + 1] * v[2 * e + 1]) << 16);
+        w[e] = f32x2_to_bf16x2(sv[2 * e] * v[2 * e], sv[2 * e + 1] * v[2 * e + 1]);
     *(uint4 *)(z + n * K_p + k0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -331,9 +369,9 @@ __global__ void __launch_bounds__(256) g32_reduce_kernel(const float *__restrict
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        const uint32_t lo = k0 + 2 * e < r ? f32_to_bf16(v[2 * e]) : 0;
-        const uint32_t hi = k0 + 2 * e + 1 < r ? f32_to_bf16(v[2 * e + 1]) : 0;
-        w[e] = lo | (hi << 16);
+        w[e] = f32x2_to_bf16x2(v[2 * e], v[2 * e + 1]);
+        if (k0 + 2 * e >= r) w[e] &= 0xffff0000u;
+        if (k0 + 2 * e + 1 >= r) w[e] &= 0x0000ffffu;
     }
     *(uint4 *)(t + e0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
@@ -378,7 +416,7 @@ size_t g32_workspace(const qbk_factor *L, size_t N) { return g32_plan(L, N).byte
 int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
             hipStream_t s) {
     const G32Plan p = g32_plan(L, N);
-    static bool lds_set = false;  // the epilogue's 66 KiB exceed the 64 KiB default
+    static bool lds_set = false;  // the epilogue's 68 KiB exceed the 64 KiB default
     if (!lds_set) {
         QBK_HIP(hipFuncSetAttribute((const void *)g32_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
         QBK_HIP(hipFuncSetAttribute((const void *)g32_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
@@ -410,8 +448,10 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.part = part;
     a.t_out = t;
     a.k_per_split = round_up(div_ceil(L->din_p, p.split), G_BK);
+    a.sign_mask = 0x80008000u;
+    a.one_pair = 0x3F803F80u;
     dim3 g1((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->r_p, G_BM), p.split);
-    hipLaunchKernelGGL((g32_kernel<1>), g1, dim3(256), G_LDS, s, a);
+    hipLaunchKernelGGL((g32_kernel<1>), g1, dim3(512), G_LDS, s, a);
     QBK_HIP(hipGetLastError());
     if (p.split > 1) {
         const size_t chunks = N * L->r_p / 8;
@@ -431,8 +471,10 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     b.bias = L->bias;
     b.y_bf16 = ybf16;
     b.vec_y = L->dout % 8 == 0 && (uintptr_t)y % 16 == 0;
+    b.sign_mask = 0x80008000u;
+    b.one_pair = 0x3F803F80u;
     dim3 g2((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->dout_p, G_BM), 1);
-    hipLaunchKernelGGL((g32_kernel<2>), g2, dim3(256), G_LDS, s, b);
+    hipLaunchKernelGGL((g32_kernel<2>), g2, dim3(512), G_LDS, s, b);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

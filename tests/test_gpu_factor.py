@@ -180,6 +180,33 @@ def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
     assert np.all(np.abs(y - y_or) <= np.abs(L["s1"]) * (uulp * 1.01 + reassoc) + 1e-6 * np.abs(y_or))
 
 
+@pytest.mark.parametrize("din", [200, 203])
+def test_prefill_activation_rounding(ctx, orc, din):
+    """z = bf16(s2 * x) (engine/mod.rs:449-452), the prefill GEMM's first
+    product, is elementwise and so bit-exact for any input: read back from
+    the head of the workspace and compared with the oracle's rounding over
+    ties, overflow to infinity, denormals and NaN payloads (din 203 takes
+    the unaligned path)."""
+    rng = np.random.default_rng(7 + din)
+    batch, dout, r = 16, 64, 32
+    L = make_layer(orc, rng, dout, din, r)
+    # scales that put a tie bit into the product's mantissa, overflow and underflow it
+    picks = np.array([1 + 2.0 ** -8, 1.5 + 2.0 ** -9, 3.0, 2.0 ** 100, 2.0 ** -100, 1.0], np.float32)
+    L["s2"] = np.where(rng.random(din) < 0.5, picks[rng.integers(0, picks.size, din)], L["s2"]).astype(np.float32)
+    xb = rng.integers(0, 1 << 16, (batch, din)).astype(np.uint16)
+    # every bf16 bit pattern class: NaNs with payloads, +-inf, denormals, zeros
+    specials = np.array([0x7F81, 0x7FC0, 0xFFA5, 0x7F80, 0xFF80, 0x0001, 0x807F, 0x0000, 0x8000, 0x7F7F],
+                        np.uint16)
+    xb.ravel()[rng.choice(xb.size, 400, replace=False)] = specials[rng.integers(0, specials.size, 400)]
+    layer = upload(ctx, L)
+    _, ws = run_dev(layer, xb)
+    din_p = -(-din // 64) * 64
+    z = ws[: batch * din_p * 2].view(np.uint16).reshape(batch, din_p)
+    want = orc.f32_to_bf16((L["s2"][None, :] * orc.bf16_to_f32(xb)).astype(np.float32))
+    assert not z[:, din:].any()
+    assert np.array_equal(z[:, :din], want), np.argwhere(z[:, :din] != want)[:5]
+
+
 def set_decode(S, x, dout):
     xd = torch.from_numpy(x.view(np.int16)).cuda()
     yd = torch.empty((x.shape[0], dout), dtype=torch.int16, device="cuda")
