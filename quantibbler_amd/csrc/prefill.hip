@@ -16,8 +16,9 @@
 //   * B (activations): 128 tokens x 64 k staged through LDS, double
 //     buffered, rows padded to 144 bytes (the 32 lanes of a fragment read
 //     rows 144 B apart: conflict-free 16-byte reads);
-//   * stage 1 reads z = bf16(s2 * x) written once by g32_prep_kernel (zero
-//     past din), splits K to fill the chip and writes f32 partials that
+//   * stage 1 forms z = bf16(s2 * x) (zero past din) while staging x through
+//     LDS -- g32_prep_kernel writes it beforehand only for rows that are not
+//     16-byte chunks -- splits K to fill the chip and writes f32 partials that
 //     g32_reduce_kernel sums in split order into t bf16 (zero past r); with
 //     no split the epilogue writes t directly;
 //   * stage 2 reads t and writes y = bf16(u) * s1 + bias, u = bf16(acc).
@@ -69,7 +70,10 @@ void g32_repack(const uint8_t *rows, size_t n_rows, size_t n_bits, size_t rows_p
 struct G32Args {
     const uint32_t *sg;    // g32 layout [M_p/128][K_p/64][64][4]
     size_t M_p, K_p, M_valid, N;
-    const uint16_t *act;   // bf16 [N][K_p] (z or t), zero for k past the valid K
+    const uint16_t *act;   // bf16 [N][K_p] (z or t), zero for k past the valid K (XM 0)
+    const void *x;         // stage 1, XM 1 / 2: x [N][din] bf16 / f32, s2 [din]; din % 8 == 0
+    const float *s2;
+    size_t din;
     // stage 1
     float *part;           // [split][N][M_p] f32 (split > 1)
     uint16_t *t_out;       // [N][M_p] bf16 (split == 1), zero for rows >= M_valid
@@ -95,7 +99,9 @@ __device__ __forceinline__ bf16x8_t g32_frag(uint32_t w, int q, uint32_t m, uint
     return __builtin_bit_cast(bf16x8_t, u);
 }
 
-template <int STAGE>
+// XM: the activation operand -- 0: bf16 rows of K_p (z or t); 1 / 2: stage 1
+// forms z = bf16(s2 * x) itself from bf16 / f32 x while staging it.
+template <int STAGE, int XM>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) g32_kernel(G32Args a) {
     // [2 tile buffers of G_BN x G_PITCH bf16] during the loop; [8 waves][32 x
     // G_TPITCH f32] in the epilogue
@@ -120,18 +126,67 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     uint32_t one;
     asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(a.one_pair));
 
-    // B tile: 128 tokens x 64 k = 1024 chunks of 8 bf16, two per thread
+    // B tile: 128 tokens x 64 k = 1024 chunks of 8 elements, two per thread
     // (tokens tid/8 + 64u, k chunk tid%8).  Every load is issued
     // unconditionally -- tokens past N are clamped to N - 1 and only feed
-    // output columns the epilogue does not store -- so that the wait for the
-    // prefetch can be a counted one at the LDS store.
-    const uint16_t *brow[2];
+    // output columns the epilogue does not store; with XM, chunks past din
+    // read chunk 0 and store zeros -- so that the wait for the prefetch can
+    // be a counted one at the LDS store.
+    const size_t kc = (tid & 7) * 8, ld = XM ? a.din : a.K_p;
+    const char *brow[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const size_t n = n0 + (tid >> 3) + 64 * u;
-        brow[u] = a.act + (n < a.N ? n : a.N - 1) * a.K_p + (tid & 7) * 8;
+        const size_t off = (n < a.N ? n : a.N - 1) * ld + kc;
+        brow[u] = XM == 2 ? (const char *)((const float *)a.x + off)
+                          : (const char *)((XM ? (const uint16_t *)a.x : a.act) + off);
     }
-    u32x4_t breg[2];
+    constexpr int NB = XM == 2 ? 4 : 2;  // staged 16-byte pieces per thread
+    u32x4_t breg[NB];
+    float4 s2r[2];                       // XM: s2 of the staged chunk
+    bool bval = true;                    // XM: the staged chunk lies below din
+#define G32_LOAD_ACT(K)                                                                         \
+    {                                                                                           \
+        size_t ko = (K);                                                                        \
+        if (XM) {                                                                               \
+            bval = ko + kc < a.din;                                                             \
+            ko = bval ? ko : 0;                                                                 \
+            s2r[0] = *(const float4 *)(a.s2 + ko + kc);                                         \
+            s2r[1] = *(const float4 *)(a.s2 + ko + kc + 4);                                     \
+        }                                                                                       \
+        _Pragma("unroll") for (int u = 0; u < 2; u++) {                                         \
+            if (XM == 2) {                                                                      \
+                breg[2 * u] = *(const u32x4_t *)((const float *)brow[u] + ko);                  \
+                breg[2 * u + 1] = *(const u32x4_t *)((const float *)brow[u] + ko + 4);          \
+            } else {                                                                            \
+                breg[u] = *(const u32x4_t *)((const uint16_t *)brow[u] + ko);                   \
+            }                                                                                   \
+        }                                                                                       \
+    }
+    // XM: z = bf16(s2 * x) of the staged chunk, formed as it is stored
+#define G32_STORE_ACT(B)                                                                        \
+    _Pragma("unroll") for (int u = 0; u < 2; u++) {                                             \
+        u32x4_t zv;                                                                             \
+        if (XM == 0) {                                                                          \
+            zv = breg[u];                                                                       \
+        } else {                                                                                \
+            const float sv[8] = {s2r[0].x, s2r[0].y, s2r[0].z, s2r[0].w,                        \
+                                 s2r[1].x, s2r[1].y, s2r[1].z, s2r[1].w};                       \
+            float xv[8];                                                                        \
+            _Pragma("unroll") for (int e = 0; e < 4; e++) {                                     \
+                if (XM == 2) {                                                                  \
+                    xv[2 * e] = __uint_as_float(breg[2 * u + (e >> 1)][2 * (e & 1)]);          \
+                    xv[2 * e + 1] = __uint_as_float(breg[2 * u + (e >> 1)][2 * (e & 1) + 1]);  \
+                } else {                                                                        \
+                    xv[2 * e] = __uint_as_float(breg[u][e] << 16);                             \
+                    xv[2 * e + 1] = __uint_as_float(breg[u][e] & 0xffff0000u);                 \
+                }                                                                               \
+            }                                                                                   \
+            _Pragma("unroll") for (int e = 0; e < 4; e++)                                       \
+                zv[e] = bval ? f32x2_to_bf16x2(sv[2 * e] * xv[2 * e], sv[2 * e + 1] * xv[2 * e + 1]) : 0u;\
+        }                                                                                       \
+        *(u32x4_t *)&bs[B][((tid >> 3) + 64 * u) * G_PITCH + kc] = zv;                          \
+    }
 
     f32x16_t acc[2][2];
 #pragma unroll
@@ -165,11 +220,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     // sign words, AWL the register set for stage i + 2's
 #define G32_STAGE(K0, B, AFC, AFN, BFC, BFN, AWU, AWL)                                          \
     {                                                                                           \
-        _Pragma("unroll") for (int u = 0; u < 2; u++)                                           \
-            *(u32x4_t *)&bs[(B) ^ 1][((tid >> 3) + 64 * u) * G_PITCH + (tid & 7) * 8] = breg[u];\
+        G32_STORE_ACT((B) ^ 1)                                                                  \
         const size_t k2 = (K0) + 2 * G_BK < ke ? (K0) + 2 * G_BK : k_last;                      \
         AWL = sp[(k2 / G_BK) * 128];                                                            \
-        _Pragma("unroll") for (int u = 0; u < 2; u++) breg[u] = *(const u32x4_t *)(brow[u] + k2);\
+        G32_LOAD_ACT(k2)                                                                        \
         __builtin_amdgcn_sched_barrier(0);                                                      \
         __syncthreads();                                                                        \
         __builtin_amdgcn_sched_barrier(0);                                                      \
@@ -185,14 +239,11 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
     if (kb < ke) {
         const size_t k1 = kb + G_BK < ke ? kb + G_BK : k_last;
-#pragma unroll
-        for (int u = 0; u < 2; u++) breg[u] = *(const u32x4_t *)(brow[u] + kb);
+        G32_LOAD_ACT(kb)
         const uint2 aw0 = sp[(kb / G_BK) * 128];
         awB = sp[(k1 / G_BK) * 128];
-#pragma unroll
-        for (int u = 0; u < 2; u++) *(u32x4_t *)&bs[0][((tid >> 3) + 64 * u) * G_PITCH + (tid & 7) * 8] = breg[u];
-#pragma unroll
-        for (int u = 0; u < 2; u++) breg[u] = *(const u32x4_t *)(brow[u] + k1);
+        G32_STORE_ACT(0)
+        G32_LOAD_ACT(k1)
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             afA[q][0] = g32_frag(aw0.x, q, m_sign, one);
@@ -209,6 +260,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     if (k0 < ke) G32_STAGE(k0, 0, afA, afB, bfA, bfB, awB, awA)  // an odd stage count's last
 #undef G32_STAGE
 #undef G32_READ_FRAGS
+#undef G32_STORE_ACT
+#undef G32_LOAD_ACT
     __syncthreads();  // the epilogue reuses the tile buffers
     // Epilogue, one 32-token n-tile at a time, through the wave's LDS region
     // T [32 tokens][G_TPITCH] f32 (the tile buffers are free: the loop ended
@@ -302,48 +355,27 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
 }
 
-// z[n][k] = bf16(s2[k] * x[n][k]) for k < din, 0 for din <= k < K_p; eight
-// elements per thread.
+// z[n][k] = bf16(s2[k] * x[n][k]) for k < din, 0 for din <= k < K_p, eight
+// elements per thread: the staging for inputs whose rows stage 1 cannot
+// read in 16-byte chunks (din % 8 != 0 or x unaligned).
 template <bool XF32>
 __global__ void __launch_bounds__(256) g32_prep_kernel(const void *x, const float *s2, size_t din,
-                                                        size_t K_p, size_t N, uint16_t *z, int vec_ok) {
+                                                        size_t K_p, size_t N, uint16_t *z) {
     const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t per_row = K_p / 8;
     if (c >= N * per_row) return;
     const size_t n = c / per_row, k0 = (c % per_row) * 8;
     float v[8], sv[8];
-    if (vec_ok && k0 + 8 <= din) {
-        if (XF32) {
-            const float4 *xp = (const float4 *)((const float *)x + n * din + k0);
-            const float4 a0 = xp[0], a1 = xp[1];
-            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-        } else {
-            const uint4 xb = *(const uint4 *)((const uint16_t *)x + n * din + k0);
-            const uint32_t w[4] = {xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                v[2 * e] = bf16_to_f32(w[e] & 0xffff);
-                v[2 * e + 1] = bf16_to_f32(w[e] >> 16);
-            }
-        }
-        const float4 *sp = (const float4 *)(s2 + k0);
-        const float4 b0 = sp[0], b1 = sp[1];
-        sv[0] = b0.x; sv[1] = b0.y; sv[2] = b0.z; sv[3] = b0.w;
-        sv[4] = b1.x; sv[5] = b1.y; sv[6] = b1.z; sv[7] = b1.w;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const size_t k = k0 + e;
-            const bool ok = k < din;
-            v[e] = !ok ? 0.0f : XF32 ? ((const float *)x)[n * din + k] : bf16_to_f32(((const uint16_t *)x)[n * din + k]);
-            sv[e] = ok ? s2[k] : 0.0f;
-        }
+    for (int e = 0; e < 8; e++) {
+        const size_t k = k0 + e;
+        const bool ok = k < din;
+        v[e] = !ok ? 0.0f : XF32 ? ((const float *)x)[n * din + k] : bf16_to_f32(((const uint16_t *)x)[n * din + k]);
+        sv[e] = ok ? s2[k] : 0.0f;
     }
     uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-        w[e] = f32x2_to_bf16x2(sv[2 * e] * v[2 * e], sv[2 * e + 1] * v[2 * e + 1]);
+    for (int e = 0; e < 4; e++) w[e] = f32x2_to_bf16x2(sv[2 * e] * v[2 * e], sv[2 * e + 1] * v[2 * e + 1]);
     *(uint4 *)(z + n * K_p + k0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -389,7 +421,8 @@ static int g32_split(const qbk_factor *L, size_t N) {
     return s;
 }
 
-// Workspace: z bf16 [N][din_p] | partials f32 [split][N][r_p] | t bf16 [N][r_p].
+// Workspace: z bf16 [N][din_p] (written only when stage 1 cannot form z from x
+// itself) | partials f32 [split][N][r_p] | t bf16 [N][r_p].
 struct G32Plan {
     int split;
     size_t o_z, o_part, o_t, bytes;
@@ -418,23 +451,26 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     const G32Plan p = g32_plan(L, N);
     static bool lds_set = false;  // the epilogue's 68 KiB exceed the 64 KiB default
     if (!lds_set) {
-        QBK_HIP(hipFuncSetAttribute((const void *)g32_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
-        QBK_HIP(hipFuncSetAttribute((const void *)g32_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
+        for (const void *k : {(const void *)g32_kernel<1, 0>, (const void *)g32_kernel<1, 1>,
+                              (const void *)g32_kernel<1, 2>, (const void *)g32_kernel<2, 0>})
+            QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
         lds_set = true;
     }
     char *w = (char *)ws;
     uint16_t *z = (uint16_t *)(w + p.o_z), *t = (uint16_t *)(w + p.o_t);
     float *part = (float *)(w + p.o_part);
-    {
+    // Stage 1 forms z itself from 16-byte chunks of x when they line up
+    // (din % 8 == 0, x aligned); otherwise g32_prep_kernel stages z first.
+    const bool fused = L->din % 8 == 0 && (uintptr_t)x % 16 == 0;
+    if (!fused) {
         const size_t chunks = N * L->din_p / 8;
-        const int vec_ok = L->din % 8 == 0 && (uintptr_t)x % 16 == 0;
         dim3 g((unsigned)div_ceil(chunks, 256));
         if (xf32)
             hipLaunchKernelGGL((g32_prep_kernel<true>), g, dim3(256), 0, s, x, (const float *)L->s2, L->din,
-                               L->din_p, N, z, vec_ok);
+                               L->din_p, N, z);
         else
             hipLaunchKernelGGL((g32_prep_kernel<false>), g, dim3(256), 0, s, x, (const float *)L->s2, L->din,
-                               L->din_p, N, z, vec_ok);
+                               L->din_p, N, z);
         QBK_HIP(hipGetLastError());
     }
     G32Args a{};
@@ -444,6 +480,9 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.M_valid = L->r;
     a.N = N;
     a.act = z;
+    a.x = x;
+    a.s2 = L->s2;
+    a.din = L->din;
     a.split = p.split;
     a.part = part;
     a.t_out = t;
@@ -451,7 +490,12 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.sign_mask = 0x80008000u;
     a.one_pair = 0x3F803F80u;
     dim3 g1((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->r_p, G_BM), p.split);
-    hipLaunchKernelGGL((g32_kernel<1>), g1, dim3(512), G_LDS, s, a);
+    if (!fused)
+        hipLaunchKernelGGL((g32_kernel<1, 0>), g1, dim3(512), G_LDS, s, a);
+    else if (xf32)
+        hipLaunchKernelGGL((g32_kernel<1, 2>), g1, dim3(512), G_LDS, s, a);
+    else
+        hipLaunchKernelGGL((g32_kernel<1, 1>), g1, dim3(512), G_LDS, s, a);
     QBK_HIP(hipGetLastError());
     if (p.split > 1) {
         const size_t chunks = N * L->r_p / 8;
@@ -474,7 +518,7 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     b.sign_mask = 0x80008000u;
     b.one_pair = 0x3F803F80u;
     dim3 g2((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->dout_p, G_BM), 1);
-    hipLaunchKernelGGL((g32_kernel<2>), g2, dim3(512), G_LDS, s, b);
+    hipLaunchKernelGGL((g32_kernel<2, 0>), g2, dim3(512), G_LDS, s, b);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

@@ -180,19 +180,22 @@ def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
     assert np.all(np.abs(y - y_or) <= np.abs(L["s1"]) * (uulp * 1.01 + reassoc) + 1e-6 * np.abs(y_or))
 
 
-@pytest.mark.parametrize("din", [200, 203])
-def test_prefill_activation_rounding(ctx, orc, din):
-    """z = bf16(s2 * x) (engine/mod.rs:449-452), the prefill GEMM's first
-    product, is elementwise and so bit-exact for any input: read back from
-    the head of the workspace and compared with the oracle's rounding over
-    ties, overflow to infinity, denormals and NaN payloads (din 203 takes
-    the unaligned path)."""
-    rng = np.random.default_rng(7 + din)
-    batch, dout, r = 16, 64, 32
-    L = make_layer(orc, rng, dout, din, r)
+def _rounding_layer(orc, rng, din):
+    L = make_layer(orc, rng, 64, din, 32)
     # scales that put a tie bit into the product's mantissa, overflow and underflow it
     picks = np.array([1 + 2.0 ** -8, 1.5 + 2.0 ** -9, 3.0, 2.0 ** 100, 2.0 ** -100, 1.0], np.float32)
     L["s2"] = np.where(rng.random(din) < 0.5, picks[rng.integers(0, picks.size, din)], L["s2"]).astype(np.float32)
+    return L
+
+
+def test_prefill_activation_rounding_staged(ctx, orc):
+    """z = bf16(s2 * x) (engine/mod.rs:449-452), the prefill GEMM's first
+    product, for rows that are not 16-byte chunks (din 203): staged whole at
+    the head of the workspace and compared bit for bit with the oracle's
+    rounding over ties, overflow to infinity, denormals and NaN payloads."""
+    rng = np.random.default_rng(210)
+    batch, din = 16, 203
+    L = _rounding_layer(orc, rng, din)
     xb = rng.integers(0, 1 << 16, (batch, din)).astype(np.uint16)
     # every bf16 bit pattern class: NaNs with payloads, +-inf, denormals, zeros
     specials = np.array([0x7F81, 0x7FC0, 0xFFA5, 0x7F80, 0xFF80, 0x0001, 0x807F, 0x0000, 0x8000, 0x7F7F],
@@ -205,6 +208,51 @@ def test_prefill_activation_rounding(ctx, orc, din):
     want = orc.f32_to_bf16((L["s2"][None, :] * orc.bf16_to_f32(xb)).astype(np.float32))
     assert not z[:, din:].any()
     assert np.array_equal(z[:, :din], want), np.argwhere(z[:, :din] != want)[:5]
+
+
+def _one_hot(orc, rng, L, batch, din, finite):
+    """x with one nonzero element per token, so that every sum of the two
+    stages is exact: t = +-z of that element, u = (integer) * z.  Values are
+    kept where z is a nonzero normal (or +-inf unless finite): the MFMA's NaN
+    sign and denormal inputs are not IEEE-specified."""
+    cols = rng.integers(0, din, batch)
+    vals = np.zeros(batch, np.float32)
+    for n in range(batch):
+        while True:
+            v = np.float32(rng.choice([-1, 1]) * 2.0 ** rng.uniform(-60, 60) * rng.uniform(1, 2))
+            if not finite and rng.random() < 0.2:
+                v = np.float32(rng.choice([-1, 1]) * 3.0e38)
+            zf = orc.bf16_to_f32(orc.f32_to_bf16(np.float32(L["s2"][cols[n]] * orc.bf16_to_f32(orc.f32_to_bf16(v)))))
+            if (np.isinf(zf) and not finite) or (np.isfinite(zf) and abs(zf) >= 2.0 ** -126):
+                vals[n] = v
+                break
+    x = np.zeros((batch, din), np.float32)
+    x[np.arange(batch), cols] = vals
+    return x, cols
+
+
+def test_prefill_activation_rounding_fused(ctx, orc):
+    """The same product formed inside the GEMM's activation staging (din % 8
+    == 0): bf16 x through the device entry point, where t read back from the
+    workspace must be exactly +-z, ties and overflow included; f32 x through
+    the host face, where y must be bit-identical to the oracle's."""
+    rng = np.random.default_rng(200)
+    batch, din = 16, 200
+    L = _rounding_layer(orc, rng, din)
+    layer = upload(ctx, L)
+    x, cols = _one_hot(orc, rng, L, batch, din, finite=False)
+    xb = orc.f32_to_bf16(x)
+    _, ws = run_dev(layer, xb)
+    t = gpu_t(layer, ws, batch)
+    z = orc.f32_to_bf16((L["s2"][cols] * orc.bf16_to_f32(xb[np.arange(batch), cols])).astype(np.float32))
+    want = z[:, None] ^ np.where(L["vts"][:, cols].T < 0, np.uint16(0x8000), np.uint16(0))
+    assert np.array_equal(t, want.astype(np.uint16)), np.argwhere(t != want)[:5]
+    # f32 x (the host face uploads it aligned): staged as f32, y exact
+    x, _ = _one_hot(orc, rng, L, batch, din, finite=True)
+    got = layer.apply(x, "bfloat16")
+    want_y = np.stack([orc.factor_apply("bf16", L["dout"], din, L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                        L["bias"], x[i]) for i in range(batch)])
+    same(got, want_y)
 
 
 def set_decode(S, x, dout):
