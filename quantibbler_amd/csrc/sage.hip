@@ -20,7 +20,8 @@
 //    ignores, so nothing is added back), INT8 Q and K with one scale per
 //    64-token block per head, S^T = K^.Q^T on INT8 MFMA (16x16x64), base-2
 //    online softmax in f32 (log2 e folded into the block scale), P and V in
-//    fp16, O^T += V^T.P^T on fp16 MFMA (16x16x32) with P kept in registers.
+//    fp16, O^T += V^T.P^T on fp16 MFMA (16x16x32) with P kept in registers
+//    and the softmax row sums l = sum of the fp16 P on the same MFMA.
 #include <math.h>
 #include <string.h>
 
@@ -474,13 +475,13 @@ static int run_ref(const qbk_attn_shape *s, const float *q, const float *k, cons
 #define BQ 128   // query rows per workgroup (4 waves x 32)
 #define HD 128   // head_dim == val_dim
 #define LOG2E_F 1.44269504088896341f
-#define KS_PITCH 144  // bytes per K^ row in LDS (128 + 16 pad)
-#define VS_PITCH 72   // fp16 per V^T row in LDS (64 + 8 pad)
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct BlkArgs {
     const uint16_t *q, *k, *v;  // bf16
@@ -492,269 +493,396 @@ struct BlkArgs {
     float *kmean;     // [B*Hk][HD]
     int8_t *khat;     // [B*Hk][Sp][HD]
     float *kscale;    // [B*Hk][nblk]
-    int8_t *qhat;     // [B*H][Sp][HD]
-    float *qscale;    // [B*H][nblk]
-    uint16_t *vt;     // [B*Hk][nblk][HD][BLK] fp16 (V^T per key block)
+    uint16_t *vt;     // [B*Hk][nblk][HD][BLK] fp16, V^T per key block, keys in PV order
+    int8_t *qhat_out; // quantize-only launch: Q codes [B*H][S][HD] and scales [B*H][nblk]
+    float *qscale_out;
+    int hpx;          // heads per XCD of the XCD-aware tile order (0: plain order)
 };
 
-// chunk partial sums of K per channel, token order within the chunk
-__global__ void __launch_bounds__(HD) blk_kpart(BlkArgs a) {
-    const size_t blk = blockIdx.x, bk = blockIdx.y, c = threadIdx.x;
-    const uint16_t *K = a.k + bk * a.S * HD;
-    size_t t0 = blk * BLK, t1 = t0 + BLK < a.S ? t0 + BLK : a.S;
-    float part = 0.0f;
-    for (size_t t = t0; t < t1; t++) part += bf16_to_f32(K[t * HD + c]);
-    a.kpart[(bk * a.nblk + blk) * HD + c] = part;
+// Key order of a V^T block: within each 32-key chunk, position 8g + e holds
+// key 4g + (e & 3) + 16 (e >> 2) -- the keys lane group g of an S^T 16x16
+// C tile pair holds, in the order that lane feeds them to the P.V MFMA as
+// its 8 fp16 B elements.  So every V^T fragment is one 16-byte read.
+__host__ __device__ __forceinline__ int vt_key(int pos) {
+    const int kc = pos >> 5, g = (pos >> 3) & 3, e = pos & 7;
+    return 32 * kc + 4 * g + (e & 3) + 16 * (e >> 2);
 }
 
-__device__ __forceinline__ float block_max(float v, float *red) {
+// chunk partial sums of K per channel, token order within the chunk: one
+// workgroup per (block, kv head), two channels per thread
+__global__ void __launch_bounds__(64) blk_kpart(BlkArgs a) {
+    const size_t blk = blockIdx.x, bk = blockIdx.y;
+    const int c = 2 * threadIdx.x;
+    const uint32_t *K = (const uint32_t *)(a.k + bk * a.S * HD + c);
+    const size_t t0 = blk * BLK, t1 = t0 + BLK < a.S ? t0 + BLK : a.S;
+    float p0 = 0.0f, p1 = 0.0f;
+    size_t t = t0;
+    for (; t + 8 <= t1; t += 8) {
+        uint32_t w[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) w[u] = K[(t + u) * (HD / 2)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            p0 += __uint_as_float(w[u] << 16);
+            p1 += __uint_as_float(w[u] & 0xffff0000u);
+        }
+    }
+    for (; t < t1; t++) {
+        const uint32_t w = K[t * (HD / 2)];
+        p0 += __uint_as_float(w << 16);
+        p1 += __uint_as_float(w & 0xffff0000u);
+    }
+    *(float2 *)&a.kpart[(bk * a.nblk + blk) * HD + c] = make_float2(p0, p1);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float r = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++) r = fmaxf(r, red[w]);
-    __syncthreads();
-    return r;
+    return v;
 }
 
 // K: mean (chunk partials summed in chunk order), smoothing, block scale,
-// codes; V: bf16 -> fp16, transposed per key block.  One workgroup per
-// (kv head, block).
+// codes; V: bf16 -> fp16, transposed per key block into PV order.  One
+// workgroup per (block, kv head); thread t holds token t/4, channels
+// 32 (t%4) .. +31.
 __global__ void __launch_bounds__(256) blk_kvquant(BlkArgs a) {
     __shared__ float mean[HD];
     __shared__ float red[4];
+    __shared__ uint16_t vs[BLK][HD + 2];  // fp16 V, token-major
     const size_t blk = blockIdx.x, bk = blockIdx.y;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < HD) {
         float tot = 0.0f;
         for (size_t p = 0; p < a.nblk; p++) tot += a.kpart[(bk * a.nblk + p) * HD + tid];
-        float mv = tot / (float)a.S;
+        const float mv = tot / (float)a.S;
         mean[tid] = mv;
         if (blk == 0) a.kmean[bk * HD + tid] = mv;
     }
     __syncthreads();
     const size_t t0 = blk * BLK;
-    const uint16_t *K = a.k + bk * a.S * HD;
-    // 64 tokens x 128 channels = 8192 elements, 32 per thread
+    const int tt = tid >> 2, c0 = 32 * (tid & 3);
+    const bool live = t0 + tt < a.S;
+    float g[32];
     float peak = 0.0f;
-    for (int e = tid; e < BLK * HD; e += 256) {
-        size_t t = t0 + e / HD;
-        int c = e % HD;
-        if (t < a.S) peak = fmaxf(peak, fabsf(bf16_to_f32(K[t * HD + c]) - mean[c]));
+    {
+        const u32x4_t *src = (const u32x4_t *)(a.k + (bk * a.S + t0 + tt) * HD + c0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const u32x4_t w = live ? src[u] : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                g[8 * u + 2 * e] = __uint_as_float(w[e] << 16) - mean[c0 + 8 * u + 2 * e];
+                g[8 * u + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u) - mean[c0 + 8 * u + 2 * e + 1];
+            }
+        }
+        if (live)
+#pragma unroll
+            for (int e = 0; e < 32; e++) peak = fmaxf(peak, fabsf(g[e]));
     }
-    peak = block_max(peak, red);
+    peak = wave_max(peak);
+    if (lane == 0) red[wave] = peak;
+    // V: fp16, token-major into LDS
+    {
+        const u32x4_t *src = (const u32x4_t *)(a.v + (bk * a.S + t0 + tt) * HD + c0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const u32x4_t w = live ? src[u] : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const f32x2_t f = {__uint_as_float(w[e] << 16), __uint_as_float(w[e] & 0xffff0000u)};
+                *(uint32_t *)&vs[tt][c0 + 8 * u + 2 * e] =
+                    __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2_t));
+            }
+        }
+    }
+    __syncthreads();
+    peak = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float inv = peak > 0.0f ? 127.0f / peak : 0.0f;
     if (tid == 0) a.kscale[bk * a.nblk + blk] = peak > 0.0f ? peak / 127.0f : 1.0f;
-    int8_t *KH = a.khat + (bk * a.Sp + t0) * HD;
-    for (int e4 = tid; e4 < BLK * HD / 4; e4 += 256) {
-        int e = e4 * 4;
-        size_t t = t0 + e / HD;
-        int c = e % HD;
-        int c4[4] = {0, 0, 0, 0};
-        if (t < a.S)
-            for (int u = 0; u < 4; u++) c4[u] = q8((bf16_to_f32(K[t * HD + c + u]) - mean[c + u]) * inv);
-        *(uint32_t *)(KH + e) = pack4(c4[0], c4[1], c4[2], c4[3]);
+    {
+        uint32_t w[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            w[u] = live ? pack4(q8(g[4 * u] * inv), q8(g[4 * u + 1] * inv), q8(g[4 * u + 2] * inv),
+                                q8(g[4 * u + 3] * inv))
+                        : 0u;
+        u32x4_t *dst = (u32x4_t *)(a.khat + (bk * a.Sp + t0 + tt) * HD + c0);
+        dst[0] = u32x4_t{w[0], w[1], w[2], w[3]};
+        dst[1] = u32x4_t{w[4], w[5], w[6], w[7]};
     }
-    // V^T block: vt[c][j] for j < 64 (zero beyond S)
-    const uint16_t *V = a.v + bk * a.S * HD;
-    uint16_t *VT = a.vt + (bk * a.nblk + blk) * HD * BLK;
-    for (int e = tid; e < BLK * HD; e += 256) {
-        int c = e / BLK, j = e % BLK;
-        size_t t = t0 + j;
-        _Float16 h = (_Float16)(t < a.S ? bf16_to_f32(V[t * HD + c]) : 0.0f);
-        VT[c * BLK + j] = __builtin_bit_cast(uint16_t, h);
-    }
-}
-
-// Q: 1/sqrt(d) folded, block scale, codes.  One workgroup per (head, block).
-__global__ void __launch_bounds__(256) blk_qquant(BlkArgs a) {
-    __shared__ float red[4];
-    const size_t blk = blockIdx.x, bh = blockIdx.y;
-    const int tid = threadIdx.x;
-    const size_t t0 = blk * BLK;
-    const uint16_t *Q = a.q + bh * a.S * HD;
-    float peak = 0.0f;
-    for (int e = tid; e < BLK * HD; e += 256) {
-        size_t t = t0 + e / HD;
-        if (t < a.S) peak = fmaxf(peak, fabsf(bf16_to_f32(Q[t * HD + e % HD]) * a.inv_sqrt_d));
-    }
-    peak = block_max(peak, red);
-    const float inv = peak > 0.0f ? 127.0f / peak : 0.0f;
-    if (tid == 0) a.qscale[bh * a.nblk + blk] = peak > 0.0f ? peak / 127.0f : 1.0f;
-    int8_t *QH = a.qhat + (bh * a.Sp + t0) * HD;
-    for (int e4 = tid; e4 < BLK * HD / 4; e4 += 256) {
-        int e = e4 * 4;
-        size_t t = t0 + e / HD;
-        int c = e % HD;
-        int c4[4] = {0, 0, 0, 0};
-        if (t < a.S)
-            for (int u = 0; u < 4; u++) c4[u] = q8((bf16_to_f32(Q[t * HD + c + u]) * a.inv_sqrt_d) * inv);
-        *(uint32_t *)(QH + e) = pack4(c4[0], c4[1], c4[2], c4[3]);
+    // V^T [HD][BLK] in PV key order: 1024 16-byte pieces (channel d, 8 positions), four per thread
+    u32x4_t *VT = (u32x4_t *)(a.vt + (bk * a.nblk + blk) * HD * BLK);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = tid + 256 * u, d = x >> 3, p0 = (x & 7) * 8;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            w[e] = (uint32_t)vs[vt_key(p0 + 2 * e)][d] | ((uint32_t)vs[vt_key(p0 + 2 * e + 1)][d] << 16);
+        VT[x] = u32x4_t{w[0], w[1], w[2], w[3]};
     }
 }
 
 #pragma clang fp contract(fast)
 
+// LDS tile of one key block: K^ [64 keys][128 B] then V^T [128 d][128 B];
+// each 128-byte row keeps its eight 16-byte chunks XOR-swizzled by the row
+// (chunk c at c ^ (row & 7)), so that the eight lanes of a 16-byte-read
+// phase -- eight consecutive rows, one chunk -- hit disjoint banks.
+#define TILE_BYTES (BLK * 128 + HD * 128)
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+
 // Main pass.  Workgroup: (128-query tile, batch*head); wave w owns queries
-// q0 + 32w .. +31 (two 16-query MFMA tiles, one quantisation block).
-// Per key block (64 keys, double-buffered in LDS: K^ 8 KB, V^T 16 KB):
-//   S^T[64 x 32] = K^[64 x 128] . Q^T  -- 4 key tiles x 2 query tiles x 2
-//                  d-chunks of i8 16x16x64; C lane l holds query l%16 and
-//                  keys 4*(l/16)+i of its key tile;
-//   online softmax per query column (4 lanes share a query: xor 16, 32);
-//   O^T[128 x 32] += V^T[128 x 64] . P^T -- 8 channel tiles x 2 query tiles
-//                  x 2 key chunks of f16 16x16x32, P^T taken straight from
-//                  the S^T registers: fragment element e of lane l is key
-//                  4*(l/16)+e of key tile 2c (e<4) or 16 + 4*(l/16)+(e-4)
-//                  of key tile 2c+1, and V^T is read with the same map.
-__global__ void __launch_bounds__(256) blk_attn(BlkArgs a) {
-    // LDS rows padded to 144 bytes: the 16 lanes of a fragment read rows
-    // 144 B apart, which lands them on disjoint bank groups.
-    __shared__ __attribute__((aligned(16))) int8_t ks[2][BLK * KS_PITCH];
-    __shared__ __attribute__((aligned(16))) uint16_t vs[2][HD * VS_PITCH];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const size_t bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-    const size_t bk = b * a.Hk + h / (a.H / a.Hk);
-    const size_t q0 = (size_t)blockIdx.x * BQ;
-    const size_t qw = q0 + 32 * wave;
+// qw = q0 + 32w .. +31 (two 16-query MFMA tiles, one quantisation block of
+// two waves).  Prologue: Q codes of the tile, block scale over the wave
+// pair.  Per key block (64 keys, double-buffered in LDS, loads for the next
+// block issued unconditionally -- the last one reloaded -- ahead of the
+// math):
+//   S^T[64 x 32] = K^[64 x 128] . Q^T  -- i8 16x16x64, 4 key tiles x 2 query
+//                  tiles x 2 d-chunks; C lane l holds query l%16, keys
+//                  4(l/16) + i of its key tile;
+//   online softmax per query column on the integer scores: block max by
+//   v_max3 (the scale is positive), one cvt + fma + exp2 per score, O and l
+//   rescaled only when a lane's max moved;
+//   O^T[128 x 32] += V^T . P^T and l += 1 . P^T -- f16 16x16x32, P^T taken
+//                  straight from the S^T registers (PV key order above), the
+//                  row sums from a ninth tile of ones.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) blk_attn(BlkArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t tl[2][TILE_BYTES];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, col = lane & 15;
-
-    // Q^ fragments (B operand): query col, 16 consecutive d per lane
-    i32x4_t qf[2][2];
-    for (int qt = 0; qt < 2; qt++)
-        for (int dc = 0; dc < 2; dc++) {
-            size_t qi = qw + 16 * qt + col;
-            const int8_t *src = a.qhat + (bh * a.Sp + qi) * HD + dc * 64 + 16 * g;
-            qf[qt][dc] = *(const i32x4_t *)src;
+    const size_t nq = (a.S + BQ - 1) / BQ, BH = a.B * a.H;
+    size_t bh, qi;
+    {
+        const size_t L = blockIdx.x;
+        if (a.hpx) {  // XCD x = L % 8 runs heads x*hpx .. +hpx-1, heaviest tiles first
+            const size_t s = L / 8;
+            bh = (L % 8) * a.hpx + s % a.hpx;
+            qi = nq - 1 - s / a.hpx;
+        } else {
+            bh = L % BH;
+            qi = nq - 1 - L / BH;
         }
-    const bool wave_live = qw < a.S;
-    const float qsc = wave_live ? a.qscale[bh * a.nblk + qw / BLK] : 0.0f;
-
-    f32x4_t o[2][8];
-    for (int qt = 0; qt < 2; qt++)
-        for (int ct = 0; ct < 8; ct++) o[qt][ct] = f32x4_t{0, 0, 0, 0};
-    float mrow[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
-    float lrow[2] = {0.0f, 0.0f};  // per-lane partial row sums
-
-    size_t kb_end = a.nblk;
-    if (a.causal) {
-        size_t last = q0 + BQ - 1 < a.S - 1 ? q0 + BQ - 1 : a.S - 1;
-        kb_end = last / BLK + 1;
     }
-    size_t wlast = qw + 31 < a.S - 1 ? qw + 31 : a.S - 1;
-    const size_t wave_kb_end = a.causal ? wlast / BLK + 1 : a.nblk;
+    const size_t b = bh / a.H, h = bh % a.H;
+    const size_t bk = b * a.Hk + h / (a.H / a.Hk);
+    const size_t q0 = qi * BQ, qw = q0 + 32 * wave;
 
-    // Next tile staged in registers: the global loads are issued before the
-    // block's math and written to LDS after it, so their latency overlaps
-    // the MFMA/softmax work.  K^ tile: 512 x 16 B chunks (2 per thread),
-    // V^T tile: 1024 x 16 B chunks (4 per thread).
-    uint4 kreg[2], vreg[4];
-    auto fetch_tile = [&](size_t kb) {
-        const uint4 *ksrc = (const uint4 *)(a.khat + (bk * a.Sp + kb * BLK) * HD);
-        for (int u = 0; u < 2; u++) kreg[u] = ksrc[tid + 256 * u];
-        const uint4 *vsrc = (const uint4 *)(a.vt + (bk * a.nblk + kb) * HD * BLK);
-        for (int u = 0; u < 4; u++) vreg[u] = vsrc[tid + 256 * u];
-    };
-    auto store_tile = [&](int buf) {
-        for (int u = 0; u < 2; u++) {
-            int x = tid + 256 * u;  // row x/8 (128 B = 8 chunks), chunk x%8
-            *(uint4 *)&ks[buf][(x >> 3) * KS_PITCH + (x & 7) * 16] = kreg[u];
+    // ---- Q codes (B operand): query qw + 16 qt + col, d = 64 dc + 16 g + e
+    i32x4_t qf[2][2];
+    float qsc;
+    {
+        float x[2][2][16];
+        float pk = 0.0f;
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            const size_t q = qw + 16 * qt + col;
+            const bool ok = q < a.S;
+#pragma unroll
+            for (int dc = 0; dc < 2; dc++) {
+                const u32x4_t *src = (const u32x4_t *)(a.q + (bh * a.S + (ok ? q : 0)) * HD + 64 * dc + 16 * g);
+                const u32x4_t w0 = ok ? src[0] : u32x4_t{0, 0, 0, 0};
+                const u32x4_t w1 = ok ? src[1] : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[qt][dc][2 * e] = __uint_as_float(w0[e] << 16) * a.inv_sqrt_d;
+                    x[qt][dc][2 * e + 1] = __uint_as_float(w0[e] & 0xffff0000u) * a.inv_sqrt_d;
+                    x[qt][dc][8 + 2 * e] = __uint_as_float(w1[e] << 16) * a.inv_sqrt_d;
+                    x[qt][dc][8 + 2 * e + 1] = __uint_as_float(w1[e] & 0xffff0000u) * a.inv_sqrt_d;
+                }
+#pragma unroll
+                for (int e = 0; e < 16; e++) pk = fmaxf(pk, fabsf(x[qt][dc][e]));
+            }
         }
-        for (int u = 0; u < 4; u++) {
-            int x = tid + 256 * u;  // row x/8 (64 fp16 = 8 chunks), chunk x%8
-            *(uint4 *)&vs[buf][(x >> 3) * VS_PITCH + (x & 7) * 8] = vreg[u];
+        pk = wave_max(pk);
+        if (lane == 0) red[wave] = pk;
+        __syncthreads();
+        const float peak = fmaxf(red[wave & ~1], red[wave | 1]);  // the wave pair's 64-query block
+        const float inv = peak > 0.0f ? 127.0f / peak : 0.0f;
+        qsc = peak > 0.0f ? peak / 127.0f : 1.0f;
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+            for (int dc = 0; dc < 2; dc++)
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+                    qf[qt][dc][w] = (int)pack4(q8(x[qt][dc][4 * w] * inv), q8(x[qt][dc][4 * w + 1] * inv),
+                                               q8(x[qt][dc][4 * w + 2] * inv), q8(x[qt][dc][4 * w + 3] * inv));
+    }
+    if (a.qhat_out) {  // quantize-only launch: export the codes and scales
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            const size_t q = qw + 16 * qt + col;
+            if (q >= a.S) continue;
+#pragma unroll
+            for (int dc = 0; dc < 2; dc++)
+                *(i32x4_t *)(a.qhat_out + (bh * a.S + q) * HD + 64 * dc + 16 * g) = qf[qt][dc];
         }
-    };
+        if ((wave & 1) == 0 && lane == 0 && qw < a.S) a.qscale_out[bh * a.nblk + qw / BLK] = qsc;
+        return;
+    }
 
-    fetch_tile(0);
-    store_tile(0);
+    // ---- key blocks
+    const size_t qlast = q0 + BQ - 1 < a.S - 1 ? q0 + BQ - 1 : a.S - 1;
+    const size_t kb_end = a.causal ? qlast / BLK + 1 : a.nblk;
+    const bool wave_live = qw < a.S;
+    const size_t wlast = qw + 31 < a.S - 1 ? qw + 31 : a.S - 1;
+    const size_t wave_kb_end = !wave_live ? 0 : a.causal ? wlast / BLK + 1 : a.nblk;
+
+    f32x4_t o[2][8], lt[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        lt[qt] = f32x4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int ct = 0; ct < 8; ct++) o[qt][ct] = f32x4_t{0, 0, 0, 0};
+    }
+    float mrow[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
+    const f16x8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+
+    // tile staging: 512 K^ chunks then 1024 V^T chunks of 16 bytes, six per thread
+    u32x4_t stg[6];
+    const u32x4_t *ksrc0 = (const u32x4_t *)(a.khat + bk * a.Sp * HD);
+    const u32x4_t *vsrc0 = (const u32x4_t *)(a.vt + bk * a.nblk * HD * BLK);
+#define BLK_FETCH(KB)                                                                           \
+    {                                                                                           \
+        const u32x4_t *ks_ = ksrc0 + (KB) * (BLK * HD / 16);                                    \
+        const u32x4_t *vs_ = vsrc0 + (KB) * (HD * BLK * 2 / 16);                                \
+        _Pragma("unroll") for (int u = 0; u < 2; u++) stg[u] = ks_[tid + 256 * u];              \
+        _Pragma("unroll") for (int u = 0; u < 4; u++) stg[2 + u] = vs_[tid + 256 * u];          \
+    }
+#define BLK_STORE(BUF)                                                                          \
+    {                                                                                           \
+        _Pragma("unroll") for (int u = 0; u < 2; u++) {                                         \
+            const int x = tid + 256 * u;                                                        \
+            *(u32x4_t *)&tl[BUF][swz(x >> 3, x & 7)] = stg[u];                                  \
+        }                                                                                       \
+        _Pragma("unroll") for (int u = 0; u < 4; u++) {                                         \
+            const int x = tid + 256 * u;                                                        \
+            *(u32x4_t *)&tl[BUF][BLK * 128 + swz(x >> 3, x & 7)] = stg[2 + u];                  \
+        }                                                                                       \
+    }
+    BLK_FETCH(0)
+    BLK_STORE(0)
     __syncthreads();
     for (size_t kb = 0; kb < kb_end; kb++) {
         const int buf = kb & 1;
-        const bool more = kb + 1 < kb_end;
-        if (more) fetch_tile(kb + 1);
-        if (wave_live && kb < wave_kb_end) {
+        const size_t kn = kb + 1 < kb_end ? kb + 1 : kb;
+        BLK_FETCH(kn)
+        __builtin_amdgcn_sched_barrier(0);
+        if (kb < wave_kb_end) {
             const float cs = (qsc * a.kscale[bk * a.nblk + kb]) * LOG2E_F;
+            const uint8_t *T = tl[buf];
             // ---- S^T = K^ Q^T
             i32x4_t st[4][2];
+#pragma unroll
             for (int kt = 0; kt < 4; kt++)
+#pragma unroll
                 for (int qt = 0; qt < 2; qt++) st[kt][qt] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
             for (int kt = 0; kt < 4; kt++)
+#pragma unroll
                 for (int dc = 0; dc < 2; dc++) {
-                    i32x4_t kf = *(const i32x4_t *)&ks[buf][(16 * kt + col) * KS_PITCH + dc * 64 + 16 * g];
+                    const i32x4_t kf = *(const i32x4_t *)&T[swz(16 * kt + col, 4 * dc + g)];
+#pragma unroll
                     for (int qt = 0; qt < 2; qt++)
                         st[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[qt][dc], st[kt][qt], 0, 0, 0);
                 }
-            // ---- softmax on the S^T columns
-            const bool diag = a.causal && (kb * BLK + BLK - 1 > qw);
-            const bool ragged = !a.causal && (kb * BLK + BLK > a.S);
-            f16x8_t pf[2][2];  // [qt][key chunk]
-            for (int qt = 0; qt < 2; qt++) {
-                const size_t qi = qw + 16 * qt + col;
-                float sv[4][4];
-                float mx = -__builtin_huge_valf();
-                for (int kt = 0; kt < 4; kt++)
-                    for (int i = 0; i < 4; i++) {
-                        float s = (float)st[kt][qt][i] * cs;
-                        size_t kj = kb * BLK + 16 * kt + 4 * g + i;
-                        if ((diag && kj > qi) || (ragged && kj >= a.S)) s = -__builtin_huge_valf();
-                        sv[kt][i] = s;
-                        mx = fmaxf(mx, s);
-                    }
-                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const float mnew = fmaxf(mrow[qt], mx);
-                const float alpha = __builtin_amdgcn_exp2f(mrow[qt] - mnew);
-                mrow[qt] = mnew;
-                float ls = 0.0f;
-                for (int kt = 0; kt < 4; kt++)
-                    for (int i = 0; i < 4; i++) {
-                        float p = __builtin_amdgcn_exp2f(sv[kt][i] - mnew);
-                        sv[kt][i] = p;
-                        ls += p;
-                    }
-                lrow[qt] = alpha * lrow[qt] + ls;
-                for (int ct = 0; ct < 8; ct++) o[qt][ct] *= alpha;
-                for (int kc = 0; kc < 2; kc++) {
-                    f16x8_t f;
-                    for (int i = 0; i < 4; i++) {
-                        f[i] = (_Float16)sv[2 * kc][i];
-                        f[4 + i] = (_Float16)sv[2 * kc + 1][i];
-                    }
-                    pf[qt][kc] = f;
+            // ---- masks: only the causal diagonal and the ragged last block
+            const bool diag = a.causal && kb * BLK + BLK - 1 > qw;
+            const bool ragged = kb * BLK + BLK > a.S;
+            if (diag || ragged) {
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++) {
+                    const int qrel = (int)(qw + 16 * qt + col - kb * BLK);  // query - first key
+                    const int klim = (int)(a.S - kb * BLK);                 // keys at or past S
+#pragma unroll
+                    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int kr = 16 * kt + 4 * g + i;
+                            if ((a.causal && kr > qrel) || kr >= klim) st[kt][qt][i] = INT32_MIN;
+                        }
                 }
             }
-            // ---- O^T += V^T P^T
-            for (int ct = 0; ct < 8; ct++)
+            // ---- online softmax per query column
+            f16x8_t pf[2][2];  // [qt][key chunk]
+            bool moved = false;
+            float alpha[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) {
+                int mi = INT32_MIN;
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+                    mi = max(max(mi, st[kt][qt][0]), max(st[kt][qt][1], max(st[kt][qt][2], st[kt][qt][3])));
+                mi = max(mi, __shfl_xor(mi, 16, 64));
+                mi = max(mi, __shfl_xor(mi, 32, 64));
+                const float mb = mi == INT32_MIN ? -__builtin_huge_valf() : (float)mi * cs;
+                const float mnew = fmaxf(mrow[qt], mb);
+                alpha[qt] = mnew == mrow[qt] ? 1.0f : __builtin_amdgcn_exp2f(mrow[qt] - mnew);
+                moved |= mnew != mrow[qt];
+                mrow[qt] = mnew;
+                const float nm = mnew == -__builtin_huge_valf() ? 0.0f : -mnew;
+#pragma unroll
                 for (int kc = 0; kc < 2; kc++) {
-                    const uint16_t *vrow = &vs[buf][(16 * ct + col) * VS_PITCH + 32 * kc];
-                    uint2 lo = *(const uint2 *)(vrow + 4 * g);
-                    uint2 hi = *(const uint2 *)(vrow + 16 + 4 * g);
-                    uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                    f16x8_t vf = __builtin_bit_cast(f16x8_t, vv);
+                    float p[8];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int s0 = st[2 * kc][qt][i], s1 = st[2 * kc + 1][qt][i];
+                        p[i] = s0 == INT32_MIN ? 0.0f : __builtin_amdgcn_exp2f((float)s0 * cs + nm);
+                        p[4 + i] = s1 == INT32_MIN ? 0.0f : __builtin_amdgcn_exp2f((float)s1 * cs + nm);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const f32x2_t pp = {p[2 * i], p[2 * i + 1]};
+                        const f16x2_t hh = __builtin_convertvector(pp, f16x2_t);
+                        pf[qt][kc][2 * i] = hh[0];
+                        pf[qt][kc][2 * i + 1] = hh[1];
+                    }
+                }
+            }
+            if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++) {
+                    lt[qt] *= alpha[qt];
+#pragma unroll
+                    for (int ct = 0; ct < 8; ct++) o[qt][ct] *= alpha[qt];
+                }
+            }
+            // ---- O^T += V^T P^T, l += 1 . P^T
+            const uint8_t *VT = T + BLK * 128;
+#pragma unroll
+            for (int kc = 0; kc < 2; kc++) {
+#pragma unroll
+                for (int ct = 0; ct < 8; ct++) {
+                    const f16x8_t vf = *(const f16x8_t *)&VT[swz(16 * ct + col, 4 * kc + g)];
+#pragma unroll
                     for (int qt = 0; qt < 2; qt++)
                         o[qt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[qt][kc], o[qt][ct], 0, 0, 0);
                 }
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++)
+                    lt[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[qt][kc], lt[qt], 0, 0, 0);
+            }
         }
-        if (more) store_tile(buf ^ 1);
+        BLK_STORE(buf ^ 1)
         __syncthreads();
     }
+#undef BLK_FETCH
+#undef BLK_STORE
     if (!wave_live) return;
-    // ---- normalise and store: lane holds query col, channels 4*(l/16)+i
+    // ---- normalise and store: lane holds query col, channels 16 ct + 4 g + i
+#pragma unroll
     for (int qt = 0; qt < 2; qt++) {
-        float l = lrow[qt];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
-        const float inv = 1.0f / l;
-        const size_t qi = qw + 16 * qt + col;
-        if (qi >= a.S) continue;
-        uint16_t *dst = a.out + (bh * a.S + qi) * HD;
+        const float inv = 1.0f / lt[qt][0];
+        const size_t q = qw + 16 * qt + col;
+        if (q >= a.S) continue;
+        uint16_t *dst = a.out + (bh * a.S + q) * HD;
+#pragma unroll
         for (int ct = 0; ct < 8; ct++) {
-            uint32_t w0 = (uint32_t)f32_to_bf16(o[qt][ct][0] * inv) |
-                          ((uint32_t)f32_to_bf16(o[qt][ct][1] * inv) << 16);
-            uint32_t w1 = (uint32_t)f32_to_bf16(o[qt][ct][2] * inv) |
-                          ((uint32_t)f32_to_bf16(o[qt][ct][3] * inv) << 16);
+            const uint32_t w0 = f32x2_to_bf16x2(o[qt][ct][0] * inv, o[qt][ct][1] * inv);
+            const uint32_t w1 = f32x2_to_bf16x2(o[qt][ct][2] * inv, o[qt][ct][3] * inv);
             *(uint2 *)(dst + 16 * ct + 4 * g) = make_uint2(w0, w1);
         }
     }
@@ -762,26 +890,24 @@ __global__ void __launch_bounds__(256) blk_attn(BlkArgs a) {
 
 #pragma clang fp contract(off)
 
-// export the pre-pass stages in natural layouts (parity checks)
-__global__ void blk_export(BlkArgs a, int8_t *qhat, int8_t *khat, uint16_t *vh) {
-    size_t x = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t nq = a.B * a.H * a.S * HD, nk = a.B * a.Hk * a.S * HD;
-    if (x < nq) {
-        size_t bh = x / (a.S * HD), rem = x % (a.S * HD);
-        qhat[x] = a.qhat[bh * a.Sp * HD + rem];
-    }
-    if (x < nk) {
-        size_t bk = x / (a.S * HD), rem = x % (a.S * HD);
-        size_t t = rem / HD, c = rem % HD;
-        khat[x] = a.khat[bk * a.Sp * HD + rem];
-        vh[x] = a.vt[((bk * a.nblk + t / BLK) * HD + c) * BLK + t % BLK];
-    }
+// export the K codes and V (fp16) of the pre-pass in natural layouts (parity checks)
+__global__ void blk_export(BlkArgs a, int8_t *khat, uint16_t *vh) {
+    const size_t x = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nk = a.B * a.Hk * a.S * HD;
+    if (x >= nk) return;
+    const size_t bk = x / (a.S * HD), rem = x % (a.S * HD);
+    const size_t t = rem / HD, c = rem % HD;
+    khat[x] = a.khat[bk * a.Sp * HD + rem];
+    // key t % 64 of its block sits at the position whose vt_key is it
+    const int kr = (int)(t % BLK), kc = kr >> 5, j = kr & 31, tt = j >> 4, r = j & 15;
+    const int pos = 32 * kc + 8 * (r >> 2) + 4 * tt + (r & 3);
+    vh[x] = a.vt[((bk * a.nblk + t / BLK) * HD + c) * BLK + pos];
 }
 
 struct BlkPlan {
     BlkArgs a;
     size_t ws;
-    size_t o_kpart, o_kmean, o_khat, o_kscale, o_qhat, o_qscale, o_vt;
+    size_t o_kpart, o_kmean, o_khat, o_kscale, o_vt;
 };
 
 static BlkPlan blk_plan(const qbk_attn_shape *s) {
@@ -792,8 +918,9 @@ static BlkPlan blk_plan(const qbk_attn_shape *s) {
     a.Hk = s->n_kv_heads;
     a.S = s->seq_q;
     a.nblk = div_ceil(a.S, BLK);
-    a.Sp = round_up(a.S, BQ);
+    a.Sp = a.nblk * BLK;
     const size_t bk = a.B * a.Hk, bh = a.B * a.H;
+    a.hpx = bh % 8 == 0 ? (int)(bh / 8) : 0;
     size_t off = 0;
     auto take = [&](size_t n) {
         size_t o = off;
@@ -804,8 +931,6 @@ static BlkPlan blk_plan(const qbk_attn_shape *s) {
     P.o_kmean = take(bk * HD * 4);
     P.o_khat = take(bk * a.Sp * HD);
     P.o_kscale = take(bk * a.nblk * 4);
-    P.o_qhat = take(bh * a.Sp * HD);
-    P.o_qscale = take(bh * a.nblk * 4);
     P.o_vt = take(bk * a.nblk * HD * BLK * 2);
     P.ws = off;
     return P;
@@ -822,8 +947,7 @@ static int validate_blk(const qbk_attn_shape *s) {
     return QBK_OK;
 }
 
-static int run_blk_prepass(BlkPlan &P, const qbk_attn_shape *s, const uint16_t *q,
-                           const uint16_t *k, const uint16_t *v, void *ws, hipStream_t st) {
+static void blk_bind(BlkPlan &P, const uint16_t *q, const uint16_t *k, const uint16_t *v, void *ws) {
     BlkArgs &a = P.a;
     a.q = q;
     a.k = k;
@@ -834,17 +958,23 @@ static int run_blk_prepass(BlkPlan &P, const qbk_attn_shape *s, const uint16_t *
     a.kmean = (float *)(w + P.o_kmean);
     a.khat = (int8_t *)(w + P.o_khat);
     a.kscale = (float *)(w + P.o_kscale);
-    a.qhat = (int8_t *)(w + P.o_qhat);
-    a.qscale = (float *)(w + P.o_qscale);
     a.vt = (uint16_t *)(w + P.o_vt);
-    // Query codes of tokens >= nblk*64 (up to the 128-row tile) are never
-    // written: those queries are computed and discarded, and each query
-    // column of the MFMA tiles is independent of the others.
-    hipLaunchKernelGGL(blk_kpart, dim3((unsigned)a.nblk, (unsigned)(a.B * a.Hk)), dim3(HD), 0, st, a);
+}
+
+// K mean, K codes and V^T (fp16) of every (kv head, block): two launches
+static int run_blk_prepass(BlkPlan &P, hipStream_t st) {
+    const BlkArgs &a = P.a;
+    hipLaunchKernelGGL(blk_kpart, dim3((unsigned)a.nblk, (unsigned)(a.B * a.Hk)), dim3(64), 0, st, a);
     QBK_HIP(hipGetLastError());
     hipLaunchKernelGGL(blk_kvquant, dim3((unsigned)a.nblk, (unsigned)(a.B * a.Hk)), dim3(256), 0, st, a);
     QBK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(blk_qquant, dim3((unsigned)a.nblk, (unsigned)(a.B * a.H)), dim3(256), 0, st, a);
+    return QBK_OK;
+}
+
+static int run_blk_attn(const BlkPlan &P, hipStream_t st) {
+    const BlkArgs &a = P.a;
+    const size_t n = div_ceil(a.S, BQ) * a.B * a.H;
+    hipLaunchKernelGGL(blk_attn, dim3((unsigned)n), dim3(256), 0, st, a);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }
@@ -913,13 +1043,11 @@ int qbk_attention_sage_blk_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const 
                     fmt("workspace of %zu bytes is smaller than the %zu this call needs",
                         workspace_size, P.ws));
     hipStream_t st = (hipStream_t)stream;
-    if ((rc = run_blk_prepass(P, shape, q, k, v, workspace, st))) return rc;
+    blk_bind(P, q, k, v, workspace);
+    if ((rc = run_blk_prepass(P, st))) return rc;
     P.a.out = out;
     P.a.causal = causal ? 1 : 0;
-    hipLaunchKernelGGL(blk_attn, dim3((unsigned)div_ceil(P.a.S, BQ), (unsigned)(P.a.B * P.a.H)),
-                       dim3(256), 0, st, P.a);
-    QBK_HIP(hipGetLastError());
-    return QBK_OK;
+    return run_blk_attn(P, st);
 }
 
 int qbk_sage_blk_quantize_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const uint16_t *q,
@@ -933,19 +1061,25 @@ int qbk_sage_blk_quantize_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const u
     hipStream_t st = (hipStream_t)stream;
     void *ws = nullptr;
     QBK_HIP(hipMallocAsync(&ws, P.ws, st));
-    rc = run_blk_prepass(P, shape, q, k, v, ws, st);
+    blk_bind(P, q, k, v, ws);
+    rc = run_blk_prepass(P, st);
+    if (!rc) {
+        // Q codes come from the attention kernel's own prologue, run in its
+        // quantize-only mode
+        P.a.qhat_out = qhat;
+        P.a.qscale_out = qscale;
+        rc = run_blk_attn(P, st);
+    }
     if (!rc) {
         const BlkArgs &a = P.a;
-        size_t n = a.B * (a.H > a.Hk ? a.H : a.Hk) * a.S * HD;
-        hipLaunchKernelGGL(blk_export, dim3((unsigned)div_ceil(n, 256)), dim3(256), 0, st, a, qhat,
-                           khat, vh);
+        const size_t n = a.B * a.Hk * a.S * HD;
+        hipLaunchKernelGGL(blk_export, dim3((unsigned)div_ceil(n, 256)), dim3(256), 0, st, a, khat, vh);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) rc = fail(QBK_ERR_DEVICE, fmt("blk_export: %s", hipGetErrorString(e)));
     }
     if (!rc) {
         const BlkArgs &a = P.a;
-        hipError_t e = hipMemcpyAsync(qscale, a.qscale, a.B * a.H * a.nblk * 4, hipMemcpyDeviceToDevice, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(kscale, a.kscale, a.B * a.Hk * a.nblk * 4, hipMemcpyDeviceToDevice, st);
+        hipError_t e = hipMemcpyAsync(kscale, a.kscale, a.B * a.Hk * a.nblk * 4, hipMemcpyDeviceToDevice, st);
         if (e == hipSuccess) e = hipMemcpyAsync(kmean, a.kmean, a.B * a.Hk * HD * 4, hipMemcpyDeviceToDevice, st);
         if (e != hipSuccess) rc = fail(QBK_ERR_DEVICE, fmt("hipMemcpyAsync: %s", hipGetErrorString(e)));
     }
