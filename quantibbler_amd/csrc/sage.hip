@@ -623,13 +623,24 @@ __global__ void __launch_bounds__(256) blk_kvquant(BlkArgs a) {
     }
 }
 
+// max over lanes l, l ^ 16, l ^ 32, l ^ 48 -- the four lanes that share a
+// query column of a 16x16 C tile -- with v_permlane16/32_swap: swapping a
+// register with itself hands each lane the other row's (half's) value in
+// one of the two results, in the VALU, with no LDS round trip.
+__device__ __forceinline__ int lanes_max4(int v) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    const int a = max((int)r16[0], (int)r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+    return max((int)r32[0], (int)r32[1]);
+}
+
 #pragma clang fp contract(fast)
 
-// LDS tile of one key block: K^ [64 keys][128 B] then V^T [128 d][128 B];
-// each 128-byte row keeps its eight 16-byte chunks XOR-swizzled by the row
-// (chunk c at c ^ (row & 7)), so that the eight lanes of a 16-byte-read
-// phase -- eight consecutive rows, one chunk -- hit disjoint banks.
-#define TILE_BYTES (BLK * 128 + HD * 128)
+// LDS tiles: K^ [64 keys][128 B], V^T [128 d][128 B], Q codes [128
+// queries][128 B]; each 128-byte row keeps its eight 16-byte chunks
+// XOR-swizzled by the row (chunk c at c ^ (row & 7)), so that the eight
+// lanes of a 16-byte-read phase -- eight consecutive rows, one chunk -- hit
+// disjoint banks.
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
 
 // Main pass.  Workgroup: (128-query tile, batch*head); wave w owns queries
@@ -642,14 +653,25 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((ch
 //                  tiles x 2 d-chunks; C lane l holds query l%16, keys
 //                  4(l/16) + i of its key tile;
 //   online softmax per query column on the integer scores: block max by
-//   v_max3 (the scale is positive), one cvt + fma + exp2 per score, O and l
-//   rescaled only when a lane's max moved;
+//   v_max3 (the scale is positive), one cvt + fma + exp2 per score, masks
+//   only on the causal diagonal and the ragged last block, and a reference
+//   max that moves (rescaling O and l) only when a block max exceeds it by
+//   more than 8 in log2 units;
 //   O^T[128 x 32] += V^T . P^T and l += 1 . P^T -- f16 16x16x32, P^T taken
 //                  straight from the S^T registers (PV key order above), the
 //                  row sums from a ninth tile of ones.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) blk_attn(BlkArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t tl[2][TILE_BYTES];
-    __shared__ float red[4];
+    // K^ and V^T tiles, double buffered -- four separate objects, so that the
+    // compiler can tell a read of one from the direct loads into another --
+    // and the tile's Q codes
+    __shared__ __attribute__((aligned(16))) uint8_t kl0[BLK * 128], kl1[BLK * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t vl0[HD * 128], vl1[HD * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t ql[BQ * 128];
+#define KL(B) ((B) ? kl1 : kl0)
+#define VL(B) ((B) ? vl1 : vl0)
+    // the prologue's block-peak exchange; V^T buffer 1 is first loaded after
+    // the barrier that ends the prologue
+    float *red = (float *)vl1;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, col = lane & 15;
@@ -671,9 +693,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
     const size_t q0 = qi * BQ, qw = q0 + 32 * wave;
 
     // ---- Q codes (B operand): query qw + 16 qt + col, d = 64 dc + 16 g + e
-    i32x4_t qf[2][2];
     float qsc;
     {
+        i32x4_t qf[2][2];
         float x[2][2][16];
         float pk = 0.0f;
 #pragma unroll
@@ -710,18 +732,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
                 for (int w = 0; w < 4; w++)
                     qf[qt][dc][w] = (int)pack4(q8(x[qt][dc][4 * w] * inv), q8(x[qt][dc][4 * w + 1] * inv),
                                                q8(x[qt][dc][4 * w + 2] * inv), q8(x[qt][dc][4 * w + 3] * inv));
-    }
-    if (a.qhat_out) {  // quantize-only launch: export the codes and scales
+        if (a.qhat_out) {  // quantize-only launch: export the codes and scales
 #pragma unroll
-        for (int qt = 0; qt < 2; qt++) {
-            const size_t q = qw + 16 * qt + col;
-            if (q >= a.S) continue;
+            for (int qt = 0; qt < 2; qt++) {
+                const size_t q = qw + 16 * qt + col;
+                if (q >= a.S) continue;
+#pragma unroll
+                for (int dc = 0; dc < 2; dc++)
+                    *(i32x4_t *)(a.qhat_out + (bh * a.S + q) * HD + 64 * dc + 16 * g) = qf[qt][dc];
+            }
+            if ((wave & 1) == 0 && lane == 0 && qw < a.S) a.qscale_out[bh * a.nblk + qw / BLK] = qsc;
+            return;
+        }
+        // the wave's codes to LDS, read back as MFMA operands each block
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++)
 #pragma unroll
             for (int dc = 0; dc < 2; dc++)
-                *(i32x4_t *)(a.qhat_out + (bh * a.S + q) * HD + 64 * dc + 16 * g) = qf[qt][dc];
-        }
-        if ((wave & 1) == 0 && lane == 0 && qw < a.S) a.qscale_out[bh * a.nblk + qw / BLK] = qsc;
-        return;
+                *(i32x4_t *)&ql[swz(32 * wave + 16 * qt + col, 4 * dc + g)] = qf[qt][dc];
     }
 
     // ---- key blocks
@@ -741,136 +769,155 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
     float mrow[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
     const f16x8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
 
-    // tile staging: 512 K^ chunks then 1024 V^T chunks of 16 bytes, six per thread
-    u32x4_t stg[6];
-    const u32x4_t *ksrc0 = (const u32x4_t *)(a.khat + bk * a.Sp * HD);
-    const u32x4_t *vsrc0 = (const u32x4_t *)(a.vt + bk * a.nblk * HD * BLK);
-#define BLK_FETCH(KB)                                                                           \
-    {                                                                                           \
-        const u32x4_t *ks_ = ksrc0 + (KB) * (BLK * HD / 16);                                    \
-        const u32x4_t *vs_ = vsrc0 + (KB) * (HD * BLK * 2 / 16);                                \
-        _Pragma("unroll") for (int u = 0; u < 2; u++) stg[u] = ks_[tid + 256 * u];              \
-        _Pragma("unroll") for (int u = 0; u < 4; u++) stg[2 + u] = vs_[tid + 256 * u];          \
+    // K^ and V^T tiles load one block ahead into double buffers (issued at
+    // the top of an iteration, waited for at its end), straight into LDS: a
+    // K^ tile is 8 and a V^T tile 16 1-KB pieces of eight 128-byte rows, and
+    // lane i of a global_load_lds_dwordx4 fills bytes 16 i .. of its piece,
+    // so it fetches the source chunk that the swizzle puts there.  Within an
+    // iteration every LDS fragment is read a phase before its MFMAs: the Q
+    // and K^ fragments and the first key chunk's V^T fragments at the top,
+    // the second chunk's under the first chunk's P.V MFMAs.
+    const int lr = lane >> 3, lcs = ((lane & 7) ^ lr) * 16;
+    // the K block scales through the constant address space: scalar loads,
+    // counted apart from the tile loads in flight
+    const __attribute__((address_space(4))) float *kscl =
+        (const __attribute__((address_space(4))) float *)(a.kscale + bk * a.nblk);
+    const uint8_t *ksrc0 = (const uint8_t *)a.khat + bk * a.Sp * HD;
+    const uint8_t *vsrc0 = (const uint8_t *)a.vt + bk * a.nblk * HD * BLK * 2;
+#define BLK_LOAD(KB, BUF)                                                                       \
+    _Pragma("unroll") for (int u = 0; u < 2; u++) {                                             \
+        const int pc = wave + 4 * u;                                                            \
+        __builtin_amdgcn_global_load_lds((const void *)(ksrc0 + (KB) * (BLK * HD) + (8 * pc + lr) * 128 + lcs),\
+                                         (__attribute__((address_space(3))) void *)&KL(BUF)[pc * 1024], 16, 0, 0);\
+    }                                                                                           \
+    _Pragma("unroll") for (int u = 0; u < 4; u++) {                                             \
+        const int pc = wave + 4 * u;                                                            \
+        __builtin_amdgcn_global_load_lds((const void *)(vsrc0 + (KB) * (HD * BLK * 2) + (8 * pc + lr) * 128 + lcs),\
+                                         (__attribute__((address_space(3))) void *)&VL(BUF)[pc * 1024], 16, 0, 0);\
     }
-#define BLK_STORE(BUF)                                                                          \
-    {                                                                                           \
-        _Pragma("unroll") for (int u = 0; u < 2; u++) {                                         \
-            const int x = tid + 256 * u;                                                        \
-            *(u32x4_t *)&tl[BUF][swz(x >> 3, x & 7)] = stg[u];                                  \
-        }                                                                                       \
-        _Pragma("unroll") for (int u = 0; u < 4; u++) {                                         \
-            const int x = tid + 256 * u;                                                        \
-            *(u32x4_t *)&tl[BUF][BLK * 128 + swz(x >> 3, x & 7)] = stg[2 + u];                  \
+    // Softmax of one block's scores st into pf / alpha / moved; MASKED (a
+    // constant) zeroes the p of the keys set in mbits.  A lane moves its
+    // reference max only when the block max exceeds it by more than 8
+    // (log2): below that p = exp2(s - m) <= 256, and O / l does not depend on
+    // which reference max the accumulators share, so most blocks skip the O
+    // rescale.
+#define BLK_SOFTMAX(MASKED)                                                                     \
+    _Pragma("unroll") for (int qt = 0; qt < 2; qt++) {                                          \
+        int mi = INT32_MIN;                                                                     \
+        _Pragma("unroll") for (int kt = 0; kt < 4; kt++)                                        \
+            mi = max(max(mi, st[kt][qt][0]), max(st[kt][qt][1], max(st[kt][qt][2], st[kt][qt][3])));\
+        mi = lanes_max4(mi);                                                                    \
+        const float mb = mi == INT32_MIN ? -__builtin_huge_valf() : (float)mi * cs;             \
+        const bool up = mb > mrow[qt] + 8.0f;                                                   \
+        alpha[qt] = up ? __builtin_amdgcn_exp2f(mrow[qt] - mb) : 1.0f;                          \
+        moved |= up;                                                                            \
+        mrow[qt] = up ? mb : mrow[qt];                                                          \
+        const float nm = mrow[qt] == -__builtin_huge_valf() ? 0.0f : -mrow[qt];                 \
+        _Pragma("unroll") for (int kc = 0; kc < 2; kc++) {                                      \
+            float p[8];                                                                         \
+            _Pragma("unroll") for (int i = 0; i < 4; i++) {                                     \
+                p[i] = __builtin_amdgcn_exp2f((float)st[2 * kc][qt][i] * cs + nm);              \
+                p[4 + i] = __builtin_amdgcn_exp2f((float)st[2 * kc + 1][qt][i] * cs + nm);      \
+                if (MASKED) {                                                                   \
+                    p[i] = (mbits[qt] >> (8 * kc + i)) & 1 ? 0.0f : p[i];                       \
+                    p[4 + i] = (mbits[qt] >> (8 * kc + 4 + i)) & 1 ? 0.0f : p[4 + i];           \
+                }                                                                               \
+            }                                                                                   \
+            _Pragma("unroll") for (int i = 0; i < 4; i++) {                                     \
+                const f32x2_t pp = {p[2 * i], p[2 * i + 1]};                                    \
+                const f16x2_t hh = __builtin_convertvector(pp, f16x2_t);                        \
+                pf[qt][kc][2 * i] = hh[0];                                                      \
+                pf[qt][kc][2 * i + 1] = hh[1];                                                  \
+            }                                                                                   \
         }                                                                                       \
     }
-    BLK_FETCH(0)
-    BLK_STORE(0)
+    // One key block KB from buffer B (masks only on the causal diagonal and
+    // the ragged last block).
+#define BLK_ITER(KB, B)                                                                         \
+    {                                                                                           \
+        const size_t k1 = (KB) + 1 < kb_end ? (KB) + 1 : kb_end - 1;                            \
+        BLK_LOAD(k1, (B) ^ 1)                                                                   \
+        __builtin_amdgcn_sched_barrier(0);                                                      \
+        if ((KB) < wave_kb_end) {                                                               \
+            const float cs = (qsc * kscl[KB]) * LOG2E_F;                                        \
+            const uint8_t *KT = KL(B), *VT = VL(B);                                             \
+            i32x4_t qf[2][2], kf[4][2];                                                         \
+            f16x8_t vf0[8];                                                                     \
+            _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                    \
+            _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                    \
+                qf[qt][dc] = *(const i32x4_t *)&ql[swz(32 * wave + 16 * qt + col, 4 * dc + g)]; \
+            _Pragma("unroll") for (int kt = 0; kt < 4; kt++)                                    \
+            _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                    \
+                kf[kt][dc] = *(const i32x4_t *)&KT[swz(16 * kt + col, 4 * dc + g)];             \
+            _Pragma("unroll") for (int ct = 0; ct < 8; ct++)                                    \
+                vf0[ct] = *(const f16x8_t *)&VT[swz(16 * ct + col, g)];                         \
+            i32x4_t st[4][2];                                                                   \
+            _Pragma("unroll") for (int kt = 0; kt < 4; kt++)                                    \
+            _Pragma("unroll") for (int qt = 0; qt < 2; qt++) {                                  \
+                st[kt][qt] = i32x4_t{0, 0, 0, 0};                                               \
+                _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                \
+                    st[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[kt][dc], qf[qt][dc], st[kt][qt], 0, 0, 0);\
+            }                                                                                   \
+            const bool masked = (a.causal && (KB) * BLK + BLK - 1 > qw) || (KB) * BLK + BLK > a.S;\
+            f16x8_t pf[2][2];                                                                   \
+            bool moved = false;                                                                 \
+            float alpha[2];                                                                     \
+            if (masked) {                                                                       \
+                uint32_t mbits[2] = {0u, 0u};                                                   \
+                _Pragma("unroll") for (int qt = 0; qt < 2; qt++) {                              \
+                    const int qrel = (int)(qw + 16 * qt + col - (KB) * BLK);                    \
+                    const int klim = (int)(a.S - (KB) * BLK);                                   \
+                    _Pragma("unroll") for (int kt = 0; kt < 4; kt++)                            \
+                    _Pragma("unroll") for (int i = 0; i < 4; i++) {                             \
+                        const int kr = 16 * kt + 4 * g + i;                                     \
+                        if ((a.causal && kr > qrel) || kr >= klim) {                            \
+                            st[kt][qt][i] = INT32_MIN;                                          \
+                            mbits[qt] |= 1u << (4 * kt + i);                                    \
+                        }                                                                       \
+                    }                                                                           \
+                }                                                                               \
+                BLK_SOFTMAX(true)                                                               \
+            } else {                                                                            \
+                const uint32_t mbits[2] = {0u, 0u};                                             \
+                BLK_SOFTMAX(false)                                                              \
+            }                                                                                   \
+            if (__builtin_amdgcn_ballot_w64(moved)) {                                           \
+                _Pragma("unroll") for (int qt = 0; qt < 2; qt++) {                              \
+                    lt[qt] *= alpha[qt];                                                        \
+                    _Pragma("unroll") for (int ct = 0; ct < 8; ct++) o[qt][ct] *= alpha[qt];    \
+                }                                                                               \
+            }                                                                                   \
+            f16x8_t vf1[8];                                                                     \
+            _Pragma("unroll") for (int ct = 0; ct < 8; ct++) {                                  \
+                vf1[ct] = *(const f16x8_t *)&VT[swz(16 * ct + col, 4 + g)];                     \
+                _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                \
+                    o[qt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf0[ct], pf[qt][0], o[qt][ct], 0, 0, 0);\
+            }                                                                                   \
+            _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                    \
+                lt[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[qt][0], lt[qt], 0, 0, 0);\
+            _Pragma("unroll") for (int ct = 0; ct < 8; ct++)                                    \
+            _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                    \
+                o[qt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf1[ct], pf[qt][1], o[qt][ct], 0, 0, 0);\
+            _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                    \
+                lt[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[qt][1], lt[qt], 0, 0, 0);\
+        }                                                                                       \
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the next block's tile has landed */ \
+        __syncthreads();                                                                        \
+    }
+    BLK_LOAD(0, 0)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    for (size_t kb = 0; kb < kb_end; kb++) {
-        const int buf = kb & 1;
-        const size_t kn = kb + 1 < kb_end ? kb + 1 : kb;
-        BLK_FETCH(kn)
-        __builtin_amdgcn_sched_barrier(0);
-        if (kb < wave_kb_end) {
-            const float cs = (qsc * a.kscale[bk * a.nblk + kb]) * LOG2E_F;
-            const uint8_t *T = tl[buf];
-            // ---- S^T = K^ Q^T
-            i32x4_t st[4][2];
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int qt = 0; qt < 2; qt++) st[kt][qt] = i32x4_t{0, 0, 0, 0};
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int dc = 0; dc < 2; dc++) {
-                    const i32x4_t kf = *(const i32x4_t *)&T[swz(16 * kt + col, 4 * dc + g)];
-#pragma unroll
-                    for (int qt = 0; qt < 2; qt++)
-                        st[kt][qt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[qt][dc], st[kt][qt], 0, 0, 0);
-                }
-            // ---- masks: only the causal diagonal and the ragged last block
-            const bool diag = a.causal && kb * BLK + BLK - 1 > qw;
-            const bool ragged = kb * BLK + BLK > a.S;
-            if (diag || ragged) {
-#pragma unroll
-                for (int qt = 0; qt < 2; qt++) {
-                    const int qrel = (int)(qw + 16 * qt + col - kb * BLK);  // query - first key
-                    const int klim = (int)(a.S - kb * BLK);                 // keys at or past S
-#pragma unroll
-                    for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const int kr = 16 * kt + 4 * g + i;
-                            if ((a.causal && kr > qrel) || kr >= klim) st[kt][qt][i] = INT32_MIN;
-                        }
-                }
-            }
-            // ---- online softmax per query column
-            f16x8_t pf[2][2];  // [qt][key chunk]
-            bool moved = false;
-            float alpha[2];
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++) {
-                int mi = INT32_MIN;
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++)
-                    mi = max(max(mi, st[kt][qt][0]), max(st[kt][qt][1], max(st[kt][qt][2], st[kt][qt][3])));
-                mi = max(mi, __shfl_xor(mi, 16, 64));
-                mi = max(mi, __shfl_xor(mi, 32, 64));
-                const float mb = mi == INT32_MIN ? -__builtin_huge_valf() : (float)mi * cs;
-                const float mnew = fmaxf(mrow[qt], mb);
-                alpha[qt] = mnew == mrow[qt] ? 1.0f : __builtin_amdgcn_exp2f(mrow[qt] - mnew);
-                moved |= mnew != mrow[qt];
-                mrow[qt] = mnew;
-                const float nm = mnew == -__builtin_huge_valf() ? 0.0f : -mnew;
-#pragma unroll
-                for (int kc = 0; kc < 2; kc++) {
-                    float p[8];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int s0 = st[2 * kc][qt][i], s1 = st[2 * kc + 1][qt][i];
-                        p[i] = s0 == INT32_MIN ? 0.0f : __builtin_amdgcn_exp2f((float)s0 * cs + nm);
-                        p[4 + i] = s1 == INT32_MIN ? 0.0f : __builtin_amdgcn_exp2f((float)s1 * cs + nm);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const f32x2_t pp = {p[2 * i], p[2 * i + 1]};
-                        const f16x2_t hh = __builtin_convertvector(pp, f16x2_t);
-                        pf[qt][kc][2 * i] = hh[0];
-                        pf[qt][kc][2 * i + 1] = hh[1];
-                    }
-                }
-            }
-            if (__builtin_amdgcn_ballot_w64(moved)) {
-#pragma unroll
-                for (int qt = 0; qt < 2; qt++) {
-                    lt[qt] *= alpha[qt];
-#pragma unroll
-                    for (int ct = 0; ct < 8; ct++) o[qt][ct] *= alpha[qt];
-                }
-            }
-            // ---- O^T += V^T P^T, l += 1 . P^T
-            const uint8_t *VT = T + BLK * 128;
-#pragma unroll
-            for (int kc = 0; kc < 2; kc++) {
-#pragma unroll
-                for (int ct = 0; ct < 8; ct++) {
-                    const f16x8_t vf = *(const f16x8_t *)&VT[swz(16 * ct + col, 4 * kc + g)];
-#pragma unroll
-                    for (int qt = 0; qt < 2; qt++)
-                        o[qt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[qt][kc], o[qt][ct], 0, 0, 0);
-                }
-#pragma unroll
-                for (int qt = 0; qt < 2; qt++)
-                    lt[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[qt][kc], lt[qt], 0, 0, 0);
-            }
-        }
-        BLK_STORE(buf ^ 1)
-        __syncthreads();
+    size_t kb = 0;
+    for (; kb + 2 <= kb_end; kb += 2) {
+        BLK_ITER(kb, 0)
+        BLK_ITER(kb + 1, 1)
     }
-#undef BLK_FETCH
-#undef BLK_STORE
+    if (kb < kb_end) BLK_ITER(kb, 0)
+#undef BLK_ITER
+#undef BLK_SOFTMAX
+#undef BLK_LOAD
+#undef KL
+#undef VL
     if (!wave_live) return;
     // ---- normalise and store: lane holds query col, channels 16 ct + 4 g + i
 #pragma unroll
