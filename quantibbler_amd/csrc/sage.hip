@@ -769,14 +769,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
     float mrow[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
     const f16x8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
 
-    // K^ and V^T tiles load one block ahead into double buffers (issued at
-    // the top of an iteration, waited for at its end), straight into LDS: a
-    // K^ tile is 8 and a V^T tile 16 1-KB pieces of eight 128-byte rows, and
-    // lane i of a global_load_lds_dwordx4 fills bytes 16 i .. of its piece,
-    // so it fetches the source chunk that the swizzle puts there.  Within an
-    // iteration every LDS fragment is read a phase before its MFMAs: the Q
-    // and K^ fragments and the first key chunk's V^T fragments at the top,
-    // the second chunk's under the first chunk's P.V MFMAs.
+    // K^ tiles load two blocks ahead and V^T tiles one, into double buffers
+    // (issued at the top of an iteration, waited for at its end), straight
+    // into LDS: a K^ tile is 8 and a V^T tile 16 1-KB pieces of eight
+    // 128-byte rows, and lane i of a global_load_lds_dwordx4 fills bytes
+    // 16 i .. of its piece, so it fetches the source chunk that the swizzle
+    // puts there.  Every LDS fragment is read a phase before its MFMAs: the
+    // next block's Q and K^ fragments at the end of an iteration (they wait
+    // out the barrier in registers), the first key chunk's V^T fragments at
+    // the top, the second chunk's under the first chunk's P.V MFMAs.
     const int lr = lane >> 3, lcs = ((lane & 7) ^ lr) * 16;
     // the K block scales through the constant address space: scalar loads,
     // counted apart from the tile loads in flight
@@ -784,16 +785,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
         (const __attribute__((address_space(4))) float *)(a.kscale + bk * a.nblk);
     const uint8_t *ksrc0 = (const uint8_t *)a.khat + bk * a.Sp * HD;
     const uint8_t *vsrc0 = (const uint8_t *)a.vt + bk * a.nblk * HD * BLK * 2;
-#define BLK_LOAD(KB, BUF)                                                                       \
-    _Pragma("unroll") for (int u = 0; u < 2; u++) {                                             \
-        const int pc = wave + 4 * u;                                                            \
-        __builtin_amdgcn_global_load_lds((const void *)(ksrc0 + (KB) * (BLK * HD) + (8 * pc + lr) * 128 + lcs),\
-                                         (__attribute__((address_space(3))) void *)&KL(BUF)[pc * 1024], 16, 0, 0);\
-    }                                                                                           \
-    _Pragma("unroll") for (int u = 0; u < 4; u++) {                                             \
-        const int pc = wave + 4 * u;                                                            \
-        __builtin_amdgcn_global_load_lds((const void *)(vsrc0 + (KB) * (HD * BLK * 2) + (8 * pc + lr) * 128 + lcs),\
-                                         (__attribute__((address_space(3))) void *)&VL(BUF)[pc * 1024], 16, 0, 0);\
+    // a lane's byte offset within tile piece wave + 4 u: row 8 (wave + 4 u) + lr,
+    // swizzled chunk (the uniform tile base stays in SGPRs)
+    const uint32_t loff = (uint32_t)(8 * wave + lr) * 128 + lcs;
+#define BLK_LOAD_K(KB, BUF)                                                                     \
+    {                                                                                           \
+        const uint8_t *kb_ = ksrc0 + (KB) * (BLK * HD);                                         \
+        _Pragma("unroll") for (int u = 0; u < 2; u++)                                           \
+            __builtin_amdgcn_global_load_lds((const void *)(kb_ + (loff + u * 4096u)),           \
+                                             (__attribute__((address_space(3))) void *)&KL(BUF)[(wave + 4 * u) * 1024], 16, 0, 0);\
+    }
+#define BLK_LOAD_V(KB, BUF)                                                                     \
+    {                                                                                           \
+        const uint8_t *vb_ = vsrc0 + (KB) * (HD * BLK * 2);                                     \
+        _Pragma("unroll") for (int u = 0; u < 4; u++)                                           \
+            __builtin_amdgcn_global_load_lds((const void *)(vb_ + (loff + u * 4096u)),           \
+                                             (__attribute__((address_space(3))) void *)&VL(BUF)[(wave + 4 * u) * 1024], 16, 0, 0);\
+    }
+    // the Q and K^ fragments of the block whose K^ tile is in buffer BUF
+#define BLK_FRAGS(BUF)                                                                          \
+    {                                                                                           \
+        _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                        \
+        _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                        \
+            qf[qt][dc] = *(const i32x4_t *)&ql[swz(32 * wave + 16 * qt + col, 4 * dc + g)];     \
+        _Pragma("unroll") for (int kt = 0; kt < 4; kt++)                                        \
+        _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                        \
+            kf[kt][dc] = *(const i32x4_t *)&KL(BUF)[swz(16 * kt + col, 4 * dc + g)];            \
     }
     // Softmax of one block's scores st into pf / alpha / moved; MASKED (a
     // constant) zeroes the p of the keys set in mbits.  A lane moves its
@@ -836,19 +853,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
 #define BLK_ITER(KB, B)                                                                         \
     {                                                                                           \
         const size_t k1 = (KB) + 1 < kb_end ? (KB) + 1 : kb_end - 1;                            \
-        BLK_LOAD(k1, (B) ^ 1)                                                                   \
+        const size_t k2 = (KB) + 2 < kb_end ? (KB) + 2 : kb_end - 1;                            \
+        BLK_LOAD_K(k2, B)                                                                       \
+        BLK_LOAD_V(k1, (B) ^ 1)                                                                 \
         __builtin_amdgcn_sched_barrier(0);                                                      \
         if ((KB) < wave_kb_end) {                                                               \
             const float cs = (qsc * kscl[KB]) * LOG2E_F;                                        \
-            const uint8_t *KT = KL(B), *VT = VL(B);                                             \
-            i32x4_t qf[2][2], kf[4][2];                                                         \
+            const uint8_t *VT = VL(B);                                                          \
             f16x8_t vf0[8];                                                                     \
-            _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                    \
-            _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                    \
-                qf[qt][dc] = *(const i32x4_t *)&ql[swz(32 * wave + 16 * qt + col, 4 * dc + g)]; \
-            _Pragma("unroll") for (int kt = 0; kt < 4; kt++)                                    \
-            _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                    \
-                kf[kt][dc] = *(const i32x4_t *)&KT[swz(16 * kt + col, 4 * dc + g)];             \
             _Pragma("unroll") for (int ct = 0; ct < 8; ct++)                                    \
                 vf0[ct] = *(const f16x8_t *)&VT[swz(16 * ct + col, g)];                         \
             i32x4_t st[4][2];                                                                   \
@@ -901,12 +913,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
             _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                    \
                 lt[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[qt][1], lt[qt], 0, 0, 0);\
         }                                                                                       \
-        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the next block's tile has landed */ \
+        __builtin_amdgcn_sched_barrier(0);                                                      \
+        BLK_FRAGS((B) ^ 1)                                                                      \
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the next tiles have landed */        \
         __syncthreads();                                                                        \
     }
-    BLK_LOAD(0, 0)
+    i32x4_t qf[2][2], kf[4][2];
+    BLK_LOAD_K(0, 0)
+    BLK_LOAD_K(kb_end > 1 ? 1 : 0, 1)
+    BLK_LOAD_V(0, 0)
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
+    BLK_FRAGS(0)
     size_t kb = 0;
     for (; kb + 2 <= kb_end; kb += 2) {
         BLK_ITER(kb, 0)
@@ -915,7 +933,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
     if (kb < kb_end) BLK_ITER(kb, 0)
 #undef BLK_ITER
 #undef BLK_SOFTMAX
-#undef BLK_LOAD
+#undef BLK_LOAD_K
+#undef BLK_LOAD_V
+#undef BLK_FRAGS
 #undef KL
 #undef VL
     if (!wave_live) return;
