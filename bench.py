@@ -315,6 +315,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--only", choices=["gemm", "sage", "cfg3"],
+                    help="run one secondary workload alone and print its figures (for profiling); "
+                         "no headline line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-traffic", action="store_true",
                     help="first run an elementwise kernel of known traffic (256 MiB read, 256 MiB "
@@ -331,6 +334,16 @@ def main():
     import quantibbler_amd as qa
 
     ctx = qa.GpuContext(0)
+    if args.only:
+        if args.only == "gemm":
+            layers, _ = make_layers(qa, ctx, np, 1, seed=1)
+            res = bench_gemm(torch, np, layers[0])
+        elif args.only == "sage":
+            res = bench_sage(qa, ctx, torch, np)
+        else:
+            res = bench_cfg3(qa, ctx, torch, np)
+        print(json.dumps({"only": args.only, "result": res}), flush=True)
+        return
     if args.calibrate_traffic:
         a = torch.ones(1 << 26, dtype=torch.int32, device="cuda")
         b = torch.empty_like(a)

@@ -45,8 +45,9 @@ __host__ __device__ inline int kq4(int g, int e) {
 }
 // Word for (row group rg, slice s, lane l, row tile rt): element e of row
 // 64rg + 16rt + l%16 is stored at bit 4*(e%8) + e/8, set when the sign is -1,
-// so VGPR v of the fp4 operand is one v_bfi of (word << (3 - v)) into
-// 0x22222222 (fp4 e2m1 +1.0 = 0x2, -1.0 = 0xA).
+// so VGPR v of the fp4 operand is one v_lshl_or_b32: (word << (3 - v)) |
+// 0x77777777, every nibble then e2m1 0111 = +6 with the sign bit on top (the
+// MFMA's A scale 2^-2 makes it +-1.5, which the epilogue divides out).
 static void repack_q4(const uint8_t *rows, size_t n_rows, size_t n_bits, size_t rows_p,
                       size_t bits_q, uint32_t *out) {
     size_t rw = div_ceil(n_bits, 8);
