@@ -487,7 +487,7 @@ static size_t q4_gemv_lds(int ncol_t, int ksplit) {
 // is too small to fill the chip (a single layer).
 static int q4_ksplit(size_t max_ns, size_t min_ns, size_t n_rg_total, int num_cus) {
     int k = 1;
-    while (k < 4 && max_ns > (size_t)(Q4_U * k)) k *= 2;
+    while (k < 4 && max_ns > (size_t)(2 * Q4_U * k)) k *= 2;
     while (k < 4 && min_ns >= (size_t)(2 * k) && n_rg_total * k < (size_t)num_cus * 8) k *= 2;
     return k;
 }
