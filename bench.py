@@ -242,7 +242,7 @@ def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=20, prefill_b=2048):
     ws = torch.empty(S.workspace_size(), dtype=torch.uint8, device="cuda")
     def token():
         S.decode_dev(x, y, ws, ws.numel(), st)
-    for _ in range(3):
+    for _ in range(100):  # ~10 ms: the clocks settle (3 tokens read ~10 % slow)
         token()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -312,7 +312,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--only", choices=["gemm", "sage", "cfg3"],

@@ -10,6 +10,12 @@ quantibbler_amd/libqbk.so, which the ctypes binding loads.  Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                 no packed FP32 VALU ops (the host pass warns
                                 that it does not know the feature; harmless)
+Per source (EXTRA):
+  decode.hip: -mllvm -amdgpu-mfma-vgpr-form=1
+                                MFMA accumulators in VGPRs: the GEMV's
+                                accumulators cross branches (partial load
+                                steps), and in AGPRs every crossing copied
+                                all sixteen of them
 """
 from __future__ import annotations
 
@@ -31,11 +37,14 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
+EXTRA = {
+    "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(ln for ln in (res.stderr or "").splitlines() if noise not in ln)

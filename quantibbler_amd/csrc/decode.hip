@@ -14,7 +14,8 @@
 // A launch covers any set of layers (any shapes): each stage reads a device
 // table of Q4Layer entries (factor_internal.h) and finds its layer from the
 // workgroup index.  Three launches per decode:
-//   1. q4_prep_kernel: x -> stage 1's fp8 operand;
+//   1. q4_prep_kernel (q4_prep_flat_kernel at batch 1 when every din is a
+//      multiple of 128): x -> stage 1's fp8 operand;
 //   2. q4_gemv_kernel<1>: t = bf16(Vb^T z), written by the epilogue straight
 //      into stage 2's fp8 operand;
 //   3. q4_gemv_kernel<2>: y = bf16(Ub t) * s1 + bias.
@@ -94,15 +95,76 @@ __device__ __forceinline__ int e8m0_of(float amax) {
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
+// One run of 16 activations z = bf16(s2 * x) as stage 1's fp8 operand:
+// z splits exactly into hi + lo, each fp8 e4m3 part keeping 4 significant
+// bits relative to its block's E8M0 exponent (e_hi from the block max of z,
+// e_lo from the block max of the residual).  The E8M0 scale given by MFMA
+// lane group G covers the activations k = 128s + kq4(G, e) (measured on
+// gfx950): the two runs 16(G>>1) + 64(G&1) + {0, 32}, i.e. runs r and r^2, so
+// the block max is one shuffle away -- the calling lanes must hold runs r
+// and r^2 of a slice at lane distance 2.
+__device__ __forceinline__ void q4_run_operand(float z[16], uint32_t hw[4], uint32_t lw[4], int &e_hi,
+                                               int &e_lo) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(z[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+    const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+    float rmax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
+        hw[q] = (uint32_t)w;
+        z[4 * q] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
+        z[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
+        z[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
+        z[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+#pragma unroll
+        for (int u = 0; u < 4; u++) rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
+    }
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
+    e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+    const float inv_lo = pow2f(-e_lo);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
+        lw[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
+    }
+}
+
+// z = bf16(s2 * x) of 16 bf16 activations (two 16-byte words) and their s2.
+__device__ __forceinline__ void q4_run_z(const u32x4_t xr[2], const u32x4_t sr[4], float z[16]) {
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            z[8 * q + 2 * h] = bf16_to_f32(xr[q][h] & 0xffff);
+            z[8 * q + 2 * h + 1] = bf16_to_f32(xr[q][h] >> 16);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            z[4 * q + u] = bf16_to_f32(f32_to_bf16(__uint_as_float(sr[q][u]) * z[4 * q + u]));
+    }
+}
+
+// Where run r (of slice u, token b) of a step's operand lives in the layout
+// [slice][4 lane groups][ncol][32 B]: lane group 2(r>>2) + ((r>>1)&1), byte
+// offset 16(r&1); hi in column 2b, lo in 2b + 1.  Its two scale bytes (hi,
+// lo) sit in [slice][4][ncol] at group 2(r&1) + (r>>2) when r & 2 == 0.
+__device__ __forceinline__ size_t q4_run_slot(size_t slice, int r, int ncol, int b) {
+    return (slice * 4 + 2 * (r >> 2) + ((r >> 1) & 1)) * ncol + 2 * b;
+}
+__device__ __forceinline__ size_t q4_run_scale(size_t slice, int r, int ncol, int b) {
+    return (slice * 4 + 2 * (r & 1) + (r >> 2)) * ncol + 2 * b;
+}
+
 // x -> stage 1's fp8 operand.  Workgroup (x, layer); one thread per run of
 // 16 activations: (token b, slice s, run r) covers k = 128s + 16r .. +15.
-// The E8M0 scale given by MFMA lane group G covers the activations k =
-// 128s + kq4(G, e) (measured on gfx950): the two runs 16(G>>1) + 64(G&1) +
-// {0, 32}, i.e. runs r and r^2 with G = 2(r&1) + (r>>2), so the block max is
-// one shuffle away.  Run r's bytes go to B lane group 2(r>>2) + ((r>>1)&1)
-// at byte offset 16(r&1): one uint4 for hi (column 2b), one for lo (2b + 1).
-// z = bf16(s2 * x) splits exactly into hi + lo: each fp8 e4m3 part keeps 4
-// significant bits relative to the block max's exponent.
 template <bool XF32>
 __global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a) {
     const uint32_t li = blockIdx.y;
@@ -124,32 +186,21 @@ __global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a) {
         const float *srcf = (const float *)a.act + off;
         const float *s2 = L.s_in;
         if (a.vec_ok && k0 + 15 < L.k_valid) {
-            float v[16];
+            u32x4_t sr[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) sr[q] = *(const u32x4_t *)(s2 + k0 + 4 * q);
             if (XF32) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const float4 f = *(const float4 *)(srcf + k0 + 4 * q);
-                    v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+                    const float v[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        z[4 * q + u] = bf16_to_f32(f32_to_bf16(__uint_as_float(sr[q][u]) * v[u]));
                 }
             } else {
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    const uint4 u = *(const uint4 *)(src + k0 + 8 * q);
-                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                    for (int h = 0; h < 4; h++) {
-                        v[8 * q + 2 * h] = bf16_to_f32(w[h] & 0xffff);
-                        v[8 * q + 2 * h + 1] = bf16_to_f32(w[h] >> 16);
-                    }
-                }
-            }
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 f = *(const float4 *)(s2 + k0 + 4 * q);
-                z[4 * q] = bf16_to_f32(f32_to_bf16(f.x * v[4 * q]));
-                z[4 * q + 1] = bf16_to_f32(f32_to_bf16(f.y * v[4 * q + 1]));
-                z[4 * q + 2] = bf16_to_f32(f32_to_bf16(f.z * v[4 * q + 2]));
-                z[4 * q + 3] = bf16_to_f32(f32_to_bf16(f.w * v[4 * q + 3]));
+                const u32x4_t xr[2] = {*(const u32x4_t *)(src + k0), *(const u32x4_t *)(src + k0 + 8)};
+                q4_run_z(xr, sr, z);
             }
         } else {
 #pragma unroll
@@ -161,45 +212,51 @@ __global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a) {
             }
         }
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(z[e]));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
-    const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
     uint32_t hw[4], lw[4];
-    float rmax = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
-        hw[q] = (uint32_t)w;
-        z[4 * q] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
-        z[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
-        z[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
-        z[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
-#pragma unroll
-        for (int u = 0; u < 4; u++) rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
-    }
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
-    const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
-    const float inv_lo = pow2f(-e_lo);
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
-        lw[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
-    }
+    int e_hi, e_lo;
+    q4_run_operand(z, hw, lw, e_hi, e_lo);
     if (!live) return;
-    const size_t gb = 2 * (r >> 2) + ((r >> 1) & 1);
-    const size_t slot = ((L.slice0 + s) * 4 + gb) * a.ncol + 2 * b;  // hi column; lo is slot + 1
+    const size_t slot = q4_run_slot(L.slice0 + s, r, a.ncol, b);  // hi column; lo is slot + 1
     const size_t byte = 16 * (r & 1);
     *(uint4 *)(a.op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     *(uint4 *)(a.op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     if ((r & 2) == 0) {
-        const size_t sc = ((L.slice0 + s) * 4 + 2 * (r & 1) + (r >> 2)) * a.ncol + 2 * b;
+        const size_t sc = q4_run_scale(L.slice0 + s, r, a.ncol, b);
         a.sc[sc] = (uint8_t)(e_hi + 127);
         a.sc[sc + 1] = (uint8_t)(e_lo + 127);
     }
+}
+
+// The same at batch 1 when every din is a multiple of 128: x is then the
+// concatenation of the layers' inputs and stage 1's slices follow the same
+// order, so run t (k = 16t .. 16t + 15 of the concatenated x) belongs to
+// global slice t / 8, and s2cat holds the layers' s2 concatenated the same
+// way -- no per-layer table lookup ahead of the loads (one dependent memory
+// round trip instead of two).
+__global__ void __launch_bounds__(256) q4_prep_flat_kernel(const uint16_t *x, const float *s2cat, uint8_t *op,
+                                                           uint8_t *sc, uint32_t n_runs) {
+    const uint32_t t0 = blockIdx.x * 256 + threadIdx.x;
+    const bool live = t0 < n_runs;
+    // lanes past the end shadow the last slice's runs (n_runs is a multiple
+    // of 8, so a shuffle partner at distance 2 shadows the same slice)
+    const uint32_t t = live ? t0 : n_runs - 8 + (t0 & 7);
+    const size_t k0 = (size_t)t * 16;
+    const gu32x4_t *xs = (const gu32x4_t *)(x + k0);
+    const gu32x4_t *ss = (const gu32x4_t *)(s2cat + k0);
+    const u32x4_t xr[2] = {xs[0], xs[1]};
+    const u32x4_t sr[4] = {ss[0], ss[1], ss[2], ss[3]};
+    float z[16];
+    q4_run_z(xr, sr, z);
+    uint32_t hw[4], lw[4];
+    int e_hi, e_lo;
+    q4_run_operand(z, hw, lw, e_hi, e_lo);
+    if (!live) return;
+    const int r = (int)(t & 7);
+    const size_t slot = q4_run_slot(t >> 3, r, 2, 0), byte = 16 * (r & 1);
+    *(uint4 *)(op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if ((r & 2) == 0)
+        *(uint16_t *)(sc + q4_run_scale(t >> 3, r, 2, 0)) = (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
 }
 
 // Signs of one 16-row tile as fp4 e2m1: nibble e of VGPR j carries bit
@@ -497,6 +554,7 @@ struct Q4Geom {
     size_t n_layers, batch, ncol;
     size_t ns1_tot, ns2_tot, max_ns1;
     bool din_mult8;  // every layer's din % 8 == 0: x blocks and rows start 16-byte aligned
+    bool din_mult128;  // every layer's din % 128 == 0: stage 1's slices are all valid
     int ks1, ks2;
     uint32_t n_wg1, n_wg2;
     size_t o_op1, o_sc1, o_op2, o_sc2, bytes;  // workspace regions
@@ -524,7 +582,11 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
     }
     G.max_ns1 = max1;
     G.din_mult8 = true;
-    for (size_t i = 0; i < n; i++) G.din_mult8 = G.din_mult8 && layers[i]->din % 8 == 0;
+    G.din_mult128 = true;
+    for (size_t i = 0; i < n; i++) {
+        G.din_mult8 = G.din_mult8 && layers[i]->din % 8 == 0;
+        G.din_mult128 = G.din_mult128 && layers[i]->din % 128 == 0;
+    }
     G.ks1 = q4_ksplit(max1, min1, rg1, num_cus);
     G.ks2 = q4_ksplit(max2, min2, rg2, num_cus);
     const size_t rpw1 = 4 / G.ks1, rpw2 = 4 / G.ks2;
@@ -584,10 +646,11 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
 // One phase of a decode over the table `tab` (device; stage-1 entries
 // [0, n), stage-2 entries [n, 2n)) and, for several layers, the per-
 // workgroup layer tables wg1 (stage 1) and wg2.  Phase 1: x -> stage 1's
-// operand; 2: stage 1 (writes stage 2's operand); 3: stage 2 -> y.
+// operand; 2: stage 1 (writes stage 2's operand); 3: stage 2 -> y.  s2cat:
+// the layers' s2 concatenated (null when some din is not a multiple of 128).
 static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32_t *wg1,
-                    const uint32_t *wg2, const void *x, bool xf32, void *y, bool ybf16, void *ws,
-                    hipStream_t s) {
+                    const uint32_t *wg2, const float *s2cat, const void *x, bool xf32, void *y, bool ybf16,
+                    void *ws, hipStream_t s) {
     char *w = (char *)ws;
     Q4Args a{};
     a.c7 = 0x77777777u;
@@ -613,6 +676,13 @@ static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32
         a.wg_layer = wg2;
     }
     if (phase == 1) {
+        if (s2cat && !xf32 && G.batch == 1 && G.din_mult128 && (uintptr_t)x % 16 == 0) {
+            const uint32_t n_runs = (uint32_t)(G.ns1_tot * 8);
+            hipLaunchKernelGGL(q4_prep_flat_kernel, dim3((unsigned)div_ceil(n_runs, 256)), dim3(256), 0, s,
+                               (const uint16_t *)x, s2cat, a.op, a.sc, n_runs);
+            QBK_HIP(hipGetLastError());
+            return QBK_OK;
+        }
         // 16-byte vector loads of x: every layer's x block and token row
         // start 16-byte aligned when x is and every din is a multiple of 8
         a.vec_ok = G.din_mult8 && (uintptr_t)x % 16 == 0;
@@ -665,8 +735,9 @@ int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y,
     Q4Layer tab[2];
     Q4Geom G;
     q4_build(&L, 1, batch, L->num_cus, tab, G);  // geometry; the device table is L->q4_tab
+    const float *s2cat = G.din_mult128 ? L->s2 : nullptr;  // one layer: its own s2
     for (int ph = 1; ph <= Q4_PHASES; ph++) {
-        int rc = q4_phase(ph, G, L->q4_tab, nullptr, nullptr, x, xf32, y, ybf16, ws, s);
+        int rc = q4_phase(ph, G, L->q4_tab, nullptr, nullptr, s2cat, x, xf32, y, ybf16, ws, s);
         if (rc) return rc;
     }
     return QBK_OK;
@@ -682,6 +753,7 @@ struct qbk_factor_set {
     size_t n;
     Q4Layer *tab;          // device: [0, n) stage 1, [n, 2n) stage 2; then the
     uint32_t *wg1, *wg2;   // per-workgroup layer tables (same allocation)
+    float *s2cat;          // device: the layers' s2 concatenated (every din % 128 == 0), else null
     Q4Geom geom;           // batch 1
     std::vector<const qbk_factor *> layers;
 };
@@ -725,10 +797,21 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
     }
     S->wg1 = (uint32_t *)((char *)S->tab + tab_bytes);
     S->wg2 = S->wg1 + S->geom.n_wg1;
+    S->s2cat = nullptr;
     e1 = hipMemcpy(S->tab, h.data(), tab_bytes, hipMemcpyHostToDevice);
     if (e1 == hipSuccess) e1 = hipMemcpy(S->wg1, wl.data(), wl.size() * 4, hipMemcpyHostToDevice);
+    if (e1 == hipSuccess && S->geom.din_mult128) {
+        // the layers' s2 in x's order, for the batch-1 flat prep
+        size_t n_in = 0;
+        for (size_t i = 0; i < n; i++) n_in += layers[i]->din;
+        e1 = hipMalloc((void **)&S->s2cat, n_in * sizeof(float));
+        if (e1 != hipSuccess) S->s2cat = nullptr;
+        for (size_t i = 0, o = 0; e1 == hipSuccess && i < n; o += layers[i]->din, i++)
+            e1 = hipMemcpy(S->s2cat + o, layers[i]->s2, layers[i]->din * sizeof(float), hipMemcpyDeviceToDevice);
+    }
     if (e1 != hipSuccess) {
         (void)hipFree(S->tab);
+        if (S->s2cat) (void)hipFree(S->s2cat);
         delete S;
         return fail(QBK_ERR_DEVICE, fmt("hipMemcpy failed: %s", hipGetErrorString(e1)));
     }
@@ -742,6 +825,7 @@ void qbk_factor_set_destroy(qbk_factor_set *S) {
     (void)hipGetDevice(&cur);
     (void)hipSetDevice(S->device);
     (void)hipFree(S->tab);
+    if (S->s2cat) (void)hipFree(S->s2cat);
     (void)hipSetDevice(cur);
     delete S;
 }
@@ -758,7 +842,7 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, c
     if (workspace_size < S->geom.bytes)
         return fail(QBK_ERR_VALIDATION, fmt("workspace of %zu bytes is smaller than the %zu this call needs",
                                             workspace_size, S->geom.bytes));
-    return q4_phase(stage, S->geom, S->tab, S->wg1, S->wg2, x, false, y, true, workspace,
+    return q4_phase(stage, S->geom, S->tab, S->wg1, S->wg2, S->s2cat, x, false, y, true, workspace,
                     (hipStream_t)stream);
 }
 

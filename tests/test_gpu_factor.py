@@ -287,6 +287,33 @@ def test_set_decode_matches_single_layers(ctx, orc, dout, din, r, n):
         same(ys[i], yi[0])
 
 
+def test_decode_flat_prep_matches_layer_prep(ctx, orc):
+    """At batch 1 with every din a multiple of 128 and x 16-byte aligned,
+    stage 1's fp8 operand comes from the flat prep (run t of the whole x, no
+    per-layer lookup); with x misaligned, from the per-layer prep.  Same
+    layer, same x values (real-valued, so every rounding matters): the two
+    outputs are bit-identical."""
+    say("factor decode flat prep vs per-layer prep")
+    rng = np.random.default_rng(123)
+    for dout, din, r in [(1024, 4096, 1102), (640, 1024, 200)]:
+        L = make_layer(orc, rng, dout, din, r)
+        layer = upload(ctx, L)
+        x = orc.f32_to_bf16_fast((3.0 * rng.standard_normal(din)).astype(np.float32))
+        xa = torch.from_numpy(x.view(np.int16)).cuda()                     # aligned: flat prep
+        xm = torch.empty(din + 1, dtype=torch.int16, device="cuda")[1:]    # 2 bytes off: layer prep
+        xm.copy_(xa)
+        assert xa.data_ptr() % 16 == 0 and xm.data_ptr() % 16 != 0
+        outs = []
+        for xd in (xa, xm):
+            y = torch.empty(dout, dtype=torch.int16, device="cuda")
+            ws = torch.zeros(layer.workspace_size(1), dtype=torch.uint8, device="cuda")
+            layer.linear_dev(xd, 1, y, "bfloat16", ws, ws.numel(), torch.cuda.current_stream())
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy().view(np.uint16))
+        assert np.all(np.isfinite(orc.bf16_to_f32(outs[0])))
+        assert np.array_equal(outs[0], outs[1]), np.argwhere(outs[0] != outs[1])[:5]
+
+
 def test_mixed_shape_set_decode(ctx, orc):
     """One set over layers of different shapes (a decoder layer's q/k/v/o/
     gate/up/down, scaled down, with ragged ranks and a din that is not a
