@@ -937,6 +937,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     BLK_FRAGS(0)
+    __syncthreads();  // every wave has read K^ buffer 0 before block 2 loads into it
     size_t kb = 0;
     for (; kb + 2 <= kb_end; kb += 2) {
         BLK_ITER(kb, 0)
