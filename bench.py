@@ -194,6 +194,59 @@ def bench_sage(qa, ctx, torch, np, iters=10):
             "shape": "B=1 H=32 S=4096 d=128 causal, bf16 in/out, includes the quantisation pre-pass"}
 
 
+def bench_sage_decode(qa, ctx, torch, np, seq=4096, iters=20):
+    """One decode step of the reference scheme (engine/mod.rs:984-1030) over a
+    row-major f32 KV cache at config 3's attention shape (32 query heads,
+    8 kv heads, d = 128, block 64): the O(seq) step, and the reference's own
+    call pattern (the query in row 0 of a zero-padded seq-row problem,
+    causal=False, the cache gathered head-major) on the same device."""
+    H, Hk, D, block = 32, 8, 128, 64
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q = torch.randn((H, D), device="cuda", generator=g)
+    k = torch.randn((seq, Hk, D), device="cuda", generator=g) + 2.0 * torch.randn((1, Hk, D), device="cuda", generator=g)
+    v = torch.randn((seq, Hk, D), device="cuda", generator=g)
+    o = torch.empty((H, D), dtype=torch.float32, device="cuda")
+    sh = qa.AttentionShape(1, H, Hk, 1, seq, D, D)
+    wn = ctx.sage_decode_workspace_size(sh, block)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream()
+    def step():
+        ctx.attention_sage_decode_dev(sh, q, k, v, block, o, ws, wn, st)
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(iters):
+        step()
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / iters
+    cache_bytes = seq * Hk * 2 * D * 4
+    # the reference's call pattern, timed once after a warm-up call (its
+    # gather and padding counted as free)
+    qp = torch.zeros((1, H, seq, D), device="cuda")
+    qp[0, :, 0, :] = q
+    kp = k.permute(1, 0, 2).contiguous()[None]
+    vp = v.permute(1, 0, 2).contiguous()[None]
+    op = torch.empty((1, H, seq, D), device="cuda")
+    shp = qa.AttentionShape(1, H, Hk, seq, seq, D, D)
+    ctx.attention_sage_dev(shp, qp, kp, vp, False, block, op, st)
+    torch.cuda.synchronize()
+    a.record(st)
+    ctx.attention_sage_dev(shp, qp, kp, vp, False, block, op, st)
+    b.record(st)
+    torch.cuda.synchronize()
+    pad_ms = a.elapsed_time(b)
+    same = bool(torch.equal(op[0, :, 0, :], o))
+    log(f"  sage decode seq={seq}: {ms * 1e3:.1f} us/step ({cache_bytes / (ms * 1e-3) / 1e9:.0f} GB/s of cache); "
+        f"padded reference call {pad_ms:.2f} ms; row 0 identical: {same}")
+    return {"us_per_step": round(ms * 1e3, 1), "cache_bytes": cache_bytes,
+            "GB/s": round(cache_bytes / (ms * 1e-3) / 1e9, 1),
+            "padded_reference_call_ms": round(pad_ms, 3), "row0_bit_identical": same,
+            "shape": f"H=32 Hkv=8 d=128 seq={seq} block 64, f32 row-major cache"}
+
+
 # BASELINE.json configs[2]: the seven projections of a Llama-3-8B-shaped
 # decoder layer, ranks from the reference's planning rule at 0.55 bits/weight
 # (v2 stream, fp16 scales): (name, dout, din, r).
@@ -315,7 +368,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["gemm", "sage", "cfg3"],
+    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode"],
                     help="run one secondary workload alone and print its figures (for profiling); "
                          "no headline line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -340,6 +393,8 @@ def main():
             res = bench_gemm(torch, np, layers[0])
         elif args.only == "sage":
             res = bench_sage(qa, ctx, torch, np)
+        elif args.only == "sage_decode":
+            res = bench_sage_decode(qa, ctx, torch, np)
         else:
             res = bench_cfg3(qa, ctx, torch, np)
         print(json.dumps({"only": args.only, "result": res}), flush=True)
@@ -377,6 +432,8 @@ def main():
         extra["prefill_gemm"] = bench_gemm(torch, np, layers[0])
         log("sage attention ...")
         extra["sage_blk"] = bench_sage(qa, ctx, torch, np)
+        log("sage decode step ...")
+        extra["sage_decode"] = bench_sage_decode(qa, ctx, torch, np)
         log("config 3 (8B decoder layer projections) ...")
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")

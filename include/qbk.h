@@ -178,6 +178,24 @@ int qbk_attention_sage_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const floa
                            const float *k, const float *v, int causal, size_t block_size,
                            float *out, void *stream);
 
+/* engine/mod.rs:984-1030 gqa_attention_sage (with KvCache::keys_head_major /
+ * vals_head_major, engine/mod.rs:1236-1268): one decode step of the reference
+ * scheme above over a KV cache.  The reference pads the step's query into
+ * row 0 of a (pos + 1)-row problem, calls attention_sage with causal = false
+ * on the head-major gathered cache and reads row 0; this computes that row
+ * alone (bit-identical) in O(seq), reading the cache in place.  shape:
+ * batch 1, seq_q 1, seq_kv = pos + 1; q (n_heads, d) f32, k (seq_kv,
+ * n_kv_heads, d) and v (seq_kv, n_kv_heads, dv) f32 row-major as cached,
+ * out (n_heads, dv) f32. */
+int qbk_attention_sage_decode(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, size_t q_len,
+                              const float *k, size_t k_len, const float *v, size_t v_len,
+                              size_t block_size, float *out, size_t out_len);
+/* Device-pointer form; workspace >= qbk_sage_decode_workspace_size(). */
+size_t qbk_sage_decode_workspace_size(const qbk_attn_shape *shape, size_t block_size);
+int qbk_attention_sage_decode_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
+                                  const float *v, size_t block_size, float *out, void *workspace,
+                                  size_t workspace_size, void *stream);
+
 /* Block-scaled SageAttention prefill (no reference symbol: the scheme the
  * north_star names).  bf16 q (B,H,S,d), k (B,Hkv,S,d), v (B,Hkv,S,dv),
  * d == 128, dv == 128, seq_q == seq_kv:

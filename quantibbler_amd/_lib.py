@@ -64,6 +64,9 @@ _SIGS = {
     "qbk_factor_set_stage_dev": (_I, [_P, _P, _I, _P, _P, _P, _Z, _P]),
     "qbk_attention_sage": (_I, [_P, C.POINTER(AttnShape), _P, _Z, _P, _Z, _P, _Z, _I, _Z, _P]),
     "qbk_attention_sage_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _I, _Z, _P, _P]),
+    "qbk_attention_sage_decode": (_I, [_P, C.POINTER(AttnShape), _P, _Z, _P, _Z, _P, _Z, _Z, _P, _Z]),
+    "qbk_sage_decode_workspace_size": (_Z, [C.POINTER(AttnShape), _Z]),
+    "qbk_attention_sage_decode_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _Z, _P, _P, _Z, _P]),
     "qbk_sage_blk_workspace_size": (_Z, [C.POINTER(AttnShape)]),
     "qbk_attention_sage_blk_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _I, _P, _P, _Z, _P]),
     "qbk_sage_blk_quantize_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),

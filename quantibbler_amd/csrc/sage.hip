@@ -97,6 +97,10 @@ struct RefArgs {
     int causal;
     float inv_sqrt_d;
     size_t nkb, d4, blk4;
+    // K / V element strides between consecutive tokens of one kv head and
+    // between kv heads: head-major (B, Hk, S, d) by default; the decode
+    // step reads a row-major cache (S, Hk, d) in place
+    size_t k_tok, k_head, v_tok, v_head;
     // pre-pass products
     float *kmean;     // [B*Hk*nkb][d]
     float *kdelta;    // [B*Hk*S]
@@ -114,62 +118,152 @@ struct RefArgs {
 // Pre-pass: one workgroup per (kv head, key block).  gpu_attention.rs:192-204
 // (block mean, sequential over the block's tokens), :211-226 (per-token peak
 // and delta), :232-251 (codes), :290-309 (per-channel V scale), :352-370.
+// The f32 operations are the reference's; the block's K (then V) is staged
+// through LDS in chunks of REF_PREP_CH(maxd) tokens with coalesced loads --
+// a block that fits is read from memory once -- and the work is spread so
+// that every thread has some: a thread per channel for the sums and V, a
+// wave per token for K (lane l holds channels 4l .. 4l+3 -- the peak is a
+// max, so a wave reduction gives the reference's value -- and writes their
+// code word).
+#define REF_PREP_LDS 61440  // with the static arrays, within the 64 KiB a launch gets by default
+__host__ __device__ __forceinline__ size_t ref_prep_ch(size_t maxd) {
+    return (REF_PREP_LDS / (4 * maxd)) & ~(size_t)3;  // tokens per LDS chunk (a multiple of 4)
+}
+
 __global__ void __launch_bounds__(256) sage_ref_prep(RefArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float tile[];  // [ch][maxd]
     __shared__ float km[REF_MAXD];
     const size_t kb = blockIdx.x, bk = blockIdx.y;
     const size_t j0 = kb * a.block;
     const size_t j1 = j0 + a.block < a.S ? j0 + a.block : a.S;
     const size_t kj = j1 - j0;
-    const float *K = a.k + bk * a.S * a.d;
-    const float *V = a.v + bk * a.S * a.dv;
-    for (size_t c = threadIdx.x; c < a.d; c += blockDim.x) {
-        float ssum = 0.0f;
-        for (size_t jj = j0; jj < j1; jj++) ssum += K[jj * a.d + c];
-        float m = ssum / (float)kj;
-        km[c] = m;
-        a.kmean[(bk * a.nkb + kb) * a.d + c] = m;
+    const float *K = a.k + bk * a.k_head;
+    const float *V = a.v + bk * a.v_head;
+    const size_t maxd = a.d > a.dv ? a.d : a.dv, CH = ref_prep_ch(maxd);
+    const bool one = kj <= CH;  // the whole block in one chunk: load once
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwave = nt >> 6;
+    // tokens t0 .. t0+tc-1 (w channels each) into the tile: a wave per token,
+    // four tokens a pass, every load of the pass issued before its stores
+    // (indices clamped into the chunk, so the loads are unconditional)
+    auto stage = [&](const float *X, size_t tok, size_t t0, size_t tc, size_t w) {
+        __syncthreads();
+        for (size_t tb = 0; tb < tc; tb += 4 * (size_t)nwave) {
+            float v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                size_t t = tb + (size_t)(u * nwave + wave);
+                t = t < tc ? t : tc - 1;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    size_t c = (size_t)(lane + 64 * e);
+                    c = c < w ? c : w - 1;
+                    v[u][e] = X[(t0 + t) * tok + c];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const size_t t = tb + (size_t)(u * nwave + wave);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const size_t c = (size_t)(lane + 64 * e);
+                    if (t < tc && c < w) tile[t * maxd + c] = v[u][e];
+                }
+            }
+        }
+        __syncthreads();
+    };
+    // block mean of K, sequential over the tokens
+    float ssum = 0.0f;
+    for (size_t t0 = j0; t0 < j1; t0 += CH) {
+        const size_t tc = j1 - t0 < CH ? j1 - t0 : CH;
+        stage(K, a.k_tok, t0, tc, a.d);
+        if ((size_t)tid < a.d)
+            for (size_t t = 0; t < tc; t++) ssum += tile[t * maxd + tid];
+    }
+    if ((size_t)tid < a.d) {
+        const float m = ssum / (float)kj;
+        km[tid] = m;
+        a.kmean[(bk * a.nkb + kb) * a.d + tid] = m;
     }
     __syncthreads();
-    for (size_t jj = j0 + threadIdx.x; jj < j1; jj += blockDim.x) {
-        const float *kt = K + jj * a.d;
-        float kpeak = 0.0f;
-        for (size_t c = 0; c < a.d; c++) {
-            float g = kt[c] - km[c];
-            float ag = g < 0.0f ? 0.0f - g : g;
-            if (ag > kpeak) kpeak = ag;
-        }
-        float kdelta = 1.0f;
-        if (kpeak > 0.0f) kdelta = kpeak / 127.0f;
-        a.kdelta[bk * a.S + jj] = kdelta;
-        uint32_t *dst = a.khat + (bk * a.S + jj) * a.d4;
-        for (size_t w = 0; w < a.d4; w++) {
-            int c4[4];
+    // per-token peak, delta and codes: a wave per token, or a half-wave per
+    // token when the codes fit in 32 words (d <= 128)
+    const bool half = a.d4 <= 32;
+    const int tpw = half ? 2 : 1, sub = half ? lane >> 5 : 0, wl = half ? lane & 31 : lane;
+    const size_t c0 = 4 * (size_t)wl;  // this lane's channels
+    for (size_t t0 = j0; t0 < j1; t0 += CH) {
+        const size_t tc = j1 - t0 < CH ? j1 - t0 : CH;
+        if (!one) stage(K, a.k_tok, t0, tc, a.d);
+        for (size_t tb = (size_t)(wave * tpw); tb < tc; tb += (size_t)(nwave * tpw)) {
+            const size_t t = tb + sub < tc ? tb + sub : tc - 1;  // a past-the-end half repeats a token
+            const size_t jj = t0 + t;
+            float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            float kpeak = 0.0f;
             for (int e = 0; e < 4; e++) {
-                size_t c = 4 * w + e;
-                c4[e] = c < a.d ? q8((kt[c] - km[c]) / kdelta) : 0;
+                const size_t c = c0 + e;
+                if (c < a.d) {
+                    g[e] = tile[t * maxd + c] - km[c];
+                    float ag = g[e] < 0.0f ? 0.0f - g[e] : g[e];
+                    if (ag > kpeak) kpeak = ag;
+                }
             }
-            dst[w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+            for (int o = half ? 16 : 32; o >= 1; o >>= 1) {
+                const float w = __shfl_xor(kpeak, o, 64);
+                kpeak = w > kpeak ? w : kpeak;
+            }
+            float kdelta = 1.0f;
+            if (kpeak > 0.0f) kdelta = kpeak / 127.0f;
+            if (wl == 0) a.kdelta[bk * a.S + jj] = kdelta;
+            if ((size_t)wl < a.d4) {
+                int c4[4];
+                for (int e = 0; e < 4; e++) c4[e] = c0 + e < a.d ? q8(g[e] / kdelta) : 0;
+                a.khat[(bk * a.S + jj) * a.d4 + wl] = pack4(c4[0], c4[1], c4[2], c4[3]);
+            }
         }
     }
-    for (size_t c = threadIdx.x; c < a.dv; c += blockDim.x) {
-        float vpeak = 0.0f;
-        for (size_t jj = j0; jj < j1; jj++) {
-            float x = V[jj * a.dv + c];
-            float ax = x < 0.0f ? 0.0f - x : x;
-            if (ax > vpeak) vpeak = ax;
-        }
-        float vd = vpeak > 0.0f ? vpeak / 127.0f : 1.0f;
-        a.vd[(bk * a.nkb + kb) * a.dv + c] = vd;
-        uint32_t *dst = a.vhat + ((bk * a.nkb + kb) * a.dv + c) * a.blk4;
-        for (size_t w = 0; w < a.blk4; w++) {
+    // V: per-channel peak over the block, then codes four tokens a word
+    float vpeak = 0.0f;
+    for (size_t t0 = j0; t0 < j1; t0 += CH) {
+        const size_t tc = j1 - t0 < CH ? j1 - t0 : CH;
+        stage(V, a.v_tok, t0, tc, a.dv);
+        if ((size_t)tid < a.dv)
+            for (size_t t = 0; t < tc; t++) {
+                float x = tile[t * maxd + tid];
+                float ax = x < 0.0f ? 0.0f - x : x;
+                if (ax > vpeak) vpeak = ax;
+            }
+    }
+    if ((size_t)tid < a.dv) {
+        const float vd = vpeak > 0.0f ? vpeak / 127.0f : 1.0f;
+        km[tid] = vd;  // the K means are no longer needed
+        a.vd[(bk * a.nkb + kb) * a.dv + tid] = vd;
+    }
+    __syncthreads();
+    // codes four tokens a word, the (channel, word) items over every thread
+    const uint32_t dv = (uint32_t)a.dv;
+    uint32_t *vrow = a.vhat + (bk * a.nkb + kb) * a.dv * a.blk4;
+    for (size_t t0 = j0; t0 < j1; t0 += CH) {
+        const size_t tc = j1 - t0 < CH ? j1 - t0 : CH;
+        if (!one) stage(V, a.v_tok, t0, tc, a.dv);
+        const uint32_t tw = (uint32_t)((tc + 3) / 4);
+        for (uint32_t x = tid; x < dv * tw; x += nt) {
+            const uint32_t c = x % dv, w = x / dv;
+            const float vd = km[c];
             int c4[4];
             for (int e = 0; e < 4; e++) {
-                size_t jj = j0 + 4 * w + e;
-                c4[e] = jj < j1 ? q8(V[jj * a.dv + c] / vd) : 0;
+                const size_t t = 4 * w + e;
+                c4[e] = t < tc ? q8(tile[t * maxd + c] / vd) : 0;
             }
-            dst[w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+            vrow[c * a.blk4 + (t0 - j0) / 4 + w] = pack4(c4[0], c4[1], c4[2], c4[3]);
         }
     }
+}
+
+// LDS bytes of a sage_ref_prep launch
+static size_t ref_prep_lds(size_t d, size_t dv, size_t block) {
+    const size_t maxd = d > dv ? d : dv, ch = ref_prep_ch(maxd);
+    return 4 * maxd * (block < ch ? block : ch);
 }
 
 // Main pass: gpu_attention.rs:89-396 for REF_ROWS consecutive query rows of
@@ -415,6 +509,10 @@ static RefPlan ref_plan(const qbk_attn_shape *s, size_t block) {
     a.blk4 = div_ceil(block < a.S ? block : a.S, 4);
     a.sc_lds = block <= REF_CH;
     a.out_lds = a.dv <= 64;
+    a.k_tok = a.d;
+    a.k_head = a.S * a.d;
+    a.v_tok = a.dv;
+    a.v_head = a.S * a.dv;
     const size_t rows = a.B * a.H * a.S, bk = a.B * a.Hk;
     size_t off = 0;
     auto take = [&](size_t n) {
@@ -458,11 +556,366 @@ static int run_ref(const qbk_attn_shape *s, const float *q, const float *k, cons
     a.gph = (uint32_t *)(w + P.off_gph);
     a.gpv = (int *)(w + P.off_gpv);
     a.gout = (float *)(w + P.off_gout);
-    hipLaunchKernelGGL(sage_ref_prep, dim3((unsigned)a.nkb, (unsigned)(a.B * a.Hk)), dim3(256), 0,
-                       st, a);
+    hipLaunchKernelGGL(sage_ref_prep, dim3((unsigned)a.nkb, (unsigned)(a.B * a.Hk)), dim3(256),
+                       ref_prep_lds(a.d, a.dv, a.block), st, a);
     QBK_HIP(hipGetLastError());
     hipLaunchKernelGGL(sage_ref_main, dim3((unsigned)div_ceil(a.S, REF_ROWS), (unsigned)(a.B * a.H)),
                        dim3(REF_ROWS), P.lds_bytes, st, a);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+// ----------------------------------------------------------------------
+// 1b. one decode step of the reference scheme over a KV cache
+// ----------------------------------------------------------------------
+//
+// engine/mod.rs:984-1030 (gqa_attention_sage) pads the one query of a decode
+// step into row 0 of a (pos + 1)-row problem, runs the scheme with causal =
+// false and reads row 0.  Row i of the scheme depends only on query i and
+// the cache (Q is quantised per row, K and V per key block), so row 0 alone
+// is that step -- here in O(seq) instead of O(seq^2): the key-block loop
+// that the main pass runs within one lane is spread over workgroups, each
+// f32 value formed by the same operations in the same order (the sums that
+// the main pass makes sequential stay sequential; the maxima and integer
+// dot products are order-free).  The pre-pass reads the row-major cache
+// (seq, n_kv_heads, d) in place -- the layout KvCache::head_major gathers
+// from (engine/mod.rs:1236-1268).
+//   sage_dec_scores  (key block, head): the block's shift, scores, max
+//   sage_dec_stats   (head): the running max, live flag and alpha per block
+//   sage_dec_pv      (key block, head): p, their sum in key order, P codes,
+//                    and each channel's (P^.V^)/127 * dv term of the block
+//   sage_dec_combine (head): l and O over the blocks in order, then O / l
+
+#define DEC_CH 4096  // keys of a block whose p and codes sit in LDS at once
+
+struct DecArgs {
+    RefArgs r;                           // shape (S = seq_kv), pre-pass products
+    float *sc;                           // [H][S] scores, then p
+    float *bmax, *bm, *balpha, *besum;   // [H][nkb]
+    int *blive;                          // [H][nkb]
+    float *pvt;                          // [H][nkb][dv]
+};
+
+// max over the workgroup (blockDim.x a multiple of 64, <= 1024)
+__device__ __forceinline__ float dec_wg_max(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wv] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int i = 1; i < nw; i++) m = red[i] > m ? red[i] : m;
+    return m;
+}
+
+__global__ void __launch_bounds__(256) sage_dec_scores(DecArgs da) {
+    const RefArgs &a = da.r;
+    __shared__ uint32_t qs[REF_MAXD / 4];
+    __shared__ float kms[REF_MAXD];
+    __shared__ float red[4];
+    __shared__ float shv;
+    const int tid = threadIdx.x;
+    const size_t kb = blockIdx.x, h = blockIdx.y;
+    const size_t bk = h / (a.H / a.Hk);
+    // psi_Q of the query (gpu_attention.rs:113-159; the peak is a max)
+    const float *qi = a.q + h * a.d;
+    float pk = 0.0f;
+    for (size_t c = tid; c < a.d; c += blockDim.x) {
+        const float x = qi[c] * a.inv_sqrt_d;
+        const float ax = x < 0.0f ? 0.0f - x : x;
+        if (ax > pk) pk = ax;
+    }
+    const float qpeak = dec_wg_max(pk, red);
+    const float qdelta = qpeak > 0.0f ? qpeak / 127.0f : 1.0f;
+    for (size_t w = tid; w < a.d4; w += blockDim.x) {
+        int c4[4];
+        for (int e = 0; e < 4; e++) {
+            const size_t c = 4 * w + e;
+            c4[e] = c < a.d ? q8((qi[c] * a.inv_sqrt_d) / qdelta) : 0;
+        }
+        qs[w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+    }
+    for (size_t c = tid; c < a.d; c += blockDim.x) kms[c] = a.kmean[(bk * a.nkb + kb) * a.d + c];
+    __syncthreads();
+    // shift = sum_c (q^_c * dq) * kmean_c in element order (:253)
+    if (tid == 0) {
+        float shift = 0.0f;
+        for (size_t c = 0; c < a.d; c++) {
+            const int qc = (int)(int8_t)(qs[c / 4] >> (8 * (c % 4)));
+            shift += ((float)qc * qdelta) * kms[c];
+        }
+        shv = shift;
+    }
+    __syncthreads();
+    const float shift = shv;
+    const size_t j0 = kb * a.block, j1 = j0 + a.block < a.S ? j0 + a.block : a.S;
+    float rm = MASKED;
+    for (size_t jj = j0 + tid; jj < j1; jj += blockDim.x) {
+        const uint32_t *kc = a.khat + (bk * a.S + jj) * a.d4;
+        int acc = 0;
+        for (size_t w = 0; w < a.d4; w++) acc = __builtin_amdgcn_sdot4((int)qs[w], (int)kc[w], acc, false);
+        const float sv = (float)acc * qdelta * a.kdelta[bk * a.S + jj] + shift;
+        da.sc[h * a.S + jj] = sv;
+        if (sv > rm) rm = sv;
+    }
+    rm = dec_wg_max(rm, red);
+    if (tid == 0) da.bmax[h * a.nkb + kb] = rm;
+}
+
+// :288-296 per block in order (m_new, live), then alpha per block; the
+// blocks' maxima staged through LDS 64 at a time for the sequential scan
+__global__ void __launch_bounds__(64) sage_dec_stats(DecArgs da) {
+    const RefArgs &a = da.r;
+    __shared__ float sm[64];
+    __shared__ float carry, cin;
+    const int tid = threadIdx.x;
+    const size_t h = blockIdx.x, nkb = a.nkb;
+    if (tid == 0) carry = MASKED;
+    for (size_t kb0 = 0; kb0 < nkb; kb0 += 64) {
+        const size_t n = nkb - kb0 < 64 ? nkb - kb0 : 64;
+        __syncthreads();
+        if ((size_t)tid < n) sm[tid] = da.bmax[h * nkb + kb0 + tid];
+        __syncthreads();
+        if (tid == 0) {
+            float m = carry;
+            cin = m;
+            for (size_t i = 0; i < n; i++) {
+                float m_new = m;
+                if (sm[i] > m_new) m_new = sm[i];
+                sm[i] = m_new;
+                m = m_new;
+            }
+            carry = m;
+        }
+        __syncthreads();
+        if ((size_t)tid < n) {
+            const size_t kb = kb0 + tid;
+            const float m_new = sm[tid], m = tid ? sm[tid - 1] : cin;
+            const int live = !(m_new < MASKED * 0.5f);
+            da.bm[h * nkb + kb] = m_new;
+            da.blive[h * nkb + kb] = live;
+            da.balpha[h * nkb + kb] = live ? qbk_expf(m - m_new) : 0.0f;
+        }
+    }
+}
+
+// :297-316 (p, esum in key order, codes) and :317-341 (P^.V^ per channel)
+__global__ void __launch_bounds__(256) sage_dec_pv(DecArgs da) {
+    const RefArgs &a = da.r;
+    __shared__ float pf[DEC_CH];
+    __shared__ uint32_t ph[DEC_CH / 4];
+    const int tid = threadIdx.x;
+    const size_t kb = blockIdx.x, h = blockIdx.y, nkb = a.nkb;
+    const size_t bk = h / (a.H / a.Hk);
+    const size_t j0 = kb * a.block, j1 = j0 + a.block < a.S ? j0 + a.block : a.S;
+    const int live = da.blive[h * nkb + kb];
+    const float m_new = da.bm[h * nkb + kb];
+    const uint32_t *vh = a.vhat + (bk * nkb + kb) * a.dv * a.blk4;
+    float esum = 0.0f;  // thread 0's running sum
+    int pv = 0;         // thread c's P^.V^ over the block (dv <= the 256 threads)
+    for (size_t t0 = j0; t0 < j1; t0 += DEC_CH) {
+        const size_t tc = j1 - t0 < DEC_CH ? j1 - t0 : DEC_CH, tw = (tc + 3) / 4;
+        __syncthreads();
+        for (size_t w = tid; w < tw; w += blockDim.x) {
+            int c4[4];
+            for (int e = 0; e < 4; e++) {
+                const size_t t = 4 * w + e;
+                int pc = 0;
+                if (t < tc) {
+                    const float p = live ? qbk_expf(da.sc[h * a.S + t0 + t] - m_new) : 0.0f;
+                    pf[t] = p;
+                    float pr = __builtin_rintf(p * 127.0f);
+                    pr = pr > 127.0f ? 127.0f : pr;
+                    pr = pr < 0.0f ? 0.0f : pr;
+                    pc = (int)pr;
+                }
+                c4[e] = pc;
+            }
+            ph[w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+        }
+        __syncthreads();
+        if (tid == 0)
+            for (size_t t = 0; t < tc; t++) esum += pf[t];
+        if ((size_t)tid < a.dv) {
+            const uint32_t *vc = vh + tid * a.blk4 + (t0 - j0) / 4;
+            for (size_t w = 0; w < tw; w++) pv = __builtin_amdgcn_sdot4((int)ph[w], (int)vc[w], pv, false);
+        }
+    }
+    if (tid == 0) da.besum[h * nkb + kb] = esum;
+    if ((size_t)tid < a.dv)
+        da.pvt[(h * nkb + kb) * a.dv + tid] = (float)pv * (1.0f / 127.0f) * a.vd[(bk * nkb + kb) * a.dv + tid];
+}
+
+// :315 and :337-338 over the blocks in order, then :346; the blocks'
+// alpha, esum and live flags staged through LDS, each thread's P.V terms
+// loaded eight blocks at a time ahead of the recurrence
+__global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da) {
+    const RefArgs &a = da.r;
+    __shared__ float sa[64], se[64];
+    __shared__ int sl[64];
+    const size_t h = blockIdx.x, nkb = a.nkb;
+    const int tid = threadIdx.x;
+    const size_t c = tid;
+    const bool act = c < a.dv;
+    float o = 0.0f, ell = 0.0f;
+    for (size_t kb0 = 0; kb0 < nkb; kb0 += 64) {
+        const size_t n = nkb - kb0 < 64 ? nkb - kb0 : 64;
+        __syncthreads();
+        if ((size_t)tid < n) {
+            sa[tid] = da.balpha[h * nkb + kb0 + tid];
+            se[tid] = da.besum[h * nkb + kb0 + tid];
+            sl[tid] = da.blive[h * nkb + kb0 + tid];
+        }
+        __syncthreads();
+        for (size_t i0 = 0; i0 < n; i0 += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                t[u] = act && i0 + u < n ? da.pvt[(h * nkb + kb0 + i0 + u) * a.dv + c] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (i0 + u >= n) break;
+                const float alpha = sa[i0 + u];
+                ell = alpha * ell + se[i0 + u];
+                const float prev = sl[i0 + u] ? o : 0.0f;
+                o = alpha * prev + t[u];
+            }
+        }
+    }
+    if (act) a.out[h * a.dv + c] = o / ell;
+}
+
+struct DecPlan {
+    DecArgs da;
+    size_t ws;
+    size_t o_kmean, o_kdelta, o_khat, o_vd, o_vhat, o_sc, o_bmax, o_bm, o_balpha, o_besum, o_blive, o_pvt;
+};
+
+static DecPlan dec_plan(const qbk_attn_shape *s, size_t block) {
+    DecPlan P{};
+    RefArgs &a = P.da.r;
+    a.B = 1;
+    a.H = s->n_heads;
+    a.Hk = s->n_kv_heads;
+    a.S = s->seq_kv;
+    a.d = s->head_dim;
+    a.dv = s->val_dim;
+    a.block = block;
+    a.causal = 0;
+    a.inv_sqrt_d = 1.0f / sqrtf((float)a.d);
+    a.nkb = div_ceil(a.S, block);
+    a.d4 = div_ceil(a.d, 4);
+    a.blk4 = div_ceil(block < a.S ? block : a.S, 4);
+    // the cache's row-major layout (seq, n_kv_heads, d)
+    a.k_tok = a.Hk * a.d;
+    a.k_head = a.d;
+    a.v_tok = a.Hk * a.dv;
+    a.v_head = a.dv;
+    const size_t bk = a.Hk, H = a.H;
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        size_t o = off;
+        off += round_up(n ? n : 4, 256);
+        return o;
+    };
+    P.o_kmean = take(bk * a.nkb * a.d * 4);
+    P.o_kdelta = take(bk * a.S * 4);
+    P.o_khat = take(bk * a.S * a.d4 * 4);
+    P.o_vd = take(bk * a.nkb * a.dv * 4);
+    P.o_vhat = take(bk * a.nkb * a.dv * a.blk4 * 4);
+    P.o_sc = take(H * a.S * 4);
+    P.o_bmax = take(H * a.nkb * 4);
+    P.o_bm = take(H * a.nkb * 4);
+    P.o_balpha = take(H * a.nkb * 4);
+    P.o_besum = take(H * a.nkb * 4);
+    P.o_blive = take(H * a.nkb * 4);
+    P.o_pvt = take(H * a.nkb * a.dv * 4);
+    P.ws = off;
+    return P;
+}
+
+// A decode step's shape: batch 1, the step's one query, the cache's keys.
+static int validate_decode(const qbk_attn_shape *s, size_t block_size, const size_t *lens) {
+    if (!s) return fail(QBK_ERR_VALIDATION, "null shape");
+    if (s->batch != 1)
+        return fail(QBK_ERR_VALIDATION, fmt("sage decode takes one sequence: batch must be 1, got %zu", s->batch));
+    if (s->n_heads == 0 || s->n_kv_heads == 0)
+        return fail(QBK_ERR_VALIDATION, "attention requires non-empty batch and head dimensions");
+    if (s->n_heads % s->n_kv_heads != 0)
+        return fail(QBK_ERR_VALIDATION, fmt("n_kv_heads must divide n_heads: n_heads=%zu, "
+                                            "n_kv_heads=%zu",
+                                            s->n_heads, s->n_kv_heads));
+    if (s->seq_q != 1)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("sage decode takes the step's one query: seq_q must be 1, got %zu", s->seq_q));
+    if (s->seq_kv == 0 || s->head_dim == 0 || s->val_dim == 0)
+        return fail(QBK_ERR_VALIDATION,
+                    "attention requires non-empty sequence and head dimensions");
+    if (block_size == 0)
+        return fail(QBK_ERR_VALIDATION,
+                    "sage attention requires a positive block_size ([SA] \xc2\xa7"
+                    "4's tile width)");
+    if (lens) {
+        const size_t eq = s->n_heads * s->head_dim, ek = s->seq_kv * s->n_kv_heads * s->head_dim,
+                     ev = s->seq_kv * s->n_kv_heads * s->val_dim, eo = s->n_heads * s->val_dim;
+        if (lens[0] != eq)
+            return fail(QBK_ERR_VALIDATION, fmt("query must hold %zu values for %s, got %zu", eq,
+                                                shape_debug(s).c_str(), lens[0]));
+        if (lens[1] != ek)
+            return fail(QBK_ERR_VALIDATION, fmt("key cache must hold %zu values for %s, got %zu", ek,
+                                                shape_debug(s).c_str(), lens[1]));
+        if (lens[2] != ev)
+            return fail(QBK_ERR_VALIDATION, fmt("value cache must hold %zu values for %s, got %zu", ev,
+                                                shape_debug(s).c_str(), lens[2]));
+        if (lens[3] != eo)
+            return fail(QBK_ERR_VALIDATION, fmt("out must hold %zu values for %s, got %zu", eo,
+                                                shape_debug(s).c_str(), lens[3]));
+    }
+    if (s->head_dim > REF_MAXD || s->val_dim > REF_MAXD)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("sage attention on this device supports head_dim and val_dim up to %d, "
+                        "got head_dim=%zu, val_dim=%zu",
+                        REF_MAXD, s->head_dim, s->val_dim));
+    return QBK_OK;
+}
+
+static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, const float *v,
+                      size_t block, float *out, void *ws, hipStream_t st) {
+    DecPlan P = dec_plan(s, block);
+    DecArgs da = P.da;
+    RefArgs &a = da.r;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    char *w = (char *)ws;
+    a.kmean = (float *)(w + P.o_kmean);
+    a.kdelta = (float *)(w + P.o_kdelta);
+    a.khat = (uint32_t *)(w + P.o_khat);
+    a.vd = (float *)(w + P.o_vd);
+    a.vhat = (uint32_t *)(w + P.o_vhat);
+    da.sc = (float *)(w + P.o_sc);
+    da.bmax = (float *)(w + P.o_bmax);
+    da.bm = (float *)(w + P.o_bm);
+    da.balpha = (float *)(w + P.o_balpha);
+    da.besum = (float *)(w + P.o_besum);
+    da.blive = (int *)(w + P.o_blive);
+    da.pvt = (float *)(w + P.o_pvt);
+    const unsigned nkb = (unsigned)a.nkb, H = (unsigned)a.H;
+    hipLaunchKernelGGL(sage_ref_prep, dim3(nkb, (unsigned)a.Hk), dim3(256), ref_prep_lds(a.d, a.dv, a.block),
+                       st, a);
+    QBK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(sage_dec_scores, dim3(nkb, H), dim3(256), 0, st, da);
+    QBK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(sage_dec_stats, dim3(H), dim3(64), 0, st, da);
+    QBK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(sage_dec_pv, dim3(nkb, H), dim3(256), 0, st, da);
+    QBK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }
@@ -1106,6 +1559,49 @@ int qbk_attention_sage_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const floa
     rc = run_ref(shape, q, k, v, causal, block_size, out, ws, (hipStream_t)stream);
     QBK_HIP(hipFreeAsync(ws, (hipStream_t)stream));
     return rc;
+}
+
+size_t qbk_sage_decode_workspace_size(const qbk_attn_shape *shape, size_t block_size) {
+    if (!shape || block_size == 0 || shape->n_kv_heads == 0) return 0;
+    return dec_plan(shape, block_size).ws;
+}
+
+int qbk_attention_sage_decode(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, size_t q_len,
+                              const float *k, size_t k_len, const float *v, size_t v_len,
+                              size_t block_size, float *out, size_t out_len) {
+    int rc;
+    const size_t lens[4] = {q_len, k_len, v_len, out_len};
+    if ((rc = validate_decode(shape, block_size, lens))) return rc;
+    if (!q || !k || !v || !out) return fail(QBK_ERR_VALIDATION, "null buffer");
+    if ((rc = bind(ctx))) return rc;
+    CallStream cs;
+    if ((rc = cs.create())) return rc;
+    DevBuf dq, dk, dvb, dout, dws;
+    if ((rc = dq.alloc(q_len * 4)) || (rc = dk.alloc(k_len * 4)) || (rc = dvb.alloc(v_len * 4)) ||
+        (rc = dout.alloc(out_len * 4)) || (rc = dws.alloc(dec_plan(shape, block_size).ws)))
+        return rc;
+    QBK_HIP(hipMemcpyAsync(dq.p, q, q_len * 4, hipMemcpyHostToDevice, cs.s));
+    QBK_HIP(hipMemcpyAsync(dk.p, k, k_len * 4, hipMemcpyHostToDevice, cs.s));
+    QBK_HIP(hipMemcpyAsync(dvb.p, v, v_len * 4, hipMemcpyHostToDevice, cs.s));
+    if ((rc = run_decode(shape, (const float *)dq.p, (const float *)dk.p, (const float *)dvb.p, block_size,
+                         (float *)dout.p, dws.p, cs.s)))
+        return rc;
+    QBK_HIP(hipMemcpyAsync(out, dout.p, out_len * 4, hipMemcpyDeviceToHost, cs.s));
+    QBK_HIP(hipStreamSynchronize(cs.s));
+    return QBK_OK;
+}
+
+int qbk_attention_sage_decode_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
+                                  const float *v, size_t block_size, float *out, void *workspace,
+                                  size_t workspace_size, void *stream) {
+    int rc;
+    if ((rc = validate_decode(shape, block_size, nullptr))) return rc;
+    if ((rc = bind(ctx))) return rc;
+    const size_t need = dec_plan(shape, block_size).ws;
+    if (workspace_size < need)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("workspace of %zu bytes is smaller than the %zu this call needs", workspace_size, need));
+    return run_decode(shape, q, k, v, block_size, out, workspace, (hipStream_t)stream);
 }
 
 size_t qbk_sage_blk_workspace_size(const qbk_attn_shape *shape) {

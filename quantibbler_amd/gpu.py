@@ -143,6 +143,40 @@ class GpuContext:
                                                  int(bool(causal)), int(block_size), _ptr(out),
                                                  _stream(stream)))
 
+    # ---- one decode step over a KV cache (engine/mod.rs:984-1030) ----------
+
+    def attention_sage_decode(self, shape: AttentionShape, query, key_cache, value_cache,
+                              block_size: int):
+        """Row 0 of the reference's padded decode call (gqa_attention_sage:
+        the step's query in row 0 of a (pos + 1)-row problem, causal=False),
+        computed alone.  query (n_heads, d); key_cache (seq_kv, n_kv_heads,
+        d) and value_cache (seq_kv, n_kv_heads, dv) as the cache holds them
+        (row-major); shape: batch 1, seq_q 1, seq_kv = pos + 1.  Returns
+        (n_heads, dv) f32."""
+        q = np.ascontiguousarray(query, dtype=np.float32).ravel()
+        k = np.ascontiguousarray(key_cache, dtype=np.float32).ravel()
+        v = np.ascontiguousarray(value_cache, dtype=np.float32).ravel()
+        out = np.zeros(shape.n_heads * shape.val_dim, np.float32)
+        sh = shape.c()
+        check(_lib.load().qbk_attention_sage_decode(self._h, C.byref(sh), _ptr(q), q.size, _ptr(k),
+                                                    k.size, _ptr(v), v.size, int(block_size),
+                                                    _ptr(out), out.size))
+        return out.reshape(shape.n_heads, shape.val_dim)
+
+    def sage_decode_workspace_size(self, shape: AttentionShape, block_size: int) -> int:
+        sh = shape.c()
+        return int(_lib.load().qbk_sage_decode_workspace_size(C.byref(sh), int(block_size)))
+
+    def attention_sage_decode_dev(self, shape: AttentionShape, q, key_cache, value_cache,
+                                  block_size: int, out, workspace, workspace_size: int,
+                                  stream=None):
+        sh = shape.c()
+        check(_lib.load().qbk_attention_sage_decode_dev(self._h, C.byref(sh), _ptr(q),
+                                                        _ptr(key_cache), _ptr(value_cache),
+                                                        int(block_size), _ptr(out),
+                                                        _ptr(workspace), int(workspace_size),
+                                                        _stream(stream)))
+
     def sage_blk_workspace_size(self, shape: AttentionShape) -> int:
         sh = shape.c()
         return int(_lib.load().qbk_sage_blk_workspace_size(C.byref(sh)))

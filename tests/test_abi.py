@@ -97,6 +97,32 @@ def test_validation_precedes_device_use(lib):
         check(lib.qbk_attention_sage(None, C.byref(sh), None, 63, None, 32, None, 32, 1, 4, None))
 
 
+def test_decode_validation_precedes_device_use(lib):
+    # the decode step's shape checks (batch 1, one query, the cache's sizes)
+    # are reported before any device is touched
+    from quantibbler_amd import KernelError
+    from quantibbler_amd._lib import AttnShape, check
+
+    def call(sh, lens, block=4):
+        return check(lib.qbk_attention_sage_decode(None, C.byref(sh), None, lens[0], None, lens[1],
+                                                   None, lens[2], block, None, lens[3]))
+
+    with pytest.raises(KernelError, match="sage decode takes one sequence: batch must be 1, got 2"):
+        call(AttnShape(2, 2, 1, 1, 8, 4, 4), (8, 32, 32, 8))
+    with pytest.raises(KernelError, match="sage decode takes the step's one query: seq_q must be 1, got 8"):
+        call(AttnShape(1, 2, 1, 8, 8, 4, 4), (8, 32, 32, 8))
+    with pytest.raises(KernelError, match=r"n_kv_heads must divide n_heads: n_heads=3, n_kv_heads=2"):
+        call(AttnShape(1, 3, 2, 1, 8, 4, 4), (12, 64, 64, 12))
+    with pytest.raises(KernelError, match="sage attention requires a positive block_size"):
+        call(AttnShape(1, 2, 1, 1, 8, 4, 4), (8, 32, 32, 8), block=0)
+    with pytest.raises(KernelError, match=r"key cache must hold 32 values for AttentionShape \{ batch: 1, "
+                       r"n_heads: 2, n_kv_heads: 1, seq_q: 1, seq_kv: 8, head_dim: 4, val_dim: 4 \}, got 31"):
+        call(AttnShape(1, 2, 1, 1, 8, 4, 4), (8, 31, 32, 8))
+    with pytest.raises(KernelError, match="out must hold 8 values"):
+        call(AttnShape(1, 2, 1, 1, 8, 4, 4), (8, 32, 32, 7))
+    assert lib.qbk_sage_decode_workspace_size(C.byref(AttnShape(1, 2, 1, 1, 8, 4, 4)), 4) > 0
+
+
 def test_init_fails_closed_without_device(lib):
     try:
         import torch

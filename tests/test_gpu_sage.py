@@ -52,6 +52,54 @@ def test_reference_scheme_fixture_battery(ctx, orc):
         assert cos >= ref["cosine"] - SLACK and rl1 <= ref["relative_l1"] + SLACK
 
 
+def padded_decode_call(ctx, qh, kc, vc, block):
+    """engine/mod.rs:984-1030 gqa_attention_sage as the reference makes it: the
+    step's query in row 0 of a zero-padded (pos + 1)-row problem, the cache
+    gathered head-major (KvCache::head_major, engine/mod.rs:1258-1268),
+    attention_sage with causal=False, row 0 of each head read back."""
+    from quantibbler_amd import AttentionShape
+
+    h, d = qh.shape
+    seq, hk, dv = vc.shape
+    q = np.zeros((1, h, seq, d), np.float32)
+    q[0, :, 0, :] = qh
+    k = np.ascontiguousarray(kc.transpose(1, 0, 2))[None]
+    v = np.ascontiguousarray(vc.transpose(1, 0, 2))[None]
+    out = ctx.attention_sage(AttentionShape(1, h, hk, seq, seq, d, dv), q, k, v, False, block)
+    return out.reshape(h, seq, dv)[:, 0, :], (q, k, v)
+
+
+@pytest.mark.parametrize("h,hk,d,dv,seq,block", [
+    (4, 2, 16, 16, 1, 1), (4, 2, 16, 16, 37, 8), (8, 2, 64, 64, 200, 64), (4, 1, 128, 128, 130, 64),
+    (2, 1, 32, 48, 150, 100), (8, 8, 128, 128, 333, 64), (4, 2, 64, 64, 90, 256),
+])
+def test_decode_step_matches_padded_reference_call(ctx, orc, h, hk, d, dv, seq, block):
+    """One decode step over a row-major KV cache: bit-identical to row 0 of the
+    reference's padded call, both on this device and in the oracle."""
+    from quantibbler_amd import AttentionShape
+
+    say("sage decode step", h, hk, d, dv, seq, block)
+    rng = np.random.default_rng(7 * seq + block + h)
+    qh = rng.standard_normal((h, d)).astype(np.float32)
+    kc = (rng.standard_normal((seq, hk, d)) + 2.0 * rng.standard_normal((1, hk, d))).astype(np.float32)
+    vc = rng.standard_normal((seq, hk, dv)).astype(np.float32)
+    sh = AttentionShape(1, h, hk, 1, seq, d, dv)
+    got = ctx.attention_sage_decode(sh, qh, kc, vc, block)
+    want_dev, (q, k, v) = padded_decode_call(ctx, qh, kc, vc, block)
+    same(got, want_dev)
+    want = orc.attention_sage_dev(q, k, v, False, block)[0, :, 0, :]
+    same(got, want)
+    # the device-pointer form, twice on one workspace
+    wn = ctx.sage_decode_workspace_size(sh, block)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    qd, kd, vd = (torch.from_numpy(a).cuda() for a in (qh, kc, vc))
+    od = torch.empty((h, dv), dtype=torch.float32, device="cuda")
+    for _ in range(2):
+        ctx.attention_sage_decode_dev(sh, qd, kd, vd, block, od, ws, wn, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        same(od.cpu().numpy(), got)
+
+
 @pytest.mark.parametrize("b,h,hk,s,d,dv,causal,block", [
     (1, 4, 2, 200, 64, 64, True, 64),
     (2, 2, 1, 130, 128, 128, True, 64),
