@@ -247,6 +247,38 @@ def bench_sage_decode(qa, ctx, torch, np, seq=4096, iters=20):
             "shape": f"H=32 Hkv=8 d=128 seq={seq} block 64, f32 row-major cache"}
 
 
+def bench_head(qa, ctx, torch, np, vocab=128256, d=4096, iters=20):
+    """The language-model head of config 5 (engine/mod.rs:781-800): one
+    decode step's logits over a bf16-valued 128256 x 4096 head (1.05 GB
+    stored as bf16, the bytes that dominate a batch-1 decode step), and a
+    batch of 8 positions."""
+    g = torch.Generator(device="cuda").manual_seed(11)
+    rows = torch.randn((vocab, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
+    H = qa.LmHead.from_rows_dev(ctx, rows, vocab, d)
+    del rows
+    torch.cuda.empty_cache()
+    hid = torch.randn((8, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
+    out = torch.empty((8, vocab), dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream()
+    res = {"vocab": vocab, "d_model": d, "stored_bf16": H.bf16, "head_bytes": vocab * d * 2}
+    for b in (1, 8):
+        for _ in range(3):
+            H.logits_dev(hid, b, out, st)
+        torch.cuda.synchronize()
+        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(iters):
+            H.logits_dev(hid, b, out, st)
+        e.record(st)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(e) / iters
+        res[f"batch{b}_us"] = round(ms * 1e3, 1)
+        res[f"batch{b}_GB/s"] = round(vocab * d * 2 / (ms * 1e-3) / 1e9, 1)
+        log(f"  lm_head batch {b}: {ms * 1e3:.1f} us, {vocab * d * 2 / (ms * 1e-3) / 1e9:.0f} GB/s")
+    H.close()
+    return res
+
+
 # BASELINE.json configs[2]: the seven projections of a Llama-3-8B-shaped
 # decoder layer, ranks from the reference's planning rule at 0.55 bits/weight
 # (v2 stream, fp16 scales): (name, dout, din, r).
@@ -368,7 +400,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode"],
+    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head"],
                     help="run one secondary workload alone and print its figures (for profiling); "
                          "no headline line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -395,6 +427,8 @@ def main():
             res = bench_sage(qa, ctx, torch, np)
         elif args.only == "sage_decode":
             res = bench_sage_decode(qa, ctx, torch, np)
+        elif args.only == "head":
+            res = bench_head(qa, ctx, torch, np)
         else:
             res = bench_cfg3(qa, ctx, torch, np)
         print(json.dumps({"only": args.only, "result": res}), flush=True)
@@ -434,6 +468,8 @@ def main():
         extra["sage_blk"] = bench_sage(qa, ctx, torch, np)
         log("sage decode step ...")
         extra["sage_decode"] = bench_sage_decode(qa, ctx, torch, np)
+        log("lm_head ...")
+        extra["lm_head"] = bench_head(qa, ctx, torch, np)
         log("config 3 (8B decoder layer projections) ...")
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")

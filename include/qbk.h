@@ -215,6 +215,27 @@ int qbk_sage_blk_quantize_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const u
                               int8_t *khat, float *kscale, float *kmean, uint16_t *vh,
                               void *stream);
 
+/* ---- language-model head (engine/mod.rs:781-800) -------------------------- */
+
+/* Engine::logits: logits[v] = sum_t hidden[t] * head[v][t], one f32 sum per
+ * vocabulary row in t order (each term a separate multiply and add), so the
+ * logits are bit-identical to the reference's.  The head is uploaded once
+ * from f32 rows (vocab, d_model) and held transposed -- as bf16 when every
+ * element is a bf16 value (bf16 serving, engine/mod.rs:695-706), else f32. */
+typedef struct qbk_head qbk_head;
+int qbk_head_create(qbk_ctx *ctx, const float *head, size_t head_len, size_t vocab, size_t d_model,
+                    qbk_head **out);
+/* The same from a device buffer of f32 rows (vocab, d_model). */
+int qbk_head_create_dev(qbk_ctx *ctx, const float *head, size_t vocab, size_t d_model, qbk_head **out);
+void qbk_head_destroy(qbk_head *head);
+int qbk_head_info(const qbk_head *head, size_t *vocab, size_t *d_model, int *bf16);
+/* hidden: rows of d_model f32 (one per position); logits: rows of vocab f32. */
+int qbk_head_logits(qbk_ctx *ctx, const qbk_head *head, const float *hidden, size_t hidden_len, float *logits,
+                    size_t logits_len);
+/* Device-pointer form, `batch` rows, stream-ordered; allocates nothing. */
+int qbk_head_logits_dev(qbk_ctx *ctx, const qbk_head *head, const float *hidden, size_t batch, float *logits,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

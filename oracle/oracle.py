@@ -76,6 +76,7 @@ def _declare(L):
         "orc_attention_sage_dev_f32": (C.c_int, [C.POINTER(AttnShape), _P, _P, _P, C.c_int, _Z, _P, _P, _P, C.c_int]),
         "orc_expf": (C.c_float, [C.c_float]),
         "orc_attention_sage_blk": (C.c_int, [C.POINTER(AttnShape), _P, _P, _P, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int]),
+        "orc_head_logits": (None, [_P, _Z, _Z, _P, _Z, _P, C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -353,3 +354,16 @@ def attention_sage_blk(q_bf16, k_bf16, v_bf16, causal=True, threads=0, stages=Fa
     if rc:
         raise OracleError("attention_sage_blk: bad shape")
     return (out, st) if stages else out
+
+
+def head_logits(head, hidden, threads=0):
+    """engine/mod.rs:781-800 Engine::logits: head (vocab, d) f32, hidden
+    (batch, d) or (d,) f32 -> logits (batch, vocab) / (vocab,)."""
+    head = np.ascontiguousarray(head, np.float32)
+    vocab, d = head.shape
+    h = np.ascontiguousarray(hidden, np.float32)
+    one = h.ndim == 1
+    h2 = h.reshape(-1, d)
+    out = np.zeros((h2.shape[0], vocab), np.float32)
+    lib().orc_head_logits(_ptr(head), vocab, d, _ptr(h2), h2.shape[0], _ptr(out), _threads(threads))
+    return out[0] if one else out

@@ -1020,3 +1020,22 @@ int orc_attention_sage_blk(const orc_attn_shape *sh, const uint16_t *q, const ui
     free(khat); free(ksc); free(kmean); free(qhat); free(qsc); free(vh);
     return 0;
 }
+
+/* engine/mod.rs:781-800 Engine::logits (and the per-position prefill loop,
+ * :1131-1147): one f32 accumulator per vocabulary row, t in order, each term
+ * a separate multiply and add (built with -ffp-contract=off).  OpenMP over
+ * rows only: each row's sum is sequential. */
+void orc_head_logits(const float *head, size_t vocab, size_t d, const float *hidden, size_t batch,
+                     float *logits, int threads) {
+    if (threads > 0) omp_set_num_threads(threads);
+    for (size_t b = 0; b < batch; b++) {
+        const float *h = hidden + b * d;
+#pragma omp parallel for schedule(static)
+        for (size_t v = 0; v < vocab; v++) {
+            const float *row = head + v * d;
+            float acc = 0.0f;
+            for (size_t t = 0; t < d; t++) acc += h[t] * row[t];
+            logits[b * vocab + v] = acc;
+        }
+    }
+}

@@ -116,4 +116,8 @@ int orc_attention_sage_blk(const orc_attn_shape *s, const uint16_t *q, const uin
 #ifdef __cplusplus
 }
 #endif
+/* engine/mod.rs:781-800 Engine::logits: sequential f32 sum per row. */
+void orc_head_logits(const float *head, size_t vocab, size_t d, const float *hidden, size_t batch,
+                     float *logits, int threads);
+
 #endif

@@ -11,7 +11,7 @@ two hot paths behind the reference's own API surface:
 All compute runs in libqbk.so (hand-written HIP, C ABI in include/qbk.h).
 """
 from ._lib import DeviceError, InitError, KernelError, load as _load_lib  # noqa: F401
-from .gpu import AttentionShape, FactorLayer, FactorSet, GpuContext, gpu_available  # noqa: F401
+from .gpu import AttentionShape, FactorLayer, FactorSet, GpuContext, LmHead, gpu_available  # noqa: F401
 
 _load_lib()
 

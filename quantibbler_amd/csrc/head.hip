@@ -1,0 +1,319 @@
+// head.hip -- the language-model head on gfx950.
+//
+// engine/mod.rs:781-800 (Engine::logits; the prefill path, :1131-1147, is
+// the same loop per position): logits[v] = sum_t hidden[t] * head[v][t],
+// one f32 sum per vocabulary row in t order, each term a separate f32
+// multiply and add.  Every row's sum stays in one lane, in that order, so
+// the logits are bit-identical to the reference's; the parallelism is the
+// rows (128256 for a Llama-3 vocabulary).
+//
+// Layout: the head is stored transposed per wave, [vocab_p / RW][d_model][RW]
+// with RW the rows one wave covers (vocab_p = vocab rounded up to the rows
+// of a workgroup, zero-padded): at step t a wave reads one contiguous run of
+// its rows' elements, and its steps follow each other in memory, so every
+// wave streams one contiguous region (one DRAM page after another; the
+// plain [d_model][vocab] transpose made each step 256 KB from the last and
+// read at 4.6 TB/s).  When every
+// element is a bf16 value (the reference's bf16 serving quantises the head
+// so, engine/mod.rs:695-706) it is stored as bf16 -- 1.05 GB instead of 2.1
+// for 128256 x 4096 -- and widened exactly on use; otherwise as f32.
+//
+// The dot product is HBM-bound (one pass over the head per call; the
+// hidden rows ride in SGPRs through scalar loads).  A lane covers two rows
+// (bf16: one dword holds both) or one (f32), reads a dword per step, and
+// keeps two 64-step chunks of loads in flight (alternating register sets,
+// so no in-flight register is ever copied; 32-step chunks read at 5.3
+// TB/s, 128-step ones at 4.9).
+#include <string.h>
+
+#include "qbk_internal.h"
+
+#pragma clang fp contract(off)
+
+struct qbk_head {
+    int device;
+    size_t vocab, d_model, vocab_p;
+    int bf16;    // elements stored as bf16 (all were bf16 values), else f32
+    void *w;     // [vocab_p / RW][d_model][RW], RW = head_rows_per_wave(bf16)
+};
+
+namespace qbk {
+
+#define HEAD_THREADS 256
+#define HEAD_CHUNK 64   // steps per load chunk
+#define HEAD_MAXB 8     // hidden rows per launch
+
+typedef __attribute__((address_space(1))) const uint32_t g32_t;
+typedef __attribute__((address_space(4))) const float cf32_t;
+
+// rows one wave / one workgroup covers
+__host__ __device__ static inline size_t head_rows_per_wave(int bf16) { return bf16 ? 128 : 64; }
+static inline size_t head_rows_per_wg(int bf16) { return (HEAD_THREADS / 64) * head_rows_per_wave(bf16); }
+
+// one chunk of HEAD_CHUNK steps from t0 on, words in W: the lane's
+// rows += hidden[b][t] * w (bf16: the word's low half is row 2c, high half
+// row 2c + 1)
+template <bool BF16, int NB>
+__device__ __forceinline__ void head_chunk(float acc[NB][2], const uint32_t W[HEAD_CHUNK], const cf32_t *h,
+                                           size_t d, size_t t0) {
+#pragma unroll
+    for (int u = 0; u < HEAD_CHUNK; u++) {
+        const float w0 = BF16 ? __uint_as_float(W[u] << 16) : __uint_as_float(W[u]);
+        const float w1 = BF16 ? __uint_as_float(W[u] & 0xffff0000u) : 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float hv = h[(size_t)b * d + t0 + u];
+            acc[b][0] = acc[b][0] + hv * w0;
+            if (BF16) acc[b][1] = acc[b][1] + hv * w1;
+        }
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void head_load(uint32_t W[HEAD_CHUNK], const uint32_t *col, size_t stride, size_t t0,
+                                          size_t tlast) {
+#pragma unroll
+    for (int u = 0; u < HEAD_CHUNK; u++) {
+        size_t t = t0 + u;
+        t = t < tlast ? t : tlast;  // past the end: a repeated (unused) step
+        W[u] = __builtin_nontemporal_load((g32_t *)(col + t * stride));
+    }
+}
+
+// logits[b][v] for NB hidden rows.  w: the per-wave blocked layout, bf16
+// (dwords of two rows) or f32; lane l of wave block wb reads dword
+// (wb * d + t) * 64 + l at step t.
+template <bool BF16, int NB>
+__global__ void __launch_bounds__(HEAD_THREADS) head_logits_kernel(const uint32_t *w, size_t vocab_p, size_t vocab,
+                                                                  size_t d, const float *hidden, float *logits) {
+    const size_t wb = (size_t)blockIdx.x * (HEAD_THREADS / 64) + (threadIdx.x >> 6);
+    const size_t lane = threadIdx.x & 63;
+    const size_t stride = 64;  // dwords per step
+    const uint32_t *col = w + wb * d * 64 + lane;
+    const cf32_t *h = (const cf32_t *)hidden;
+    float acc[NB][2];
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[b][0] = acc[b][1] = 0.0f;
+    const size_t dmain = d / (2 * HEAD_CHUNK) * (2 * HEAD_CHUNK);
+    uint32_t A[HEAD_CHUNK], Bw[HEAD_CHUNK];
+    if (dmain) {
+        head_load<BF16>(A, col, stride, 0, d - 1);
+        for (size_t t0 = 0; t0 < dmain; t0 += 2 * HEAD_CHUNK) {
+            head_load<BF16>(Bw, col, stride, t0 + HEAD_CHUNK, d - 1);
+            head_chunk<BF16, NB>(acc, A, h, d, t0);
+            head_load<BF16>(A, col, stride, t0 + 2 * HEAD_CHUNK, d - 1);
+            head_chunk<BF16, NB>(acc, Bw, h, d, t0 + HEAD_CHUNK);
+        }
+    }
+    for (size_t t = dmain; t < d; t++) {  // the last d % 64 steps, in order
+        const uint32_t wv = col[t * stride];
+        const float w0 = BF16 ? __uint_as_float(wv << 16) : __uint_as_float(wv);
+        const float w1 = BF16 ? __uint_as_float(wv & 0xffff0000u) : 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float hv = h[(size_t)b * d + t];
+            acc[b][0] = acc[b][0] + hv * w0;
+            if (BF16) acc[b][1] = acc[b][1] + hv * w1;
+        }
+    }
+    const size_t v0 = wb * head_rows_per_wave(BF16) + (BF16 ? 2 * lane : lane);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        if (v0 < vocab) logits[(size_t)b * vocab + v0] = acc[b][0];
+        if (BF16 && v0 + 1 < vocab) logits[(size_t)b * vocab + v0 + 1] = acc[b][1];
+    }
+}
+
+// any element of src (f32, n of them) not a bf16 value -> *flag = 1
+__global__ void head_bf16_check(const float *src, size_t n, uint32_t *flag) {
+    uint32_t bad = 0;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        bad |= __float_as_uint(src[i]) & 0xffffu;
+    if (__builtin_amdgcn_ballot_w64(bad != 0) && (threadIdx.x & 63) == 0) atomicOr(flag, 1u);
+}
+
+// [vocab][d] f32 -> the per-wave blocked layout (bf16 halves or f32), zero
+// padding; 32 x 32 tiles through LDS
+template <bool BF16>
+__global__ void __launch_bounds__(256) head_transpose(const float *src, size_t vocab, size_t d, size_t vocab_p,
+                                                      void *dst) {
+    __shared__ float tile[32][33];
+    const size_t v0 = (size_t)blockIdx.x * 32, t0 = (size_t)blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        const size_t v = v0 + r, t = t0 + tx;
+        tile[r][tx] = v < vocab && t < d ? src[v * d + t] : 0.0f;
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const size_t t = t0 + r, v = v0 + tx;
+        if (t >= d || v >= vocab_p) continue;
+        const float x = tile[tx][r];
+        const size_t rw = head_rows_per_wave(BF16);
+        const size_t o = ((v / rw) * d + t) * rw + v % rw;
+        if (BF16)
+            ((uint16_t *)dst)[o] = (uint16_t)(__float_as_uint(x) >> 16);
+        else
+            ((float *)dst)[o] = x;
+    }
+}
+
+static int head_build(qbk_ctx *ctx, const float *src_dev, size_t vocab, size_t d_model, qbk_head **out) {
+    qbk_head *H = new qbk_head();
+    H->device = ctx->device;
+    H->vocab = vocab;
+    H->d_model = d_model;
+    uint32_t *flag = nullptr;
+    hipError_t e = hipMalloc((void **)&flag, 4);
+    if (e == hipSuccess) e = hipMemset(flag, 0, 4);
+    if (e == hipSuccess) {
+        const size_t n = vocab * d_model;
+        hipLaunchKernelGGL(head_bf16_check, dim3((unsigned)(div_ceil(n, 256) < 4096 ? div_ceil(n, 256) : 4096)),
+                           dim3(256), 0, 0, src_dev, n, flag);
+        e = hipGetLastError();
+    }
+    uint32_t f = 1;
+    if (e == hipSuccess) e = hipMemcpy(&f, flag, 4, hipMemcpyDeviceToHost);
+    if (flag) (void)hipFree(flag);
+    H->bf16 = f == 0;
+    H->vocab_p = round_up(vocab, head_rows_per_wg(H->bf16));
+    const size_t bytes = d_model * H->vocab_p * (H->bf16 ? 2 : 4);
+    if (e == hipSuccess) e = hipMalloc(&H->w, bytes);
+    if (e == hipSuccess) {
+        dim3 g((unsigned)div_ceil(H->vocab_p, 32), (unsigned)div_ceil(d_model, 32));
+        if (H->bf16)
+            hipLaunchKernelGGL(head_transpose<true>, g, dim3(256), 0, 0, src_dev, vocab, d_model, H->vocab_p, H->w);
+        else
+            hipLaunchKernelGGL(head_transpose<false>, g, dim3(256), 0, 0, src_dev, vocab, d_model, H->vocab_p, H->w);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        if (H->w) (void)hipFree(H->w);
+        delete H;
+        return fail(QBK_ERR_DEVICE, fmt("lm_head upload failed: %s", hipGetErrorString(e)));
+    }
+    *out = H;
+    return QBK_OK;
+}
+
+static int head_run(const qbk_head *H, const float *hidden, size_t batch, float *logits, hipStream_t s) {
+    const size_t rpw = head_rows_per_wg(H->bf16);
+    const dim3 g((unsigned)(H->vocab_p / rpw));
+    for (size_t b0 = 0; b0 < batch; b0 += HEAD_MAXB) {
+        const size_t nb = batch - b0 < HEAD_MAXB ? batch - b0 : HEAD_MAXB;
+        const float *hb = hidden + b0 * H->d_model;
+        float *lb = logits + b0 * H->vocab;
+        const uint32_t *w = (const uint32_t *)H->w;
+#define HEAD_LAUNCH(BF, NB)                                                                                   \
+    hipLaunchKernelGGL((head_logits_kernel<BF, NB>), g, dim3(HEAD_THREADS), 0, s, w, H->vocab_p, H->vocab,     \
+                       H->d_model, hb, lb)
+#define HEAD_BATCH(BF)                                                                                        \
+    switch (nb) {                                                                                             \
+        case 1: HEAD_LAUNCH(BF, 1); break;                                                                    \
+        case 2: HEAD_LAUNCH(BF, 2); break;                                                                    \
+        case 3: HEAD_LAUNCH(BF, 3); break;                                                                    \
+        case 4: HEAD_LAUNCH(BF, 4); break;                                                                    \
+        case 5: HEAD_LAUNCH(BF, 5); break;                                                                    \
+        case 6: HEAD_LAUNCH(BF, 6); break;                                                                    \
+        case 7: HEAD_LAUNCH(BF, 7); break;                                                                    \
+        default: HEAD_LAUNCH(BF, 8); break;                                                                   \
+    }
+        if (H->bf16) {
+            HEAD_BATCH(true)
+        } else {
+            HEAD_BATCH(false)
+        }
+#undef HEAD_BATCH
+#undef HEAD_LAUNCH
+        QBK_HIP(hipGetLastError());
+    }
+    return QBK_OK;
+}
+
+}  // namespace qbk
+
+using namespace qbk;
+
+extern "C" {
+
+int qbk_head_create(qbk_ctx *ctx, const float *head, size_t head_len, size_t vocab, size_t d_model,
+                    qbk_head **out) {
+    int rc;
+    if (!out) return fail(QBK_ERR_VALIDATION, "null output handle");
+    *out = nullptr;
+    if (vocab == 0 || d_model == 0) return fail(QBK_ERR_VALIDATION, "lm_head requires non-empty vocab and d_model");
+    if (head_len != vocab * d_model)
+        return fail(QBK_ERR_VALIDATION, fmt("lm_head is %zu floats; expected %zux%zu = %zu", head_len, vocab,
+                                            d_model, vocab * d_model));
+    if (!head) return fail(QBK_ERR_VALIDATION, "null buffer");
+    if ((rc = bind(ctx))) return rc;
+    DevBuf src;
+    if ((rc = src.alloc(head_len * 4))) return rc;
+    QBK_HIP(hipMemcpy(src.p, head, head_len * 4, hipMemcpyHostToDevice));
+    return head_build(ctx, (const float *)src.p, vocab, d_model, out);
+}
+
+int qbk_head_create_dev(qbk_ctx *ctx, const float *head, size_t vocab, size_t d_model, qbk_head **out) {
+    int rc;
+    if (!out) return fail(QBK_ERR_VALIDATION, "null output handle");
+    *out = nullptr;
+    if (vocab == 0 || d_model == 0) return fail(QBK_ERR_VALIDATION, "lm_head requires non-empty vocab and d_model");
+    if ((rc = bind(ctx))) return rc;
+    return head_build(ctx, head, vocab, d_model, out);
+}
+
+void qbk_head_destroy(qbk_head *H) {
+    if (!H) return;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(H->device);
+    (void)hipFree(H->w);
+    (void)hipSetDevice(cur);
+    delete H;
+}
+
+int qbk_head_info(const qbk_head *H, size_t *vocab, size_t *d_model, int *bf16) {
+    if (!H) return fail(QBK_ERR_VALIDATION, "null lm_head");
+    if (vocab) *vocab = H->vocab;
+    if (d_model) *d_model = H->d_model;
+    if (bf16) *bf16 = H->bf16;
+    return QBK_OK;
+}
+
+int qbk_head_logits(qbk_ctx *ctx, const qbk_head *H, const float *hidden, size_t hidden_len, float *logits,
+                    size_t logits_len) {
+    int rc;
+    if (!H) return fail(QBK_ERR_VALIDATION, "null lm_head");
+    if (hidden_len == 0 || hidden_len % H->d_model != 0)
+        return fail(QBK_ERR_VALIDATION, fmt("hidden must hold rows of d_model = %zu values, got %zu", H->d_model,
+                                            hidden_len));
+    const size_t batch = hidden_len / H->d_model;
+    if (logits_len != batch * H->vocab)
+        return fail(QBK_ERR_VALIDATION, fmt("logits must hold %zu values (%zu rows x vocab %zu), got %zu",
+                                            batch * H->vocab, batch, H->vocab, logits_len));
+    if (!hidden || !logits) return fail(QBK_ERR_VALIDATION, "null buffer");
+    if ((rc = bind(ctx))) return rc;
+    if (H->device != ctx->device) return fail(QBK_ERR_VALIDATION, "lm_head lives on another device");
+    CallStream cs;
+    if ((rc = cs.create())) return rc;
+    DevBuf dh, dl;
+    if ((rc = dh.alloc(hidden_len * 4)) || (rc = dl.alloc(logits_len * 4))) return rc;
+    QBK_HIP(hipMemcpyAsync(dh.p, hidden, hidden_len * 4, hipMemcpyHostToDevice, cs.s));
+    if ((rc = head_run(H, (const float *)dh.p, batch, (float *)dl.p, cs.s))) return rc;
+    QBK_HIP(hipMemcpyAsync(logits, dl.p, logits_len * 4, hipMemcpyDeviceToHost, cs.s));
+    QBK_HIP(hipStreamSynchronize(cs.s));
+    return QBK_OK;
+}
+
+int qbk_head_logits_dev(qbk_ctx *ctx, const qbk_head *H, const float *hidden, size_t batch, float *logits,
+                        void *stream) {
+    int rc;
+    if (!H) return fail(QBK_ERR_VALIDATION, "null lm_head");
+    if (batch == 0) return fail(QBK_ERR_VALIDATION, "batch must be at least 1");
+    if ((rc = bind(ctx))) return rc;
+    if (H->device != ctx->device) return fail(QBK_ERR_VALIDATION, "lm_head lives on another device");
+    return head_run(H, hidden, batch, logits, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -198,6 +198,61 @@ class GpuContext:
                                                     _ptr(vh), _stream(stream)))
 
 
+class LmHead:
+    """Device-resident language-model head (engine/mod.rs:781-800
+    Engine::logits): logits[v] = sum_t hidden[t] * head[v][t], one f32 sum
+    per vocabulary row in t order -- bit-identical to the reference's loop.
+    Stored transposed, as bf16 when every element is a bf16 value."""
+
+    def __init__(self, ctx: GpuContext, handle):
+        self._ctx = ctx
+        self._h = handle
+        v, d, b = C.c_size_t(), C.c_size_t(), C.c_int()
+        check(_lib.load().qbk_head_info(handle, C.byref(v), C.byref(d), C.byref(b)))
+        self.vocab, self.d_model, self.bf16 = v.value, d.value, bool(b.value)
+
+    @classmethod
+    def from_rows(cls, ctx: GpuContext, head) -> "LmHead":
+        h = np.ascontiguousarray(head, dtype=np.float32)
+        vocab, d = h.shape
+        out = C.c_void_p()
+        check(_lib.load().qbk_head_create(ctx.handle, _ptr(h), h.size, vocab, d, C.byref(out)))
+        return cls(ctx, out)
+
+    @classmethod
+    def from_rows_dev(cls, ctx: GpuContext, head_dev, vocab: int, d_model: int) -> "LmHead":
+        out = C.c_void_p()
+        check(_lib.load().qbk_head_create_dev(ctx.handle, _ptr(head_dev), int(vocab), int(d_model),
+                                              C.byref(out)))
+        return cls(ctx, out)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def logits(self, hidden) -> np.ndarray:
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        rows = h.size // max(self.d_model, 1)
+        out = np.zeros(rows * self.vocab, np.float32)
+        check(_lib.load().qbk_head_logits(self._ctx.handle, self._h, _ptr(h), h.size, _ptr(out), out.size))
+        return out.reshape(self.vocab) if h.ndim == 1 else out.reshape(rows, self.vocab)
+
+    def logits_dev(self, hidden, batch: int, logits, stream=None):
+        check(_lib.load().qbk_head_logits_dev(self._ctx.handle, self._h, _ptr(hidden), int(batch),
+                                              _ptr(logits), _stream(stream)))
+
+    def close(self):
+        if self._h:
+            _lib.load().qbk_head_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class FactorLayer:
     """Device-resident binary factor linear (engine/mod.rs:313-481 PackedLayer)."""
 

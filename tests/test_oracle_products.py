@@ -160,3 +160,27 @@ def test_fast_face_backward_error_and_repeatability(orc):
         m = rng.standard_normal((n_bits, 3))
         assert orc.fast_packed_matmul(packed, n_rows, n_bits, m, 3).tobytes() == \
             orc.packed_matmul(packed, n_rows, n_bits, m, 3).tobytes()
+
+
+def test_head_logits_pins(orc):
+    """engine/mod.rs:781-800 Engine::logits, pinned without retyping it:
+    the summation order (2^24 + 1 - 2^24 is 0 only left to right), separate
+    multiply and add (a case an FMA rounds differently), one-hot rows (a
+    column of the head exactly), and integer inputs (exact int64 products)."""
+    h = np.array([[2.0 ** 24, 1.0, -2.0 ** 24], [2.0 ** 24, -2.0 ** 24, 1.0]], np.float32)
+    assert orc.head_logits(h, np.ones(3, np.float32)).tolist() == [0.0, 1.0]
+    # acc = -0x1.00060ap+0 after t = 0, then + h*w: 0x1.97ap-12 with the
+    # product rounded first, 0x1.97af7ep-12 fused
+    hh = np.array([[float.fromhex("-0x1.00060ap+0"), float.fromhex("0x1.00106p+0")]], np.float32)
+    x = np.array([1.0, float.fromhex("0x1.000f24p+0")], np.float32)
+    assert orc.head_logits(hh, x)[0] == np.float32(float.fromhex("0x1.97ap-12"))
+    rng = np.random.default_rng(4)
+    head = rng.standard_normal((37, 19)).astype(np.float32)
+    for t in (0, 7, 18):
+        e = np.zeros(19, np.float32)
+        e[t] = 1.0
+        assert orc.head_logits(head, e).tobytes() == head[:, t].tobytes()
+    hi = rng.integers(-8, 9, (50, 33)).astype(np.float32)
+    xi = rng.integers(-8, 9, (3, 33)).astype(np.float32)
+    want = (xi.astype(np.int64) @ hi.astype(np.int64).T).astype(np.float32)
+    assert orc.head_logits(hi, xi).tobytes() == want.tobytes()
