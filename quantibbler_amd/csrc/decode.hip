@@ -471,14 +471,18 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
     for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
     for (size_t sb = s0; sb < s1; sb += Q4_U) {
         const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
-        uint4 stg[NCOL > 0 ? NCOL : 1];
+        // a step's operand: Q4_U slices x 4 lane groups x NCOL columns x 32 B,
+        // SQ 16-byte words per lane
+        constexpr int SQ = NCOL > 0 ? Q4_U * NCOL / 8 : 1;
+        static_assert(NCOL == 0 || Q4_U * NCOL % 8 == 0, "whole 16-byte words per lane");
+        uint4 stg[SQ];
         uint32_t stgs = 0;
         if (NCOL > 0) {
-            // operand of slices sb..sb+nsl-1: NCOL uint4 + one dword of scales per lane
+            // operand of slices sb..sb+nsl-1: SQ uint4 + one dword of scales per lane
             const uint32_t ob = nsl * 4 * NCOL * 32, os = nsl * 4 * NCOL;
             const uint8_t *gbs = gb + sb * 4 * NCOL * 32, *gss = gs + sb * 4 * NCOL;
 #pragma unroll
-            for (int q = 0; q < (NCOL > 0 ? NCOL : 1); q++) {
+            for (int q = 0; q < SQ; q++) {
                 uint32_t o = (lane + 64 * q) * 16;
                 o = o < ob ? o : ob - 16;
                 stg[q] = *(const uint4 *)(gbs + o);
@@ -496,7 +500,7 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
         }
         if (NCOL > 0) {
 #pragma unroll
-            for (int q = 0; q < (NCOL > 0 ? NCOL : 1); q++) *(uint4 *)(wl + (lane + 64 * q) * 16) = stg[q];
+            for (int q = 0; q < SQ; q++) *(uint4 *)(wl + (lane + 64 * q) * 16) = stg[q];
             *(uint32_t *)(wl + OPB + lane * 4) = stgs;  // lanes past the scales fill the padding
             __builtin_amdgcn_wave_barrier();
         }
