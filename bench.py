@@ -295,7 +295,7 @@ def random_rows(np, rng, n_rows, n_bits):
     return b
 
 
-def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=20, prefill_b=2048):
+def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
     """Decode (batch 1) of every projection of n_layers distinct decoder
     layers -- 480 MB of signs, beyond the 256 MB MALL -- as one FactorSet
     over all of them (three launches per token); then the prefill GEMM of
