@@ -86,6 +86,34 @@ def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
     same(got_b, orc.f32_to_bf16_fast(want))
 
 
+def test_prefill_gemm_config2_full_size_integer_exact(ctx, orc):
+    """Config 2 at its largest batch (m = n = 4096, r = 1024, B = 2048) on
+    integer-exact inputs (s2 = 1, x in {-2..2}): the expectation is formed on
+    the device by fp32 products of the unpacked +-1 factors, exact for these
+    integers in any summation order (|t| <= 8192, |u| < 2^24), with the bf16
+    roundings of t and u and the final s1 / bias in separate fp32 operations,
+    as engine/mod.rs:449-460 does them."""
+    say("factor full-size prefill B=2048 integer-exact")
+    rng = np.random.default_rng(2048)
+    dout = din = 4096
+    r, batch = 1024, 2048
+    L = make_layer(orc, rng, dout, din, r, integer=True)
+    layer = upload(ctx, L)
+    x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (batch, din)).astype(np.float32))
+    got, _ = run_dev(layer, x)
+    got_b, _ = run_dev(layer, x, "bfloat16")
+    xf = torch.from_numpy(orc.bf16_to_f32(x)).cuda()
+    vt_t = torch.from_numpy(L["vts"].astype(np.float32).T.copy()).cuda()   # (din, r)
+    u_t = torch.from_numpy(L["ubs"].astype(np.float32).T.copy()).cuda()    # (r, dout)
+    t = torch.matmul(xf, vt_t).to(torch.bfloat16).float()
+    u = torch.matmul(t, u_t).to(torch.bfloat16).float()
+    y = u * torch.from_numpy(L["s1"]).cuda()
+    y = y + torch.from_numpy(L["bias"]).cuda()
+    want = y.cpu().numpy()
+    same(got, want, "f32 out")
+    same(got_b, orc.f32_to_bf16_fast(want), "bf16 out")
+
+
 def e4m3(b):
     """OCP fp8 e4m3 bytes -> float64 (bias 7, subnormals, no infinities)."""
     b = np.asarray(b, np.uint8).astype(np.int64)
