@@ -195,6 +195,21 @@ size_t qbk_sage_decode_workspace_size(const qbk_attn_shape *shape, size_t block_
 int qbk_attention_sage_decode_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
                                   const float *v, size_t block_size, float *out, void *workspace,
                                   size_t workspace_size, void *stream);
+/* The same step (engine/mod.rs:984-1030, bit-identical output) for a decode
+ * loop that keeps a state across steps: the state is a workspace laid out
+ * for a cache of `capacity` tokens (state_size >=
+ * qbk_sage_decode_workspace_size() of the shape with seq_kv = capacity).
+ * cached_tokens is the previous step's seq_kv on this state (0 for a new
+ * state, or after the cache's first cached_tokens rows changed): the codes
+ * of the key blocks complete within those rows are kept and only the later
+ * blocks -- at most one block plus the new tokens -- are quantised again,
+ * which takes the per-step cost of the pre-pass off the cache length.
+ * seq_kv <= capacity, cached_tokens <= seq_kv.  Calls that share a state
+ * must be ordered (one stream). */
+int qbk_attention_sage_decode_step_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q,
+                                       const float *k, const float *v, size_t block_size, float *out,
+                                       void *state, size_t state_size, size_t capacity, size_t cached_tokens,
+                                       void *stream);
 
 /* Block-scaled SageAttention prefill (no reference symbol: the scheme the
  * north_star names).  bf16 q (B,H,S,d), k (B,Hkv,S,d), v (B,Hkv,S,dv),

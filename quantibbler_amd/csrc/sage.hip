@@ -82,6 +82,9 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 
 #define MASKED (-3.0e38f)
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 // ======================================================================
 // 1. reference scheme
 // ======================================================================
@@ -101,12 +104,16 @@ struct RefArgs {
     // between kv heads: head-major (B, Hk, S, d) by default; the decode
     // step reads a row-major cache (S, Hk, d) in place
     size_t k_tok, k_head, v_tok, v_head;
-    // pre-pass products
-    float *kmean;     // [B*Hk*nkb][d]
-    float *kdelta;    // [B*Hk*S]
-    uint32_t *khat;   // [B*Hk*S][d4]
-    float *vd;        // [B*Hk*nkb][dv]
-    uint32_t *vhat;   // [B*Hk*nkb][dv][blk4]
+    // pre-pass products, laid out for pst tokens (pnkb key blocks) per kv
+    // head: S (nkb) except for a decode state sized for a cache's capacity;
+    // the pre-pass quantises key blocks kb0 .. nkb-1 (kb0 > 0 only when the
+    // codes of the earlier, complete blocks are kept from a previous step)
+    size_t pst, pnkb, kb0;
+    float *kmean;     // [B*Hk*pnkb][d]
+    float *kdelta;    // [B*Hk*pst]
+    uint32_t *khat;   // [B*Hk*pst][d4]
+    float *vd;        // [B*Hk*pnkb][dv]
+    uint32_t *vhat;   // [B*Hk*pnkb][dv][blk4]
     // per-row state when it does not fit in LDS ([slot][row], rows = B*H*S)
     float *gsc;       // [block][rows]
     uint32_t *gph;    // [blk4][rows]
@@ -133,7 +140,7 @@ __host__ __device__ __forceinline__ size_t ref_prep_ch(size_t maxd) {
 __global__ void __launch_bounds__(256) sage_ref_prep(RefArgs a) {
     extern __shared__ __attribute__((aligned(16))) float tile[];  // [ch][maxd]
     __shared__ float km[REF_MAXD];
-    const size_t kb = blockIdx.x, bk = blockIdx.y;
+    const size_t kb = a.kb0 + blockIdx.x, bk = blockIdx.y;
     const size_t j0 = kb * a.block;
     const size_t j1 = j0 + a.block < a.S ? j0 + a.block : a.S;
     const size_t kj = j1 - j0;
@@ -173,18 +180,48 @@ __global__ void __launch_bounds__(256) sage_ref_prep(RefArgs a) {
         }
         __syncthreads();
     };
+    // A block whose K and V each take at most 8 16-byte loads a thread (and
+    // whose rows are 16-byte aligned): every load of the block is issued at
+    // once, V held in registers while K is worked on -- one trip to memory
+    // instead of one per staged pass.
+    const uint32_t dq = (uint32_t)(a.d / 4), vq = (uint32_t)(a.dv / 4);
+    const bool fast = one && a.d % 4 == 0 && a.dv % 4 == 0 && a.k_tok % 4 == 0 && a.v_tok % 4 == 0 &&
+                      ((((uintptr_t)K) | ((uintptr_t)V)) & 15) == 0 && kj * dq <= 8 * (size_t)nt &&
+                      kj * vq <= 8 * (size_t)nt;
+    const uint32_t nkq = (uint32_t)kj * dq, nvq = (uint32_t)kj * vq;
+    f32x4_t vr[8];
+    if (fast) {
+        f32x4_t kr[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t it = (uint32_t)(tid + u * nt), i = it < nkq ? it : nkq - 1;
+            kr[u] = *(const f32x4_t *)(K + (j0 + i / dq) * a.k_tok + 4 * (i % dq));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t it = (uint32_t)(tid + u * nt), i = it < nvq ? it : nvq - 1;
+            vr[u] = *(const f32x4_t *)(V + (j0 + i / vq) * a.v_tok + 4 * (i % vq));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t it = (uint32_t)(tid + u * nt);
+            if (it < nkq) *(f32x4_t *)&tile[(it / dq) * maxd + 4 * (it % dq)] = kr[u];
+        }
+        __syncthreads();
+    }
     // block mean of K, sequential over the tokens
     float ssum = 0.0f;
     for (size_t t0 = j0; t0 < j1; t0 += CH) {
         const size_t tc = j1 - t0 < CH ? j1 - t0 : CH;
-        stage(K, a.k_tok, t0, tc, a.d);
+        if (!fast) stage(K, a.k_tok, t0, tc, a.d);
         if ((size_t)tid < a.d)
+#pragma unroll 8
             for (size_t t = 0; t < tc; t++) ssum += tile[t * maxd + tid];
     }
     if ((size_t)tid < a.d) {
         const float m = ssum / (float)kj;
         km[tid] = m;
-        a.kmean[(bk * a.nkb + kb) * a.d + tid] = m;
+        a.kmean[(bk * a.pnkb + kb) * a.d + tid] = m;
     }
     __syncthreads();
     // per-token peak, delta and codes: a wave per token, or a half-wave per
@@ -214,11 +251,11 @@ __global__ void __launch_bounds__(256) sage_ref_prep(RefArgs a) {
             }
             float kdelta = 1.0f;
             if (kpeak > 0.0f) kdelta = kpeak / 127.0f;
-            if (wl == 0) a.kdelta[bk * a.S + jj] = kdelta;
+            if (wl == 0) a.kdelta[bk * a.pst + jj] = kdelta;
             if ((size_t)wl < a.d4) {
                 int c4[4];
                 for (int e = 0; e < 4; e++) c4[e] = c0 + e < a.d ? q8(g[e] / kdelta) : 0;
-                a.khat[(bk * a.S + jj) * a.d4 + wl] = pack4(c4[0], c4[1], c4[2], c4[3]);
+                a.khat[(bk * a.pst + jj) * a.d4 + wl] = pack4(c4[0], c4[1], c4[2], c4[3]);
             }
         }
     }
@@ -226,8 +263,19 @@ __global__ void __launch_bounds__(256) sage_ref_prep(RefArgs a) {
     float vpeak = 0.0f;
     for (size_t t0 = j0; t0 < j1; t0 += CH) {
         const size_t tc = j1 - t0 < CH ? j1 - t0 : CH;
-        stage(V, a.v_tok, t0, tc, a.dv);
+        if (fast) {
+            __syncthreads();  // every wave is done with K's tile
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t it = (uint32_t)(tid + u * nt);
+                if (it < nvq) *(f32x4_t *)&tile[(it / vq) * maxd + 4 * (it % vq)] = vr[u];
+            }
+            __syncthreads();
+        } else {
+            stage(V, a.v_tok, t0, tc, a.dv);
+        }
         if ((size_t)tid < a.dv)
+#pragma unroll 8
             for (size_t t = 0; t < tc; t++) {
                 float x = tile[t * maxd + tid];
                 float ax = x < 0.0f ? 0.0f - x : x;
@@ -237,12 +285,12 @@ __global__ void __launch_bounds__(256) sage_ref_prep(RefArgs a) {
     if ((size_t)tid < a.dv) {
         const float vd = vpeak > 0.0f ? vpeak / 127.0f : 1.0f;
         km[tid] = vd;  // the K means are no longer needed
-        a.vd[(bk * a.nkb + kb) * a.dv + tid] = vd;
+        a.vd[(bk * a.pnkb + kb) * a.dv + tid] = vd;
     }
     __syncthreads();
     // codes four tokens a word, the (channel, word) items over every thread
     const uint32_t dv = (uint32_t)a.dv;
-    uint32_t *vrow = a.vhat + (bk * a.nkb + kb) * a.dv * a.blk4;
+    uint32_t *vrow = a.vhat + (bk * a.pnkb + kb) * a.dv * a.blk4;
     for (size_t t0 = j0; t0 < j1; t0 += CH) {
         const size_t tc = j1 - t0 < CH ? j1 - t0 : CH;
         if (!one) stage(V, a.v_tok, t0, tc, a.dv);
@@ -338,8 +386,8 @@ __global__ void __launch_bounds__(REF_ROWS) sage_ref_main(RefArgs a) {
         const size_t kj = j1 - j0, kb = j0 / a.block;
         const bool active = j0 < j_stop;
         __syncthreads();
-        for (size_t c = tid; c < a.d; c += REF_ROWS) kms[c] = a.kmean[(bk * a.nkb + kb) * a.d + c];
-        for (size_t c = tid; c < dv; c += REF_ROWS) vdl[c] = a.vd[(bk * a.nkb + kb) * dv + c];
+        for (size_t c = tid; c < a.d; c += REF_ROWS) kms[c] = a.kmean[(bk * a.pnkb + kb) * a.d + c];
+        for (size_t c = tid; c < dv; c += REF_ROWS) vdl[c] = a.vd[(bk * a.pnkb + kb) * dv + c];
         __syncthreads();
         // shift = sum_c (q^_c * dq) * kmean_c, element order (:253)
         float shift = 0.0f;
@@ -358,9 +406,9 @@ __global__ void __launch_bounds__(REF_ROWS) sage_ref_main(RefArgs a) {
         for (size_t t0 = 0; t0 < kj; t0 += REF_CH) {
             const size_t tc = kj - t0 < REF_CH ? kj - t0 : REF_CH;
             __syncthreads();
-            for (size_t t = tid; t < tc; t += REF_ROWS) kdl[t] = a.kdelta[bk * a.S + j0 + t0 + t];
+            for (size_t t = tid; t < tc; t += REF_ROWS) kdl[t] = a.kdelta[bk * a.pst + j0 + t0 + t];
             for (size_t x = tid; x < tc * d4; x += REF_ROWS)
-                kc[x] = a.khat[(bk * a.S + j0 + t0) * d4 + x];
+                kc[x] = a.khat[(bk * a.pst + j0 + t0) * d4 + x];
             __syncthreads();
             if (active) {
                 for (size_t t = 0; t < tc; t++) {
@@ -416,7 +464,7 @@ __global__ void __launch_bounds__(REF_ROWS) sage_ref_main(RefArgs a) {
             __syncthreads();
             for (size_t x = tid; x < dv * tw; x += REF_ROWS) {
                 size_t c = x / tw, w = x % tw;
-                vc[c * (REF_CH / 4) + w] = a.vhat[((bk * a.nkb + kb) * dv + c) * a.blk4 + w0 + w];
+                vc[c * (REF_CH / 4) + w] = a.vhat[((bk * a.pnkb + kb) * dv + c) * a.blk4 + w0 + w];
             }
             __syncthreads();
             if (active) {
@@ -513,6 +561,9 @@ static RefPlan ref_plan(const qbk_attn_shape *s, size_t block) {
     a.k_head = a.S * a.d;
     a.v_tok = a.dv;
     a.v_head = a.S * a.dv;
+    a.pst = a.S;
+    a.pnkb = a.nkb;
+    a.kb0 = 0;
     const size_t rows = a.B * a.H * a.S, bk = a.B * a.Hk;
     size_t off = 0;
     auto take = [&](size_t n) {
@@ -581,9 +632,9 @@ static int run_ref(const qbk_attn_shape *s, const float *q, const float *k, cons
 // (seq, n_kv_heads, d) in place -- the layout KvCache::head_major gathers
 // from (engine/mod.rs:1236-1268).
 //   sage_dec_scores  (key block, head): the block's shift, scores, max
-//   sage_dec_stats   (head): the running max, live flag and alpha per block
-//   sage_dec_pv      (key block, head): p, their sum in key order, P codes,
-//                    and each channel's (P^.V^)/127 * dv term of the block
+//   sage_dec_pv      (key block, head): the running max, live flag and alpha
+//                    of the block, p, their sum in key order, P codes, and
+//                    each channel's (P^.V^)/127 * dv term of the block
 //   sage_dec_combine (head): l and O over the blocks in order, then O / l
 
 #define DEC_CH 4096  // keys of a block whose p and codes sit in LDS at once
@@ -591,9 +642,11 @@ static int run_ref(const qbk_attn_shape *s, const float *q, const float *k, cons
 struct DecArgs {
     RefArgs r;                           // shape (S = seq_kv), pre-pass products
     float *sc;                           // [H][S] scores, then p
-    float *bmax, *bm, *balpha, *besum;   // [H][nkb]
+    float *bmax, *balpha, *besum;        // [H][nkb]
     int *blive;                          // [H][nkb]
     float *pvt;                          // [H][nkb][dv]
+    uint32_t *qsw;                       // [H][d4] the query's codes (grouped kernels)
+    float *qdl;                          // [H] and its delta
 };
 
 // max over the workgroup (blockDim.x a multiple of 64, <= 1024)
@@ -612,15 +665,295 @@ __device__ __forceinline__ float dec_wg_max(float v, float *red) {
     return m;
 }
 
+// Pre-pass of a decode step, for blocks that fit in LDS: the (key block, kv
+// head) work of sage_ref_prep (the same f32 operations) spread over
+// DPREP_KS workgroups for K -- each forms the block's channel means (the
+// first writes them) and then the deltas and codes of its share of the
+// tokens -- and DPREP_VS for V, each a share of the channels.  Each
+// workgroup issues all of its loads at once (up to DPREP_U 16-byte loads a
+// thread), so a step's pre-pass costs about one trip to memory and a short
+// serial tail instead of one workgroup's whole sequence.
+#define DPREP_KS 4
+#define DPREP_VS 4
+#define DPREP_U 16
+#define DPREP_LDS 61440
+
+struct DPrepGeom {
+    uint32_t kq, kstep, vq, vstep;  // 16-byte columns and rows per pass of a K / V load
+    size_t lds;
+    bool ok;
+};
+
+static DPrepGeom dprep_geom(const RefArgs &a, const void *k, const void *v) {
+    DPrepGeom g{};
+    const size_t kj = a.block < a.S ? a.block : a.S;
+    if (a.d % 4 || a.dv % 4 || ((uintptr_t)k & 15) || ((uintptr_t)v & 15)) return g;
+    g.kq = (uint32_t)(a.d / 4);
+    g.kstep = 256 / g.kq;
+    g.vq = (uint32_t)div_ceil(a.dv / 4, DPREP_VS);
+    g.vstep = 256 / g.vq;
+    const size_t kjp = 4 * div_ceil(kj, 4);  // V is staged channel-major with rows of kjp tokens
+    g.lds = 4 * (kj * a.d > 4 * (size_t)g.vq * kjp ? kj * a.d : 4 * (size_t)g.vq * kjp);
+    g.ok = g.kstep > 0 && g.vstep > 0 && kj <= (size_t)DPREP_U * g.kstep && kj <= (size_t)DPREP_U * g.vstep &&
+           g.lds <= DPREP_LDS && div_ceil(kj, DPREP_KS) <= 256;
+    return g;
+}
+
+// psi_Q of the step's query (gpu_attention.rs:113-159) for the heads of kv
+// head bk: a wave per head, lane l holding channels 4l .. 4l+3 (d <= 256);
+// the peak is a max, so a wave reduction gives the reference's value
+__device__ void dec_query_codes(const RefArgs &a, uint32_t bk, uint32_t *qsw, float *qdl) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t G = (uint32_t)(a.H / a.Hk), d4 = (uint32_t)a.d / 4;
+    for (uint32_t hg = wave; hg < G; hg += 4) {
+        const uint32_t h = bk * G + hg;
+        const float *qi = a.q + (size_t)h * a.d;
+        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (lane < d4)
+#pragma unroll
+            for (int e = 0; e < 4; e++) x[e] = qi[4 * lane + e];
+        float pk = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float v = x[e] * a.inv_sqrt_d;
+            const float av = v < 0.0f ? 0.0f - v : v;
+            if (av > pk) pk = av;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float w = __shfl_xor(pk, o, 64);
+            pk = w > pk ? w : pk;
+        }
+        const float qdelta = pk > 0.0f ? pk / 127.0f : 1.0f;
+        if (lane < d4) {
+            int c4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) c4[e] = q8((x[e] * a.inv_sqrt_d) / qdelta);
+            qsw[(size_t)h * d4 + lane] = pack4(c4[0], c4[1], c4[2], c4[3]);
+        }
+        if (lane == 0) qdl[h] = qdelta;
+    }
+}
+
+// grid (max(nkb - kb0, 1), Hk, DPREP_KS + DPREP_VS + 1): the last slice
+// forms the query's codes (once per kv head, when qsw is given)
+__global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uint32_t *qsw, float *qdl) {
+    extern __shared__ __attribute__((aligned(16))) float tile[];  // [kj][row of this workgroup]
+    __shared__ __attribute__((aligned(16))) float km[REF_MAXD];  // K means, then V scales
+    __shared__ float kdl[256];                                    // deltas of this workgroup's tokens
+    const uint32_t tid = threadIdx.x, z = blockIdx.z;
+    if (z == DPREP_KS + DPREP_VS) {
+        if (blockIdx.x == 0 && qsw) dec_query_codes(a, blockIdx.y, qsw, qdl);
+        return;
+    }
+    const uint32_t kb = (uint32_t)a.kb0 + blockIdx.x, bk = blockIdx.y;
+    if (kb >= a.nkb) return;
+    const uint32_t j0 = kb * (uint32_t)a.block;
+    const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
+    const uint32_t d = (uint32_t)a.d, d4 = d / 4;
+    f32x4_t r[DPREP_U];
+    if (z < DPREP_KS) {
+        const float *K = a.k + bk * a.k_head + (size_t)j0 * a.k_tok;
+        const uint32_t q = tid % g.kq, r0 = tid / g.kq;
+        const bool lane_ok = r0 < g.kstep;
+#pragma unroll
+        for (uint32_t u = 0; u < DPREP_U; u++) {
+            const uint32_t row = r0 + u * g.kstep;
+            r[u] = *(const f32x4_t *)(K + (size_t)(row < kj ? row : kj - 1) * a.k_tok + 4 * q);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < DPREP_U; u++) {
+            const uint32_t row = r0 + u * g.kstep;
+            if (lane_ok && row < kj) *(f32x4_t *)&tile[row * d + 4 * q] = r[u];
+        }
+        __syncthreads();
+        // the block's mean per channel, sequential over its tokens
+        if (tid < d) {
+            float ssum = 0.0f;
+#pragma unroll 8
+            for (uint32_t t = 0; t < kj; t++) ssum += tile[t * d + tid];
+            const float m = ssum / (float)kj;
+            km[tid] = m;
+            if (z == 0) a.kmean[((size_t)bk * a.pnkb + kb) * d + tid] = m;
+        }
+        __syncthreads();
+        // this workgroup's tokens
+        const uint32_t per = (kj + DPREP_KS - 1) / DPREP_KS, t0 = z * per;
+        const uint32_t t1 = t0 + per < kj ? t0 + per : kj;
+        if (t0 >= t1) return;
+        const uint32_t nt = t1 - t0;
+        if ((d4 & (d4 - 1)) == 0) {
+            // a token's d4 words in d4 consecutive lanes: its peak by a lane
+            // reduction (a max), then each lane's word of codes
+            const uint32_t lg = 31 - __builtin_clz(d4);
+            for (uint32_t i0 = 0; i0 < nt * d4; i0 += 256) {
+                const uint32_t it = i0 + tid;
+                const bool ok = it < nt * d4;
+                const uint32_t tt = ok ? it >> lg : 0, w = it & (d4 - 1), t = t0 + tt;
+                const f32x4_t x = *(const f32x4_t *)&tile[t * d + 4 * w];
+                const f32x4_t m = *(const f32x4_t *)&km[4 * w];
+                float gv[4], kpeak = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    gv[e] = x[e] - m[e];
+                    const float ag = gv[e] < 0.0f ? 0.0f - gv[e] : gv[e];
+                    if (ag > kpeak) kpeak = ag;
+                }
+                for (uint32_t o = 1; o < d4; o <<= 1) {
+                    const float wv = __shfl_xor(kpeak, o, 64);
+                    kpeak = wv > kpeak ? wv : kpeak;
+                }
+                float kdelta = 1.0f;
+                if (kpeak > 0.0f) kdelta = kpeak / 127.0f;
+                if (ok) {
+                    if (w == 0) a.kdelta[(size_t)bk * a.pst + j0 + t] = kdelta;
+                    int c4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) c4[e] = q8(gv[e] / kdelta);
+                    a.khat[((size_t)bk * a.pst + j0 + t) * d4 + w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+                }
+            }
+            return;
+        }
+        // otherwise a thread per token for the peak, then (token, word) items
+        if (tid < nt) {
+            const uint32_t t = t0 + tid;
+            float kpeak = 0.0f;
+            for (uint32_t w = 0; w < d4; w++) {
+                const f32x4_t x = *(const f32x4_t *)&tile[t * d + 4 * w];
+                const f32x4_t m = *(const f32x4_t *)&km[4 * w];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float gv = x[e] - m[e];
+                    const float ag = gv < 0.0f ? 0.0f - gv : gv;
+                    if (ag > kpeak) kpeak = ag;
+                }
+            }
+            float kdelta = 1.0f;
+            if (kpeak > 0.0f) kdelta = kpeak / 127.0f;
+            kdl[tid] = kdelta;
+            a.kdelta[(size_t)bk * a.pst + j0 + t] = kdelta;
+        }
+        __syncthreads();
+        for (uint32_t it = tid; it < nt * d4; it += 256) {
+            const uint32_t tt = it / d4, w = it % d4, t = t0 + tt;
+            const f32x4_t x = *(const f32x4_t *)&tile[t * d + 4 * w];
+            const f32x4_t m = *(const f32x4_t *)&km[4 * w];
+            const float kdelta = kdl[tt];
+            int c4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) c4[e] = q8((x[e] - m[e]) / kdelta);
+            a.khat[((size_t)bk * a.pst + j0 + t) * d4 + w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+        }
+    } else {
+        // V: channels 4 * c4_0 .. of this workgroup, all of the block's
+        // tokens, staged channel-major ([cw][kjp], kjp = kj rounded up to 4)
+        const uint32_t dv4 = (uint32_t)a.dv / 4, c4_0 = (z - DPREP_KS) * g.vq;
+        if (c4_0 >= dv4) return;
+        const uint32_t cq = dv4 - c4_0 < g.vq ? dv4 - c4_0 : g.vq, cw = 4 * cq;
+        const uint32_t step = 256 / cq, tw = (kj + 3) / 4, kjp = 4 * tw;
+        const float *V = a.v + bk * a.v_head + (size_t)j0 * a.v_tok + 4 * c4_0;
+        const uint32_t q = tid % cq, r0 = tid / cq;
+        const bool lane_ok = r0 < step;
+#pragma unroll
+        for (uint32_t u = 0; u < DPREP_U; u++) {
+            const uint32_t row = r0 + u * step;
+            r[u] = *(const f32x4_t *)(V + (size_t)(row < kj ? row : kj - 1) * a.v_tok + 4 * q);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < DPREP_U; u++) {
+            const uint32_t row = r0 + u * step;
+            if (lane_ok && row < kj)
+#pragma unroll
+                for (int e = 0; e < 4; e++) tile[(4 * q + e) * kjp + row] = r[u][e];
+        }
+        __syncthreads();
+        uint32_t *vrow = a.vhat + ((size_t)bk * a.pnkb + kb) * a.dv * a.blk4;
+        if ((tw & (tw - 1)) == 0 && tw <= 64) {
+            // a channel's tw words in tw consecutive lanes: its peak over the
+            // block by a lane reduction (a max), then each lane's word
+            const uint32_t lg = 31 - __builtin_clz(tw);
+            for (uint32_t i0 = 0; i0 < cw * tw; i0 += 256) {
+                const uint32_t it = i0 + tid;
+                const bool ok = it < cw * tw;
+                const uint32_t c = ok ? it >> lg : 0, w = it & (tw - 1);
+                const f32x4_t x = *(const f32x4_t *)&tile[c * kjp + 4 * w];
+                float vpeak = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float xv = 4 * w + e < kj ? x[e] : 0.0f;
+                    const float ax = xv < 0.0f ? 0.0f - xv : xv;
+                    if (ax > vpeak) vpeak = ax;
+                }
+                for (uint32_t o = 1; o < tw; o <<= 1) {
+                    const float wv = __shfl_xor(vpeak, o, 64);
+                    vpeak = wv > vpeak ? wv : vpeak;
+                }
+                const float vd = vpeak > 0.0f ? vpeak / 127.0f : 1.0f;
+                if (ok) {
+                    if (w == 0) a.vd[((size_t)bk * a.pnkb + kb) * a.dv + 4 * c4_0 + c] = vd;
+                    int c4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) c4[e] = 4 * w + e < kj ? q8(x[e] / vd) : 0;
+                    vrow[(size_t)(4 * c4_0 + c) * a.blk4 + w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+                }
+            }
+            return;
+        }
+        // otherwise a thread per channel for the peak, then (channel, word) items
+        if (tid < cw) {
+            float vpeak = 0.0f;
+#pragma unroll 8
+            for (uint32_t t = 0; t < kj; t++) {
+                const float x = tile[tid * kjp + t];
+                const float ax = x < 0.0f ? 0.0f - x : x;
+                if (ax > vpeak) vpeak = ax;
+            }
+            const float vd = vpeak > 0.0f ? vpeak / 127.0f : 1.0f;
+            km[tid] = vd;
+            a.vd[((size_t)bk * a.pnkb + kb) * a.dv + 4 * c4_0 + tid] = vd;
+        }
+        __syncthreads();
+        for (uint32_t it = tid; it < cw * tw; it += 256) {
+            const uint32_t c = it % cw, w = it / cw;
+            const float vd = km[c];
+            int c4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t t = 4 * w + e;
+                c4[e] = t < kj ? q8(tile[c * kjp + t] / vd) : 0;
+            }
+            vrow[(size_t)(4 * c4_0 + c) * a.blk4 + w] = pack4(c4[0], c4[1], c4[2], c4[3]);
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256) sage_dec_scores(DecArgs da) {
     const RefArgs &a = da.r;
     __shared__ uint32_t qs[REF_MAXD / 4];
-    __shared__ float kms[REF_MAXD];
+    __shared__ __attribute__((aligned(16))) float term[REF_MAXD];
     __shared__ float red[4];
     __shared__ float shv;
     const int tid = threadIdx.x;
     const size_t kb = blockIdx.x, h = blockIdx.y;
     const size_t bk = h / (a.H / a.Hk);
+    const size_t j0 = kb * a.block, j1 = j0 + a.block < a.S ? j0 + a.block : a.S;
+    // this thread's loads that do not wait on the query: its key's delta
+    // and the block's mean of its channel
+    const size_t jj0 = j0 + tid;
+    const float kd0 = jj0 < j1 ? a.kdelta[bk * a.pst + jj0] : 0.0f;
+    const float kmc = (size_t)tid < a.d ? a.kmean[(bk * a.pnkb + kb) * a.d + tid] : 0.0f;
+    // and, for code rows of at most 8 whole 16-byte words (d <= 128), its
+    // key's codes
+    const bool vec = (a.d4 & 3) == 0;
+    const size_t n4 = a.d4 >> 2;
+    const bool pre = vec && n4 <= 8 && jj0 < j1;
+    u32x4_t kv0[8];
+    if (pre) {
+        const u32x4_t *kc = (const u32x4_t *)(a.khat + (bk * a.pst + jj0) * a.d4);
+#pragma unroll
+        for (int u = 0; u < 8; u++) kv0[u] = (size_t)u < n4 ? kc[u] : u32x4_t{0, 0, 0, 0};
+    }
     // psi_Q of the query (gpu_attention.rs:113-159; the peak is a max)
     const float *qi = a.q + h * a.d;
     float pk = 0.0f;
@@ -639,26 +972,62 @@ __global__ void __launch_bounds__(256) sage_dec_scores(DecArgs da) {
         }
         qs[w] = pack4(c4[0], c4[1], c4[2], c4[3]);
     }
-    for (size_t c = tid; c < a.d; c += blockDim.x) kms[c] = a.kmean[(bk * a.nkb + kb) * a.d + c];
+    // shift = sum_c (q^_c * dq) * kmean_c in element order (:253): the
+    // products in parallel (d <= REF_MAXD <= the 256 threads), the sum by
+    // one thread over them in order
+    if ((size_t)tid < a.d) {
+        const int qc = q8((qi[tid] * a.inv_sqrt_d) / qdelta);
+        term[tid] = ((float)qc * qdelta) * kmc;
+    }
     __syncthreads();
-    // shift = sum_c (q^_c * dq) * kmean_c in element order (:253)
     if (tid == 0) {
         float shift = 0.0f;
-        for (size_t c = 0; c < a.d; c++) {
-            const int qc = (int)(int8_t)(qs[c / 4] >> (8 * (c % 4)));
-            shift += ((float)qc * qdelta) * kms[c];
+        size_t c = 0;
+#pragma unroll 4
+        for (; c + 4 <= a.d; c += 4) {
+            const float4 t4 = *(const float4 *)&term[c];
+            shift += t4.x;
+            shift += t4.y;
+            shift += t4.z;
+            shift += t4.w;
         }
+        for (; c < a.d; c++) shift += term[c];
         shv = shift;
     }
     __syncthreads();
     const float shift = shv;
-    const size_t j0 = kb * a.block, j1 = j0 + a.block < a.S ? j0 + a.block : a.S;
     float rm = MASKED;
-    for (size_t jj = j0 + tid; jj < j1; jj += blockDim.x) {
-        const uint32_t *kc = a.khat + (bk * a.S + jj) * a.d4;
+    for (size_t jj = jj0; jj < j1; jj += blockDim.x) {
+        const uint32_t *kc = a.khat + (bk * a.pst + jj) * a.d4;
         int acc = 0;
-        for (size_t w = 0; w < a.d4; w++) acc = __builtin_amdgcn_sdot4((int)qs[w], (int)kc[w], acc, false);
-        const float sv = (float)acc * qdelta * a.kdelta[bk * a.S + jj] + shift;
+        if (pre && jj == jj0) {
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if ((size_t)u < n4) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        acc = __builtin_amdgcn_sdot4((int)qs[4 * u + e], (int)kv0[u][e], acc, false);
+                }
+        } else if (vec) {
+            for (size_t w0 = 0; w0 < n4; w0 += 8) {
+                u32x4_t kv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    kv[u] = w0 + u < n4 ? ((const u32x4_t *)kc)[w0 + u] : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (w0 + u < n4) {
+                        const uint32_t *qw = qs + 4 * (w0 + u);
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            acc = __builtin_amdgcn_sdot4((int)qw[e], (int)kv[u][e], acc, false);
+                    }
+            }
+        } else {
+            for (size_t w = 0; w < a.d4; w++) acc = __builtin_amdgcn_sdot4((int)qs[w], (int)kc[w], acc, false);
+        }
+        const float kdl = jj == jj0 ? kd0 : a.kdelta[bk * a.pst + jj];
+        const float sv = (float)acc * qdelta * kdl + shift;
         da.sc[h * a.S + jj] = sv;
         if (sv > rm) rm = sv;
     }
@@ -666,59 +1035,57 @@ __global__ void __launch_bounds__(256) sage_dec_scores(DecArgs da) {
     if (tid == 0) da.bmax[h * a.nkb + kb] = rm;
 }
 
-// :288-296 per block in order (m_new, live), then alpha per block; the
-// blocks' maxima staged through LDS 64 at a time for the sequential scan
-__global__ void __launch_bounds__(64) sage_dec_stats(DecArgs da) {
-    const RefArgs &a = da.r;
-    __shared__ float sm[64];
-    __shared__ float carry, cin;
-    const int tid = threadIdx.x;
-    const size_t h = blockIdx.x, nkb = a.nkb;
-    if (tid == 0) carry = MASKED;
-    for (size_t kb0 = 0; kb0 < nkb; kb0 += 64) {
-        const size_t n = nkb - kb0 < 64 ? nkb - kb0 : 64;
-        __syncthreads();
-        if ((size_t)tid < n) sm[tid] = da.bmax[h * nkb + kb0 + tid];
-        __syncthreads();
-        if (tid == 0) {
-            float m = carry;
-            cin = m;
-            for (size_t i = 0; i < n; i++) {
-                float m_new = m;
-                if (sm[i] > m_new) m_new = sm[i];
-                sm[i] = m_new;
-                m = m_new;
-            }
-            carry = m;
-        }
-        __syncthreads();
-        if ((size_t)tid < n) {
-            const size_t kb = kb0 + tid;
-            const float m_new = sm[tid], m = tid ? sm[tid - 1] : cin;
-            const int live = !(m_new < MASKED * 0.5f);
-            da.bm[h * nkb + kb] = m_new;
-            da.blive[h * nkb + kb] = live;
-            da.balpha[h * nkb + kb] = live ? qbk_expf(m - m_new) : 0.0f;
-        }
-    }
-}
-
-// :297-316 (p, esum in key order, codes) and :317-341 (P^.V^ per channel)
+// :288-296 (the running max, live flag and alpha of this block), :297-316
+// (p, esum in key order, codes) and :317-341 (P^.V^ per channel).  The
+// running max before a block is the max of MASKED and the earlier blocks'
+// maxima: a max, so the reference's scan and a reduction give one value
+// (no score is -0.0: shift starts at +0.0).
 __global__ void __launch_bounds__(256) sage_dec_pv(DecArgs da) {
     const RefArgs &a = da.r;
-    __shared__ float pf[DEC_CH];
+    __shared__ __attribute__((aligned(16))) float pf[DEC_CH];
     __shared__ uint32_t ph[DEC_CH / 4];
+    __shared__ float red[4];
     const int tid = threadIdx.x;
     const size_t kb = blockIdx.x, h = blockIdx.y, nkb = a.nkb;
     const size_t bk = h / (a.H / a.Hk);
     const size_t j0 = kb * a.block, j1 = j0 + a.block < a.S ? j0 + a.block : a.S;
-    const int live = da.blive[h * nkb + kb];
-    const float m_new = da.bm[h * nkb + kb];
-    const uint32_t *vh = a.vhat + (bk * nkb + kb) * a.dv * a.blk4;
+    const uint32_t *vh = a.vhat + (bk * a.pnkb + kb) * a.dv * a.blk4;
+    // loads that wait on nothing, issued first: this thread's four scores of
+    // the first chunk and its channel's first code words (up to 8 16-byte
+    // words) and scale, alongside the earlier blocks' maxima
+    const size_t tc0 = j1 - j0 < DEC_CH ? j1 - j0 : DEC_CH, tw0 = (tc0 + 3) / 4;
+    const bool spre = (size_t)tid < tw0 && tw0 <= blockDim.x;
+    float sc0[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (spre)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const size_t t = 4 * (size_t)tid + e;
+            sc0[e] = t < tc0 ? da.sc[h * a.S + j0 + t] : 0.0f;
+        }
+    const bool vvec = (a.blk4 & 3) == 0;  // whole 16-byte words (t0 - j0 is a multiple of DEC_CH)
+    const size_t vn0 = (tw0 + 3) >> 2;
+    const bool vpre = vvec && vn0 <= 8 && (size_t)tid < a.dv;
+    u32x4_t vv0[8];
+    if (vpre) {
+        const u32x4_t *vc = (const u32x4_t *)(vh + tid * a.blk4);
+#pragma unroll
+        for (int u = 0; u < 8; u++) vv0[u] = (size_t)u < vn0 ? vc[u] : u32x4_t{0, 0, 0, 0};
+    }
+    const float vdc = (size_t)tid < a.dv ? a.vd[(bk * a.pnkb + kb) * a.dv + tid] : 0.0f;
+    float pm = MASKED;
+    for (size_t i = tid; i < kb; i += blockDim.x) {
+        const float x = da.bmax[h * nkb + i];
+        pm = x > pm ? x : pm;
+    }
+    const float bx = da.bmax[h * nkb + kb];
+    const float m = dec_wg_max(pm, red);
+    const float m_new = bx > m ? bx : m;
+    const int live = !(m_new < MASKED * 0.5f);
     float esum = 0.0f;  // thread 0's running sum
     int pv = 0;         // thread c's P^.V^ over the block (dv <= the 256 threads)
     for (size_t t0 = j0; t0 < j1; t0 += DEC_CH) {
         const size_t tc = j1 - t0 < DEC_CH ? j1 - t0 : DEC_CH, tw = (tc + 3) / 4;
+        const bool first = t0 == j0;
         __syncthreads();
         for (size_t w = tid; w < tw; w += blockDim.x) {
             int c4[4];
@@ -726,7 +1093,8 @@ __global__ void __launch_bounds__(256) sage_dec_pv(DecArgs da) {
                 const size_t t = 4 * w + e;
                 int pc = 0;
                 if (t < tc) {
-                    const float p = live ? qbk_expf(da.sc[h * a.S + t0 + t] - m_new) : 0.0f;
+                    const float scv = first && spre ? sc0[e] : da.sc[h * a.S + t0 + t];
+                    const float p = live ? qbk_expf(scv - m_new) : 0.0f;
                     pf[t] = p;
                     float pr = __builtin_rintf(p * 127.0f);
                     pr = pr > 127.0f ? 127.0f : pr;
@@ -738,64 +1106,305 @@ __global__ void __launch_bounds__(256) sage_dec_pv(DecArgs da) {
             ph[w] = pack4(c4[0], c4[1], c4[2], c4[3]);
         }
         __syncthreads();
-        if (tid == 0)
-            for (size_t t = 0; t < tc; t++) esum += pf[t];
+        if (tid == 0) {
+            size_t t = 0;
+#pragma unroll 4
+            for (; t + 4 <= tc; t += 4) {
+                const float4 p4 = *(const float4 *)&pf[t];
+                esum += p4.x;
+                esum += p4.y;
+                esum += p4.z;
+                esum += p4.w;
+            }
+            for (; t < tc; t++) esum += pf[t];
+        }
         if ((size_t)tid < a.dv) {
             const uint32_t *vc = vh + tid * a.blk4 + (t0 - j0) / 4;
-            for (size_t w = 0; w < tw; w++) pv = __builtin_amdgcn_sdot4((int)ph[w], (int)vc[w], pv, false);
-        }
-    }
-    if (tid == 0) da.besum[h * nkb + kb] = esum;
-    if ((size_t)tid < a.dv)
-        da.pvt[(h * nkb + kb) * a.dv + tid] = (float)pv * (1.0f / 127.0f) * a.vd[(bk * nkb + kb) * a.dv + tid];
-}
-
-// :315 and :337-338 over the blocks in order, then :346; the blocks'
-// alpha, esum and live flags staged through LDS, each thread's P.V terms
-// loaded eight blocks at a time ahead of the recurrence
-__global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da) {
-    const RefArgs &a = da.r;
-    __shared__ float sa[64], se[64];
-    __shared__ int sl[64];
-    const size_t h = blockIdx.x, nkb = a.nkb;
-    const int tid = threadIdx.x;
-    const size_t c = tid;
-    const bool act = c < a.dv;
-    float o = 0.0f, ell = 0.0f;
-    for (size_t kb0 = 0; kb0 < nkb; kb0 += 64) {
-        const size_t n = nkb - kb0 < 64 ? nkb - kb0 : 64;
-        __syncthreads();
-        if ((size_t)tid < n) {
-            sa[tid] = da.balpha[h * nkb + kb0 + tid];
-            se[tid] = da.besum[h * nkb + kb0 + tid];
-            sl[tid] = da.blive[h * nkb + kb0 + tid];
-        }
-        __syncthreads();
-        for (size_t i0 = 0; i0 < n; i0 += 8) {
-            float t[8];
+            if (first && vpre) {
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                t[u] = act && i0 + u < n ? da.pvt[(h * nkb + kb0 + i0 + u) * a.dv + c] : 0.0f;
+                for (int u = 0; u < 8; u++)
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                if (i0 + u >= n) break;
-                const float alpha = sa[i0 + u];
-                ell = alpha * ell + se[i0 + u];
-                const float prev = sl[i0 + u] ? o : 0.0f;
-                o = alpha * prev + t[u];
+                    for (int e = 0; e < 4; e++) {
+                        const size_t w = 4 * (size_t)u + e;
+                        if (w < tw) pv = __builtin_amdgcn_sdot4((int)ph[w], (int)vv0[u][e], pv, false);
+                    }
+            } else if (vvec) {
+                const size_t n4 = (tw + 3) >> 2;
+                for (size_t w0 = 0; w0 < n4; w0 += 8) {
+                    u32x4_t vv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        vv[u] = w0 + u < n4 ? ((const u32x4_t *)vc)[w0 + u] : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const size_t w = 4 * (w0 + u) + e;
+                            if (w < tw) pv = __builtin_amdgcn_sdot4((int)ph[w], (int)vv[u][e], pv, false);
+                        }
+                }
+            } else {
+                for (size_t w = 0; w < tw; w++) pv = __builtin_amdgcn_sdot4((int)ph[w], (int)vc[w], pv, false);
             }
         }
     }
-    if (act) a.out[h * a.dv + c] = o / ell;
+    if (tid == 0) {
+        da.besum[h * nkb + kb] = esum;
+        da.blive[h * nkb + kb] = live;
+        da.balpha[h * nkb + kb] = live ? qbk_expf(m - m_new) : 0.0f;
+    }
+    if ((size_t)tid < a.dv)
+        da.pvt[(h * nkb + kb) * a.dv + tid] = (float)pv * (1.0f / 127.0f) * vdc;
+}
+
+// :315 and :337-338 over the blocks in order, then :346.  DEC_CB blocks at
+// a time: every thread's P.V terms and the blocks' alpha, esum and live
+// flags loaded at once (indices clamped into the chunk) and staged through
+// LDS, then the recurrence reads them from there.  Indices are 32-bit and
+// the code is kept short: a launch this small is bound by its serial
+// instruction stream, fetches included.
+#define DEC_CB 32
+__global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da) {
+    const RefArgs &a = da.r;
+    __shared__ float sa[DEC_CB], se[DEC_CB];
+    __shared__ int sl[DEC_CB];
+    __shared__ float pvl[DEC_CB * REF_MAXD];
+    const uint32_t h = blockIdx.x, nkb = (uint32_t)a.nkb, dv = (uint32_t)a.dv, tid = threadIdx.x;
+    const bool act = tid < dv;
+    const uint32_t c = act ? tid : 0;
+    const float *pt = da.pvt + (size_t)h * nkb * dv + c;
+    const float *pa = da.balpha + (size_t)h * nkb, *pe = da.besum + (size_t)h * nkb;
+    const int *pl = da.blive + (size_t)h * nkb;
+    float o = 0.0f, ell = 0.0f;
+    for (uint32_t kb0 = 0; kb0 < nkb; kb0 += DEC_CB) {
+        const uint32_t n = nkb - kb0 < DEC_CB ? nkb - kb0 : DEC_CB;
+        float t[DEC_CB];
+#pragma unroll
+        for (uint32_t u = 0; u < DEC_CB; u++) t[u] = pt[(kb0 + (u < n ? u : n - 1)) * dv];
+        const uint32_t i = kb0 + (tid < n ? tid : n - 1);
+        const float ra = pa[i], re = pe[i];
+        const int rl = pl[i];
+        __syncthreads();
+        if (tid < DEC_CB) {
+            sa[tid] = ra;
+            se[tid] = re;
+            sl[tid] = rl;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < DEC_CB; u++) pvl[u * REF_MAXD + c] = t[u];
+        __syncthreads();
+        if (act) {
+#pragma unroll 4
+            for (uint32_t u = 0; u < n; u++) {
+                const float alpha = sa[u];
+                ell = alpha * ell + se[u];
+                const float prev = sl[u] ? o : 0.0f;
+                o = alpha * prev + pvl[u * REF_MAXD + c];
+            }
+        }
+    }
+    if (act) a.out[(size_t)h * dv + c] = o / ell;
+}
+
+// Grouped form of sage_dec_scores and sage_dec_pv: one workgroup per (key
+// block, kv head) for the G = n_heads / n_kv_heads query heads that share
+// the kv head, a wave per head, so a block's key codes are read once per
+// group and a step launches G times fewer workgroups; the query's codes
+// come from the pre-pass.  The same f32 operations in the same order as
+// the per-head kernels.  Used when G <= DEC_GMAX, a block has at most
+// DEC_KMAX keys, d and the code rows are whole 16-byte words, and there are
+// at most DEC_PMAX blocks (each workgroup reads the earlier blocks' maxima).
+#define DEC_GMAX 16
+#define DEC_KMAX 256
+#define DEC_PMAX 512
+
+__global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da) {
+    const RefArgs &a = da.r;
+    __shared__ uint32_t qs[DEC_GMAX * (REF_MAXD / 4)];
+    __shared__ float qd[DEC_GMAX];
+    __shared__ float kms[REF_MAXD];
+    __shared__ __attribute__((aligned(16))) float term[DEC_GMAX * REF_MAXD];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t kb = blockIdx.x, bk = blockIdx.y, G = (uint32_t)(a.H / a.Hk);
+    const uint32_t d = (uint32_t)a.d, d4 = d / 4, n4 = d4 / 4;
+    const uint32_t j0 = kb * (uint32_t)a.block;
+    const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
+    // the loads that wait on nothing, first: the group's query codes and
+    // deltas, the block's means, this lane's first key's codes and delta
+    for (uint32_t i = tid; i < G * d4; i += 256) qs[i] = da.qsw[(size_t)bk * G * d4 + i];
+    if (tid < G) qd[tid] = da.qdl[bk * G + tid];
+    if (tid < d) kms[tid] = a.kmean[((size_t)bk * a.pnkb + kb) * d + tid];
+    const uint32_t jl = lane < kj ? lane : kj - 1;
+    const u32x4_t *krow = (const u32x4_t *)(a.khat + ((size_t)bk * a.pst + j0 + jl) * d4);
+    u32x4_t kv[REF_MAXD / 16];
+#pragma unroll
+    for (uint32_t u = 0; u < REF_MAXD / 16; u++)
+        if (u < n4) kv[u] = krow[u];
+    const float kd0 = a.kdelta[(size_t)bk * a.pst + j0 + jl];
+    __syncthreads();
+    // the shift's terms (q^_c * dq) * kmean_c, every (head, channel) at once
+    for (uint32_t i = tid; i < G * d; i += 256) {
+        const uint32_t hg = i / d, c = i % d;
+        const int qc = (int)(int8_t)(qs[hg * d4 + c / 4] >> (8 * (c % 4)));
+        term[i] = ((float)qc * qd[hg]) * kms[c];
+    }
+    __syncthreads();
+    for (uint32_t hg = wave; hg < G; hg += 4) {
+        // shift: the terms summed in channel order (:253) by lane 0
+        float shift = 0.0f;
+        if (lane == 0) {
+            const float *t = term + hg * d;
+#pragma unroll 4
+            for (uint32_t c = 0; c < d; c += 4) {
+                const f32x4_t t4 = *(const f32x4_t *)&t[c];
+                shift += t4[0];
+                shift += t4[1];
+                shift += t4[2];
+                shift += t4[3];
+            }
+        }
+        shift = __shfl(shift, 0, 64);
+        const float qdh = qd[hg];
+        const uint32_t *qh = qs + hg * d4;
+        const size_t h = (size_t)bk * G + hg;
+        float rm = MASKED;
+        for (uint32_t j = lane; j < kj; j += 64) {
+            int acc = 0;
+            float kdl;
+            if (j == lane) {
+#pragma unroll
+                for (uint32_t u = 0; u < REF_MAXD / 16; u++)
+                    if (u < n4)
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            acc = __builtin_amdgcn_sdot4((int)qh[4 * u + e], (int)kv[u][e], acc, false);
+                kdl = kd0;
+            } else {
+                const u32x4_t *kr = (const u32x4_t *)(a.khat + ((size_t)bk * a.pst + j0 + j) * d4);
+                for (uint32_t u = 0; u < n4; u++) {
+                    const u32x4_t k4 = kr[u];
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        acc = __builtin_amdgcn_sdot4((int)qh[4 * u + e], (int)k4[e], acc, false);
+                }
+                kdl = a.kdelta[(size_t)bk * a.pst + j0 + j];
+            }
+            const float sv = (float)acc * qdh * kdl + shift;
+            da.sc[h * a.S + j0 + j] = sv;
+            if (sv > rm) rm = sv;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float w = __shfl_xor(rm, o, 64);
+            rm = w > rm ? w : rm;
+        }
+        if (lane == 0) da.bmax[h * a.nkb + kb] = rm;
+    }
+}
+
+__global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da) {
+    const RefArgs &a = da.r;
+    __shared__ __attribute__((aligned(16))) float pf[DEC_GMAX * DEC_KMAX];
+    __shared__ __attribute__((aligned(16))) uint8_t ph[DEC_GMAX * DEC_KMAX];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t kb = blockIdx.x, bk = blockIdx.y, G = (uint32_t)(a.H / a.Hk), nkb = (uint32_t)a.nkb;
+    const uint32_t dv = (uint32_t)a.dv;
+    const uint32_t j0 = kb * (uint32_t)a.block;
+    const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
+    const uint32_t tw = (kj + 3) / 4, vn4 = (tw + 3) / 4;
+    // first, this thread's channel's V codes and scale (256 / dv threads a
+    // channel, each for every (256 / dv)-th head of the group)
+    const uint32_t hstep = 256 / dv, c = tid % dv, hs = tid / dv;
+    const size_t vb = ((size_t)bk * a.pnkb + kb) * dv + c;
+    const u32x4_t *vrow = (const u32x4_t *)(a.vhat + vb * a.blk4);
+    u32x4_t vv[DEC_KMAX / 16];
+#pragma unroll
+    for (uint32_t u = 0; u < DEC_KMAX / 16; u++)
+        if (u < vn4) vv[u] = vrow[u];
+    const float vdc = a.vd[vb];
+    // and the scores of this wave's first head at this lane's first key
+    const float sc0 = wave < G && lane < kj ? da.sc[((size_t)bk * G + wave) * a.S + j0 + lane] : 0.0f;
+    // a wave per head: the running max before and after this block (a max
+    // of MASKED and the earlier blocks' maxima: the reference's scan and a
+    // reduction give one value), its live flag and alpha, p and its codes
+    for (uint32_t hg = wave; hg < G; hg += 4) {
+        const size_t h = (size_t)bk * G + hg;
+        const float *bm = da.bmax + h * nkb;
+        float pm = MASKED;
+        for (uint32_t i = lane; i < kb; i += 64) {
+            const float x = bm[i];
+            pm = x > pm ? x : pm;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float w = __shfl_xor(pm, o, 64);
+            pm = w > pm ? w : pm;
+        }
+        const float bx = bm[kb];
+        const float m_new = bx > pm ? bx : pm;
+        const int live = !(m_new < MASKED * 0.5f);
+        for (uint32_t j = lane; j < 4 * tw; j += 64) {
+            float p = 0.0f;
+            int pc = 0;
+            if (j < kj) {
+                const float scv = hg == wave && j == lane ? sc0 : da.sc[h * a.S + j0 + j];
+                p = live ? qbk_expf(scv - m_new) : 0.0f;
+                float pr = __builtin_rintf(p * 127.0f);
+                pr = pr > 127.0f ? 127.0f : pr;
+                pr = pr < 0.0f ? 0.0f : pr;
+                pc = (int)pr;
+            }
+            pf[hg * DEC_KMAX + j] = p;
+            ph[hg * DEC_KMAX + j] = (uint8_t)pc;
+        }
+        if (lane == 0) {
+            da.blive[h * nkb + kb] = live;
+            da.balpha[h * nkb + kb] = live ? qbk_expf(pm - m_new) : 0.0f;
+        }
+    }
+    __syncthreads();
+    // esum: p summed in key order (:315), by lane 0 of the head's wave
+    for (uint32_t hg = wave; hg < G; hg += 4)
+        if (lane == 0) {
+            const float *pp = pf + hg * DEC_KMAX;
+            float esum = 0.0f;
+            uint32_t t = 0;
+#pragma unroll 4
+            for (; t + 4 <= kj; t += 4) {
+                const f32x4_t p4 = *(const f32x4_t *)&pp[t];
+                esum += p4[0];
+                esum += p4[1];
+                esum += p4[2];
+                esum += p4[3];
+            }
+            for (; t < kj; t++) esum += pp[t];
+            da.besum[((size_t)bk * G + hg) * nkb + kb] = esum;
+        }
+    // P^.V^ per (head, channel) (:317-341)
+    if (hs < hstep)
+        for (uint32_t hg = hs; hg < G; hg += hstep) {
+            const uint32_t *pw = (const uint32_t *)(ph + hg * DEC_KMAX);
+            int pv = 0;
+#pragma unroll
+            for (uint32_t u = 0; u < DEC_KMAX / 16; u++)
+                if (u < vn4)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (4 * u + e < tw) pv = __builtin_amdgcn_sdot4((int)pw[4 * u + e], (int)vv[u][e], pv, false);
+            da.pvt[(((size_t)bk * G + hg) * nkb + kb) * dv + c] = (float)pv * (1.0f / 127.0f) * vdc;
+        }
 }
 
 struct DecPlan {
     DecArgs da;
     size_t ws;
-    size_t o_kmean, o_kdelta, o_khat, o_vd, o_vhat, o_sc, o_bmax, o_bm, o_balpha, o_besum, o_blive, o_pvt;
+    size_t o_kmean, o_kdelta, o_khat, o_vd, o_vhat, o_sc, o_bmax, o_balpha, o_besum, o_blive, o_pvt, o_qsw, o_qdl;
 };
 
-static DecPlan dec_plan(const qbk_attn_shape *s, size_t block) {
+// The workspace is laid out for a cache of cap tokens (cap >= seq_kv): the
+// pre-pass products of the complete key blocks stay where they are as the
+// cache grows, so a later step can keep them.
+static DecPlan dec_plan(const qbk_attn_shape *s, size_t block, size_t cap) {
     DecPlan P{};
     RefArgs &a = P.da.r;
     a.B = 1;
@@ -809,31 +1418,35 @@ static DecPlan dec_plan(const qbk_attn_shape *s, size_t block) {
     a.inv_sqrt_d = 1.0f / sqrtf((float)a.d);
     a.nkb = div_ceil(a.S, block);
     a.d4 = div_ceil(a.d, 4);
-    a.blk4 = div_ceil(block < a.S ? block : a.S, 4);
+    a.blk4 = div_ceil(block < cap ? block : cap, 4);
     // the cache's row-major layout (seq, n_kv_heads, d)
     a.k_tok = a.Hk * a.d;
     a.k_head = a.d;
     a.v_tok = a.Hk * a.dv;
     a.v_head = a.dv;
-    const size_t bk = a.Hk, H = a.H;
+    a.pst = cap;
+    a.pnkb = div_ceil(cap, block);
+    a.kb0 = 0;
+    const size_t bk = a.Hk, H = a.H, cb = a.pnkb;
     size_t off = 0;
     auto take = [&](size_t n) {
         size_t o = off;
         off += round_up(n ? n : 4, 256);
         return o;
     };
-    P.o_kmean = take(bk * a.nkb * a.d * 4);
-    P.o_kdelta = take(bk * a.S * 4);
-    P.o_khat = take(bk * a.S * a.d4 * 4);
-    P.o_vd = take(bk * a.nkb * a.dv * 4);
-    P.o_vhat = take(bk * a.nkb * a.dv * a.blk4 * 4);
-    P.o_sc = take(H * a.S * 4);
-    P.o_bmax = take(H * a.nkb * 4);
-    P.o_bm = take(H * a.nkb * 4);
-    P.o_balpha = take(H * a.nkb * 4);
-    P.o_besum = take(H * a.nkb * 4);
-    P.o_blive = take(H * a.nkb * 4);
-    P.o_pvt = take(H * a.nkb * a.dv * 4);
+    P.o_kmean = take(bk * cb * a.d * 4);
+    P.o_kdelta = take(bk * cap * 4);
+    P.o_khat = take(bk * cap * a.d4 * 4);
+    P.o_vd = take(bk * cb * a.dv * 4);
+    P.o_vhat = take(bk * cb * a.dv * a.blk4 * 4);
+    P.o_sc = take(H * cap * 4);
+    P.o_bmax = take(H * cb * 4);
+    P.o_balpha = take(H * cb * 4);
+    P.o_besum = take(H * cb * 4);
+    P.o_blive = take(H * cb * 4);
+    P.o_pvt = take(H * cb * a.dv * 4);
+    P.o_qsw = take(H * a.d4 * 4);
+    P.o_qdl = take(H * 4);
     P.ws = off;
     return P;
 }
@@ -883,9 +1496,13 @@ static int validate_decode(const qbk_attn_shape *s, size_t block_size, const siz
     return QBK_OK;
 }
 
+// One step over seq_kv cached tokens with a workspace laid out for cap; the
+// products of the key blocks that were complete at cached tokens are taken
+// as they are (the caller guarantees that those cache rows are the ones the
+// workspace's earlier step quantised) and the rest are quantised again.
 static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, const float *v,
-                      size_t block, float *out, void *ws, hipStream_t st) {
-    DecPlan P = dec_plan(s, block);
+                      size_t block, float *out, void *ws, size_t cap, size_t cached, hipStream_t st) {
+    DecPlan P = dec_plan(s, block, cap);
     DecArgs da = P.da;
     RefArgs &a = da.r;
     a.q = q;
@@ -900,18 +1517,38 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     a.vhat = (uint32_t *)(w + P.o_vhat);
     da.sc = (float *)(w + P.o_sc);
     da.bmax = (float *)(w + P.o_bmax);
-    da.bm = (float *)(w + P.o_bm);
     da.balpha = (float *)(w + P.o_balpha);
     da.besum = (float *)(w + P.o_besum);
     da.blive = (int *)(w + P.o_blive);
     da.pvt = (float *)(w + P.o_pvt);
+    da.qsw = (uint32_t *)(w + P.o_qsw);
+    da.qdl = (float *)(w + P.o_qdl);
     const unsigned nkb = (unsigned)a.nkb, H = (unsigned)a.H;
-    hipLaunchKernelGGL(sage_ref_prep, dim3(nkb, (unsigned)a.Hk), dim3(256), ref_prep_lds(a.d, a.dv, a.block),
-                       st, a);
-    QBK_HIP(hipGetLastError());
+    a.kb0 = cached / block;
+    const DPrepGeom g = dprep_geom(a, k, v);
+    const size_t G = a.H / a.Hk, kjm = a.block < a.S ? a.block : a.S;
+    const bool grouped = g.ok && G <= DEC_GMAX && kjm <= DEC_KMAX && a.d % 16 == 0 && a.blk4 % 4 == 0 &&
+                         a.nkb <= DEC_PMAX;
+    if (g.ok && (a.kb0 < a.nkb || grouped)) {
+        const unsigned nx = (unsigned)(a.kb0 < a.nkb ? a.nkb - a.kb0 : 1);
+        hipLaunchKernelGGL(sage_dec_prep, dim3(nx, (unsigned)a.Hk, DPREP_KS + DPREP_VS + (grouped ? 1 : 0)),
+                           dim3(256), g.lds, st, a, g, grouped ? da.qsw : nullptr, grouped ? da.qdl : nullptr);
+        QBK_HIP(hipGetLastError());
+    } else if (a.kb0 < a.nkb) {
+        hipLaunchKernelGGL(sage_ref_prep, dim3((unsigned)(a.nkb - a.kb0), (unsigned)a.Hk), dim3(256),
+                           ref_prep_lds(a.d, a.dv, a.block), st, a);
+        QBK_HIP(hipGetLastError());
+    }
+    if (grouped) {
+        hipLaunchKernelGGL(sage_dec_scores_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da);
+        QBK_HIP(hipGetLastError());
+        hipLaunchKernelGGL(sage_dec_pv_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da);
+        QBK_HIP(hipGetLastError());
+        hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da);
+        QBK_HIP(hipGetLastError());
+        return QBK_OK;
+    }
     hipLaunchKernelGGL(sage_dec_scores, dim3(nkb, H), dim3(256), 0, st, da);
-    QBK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(sage_dec_stats, dim3(H), dim3(64), 0, st, da);
     QBK_HIP(hipGetLastError());
     hipLaunchKernelGGL(sage_dec_pv, dim3(nkb, H), dim3(256), 0, st, da);
     QBK_HIP(hipGetLastError());
@@ -930,11 +1567,9 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
 #define LOG2E_F 1.44269504088896341f
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct BlkArgs {
     const uint16_t *q, *k, *v;  // bf16
@@ -1563,7 +2198,7 @@ int qbk_attention_sage_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const floa
 
 size_t qbk_sage_decode_workspace_size(const qbk_attn_shape *shape, size_t block_size) {
     if (!shape || block_size == 0 || shape->n_kv_heads == 0) return 0;
-    return dec_plan(shape, block_size).ws;
+    return dec_plan(shape, block_size, shape->seq_kv).ws;
 }
 
 int qbk_attention_sage_decode(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, size_t q_len,
@@ -1578,13 +2213,13 @@ int qbk_attention_sage_decode(qbk_ctx *ctx, const qbk_attn_shape *shape, const f
     if ((rc = cs.create())) return rc;
     DevBuf dq, dk, dvb, dout, dws;
     if ((rc = dq.alloc(q_len * 4)) || (rc = dk.alloc(k_len * 4)) || (rc = dvb.alloc(v_len * 4)) ||
-        (rc = dout.alloc(out_len * 4)) || (rc = dws.alloc(dec_plan(shape, block_size).ws)))
+        (rc = dout.alloc(out_len * 4)) || (rc = dws.alloc(dec_plan(shape, block_size, shape->seq_kv).ws)))
         return rc;
     QBK_HIP(hipMemcpyAsync(dq.p, q, q_len * 4, hipMemcpyHostToDevice, cs.s));
     QBK_HIP(hipMemcpyAsync(dk.p, k, k_len * 4, hipMemcpyHostToDevice, cs.s));
     QBK_HIP(hipMemcpyAsync(dvb.p, v, v_len * 4, hipMemcpyHostToDevice, cs.s));
     if ((rc = run_decode(shape, (const float *)dq.p, (const float *)dk.p, (const float *)dvb.p, block_size,
-                         (float *)dout.p, dws.p, cs.s)))
+                         (float *)dout.p, dws.p, shape->seq_kv, 0, cs.s)))
         return rc;
     QBK_HIP(hipMemcpyAsync(out, dout.p, out_len * 4, hipMemcpyDeviceToHost, cs.s));
     QBK_HIP(hipStreamSynchronize(cs.s));
@@ -1597,11 +2232,35 @@ int qbk_attention_sage_decode_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, con
     int rc;
     if ((rc = validate_decode(shape, block_size, nullptr))) return rc;
     if ((rc = bind(ctx))) return rc;
-    const size_t need = dec_plan(shape, block_size).ws;
+    const size_t need = dec_plan(shape, block_size, shape->seq_kv).ws;
     if (workspace_size < need)
         return fail(QBK_ERR_VALIDATION,
                     fmt("workspace of %zu bytes is smaller than the %zu this call needs", workspace_size, need));
-    return run_decode(shape, q, k, v, block_size, out, workspace, (hipStream_t)stream);
+    return run_decode(shape, q, k, v, block_size, out, workspace, shape->seq_kv, 0, (hipStream_t)stream);
+}
+
+int qbk_attention_sage_decode_step_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q,
+                                       const float *k, const float *v, size_t block_size, float *out,
+                                       void *state, size_t state_size, size_t capacity, size_t cached_tokens,
+                                       void *stream) {
+    int rc;
+    if ((rc = validate_decode(shape, block_size, nullptr))) return rc;
+    if (shape->seq_kv > capacity)
+        return fail(QBK_ERR_VALIDATION, fmt("the cache holds %zu tokens, beyond the state's capacity of %zu",
+                                            shape->seq_kv, capacity));
+    if (cached_tokens > shape->seq_kv)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("cached_tokens (%zu) exceeds the %zu tokens of the cache; a shorter cache "
+                        "starts again from cached_tokens = 0",
+                        cached_tokens, shape->seq_kv));
+    const size_t need = dec_plan(shape, block_size, capacity).ws;
+    if (state_size < need)
+        return fail(QBK_ERR_VALIDATION, fmt("decode state of %zu bytes is smaller than the %zu a capacity of "
+                                            "%zu tokens needs",
+                                            state_size, need, capacity));
+    if (!q || !k || !v || !out || !state) return fail(QBK_ERR_VALIDATION, "null buffer");
+    if ((rc = bind(ctx))) return rc;
+    return run_decode(shape, q, k, v, block_size, out, state, capacity, cached_tokens, (hipStream_t)stream);
 }
 
 size_t qbk_sage_blk_workspace_size(const qbk_attn_shape *shape) {

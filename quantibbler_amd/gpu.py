@@ -177,6 +177,15 @@ class GpuContext:
                                                         _ptr(workspace), int(workspace_size),
                                                         _stream(stream)))
 
+    def attention_sage_decode_step_dev(self, shape: AttentionShape, q, key_cache, value_cache,
+                                       block_size: int, out, state, state_size: int, capacity: int,
+                                       cached_tokens: int, stream=None):
+        sh = shape.c()
+        check(_lib.load().qbk_attention_sage_decode_step_dev(
+            self._h, C.byref(sh), _ptr(q), _ptr(key_cache), _ptr(value_cache), int(block_size),
+            _ptr(out), _ptr(state), int(state_size), int(capacity), int(cached_tokens),
+            _stream(stream)))
+
     def sage_blk_workspace_size(self, shape: AttentionShape) -> int:
         sh = shape.c()
         return int(_lib.load().qbk_sage_blk_workspace_size(C.byref(sh)))
@@ -196,6 +205,49 @@ class GpuContext:
                                                     _ptr(v), _ptr(qhat), _ptr(qscale),
                                                     _ptr(khat), _ptr(kscale), _ptr(kmean),
                                                     _ptr(vh), _stream(stream)))
+
+
+class SageDecodeState:
+    """A decode loop's attention state for one layer (engine/mod.rs:984-1030
+    gqa_attention_sage, called once per generated token over a growing
+    KvCache): a device buffer, supplied by the caller, laid out for a cache
+    of ``capacity`` tokens, and the number of cache rows whose codes it holds.
+    Each step re-quantises only the key blocks from the last complete one on;
+    the output is bit-identical to a fresh call.  ``reset()`` after the
+    cache's earlier rows change (a new sequence)."""
+
+    def __init__(self, ctx: GpuContext, n_heads: int, n_kv_heads: int, head_dim: int,
+                 val_dim: int, capacity: int, block_size: int, state):
+        self.ctx = ctx
+        self.n_heads, self.n_kv_heads = int(n_heads), int(n_kv_heads)
+        self.head_dim, self.val_dim = int(head_dim), int(val_dim)
+        self.capacity, self.block_size = int(capacity), int(block_size)
+        self.state = state
+        self.state_size = self.size(ctx, n_heads, n_kv_heads, head_dim, val_dim, capacity,
+                                    block_size)
+        self.tokens = 0
+
+    @staticmethod
+    def size(ctx: GpuContext, n_heads, n_kv_heads, head_dim, val_dim, capacity, block_size) -> int:
+        """Bytes of device memory a state for ``capacity`` tokens needs."""
+        shape = AttentionShape(1, n_heads, n_kv_heads, 1, capacity, head_dim, val_dim)
+        return ctx.sage_decode_workspace_size(shape, block_size)
+
+    def reset(self):
+        self.tokens = 0
+
+    def step(self, q, key_cache, value_cache, seq_kv: int, out, stream=None):
+        """Attention of the step's query ``q`` (n_heads, head_dim) over the
+        first ``seq_kv`` rows of the row-major caches into ``out``
+        (n_heads, val_dim); a cache shorter than the last step's starts over."""
+        seq_kv = int(seq_kv)
+        cached = self.tokens if self.tokens <= seq_kv else 0
+        shape = AttentionShape(1, self.n_heads, self.n_kv_heads, 1, seq_kv, self.head_dim,
+                               self.val_dim)
+        self.ctx.attention_sage_decode_step_dev(shape, q, key_cache, value_cache,
+                                                self.block_size, out, self.state,
+                                                self.state_size, self.capacity, cached, stream)
+        self.tokens = seq_kv
 
 
 class LmHead:

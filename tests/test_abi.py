@@ -123,6 +123,33 @@ def test_decode_validation_precedes_device_use(lib):
     assert lib.qbk_sage_decode_workspace_size(C.byref(AttnShape(1, 2, 1, 1, 8, 4, 4)), 4) > 0
 
 
+def test_decode_state_validation_precedes_device_use(lib):
+    # the kept-state step checks its capacity, cached count and state size
+    # before any device is touched
+    from quantibbler_amd import KernelError
+    from quantibbler_amd._lib import AttnShape, check
+
+    sh = AttnShape(1, 2, 1, 1, 8, 4, 4)
+    need = lib.qbk_sage_decode_workspace_size(C.byref(AttnShape(1, 2, 1, 1, 4096, 4, 4)), 4)
+    assert need > lib.qbk_sage_decode_workspace_size(C.byref(sh), 4)
+
+    def call(cap, cached, size=need, shape=sh):
+        return check(lib.qbk_attention_sage_decode_step_dev(None, C.byref(shape), None, None, None, 4, None,
+                                                            None, size, cap, cached, None))
+
+    with pytest.raises(KernelError, match="the cache holds 8 tokens, beyond the state's capacity of 7"):
+        call(7, 0)
+    with pytest.raises(KernelError, match=r"cached_tokens \(9\) exceeds the 8 tokens of the cache"):
+        call(4096, 9)
+    with pytest.raises(KernelError, match=f"decode state of {need - 1} bytes is smaller than the {need} "
+                       "a capacity of 4096 tokens needs"):
+        call(4096, 8, need - 1)
+    with pytest.raises(KernelError, match="sage decode takes the step's one query"):
+        call(4096, 0, shape=AttnShape(1, 2, 1, 2, 8, 4, 4))
+    with pytest.raises(KernelError, match="null buffer"):
+        call(4096, 8)
+
+
 def test_init_fails_closed_without_device(lib):
     try:
         import torch

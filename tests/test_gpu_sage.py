@@ -72,6 +72,8 @@ def padded_decode_call(ctx, qh, kc, vc, block):
 @pytest.mark.parametrize("h,hk,d,dv,seq,block", [
     (4, 2, 16, 16, 1, 1), (4, 2, 16, 16, 37, 8), (8, 2, 64, 64, 200, 64), (4, 1, 128, 128, 130, 64),
     (2, 1, 32, 48, 150, 100), (8, 8, 128, 128, 333, 64), (4, 2, 64, 64, 90, 256),
+    (2, 1, 6, 10, 45, 16),   # channels not a multiple of 4: the general pre-pass
+    (32, 2, 128, 128, 129, 64),   # 16 heads a kv head
 ])
 def test_decode_step_matches_padded_reference_call(ctx, orc, h, hk, d, dv, seq, block):
     """One decode step over a row-major KV cache: bit-identical to row 0 of the
@@ -100,6 +102,57 @@ def test_decode_step_matches_padded_reference_call(ctx, orc, h, hk, d, dv, seq, 
         same(od.cpu().numpy(), got)
 
 
+@pytest.mark.parametrize("h,hk,d,dv,block,steps", [
+    (4, 2, 64, 64, 16, [1, 2, 15, 16, 17, 18, 31, 32, 33, 60, 61, 64, 65, 100]),
+    (8, 2, 128, 128, 64, [1, 63, 64, 65, 66, 127, 128, 129, 200, 255, 256, 257]),
+    (2, 1, 32, 48, 100, [5, 99, 100, 101, 150, 230]),   # blocks wider than one LDS chunk
+])
+def test_decode_state_steps_match_fresh_calls(ctx, orc, h, hk, d, dv, block, steps):
+    """A decode loop over a growing cache on one kept state (only the blocks
+    from the last complete one on quantised again): every step bit-identical
+    to a fresh call; a reset state on a different cache starts over."""
+    from quantibbler_amd import AttentionShape, SageDecodeState
+
+    say("sage decode state", h, hk, d, dv, block, steps[-1])
+    cap = steps[-1] + 7
+    rng = np.random.default_rng(11 * block + h)
+    kc = (rng.standard_normal((cap, hk, d)) + 2.0 * rng.standard_normal((1, hk, d))).astype(np.float32)
+    vc = rng.standard_normal((cap, hk, dv)).astype(np.float32)
+    kd, vd = torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda()
+    size = SageDecodeState.size(ctx, h, hk, d, dv, cap, block)
+    st = SageDecodeState(ctx, h, hk, d, dv, cap, block, torch.empty(size, dtype=torch.uint8, device="cuda"))
+    od = torch.empty((h, dv), dtype=torch.float32, device="cuda")
+    for i, seq in enumerate(steps):
+        qh = rng.standard_normal((h, d)).astype(np.float32)
+        st.step(torch.from_numpy(qh).cuda(), kd, vd, seq, od, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        sh = AttentionShape(1, h, hk, 1, seq, d, dv)
+        want = ctx.attention_sage_decode(sh, qh, kc[:seq], vc[:seq], block)
+        same(od.cpu().numpy(), want)
+        if i % 5 == 4:
+            q = np.zeros((1, h, seq, d), np.float32)
+            q[0, :, 0, :] = qh
+            k = np.ascontiguousarray(kc[:seq].transpose(1, 0, 2))[None]
+            v = np.ascontiguousarray(vc[:seq].transpose(1, 0, 2))[None]
+            same(od.cpu().numpy(), orc.attention_sage_dev(q, k, v, False, block)[0, :, 0, :])
+    # a new sequence in the same cache buffers: the kept codes are stale
+    kc2 = rng.standard_normal((cap, hk, d)).astype(np.float32)
+    kd.copy_(torch.from_numpy(kc2))
+    st.reset()
+    qh = rng.standard_normal((h, d)).astype(np.float32)
+    seq = steps[len(steps) // 2]
+    st.step(torch.from_numpy(qh).cuda(), kd, vd, seq, od, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    same(od.cpu().numpy(), ctx.attention_sage_decode(AttentionShape(1, h, hk, 1, seq, d, dv), qh, kc2[:seq],
+                                                      vc[:seq], block))
+    # a shorter cache than the last step's starts over by itself
+    seq2 = max(1, seq - block - 1)
+    st.step(torch.from_numpy(qh).cuda(), kd, vd, seq2, od, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    same(od.cpu().numpy(), ctx.attention_sage_decode(AttentionShape(1, h, hk, 1, seq2, d, dv), qh,
+                                                      kc2[:seq2], vc[:seq2], block))
+
+
 @pytest.mark.parametrize("b,h,hk,s,d,dv,causal,block", [
     (1, 4, 2, 200, 64, 64, True, 64),
     (2, 2, 1, 130, 128, 128, True, 64),
@@ -107,8 +160,6 @@ def test_decode_step_matches_padded_reference_call(ctx, orc, h, hk, d, dv, seq, 
     (1, 2, 1, 150, 16, 16, True, 100),   # blocks wider than one LDS chunk
     (1, 1, 1, 70, 8, 8, False, 70),
 ])
-
-
 def test_reference_scheme_random_bit_identical(ctx, orc, b, h, hk, s, d, dv, causal, block):
     say("sage ref random", b, h, hk, s, d, dv, causal, block)
     rng = np.random.default_rng(s + d + block)
