@@ -84,6 +84,7 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 // ======================================================================
 // 1. reference scheme
@@ -1569,7 +1570,6 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 struct BlkArgs {
     const uint16_t *q, *k, *v;  // bf16
