@@ -300,6 +300,19 @@ int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *L, const uint16_t *x, 
     return g32_run(L, x, false, batch, y, y_dtype == QBK_BF16, workspace, s);
 }
 
+// The f64 serving path's two elementwise ends (engine/mod.rs:419-436):
+// z = f64(s2 * x), an f32 product widened; y = f32(u) * s1 + b, a multiply
+// then an add (the file is built without contraction).
+__global__ void factor_f64_in(const float *x, const float *s2, double *z, size_t n) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i < n) z[i] = (double)(s2[i] * x[i]);
+}
+
+__global__ void factor_f64_out(const double *u, const float *s1, const float *bias, float *y, size_t n) {
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i < n) y[i] = ((float)u[i]) * s1[i] + bias[i];
+}
+
 // engine/mod.rs:393-460 apply / apply_bf16 with host buffers.
 int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *L, int serving, const float *x, size_t batch,
                      float *y) {
@@ -312,29 +325,29 @@ int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *L, int serving, const float
     CallStream cs;
     if ((rc = cs.create())) return rc;
     if (serving == QBK_F32) {
-        // z = f64(s2*x) on the host (f32 multiply, widen), then the two f64
-        // matvecs in element order on the device, y = f32(u)*s1 + b.
-        std::vector<float> s1(L->dout), s2(L->din), bias(L->dout);
-        QBK_HIP(hipMemcpy(s1.data(), L->s1, L->dout * 4, hipMemcpyDeviceToHost));
-        QBK_HIP(hipMemcpy(s2.data(), L->s2, L->din * 4, hipMemcpyDeviceToHost));
-        QBK_HIP(hipMemcpy(bias.data(), L->bias, L->dout * 4, hipMemcpyDeviceToHost));
-        DevBuf dz, dt, du;
-        if ((rc = dz.alloc(L->din * 8)) || (rc = dt.alloc(L->r * 8)) || (rc = du.alloc(L->dout * 8)))
+        // per token: z = f64(s2*x), the two f64 matvecs in element order,
+        // y = f32(u)*s1 + b -- all on the device
+        DevBuf dx, dy, dz, dt, du;
+        if ((rc = dx.alloc(batch * L->din * 4)) || (rc = dy.alloc(batch * L->dout * 4)) ||
+            (rc = dz.alloc(L->din * 8)) || (rc = dt.alloc(L->r * 8)) || (rc = du.alloc(L->dout * 8)))
             return rc;
-        std::vector<double> z(L->din), u(L->dout);
+        QBK_HIP(hipMemcpyAsync(dx.p, x, batch * L->din * 4, hipMemcpyHostToDevice, cs.s));
+        const unsigned gi = (unsigned)((L->din + 255) / 256), go = (unsigned)((L->dout + 255) / 256);
         for (size_t bb = 0; bb < batch; bb++) {
-            const float *xb = x + bb * L->din;
-            for (size_t j = 0; j < L->din; j++) z[j] = (double)(s2[j] * xb[j]);
-            QBK_HIP(hipMemcpyAsync(dz.p, z.data(), L->din * 8, hipMemcpyHostToDevice, cs.s));
+            hipLaunchKernelGGL(factor_f64_in, dim3(gi), dim3(256), 0, cs.s, (const float *)dx.p + bb * L->din,
+                               (const float *)L->s2, (double *)dz.p, L->din);
+            QBK_HIP(hipGetLastError());
             if ((rc = qbk_packed_matvec_dev(ctx, QBK_F64, L->vbt_rows, L->r, L->din, dz.p, dt.p, cs.s)))
                 return rc;
             if ((rc = qbk_packed_matvec_dev(ctx, QBK_F64, L->ub_rows, L->dout, L->r, dt.p, du.p, cs.s)))
                 return rc;
-            QBK_HIP(hipMemcpyAsync(u.data(), du.p, L->dout * 8, hipMemcpyDeviceToHost, cs.s));
-            QBK_HIP(hipStreamSynchronize(cs.s));
-            float *yb = y + bb * L->dout;
-            for (size_t i = 0; i < L->dout; i++) yb[i] = ((float)u[i]) * s1[i] + bias[i];
+            hipLaunchKernelGGL(factor_f64_out, dim3(go), dim3(256), 0, cs.s, (const double *)du.p,
+                               (const float *)L->s1, (const float *)L->bias, (float *)dy.p + bb * L->dout,
+                               L->dout);
+            QBK_HIP(hipGetLastError());
         }
+        QBK_HIP(hipMemcpyAsync(y, dy.p, batch * L->dout * 4, hipMemcpyDeviceToHost, cs.s));
+        QBK_HIP(hipStreamSynchronize(cs.s));
         return QBK_OK;
     }
     DevBuf dx, dy, dws;

@@ -383,6 +383,10 @@ def test_apply_host_faces(ctx, orc):
     got = layer.apply(x, "float32")
     want = orc.factor_apply("fp32", 96, 160, 40, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
     same(got, want)
+    xs = rng.standard_normal((3, 160)).astype(np.float32)
+    got3 = layer.apply(xs, "float32")
+    for i in range(3):
+        same(got3[i], orc.factor_apply("fp32", 96, 160, 40, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], xs[i]))
     # bf16 serving with an f32 x: z = bf16(s2*x) as apply_bf16 does
     got_b = layer.apply(x, "bfloat16")
     want_b = orc.factor_apply("bf16", 96, 160, 40, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], x)
