@@ -648,6 +648,7 @@ struct DecArgs {
     float *pvt;                          // [H][nkb][dv]
     uint32_t *qsw;                       // [H][d4] the query's codes (grouped kernels)
     float *qdl;                          // [H] and its delta
+    float *mprev;                        // [H][nkb] running max before each block, or null
 };
 
 // max over the workgroup (blockDim.x a multiple of 64, <= 1024)
@@ -1036,6 +1037,52 @@ __global__ void __launch_bounds__(256) sage_dec_scores(DecArgs da) {
     if (tid == 0) da.bmax[h * a.nkb + kb] = rm;
 }
 
+// :288-296's running max before each block, for caches of more than
+// DEC_PMAX blocks (where each P.V workgroup reducing the earlier maxima
+// itself would read O(nkb^2) values): mprev[kb] = max(MASKED, bmax[0..kb-1]),
+// a max, so a parallel scan gives the reference's sequential value.  One
+// workgroup per head, 8 blocks a thread, 2048 blocks a pass.
+__global__ void __launch_bounds__(256) sage_dec_runmax(DecArgs da) {
+    __shared__ float wm[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t h = blockIdx.x, nkb = da.r.nkb;
+    const float *bm = da.bmax + h * nkb;
+    float *mp = da.mprev + h * nkb;
+    float carry = MASKED;
+    for (size_t base = 0; base < nkb; base += 2048) {
+        float v[8], ex[8], run = MASKED;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const size_t i = base + 8 * tid + u;
+            v[u] = i < nkb ? bm[i] : MASKED;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            ex[u] = run;
+            run = v[u] > run ? v[u] : run;
+        }
+        float incl = run;  // inclusive scan over the wave's lanes
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float w = __shfl_up(incl, o, 64);
+            if ((int)lane >= o) incl = w > incl ? w : incl;
+        }
+        __syncthreads();
+        if (lane == 63) wm[wave] = incl;
+        __syncthreads();
+        float before = carry;  // the earlier waves of this pass and the earlier passes
+        for (uint32_t w2 = 0; w2 < wave; w2++) before = wm[w2] > before ? wm[w2] : before;
+        const float up = __shfl_up(incl, 1, 64);
+        const float tex = lane == 0 ? before : (up > before ? up : before);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const size_t i = base + 8 * tid + u;
+            if (i < nkb) mp[i] = ex[u] > tex ? ex[u] : tex;
+        }
+        for (int w2 = 0; w2 < 4; w2++) carry = wm[w2] > carry ? wm[w2] : carry;
+    }
+}
+
 // :288-296 (the running max, live flag and alpha of this block), :297-316
 // (p, esum in key order, codes) and :317-341 (P^.V^ per channel).  The
 // running max before a block is the max of MASKED and the earlier blocks'
@@ -1073,13 +1120,16 @@ __global__ void __launch_bounds__(256) sage_dec_pv(DecArgs da) {
         for (int u = 0; u < 8; u++) vv0[u] = (size_t)u < vn0 ? vc[u] : u32x4_t{0, 0, 0, 0};
     }
     const float vdc = (size_t)tid < a.dv ? a.vd[(bk * a.pnkb + kb) * a.dv + tid] : 0.0f;
+    // the running max before this block: from sage_dec_runmax when the
+    // cache has many blocks, else reduced here over the earlier maxima
     float pm = MASKED;
-    for (size_t i = tid; i < kb; i += blockDim.x) {
-        const float x = da.bmax[h * nkb + i];
-        pm = x > pm ? x : pm;
-    }
+    if (!da.mprev)
+        for (size_t i = tid; i < kb; i += blockDim.x) {
+            const float x = da.bmax[h * nkb + i];
+            pm = x > pm ? x : pm;
+        }
     const float bx = da.bmax[h * nkb + kb];
-    const float m = dec_wg_max(pm, red);
+    const float m = da.mprev ? da.mprev[h * nkb + kb] : dec_wg_max(pm, red);
     const float m_new = bx > m ? bx : m;
     const int live = !(m_new < MASKED * 0.5f);
     float esum = 0.0f;  // thread 0's running sum
@@ -1213,8 +1263,9 @@ __global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da) {
 // group and a step launches G times fewer workgroups; the query's codes
 // come from the pre-pass.  The same f32 operations in the same order as
 // the per-head kernels.  Used when G <= DEC_GMAX, a block has at most
-// DEC_KMAX keys, d and the code rows are whole 16-byte words, and there are
-// at most DEC_PMAX blocks (each workgroup reads the earlier blocks' maxima).
+// DEC_KMAX keys, and d and the code rows are whole 16-byte words.  Up to
+// DEC_PMAX blocks each P.V workgroup reduces the earlier blocks' maxima
+// itself; beyond, sage_dec_runmax scans them first.
 #define DEC_GMAX 16
 #define DEC_KMAX 256
 #define DEC_PMAX 512
@@ -1332,14 +1383,18 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da) {
         const size_t h = (size_t)bk * G + hg;
         const float *bm = da.bmax + h * nkb;
         float pm = MASKED;
-        for (uint32_t i = lane; i < kb; i += 64) {
-            const float x = bm[i];
-            pm = x > pm ? x : pm;
-        }
+        if (da.mprev) {
+            pm = da.mprev[h * nkb + kb];
+        } else {
+            for (uint32_t i = lane; i < kb; i += 64) {
+                const float x = bm[i];
+                pm = x > pm ? x : pm;
+            }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float w = __shfl_xor(pm, o, 64);
-            pm = w > pm ? w : pm;
+            for (int o = 32; o >= 1; o >>= 1) {
+                const float w = __shfl_xor(pm, o, 64);
+                pm = w > pm ? w : pm;
+            }
         }
         const float bx = bm[kb];
         const float m_new = bx > pm ? bx : pm;
@@ -1399,7 +1454,8 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da) {
 struct DecPlan {
     DecArgs da;
     size_t ws;
-    size_t o_kmean, o_kdelta, o_khat, o_vd, o_vhat, o_sc, o_bmax, o_balpha, o_besum, o_blive, o_pvt, o_qsw, o_qdl;
+    size_t o_kmean, o_kdelta, o_khat, o_vd, o_vhat, o_sc, o_bmax, o_balpha, o_besum, o_blive, o_pvt, o_qsw, o_qdl,
+        o_mprev;
 };
 
 // The workspace is laid out for a cache of cap tokens (cap >= seq_kv): the
@@ -1448,6 +1504,7 @@ static DecPlan dec_plan(const qbk_attn_shape *s, size_t block, size_t cap) {
     P.o_pvt = take(H * cb * a.dv * 4);
     P.o_qsw = take(H * a.d4 * 4);
     P.o_qdl = take(H * 4);
+    P.o_mprev = take(H * cb * 4);
     P.ws = off;
     return P;
 }
@@ -1524,12 +1581,12 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     da.pvt = (float *)(w + P.o_pvt);
     da.qsw = (uint32_t *)(w + P.o_qsw);
     da.qdl = (float *)(w + P.o_qdl);
+    da.mprev = nullptr;
     const unsigned nkb = (unsigned)a.nkb, H = (unsigned)a.H;
     a.kb0 = cached / block;
     const DPrepGeom g = dprep_geom(a, k, v);
     const size_t G = a.H / a.Hk, kjm = a.block < a.S ? a.block : a.S;
-    const bool grouped = g.ok && G <= DEC_GMAX && kjm <= DEC_KMAX && a.d % 16 == 0 && a.blk4 % 4 == 0 &&
-                         a.nkb <= DEC_PMAX;
+    const bool grouped = g.ok && G <= DEC_GMAX && kjm <= DEC_KMAX && a.d % 16 == 0 && a.blk4 % 4 == 0;
     if (g.ok && (a.kb0 < a.nkb || grouped)) {
         const unsigned nx = (unsigned)(a.kb0 < a.nkb ? a.nkb - a.kb0 : 1);
         hipLaunchKernelGGL(sage_dec_prep, dim3(nx, (unsigned)a.Hk, DPREP_KS + DPREP_VS + (grouped ? 1 : 0)),
@@ -1543,6 +1600,11 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     if (grouped) {
         hipLaunchKernelGGL(sage_dec_scores_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da);
         QBK_HIP(hipGetLastError());
+        if (a.nkb > DEC_PMAX) {
+            da.mprev = (float *)(w + P.o_mprev);
+            hipLaunchKernelGGL(sage_dec_runmax, dim3(H), dim3(256), 0, st, da);
+            QBK_HIP(hipGetLastError());
+        }
         hipLaunchKernelGGL(sage_dec_pv_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da);
         QBK_HIP(hipGetLastError());
         hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da);
@@ -1551,6 +1613,11 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     }
     hipLaunchKernelGGL(sage_dec_scores, dim3(nkb, H), dim3(256), 0, st, da);
     QBK_HIP(hipGetLastError());
+    if (a.nkb > DEC_PMAX) {
+        da.mprev = (float *)(w + P.o_mprev);
+        hipLaunchKernelGGL(sage_dec_runmax, dim3(H), dim3(256), 0, st, da);
+        QBK_HIP(hipGetLastError());
+    }
     hipLaunchKernelGGL(sage_dec_pv, dim3(nkb, H), dim3(256), 0, st, da);
     QBK_HIP(hipGetLastError());
     hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da);

@@ -74,6 +74,9 @@ def padded_decode_call(ctx, qh, kc, vc, block):
     (2, 1, 32, 48, 150, 100), (8, 8, 128, 128, 333, 64), (4, 2, 64, 64, 90, 256),
     (2, 1, 6, 10, 45, 16),   # channels not a multiple of 4: the general pre-pass
     (32, 2, 128, 128, 129, 64),   # 16 heads a kv head
+    # more than 512 blocks: the running max scanned first (per-head kernels;
+    # two scan passes past 2048 blocks; grouped kernels)
+    (2, 1, 16, 16, 1100, 2), (2, 1, 16, 16, 4200, 2), (4, 2, 64, 64, 8400, 16),
 ])
 def test_decode_step_matches_padded_reference_call(ctx, orc, h, hk, d, dv, seq, block):
     """One decode step over a row-major KV cache: bit-identical to row 0 of the
@@ -89,8 +92,9 @@ def test_decode_step_matches_padded_reference_call(ctx, orc, h, hk, d, dv, seq, 
     got = ctx.attention_sage_decode(sh, qh, kc, vc, block)
     want_dev, (q, k, v) = padded_decode_call(ctx, qh, kc, vc, block)
     same(got, want_dev)
-    want = orc.attention_sage_dev(q, k, v, False, block)[0, :, 0, :]
-    same(got, want)
+    if seq * seq * d * h <= 2e9:  # the oracle's padded call is O(seq^2)
+        want = orc.attention_sage_dev(q, k, v, False, block)[0, :, 0, :]
+        same(got, want)
     # the device-pointer form, twice on one workspace
     wn = ctx.sage_decode_workspace_size(sh, block)
     ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
