@@ -1829,11 +1829,9 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((ch
 //                  row sums from a ninth tile of ones.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) blk_attn(BlkArgs a) {
     // K^ and V^T tiles, double buffered -- four separate objects, so that the
-    // compiler can tell a read of one from the direct loads into another --
-    // and the tile's Q codes
+    // compiler can tell a read of one from the direct loads into another
     __shared__ __attribute__((aligned(16))) uint8_t kl0[BLK * 128], kl1[BLK * 128];
     __shared__ __attribute__((aligned(16))) uint8_t vl0[HD * 128], vl1[HD * 128];
-    __shared__ __attribute__((aligned(16))) uint8_t ql[BQ * 128];
 #define KL(B) ((B) ? kl1 : kl0)
 #define VL(B) ((B) ? vl1 : vl0)
     // the prologue's block-peak exchange; V^T buffer 1 is first loaded after
@@ -1859,10 +1857,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
     const size_t bk = b * a.Hk + h / (a.H / a.Hk);
     const size_t q0 = qi * BQ, qw = q0 + 32 * wave;
 
-    // ---- Q codes (B operand): query qw + 16 qt + col, d = 64 dc + 16 g + e
+    // ---- Q codes (B operand): query qw + 16 qt + col, d = 64 dc + 16 g + e,
+    // kept in registers for every key block
     float qsc;
+    i32x4_t qf[2][2];
     {
-        i32x4_t qf[2][2];
         float x[2][2][16];
         float pk = 0.0f;
 #pragma unroll
@@ -1911,12 +1910,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
             if ((wave & 1) == 0 && lane == 0 && qw < a.S) a.qscale_out[bh * a.nblk + qw / BLK] = qsc;
             return;
         }
-        // the wave's codes to LDS, read back as MFMA operands each block
-#pragma unroll
-        for (int qt = 0; qt < 2; qt++)
-#pragma unroll
-            for (int dc = 0; dc < 2; dc++)
-                *(i32x4_t *)&ql[swz(32 * wave + 16 * qt + col, 4 * dc + g)] = qf[qt][dc];
     }
 
     // ---- key blocks
@@ -1969,12 +1962,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
             __builtin_amdgcn_global_load_lds((const void *)(vb_ + (loff + u * 4096u)),           \
                                              (__attribute__((address_space(3))) void *)&VL(BUF)[(wave + 4 * u) * 1024], 16, 0, 0);\
     }
-    // the Q and K^ fragments of the block whose K^ tile is in buffer BUF
+    // the K^ fragments of the block whose K^ tile is in buffer BUF
 #define BLK_FRAGS(BUF)                                                                          \
     {                                                                                           \
-        _Pragma("unroll") for (int qt = 0; qt < 2; qt++)                                        \
-        _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                        \
-            qf[qt][dc] = *(const i32x4_t *)&ql[swz(32 * wave + 16 * qt + col, 4 * dc + g)];     \
         _Pragma("unroll") for (int kt = 0; kt < 4; kt++)                                        \
         _Pragma("unroll") for (int dc = 0; dc < 2; dc++)                                        \
             kf[kt][dc] = *(const i32x4_t *)&KL(BUF)[swz(16 * kt + col, 4 * dc + g)];            \
@@ -2085,7 +2075,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the next tiles have landed */        \
         __syncthreads();                                                                        \
     }
-    i32x4_t qf[2][2], kf[4][2];
+    i32x4_t kf[4][2];
     BLK_LOAD_K(0, 0)
     BLK_LOAD_K(kb_end > 1 ? 1 : 0, 1)
     BLK_LOAD_V(0, 0)
