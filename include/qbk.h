@@ -204,8 +204,9 @@ int qbk_attention_sage_decode_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, con
  * of the key blocks complete within those rows are kept and only the later
  * blocks -- at most one block plus the new tokens -- are quantised again,
  * which takes the per-step cost of the pre-pass off the cache length.
- * seq_kv <= capacity, cached_tokens <= seq_kv.  Calls that share a state
- * must be ordered (one stream). */
+ * seq_kv <= capacity, cached_tokens <= seq_kv; the shape's heads and dims,
+ * block_size and capacity stay those of the state's first call.  Calls that
+ * share a state must be ordered (one stream). */
 int qbk_attention_sage_decode_step_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q,
                                        const float *k, const float *v, size_t block_size, float *out,
                                        void *state, size_t state_size, size_t capacity, size_t cached_tokens,

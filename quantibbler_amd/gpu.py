@@ -36,6 +36,16 @@ def _ptr(x):
     raise TypeError(f"cannot take a pointer of {type(x)!r}")
 
 
+def _nbytes(x):
+    """Bytes behind a buffer given as a tensor or an array (None for a raw
+    address, whose size the caller vouches for)."""
+    if hasattr(x, "element_size") and hasattr(x, "numel"):
+        return int(x.element_size() * x.numel())
+    if isinstance(x, np.ndarray):
+        return int(x.nbytes)
+    return None
+
+
 def _stream(s):
     if s is None:
         return None
@@ -223,8 +233,12 @@ class SageDecodeState:
         self.head_dim, self.val_dim = int(head_dim), int(val_dim)
         self.capacity, self.block_size = int(capacity), int(block_size)
         self.state = state
-        self.state_size = self.size(ctx, n_heads, n_kv_heads, head_dim, val_dim, capacity,
-                                    block_size)
+        need = self.size(ctx, n_heads, n_kv_heads, head_dim, val_dim, capacity, block_size)
+        have = _nbytes(state)
+        if have is not None and have < need:
+            raise _lib.KernelError(f"decode state of {have} bytes is smaller than the {need} a "
+                                   f"capacity of {capacity} tokens needs")
+        self.state_size = have if have is not None else need
         self.tokens = 0
 
     @staticmethod

@@ -115,7 +115,7 @@ def test_decode_state_steps_match_fresh_calls(ctx, orc, h, hk, d, dv, block, ste
     """A decode loop over a growing cache on one kept state (only the blocks
     from the last complete one on quantised again): every step bit-identical
     to a fresh call; a reset state on a different cache starts over."""
-    from quantibbler_amd import AttentionShape, SageDecodeState
+    from quantibbler_amd import AttentionShape, KernelError, SageDecodeState
 
     say("sage decode state", h, hk, d, dv, block, steps[-1])
     cap = steps[-1] + 7
@@ -124,6 +124,8 @@ def test_decode_state_steps_match_fresh_calls(ctx, orc, h, hk, d, dv, block, ste
     vc = rng.standard_normal((cap, hk, dv)).astype(np.float32)
     kd, vd = torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda()
     size = SageDecodeState.size(ctx, h, hk, d, dv, cap, block)
+    with pytest.raises(KernelError, match="decode state of .* bytes is smaller than the"):
+        SageDecodeState(ctx, h, hk, d, dv, cap, block, torch.empty(size - 1, dtype=torch.uint8, device="cuda"))
     st = SageDecodeState(ctx, h, hk, d, dv, cap, block, torch.empty(size, dtype=torch.uint8, device="cuda"))
     od = torch.empty((h, dv), dtype=torch.float32, device="cuda")
     for i, seq in enumerate(steps):
