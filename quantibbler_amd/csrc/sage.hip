@@ -1690,11 +1690,9 @@ __global__ void __launch_bounds__(64) blk_kpart(BlkArgs a) {
     *(float2 *)&a.kpart[(bk * a.nblk + blk) * HD + c] = make_float2(p0, p1);
 }
 
-// K channel means: the chunk partials summed in chunk order, / S.  One
-// workgroup per kv head, one thread per channel.
-__global__ void __launch_bounds__(HD) blk_kmean(BlkArgs a) {
-    const size_t bk = blockIdx.x;
-    const int c = threadIdx.x;
+// K channel mean of channel c of kv head bk: the chunk partials summed in
+// chunk order, / S.
+__device__ __forceinline__ float blk_mean_of(const BlkArgs &a, size_t bk, int c) {
     const float *part = a.kpart + bk * a.nblk * HD + c;
     float tot = 0.0f;
     size_t p = 0;
@@ -1706,7 +1704,7 @@ __global__ void __launch_bounds__(HD) blk_kmean(BlkArgs a) {
         for (int u = 0; u < 16; u++) tot += v[u];
     }
     for (; p < a.nblk; p++) tot += part[p * HD];
-    a.kmean[bk * HD + c] = tot / (float)a.S;
+    return tot / (float)a.S;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -1717,14 +1715,21 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // K: smoothing by the channel mean, block scale, codes; V: bf16 -> fp16,
 // transposed per key block into PV order.  One workgroup per (block, kv
-// head); thread t holds token t/4, channels 32 (t%4) .. +31.
+// head); thread t holds token t/4, channels 32 (t%4) .. +31.  Each
+// workgroup forms the channel means itself from the chunk partials (the
+// first of a kv head also stores them): a separate launch cost more than
+// the redundant sums, which stay in L2.
 __global__ void __launch_bounds__(256) blk_kvquant(BlkArgs a) {
     __shared__ float mean[HD];
     __shared__ float red[4];
     __shared__ uint16_t vs[BLK][HD + 2];  // fp16 V, token-major
     const size_t blk = blockIdx.x, bk = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < HD) mean[tid] = a.kmean[bk * HD + tid];
+    if (tid < HD) {
+        const float m = blk_mean_of(a, bk, tid);
+        mean[tid] = m;
+        if (blk == 0) a.kmean[bk * HD + tid] = m;
+    }
     __syncthreads();
     const size_t t0 = blk * BLK;
     const int tt = tid >> 2, c0 = 32 * (tid & 3);
@@ -2190,8 +2195,6 @@ static void blk_bind(BlkPlan &P, const uint16_t *q, const uint16_t *k, const uin
 static int run_blk_prepass(BlkPlan &P, hipStream_t st) {
     const BlkArgs &a = P.a;
     hipLaunchKernelGGL(blk_kpart, dim3((unsigned)a.nblk, (unsigned)(a.B * a.Hk)), dim3(64), 0, st, a);
-    QBK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(blk_kmean, dim3((unsigned)(a.B * a.Hk)), dim3(HD), 0, st, a);
     QBK_HIP(hipGetLastError());
     hipLaunchKernelGGL(blk_kvquant, dim3((unsigned)a.nblk, (unsigned)(a.B * a.Hk)), dim3(256), 0, st, a);
     QBK_HIP(hipGetLastError());
