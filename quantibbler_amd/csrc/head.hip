@@ -7,13 +7,15 @@
 // the logits are bit-identical to the reference's; the parallelism is the
 // rows (128256 for a Llama-3 vocabulary).
 //
-// Layout: the head is stored transposed per wave, [vocab_p / RW][d_model][RW]
-// with RW the rows one wave covers (vocab_p = vocab rounded up to the rows
-// of a workgroup, zero-padded): at step t a wave reads one contiguous run of
-// its rows' elements, and its steps follow each other in memory, so every
-// wave streams one contiguous region (one DRAM page after another; the
-// plain [d_model][vocab] transpose made each step 256 KB from the last and
-// read at 4.6 TB/s).  When every
+// Layout: the head is stored transposed per wave and grouped four steps a
+// lane, [vocab_p / RW][d_p / 4][64 lanes][4 steps] dwords, with RW the rows
+// one wave covers (vocab_p = vocab rounded up to the rows of a workgroup,
+// d_p = d_model rounded up to 4, both zero-padded): a lane's four steps are
+// one 16-byte load, a wave's four steps one contiguous KiB, and a wave's
+// steps follow each other in memory, so every wave streams one contiguous
+// region (the plain [d_model][vocab] transpose made each step 256 KB from
+// the last and read at 4.6 TB/s; one dword a lane a step, 5.4 TB/s: a wave
+// can have at most 63 loads in flight, 16 KiB of dwords).  When every
 // element is a bf16 value (the reference's bf16 serving quantises the head
 // so, engine/mod.rs:695-706) it is stored as bf16 -- 1.05 GB instead of 2.1
 // for 128256 x 4096 -- and widened exactly on use; otherwise as f32.
@@ -21,9 +23,8 @@
 // The dot product is HBM-bound (one pass over the head per call; the
 // hidden rows ride in SGPRs through scalar loads).  A lane covers two rows
 // (bf16: one dword holds both) or one (f32), reads a dword per step, and
-// keeps two 64-step chunks of loads in flight (alternating register sets,
-// so no in-flight register is ever copied; 32-step chunks read at 5.3
-// TB/s, 128-step ones at 4.9).
+// keeps two chunks of loads in flight (alternating register sets, so no
+// in-flight register is ever copied).
 #include <string.h>
 
 #include "qbk_internal.h"
@@ -34,7 +35,7 @@ struct qbk_head {
     int device;
     size_t vocab, d_model, vocab_p;
     int bf16;    // elements stored as bf16 (all were bf16 values), else f32
-    void *w;     // [vocab_p / RW][d_model][RW], RW = head_rows_per_wave(bf16)
+    void *w;     // [vocab_p / RW][d_p / 4][64][4] dwords, RW = head_rows_per_wave(bf16)
 };
 
 namespace qbk {
@@ -50,63 +51,75 @@ typedef __attribute__((address_space(4))) const float cf32_t;
 __host__ __device__ static inline size_t head_rows_per_wave(int bf16) { return bf16 ? 128 : 64; }
 static inline size_t head_rows_per_wg(int bf16) { return (HEAD_THREADS / 64) * head_rows_per_wave(bf16); }
 
-// one chunk of HEAD_CHUNK steps from t0 on, words in W: the lane's
+// one chunk of CH steps from t0 on, words in W: the lane's
 // rows += hidden[b][t] * w (bf16: the word's low half is row 2c, high half
 // row 2c + 1)
-template <bool BF16, int NB>
-__device__ __forceinline__ void head_chunk(float acc[NB][2], const uint32_t W[HEAD_CHUNK], const cf32_t *h,
-                                           size_t d, size_t t0) {
+template <bool BF16, int NB, int CH>
+__device__ __forceinline__ void head_chunk(float acc[NB][2], const uint32_t W[CH], const cf32_t *h, size_t d,
+                                           size_t t0) {
+    float w0[CH], w1[CH];
 #pragma unroll
-    for (int u = 0; u < HEAD_CHUNK; u++) {
-        const float w0 = BF16 ? __uint_as_float(W[u] << 16) : __uint_as_float(W[u]);
-        const float w1 = BF16 ? __uint_as_float(W[u] & 0xffff0000u) : 0.0f;
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const float hv = h[(size_t)b * d + t0 + u];
-            acc[b][0] = acc[b][0] + hv * w0;
-            if (BF16) acc[b][1] = acc[b][1] + hv * w1;
-        }
+    for (int u = 0; u < CH; u++) {
+        w0[u] = BF16 ? __uint_as_float(W[u] << 16) : __uint_as_float(W[u]);
+        w1[u] = BF16 ? __uint_as_float(W[u] & 0xffff0000u) : 0.0f;
     }
+    // hidden row by hidden row (each row's steps in order), so that only one
+    // row's values of the chunk are live in SGPRs at a time
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const float hv = h[(size_t)b * d + t0 + u];
+            acc[b][0] = acc[b][0] + hv * w0[u];
+            if (BF16) acc[b][1] = acc[b][1] + hv * w1[u];
+        }
 }
 
-template <bool BF16>
-__device__ __forceinline__ void head_load(uint32_t W[HEAD_CHUNK], const uint32_t *col, size_t stride, size_t t0,
-                                          size_t tlast) {
+typedef uint32_t hu32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const hu32x4_t g128_t;
+
+// steps t0 .. t0 + CH - 1 (t0 a multiple of 4) of the lane's column, four
+// a load; q4last = the last four-step group
+template <int CH>
+__device__ __forceinline__ void head_load(uint32_t W[CH], const uint32_t *col, size_t t0, size_t q4last) {
 #pragma unroll
-    for (int u = 0; u < HEAD_CHUNK; u++) {
-        size_t t = t0 + u;
-        t = t < tlast ? t : tlast;  // past the end: a repeated (unused) step
-        W[u] = __builtin_nontemporal_load((g32_t *)(col + t * stride));
+    for (int u = 0; u < CH / 4; u++) {
+        size_t q = t0 / 4 + u;
+        q = q < q4last ? q : q4last;  // past the end: a repeated (unused) group
+        const hu32x4_t v = __builtin_nontemporal_load((g128_t *)(col + q * 256));
+#pragma unroll
+        for (int e = 0; e < 4; e++) W[4 * u + e] = v[e];
     }
 }
 
 // logits[b][v] for NB hidden rows.  w: the per-wave blocked layout, bf16
 // (dwords of two rows) or f32; lane l of wave block wb reads dword
-// (wb * d + t) * 64 + l at step t.
+// ((wb * d_p / 4 + t / 4) * 64 + l) * 4 + t % 4 at step t.
 template <bool BF16, int NB>
 __global__ void __launch_bounds__(HEAD_THREADS) head_logits_kernel(const uint32_t *w, size_t vocab_p, size_t vocab,
                                                                   size_t d, const float *hidden, float *logits) {
     const size_t wb = (size_t)blockIdx.x * (HEAD_THREADS / 64) + (threadIdx.x >> 6);
     const size_t lane = threadIdx.x & 63;
-    const size_t stride = 64;  // dwords per step
-    const uint32_t *col = w + wb * d * 64 + lane;
+    const size_t dq = (d + 3) / 4;  // four-step groups
+    const uint32_t *col = w + wb * dq * 256 + lane * 4;
     const cf32_t *h = (const cf32_t *)hidden;
     float acc[NB][2];
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[b][0] = acc[b][1] = 0.0f;
-    const size_t dmain = d / (2 * HEAD_CHUNK) * (2 * HEAD_CHUNK);
-    uint32_t A[HEAD_CHUNK], Bw[HEAD_CHUNK];
+    constexpr int CH = HEAD_CHUNK;
+    const size_t dmain = d / (2 * CH) * (2 * CH);
+    uint32_t A[CH], Bw[CH];
     if (dmain) {
-        head_load<BF16>(A, col, stride, 0, d - 1);
-        for (size_t t0 = 0; t0 < dmain; t0 += 2 * HEAD_CHUNK) {
-            head_load<BF16>(Bw, col, stride, t0 + HEAD_CHUNK, d - 1);
-            head_chunk<BF16, NB>(acc, A, h, d, t0);
-            head_load<BF16>(A, col, stride, t0 + 2 * HEAD_CHUNK, d - 1);
-            head_chunk<BF16, NB>(acc, Bw, h, d, t0 + HEAD_CHUNK);
+        head_load<CH>(A, col, 0, dq - 1);
+        for (size_t t0 = 0; t0 < dmain; t0 += 2 * CH) {
+            head_load<CH>(Bw, col, t0 + CH, dq - 1);
+            head_chunk<BF16, NB, CH>(acc, A, h, d, t0);
+            head_load<CH>(A, col, t0 + 2 * CH, dq - 1);
+            head_chunk<BF16, NB, CH>(acc, Bw, h, d, t0 + CH);
         }
     }
-    for (size_t t = dmain; t < d; t++) {  // the last d % 64 steps, in order
-        const uint32_t wv = col[t * stride];
+    for (size_t t = dmain; t < d; t++) {  // the last d % (2 CH) steps, in order
+        const uint32_t wv = col[(t / 4) * 256 + t % 4];
         const float w0 = BF16 ? __uint_as_float(wv << 16) : __uint_as_float(wv);
         const float w1 = BF16 ? __uint_as_float(wv & 0xffff0000u) : 0.0f;
 #pragma unroll
@@ -149,12 +162,13 @@ __global__ void __launch_bounds__(256) head_transpose(const float *src, size_t v
         const size_t t = t0 + r, v = v0 + tx;
         if (t >= d || v >= vocab_p) continue;
         const float x = tile[tx][r];
-        const size_t rw = head_rows_per_wave(BF16);
-        const size_t o = ((v / rw) * d + t) * rw + v % rw;
+        const size_t rw = head_rows_per_wave(BF16), rr = v % rw, dq = (d + 3) / 4;
+        const size_t lane = BF16 ? rr / 2 : rr;
+        const size_t dw = (((v / rw) * dq + t / 4) * 64 + lane) * 4 + t % 4;  // the dword
         if (BF16)
-            ((uint16_t *)dst)[o] = (uint16_t)(__float_as_uint(x) >> 16);
+            ((uint16_t *)dst)[2 * dw + rr % 2] = (uint16_t)(__float_as_uint(x) >> 16);
         else
-            ((float *)dst)[o] = x;
+            ((float *)dst)[dw] = x;
     }
 }
 
@@ -177,8 +191,9 @@ static int head_build(qbk_ctx *ctx, const float *src_dev, size_t vocab, size_t d
     if (flag) (void)hipFree(flag);
     H->bf16 = f == 0;
     H->vocab_p = round_up(vocab, head_rows_per_wg(H->bf16));
-    const size_t bytes = d_model * H->vocab_p * (H->bf16 ? 2 : 4);
+    const size_t bytes = round_up(d_model, 4) * H->vocab_p * (H->bf16 ? 2 : 4);
     if (e == hipSuccess) e = hipMalloc(&H->w, bytes);
+    if (e == hipSuccess) e = hipMemset(H->w, 0, bytes);  // the padded steps
     if (e == hipSuccess) {
         dim3 g((unsigned)div_ceil(H->vocab_p, 32), (unsigned)div_ceil(d_model, 32));
         if (H->bf16)
