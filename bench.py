@@ -9,7 +9,7 @@ measured).  One step = one decode of every layer in the set: three launches
 (the fp8 split of x; stage 1, t = bf16(Vb^T bf16(s2*x)), written as stage 2's
 fp8 operand; stage 2, y = bf16(bf16(Ub t)*s1)).
 
-value = algorithmic bytes of all layers / step time, with the BASELINE.md
+value = algorithmic bytes of all layers / step time, with config 1's
 per-layer count 1,097,728 B (U 512 KiB + V 512 KiB + x 8 KiB + y 8 KiB + s1,
 s2 32 KiB).  The timed region holds only the steps between two events.  The
 roofline's kernel duration: that phase alone, launched `steps` times back to
@@ -36,7 +36,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK = 8.0e12          # B/s
 BF16_PEAK = 2.5e15         # dense FLOP/s
 INT8_PEAK = 5.0e15         # dense OP/s
-LAYER_BYTES = 1_097_728    # BASELINE.md config 1, per layer
+LAYER_BYTES = 1_097_728    # config 1's algorithmic bytes per layer
 M = N = 4096
 R = 1024
 METRIC = "factor-linear GB/s & %HBM peak (B=1); GEMM+SageAttn TFLOP/s & %MFMA peak"
@@ -432,7 +432,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the path's multi-GPU sharding is described in DESIGN.md)", file=sys.stderr)
+              "(one process drives one GPU; this build runs no collectives)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
