@@ -25,6 +25,8 @@ def say(*a):
 
 @pytest.mark.parametrize("vocab,d,bf16,batch", [
     (1000, 64, True, 1), (777, 100, True, 3), (1537, 256, False, 2), (513, 4096, True, 11), (300, 7, False, 8),
+    # whole 128-step chunks and a ragged tail that ends inside a four-step group
+    (650, 262, True, 2), (130, 262, False, 1),
 ])
 def test_head_logits_bit_identical(ctx, orc, vocab, d, bf16, batch):
     from quantibbler_amd import LmHead
