@@ -317,6 +317,45 @@ def random_rows(np, rng, n_rows, n_bits):
     return b
 
 
+def bench_block(qa, ctx, torch, np, ctx_tokens=2048, steps=50):
+    """One decoder block of config 3 (engine/mod.rs:878-945: norm, q/k/v,
+    RoPE, cache append, the sage decode attention on a kept state, o +
+    residual, norm, gate/up, SwiGLU, down + residual) at one position, with
+    ctx_tokens already in its cache: time per block per token, and that
+    times 32 for the trunk of a 32-block model.  Scales keep activations
+    near unit size (s1 ~ 1/sqrt(r din))."""
+    rng = np.random.default_rng(44)
+    layers = []
+    for name, m, n, r in CFG3:
+        s1 = (np.exp(0.3 * rng.standard_normal(m)) / np.sqrt(r * n)).astype(np.float32)
+        s2 = np.exp(0.3 * rng.standard_normal(n)).astype(np.float32)
+        layers.append(qa.FactorLayer.from_rows(ctx, m, n, r, random_rows(np, rng, m, r),
+                                               random_rows(np, rng, r, n), s1, s2, None))
+    d = 4096
+    w_in = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    w_post = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    B = qa.DecoderBlock(ctx, layers, w_in, w_post, 32, 8, 128, 500000.0, 1e-5, ctx_tokens + steps + 64, 64)
+    st = torch.cuda.current_stream()
+    hs = torch.randn((ctx_tokens + steps, d), device="cuda")
+    for pos in range(ctx_tokens):  # fill the cache, one position a call
+        B.decode_dev(hs[pos], pos, st)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for pos in range(ctx_tokens, ctx_tokens + steps):
+        B.decode_dev(hs[pos], pos, st)
+    b.record(st)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / steps * 1e3
+    finite = bool(torch.isfinite(hs[ctx_tokens:]).all())
+    B.close()
+    log(f"  decoder block (config 3 shapes) at {ctx_tokens}-{ctx_tokens + steps} cached tokens: "
+        f"{us:.1f} us per block per token, x32 = {32 * us / 1e3:.2f} ms")
+    return {"us_per_block_token": round(us, 1), "trunk_32_blocks_ms": round(32 * us / 1e3, 3),
+            "cached_tokens": ctx_tokens, "outputs_finite": finite,
+            "shape": "d 4096, 32/8 heads x 128, ffn 14336, config-3 ranks; bf16 serving, sage decode attention"}
+
+
 def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
     """Decode (batch 1) of every projection of n_layers distinct decoder
     layers -- 480 MB of signs, beyond the 256 MB MALL -- as one FactorSet
@@ -422,7 +461,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head"],
+    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head", "block"],
                     help="run one secondary workload alone and print its figures (for profiling); "
                          "no headline line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -451,6 +490,8 @@ def main():
             res = bench_sage_decode(qa, ctx, torch, np)
         elif args.only == "head":
             res = bench_head(qa, ctx, torch, np)
+        elif args.only == "block":
+            res = bench_block(qa, ctx, torch, np)
         else:
             res = bench_cfg3(qa, ctx, torch, np)
         print(json.dumps({"only": args.only, "result": res}), flush=True)
@@ -492,6 +533,7 @@ def main():
         extra["sage_decode"] = bench_sage_decode(qa, ctx, torch, np)
         log("lm_head ...")
         extra["lm_head"] = bench_head(qa, ctx, torch, np)
+        extra["decoder_block"] = bench_block(qa, ctx, torch, np)
         log("config 3 (8B decoder layer projections) ...")
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")

@@ -158,6 +158,33 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *set, int stage,
                              size_t workspace_size, void *stream);
 
 
+/* ---- decoder block (engine/mod.rs:878-945) --------------------------------- */
+
+/* One decoder block of Engine::transformer at one position, bf16 serving,
+ * the sage decode attention (engine/mod.rs:984-1030) on a kept state:
+ *   x = bf16(rmsnorm(bf16(h)) w_in); q, k, v = apply_bf16(x); RoPE
+ *   (engine/mod.rs:1169-1187) at pos; k, v appended to the block's cache;
+ *   a = attention over pos + 1 rows; h1 = o(a) + h;
+ *   x2 = bf16(rmsnorm(bf16(h1)) w_post); h' = down(g u / (1 + exp(-g))) + h1
+ * with g, u = gate(x2), up(x2).  layers: q, k, v, o, gate, up, down (the
+ * block borrows them; they must outlive it).  The block owns its KV cache of
+ * `capacity` rows and the attention state.  Its norms' sums run as trees
+ * and its exp is the device's, so the block agrees with the reference to a
+ * tolerance, not bit for bit.  Calls on one block must be ordered. */
+typedef struct qbk_block qbk_block;
+int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float *input_norm,
+                     const float *post_norm, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                     double rope_theta, double rms_norm_eps, size_t capacity, size_t block_size,
+                     qbk_block **out);
+void qbk_block_destroy(qbk_block *block);
+/* h: f32 [d_model] on the device, replaced by the block's output; pos = the
+ * number of positions already in the block's cache (0 for a new sequence,
+ * after qbk_block_reset). */
+int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *block, float *h, size_t pos, void *stream);
+int qbk_block_reset(qbk_block *block);
+/* The block's KV cache (device, f32 [capacity][n_kv_heads * head_dim] each). */
+int qbk_block_cache(const qbk_block *block, float **k_cache, float **v_cache);
+
 /* ---- attention (gpu_attention.rs) ----------------------------------------- */
 
 /* gpu_attention.rs:402-411 AttentionShape */

@@ -367,3 +367,70 @@ def head_logits(head, hidden, threads=0):
     out = np.zeros((h2.shape[0], vocab), np.float32)
     lib().orc_head_logits(_ptr(head), vocab, d, _ptr(h2), h2.shape[0], _ptr(out), _threads(threads))
     return out[0] if one else out
+
+
+# ---- one decoder block at one position (engine/mod.rs:878-945) --------------
+
+def rms_norm_bf16(x, w, eps) -> np.ndarray:
+    """engine/mod.rs:837-852 norm_apply at bf16 serving over rms_norm_into
+    (:1154-1166): the operand rounded to bf16, its sum of squares taken
+    sequentially in f32, / len, inv = 1 / sqrt(ss + eps) in f32, out =
+    v * inv * w, rounded to bf16."""
+    xb = bf16_to_f32(f32_to_bf16_fast(np.asarray(x, np.float32)))
+    ss = np.float32(0.0)
+    for v in xb:
+        ss = np.float32(ss + np.float32(v * v))
+    ss = np.float32(ss / np.float32(len(xb)))
+    inv = np.float32(np.float32(1.0) / np.sqrt(np.float32(ss + np.float32(eps))))
+    out = (xb * inv).astype(np.float32) * np.asarray(w, np.float32)
+    return bf16_to_f32(f32_to_bf16_fast(out.astype(np.float32)))
+
+
+def rope_rotate(v, head_dim, pos, theta) -> np.ndarray:
+    """engine/mod.rs:1169-1187: rotate_half pairs (i, i + hd/2) of every head
+    by pos * theta^(-2i/hd), the angle's sin and cos in f64, applied in f32."""
+    import math
+
+    v = np.array(v, np.float32)
+    half = head_dim // 2
+    for base in range(0, len(v), head_dim):
+        for i in range(half):
+            inv_freq = math.pow(theta, -(2.0 * i) / head_dim)
+            ang = pos * inv_freq
+            s, c = np.float32(math.sin(ang)), np.float32(math.cos(ang))
+            a, b = v[base + i], v[base + half + i]
+            v[base + i] = np.float32(np.float32(a * c) - np.float32(b * s))
+            v[base + half + i] = np.float32(np.float32(b * c) + np.float32(a * s))
+    return v
+
+
+def block_decode(layers, w_in, w_post, h, pos, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+                 theta, eps, block) -> np.ndarray:
+    """engine/mod.rs:878-945, one block at position pos, bf16 serving and the
+    sage decode attention (the padded call of :984-1030, row 0).  layers: the
+    seven dicts q, k, v, o, gate, up, down with dout, din, r, ub, vt, s1, s2,
+    bias; k_cache / v_cache: f32 [capacity][n_kv_heads * head_dim], row pos
+    written here.  Returns the block's output h."""
+    def proj(L, x):
+        return factor_apply("bf16", L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                            L["bias"], x)
+
+    q_l, k_l, v_l, o_l, g_l, u_l, d_l = layers
+    h = np.asarray(h, np.float32)
+    x = rms_norm_bf16(h, w_in, eps)
+    q = rope_rotate(proj(q_l, x), head_dim, pos, theta)
+    k = rope_rotate(proj(k_l, x), head_dim, pos, theta)
+    v = proj(v_l, x)
+    k_cache[pos] = k
+    v_cache[pos] = v
+    seq = pos + 1
+    qp = np.zeros((1, n_heads, seq, head_dim), np.float32)
+    qp[0, :, 0, :] = q.reshape(n_heads, head_dim)
+    kp = np.ascontiguousarray(k_cache[:seq].reshape(seq, n_kv_heads, head_dim).transpose(1, 0, 2))[None]
+    vp = np.ascontiguousarray(v_cache[:seq].reshape(seq, n_kv_heads, head_dim).transpose(1, 0, 2))[None]
+    attn = attention_sage_dev(qp, kp, vp, False, block)[0, :, 0, :].reshape(-1)
+    h1 = (proj(o_l, attn) + h).astype(np.float32)
+    x2 = rms_norm_bf16(h1, w_post, eps)
+    g, u = proj(g_l, x2), proj(u_l, x2)
+    hid = ((g * u).astype(np.float32) / (np.float32(1.0) + np.exp(-g).astype(np.float32))).astype(np.float32)
+    return (proj(d_l, hid) + h1).astype(np.float32)

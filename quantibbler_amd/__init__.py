@@ -11,8 +11,8 @@ two hot paths behind the reference's own API surface:
 All compute runs in libqbk.so (hand-written HIP, C ABI in include/qbk.h).
 """
 from ._lib import DeviceError, InitError, KernelError, load as _load_lib  # noqa: F401
-from .gpu import (AttentionShape, FactorLayer, FactorSet, GpuContext, LmHead,  # noqa: F401
-                  SageDecodeState, gpu_available)
+from .gpu import (AttentionShape, DecoderBlock, FactorLayer, FactorSet, GpuContext,  # noqa: F401
+                  LmHead, SageDecodeState, gpu_available)
 
 _load_lib()
 

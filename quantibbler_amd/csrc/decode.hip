@@ -762,6 +762,22 @@ struct qbk_factor_set {
     std::vector<const qbk_factor *> layers;
 };
 
+namespace qbk {
+
+// A set's decode with the x and y dtypes of the caller's choice (the C ABI's
+// form is bf16 in and out): x the concatenation of the layers' inputs.
+int q4_set_run(const qbk_factor_set *S, const void *x, bool xf32, void *y, bool ybf16, void *ws, hipStream_t s) {
+    for (int ph = 1; ph <= Q4_PHASES; ph++) {
+        int rc = q4_phase(ph, S->geom, S->tab, S->wg1, S->wg2, S->s2cat, x, xf32, y, ybf16, ws, s);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
+
+size_t q4_set_workspace(const qbk_factor_set *S) { return S->geom.bytes; }
+
+}  // namespace qbk
+
 extern "C" {
 
 int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t n,

@@ -59,6 +59,11 @@ size_t q4_workspace(const qbk_factor *L, size_t batch);
 int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y, bool ybf16,
            void *ws, hipStream_t s);
 
+// decode.hip: a layer set's three launches with f32 or bf16 x and y, and its
+// workspace bytes.
+int q4_set_run(const qbk_factor_set *S, const void *x, bool xf32, void *y, bool ybf16, void *ws, hipStream_t s);
+size_t q4_set_workspace(const qbk_factor_set *S);
+
 // prefill.hip: the sign layout of the prefill GEMM (rows_p a multiple of
 // 128, bits_p of 64), its workspace, and the two-stage GEMM for N tokens:
 // x [N][din] (bf16, or f32 when xf32) -> y [N][dout].

@@ -264,6 +264,57 @@ class SageDecodeState:
         self.tokens = seq_kv
 
 
+class DecoderBlock:
+    """One decoder block of the server's transformer at one position
+    (engine/mod.rs:878-945; bf16 serving, the sage decode attention on a
+    kept state): norm -> q/k/v -> RoPE -> cache append -> attention -> o +
+    residual -> norm -> gate/up -> SwiGLU -> down + residual, on the device.
+    ``layers`` are the seven FactorLayers q, k, v, o, gate, up, down (kept
+    alive here); the block owns its KV cache of ``capacity`` rows."""
+
+    def __init__(self, ctx: GpuContext, layers, input_norm, post_norm, n_heads: int,
+                 n_kv_heads: int, head_dim: int, rope_theta: float, rms_norm_eps: float,
+                 capacity: int, block_size: int = 64):
+        if len(layers) != 7:
+            raise _lib.KernelError("a decoder block takes 7 layers: q, k, v, o, gate, up, down")
+        self.ctx = ctx
+        self.layers = list(layers)
+        arr = (C.c_void_p * 7)(*[L.handle for L in self.layers])
+        w_in = np.ascontiguousarray(input_norm, np.float32)
+        w_post = np.ascontiguousarray(post_norm, np.float32)
+        out = C.c_void_p()
+        check(_lib.load().qbk_block_create(ctx.handle, arr, _ptr(w_in), _ptr(w_post), int(n_heads),
+                                           int(n_kv_heads), int(head_dim), float(rope_theta),
+                                           float(rms_norm_eps), int(capacity), int(block_size),
+                                           C.byref(out)))
+        self._h = out
+        self.capacity = int(capacity)
+
+    def decode_dev(self, h, pos: int, stream=None):
+        """h: device f32 [d_model], replaced by the block's output at position pos."""
+        check(_lib.load().qbk_block_decode_dev(self.ctx.handle, self._h, _ptr(h), int(pos),
+                                               _stream(stream)))
+
+    def reset(self):
+        check(_lib.load().qbk_block_reset(self._h))
+
+    def cache_ptrs(self):
+        k, v = C.c_void_p(), C.c_void_p()
+        check(_lib.load().qbk_block_cache(self._h, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def close(self):
+        if self._h:
+            _lib.load().qbk_block_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class LmHead:
     """Device-resident language-model head (engine/mod.rs:781-800
     Engine::logits): logits[v] = sum_t hidden[t] * head[v][t], one f32 sum

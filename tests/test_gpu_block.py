@@ -1,0 +1,77 @@
+"""GPU check: one decoder block at one position (engine/mod.rs:878-945, bf16
+serving, sage decode attention) through the C ABI, against the oracle's
+restatement over a run of positions that crosses key-block boundaries.
+
+The block's projections are the device factor linears, whose f32 sums run in
+MFMA order (the reference sums each row sequentially), its norms' sums are
+trees and its exp is the device's, so the block is held to a tolerance: per
+position, cosine and relative L2 error of the output against the oracle fed
+the same inputs (each position a fresh input, as a new token's embedding
+would be; the caches of the two sides grow separately)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+COS_MIN = 0.9999
+REL_MAX = 0.01
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from quantibbler_amd import GpuContext
+
+    return GpuContext(0)
+
+
+def scaled_layer(orc, rng, dout, din, r):
+    """Random signs; scales that keep |y| near |x| (s1 ~ 1/sqrt(r din))."""
+    ubs = rng.choice([-1, 1], (dout, r)).astype(np.int8)
+    vts = rng.choice([-1, 1], (r, din)).astype(np.int8)
+    s2 = np.exp(0.3 * rng.standard_normal(din)).astype(np.float32)
+    s1 = (np.exp(0.3 * rng.standard_normal(dout)) / np.sqrt(r * din)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(dout)).astype(np.float32)
+    return dict(dout=dout, din=din, r=r, ub=orc.pack_bits(ubs), vt=orc.pack_bits(vts), s1=s1, s2=s2,
+                bias=bias)
+
+
+def metrics(got, want):
+    got, want = np.asarray(got, np.float64).ravel(), np.asarray(want, np.float64).ravel()
+    cos = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want) + 1e-300))
+    rel = float(np.linalg.norm(got - want) / (np.linalg.norm(want) + 1e-300))
+    return cos, rel
+
+
+def test_decoder_block_matches_oracle(ctx, orc):
+    from quantibbler_amd import DecoderBlock, FactorLayer
+
+    d, H, Hk, hd, ffn, cap, blk = 256, 4, 2, 64, 512, 40, 16
+    theta, eps = 500000.0, 1e-5
+    rng = np.random.default_rng(17)
+    shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
+              (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    w_in = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    w_post = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    block = DecoderBlock(ctx, devs, w_in, w_post, H, Hk, hd, theta, eps, cap, blk)
+    kc = np.zeros((cap, Hk * hd), np.float32)
+    vc = np.zeros((cap, Hk * hd), np.float32)
+    assert all(block.cache_ptrs())
+    st = torch.cuda.current_stream()
+    worst = (1.0, 0.0)
+    for pos in range(20):
+        h = rng.standard_normal(d).astype(np.float32)
+        hd_dev = torch.from_numpy(h).cuda()
+        block.decode_dev(hd_dev, pos, st)
+        torch.cuda.synchronize()
+        want = orc.block_decode(layers, w_in, w_post, h, pos, kc, vc, H, Hk, hd, theta, eps, blk)
+        got = hd_dev.cpu().numpy()
+        cos, rel = metrics(got, want)
+        print(f"pos {pos}: out cos {cos:.7f} rel {rel:.2e}", flush=True)
+        worst = (min(worst[0], cos), max(worst[1], rel))
+        assert cos >= COS_MIN and rel <= REL_MAX, (pos, cos, rel)
+    print("worst", worst, flush=True)
+    block.close()
