@@ -18,11 +18,16 @@ back between two events on the launch stream (rocprofv3 --kernel-trace
 
 Extras (same JSON line): single-layer decode latency; prefill GEMM TFLOP/s at
 B in {16, 128, 512, 2048}; block-scaled SageAttention prefill at
-B=1, H=32, S=4096, d=128, causal; and the CPU baseline: the
-oracle's C restatement of the reference fast face (fast.rs, f64, OpenMP over
-64-row blocks) timed on the host on a bounded sample of the decode workload.
+B=1, H=32, S=4096, d=128, causal; the reference scheme's decode
+attention step at 4096 cached tokens (from scratch and on a kept state); the
+lm_head at 128256 x 4096; one decoder block at config 3's shapes; config 3's
+seven projections over 32 decoder layers (decode and prefill); and the CPU
+baseline: the oracle's C restatement of the reference fast face (fast.rs,
+f64, OpenMP over 64-row blocks) timed on the host on a bounded sample of the
+decode workload.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--layers 512]
+    python bench.py --only gemm|sage|cfg3|sage_decode|head|block
 """
 import argparse
 import json
