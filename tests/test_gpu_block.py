@@ -75,3 +75,25 @@ def test_decoder_block_matches_oracle(ctx, orc):
         assert cos >= COS_MIN and rel <= REL_MAX, (pos, cos, rel)
     print("worst", worst, flush=True)
     block.close()
+
+
+def test_decoder_block_validation(ctx, orc):
+    from quantibbler_amd import DecoderBlock, FactorLayer, KernelError
+
+    rng = np.random.default_rng(23)
+    d, H, Hk, hd, ffn = 128, 2, 1, 64, 256
+    shapes = [(H * hd, d, 16), (Hk * hd, d, 16), (Hk * hd, d, 16), (d, H * hd, 16),
+              (ffn, d, 16), (ffn, d, 16), (d, ffn, 16)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    w = np.ones(d, np.float32)
+    with pytest.raises(KernelError, match=r"decoder block: k is 128x128, expected 64x128"):
+        DecoderBlock(ctx, [devs[0], devs[0]] + devs[2:], w, w, H, Hk, hd, 1e4, 1e-5, 16)
+    with pytest.raises(KernelError, match="n_kv_heads dividing n_heads"):
+        DecoderBlock(ctx, devs, w, w, 3, 2, hd, 1e4, 1e-5, 16)
+    block = DecoderBlock(ctx, devs, w, w, H, Hk, hd, 1e4, 1e-5, 4, 16)
+    h = torch.zeros(d, dtype=torch.float32, device="cuda")
+    with pytest.raises(KernelError, match="position 4 is past the block's cache capacity of 4"):
+        block.decode_dev(h, 4)
+    block.close()
