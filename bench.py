@@ -20,14 +20,15 @@ Extras (same JSON line): single-layer decode latency; prefill GEMM TFLOP/s at
 B in {16, 128, 512, 2048}; block-scaled SageAttention prefill at
 B=1, H=32, S=4096, d=128, causal; the reference scheme's decode
 attention step at 4096 cached tokens (from scratch and on a kept state); the
-lm_head at 128256 x 4096; one decoder block at config 3's shapes; config 3's
+lm_head at 128256 x 4096; one decoder block at config 3's shapes, and a decode
+token through 32 such blocks and the lm_head; config 3's
 seven projections over 32 decoder layers (decode and prefill); and the CPU
 baseline: the oracle's C restatement of the reference fast face (fast.rs,
 f64, OpenMP over 64-row blocks) timed on the host on a bounded sample of the
 decode workload.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--layers 512]
-    python bench.py --only gemm|sage|cfg3|sage_decode|head|block
+    python bench.py --only gemm|sage|cfg3|sage_decode|head|block|token
 """
 import argparse
 import json
@@ -361,6 +362,61 @@ def bench_block(qa, ctx, torch, np, ctx_tokens=2048, steps=50):
             "shape": "d 4096, 32/8 heads x 128, ffn 14336, config-3 ranks; bf16 serving, sage decode attention"}
 
 
+def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab=128256):
+    """A decode token through a 32-block config-3-shaped trunk and the
+    lm_head, all on the device (config 5's decode at batch 1 without the
+    embedding lookup and sampling): 32 DecoderBlock calls, then the logits.
+    Every block has its own layers (480 MB of signs in all) and cache, filled
+    one position a token to ctx_tokens before the timed tokens."""
+    rng = np.random.default_rng(55)
+    d = 4096
+    blocks, keep = [], []
+    for bi in range(n_blocks):
+        layers = []
+        for name, m, n, r in CFG3:
+            s1 = (np.exp(0.3 * rng.standard_normal(m)) / np.sqrt(r * n)).astype(np.float32)
+            s2 = np.exp(0.3 * rng.standard_normal(n)).astype(np.float32)
+            layers.append(qa.FactorLayer.from_rows(ctx, m, n, r, random_rows(np, rng, m, r),
+                                                   random_rows(np, rng, r, n), s1, s2, None))
+        w = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+        blocks.append(qa.DecoderBlock(ctx, layers, w, w, 32, 8, 128, 500000.0, 1e-5,
+                                      ctx_tokens + steps + 64, 64))
+        keep.append(layers)
+    g = torch.Generator(device="cuda").manual_seed(56)
+    rows = (0.02 * torch.randn((vocab, d), device="cuda", generator=g)).to(torch.bfloat16).to(torch.float32)
+    head = qa.LmHead.from_rows_dev(ctx, rows, vocab, d)
+    del rows
+    logits = torch.empty(vocab, dtype=torch.float32, device="cuda")
+    st = torch.cuda.current_stream()
+    hs = torch.randn((ctx_tokens + steps, d), device="cuda", generator=g)
+
+    def token(pos):
+        h = hs[pos]
+        for B in blocks:
+            B.decode_dev(h, pos, st)
+        head.logits_dev(h, 1, logits, st)
+
+    for pos in range(ctx_tokens):
+        token(pos)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for pos in range(ctx_tokens, ctx_tokens + steps):
+        token(pos)
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    finite = bool(torch.isfinite(logits).all())
+    for B in blocks:
+        B.close()
+    head.close()
+    log(f"  decode token (32 blocks + lm_head) at {ctx_tokens} cached tokens: {ms:.3f} ms")
+    return {"ms_per_token": round(ms, 3), "tokens_per_s": round(1e3 / ms, 1), "cached_tokens": ctx_tokens,
+            "logits_finite": finite,
+            "shape": "32 config-3 blocks (bf16 serving, sage decode attention) + lm_head 128256 x 4096 bf16; "
+                     "no embedding lookup or sampling"}
+
+
 def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
     """Decode (batch 1) of every projection of n_layers distinct decoder
     layers -- 480 MB of signs, beyond the 256 MB MALL -- as one FactorSet
@@ -466,7 +522,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head", "block"],
+    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head", "block", "token"],
                     help="run one secondary workload alone and print its figures (for profiling); "
                          "no headline line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -497,6 +553,8 @@ def main():
             res = bench_head(qa, ctx, torch, np)
         elif args.only == "block":
             res = bench_block(qa, ctx, torch, np)
+        elif args.only == "token":
+            res = bench_token(qa, ctx, torch, np)
         else:
             res = bench_cfg3(qa, ctx, torch, np)
         print(json.dumps({"only": args.only, "result": res}), flush=True)
@@ -539,6 +597,8 @@ def main():
         log("lm_head ...")
         extra["lm_head"] = bench_head(qa, ctx, torch, np)
         extra["decoder_block"] = bench_block(qa, ctx, torch, np)
+        log("decode token (32 blocks + lm_head) ...")
+        extra["decode_token"] = bench_token(qa, ctx, torch, np)
         log("config 3 (8B decoder layer projections) ...")
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")
