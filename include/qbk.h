@@ -162,28 +162,58 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *set, int stage,
 
 /* One decoder block of Engine::transformer at one position, bf16 serving,
  * the sage decode attention (engine/mod.rs:984-1030) on a kept state:
- *   x = bf16(rmsnorm(bf16(h)) w_in); q, k, v = apply_bf16(x); RoPE
- *   (engine/mod.rs:1169-1187) at pos; k, v appended to the block's cache;
- *   a = attention over pos + 1 rows; h1 = o(a) + h;
+ *   x = bf16(rmsnorm(bf16(h)) w_in); q, k, v = apply_bf16(x); with q/k
+ *   norms, q and k per-head norm_apply (engine/mod.rs:854-876, :907-910);
+ *   RoPE (engine/mod.rs:1169-1187) at pos; k, v appended to the block's
+ *   cache; a = attention over pos + 1 rows; h1 = o(a) + h;
  *   x2 = bf16(rmsnorm(bf16(h1)) w_post); h' = down(g u / (1 + exp(-g))) + h1
  * with g, u = gate(x2), up(x2).  layers: q, k, v, o, gate, up, down (the
- * block borrows them; they must outlive it).  The block owns its KV cache of
- * `capacity` rows and the attention state.  Its norms' sums run as trees
- * and its exp is the device's, so the block agrees with the reference to a
- * tolerance, not bit for bit.  Calls on one block must be ordered. */
+ * block borrows them; they must outlive it).  input_norm / post_norm hold
+ * d_model floats each (their lengths are checked); q_norm and k_norm are
+ * both NULL (no per-head norms, Llama-style) or both head_dim floats
+ * (qk_norm_len).  The block owns its KV cache of `capacity` rows and the
+ * attention state.  Its norms' sums run as trees and its exp is the
+ * device's, so the block agrees with the reference to a tolerance, not bit
+ * for bit.  Calls on one block must be ordered. */
 typedef struct qbk_block qbk_block;
 int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float *input_norm,
-                     const float *post_norm, size_t n_heads, size_t n_kv_heads, size_t head_dim,
-                     double rope_theta, double rms_norm_eps, size_t capacity, size_t block_size,
-                     qbk_block **out);
+                     size_t input_norm_len, const float *post_norm, size_t post_norm_len,
+                     const float *q_norm, const float *k_norm, size_t qk_norm_len, size_t n_heads,
+                     size_t n_kv_heads, size_t head_dim, double rope_theta, double rms_norm_eps,
+                     size_t capacity, size_t block_size, qbk_block **out);
 void qbk_block_destroy(qbk_block *block);
 /* h: f32 [d_model] on the device, replaced by the block's output; pos = the
  * number of positions already in the block's cache (0 for a new sequence,
- * after qbk_block_reset). */
+ * after qbk_block_reset).  A pos beyond the positions the block holds is a
+ * validation error; a smaller pos rewinds (the cache rows from pos on are
+ * overwritten and the attention state is rebuilt). */
 int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *block, float *h, size_t pos, void *stream);
 int qbk_block_reset(qbk_block *block);
-/* The block's KV cache (device, f32 [capacity][n_kv_heads * head_dim] each). */
+/* The block's KV cache (device, f32 [capacity][n_kv_heads * head_dim] each).
+ * Rows written through these pointers are not seen by the attention state
+ * until qbk_block_reset. */
 int qbk_block_cache(const qbk_block *block, float **k_cache, float **v_cache);
+
+/* ---- trunk pieces around the blocks (engine/mod.rs:763-800, 943) ---------- */
+
+/* Engine::embed (engine/mod.rs:768-778): out[i] = table[tokens[i]], f32
+ * rows of d_model, table on the device (vocab x d_model).  The host form
+ * takes host token ids and refuses an id outside the vocabulary with the
+ * reference's text; it returns once the rows are written.  The device form
+ * takes device ids and cannot refuse: an out-of-range id gets a NaN row. */
+int qbk_embed(qbk_ctx *ctx, const float *table, size_t vocab, size_t d_model, const int32_t *tokens,
+              size_t n, float *out, void *stream);
+int qbk_embed_dev(qbk_ctx *ctx, const float *table, size_t vocab, size_t d_model, const int32_t *tokens,
+                  size_t n, float *out, void *stream);
+/* The final norm (engine/mod.rs:943, norm_apply at bf16 serving, :837-852):
+ * per row, bf16 operand, f32 mean square, out = bf16(b * inv * w) held as f32
+ * (device pointers, rows x d). */
+int qbk_rms_norm_dev(qbk_ctx *ctx, const float *x, size_t rows, size_t d, const float *w, double eps,
+                     float *out, void *stream);
+/* sampler.rs:4-15 greedy: per row of `vocab` logits, the first index of the
+ * largest value (NaN never wins; 0 when nothing beats -inf). */
+int qbk_argmax_dev(qbk_ctx *ctx, const float *logits, size_t rows, size_t vocab, int32_t *out,
+                   void *stream);
 
 /* ---- attention (gpu_attention.rs) ----------------------------------------- */
 
@@ -196,7 +226,8 @@ typedef struct {
  * scheme (per-token INT8 Q with 1/sqrt(d) folded, per-K-block mean, per-token
  * INT8 K, P at the static 1/127 scale, per-channel INT8 V per tile), f32
  * q (B,H,S,d), k (B,Hkv,S,d), v (B,Hkv,S,dv) -> out (B,H,S,dv), same
- * validation and messages.  Both INT8 products run on INT8 MFMA. */
+ * validation and messages.  Both INT8 products are exact integer dot
+ * products on v_dot4_i32_i8 (the scheme is per-row, VALU-bound). */
 int qbk_attention_sage(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, size_t q_len,
                        const float *k, size_t k_len, const float *v, size_t v_len, int causal,
                        size_t block_size, float *out);

@@ -77,6 +77,9 @@ def _declare(L):
         "orc_expf": (C.c_float, [C.c_float]),
         "orc_attention_sage_blk": (C.c_int, [C.POINTER(AttnShape), _P, _P, _P, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int]),
         "orc_head_logits": (None, [_P, _Z, _Z, _P, _Z, _P, C.c_int]),
+        "orc_rms_norm_f32": (None, [_P, _P, _Z, C.c_double, _P]),
+        "orc_rope_rotate": (None, [_P, _Z, _Z, _Z, C.c_double]),
+        "orc_gqa_attention_scalar": (None, [_P, _P, _P, _Z, _Z, _Z, _Z, _P, _P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -222,6 +225,21 @@ def qpk1_parse(stream: bytes) -> dict:
         "ub_packed": b[hdr.ub_off:hdr.ub_off + ub_len].copy(),
         "vb_packed": b[hdr.vb_off:hdr.vb_off + vb_len].copy(),
     }
+
+
+def qpk1_layer(stream: bytes) -> dict:
+    """crates/quantibbler-qpk1/src/lib.rs:229-320 parse, then
+    engine/mod.rs:342-381 PackedLayer::from_layer: the per-row bitplanes
+    (container_to_rows / _transposed) and the f32 scales (f16 and f32 widen
+    exactly; a v1 layer's bias is the zero map)."""
+    L = qpk1_parse(stream)
+    dout, din, r = L["dout"], L["din"], L["r"]
+    bias = L["bias"] if L["bias"].size else np.zeros(dout)
+    return dict(dout=dout, din=din, r=r, version=L["version"], dtype_tag=L["dtype_tag"],
+                ub=container_to_rows(L["ub_packed"], dout, r),
+                vt=container_to_rows_transposed(L["vb_packed"], din, r),
+                s1=L["s1"].astype(np.float32), s2=L["s2"].astype(np.float32),
+                bias=bias.astype(np.float32))
 
 
 def qpk1_expected_size(dout, din, r, itemsize, with_bias) -> int:
@@ -434,3 +452,144 @@ def block_decode(layers, w_in, w_post, h, pos, k_cache, v_cache, n_heads, n_kv_h
     g, u = proj(g_l, x2), proj(u_l, x2)
     hid = ((g * u).astype(np.float32) / (np.float32(1.0) + np.exp(-g).astype(np.float32))).astype(np.float32)
     return (proj(d_l, hid) + h1).astype(np.float32)
+
+
+# ---- the transformer trunk (engine/mod.rs:878-945, 763-800) ------------------
+
+def rms_norm_f32(x, w, eps) -> np.ndarray:
+    """engine/mod.rs:1152-1160 rms_norm_into (sequential f32 sum of squares)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rms_norm_f32(_ptr(x), _ptr(w), x.size, float(eps), _ptr(out))
+    return out
+
+
+def norm_apply(x, w, eps, serving) -> np.ndarray:
+    """engine/mod.rs:837-852 norm_apply: fp32 serving is rms_norm_into as is;
+    bf16 serving rounds the operand to bf16 first and the output after."""
+    if serving == "fp32":
+        return rms_norm_f32(x, w, eps)
+    xb = bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32)))
+    return bf16_to_f32(f32_to_bf16(rms_norm_f32(xb, w, eps)))
+
+
+def per_head_norm(v, w, head_dim, eps, serving) -> np.ndarray:
+    """engine/mod.rs:854-876 per_head_norm: norm_apply on every head_dim slice
+    with one head_dim weight."""
+    v = np.asarray(v, np.float32)
+    return np.concatenate([norm_apply(v[i:i + head_dim], w, eps, serving)
+                           for i in range(0, v.size, head_dim)])
+
+
+def rope(v, head_dim, pos, theta) -> np.ndarray:
+    """engine/mod.rs:1169-1187 rope_rotate (f64 angles, f32 rotation)."""
+    v = np.array(v, np.float32)
+    lib().orc_rope_rotate(_ptr(v), v.size, int(head_dim), int(pos), float(theta))
+    return v
+
+
+def gqa_attention_scalar(qh, k_cache, v_cache, n_heads, n_kv_heads, head_dim, pos) -> np.ndarray:
+    """engine/mod.rs:1073-1116: one query position over the row-major cache
+    rows 0..pos (f32 [rows][n_kv_heads * head_dim])."""
+    q = np.ascontiguousarray(qh, np.float32)
+    kc = np.ascontiguousarray(k_cache[:pos + 1], np.float32)
+    vc = np.ascontiguousarray(v_cache[:pos + 1], np.float32)
+    out = np.zeros(n_heads * head_dim, np.float32)
+    scratch = np.zeros(pos + 1, np.float32)
+    lib().orc_gqa_attention_scalar(_ptr(q), _ptr(kc), _ptr(vc), n_heads, n_kv_heads, head_dim, pos,
+                                   _ptr(out), _ptr(scratch))
+    return out
+
+
+def swiglu(g, u) -> np.ndarray:
+    """engine/mod.rs:930-934: g * u / (1 + exp(-g)) in f32 (exp rounded from
+    the f64 value, as libm's correctly rounded expf gives)."""
+    g = np.asarray(g, np.float32)
+    u = np.asarray(u, np.float32)
+    e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    return ((g * u).astype(np.float32) / (np.float32(1.0) + e).astype(np.float32)).astype(np.float32)
+
+
+def block_step(layers, norms, h, pos, k_cache, v_cache, n_heads, n_kv_heads, head_dim, theta, eps,
+               serving="fp32", attention="scalar", block=64) -> np.ndarray:
+    """engine/mod.rs:886-941, one block at position pos.  layers: the seven
+    layer dicts q, k, v, o, gate, up, down (dout, din, r, ub, vt, s1, s2,
+    bias); norms: {"input", "post_attention"[, "q_norm", "k_norm"]}; the
+    caches are f32 [capacity][n_kv_heads * head_dim], row pos written here.
+    serving "fp32" (apply: f64 matvecs) or "bf16" (apply_bf16); attention
+    "scalar" (gqa_attention_scalar, the default face) or "sage" (row 0 of the
+    padded reference-scheme call, :984-1030, block `block`)."""
+    def proj(L, x):
+        return factor_apply(serving, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                            L["bias"], x)
+
+    q_l, k_l, v_l, o_l, g_l, u_l, d_l = layers
+    h = np.asarray(h, np.float32)
+    x = norm_apply(h, norms["input"], eps, serving)
+    q, k, v = proj(q_l, x), proj(k_l, x), proj(v_l, x)
+    if "q_norm" in norms and "k_norm" in norms:
+        q = per_head_norm(q, norms["q_norm"], head_dim, eps, serving)
+        k = per_head_norm(k, norms["k_norm"], head_dim, eps, serving)
+    q = rope(q, head_dim, pos, theta)
+    k = rope(k, head_dim, pos, theta)
+    k_cache[pos] = k
+    v_cache[pos] = v
+    if attention == "scalar":
+        attn = gqa_attention_scalar(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, pos)
+    else:
+        seq = pos + 1
+        qp = np.zeros((1, n_heads, seq, head_dim), np.float32)
+        qp[0, :, 0, :] = q.reshape(n_heads, head_dim)
+        kp = np.ascontiguousarray(k_cache[:seq].reshape(seq, n_kv_heads, head_dim).transpose(1, 0, 2))[None]
+        vp = np.ascontiguousarray(v_cache[:seq].reshape(seq, n_kv_heads, head_dim).transpose(1, 0, 2))[None]
+        attn = attention_sage_dev(qp, kp, vp, False, block)[0, :, 0, :].reshape(-1)
+    h1 = (proj(o_l, attn) + h).astype(np.float32)
+    x2 = norm_apply(h1, norms["post_attention"], eps, serving)
+    hid = swiglu(proj(g_l, x2), proj(u_l, x2))
+    return (proj(d_l, hid) + h1).astype(np.float32)
+
+
+class Trunk:
+    """Engine::forward_prefill (engine/mod.rs:805-822): per token, the
+    embedding row, every block over its KV cache, the final norm and the
+    logits (Engine::logits, :788-800).  Built from a model directory (or any
+    object with the same fields) at a serving dtype; under bf16 serving the
+    remainder tensors are rounded to bf16 (engine/mod.rs:695-706)."""
+
+    def __init__(self, md, serving="fp32", attention="scalar", capacity=None, block=64):
+        self.md, self.serving, self.attention, self.block = md, serving, attention, block
+        q = (lambda a: bf16_to_f32(f32_to_bf16(np.asarray(a, np.float32)))) if serving == "bf16" else \
+            (lambda a: np.asarray(a, np.float32))
+        self.embedding = q(md.embedding)
+        self.head = q(md.head_rows())
+        self.final_norm = q(md.final_norm())
+        self.blocks = []
+        for b in range(md.n_layers):
+            layers = [qpk1_layer(s) for s in md.block_layers(b)]
+            norms = {k: q(v) for k, v in md.block_norms(b).items()}
+            self.blocks.append((layers, norms))
+        cap = capacity or 4096
+        kv = md.n_kv_heads * md.head_dim
+        self.kc = [np.zeros((cap, kv), np.float32) for _ in range(md.n_layers)]
+        self.vc = [np.zeros((cap, kv), np.float32) for _ in range(md.n_layers)]
+        self.pos = 0
+
+    def reset(self):
+        self.pos = 0
+
+    def hidden(self, token: int) -> np.ndarray:
+        """engine/mod.rs:878-945 transformer over one token at the next
+        position: the final-normed hidden row."""
+        md = self.md
+        h = self.embedding[int(token)].copy()
+        for b, (layers, norms) in enumerate(self.blocks):
+            h = block_step(layers, norms, h, self.pos, self.kc[b], self.vc[b], md.n_heads, md.n_kv_heads,
+                           md.head_dim, md.rope_theta, md.rms_norm_eps, self.serving, self.attention,
+                           self.block)
+        self.pos += 1
+        return norm_apply(h, self.final_norm, md.rms_norm_eps, self.serving)
+
+    def step(self, token: int) -> np.ndarray:
+        """Engine::forward (:802-806): the logits of one token."""
+        return head_logits(self.head, self.hidden(token))

@@ -1039,3 +1039,70 @@ void orc_head_logits(const float *head, size_t vocab, size_t d, const float *hid
         }
     }
 }
+
+/* ======================================================================= */
+/* transformer trunk pieces (engine/mod.rs:878-945 and helpers)            */
+/* ======================================================================= */
+
+/* engine/mod.rs:1152-1160 rms_norm_into: f32 end to end; the sum of squares
+ * is one sequential f32 fold, then / len, inv = 1 / sqrt(ss + eps as f32),
+ * out = (v * inv) * w. */
+void orc_rms_norm_f32(const float *x, const float *w, size_t n, double eps, float *out) {
+    float ss = 0.0f;
+    for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
+    ss = ss / (float)n;
+    float inv = 1.0f / sqrtf(ss + (float)eps);
+    for (size_t i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
+}
+
+/* engine/mod.rs:1169-1187 rope_rotate: rotate_half pairs (i, i + hd/2) of
+ * every head_dim slice of v (n values) by pos * theta^(-2i/hd); the angle's
+ * pow/sin/cos in f64, the rotation in f32. */
+void orc_rope_rotate(float *v, size_t n, size_t hd, size_t pos, double theta) {
+    size_t half = hd / 2;
+    for (size_t base = 0; base + hd <= n; base += hd)
+        for (size_t i = 0; i < half; i++) {
+            double inv_freq = pow(theta, -(2.0 * (double)i) / (double)hd);
+            double ang = (double)pos * inv_freq;
+            float s = (float)sin(ang), c = (float)cos(ang);
+            float a = v[base + i], b = v[base + half + i];
+            v[base + i] = a * c - b * s;
+            v[base + half + i] = b * c + a * s;
+        }
+}
+
+/* engine/mod.rs:1073-1116 gqa_attention_scalar: one query position over a
+ * row-major cache (k, v: [pos + 1][n_kv * hd]); per head, scores are the
+ * sequential f32 dot times 1/sqrt(hd), softmax by max-subtracted exp with a
+ * sequential denominator, output the sum of w * v over positions whose weight
+ * is not zero.  scratch: pos + 1 floats. */
+void orc_gqa_attention_scalar(const float *qh, const float *kc, const float *vc, size_t n_heads,
+                              size_t n_kv, size_t hd, size_t pos, float *out, float *scratch) {
+    size_t groups = n_heads / n_kv, kv_dim = n_kv * hd;
+    float scale = 1.0f / sqrtf((float)hd);
+    for (size_t i = 0; i < n_heads * hd; i++) out[i] = 0.0f;
+    for (size_t h = 0; h < n_heads; h++) {
+        size_t kvh = h / groups;
+        const float *q = qh + h * hd;
+        float maxs = -INFINITY;
+        for (size_t p = 0; p <= pos; p++) {
+            const float *k = kc + p * kv_dim + kvh * hd;
+            float dot = 0.0f;
+            for (size_t t = 0; t < hd; t++) dot += q[t] * k[t];
+            scratch[p] = dot * scale;
+            maxs = fmaxf(maxs, scratch[p]);
+        }
+        float denom = 0.0f;
+        for (size_t p = 0; p <= pos; p++) {
+            scratch[p] = expf(scratch[p] - maxs);
+            denom += scratch[p];
+        }
+        float *oh = out + h * hd;
+        for (size_t p = 0; p <= pos; p++) {
+            float w = scratch[p] / denom;
+            if (w == 0.0f) continue;
+            const float *v = vc + p * kv_dim + kvh * hd;
+            for (size_t t = 0; t < hd; t++) oh[t] += w * v[t];
+        }
+    }
+}

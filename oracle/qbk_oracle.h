@@ -113,11 +113,18 @@ int orc_attention_sage_blk(const orc_attn_shape *s, const uint16_t *q, const uin
                            float *qscale, int8_t *khat, float *kscale, float *kmean,
                            int threads);
 
-#ifdef __cplusplus
-}
-#endif
 /* engine/mod.rs:781-800 Engine::logits: sequential f32 sum per row. */
 void orc_head_logits(const float *head, size_t vocab, size_t d, const float *hidden, size_t batch,
                      float *logits, int threads);
+
+/* transformer trunk pieces (engine/mod.rs:1073-1187) */
+void orc_rms_norm_f32(const float *x, const float *w, size_t n, double eps, float *out);
+void orc_rope_rotate(float *v, size_t n, size_t hd, size_t pos, double theta);
+void orc_gqa_attention_scalar(const float *qh, const float *kc, const float *vc, size_t n_heads,
+                              size_t n_kv, size_t hd, size_t pos, float *out, float *scratch);
+
+#ifdef __cplusplus
+}
+#endif
 
 #endif

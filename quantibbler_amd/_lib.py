@@ -67,7 +67,12 @@ _SIGS = {
     "qbk_attention_sage_decode": (_I, [_P, C.POINTER(AttnShape), _P, _Z, _P, _Z, _P, _Z, _Z, _P, _Z]),
     "qbk_sage_decode_workspace_size": (_Z, [C.POINTER(AttnShape), _Z]),
     "qbk_attention_sage_decode_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _Z, _P, _P, _Z, _P]),
-    "qbk_block_create": (_I, [_P, _P, _P, _P, _Z, _Z, _Z, C.c_double, C.c_double, _Z, _Z, _P]),
+    "qbk_block_create": (_I, [_P, _P, _P, _Z, _P, _Z, _P, _P, _Z, _Z, _Z, _Z, C.c_double, C.c_double, _Z, _Z,
+                              _P]),
+    "qbk_embed": (_I, [_P, _P, _Z, _Z, _P, _Z, _P, _P]),
+    "qbk_embed_dev": (_I, [_P, _P, _Z, _Z, _P, _Z, _P, _P]),
+    "qbk_rms_norm_dev": (_I, [_P, _P, _Z, _Z, _P, C.c_double, _P, _P]),
+    "qbk_argmax_dev": (_I, [_P, _P, _Z, _Z, _P, _P]),
     "qbk_block_destroy": (None, [_P]),
     "qbk_block_decode_dev": (_I, [_P, _P, _P, _Z, _P]),
     "qbk_block_reset": (_I, [_P]),

@@ -5,6 +5,7 @@
 //
 //   x  = bf16(rmsnorm(bf16(h)) * w_in)                 (:837-852, :1154-1166)
 //   q, k, v = apply_bf16(x)                             (:901-906)
+//   q, k per-head RMSNorm when the block has q/k norms  (:907-910, :854-876)
 //   q, k rotated by RoPE at position pos                (:911-912, :1169-1187)
 //   k, v appended to the block's cache                  (:913)
 //   a  = attention of q over the cache's pos + 1 rows   (:918)
@@ -22,7 +23,7 @@
 // norm's sum of squares is a tree (the reference's is one 4096-long chain)
 // and exp is the device's.  The block is checked against the oracle's
 // restatement to a stated tolerance; its parts that are bit-exact stay so.
-// No per-head q/k norms (Llama-style blocks).
+// The per-head q/k norms (Qwen-style blocks) are optional.
 #include <math.h>
 #include <string.h>
 
@@ -39,6 +40,7 @@ struct qbk_block {
     const qbk_factor *o, *down;
     qbk_factor_set *qkv, *gu;
     float *w_in, *w_post;     // d each
+    float *w_q, *w_k;         // head_dim each, or null (no per-head q/k norms)
     float2 *rope;             // [cap][hd / 2] (cos, sin) in f32, from f64
     float *kc, *vc;           // [cap][Hk * hd] the block's KV cache
     void *state;              // the attention's kept decode state
@@ -93,28 +95,48 @@ __global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm(const float *a, c
     }
 }
 
-// RoPE (rotate_half pairs (i, i + hd/2)) of q and k at position pos, q to
-// qrot, k and v to cache row pos; qkv = [q (H hd) | k (Hk hd) | v (Hk hd)]
-__global__ void blkd_rope_append(const float *qkv, const float2 *rope, size_t pos, float *qrot, float *kc,
-                                 float *vc, int H, int Hk, int hd) {
-    const int half = hd / 2;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    const int nq = H * half, nk = Hk * half;
-    const float2 cs = rope[pos * (size_t)half + (i < nq ? i % half : (i - nq) % half)];
-    if (i < nq) {
-        const int head = i / half, j = i % half, base = head * hd;
-        const float a = qkv[base + j], b = qkv[base + half + j];
-        qrot[base + j] = a * cs.x - b * cs.y;
-        qrot[base + half + j] = b * cs.x + a * cs.y;
-    } else if (i < nq + nk) {
-        const int t = i - nq, head = t / half, j = t % half, base = head * hd;
-        const float *k = qkv + (size_t)H * hd, *v = k + (size_t)Hk * hd;
-        float *kr = kc + pos * (size_t)Hk * hd, *vr = vc + pos * (size_t)Hk * hd;
-        const float a = k[base + j], b = k[base + half + j];
-        kr[base + j] = a * cs.x - b * cs.y;
-        kr[base + half + j] = b * cs.x + a * cs.y;
-        vr[base + j] = v[base + j];
-        vr[base + half + j] = v[base + half + j];
+// Per-head RMSNorm (optional) and RoPE of q and k at position pos: one wave
+// per head, q heads first, then k heads (which also copy their v head to
+// the cache).  qkv = [q (H hd) | k (Hk hd) | v (Hk hd)] as the projections
+// wrote them; q goes to qrot, k and v to cache row pos.  The norm is
+// norm_apply at bf16 serving over one head (engine/mod.rs:854-876): the
+// head's values rounded to bf16, their mean square (a tree here), then
+// bf16(v * inv * w).  RoPE pairs (i, i + hd/2) (engine/mod.rs:1169-1187).
+__global__ void __launch_bounds__(64) blkd_qk_rope(const float *qkv, const float2 *rope, size_t pos,
+                                                   const float *wq, const float *wk, float eps, float *qrot,
+                                                   float *kc, float *vc, int H, int Hk, int hd) {
+    const int head = blockIdx.x, lane = threadIdx.x, half = hd / 2;
+    const bool is_q = head < H;
+    const int hh = is_q ? head : head - H;
+    const float *src = is_q ? qkv + (size_t)hh * hd : qkv + (size_t)H * hd + (size_t)hh * hd;
+    float *dst = is_q ? qrot + (size_t)hh * hd : kc + pos * (size_t)Hk * hd + (size_t)hh * hd;
+    const float *w = is_q ? wq : wk;
+    float inv = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int j = lane; j < hd; j += 64) {
+            const float b = bf16_to_f32(f32_to_bf16(src[j]));
+            ss += b * b;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    }
+    const float2 *cs = rope + pos * (size_t)half;
+    for (int j = lane; j < half; j += 64) {
+        float a = src[j], b = src[j + half];
+        if (w) {
+            a = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(a)) * inv * w[j]));
+            b = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(b)) * inv * w[j + half]));
+        }
+        const float2 c = cs[j];
+        dst[j] = a * c.x - b * c.y;
+        dst[j + half] = b * c.x + a * c.y;
+    }
+    if (!is_q) {
+        const float *v = qkv + (size_t)(H + Hk) * hd + (size_t)hh * hd;
+        float *vr = vc + pos * (size_t)Hk * hd + (size_t)hh * hd;
+        for (int j = lane; j < hd; j += 64) vr[j] = v[j];
     }
 }
 
@@ -149,11 +171,14 @@ void qbk_block_destroy(qbk_block *B) {
 }
 
 int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float *input_norm,
-                     const float *post_norm, size_t n_heads, size_t n_kv_heads, size_t head_dim,
-                     double rope_theta, double rms_norm_eps, size_t capacity, size_t block_size,
-                     qbk_block **out) {
+                     size_t input_norm_len, const float *post_norm, size_t post_norm_len, const float *q_norm,
+                     const float *k_norm, size_t qk_norm_len, size_t n_heads, size_t n_kv_heads,
+                     size_t head_dim, double rope_theta, double rms_norm_eps, size_t capacity,
+                     size_t block_size, qbk_block **out) {
     int rc;
     if (!layers || !input_norm || !post_norm || !out) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (!q_norm != !k_norm)
+        return fail(QBK_ERR_VALIDATION, "decoder block: q_norm and k_norm come together or not at all");
     for (int i = 0; i < 7; i++)
         if (!layers[i]) return fail(QBK_ERR_VALIDATION, "null layer");
     size_t dims[7][3];
@@ -168,6 +193,12 @@ int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float 
         if (dims[i][0] != want[i][0] || dims[i][1] != want[i][1])
             return fail(QBK_ERR_VALIDATION, fmt("decoder block: %s is %zux%zu, expected %zux%zu", names[i],
                                                 dims[i][0], dims[i][1], want[i][0], want[i][1]));
+    if (input_norm_len != d || post_norm_len != d)
+        return fail(QBK_ERR_VALIDATION, fmt("decoder block: norm weights of %zu and %zu floats; d_model is %zu",
+                                            input_norm_len, post_norm_len, d));
+    if (q_norm && qk_norm_len != hd)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("decoder block: q/k norm weights of %zu floats; head_dim is %zu", qk_norm_len, hd));
     if (capacity == 0 || block_size == 0) return fail(QBK_ERR_VALIDATION, "decoder block needs a capacity and a block size");
     if ((rc = bind(ctx))) return rc;
     qbk_block *B = new qbk_block();
@@ -194,6 +225,7 @@ int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float 
     const size_t kv = capacity * Hk * hd * 4;
     if ((rc = qbk_factor_set_create(ctx, qkv, 3, &B->qkv)) || (rc = qbk_factor_set_create(ctx, gu, 2, &B->gu)) ||
         (rc = alloc((void **)&B->w_in, d * 4)) || (rc = alloc((void **)&B->w_post, d * 4)) ||
+        (q_norm && ((rc = alloc((void **)&B->w_q, hd * 4)) || (rc = alloc((void **)&B->w_k, hd * 4)))) ||
         (rc = alloc((void **)&B->rope, capacity * (hd / 2) * 8)) || (rc = alloc((void **)&B->kc, kv)) ||
         (rc = alloc((void **)&B->vc, kv)) || (rc = alloc(&B->state, B->state_bytes)) ||
         (rc = alloc((void **)&B->xcat, 3 * d * 2)) ||
@@ -224,6 +256,8 @@ int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float 
     hipError_t e = hipMemcpy(B->rope, tab.data(), tab.size() * 8, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(B->w_in, input_norm, d * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(B->w_post, post_norm, d * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && q_norm) e = hipMemcpy(B->w_q, q_norm, hd * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && k_norm) e = hipMemcpy(B->w_k, k_norm, hd * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         qbk_block_destroy(B);
         return fail(QBK_ERR_DEVICE, fmt("hipMemcpy: %s", hipGetErrorString(e)));
@@ -244,6 +278,9 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     if (!B || !h) return fail(QBK_ERR_VALIDATION, "null argument");
     if (pos >= B->cap)
         return fail(QBK_ERR_VALIDATION, fmt("position %zu is past the block's cache capacity of %zu", pos, B->cap));
+    if (pos > B->tokens)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("position %zu skips cache rows: the block holds %zu positions", pos, B->tokens));
     if ((rc = bind(ctx))) return rc;
     if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
     hipStream_t s = (hipStream_t)stream;
@@ -253,9 +290,8 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
                        (float *)nullptr, B->w_in, B->eps, B->xcat, 3, d);
     QBK_HIP(hipGetLastError());
     if ((rc = q4_set_run(B->qkv, B->xcat, false, B->ycat, false, B->ws, s))) return rc;
-    const int nr = (H + Hk) * (hd / 2);
-    hipLaunchKernelGGL(blkd_rope_append, dim3((nr + 255) / 256), dim3(256), 0, s, B->ycat, B->rope, pos, B->qrot,
-                       B->kc, B->vc, H, Hk, hd);
+    hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, B->w_q, B->w_k,
+                       B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
     QBK_HIP(hipGetLastError());
     const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos + 1, B->hd, B->hd};
     const size_t cached = B->tokens <= pos ? B->tokens : 0;

@@ -24,6 +24,8 @@
 //   * stage 2 reads t and writes y = bf16(u) * s1 + bias, u = bf16(acc).
 #include <string.h>
 
+#include <mutex>
+
 #include "factor_internal.h"
 
 namespace qbk {
@@ -449,12 +451,20 @@ size_t g32_workspace(const qbk_factor *L, size_t N) { return g32_plan(L, N).byte
 int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
             hipStream_t s) {
     const G32Plan p = g32_plan(L, N);
-    static bool lds_set = false;  // the epilogue's 68 KiB exceed the 64 KiB default
-    if (!lds_set) {
-        for (const void *k : {(const void *)g32_kernel<1, 0>, (const void *)g32_kernel<1, 1>,
-                              (const void *)g32_kernel<1, 2>, (const void *)g32_kernel<2, 0>})
-            QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
-        lds_set = true;
+    {
+        // the epilogue's 68 KiB exceed the 64 KiB default; the attribute is
+        // per device, set once on each under a lock (callers may share a ctx)
+        static std::mutex mu;
+        static uint64_t done = 0;
+        int dev = 0;
+        QBK_HIP(hipGetDevice(&dev));
+        std::lock_guard<std::mutex> lock(mu);
+        if (dev < 64 && !((done >> dev) & 1)) {
+            for (const void *k : {(const void *)g32_kernel<1, 0>, (const void *)g32_kernel<1, 1>,
+                                  (const void *)g32_kernel<1, 2>, (const void *)g32_kernel<2, 0>})
+                QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
+            done |= 1ull << dev;
+        }
     }
     char *w = (char *)ws;
     uint16_t *z = (uint16_t *)(w + p.o_z), *t = (uint16_t *)(w + p.o_t);

@@ -217,6 +217,32 @@ class GpuContext:
                                                     _ptr(vh), _stream(stream)))
 
 
+def embed(ctx: GpuContext, table, vocab: int, d_model: int, tokens, out, stream=None):
+    """engine/mod.rs:768-778 Engine::embed: host token ids (validated with the
+    reference's text) -> f32 rows of the device table into ``out``."""
+    t = np.ascontiguousarray(tokens, np.int32).ravel()
+    check(_lib.load().qbk_embed(ctx.handle, _ptr(table), int(vocab), int(d_model), _ptr(t), t.size, _ptr(out),
+                                _stream(stream)))
+
+
+def embed_dev(ctx: GpuContext, table, vocab: int, d_model: int, tokens, n: int, out, stream=None):
+    """Device token ids (int32); an out-of-range id yields a NaN row."""
+    check(_lib.load().qbk_embed_dev(ctx.handle, _ptr(table), int(vocab), int(d_model), _ptr(tokens), int(n),
+                                    _ptr(out), _stream(stream)))
+
+
+def rms_norm_dev(ctx: GpuContext, x, rows: int, d: int, w, eps: float, out, stream=None):
+    """The final norm (engine/mod.rs:943) at bf16 serving, per row."""
+    check(_lib.load().qbk_rms_norm_dev(ctx.handle, _ptr(x), int(rows), int(d), _ptr(w), float(eps), _ptr(out),
+                                       _stream(stream)))
+
+
+def argmax_dev(ctx: GpuContext, logits, rows: int, vocab: int, out, stream=None):
+    """sampler.rs:4-15 greedy, per row (int32 ids into ``out``)."""
+    check(_lib.load().qbk_argmax_dev(ctx.handle, _ptr(logits), int(rows), int(vocab), _ptr(out),
+                                     _stream(stream)))
+
+
 class SageDecodeState:
     """A decode loop's attention state for one layer (engine/mod.rs:984-1030
     gqa_attention_sage, called once per generated token over a growing
@@ -267,31 +293,49 @@ class SageDecodeState:
 class DecoderBlock:
     """One decoder block of the server's transformer at one position
     (engine/mod.rs:878-945; bf16 serving, the sage decode attention on a
-    kept state): norm -> q/k/v -> RoPE -> cache append -> attention -> o +
-    residual -> norm -> gate/up -> SwiGLU -> down + residual, on the device.
-    ``layers`` are the seven FactorLayers q, k, v, o, gate, up, down (kept
-    alive here); the block owns its KV cache of ``capacity`` rows."""
+    kept state): norm -> q/k/v -> [per-head q/k norms] -> RoPE -> cache
+    append -> attention -> o + residual -> norm -> gate/up -> SwiGLU ->
+    down + residual, on the device.  ``layers`` are the seven FactorLayers
+    q, k, v, o, gate, up, down (kept alive here); ``q_norm``/``k_norm`` are
+    optional head_dim weights; the block owns its KV cache of ``capacity``
+    rows."""
 
     def __init__(self, ctx: GpuContext, layers, input_norm, post_norm, n_heads: int,
                  n_kv_heads: int, head_dim: int, rope_theta: float, rms_norm_eps: float,
-                 capacity: int, block_size: int = 64):
+                 capacity: int, block_size: int = 64, q_norm=None, k_norm=None):
         if len(layers) != 7:
             raise _lib.KernelError("a decoder block takes 7 layers: q, k, v, o, gate, up, down")
         self.ctx = ctx
         self.layers = list(layers)
+        self.d_model = self.layers[3].dout
         arr = (C.c_void_p * 7)(*[L.handle for L in self.layers])
-        w_in = np.ascontiguousarray(input_norm, np.float32)
-        w_post = np.ascontiguousarray(post_norm, np.float32)
+        w_in = np.ascontiguousarray(input_norm, np.float32).ravel()
+        w_post = np.ascontiguousarray(post_norm, np.float32).ravel()
+        wq = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32).ravel()
+        wk = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32).ravel()
+        qk_len = 0 if wq is None else wq.size
+        if wq is not None and wk is not None and wk.size != wq.size:
+            raise _lib.KernelError(f"decoder block: q/k norm weights of {wq.size} and {wk.size} floats differ")
         out = C.c_void_p()
-        check(_lib.load().qbk_block_create(ctx.handle, arr, _ptr(w_in), _ptr(w_post), int(n_heads),
-                                           int(n_kv_heads), int(head_dim), float(rope_theta),
-                                           float(rms_norm_eps), int(capacity), int(block_size),
-                                           C.byref(out)))
+        check(_lib.load().qbk_block_create(ctx.handle, arr, _ptr(w_in), w_in.size, _ptr(w_post), w_post.size,
+                                           _ptr(wq), _ptr(wk), qk_len, int(n_heads), int(n_kv_heads),
+                                           int(head_dim), float(rope_theta), float(rms_norm_eps),
+                                           int(capacity), int(block_size), C.byref(out)))
         self._h = out
         self.capacity = int(capacity)
 
     def decode_dev(self, h, pos: int, stream=None):
-        """h: device f32 [d_model], replaced by the block's output at position pos."""
+        """h: device f32 [d_model] (a contiguous torch tensor, or a raw device
+        address the caller vouches for), replaced by the block's output at
+        position pos."""
+        if hasattr(h, "is_cuda"):
+            if not h.is_cuda or str(h.dtype) != "torch.float32" or not h.is_contiguous() \
+                    or h.numel() != self.d_model:
+                raise _lib.KernelError(
+                    f"decoder block input must be a contiguous float32 device tensor of {self.d_model} "
+                    f"values; got {h.dtype} of {h.numel()} on {h.device}")
+        elif not isinstance(h, int):
+            raise _lib.KernelError("decoder block input must be a device tensor or a device address")
         check(_lib.load().qbk_block_decode_dev(self.ctx.handle, self._h, _ptr(h), int(pos),
                                                _stream(stream)))
 
@@ -302,6 +346,10 @@ class DecoderBlock:
         k, v = C.c_void_p(), C.c_void_p()
         check(_lib.load().qbk_block_cache(self._h, C.byref(k), C.byref(v)))
         return k.value, v.value
+
+    @property
+    def handle(self):
+        return self._h
 
     def close(self):
         if self._h:

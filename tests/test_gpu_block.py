@@ -43,20 +43,25 @@ def metrics(got, want):
     return cos, rel
 
 
-def test_decoder_block_matches_oracle(ctx, orc):
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_decoder_block_matches_oracle(ctx, orc, qk_norm):
     from quantibbler_amd import DecoderBlock, FactorLayer
 
     d, H, Hk, hd, ffn, cap, blk = 256, 4, 2, 64, 512, 40, 16
     theta, eps = 500000.0, 1e-5
-    rng = np.random.default_rng(17)
+    rng = np.random.default_rng(17 + qk_norm)
     shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
               (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
     layers = [scaled_layer(orc, rng, *s) for s in shapes]
     devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
                                   L["bias"]) for L in layers]
-    w_in = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
-    w_post = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
-    block = DecoderBlock(ctx, devs, w_in, w_post, H, Hk, hd, theta, eps, cap, blk)
+    bfv = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a.astype(np.float32)))
+    norms = {"input": bfv(1.0 + 0.1 * rng.standard_normal(d)), "post_attention": bfv(1.0 + 0.1 * rng.standard_normal(d))}
+    if qk_norm:
+        norms["q_norm"] = bfv(1.0 + 0.2 * rng.standard_normal(hd))
+        norms["k_norm"] = bfv(1.0 + 0.2 * rng.standard_normal(hd))
+    block = DecoderBlock(ctx, devs, norms["input"], norms["post_attention"], H, Hk, hd, theta, eps, cap, blk,
+                         norms.get("q_norm"), norms.get("k_norm"))
     kc = np.zeros((cap, Hk * hd), np.float32)
     vc = np.zeros((cap, Hk * hd), np.float32)
     assert all(block.cache_ptrs())
@@ -67,7 +72,7 @@ def test_decoder_block_matches_oracle(ctx, orc):
         hd_dev = torch.from_numpy(h).cuda()
         block.decode_dev(hd_dev, pos, st)
         torch.cuda.synchronize()
-        want = orc.block_decode(layers, w_in, w_post, h, pos, kc, vc, H, Hk, hd, theta, eps, blk)
+        want = orc.block_step(layers, norms, h, pos, kc, vc, H, Hk, hd, theta, eps, "bf16", "sage", blk)
         got = hd_dev.cpu().numpy()
         cos, rel = metrics(got, want)
         print(f"pos {pos}: out cos {cos:.7f} rel {rel:.2e}", flush=True)
@@ -92,8 +97,26 @@ def test_decoder_block_validation(ctx, orc):
         DecoderBlock(ctx, [devs[0], devs[0]] + devs[2:], w, w, H, Hk, hd, 1e4, 1e-5, 16)
     with pytest.raises(KernelError, match="n_kv_heads dividing n_heads"):
         DecoderBlock(ctx, devs, w, w, 3, 2, hd, 1e4, 1e-5, 16)
+    with pytest.raises(KernelError, match="norm weights of 127 and 128 floats; d_model is 128"):
+        DecoderBlock(ctx, devs, w[:127], w, H, Hk, hd, 1e4, 1e-5, 16)
+    with pytest.raises(KernelError, match="q/k norm weights of 32 floats; head_dim is 64"):
+        DecoderBlock(ctx, devs, w, w, H, Hk, hd, 1e4, 1e-5, 16, 16, w[:32], w[:32])
+    with pytest.raises(KernelError, match="q_norm and k_norm come together"):
+        DecoderBlock(ctx, devs, w, w, H, Hk, hd, 1e4, 1e-5, 16, 16, w[:64], None)
     block = DecoderBlock(ctx, devs, w, w, H, Hk, hd, 1e4, 1e-5, 4, 16)
     h = torch.zeros(d, dtype=torch.float32, device="cuda")
     with pytest.raises(KernelError, match="position 4 is past the block's cache capacity of 4"):
         block.decode_dev(h, 4)
+    with pytest.raises(KernelError, match="position 2 skips cache rows: the block holds 0 positions"):
+        block.decode_dev(h, 2)
+    for bad in (torch.zeros(d, dtype=torch.float32), torch.zeros(d, dtype=torch.bfloat16, device="cuda"),
+                torch.zeros(d - 1, dtype=torch.float32, device="cuda"),
+                torch.zeros(2 * d, dtype=torch.float32, device="cuda")[::2]):
+        with pytest.raises(KernelError, match="contiguous float32 device tensor of 128 values"):
+            block.decode_dev(bad, 0)
+    block.decode_dev(h, 0)
+    block.decode_dev(h, 1)
+    block.decode_dev(h, 1)      # a rewind to position 1 is allowed
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(h).all())
     block.close()

@@ -434,3 +434,92 @@ def test_from_qpk1_matches_from_rows(ctx, orc):
     same(run_dev(a, x)[0], run_dev(b, x)[0])
     with pytest.raises(KernelError, match="trailing garbage"):
         FactorLayer.from_qpk1(ctx, stream + b"\0")
+
+
+def gpu_z(layer, ws, batch):
+    """Stage 1's fp8 operand read back from the decode workspace
+    ([op1 [slice][4][ncol][32] | sc1 [slice][4][ncol] | ...]): the value
+    hi + lo each activation z = bf16(s2*x) is fed to the MFMA as."""
+    rnd = lambda n: -(-n // 256) * 256
+    ns1, ncol = -(-layer.din // 128), 2 * batch
+    op = ws[: ns1 * 4 * ncol * 32].reshape(ns1, 4, ncol, 32)
+    sc = ws[rnd(ns1 * 4 * ncol * 32):][: ns1 * 4 * ncol].reshape(ns1, 4, ncol).astype(np.int64)
+    z = np.zeros((batch, ns1 * 128))
+    for g in range(4):
+        for e in range(32):
+            gb, byte, k = 2 * (g & 1) + (e >> 4), 16 * (g >> 1) + (e & 15), kq4(g, e)
+            for b in range(batch):
+                hi = e4m3(op[:, gb, 2 * b, byte]) * 2.0 ** (sc[:, g, 2 * b] - 127)
+                lo = e4m3(op[:, gb, 2 * b + 1, byte]) * 2.0 ** (sc[:, g, 2 * b + 1] - 127)
+                z[b, np.arange(ns1) * 128 + k] = hi + lo
+    return z[:, :layer.din]
+
+
+def test_decode_fp8_split_tail(ctx, orc):
+    """The decode GEMV feeds each activation z to the fp4 x fp8 MFMA as two
+    e4m3 pieces, hi + lo, each scaled by one E8M0 exponent per 32-activation
+    group (the two 16-runs MFMA lane group g covers).  Every z within 2^14
+    of its group's largest |z| is carried exactly; smaller ones can lose low
+    bits in the e4m3 subnormals, by at most 2^-21 of the group maximum (the
+    lo piece's subnormal step is 2^-9 of its scale, which is at most 2^-7 of
+    the largest residual, itself at most 2^-4 of the group maximum).  Groups
+    built here: one element 2^10, the others 2^-8 .. 2^2 with full 8-bit
+    mantissas, some zero."""
+    say("factor decode fp8 split tail")
+    rng = np.random.default_rng(4321)
+    din = 256
+    L = make_layer(orc, rng, 64, din, 64, integer=True)
+    layer = upload(ctx, L)
+    batch = 2
+    mags = 2.0 ** rng.integers(-8, 3, (batch, din)) * (1 + rng.integers(0, 128, (batch, din)) / 128.0)
+    x = (rng.choice([-1, 1], (batch, din)) * mags).astype(np.float32)
+    x[rng.random((batch, din)) < 0.05] = 0.0
+    groups = [np.concatenate([np.arange(16) + 16 * (g >> 1) + 64 * (g & 1),
+                              np.arange(16) + 16 * (g >> 1) + 64 * (g & 1) + 32]) for g in range(4)]
+    for b in range(batch):
+        for s in range(din // 128):
+            for g in range(4):
+                x[b, 128 * s + rng.choice(groups[g])] = rng.choice([-1, 1]) * 1024.0
+    xb = orc.f32_to_bf16_fast(x)
+    _, ws = run_dev(layer, xb)
+    zd = gpu_z(layer, ws, batch)
+    z = orc.bf16_to_f32(xb).astype(np.float64)
+    inexact = 0
+    for b in range(batch):
+        for s in range(din // 128):
+            for g in range(4):
+                k = 128 * s + groups[g]
+                amax = np.abs(z[b, k]).max()
+                err = np.abs(zd[b, k] - z[b, k])
+                near = np.abs(z[b, k]) >= amax * 2.0 ** -14
+                assert not err[near].any(), (b, s, g)
+                assert np.all(err <= amax * 2.0 ** -21), (b, s, g, err.max() / amax)
+                inexact += int((err > 0).sum())
+    say(f"  {inexact} of {z.size} activations below 2^-14 of their group maximum lost low bits")
+
+
+def test_decode_nonfinite_activations(ctx, orc):
+    """inf, NaN and overflow of s2*x to inf on the decode path (batch 4, one
+    clean token): the clean token stays bit-identical to the oracle; a token
+    holding a non-finite z gives NaN in every output where the reference's
+    sequential composite does (with random signs and r >= 2 every u sums
+    infinities of both signs), and the same finite values elsewhere."""
+    say("factor decode non-finite activations")
+    rng = np.random.default_rng(4322)
+    din, r, dout = 256, 64, 96
+    L = make_layer(orc, rng, dout, din, r, integer=True)
+    L["s2"][7] = np.float32(2.0 ** 120)
+    layer = upload(ctx, L)
+    x = rng.integers(-2, 3, (4, din)).astype(np.float32)
+    x[:, 7] = 0.0
+    x[0, 3] = np.inf
+    x[2, 7] = 1024.0          # s2 * x = 2^130: inf in f32 and bf16
+    x[3, 100] = np.nan
+    xb = orc.f32_to_bf16_fast(x)
+    xb[1, 7] = 0x3F80          # the clean token: z_7 = 2^120, a finite term that swamps the rest
+    want = orc.factor_apply_bf16_batch(dout, din, r, L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], xb)
+    got, _ = run_dev(layer, xb)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    same(got[fin], want[fin], "finite outputs")
+    assert np.isnan(want[[0, 2, 3]]).all() and np.isfinite(want[1]).all()

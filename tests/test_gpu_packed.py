@@ -101,3 +101,39 @@ def test_pyo3_face_on_gpu(orc):
     same(K.packed_matmul(p, 13, m), orc.packed_matmul(p, 6, 13, m, 4))
     vb = orc.f32_to_bf16_fast(v.astype(np.float32))
     same(K.packed_matvec_dtype(p, 13, vb, "bfloat16"), orc.packed_matvec(p, 6, 13, vb, "bfloat16"))
+
+
+def test_host_bit_layout_on_the_gpu_box(orc):
+    """core.rs:129-189 pack_bits / unpack_bits and sign_estimate through the
+    product library, in the GPU job: byte-identical to the reference's
+    pack_bits.json records (including the 16x16 bit-order record and the
+    empty shapes) and sign_estimate.json, and to the oracle on random shapes."""
+    from conftest import load_golden
+
+    from quantibbler_amd import kernels as K
+
+    say("host bit layout (A1/A2) vs fixtures")
+    for rec in load_golden("pack_bits.json"):
+        exp = rec["faces"]["numpy-reference"]
+        nb = rec["dtypes"]["n_bits"]
+        factor = np.array(rec["inputs"]["factor"], dtype=np.int8)
+        if "shape" in rec["inputs"]:
+            factor = factor.reshape(rec["inputs"]["shape"])
+        rows = factor.shape[0] if factor.ndim == 2 else 0
+        f = factor.reshape(rows, nb)
+        p = K.pack_bits(f) if rows else np.zeros((0, (nb + 7) // 8), np.uint8)
+        assert p.tolist() == np.array(exp["packed"], np.uint8).reshape(p.shape).tolist(), rec["scenario"]
+        assert p.tobytes() == orc.pack_bits(f).tobytes() if rows else True
+        if "unpacked" in exp:
+            assert K.unpack_bits(p, nb, "int8").tolist() == exp["unpacked"], rec["scenario"]
+        if "expected_bytes" in exp:
+            assert p.ravel().tolist() == np.array(exp["expected_bytes"]).ravel().tolist()
+    for rec in load_golden("sign_estimate.json"):
+        x = np.array(rec["inputs"]["x"], np.float64)
+        assert K.sign_estimate(x).ravel().tolist() == rec["faces"]["numpy-reference"]["signs"], rec["scenario"]
+    rng = np.random.default_rng(22)
+    for rows, cols in [(5, 11), (3, 64), (7, 1), (1, 129), (33, 1000)]:
+        f = rng.choice([-1, 1], (rows, cols)).astype(np.int8)
+        p = K.pack_bits(f)
+        assert p.tobytes() == orc.pack_bits(f).tobytes()
+        assert K.unpack_bits(p, cols, "float64").tolist() == f.astype(np.float64).tolist()

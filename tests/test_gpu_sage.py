@@ -309,3 +309,39 @@ def test_blk_attention_config4_full_size_quality(ctx):
         cos_min, rl1_max = min(cos_min, c), max(rl1_max, r)
     say("  cos_min", cos_min, "rl1_max", rl1_max)
     assert cos_min >= COS_MIN and rl1_max <= RL1_MAX, (cos_min, rl1_max)
+
+
+def test_blk_attention_closed_forms(ctx, orc):
+    """Cases whose block-scaled output is fixed by the mathematics, not by the
+    oracle: (i) every key equal -> every score 0, p = 1, row i = mean of V
+    over keys 0..i; (ii) one key scoring more than 150 (log2 units) above the
+    rest -> every other p underflows, the output row is that key's V row
+    exactly (rows from it on; causal rows of the first key block are case
+    (i) again)."""
+    say("sage blk closed forms")
+    rng = np.random.default_rng(9330)
+    s = 192
+    q = rng.standard_normal((1, 2, s, 128)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, 1, 1, 128)).astype(np.float32), s, axis=2)
+    v = rng.standard_normal((1, 1, s, 128)).astype(np.float32)
+    qb, kb, vb = (orc.f32_to_bf16_fast(a) for a in (q, k, v))
+    vf = orc.bf16_to_f32(vb).astype(np.float64)[0, 0]
+    for causal in (True, False):
+        got = orc.bf16_to_f32(run_blk(ctx, qb, kb, vb, causal)).astype(np.float64)
+        mean = (np.cumsum(vf, axis=0) / np.arange(1, s + 1)[:, None]) if causal else \
+            np.broadcast_to(vf.mean(axis=0), (s, 128))
+        for h in range(2):
+            assert np.all(np.abs(got[0, h] - mean) <= 2 ** -8 * np.abs(mean) + 1e-6), (causal, h)
+    star = 150
+    q = np.zeros((1, 1, s, 128), np.float32)
+    q[..., 0] = 64.0
+    k = np.zeros((1, 1, s, 128), np.float32)
+    k[0, 0, :, 0] = -1.0
+    k[0, 0, star, 0] = 60.0
+    qb, kb = orc.f32_to_bf16_fast(q), orc.f32_to_bf16_fast(k)
+    got = orc.bf16_to_f32(run_blk(ctx, qb, kb, vb[:, :1], False))[0, 0]
+    assert np.array_equal(got, np.broadcast_to(orc.bf16_to_f32(vb)[0, 0, star], (s, 128)))
+    got = orc.bf16_to_f32(run_blk(ctx, qb, kb, vb[:, :1], True))[0, 0].astype(np.float64)
+    assert np.array_equal(got[star:], np.broadcast_to(vf[star], (s - star, 128)))
+    mean = np.cumsum(vf, axis=0) / np.arange(1, s + 1)[:, None]
+    assert np.all(np.abs(got[:64] - mean[:64]) <= 2 ** -8 * np.abs(mean[:64]) + 1e-6)

@@ -1,0 +1,155 @@
+"""GPU checks of the trunk around the decoder blocks and of the whole device
+trunk on the reference's parity-tiny model:
+
+* embedding lookup (engine/mod.rs:768-778): rows bit-identical to the table;
+  the host form refuses an out-of-range id with the reference's text, the
+  device form poisons that row with NaN;
+* the final norm (engine/mod.rs:943, norm_apply at bf16 serving): within one
+  bf16 ulp of the oracle (its sum of squares is a tree on the device);
+* greedy argmax (sampler.rs:4-15): first maximum, NaN never wins, 0 when
+  nothing beats -inf -- bit-exact on the edge cases;
+* DeviceModel (embedding -> 2 blocks with q/k norms -> final norm -> lm_head
+  on the device, bf16 serving, sage decode attention) on
+  tests/fixtures/parity-tiny: every position's logits within the reference's
+  1e-2 budget of the HF goldens (crates/quantibbler-server/tests/
+  parity_tiny.rs:25-100), and close to the oracle's trunk in the same
+  configuration.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+TINY = os.path.join(GOLDEN, "parity_tiny")
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from quantibbler_amd import GpuContext
+
+    return GpuContext(0)
+
+
+def test_embed_host_and_device(ctx):
+    from quantibbler_amd import KernelError
+    from quantibbler_amd.gpu import embed, embed_dev
+
+    say("trunk embed")
+    rng = np.random.default_rng(5)
+    vocab, d = 300, 96
+    table = rng.standard_normal((vocab, d)).astype(np.float32)
+    td = torch.from_numpy(table).cuda()
+    ids = np.array([0, 299, 17, 17, 5], np.int32)
+    out = torch.empty((5, d), dtype=torch.float32, device="cuda")
+    embed(ctx, td, vocab, d, ids, out)
+    assert np.array_equal(out.cpu().numpy(), table[ids])
+    with pytest.raises(KernelError, match=r"token id 300 is outside the vocabulary \(size 300\)"):
+        embed(ctx, td, vocab, d, np.array([1, 300], np.int32), out)
+    idd = torch.tensor([3, -1, 400, 299], dtype=torch.int32, device="cuda")
+    out4 = torch.empty((4, d), dtype=torch.float32, device="cuda")
+    embed_dev(ctx, td, vocab, d, idd, 4, out4, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    o = out4.cpu().numpy()
+    assert np.array_equal(o[0], table[3]) and np.array_equal(o[3], table[299])
+    assert np.isnan(o[1]).all() and np.isnan(o[2]).all()
+
+
+def test_final_norm_against_oracle(ctx, orc):
+    from quantibbler_amd.gpu import rms_norm_dev
+
+    say("trunk final norm")
+    rng = np.random.default_rng(6)
+    for d in (64, 4096, 4099):
+        x = (3 * rng.standard_normal((3, d))).astype(np.float32)
+        w = orc.bf16_to_f32(orc.f32_to_bf16((1 + 0.1 * rng.standard_normal(d)).astype(np.float32)))
+        xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+        od = torch.empty_like(xd)
+        rms_norm_dev(ctx, xd, 3, d, wd, 1e-5, od, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        got = od.cpu().numpy()
+        for r in range(3):
+            want = orc.norm_apply(x[r], w, 1e-5, "bf16")
+            assert np.array_equal(orc.bf16_to_f32(orc.f32_to_bf16(got[r])), got[r])   # bf16 values
+            ulp = np.spacing(np.abs(want).astype(np.float32)) * 2 ** 16
+            assert np.all(np.abs(got[r] - want) <= ulp), (d, r)
+
+
+def greedy(row):
+    best, best_v = 0, -np.inf
+    for i, v in enumerate(row):
+        if v > best_v:
+            best, best_v = i, v
+    return best
+
+
+def test_argmax_first_max_rule(ctx):
+    from quantibbler_amd.gpu import argmax_dev
+
+    say("trunk argmax")
+    rng = np.random.default_rng(7)
+    vocab = 1000
+    rows = [rng.standard_normal(vocab).astype(np.float32) for _ in range(4)]
+    r = rng.integers(-3, 3, vocab).astype(np.float32)          # many ties at the max
+    rows.append(r)
+    r = np.full(vocab, -np.inf, np.float32)                      # nothing beats -inf
+    rows.append(r)
+    r = np.full(vocab, np.nan, np.float32)
+    r[[10, 900]] = 2.0                                            # NaN never wins; first of ties
+    rows.append(r)
+    r = rng.standard_normal(vocab).astype(np.float32)
+    r[0] = np.nan
+    r[999] = 50.0
+    rows.append(r)
+    x = np.stack(rows)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty(len(rows), dtype=torch.int32, device="cuda")
+    argmax_dev(ctx, xd, len(rows), vocab, out, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert out.cpu().numpy().tolist() == [greedy(row) for row in rows]
+
+
+@pytest.fixture(scope="module")
+def md():
+    from quantibbler_amd.model import ModelDir
+
+    return ModelDir.load(TINY)
+
+
+def test_device_trunk_parity_tiny_goldens(ctx, orc, md):
+    from quantibbler_amd.model import DeviceModel
+
+    say("device trunk on parity-tiny")
+    with open(os.path.join(TINY, "goldens.json")) as f:
+        g = json.load(f)
+    ids = g["input_ids"]
+    m = DeviceModel(ctx, md, capacity=16)
+    ref = orc.Trunk(md, serving="bf16", attention="sage", capacity=16)
+    worst_gold, worst_orc = 0.0, 0.0
+    for pos, tok in enumerate(ids):
+        logits = m.step(tok, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        got = logits.cpu().numpy()
+        want = ref.step(tok)
+        gold = np.array(g["logits"][pos], np.float32)
+        worst_gold = max(worst_gold, float(np.abs(got - gold).max()))
+        worst_orc = max(worst_orc, float(np.abs(got - want).max()))
+        say(f"  pos {pos}: |device - HF| {np.abs(got - gold).max():.3g}  |device - oracle| "
+            f"{np.abs(got - want).max():.3g}")
+    assert worst_gold <= 1e-2, worst_gold
+    assert worst_orc <= 2e-3, worst_orc
+    # a fresh sequence after reset reproduces the first position
+    m.reset()
+    again = m.step(ids[0], torch.cuda.current_stream()).cpu().numpy()
+    ref0 = orc.Trunk(md, serving="bf16", attention="sage", capacity=16).step(ids[0])
+    assert np.abs(again - ref0).max() <= 2e-3
+    m.close()

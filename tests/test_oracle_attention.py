@@ -187,3 +187,118 @@ def test_sage_blk_mean_shift_invariance(orc):
     o2 = orc.attention_sage_blk(qb, kb2, vb, causal=True)
     cos, rl1 = metrics(o1, o2)
     assert cos > 0.9999 and rl1 < 5e-3
+
+
+# ---- block-scaled scheme: closed forms a plausible mistake would fail --------
+
+def _f32(a):
+    return np.asarray(a, np.float32)
+
+
+def _codes(x, peak):
+    """INT8 codes of x at one block's peak, in the f32 order the scheme fixes:
+    invs = 127 / peak, rint(x * invs) half-even, clamped to +-127."""
+    invs = np.float32(127.0) / np.float32(peak) if peak > 0 else np.float32(0.0)
+    return np.clip(np.rint(_f32(x) * invs), -127, 127).astype(np.int8)
+
+
+@pytest.mark.parametrize("s", [64, 200])
+def test_sage_blk_q_and_k_codes_closed_form(orc, s):
+    """Q: one scale per 64-token block per head, taken over exactly tokens
+    64b .. 64b+63 of x = q * (1/sqrt(d)) (f32), scale = peak / 127, codes by
+    round-half-even.  K: the same over g = k - mean.  A per-token scale, a
+    block window off by one token, or truncating codes all fail here."""
+    rng = np.random.default_rng(9300 + s)
+    q, k, v = _blk_inputs(rng, 1, 4, 2, s)
+    # vary each token's magnitude so that a per-token scale would differ
+    q *= np.exp(rng.standard_normal((1, 4, s, 1))).astype(np.float32)
+    qb, kb, vb = (orc.f32_to_bf16_fast(a) for a in (q, k, v))
+    _, st = orc.attention_sage_blk(qb, kb, vb, causal=True, stages=True)
+    inv_sqrt_d = np.float32(1.0) / np.sqrt(np.float32(128.0))
+    x = _f32(orc.bf16_to_f32(qb)) * inv_sqrt_d
+    g = _f32(orc.bf16_to_f32(kb)) - st["kmean"][:, :, None, :]
+    nblk = (s + 63) // 64
+    for h in range(4):
+        for blk in range(nblk):
+            sl = slice(64 * blk, min(64 * blk + 64, s))
+            peak = np.abs(x[0, h, sl]).max()
+            assert st["qscale"][0, h, blk] == np.float32(peak) / np.float32(127.0)
+            assert np.array_equal(st["qhat"][0, h, sl], _codes(x[0, h, sl], peak)), (h, blk)
+    for hk in range(2):
+        for blk in range(nblk):
+            sl = slice(64 * blk, min(64 * blk + 64, s))
+            peak = np.abs(g[0, hk, sl]).max()
+            assert st["kscale"][0, hk, blk] == np.float32(peak) / np.float32(127.0)
+            assert np.array_equal(st["khat"][0, hk, sl], _codes(g[0, hk, sl], peak)), (hk, blk)
+    # half-even: a code from an exact .5 rounds to the even neighbour
+    assert _codes(np.array([0.5, 1.5, 2.5, -0.5], np.float32), 127.0).tolist() == [0, 2, 2, 0]
+
+
+def test_sage_blk_identical_keys_give_the_mean_of_v(orc):
+    """Every key equal: K - mean is zero, so every score is 0, p = 1 for every
+    key in the window, and row i's output is the mean of V over keys 0..i
+    (causal) -- V as the fp16 values P.V multiplies."""
+    rng = np.random.default_rng(9310)
+    s = 130
+    q = rng.standard_normal((1, 2, s, 128)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, 1, 1, 128)).astype(np.float32), s, axis=2)
+    v = rng.standard_normal((1, 1, s, 128)).astype(np.float32)
+    qb, kb, vb = (orc.f32_to_bf16_fast(a) for a in (q, k, v))
+    out = orc.attention_sage_blk(qb, kb, vb, causal=True).astype(np.float64)
+    vf = orc.bf16_to_f32(vb).astype(np.float16).astype(np.float64)[0, 0]
+    want = np.cumsum(vf, axis=0) / np.arange(1, s + 1)[:, None]
+    for h in range(2):
+        assert np.abs(out[0, h] - want).max() <= 1e-6 * np.abs(vf).max(), h
+    out_nc = orc.attention_sage_blk(qb, kb, vb, causal=False).astype(np.float64)
+    assert np.abs(out_nc[0, 0] - vf.mean(axis=0)[None, :]).max() <= 1e-6 * np.abs(vf).max()
+
+
+def test_sage_blk_one_hot_softmax_returns_that_value_row(orc):
+    """One key whose score exceeds every other by more than 150 (log2 units):
+    every other p underflows to zero in exp2, so the output row is exactly
+    that key's V row (its fp16 value; bf16 V values are fp16-exact here)."""
+    s, star = 96, 70
+    q = np.zeros((1, 1, s, 128), np.float32)
+    q[..., 0] = 64.0
+    k = np.zeros((1, 1, s, 128), np.float32)
+    k[0, 0, :, 0] = -1.0
+    k[0, 0, star, 0] = 60.0
+    rng = np.random.default_rng(9320)
+    v = rng.standard_normal((1, 1, s, 128)).astype(np.float32)
+    qb, kb, vb = (orc.f32_to_bf16_fast(a) for a in (q, k, v))
+    out = orc.attention_sage_blk(qb, kb, vb, causal=False)
+    vf = orc.bf16_to_f32(vb)[0, 0]
+    assert np.array_equal(out[0, 0], np.broadcast_to(vf[star], (s, 128)))
+    # causal: rows from the star on see it; rows of the first key block
+    # (whose keys all share one code and one scale) weigh keys 0..i alike
+    outc = orc.attention_sage_blk(qb, kb, vb, causal=True).astype(np.float64)
+    assert np.array_equal(outc[0, 0, star:], np.broadcast_to(vf[star], (s - star, 128)).astype(np.float64))
+    want = np.cumsum(vf.astype(np.float64), axis=0) / np.arange(1, s + 1)[:, None]
+    assert np.abs(outc[0, 0, :64] - want[:64]).max() <= 1e-6
+
+
+def test_sage_blk_p_is_fp16_and_ell_unquantised(orc):
+    """Two keys at scores +s0 and -s0 (codes +-127, mean 0): p0 = 1,
+    p1 = 2^(-2 s0).  With V = (0, 1) on one channel the output is
+    fp16(p1) / (1 + p1): P.V multiplies the fp16 P, the row sum l adds the
+    f32 p.  A bf16 P, an f32 P or an l over the rounded P each miss it."""
+    q = np.zeros((1, 1, 2, 128), np.float32)
+    q[..., 0] = 4.0
+    k = np.zeros((1, 1, 2, 128), np.float32)
+    k[0, 0, 0, 0], k[0, 0, 1, 0] = 1.0, -1.0
+    v = np.zeros((1, 1, 2, 128), np.float32)
+    v[0, 0, 1, 5] = 1.0
+    qb, kb, vb = (orc.f32_to_bf16_fast(a) for a in (q, k, v))
+    out, st = orc.attention_sage_blk(qb, kb, vb, causal=False, stages=True)
+    assert st["khat"][0, 0, :, 0].tolist() == [127, -127] and st["qhat"][0, 0, :, 0].tolist() == [127, 127]
+    cs = np.float32(np.float32(st["qscale"][0, 0, 0] * st["kscale"][0, 0, 0]) * np.float32(1.4426950408889634))
+    s0 = np.float32(np.float32(127 * 127) * cs)
+    p1 = float(np.exp2(np.float64(np.float32(-s0) - s0)))
+    assert 0.3 < p1 < 0.7
+    want = float(np.float16(p1)) / (1.0 + p1)
+    got = float(out[0, 0, 0, 5])
+    assert abs(got - want) <= 4e-7 * want, (got, want)
+    bf16_p = float(orc.bf16_to_f32(orc.f32_to_bf16(np.array([p1], np.float32)))[0])
+    assert abs(bf16_p / (1 + p1) - want) > 100 * 4e-7 * want
+    assert abs(p1 / (1 + p1) - want) > 100 * 4e-7 * want
+    assert abs(float(np.float16(p1)) / (1 + float(np.float16(p1))) - want) > 100 * 4e-7 * want
