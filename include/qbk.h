@@ -127,6 +127,18 @@ size_t qbk_factor_workspace_size(const qbk_factor *layer, size_t batch);
 int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *layer, const uint16_t *x, size_t batch,
                           void *y, int y_dtype, void *workspace, size_t workspace_size,
                           void *stream);
+/* No counterpart in the reference: qbk_factor_linear_dev for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * or harnesses that forbid hipMalloc).  It allocates nothing: the workspace
+ * is a file-scope device array of QBK_NOALLOC_SCRATCH_BYTES (32 MiB) that
+ * each GPU the library runs on holds until the process ends.  A call whose
+ * workspace (qbk_factor_workspace_size) exceeds that is refused with a
+ * validation error.  Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU race, so order them (one stream).  Same
+ * arithmetic and results as qbk_factor_linear_dev. */
+#define QBK_NOALLOC_SCRATCH_BYTES (32u << 20)
+int qbk_factor_linear_noalloc_dev(qbk_ctx *ctx, const qbk_factor *layer, const uint16_t *x,
+                                  size_t batch, void *y, int y_dtype, void *stream);
 /* Host form of PackedLayer::apply / apply_bf16 (engine/mod.rs:393-460) on
  * the device: x f32 [batch][din] -> y f32 [batch][dout].  serving QBK_BF16 is
  * apply_bf16's composite; serving QBK_F32 is apply's (f64 matvecs). */

@@ -57,6 +57,7 @@ _SIGS = {
     "qbk_factor_workspace_size": (_Z, [_P, _Z]),
     "qbk_factor_linear_dev": (_I, [_P, _P, _P, _Z, _P, _I, _P, _Z, _P]),
     "qbk_factor_apply": (_I, [_P, _P, _I, _P, _Z, _P]),
+    "qbk_factor_linear_noalloc_dev": (_I, [_P, _P, _P, _Z, _P, _I, _P]),
     "qbk_factor_set_create": (_I, [_P, _P, _Z, C.POINTER(_P)]),
     "qbk_factor_set_destroy": (None, [_P]),
     "qbk_factor_set_workspace_size": (_Z, [_P]),

@@ -25,6 +25,8 @@
 
 #include <vector>
 
+#include <mutex>
+
 #include "factor_internal.h"
 
 namespace qbk {
@@ -166,6 +168,33 @@ static size_t ws_bytes(const qbk_factor *L, size_t batch) {
     return batch <= Q4_MAXB ? q4_workspace(L, batch) : g32_workspace(L, batch);
 }
 
+// ---- the no-allocation form of qbk_factor_linear_dev --------------------
+//
+// For callers that cannot allocate (code under graph capture, serving loops
+// that forbid hipMalloc): the workspace is this file-scope device array, one
+// copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the
+// symbol); it passes the device address hipGetSymbolAddress returns, looked
+// up once per device with that device current and kept per device.
+// Every call on a GPU shares that GPU's array, so calls that overlap on one
+// GPU race; the kernels write every byte they later read, so nothing needs
+// clearing between calls.
+static __device__ __align__(256) uint8_t scratch[QBK_NOALLOC_SCRATCH_BYTES];
+
+static int scratch_address(int device, void **out) {
+    static std::mutex mu;
+    static void *addr[64] = {};
+    if (device < 0 || device >= 64) return fail(QBK_ERR_DEVICE, fmt("device index %d out of range", device));
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[device]) {
+        void *p = nullptr;
+        QBK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        addr[device] = p;
+    }
+    *out = addr[device];
+    return QBK_OK;
+}
+
 }  // namespace qbk
 
 using namespace qbk;
@@ -298,6 +327,23 @@ int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *L, const uint16_t *x, 
     hipStream_t s = (hipStream_t)stream;
     if (batch <= Q4_MAXB) return q4_run(L, batch, x, false, y, y_dtype == QBK_BF16, workspace, s);
     return g32_run(L, x, false, batch, y, y_dtype == QBK_BF16, workspace, s);
+}
+
+int qbk_factor_linear_noalloc_dev(qbk_ctx *ctx, const qbk_factor *L, const uint16_t *x, size_t batch, void *y,
+                                  int y_dtype, void *stream) {
+    int rc;
+    if (!L) return fail(QBK_ERR_VALIDATION, "null layer");
+    if (batch == 0) return QBK_OK;
+    const size_t need = ws_bytes(L, batch);
+    if (need > QBK_NOALLOC_SCRATCH_BYTES)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("this call needs %zu bytes of workspace; the no-allocation entry point holds %zu "
+                        "(use qbk_factor_linear_dev with a workspace)",
+                        need, (size_t)QBK_NOALLOC_SCRATCH_BYTES));
+    if ((rc = bind(ctx))) return rc;
+    void *ws = nullptr;
+    if ((rc = scratch_address(ctx->device, &ws))) return rc;
+    return qbk_factor_linear_dev(ctx, L, x, batch, y, y_dtype, ws, need, stream);
 }
 
 // The f64 serving path's two elementwise ends (engine/mod.rs:419-436):

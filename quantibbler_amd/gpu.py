@@ -468,6 +468,14 @@ class FactorLayer:
                                                 _ptr(y), code, _ptr(workspace),
                                                 int(workspace_size), _stream(stream)))
 
+    def linear_noalloc_dev(self, x, batch: int, y, y_dtype: str, stream=None):
+        """linear_dev without a workspace: the library's per-GPU scratch
+        array (QBK_NOALLOC_SCRATCH_BYTES); allocates nothing.  Calls that
+        overlap on one GPU race."""
+        code = _DTYPES[y_dtype][0]
+        check(_lib.load().qbk_factor_linear_noalloc_dev(self.ctx.handle, self._h, _ptr(x), int(batch),
+                                                        _ptr(y), code, _stream(stream)))
+
     def apply(self, x, serving: str = "bfloat16") -> np.ndarray:
         """PackedLayer::apply ("float32": f64 matvecs) / apply_bf16 ("bfloat16")."""
         code = _DTYPES[serving][0]
