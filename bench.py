@@ -12,9 +12,10 @@ fp8 operand; stage 2, y = bf16(bf16(Ub t)*s1)).
 value = algorithmic bytes of all layers / step time, with config 1's
 per-layer count 1,097,728 B (U 512 KiB + V 512 KiB + x 8 KiB + y 8 KiB + s1,
 s2 32 KiB).  The timed region holds only the steps between two events.  The
-roofline's kernel duration: that phase alone, launched `steps` times back to
-back between two events on the launch stream (rocprofv3 --kernel-trace
---stats of the same command agrees; profiles/).
+roofline's kernel duration: the dominant kernel's average over the same
+number of steps run again with an event between consecutive launches on the
+launch stream, so each kernel is timed inside the step it belongs to
+(rocprofv3 --kernel-trace --stats of the same command agrees; profiles/).
 
 Extras (same JSON line): single-layer decode latency; prefill GEMM TFLOP/s at
 B in {16, 128, 512, 2048}; block-scaled SageAttention prefill at
@@ -23,9 +24,11 @@ attention step at 4096 cached tokens (from scratch and on a kept state); the
 lm_head at 128256 x 4096; one decoder block at config 3's shapes, and a decode
 token through 32 such blocks and the lm_head; config 3's
 seven projections over 32 decoder layers (decode and prefill); and the CPU
-baseline: the oracle's C restatement of the reference fast face (fast.rs,
-f64, OpenMP over 64-row blocks) timed on the host on a bounded sample of the
-decode workload.
+baselines, each a bounded sample on the job's host CPUs (up to the 16-CPU
+share of a one-GPU box): the headline's, the reference's bf16 serving
+composite (apply_bf16 over the scalar core face) one layer per thread; the
+reference fast face (fast.rs, f64x4, OpenMP over 64-row blocks) in the fp32
+composite; the reference SageAttention scheme in f32 on two heads of config 4.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--layers 512]
     python bench.py --only gemm|sage|cfg3|sage_decode|head|block|token
@@ -88,9 +91,10 @@ def make_layers(qa, ctx, np, count, seed):
 
 def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
     """The timed region: `steps` decodes of the whole set (three launches
-    each), bracketed by two events and nothing else.  Then each phase alone,
-    `steps` launches back to back between two events, for its average
-    launch duration (the roofline's denominator)."""
+    each), bracketed by two events and nothing else.  Then the same steps
+    again with an event between consecutive launches, all on the launch
+    stream, for each kernel's duration inside the step it belongs to (the
+    roofline's denominator: the dominant kernel's average launch)."""
     S = qa.FactorSet(ctx, layers)
     L = len(layers)
     rng = np.random.default_rng(7)
@@ -112,15 +116,15 @@ def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / steps
-    phase_ms = []
-    for ph in range(1, 4):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(st)
-        for _ in range(steps):
+    # in-step kernel durations: events e0 | prep | e1 | stage 1 | e2 | stage 2 | e3
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(st)
+        for ph in range(1, 4):
             S.stage_dev(ph, x, y, ws, ws_n, st)
-        b.record(st)
-        torch.cuda.synchronize()
-        phase_ms.append(a.elapsed_time(b) / steps)
+            ev[i][ph].record(st)
+    torch.cuda.synchronize()
+    phase_ms = [sum(ev[i][ph - 1].elapsed_time(ev[i][ph]) for i in range(steps)) / steps for ph in range(1, 4)]
     return dict(ms_per_step=ms_step, phase_ms=phase_ms, wall_s=wall, set=S)
 
 
@@ -363,11 +367,14 @@ def bench_block(qa, ctx, torch, np, ctx_tokens=2048, steps=50):
 
 
 def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab=128256):
-    """A decode token through a 32-block config-3-shaped trunk and the
-    lm_head, all on the device (config 5's decode at batch 1 without the
-    embedding lookup and sampling): 32 DecoderBlock calls, then the logits.
-    Every block has its own layers (480 MB of signs in all) and cache, filled
+    """Greedy decode tokens of config 5 at batch 1, all on the device: the
+    embedding row of the previous token, 32 config-3-shaped DecoderBlocks
+    (each its own layers, 480 MB of signs in all, and its own cache), the
+    final norm, the lm_head logits and the greedy argmax that picks the next
+    token (engine/mod.rs:802-806, sampler.rs:4-15).  The caches are filled
     one position a token to ctx_tokens before the timed tokens."""
+    from quantibbler_amd.gpu import argmax_dev, embed_dev, rms_norm_dev
+
     rng = np.random.default_rng(55)
     d = 4096
     blocks, keep = [], []
@@ -386,15 +393,21 @@ def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab
     rows = (0.02 * torch.randn((vocab, d), device="cuda", generator=g)).to(torch.bfloat16).to(torch.float32)
     head = qa.LmHead.from_rows_dev(ctx, rows, vocab, d)
     del rows
+    table = torch.randn((vocab, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
+    w_final = torch.ones(d, dtype=torch.float32, device="cuda")
     logits = torch.empty(vocab, dtype=torch.float32, device="cuda")
+    h = torch.empty(d, dtype=torch.float32, device="cuda")
+    hn = torch.empty(d, dtype=torch.float32, device="cuda")
+    tok = torch.tensor([1], dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream()
-    hs = torch.randn((ctx_tokens + steps, d), device="cuda", generator=g)
 
     def token(pos):
-        h = hs[pos]
+        embed_dev(ctx, table, vocab, d, tok, 1, h, st)
         for B in blocks:
             B.decode_dev(h, pos, st)
-        head.logits_dev(h, 1, logits, st)
+        rms_norm_dev(ctx, h, 1, d, w_final, 1e-5, hn, st)
+        head.logits_dev(hn, 1, logits, st)
+        argmax_dev(ctx, logits, 1, vocab, tok, st)
 
     for pos in range(ctx_tokens):
         token(pos)
@@ -410,11 +423,12 @@ def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab
     for B in blocks:
         B.close()
     head.close()
-    log(f"  decode token (32 blocks + lm_head) at {ctx_tokens} cached tokens: {ms:.3f} ms")
+    log(f"  greedy decode token (embedding, 32 blocks, final norm, lm_head, argmax) at {ctx_tokens} "
+        f"cached tokens: {ms:.3f} ms")
     return {"ms_per_token": round(ms, 3), "tokens_per_s": round(1e3 / ms, 1), "cached_tokens": ctx_tokens,
             "logits_finite": finite,
-            "shape": "32 config-3 blocks (bf16 serving, sage decode attention) + lm_head 128256 x 4096 bf16; "
-                     "no embedding lookup or sampling"}
+            "shape": "embedding 128256 x 4096, 32 config-3 blocks (bf16 serving, sage decode attention), "
+                     "final norm, lm_head 128256 x 4096 bf16, greedy argmax"}
 
 
 def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
@@ -494,12 +508,84 @@ def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
     return out
 
 
+def host_info():
+    """The host the CPU baselines ran on: CPU model, logical CPUs, the CPUs
+    this process may use, and the oracle's compiler flags."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    flags = ""
+    try:
+        with open(os.path.join(ROOT, "oracle", "Makefile")) as f:
+            for line in f:
+                if line.startswith("CFLAGS"):
+                    flags = line.split("=", 1)[1].strip()
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": os.cpu_count(), "cpus_allowed": allowed,
+            "compiler": "gcc " + flags}
+
+
+def cpu_threads():
+    """Threads for the CPU baselines: every CPU this process may use, capped
+    at the 16-CPU share a one-GPU box grants a job."""
+    info = host_info()
+    return max(1, min(16, info["cpus_allowed"]))
+
+
 def bench_cpu(np, host, budget_s=10.0):
+    """The headline's CPU baseline: the reference's bf16 serving composite
+    (engine/mod.rs:449-460 apply_bf16 over the scalar core face,
+    core.rs:202-260, as the reference serves bf16 on the CPU) on the decode
+    workload's independent layers, one layer per thread at a time on every
+    thread of the job's CPU share, for about budget_s seconds."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from oracle import oracle as orc
 
     orc.build()
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     rng = np.random.default_rng(11)
+    x = rng.standard_normal(N).astype(np.float32)
+
+    def one(i):
+        ub, vt, s1, s2 = host[i % len(host)]
+        orc.factor_apply("bf16", M, N, R, ub, vt, s1, s2, None, x)
+
+    calls, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        while time.perf_counter() - t0 < budget_s:
+            list(pool.map(one, range(calls, calls + threads)))
+            calls += threads
+    dt = time.perf_counter() - t0
+    out = {"value": round(calls * LAYER_BYTES / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
+           "kind": "port",
+           "sample": f"{calls} bf16-serving decode calls of config-1 layers (m=n=4096, r=1024, B=1) "
+                     f"cycling {len(host)} distinct layers in {dt:.1f} s, one layer per thread: the "
+                     "oracle's C restatement of apply_bf16 (engine/mod.rs:449-460) over the scalar "
+                     "core face (core.rs:202-260)"}
+    out.update(host_info())
+    return out
+
+
+def bench_cpu_fast(np, host, budget_s=5.0):
+    """The reference's fastest CPU face, fast.rs:28-110 (f64x4 lanes, 64-row
+    tasks over every thread) inside the fp32 serving composite
+    (engine/mod.rs:393-437), on the same layers."""
+    from oracle import oracle as orc
+
+    threads = cpu_threads()
+    rng = np.random.default_rng(12)
     x = rng.standard_normal(N).astype(np.float32)
     calls, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < budget_s:
@@ -507,12 +593,30 @@ def bench_cpu(np, host, budget_s=10.0):
         orc.factor_apply("fp32", M, N, R, ub, vt, s1, s2, None, x, fast=True, threads=threads)
         calls += 1
     dt = time.perf_counter() - t0
-    return {"value": round(calls * LAYER_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{calls} decode calls of config-1 layers (m=n=4096, r=1024, B=1) cycling "
-                      f"{len(host)} distinct layers in {dt:.1f} s: the oracle's C restatement of the "
-                      "reference fast face (fast.rs:28-110, f64, 64-row blocks, OpenMP) inside "
-                      "PackedLayer::apply (engine/mod.rs:393-437)"}
+    return {"value": round(calls * LAYER_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{calls} fp32-serving decode calls in {dt:.1f} s (fast face, f64x4, OpenMP)"}
+
+
+def bench_cpu_sage(np, heads=2, seq=4096):
+    """The reference SageAttention scheme in f32 (gpu_attention.rs:89-396
+    semantics, the oracle's restatement, OpenMP over query rows) on a bounded
+    sample of config 4: `heads` of its 32 heads at its full sequence, causal,
+    block 64; reported as config 4's operation rate (per head: 2 S^2 d / 2
+    INT8 ops + the same in P.V)."""
+    from oracle import oracle as orc
+
+    threads = cpu_threads()
+    rng = np.random.default_rng(13)
+    q = rng.standard_normal((1, heads, seq, 128)).astype(np.float32)
+    k = (rng.standard_normal((1, heads, seq, 128)) + 2 * rng.standard_normal((1, heads, 1, 128))).astype(np.float32)
+    v = rng.standard_normal((1, heads, seq, 128)).astype(np.float32)
+    t0 = time.perf_counter()
+    orc.attention_sage_dev(q, k, v, True, 64, threads=threads)
+    dt = time.perf_counter() - t0
+    ops = heads * 2 * (2 * seq * seq * 128 / 2)
+    return {"value": round(ops / dt / 1e12, 5), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{heads} heads x {seq} tokens x d 128, causal, block 64 in {dt:.1f} s "
+                      f"({dt / heads * 32:.0f} s for config 4's 32 heads)"}
 
 
 def main():
@@ -603,6 +707,10 @@ def main():
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")
     cpu = bench_cpu(np, host, args.cpu_seconds)
+    if not args.no_extra:
+        log("cpu baselines: fast face, reference sage scheme ...")
+        extra["cpu_fast_face_f64"] = bench_cpu_fast(np, host)
+        extra["cpu_sage_reference_f32"] = bench_cpu_sage(np)
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -629,6 +737,7 @@ def main():
             "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
             "kernel": f"q4_gemv_kernel<{dom},*,2> (decode stage {dom}, fp4 x fp8 scaled MFMA)",
             "bytes_per_launch": bytes_launch, "avg_launch_ms": round(dom_ms, 4),
+            "avg_launch_source": "HIP events between consecutive launches inside the timed steps",
         },
         "cpu_baseline": cpu,
         "extra": extra,

@@ -262,20 +262,24 @@ static void lut_init(void) {
     g_lut_ready = 1;
 }
 
-/* fast.rs:51-81 row_dot: four lane-sequential partials over 4-element groups,
- * the fixed reduce (a0+a2)+(a1+a3), then the scalar tail in element order. */
+/* fast.rs:51-81 row_dot: four lane-sequential partials over 4-element groups
+ * held in one f64x4 register (wide::f64x4 there, a GCC vector here: AVX2
+ * with -march=x86-64-v3), lane-wise multiply then add (no contraction), the
+ * fixed reduce (a0+a2)+(a1+a3), then the scalar tail in element order. */
+typedef double orc_f64x4 __attribute__((vector_size(32)));
+
 static double row_dot(const uint8_t *row, const double *vec, size_t n_bits) {
-    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+    orc_f64x4 acc = {0.0, 0.0, 0.0, 0.0};
     size_t n4 = n_bits / 4;
     for (size_t t = 0; t < n4; t++) {
         size_t base = t * 4;
-        const double *s = g_lut[row[base >> 3]] + (base & 7);
-        a0 = a0 + s[0] * vec[base];
-        a1 = a1 + s[1] * vec[base + 1];
-        a2 = a2 + s[2] * vec[base + 2];
-        a3 = a3 + s[3] * vec[base + 3];
+        orc_f64x4 sg, v;
+        memcpy(&sg, g_lut[row[base >> 3]] + (base & 7), sizeof sg);
+        memcpy(&v, vec + base, sizeof v);
+        orc_f64x4 p = sg * v;
+        acc = acc + p;
     }
-    double v4 = (a0 + a2) + (a1 + a3);
+    double v4 = (acc[0] + acc[2]) + (acc[1] + acc[3]);
     double tail = 0.0;
     for (size_t k = n4 * 4; k < n_bits; k++) tail = tail + (bit_at(row, k) ? 1.0 : -1.0) * vec[k];
     return v4 + tail;
