@@ -234,6 +234,19 @@ typedef struct {
     size_t batch, n_heads, n_kv_heads, seq_q, seq_kv, head_dim, val_dim;
 } qbk_attn_shape;
 
+/* gpu_attention.rs:451-570 GpuContext::attention (over cubek-attention's
+ * launch_ref in the reference): exact f32 attention, q (B,H,Sq,d) unscaled
+ * (1/sqrt(d) applied here), k (B,Hkv,Skv,d), v (B,Hkv,Skv,dv) -> out
+ * (B,H,Sq,dv); query head h reads kv head h / (H/Hkv); causal masks key j
+ * of query i when j + Sq > i + Skv (so Sq = 1 sees every key), and a row
+ * with every key masked is NaN.  Same validation messages and u32 index
+ * ceiling as the reference face.  The quality reference of the quantised
+ * schemes, and the engine's tiled decode face (engine/mod.rs:1041-1067). */
+int qbk_attention(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, size_t q_len, const float *k,
+                  size_t k_len, const float *v, size_t v_len, int causal, float *out);
+int qbk_attention_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
+                      const float *v, int causal, float *out, void *stream);
+
 /* gpu_attention.rs:589-756 GpuContext::attention_sage: the [SA] s4 reference
  * scheme (per-token INT8 Q with 1/sqrt(d) folded, per-K-block mean, per-token
  * INT8 K, P at the static 1/127 scale, per-channel INT8 V per tile), f32

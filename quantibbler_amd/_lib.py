@@ -63,6 +63,8 @@ _SIGS = {
     "qbk_factor_set_workspace_size": (_Z, [_P]),
     "qbk_factor_set_decode_dev": (_I, [_P, _P, _P, _P, _P, _Z, _P]),
     "qbk_factor_set_stage_dev": (_I, [_P, _P, _I, _P, _P, _P, _Z, _P]),
+    "qbk_attention": (_I, [_P, C.POINTER(AttnShape), _P, _Z, _P, _Z, _P, _Z, _I, _P]),
+    "qbk_attention_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _I, _P, _P]),
     "qbk_attention_sage": (_I, [_P, C.POINTER(AttnShape), _P, _Z, _P, _Z, _P, _Z, _I, _Z, _P]),
     "qbk_attention_sage_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _I, _Z, _P, _P]),
     "qbk_attention_sage_decode": (_I, [_P, C.POINTER(AttnShape), _P, _Z, _P, _Z, _P, _Z, _Z, _P, _Z]),

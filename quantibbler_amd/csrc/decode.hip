@@ -456,20 +456,33 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
         if (lane == 2) wl[ZS + 32] = 127;
     }
 
-    // stage 2: this lane's row of the group, for the epilogue
+    // stage 2: this lane's row of the group, for the epilogue (a layer
+    // without a bias, or with an all +0.0 one, has no bias pointer: y adds
+    // +0.0 all the same)
     float so = 0.0f, bi = 0.0f;
     if (STAGE == 2) {
         const size_t row = rgc * 64 + lane;
         const size_t rc = row < L.rows_valid ? row : L.rows_valid - 1;
         so = ((gf32_t *)L.s_out)[rc];
-        bi = ((gf32_t *)L.bias)[rc];
+        if (L.bias) bi = ((gf32_t *)L.bias)[rc];
     }
 
+    // Padding is not streamed.  A row group wholly past the valid rows (the
+    // rank padded to 128 in stage 1) loads nothing: its accumulators stay 0
+    // and the epilogue writes t = 0.  In a slice that ends past the valid K
+    // (the last one of a padded rank in stage 2), a lane group whose k run
+    // lies wholly past it (first k 16(g>>1) + 64(g&1) of the slice) reads
+    // lane group 0's words of the same slice instead -- lines the wave
+    // fetches anyway -- since its activations there are zero.
     const uint4 *wp = (const uint4 *)L.bits + (rgc * ns) * 64 + lane;
+    const uint32_t kmin = 16 * (g >> 1) + 64 * (g & 1);
+    const size_t sdead = L.k_valid > kmin ? (L.k_valid - kmin + 127) / 128 : 0;  // first slice all past K
+    const uint32_t dead_off = (uint32_t)(lane & 48);
+    const bool rows_dead = rgc * 64 >= L.rows_valid;
     f32x4_t acc[4];
 #pragma unroll
     for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
-    for (size_t sb = s0; sb < s1; sb += Q4_U) {
+    for (size_t sb = s0; sb < (rows_dead ? s0 : s1); sb += Q4_U) {
         const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
         // a step's operand: Q4_U slices x 4 lane groups x NCOL columns x 32 B,
         // SQ 16-byte words per lane
@@ -495,7 +508,7 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
 #pragma unroll
         for (int u = 0; u < Q4_U; u++) {
             const size_t sl = sb + (u < (int)nsl ? u : nsl - 1);
-            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64));
+            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64 - (sl >= sdead ? dead_off : 0)));
             w4[u] = make_uint4(q[0], q[1], q[2], q[3]);
         }
         if (NCOL > 0) {
@@ -615,7 +628,7 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
         a.act0 = act;
         b.bits = L->u_q4;
         b.s_out = L->s1;
-        b.bias = L->bias;
+        b.bias = L->bias_zero ? nullptr : L->bias;
         b.rows_p = (uint32_t)L->dout_p;
         b.rows_valid = (uint32_t)L->dout;
         b.ns = (uint32_t)ns2;

@@ -134,6 +134,15 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
     repack_q4(vbt_rows, r, din, L->r_p, L->din_q, vq.data());
     repack_q4(ub_rows, dout, r, L->dout_p, L->r_q, uq.data());
     std::vector<float> zb(dout, 0.0f);
+    L->bias_zero = true;  // no bias, or every entry +0.0: y = v * s1 + 0.0 needs no load
+    for (size_t i = 0; bias && i < dout; i++) {
+        uint32_t u;
+        memcpy(&u, bias + i, 4);
+        if (u != 0) {
+            L->bias_zero = false;
+            break;
+        }
+    }
     void *p;
 #define UP(field, src, n)                                                  \
     if ((rc = dev_upload(L, &p, src, n))) {                                \

@@ -39,6 +39,7 @@ struct qbk_factor {
     size_t din_q, r_q;                // K of the fp4 decode layout: multiples of 128
     uint32_t *vt_q4, *u_q4;           // [r_p/64][din_q/128][64][4], [dout_p/64][r_q/128][64][4]
     float *s1, *s2, *bias;            // dout, din, dout (zeros when absent)
+    bool bias_zero;                   // bias absent or all +0.0 (the decode skips its load)
     qbk::Q4Layer *q4_tab;             // device Q4Layer[2] of this layer alone: stage 1, stage 2
     std::vector<void *> allocs;
 };

@@ -34,12 +34,9 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-#define G_BM 256
-#define G_BN 128
 #define G_BK 64
 #define G_PITCH 72    // bf16 per LDS row of the activation tile: 64 + 8 of padding
 #define G_TPITCH 68   // f32 per token row of the epilogue transpose: 64 + 4
-#define G_LDS (8 * 32 * G_TPITCH * 4)  // >= 2 * G_BN * G_PITCH * 2
 
 // g32 sign layout: blocks of (128-row group g, 64-k slice s), 64 lanes x 4
 // words.  Word j of lane l holds row 128g + 32j + l%32 at
@@ -103,16 +100,31 @@ __device__ __forceinline__ bf16x8_t g32_frag(uint32_t w, int q, uint32_t m, uint
 
 // XM: the activation operand -- 0: bf16 rows of K_p (z or t); 1 / 2: stage 1
 // forms z = bf16(s2 * x) itself from bf16 / f32 x while staging it.
-template <int STAGE, int XM>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) g32_kernel(G32Args a) {
-    // [2 tile buffers of G_BN x G_PITCH bf16] during the loop; [8 waves][32 x
+// Wave grid WM (rows) x WN (tokens), wave tile 64 rows x 32 NT tokens, so
+// the workgroup tile is 64 WM x 32 NT WN with 64 WM WN threads; the tile
+// staging gives each thread two 8-element chunks, which needs BN = threads/4
+// (WM = 2 NT).  Shapes: 4 x 2 x 2 (256 x 128, 8 waves) for grids that fill the
+// chip; 2 x 2 x 1 (128 x 64, 4 waves) for the others.
+template <int WM, int WN, int NT>
+struct G32Shape {
+    static constexpr int THREADS = 64 * WM * WN, BM = 64 * WM, BN = 32 * NT * WN;
+    static constexpr int LDS_TILES = 2 * BN * G_PITCH * 2, LDS_EPI = WM * WN * 32 * G_TPITCH * 4;
+    static constexpr int LDS = LDS_TILES > LDS_EPI ? LDS_TILES : LDS_EPI;
+    static_assert(BN == THREADS / 4 && WM % 2 == 0, "two staged chunks per thread, 128-row sign groups");
+};
+
+template <int STAGE, int XM, int WM, int WN, int NT>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 2))) g32_kernel(G32Args a) {
+    using SH = G32Shape<WM, WN, NT>;
+    constexpr int BN = SH::BN, BM = SH::BM, TPB8 = SH::THREADS / 8;
+    // [2 tile buffers of BN x G_PITCH bf16] during the loop; [waves][32 x
     // G_TPITCH f32] in the epilogue
     extern __shared__ __attribute__((aligned(16))) uint8_t g32_lds[];
-    uint16_t(*bs)[G_BN * G_PITCH] = (uint16_t(*)[G_BN * G_PITCH])g32_lds;
+    uint16_t(*bs)[BN * G_PITCH] = (uint16_t(*)[BN * G_PITCH])g32_lds;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wr = wave & 3, wc = wave >> 2;  // 64-row block, 64-token half
-    const size_t n0 = (size_t)blockIdx.x * G_BN, m0 = (size_t)blockIdx.y * G_BM;
+    const int wr = wave % WM, wc = wave / WM;  // 64-row block, 32 NT-token block
+    const size_t n0 = (size_t)blockIdx.x * BN, m0 = (size_t)blockIdx.y * BM;
     size_t kb = 0, ke = a.K_p;
     if (STAGE == 1) {
         kb = (size_t)blockIdx.z * a.k_per_split;
@@ -128,8 +140,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     uint32_t one;
     asm volatile("v_mov_b32 %0, %1" : "=v"(one) : "s"(a.one_pair));
 
-    // B tile: 128 tokens x 64 k = 1024 chunks of 8 elements, two per thread
-    // (tokens tid/8 + 64u, k chunk tid%8).  Every load is issued
+    // B tile: BN tokens x 64 k = 8 BN chunks of 8 elements, two per thread
+    // (tokens tid/8 + (threads/8) u, k chunk tid%8).  Every load is issued
     // unconditionally -- tokens past N are clamped to N - 1 and only feed
     // output columns the epilogue does not store; with XM, chunks past din
     // read chunk 0 and store zeros -- so that the wait for the prefetch can
@@ -138,7 +150,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     const char *brow[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-        const size_t n = n0 + (tid >> 3) + 64 * u;
+        const size_t n = n0 + (tid >> 3) + TPB8 * u;
         const size_t off = (n < a.N ? n : a.N - 1) * ld + kc;
         brow[u] = XM == 2 ? (const char *)((const float *)a.x + off)
                           : (const char *)((XM ? (const uint16_t *)a.x : a.act) + off);
@@ -187,14 +199,14 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
             _Pragma("unroll") for (int e = 0; e < 4; e++)                                       \
                 zv[e] = bval ? f32x2_to_bf16x2(sv[2 * e] * xv[2 * e], sv[2 * e + 1] * xv[2 * e + 1]) : 0u;\
         }                                                                                       \
-        *(u32x4_t *)&bs[B][((tid >> 3) + 64 * u) * G_PITCH + kc] = zv;                          \
+        *(u32x4_t *)&bs[B][((tid >> 3) + TPB8 * u) * G_PITCH + kc] = zv;                        \
     }
 
-    f32x16_t acc[2][2];
+    f32x16_t acc[2][NT];
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++)
+        for (int nt = 0; nt < NT; nt++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[j][nt][i] = 0.0f;
 
@@ -210,12 +222,12 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     // value still in flight would wait for it).
     const size_t k_last = ke > kb ? ke - G_BK : kb;
     uint2 awA = make_uint2(0, 0), awB = make_uint2(0, 0);
-    bf16x8_t afA[4][2], afB[4][2], bfA[4][2], bfB[4][2];
+    bf16x8_t afA[4][2], afB[4][2], bfA[4][NT], bfB[4][NT];
 #define G32_READ_FRAGS(B, F)                                                                    \
     _Pragma("unroll") for (int q = 0; q < 4; q++)                                               \
-    _Pragma("unroll") for (int nt = 0; nt < 2; nt++)                                            \
+    _Pragma("unroll") for (int nt = 0; nt < NT; nt++)                                           \
         F[q][nt] = __builtin_bit_cast(                                                          \
-            bf16x8_t, *(const u32x4_t *)&bs[B][(wc * 64 + nt * 32 + (lane & 31)) * G_PITCH +    \
+            bf16x8_t, *(const u32x4_t *)&bs[B][(wc * 32 * NT + nt * 32 + (lane & 31)) * G_PITCH + \
                                               16 * q + 8 * (lane >> 5)]);
     // one stage: K0 its first k, B its LDS buffer, AFC/BFC its sign and
     // activation fragments, AFN/BFN the next stage's, AWU the next stage's
@@ -235,7 +247,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
             AFN[q][0] = g32_frag(AWU.x, q, m_sign, one);                                        \
             AFN[q][1] = g32_frag(AWU.y, q, m_sign, one);                                        \
             _Pragma("unroll") for (int j = 0; j < 2; j++)                                       \
-            _Pragma("unroll") for (int nt = 0; nt < 2; nt++)                                    \
+            _Pragma("unroll") for (int nt = 0; nt < NT; nt++)                                   \
                 acc[j][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(AFC[q][j], BFC[q][nt], acc[j][nt], 0, 0, 0);\
         }                                                                                       \
     }
@@ -285,7 +297,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
         }
     }
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
+    for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -294,7 +306,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
                     make_float4(acc[j][nt][4 * h], acc[j][nt][4 * h + 1], acc[j][nt][4 * h + 2],
                                 acc[j][nt][4 * h + 3]);
         __builtin_amdgcn_wave_barrier();
-        const size_t nb = n0 + wc * 64 + nt * 32;  // first token of the n-tile
+        const size_t nb = n0 + wc * 32 * NT + nt * 32;  // first token of the n-tile
         if (gvalid) {
             if (STAGE == 1 && a.split > 1) {
                 // f32 partials: 16 lanes per token (4 rows each), four tokens per store
@@ -414,10 +426,31 @@ __global__ void __launch_bounds__(256) g32_reduce_kernel(const float *__restrict
 // host side
 // ------------------------------------------------------------------------
 
-// Stage-1 K split: enough workgroups to cover every CU, at least four
-// 64-k stages per split.
+// The two workgroup shapes: 256 x 128 tiles (8 waves) and 128 x 64 tiles
+// (4 waves).  Stage 2 takes the large ones when they alone give every CU a
+// workgroup.
+typedef G32Shape<4, 2, 2> G32Big;
+typedef G32Shape<2, 2, 1> G32Small;
+
+static bool g32_big(size_t M_p, size_t N, int num_cus) {
+    return div_ceil(N, G32Big::BN) * div_ceil(M_p, G32Big::BM) >= (size_t)num_cus;
+}
+
+// Stage-1 K split, only where even the small tiles leave CUs idle: enough
+// workgroups to cover every CU, at least four 64-k stages per split.
+// Stage 1 shape: the 256 x 128 tiles, split over K, while they alone cover
+// a quarter of the CUs (measured at B = 2048: 56.6 us for the layer, against
+// 60-82 us for every 128 x 64 choice); below that the 128 x 64 tiles (at
+// B <= 512: 21-31 us, against 38-45 us).  Either way the K split brings the
+// workgroups up to the CU count, at least four 64-k stages per split.
+static bool g32_big1(const qbk_factor *L, size_t N) {
+    return div_ceil(N, G32Big::BN) * div_ceil(L->r_p, G32Big::BM) * 4 >= (size_t)L->num_cus;
+}
+
 static int g32_split(const qbk_factor *L, size_t N) {
-    const size_t tiles = div_ceil(N, G_BN) * div_ceil(L->r_p, G_BM);
+    const bool big = g32_big1(L, N);
+    const size_t tiles = big ? div_ceil(N, G32Big::BN) * div_ceil(L->r_p, G32Big::BM)
+                             : div_ceil(N, G32Small::BN) * div_ceil(L->r_p, G32Small::BM);
     int s = 1;
     while (tiles * s < (size_t)L->num_cus && s < 8 && L->din_p / (G_BK * 2 * s) >= 4) s *= 2;
     return s;
@@ -446,6 +479,20 @@ static G32Plan g32_plan(const qbk_factor *L, size_t N) {
     return p;
 }
 
+template <int STAGE, int XM, class SH, int WM, int WN, int NT>
+static void g32_launch(const G32Args &a, size_t M_p, int split, hipStream_t s) {
+    dim3 g((unsigned)div_ceil(a.N, SH::BN), (unsigned)div_ceil(M_p, SH::BM), split);
+    hipLaunchKernelGGL((g32_kernel<STAGE, XM, WM, WN, NT>), g, dim3(SH::THREADS), SH::LDS, s, a);
+}
+
+template <int STAGE, int XM>
+static void g32_launch_any(const G32Args &a, size_t M_p, int split, bool big, hipStream_t s) {
+    if (big)
+        g32_launch<STAGE, XM, G32Big, 4, 2, 2>(a, M_p, split, s);
+    else
+        g32_launch<STAGE, XM, G32Small, 2, 2, 1>(a, M_p, split, s);
+}
+
 size_t g32_workspace(const qbk_factor *L, size_t N) { return g32_plan(L, N).bytes; }
 
 int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
@@ -460,9 +507,9 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
         QBK_HIP(hipGetDevice(&dev));
         std::lock_guard<std::mutex> lock(mu);
         if (dev < 64 && !((done >> dev) & 1)) {
-            for (const void *k : {(const void *)g32_kernel<1, 0>, (const void *)g32_kernel<1, 1>,
-                                  (const void *)g32_kernel<1, 2>, (const void *)g32_kernel<2, 0>})
-                QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, G_LDS));
+            for (const void *k : {(const void *)g32_kernel<1, 0, 4, 2, 2>, (const void *)g32_kernel<1, 1, 4, 2, 2>,
+                                  (const void *)g32_kernel<1, 2, 4, 2, 2>, (const void *)g32_kernel<2, 0, 4, 2, 2>})
+                QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, G32Big::LDS));
             done |= 1ull << dev;
         }
     }
@@ -499,13 +546,13 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.k_per_split = round_up(div_ceil(L->din_p, p.split), G_BK);
     a.sign_mask = 0x80008000u;
     a.one_pair = 0x3F803F80u;
-    dim3 g1((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->r_p, G_BM), p.split);
+    const bool big1 = g32_big1(L, N);
     if (!fused)
-        hipLaunchKernelGGL((g32_kernel<1, 0>), g1, dim3(512), G_LDS, s, a);
+        g32_launch_any<1, 0>(a, L->r_p, p.split, big1, s);
     else if (xf32)
-        hipLaunchKernelGGL((g32_kernel<1, 2>), g1, dim3(512), G_LDS, s, a);
+        g32_launch_any<1, 2>(a, L->r_p, p.split, big1, s);
     else
-        hipLaunchKernelGGL((g32_kernel<1, 1>), g1, dim3(512), G_LDS, s, a);
+        g32_launch_any<1, 1>(a, L->r_p, p.split, big1, s);
     QBK_HIP(hipGetLastError());
     if (p.split > 1) {
         const size_t chunks = N * L->r_p / 8;
@@ -527,8 +574,7 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     b.vec_y = L->dout % 8 == 0 && (uintptr_t)y % 16 == 0;
     b.sign_mask = 0x80008000u;
     b.one_pair = 0x3F803F80u;
-    dim3 g2((unsigned)div_ceil(N, G_BN), (unsigned)div_ceil(L->dout_p, G_BM), 1);
-    hipLaunchKernelGGL((g32_kernel<2, 0>), g2, dim3(512), G_LDS, s, b);
+    g32_launch_any<2, 0>(b, L->dout_p, 1, g32_big(L->dout_p, N, L->num_cus), s);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

@@ -528,6 +528,16 @@ static int validate_sage(const qbk_attn_shape *s, size_t block_size, const size_
         if (lens[2] != ev)
             return fail(QBK_ERR_VALIDATION, fmt("value must hold %zu values for %s, got %zu", ev,
                                                 shape_debug(s).c_str(), lens[2]));
+        // gpu_attention.rs:652-669: the reference face's u32 index ceiling over
+        // the operands and every per-row extent its kernel derives
+        const uint64_t rows = (uint64_t)s->batch * s->n_heads * s->seq_q;
+        uint64_t largest = eq > ek ? eq : ek;
+        const uint64_t ext[5] = {ev, rows * s->head_dim, rows * s->val_dim, rows * block_size,
+                                 rows * block_size + block_size};
+        for (uint64_t x : ext) largest = x > largest ? x : largest;
+        if (largest > 0xFFFFFFFFull)
+            return fail(QBK_ERR_VALIDATION, "sage attention inputs exceed the device u32 index ceiling "
+                                            "(4294967295); use the reference face");
     }
     if (s->head_dim > REF_MAXD || s->val_dim > REF_MAXD)
         return fail(QBK_ERR_VALIDATION,

@@ -116,6 +116,16 @@ class GpuContext:
         code, npdt = _DTYPES[dtype]
         p = np.ascontiguousarray(packed, dtype=np.uint8).ravel()
         v = np.ascontiguousarray(vec, dtype=npdt).ravel()
+        if dtype == "float64":
+            # gpu.rs:116-137: after the shape and length checks, the reference
+            # device face's u32 index ceiling
+            nw = C.c_size_t()
+            check(_lib.load().qbk_validate_packed(p.size, int(n_rows), int(n_bits), C.byref(nw)))
+            if v.size != int(n_bits):
+                raise _lib.KernelError(f"vec must have length {n_bits}, got {v.size}")
+            if int(n_rows) * nw.value > 0xFFFFFFFF or int(n_rows) > 0xFFFFFFFF:
+                raise _lib.KernelError(f"packed shape {n_rows} x {nw.value} words exceeds the device u32 index "
+                                       f"ceiling (4294967295); use the CPU rlib face")
         out = np.zeros(n_rows, dtype=npdt)
         check(_lib.load().qbk_packed_matvec(self._h, code, _ptr(p), p.size, n_rows, n_bits,
                                             _ptr(v), v.size, _ptr(out)))
@@ -132,7 +142,25 @@ class GpuContext:
                                             _ptr(m), m.size, n_cols, _ptr(out)))
         return out.reshape(n_rows, k)
 
-    # ---- attention (gpu_attention.rs:589-756) -----------------------------
+    # ---- attention (gpu_attention.rs:451-756) -----------------------------
+
+    def attention(self, shape: AttentionShape, query, key, value, causal: bool):
+        """gpu_attention.rs:451-570 GpuContext::attention: exact f32
+        attention, Q unscaled, GQA, bottom-right causal; (B*H*Sq*dv,) f32."""
+        q = np.ascontiguousarray(query, dtype=np.float32).ravel()
+        k = np.ascontiguousarray(key, dtype=np.float32).ravel()
+        v = np.ascontiguousarray(value, dtype=np.float32).ravel()
+        out = np.zeros(shape.batch * shape.n_heads * shape.seq_q * shape.val_dim, np.float32)
+        sh = shape.c()
+        check(_lib.load().qbk_attention(self._h, C.byref(sh), _ptr(q), q.size, _ptr(k), k.size, _ptr(v),
+                                        v.size, int(bool(causal)), _ptr(out)))
+        return out
+
+    def attention_dev(self, shape: AttentionShape, q, k, v, causal: bool, out, stream=None):
+        sh = shape.c()
+        check(_lib.load().qbk_attention_dev(self._h, C.byref(sh), _ptr(q), _ptr(k), _ptr(v),
+                                            int(bool(causal)), _ptr(out), _stream(stream)))
+
 
     def attention_sage(self, shape: AttentionShape, query, key, value, causal: bool,
                        block_size: int):

@@ -97,6 +97,30 @@ def test_validation_precedes_device_use(lib):
         check(lib.qbk_attention_sage(None, C.byref(sh), None, 63, None, 32, None, 32, 1, 4, None))
 
 
+def test_exact_attention_validation_and_ceiling_precede_device_use(lib):
+    # gpu_attention.rs:466-509: the exact face's messages, then its u32
+    # index ceiling -- both before any device is touched
+    from quantibbler_amd import KernelError
+    from quantibbler_amd._lib import AttnShape, check
+
+    with pytest.raises(KernelError, match="n_kv_heads must divide n_heads: n_heads=3, n_kv_heads=2"):
+        sh = AttnShape(1, 3, 2, 8, 8, 4, 4)
+        check(lib.qbk_attention(None, C.byref(sh), None, 0, None, 0, None, 0, 1, None))
+    with pytest.raises(KernelError, match=r"key must hold 32 values for AttentionShape \{ batch: 1, "
+                       r"n_heads: 2, n_kv_heads: 1, seq_q: 8, seq_kv: 8, head_dim: 4, val_dim: 4 \}, got 31"):
+        sh = AttnShape(1, 2, 1, 8, 8, 4, 4)
+        check(lib.qbk_attention(None, C.byref(sh), None, 64, None, 31, None, 32, 1, None))
+    big = 1 << 31   # 2^31 keys x 4 channels: past the u32 ceiling; lengths match, nothing is read
+    sh = AttnShape(1, 1, 1, 1, big, 4, 4)
+    with pytest.raises(KernelError, match=r"attention inputs exceed the device u32 index ceiling \(4294967295\); "
+                                          "use the CPU reference face"):
+        check(lib.qbk_attention(None, C.byref(sh), None, 4, None, 4 * big, None, 4 * big, 0, None))
+    with pytest.raises(KernelError, match=r"sage attention inputs exceed the device u32 index ceiling"):
+        sh = AttnShape(1, 1, 1, big, big, 4, 4)
+        check(lib.qbk_attention_sage(None, C.byref(sh), None, 4 * big, None, 4 * big, None, 4 * big, 0, 64,
+                                     None))
+
+
 def test_decode_validation_precedes_device_use(lib):
     # the decode step's shape checks (batch 1, one query, the cache's sizes)
     # are reported before any device is touched
