@@ -201,6 +201,19 @@ void qbk_block_destroy(qbk_block *block);
  * overwritten and the attention state is rebuilt). */
 int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *block, float *h, size_t pos, void *stream);
 int qbk_block_reset(qbk_block *block);
+/* Prefill: n tokens of a new sequence at positions 0 .. n - 1 in one pass
+ * (engine/mod.rs:811-822 forward_prefill runs them one at a time; each
+ * token's row here is the same block arithmetic): h f32 [n][d_model] rows on
+ * the device, replaced by the block's outputs.  The projections run at batch
+ * n (the bf16-MFMA GEMM beyond batch 8), the attention is the causal
+ * block-scaled SageAttention over the n tokens (head_dim 128), and k, v fill
+ * cache rows 0 .. n - 1, so that decoding continues at position n (its
+ * attention state rebuilds from the cache on the first step).  The caller
+ * supplies `workspace` of at least qbk_block_prefill_workspace_size(block, n)
+ * bytes; nothing is allocated. */
+size_t qbk_block_prefill_workspace_size(const qbk_block *block, size_t n_tokens);
+int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *block, float *h, size_t n_tokens, void *workspace,
+                          size_t workspace_size, void *stream);
 /* The block's KV cache (device, f32 [capacity][n_kv_heads * head_dim] each).
  * Rows written through these pointers are not seen by the attention state
  * until qbk_block_reset. */

@@ -550,6 +550,46 @@ def block_step(layers, norms, h, pos, k_cache, v_cache, n_heads, n_kv_heads, hea
     return (proj(d_l, hid) + h1).astype(np.float32)
 
 
+def block_prefill(layers, norms, h_rows, k_cache, v_cache, n_heads, n_kv_heads, head_dim, theta, eps):
+    """The device block prefill's arithmetic at bf16 serving: every row of
+    engine/mod.rs:886-941 at positions 0 .. n - 1 (norms, apply_bf16
+    projections, q/k norms, RoPE, cache rows), with the attention of the n
+    tokens the block-scaled SageAttention (causal) over their bf16 q, k, v,
+    its output taken as bf16 for the o projection.  Returns the output rows;
+    fills cache rows 0 .. n - 1."""
+    def proj(L, x):
+        return factor_apply("bf16", L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                            L["bias"], x)
+
+    q_l, k_l, v_l, o_l, g_l, u_l, d_l = layers
+    h_rows = np.asarray(h_rows, np.float32)
+    n = h_rows.shape[0]
+    qs, ks, vs = [], [], []
+    for t in range(n):
+        x = norm_apply(h_rows[t], norms["input"], eps, "bf16")
+        q, k, v = proj(q_l, x), proj(k_l, x), proj(v_l, x)
+        if "q_norm" in norms and "k_norm" in norms:
+            q = per_head_norm(q, norms["q_norm"], head_dim, eps, "bf16")
+            k = per_head_norm(k, norms["k_norm"], head_dim, eps, "bf16")
+        q, k = rope(q, head_dim, t, theta), rope(k, head_dim, t, theta)
+        k_cache[t], v_cache[t] = k, v
+        qs.append(q)
+        ks.append(k)
+        vs.append(v)
+    qb = f32_to_bf16(np.stack(qs).reshape(n, n_heads, head_dim).transpose(1, 0, 2)[None].copy())
+    kb = f32_to_bf16(np.stack(ks).reshape(n, n_kv_heads, head_dim).transpose(1, 0, 2)[None].copy())
+    vb = f32_to_bf16(np.stack(vs).reshape(n, n_kv_heads, head_dim).transpose(1, 0, 2)[None].copy())
+    att = attention_sage_blk(qb, kb, vb, causal=True)[0]                        # (H, n, hd) f32
+    att = bf16_to_f32(f32_to_bf16(att.transpose(1, 0, 2).reshape(n, -1).copy()))
+    out = np.zeros_like(h_rows)
+    for t in range(n):
+        h1 = (proj(o_l, att[t]) + h_rows[t]).astype(np.float32)
+        x2 = norm_apply(h1, norms["post_attention"], eps, "bf16")
+        hid = swiglu(proj(g_l, x2), proj(u_l, x2))
+        out[t] = (proj(d_l, hid) + h1).astype(np.float32)
+    return out
+
+
 class Trunk:
     """Engine::forward_prefill (engine/mod.rs:805-822): per token, the
     embedding row, every block over its KV cache, the final norm and the

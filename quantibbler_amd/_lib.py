@@ -79,6 +79,8 @@ _SIGS = {
     "qbk_block_destroy": (None, [_P]),
     "qbk_block_decode_dev": (_I, [_P, _P, _P, _Z, _P]),
     "qbk_block_reset": (_I, [_P]),
+    "qbk_block_prefill_workspace_size": (_Z, [_P, _Z]),
+    "qbk_block_prefill_dev": (_I, [_P, _P, _P, _Z, _P, _Z, _P]),
     "qbk_block_cache": (_I, [_P, _P, _P]),
     "qbk_attention_sage_decode_step_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _Z, _P, _P, _Z, _Z,
                                                 _Z, _P]),

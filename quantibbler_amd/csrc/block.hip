@@ -37,6 +37,7 @@ struct qbk_block {
     int device;
     size_t d, H, Hk, hd, ffn, cap, block;
     float eps;
+    const qbk_factor *lay[7];  // q, k, v, o, gate, up, down
     const qbk_factor *o, *down;
     qbk_factor_set *qkv, *gu;
     float *w_in, *w_post;     // d each
@@ -45,7 +46,8 @@ struct qbk_block {
     float *kc, *vc;           // [cap][Hk * hd] the block's KV cache
     void *state;              // the attention's kept decode state
     size_t state_bytes;
-    size_t tokens;            // cache rows the state's codes cover
+    size_t tokens;            // cache rows the attention state's codes cover
+    size_t filled;            // cache rows holding this sequence's keys and values
     // per-call buffers
     uint16_t *xcat;           // bf16 [3 d] (q, k, v inputs), then [2 d] (gate, up)
     float *ycat;              // f32 [(H + 2 Hk) hd], then [2 ffn]
@@ -154,6 +156,166 @@ __global__ void blkd_add(const float *a, const float *b, float *out, int n) {
     if (i < n) out[i] = a[i] + b[i];
 }
 
+// ---- prefill (n tokens at positions 0 .. n - 1) ---------------------------
+
+// Per row of d: hsum = a (+ r), optionally stored to hout; x = bf16 of the
+// RMS-normalised bf16(hsum) times w (the decode's blkd_norm, a row per
+// workgroup).
+__global__ void __launch_bounds__(256) blkp_norm(const float *a, const float *r, float *hout, const float *w,
+                                                 float eps, uint16_t *x, int d) {
+    __shared__ float red[4];
+    const size_t off = (size_t)blockIdx.x * d;
+    const int tid = threadIdx.x;
+    float ss = 0.0f;
+    for (int i = tid; i < d; i += 256) {
+        float v = a[off + i];
+        if (r) v = v + r[off + i];
+        if (hout) hout[off + i] = v;
+        const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
+        ss += b * b;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+    for (int i = tid; i < d; i += 256) {
+        float v = a[off + i];
+        if (r) v = v + r[off + i];
+        const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
+        x[off + i] = blkd_bf16(b * inv * w[i]);
+    }
+}
+
+// Row t's q, k, v (token-major f32, as the projections wrote them): per-head
+// q/k norm (optional) and RoPE at position t, as blkd_qk_rope; k and v also
+// to cache row t.  The attention operands go out head-major in bf16:
+// qb [H][n][hd], kb / vb [Hk][n][hd].  Grid (H + Hk, n), a wave per head.
+__global__ void __launch_bounds__(64) blkp_qk_rope(const float *q, const float *k, const float *v, const float2 *rope,
+                                                   const float *wq, const float *wk, float eps, float *kc, float *vc,
+                                                   uint16_t *qb, uint16_t *kb, uint16_t *vb, int H, int Hk, int hd,
+                                                   int n) {
+    const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, half = hd / 2;
+    const bool is_q = head < H;
+    const int hh = is_q ? head : head - H;
+    const float *src = is_q ? q + ((size_t)t * H + hh) * hd : k + ((size_t)t * Hk + hh) * hd;
+    const float *w = is_q ? wq : wk;
+    float inv = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int j = lane; j < hd; j += 64) {
+            const float b = bf16_to_f32(f32_to_bf16(src[j]));
+            ss += b * b;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    }
+    const float2 *cs = rope + (size_t)t * half;
+    uint16_t *ob = is_q ? qb + ((size_t)hh * n + t) * hd : kb + ((size_t)hh * n + t) * hd;
+    float *crow = kc + ((size_t)t * Hk + hh) * hd;
+    for (int j = lane; j < half; j += 64) {
+        float a = src[j], b = src[j + half];
+        if (w) {
+            a = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(a)) * inv * w[j]));
+            b = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(b)) * inv * w[j + half]));
+        }
+        const float2 c = cs[j];
+        const float ra = a * c.x - b * c.y, rb = b * c.x + a * c.y;
+        ob[j] = f32_to_bf16(ra);
+        ob[j + half] = f32_to_bf16(rb);
+        if (!is_q) {
+            crow[j] = ra;
+            crow[j + half] = rb;
+        }
+    }
+    if (!is_q) {
+        const float *vs = v + ((size_t)t * Hk + hh) * hd;
+        float *vr = vc + ((size_t)t * Hk + hh) * hd;
+        uint16_t *vo = vb + ((size_t)hh * n + t) * hd;
+        for (int j = lane; j < hd; j += 64) {
+            vr[j] = vs[j];
+            vo[j] = f32_to_bf16(vs[j]);
+        }
+    }
+}
+
+// Attention output, head-major bf16 [H][n][hd] -> token-major [n][H hd], the
+// o projection's rows.
+__global__ void blkp_heads_to_rows(const uint16_t *ao, uint16_t *rows, int H, int hd, int n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)H * n * hd;
+    if (i >= total) return;
+    const size_t c = i % hd, t = (i / hd) % n, h = i / ((size_t)hd * n);
+    rows[(t * H + h) * hd + c] = ao[i];
+}
+
+// hidden = g u / (1 + exp(-g)), elementwise over n rows of ffn
+__global__ void blkp_swiglu(const float *g, const float *u, float *hid, size_t count) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) {
+        const float gv = g[i], uv = u[i];
+        hid[i] = gv * uv / (1.0f + expf(0.0f - gv));
+    }
+}
+
+__global__ void blkp_add(const float *a, const float *b, float *out, size_t count) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) out[i] = a[i] + b[i];
+}
+
+// A projection of n rows: the decode GEMV up to its batch limit, the GEMM
+// beyond; y f32.
+static size_t blkp_proj_ws(const qbk_factor *L, size_t n) {
+    return n <= Q4_MAXB ? q4_workspace(L, n) : g32_workspace(L, n);
+}
+static int blkp_proj(const qbk_factor *L, size_t n, const void *x, bool xf32, float *y, void *ws, hipStream_t s) {
+    return n <= Q4_MAXB ? q4_run(L, n, x, xf32, y, false, ws, s) : g32_run(L, x, xf32, n, y, false, ws, s);
+}
+
+// Prefill workspace regions (256-byte aligned), for n rows.
+struct BlkpPlan {
+    size_t o_x, o_q, o_k, o_v, o_qb, o_kb, o_vb, o_sage, o_ao, o_arow, o_oo, o_h1, o_g, o_u, o_gemm, bytes;
+    size_t sage_bytes, gemm_bytes;
+};
+
+static BlkpPlan blkp_plan(const qbk_block *B, const qbk_factor *const L[7], size_t n) {
+    BlkpPlan p{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += round_up(bytes ? bytes : 4, 256);
+        return o;
+    };
+    const size_t d = B->d, qd = B->H * B->hd, kd = B->Hk * B->hd;
+    p.o_x = take(n * (d > qd ? d : qd) * 2);
+    p.o_q = take(n * qd * 4);
+    p.o_k = take(n * kd * 4);
+    p.o_v = take(n * kd * 4);
+    p.o_qb = take(n * qd * 2);
+    p.o_kb = take(n * kd * 2);
+    p.o_vb = take(n * kd * 2);
+    const qbk_attn_shape sh{1, B->H, B->Hk, n, n, B->hd, B->hd};
+    p.sage_bytes = qbk_sage_blk_workspace_size(&sh);
+    p.o_sage = take(p.sage_bytes);
+    p.o_ao = take(n * qd * 2);
+    p.o_arow = take(n * qd * 2);
+    p.o_oo = take(n * d * 4);
+    p.o_h1 = take(n * d * 4);
+    p.o_g = take(n * B->ffn * 4);
+    p.o_u = take(n * B->ffn * 4);
+    size_t g = 0;
+    for (int i = 0; i < 7; i++) {
+        const size_t w = blkp_proj_ws(L[i], n);
+        g = w > g ? w : g;
+    }
+    p.gemm_bytes = g;
+    p.o_gemm = take(g);
+    p.bytes = off;
+    return p;
+}
+
 }  // namespace qbk
 
 using namespace qbk;
@@ -211,6 +373,7 @@ int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float 
     B->cap = capacity;
     B->block = block_size;
     B->eps = (float)rms_norm_eps;
+    for (int i = 0; i < 7; i++) B->lay[i] = layers[i];
     B->o = layers[3];
     B->down = layers[6];
     auto alloc = [&](void **p, size_t n) -> int {
@@ -278,9 +441,9 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     if (!B || !h) return fail(QBK_ERR_VALIDATION, "null argument");
     if (pos >= B->cap)
         return fail(QBK_ERR_VALIDATION, fmt("position %zu is past the block's cache capacity of %zu", pos, B->cap));
-    if (pos > B->tokens)
+    if (pos > B->filled)
         return fail(QBK_ERR_VALIDATION,
-                    fmt("position %zu skips cache rows: the block holds %zu positions", pos, B->tokens));
+                    fmt("position %zu skips cache rows: the block holds %zu positions", pos, B->filled));
     if ((rc = bind(ctx))) return rc;
     if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
     hipStream_t s = (hipStream_t)stream;
@@ -299,6 +462,7 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
                                                  B->state_bytes, B->cap, cached, stream)))
         return rc;
     B->tokens = pos + 1;
+    B->filled = pos + 1;
     if ((rc = q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s))) return rc;
     // MLP sublayer: h1 = o + h, then its norm
     hipLaunchKernelGGL(blkd_norm, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
@@ -316,6 +480,73 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
 int qbk_block_reset(qbk_block *B) {
     if (!B) return fail(QBK_ERR_VALIDATION, "null block");
     B->tokens = 0;
+    B->filled = 0;
+    return QBK_OK;
+}
+
+size_t qbk_block_prefill_workspace_size(const qbk_block *B, size_t n_tokens) {
+    if (!B || n_tokens == 0) return 0;
+    return blkp_plan(B, B->lay, n_tokens).bytes;
+}
+
+int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t n, void *workspace, size_t workspace_size,
+                          void *stream) {
+    int rc;
+    if (!B || !h) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (n == 0) return fail(QBK_ERR_VALIDATION, "prefill needs at least one token");
+    if (n > B->cap)
+        return fail(QBK_ERR_VALIDATION, fmt("prefill of %zu tokens exceeds the block's cache capacity of %zu", n, B->cap));
+    if (B->hd != 128)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("block prefill runs the block-scaled SageAttention, which needs head_dim 128; got %zu", B->hd));
+    const BlkpPlan P = blkp_plan(B, B->lay, n);
+    if (!workspace || workspace_size < P.bytes)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("workspace of %zu bytes is smaller than the %zu this prefill needs", workspace_size, P.bytes));
+    if ((rc = bind(ctx))) return rc;
+    if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
+    hipStream_t s = (hipStream_t)stream;
+    char *w = (char *)workspace;
+    uint16_t *x = (uint16_t *)(w + P.o_x), *qb = (uint16_t *)(w + P.o_qb), *kb = (uint16_t *)(w + P.o_kb),
+             *vb = (uint16_t *)(w + P.o_vb), *ao = (uint16_t *)(w + P.o_ao), *arow = (uint16_t *)(w + P.o_arow);
+    float *q = (float *)(w + P.o_q), *k = (float *)(w + P.o_k), *v = (float *)(w + P.o_v),
+          *oo = (float *)(w + P.o_oo), *h1 = (float *)(w + P.o_h1), *g = (float *)(w + P.o_g),
+          *u = (float *)(w + P.o_u);
+    void *ws = w + P.o_gemm;
+    const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk;
+    const size_t nd = n * B->d, nf = n * B->ffn;
+    // attention sublayer: norm, q/k/v at batch n, q/k norms + RoPE + cache
+    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, h, (const float *)nullptr, (float *)nullptr,
+                       B->w_in, B->eps, x, d);
+    QBK_HIP(hipGetLastError());
+    if ((rc = blkp_proj(B->lay[0], n, x, false, q, ws, s)) || (rc = blkp_proj(B->lay[1], n, x, false, k, ws, s)) ||
+        (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s)))
+        return rc;
+    hipLaunchKernelGGL(blkp_qk_rope, dim3(H + Hk, (unsigned)n), dim3(64), 0, s, q, k, v, B->rope, B->w_q, B->w_k,
+                       B->eps, B->kc, B->vc, qb, kb, vb, H, Hk, hd, (int)n);
+    QBK_HIP(hipGetLastError());
+    // causal block-scaled SageAttention over the n tokens
+    const qbk_attn_shape sh{1, B->H, B->Hk, n, n, B->hd, B->hd};
+    if ((rc = qbk_attention_sage_blk_dev(ctx, &sh, qb, kb, vb, 1, ao, w + P.o_sage, P.sage_bytes, stream))) return rc;
+    {
+        const size_t tot = n * B->H * B->hd;
+        hipLaunchKernelGGL(blkp_heads_to_rows, dim3((unsigned)div_ceil(tot, 256)), dim3(256), 0, s, ao, arow, H, hd,
+                           (int)n);
+        QBK_HIP(hipGetLastError());
+    }
+    // o + residual, norm, gate / up, SwiGLU, down + residual
+    if ((rc = blkp_proj(B->o, n, arow, false, oo, ws, s))) return rc;
+    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, oo, (const float *)h, h1, B->w_post, B->eps, x, d);
+    QBK_HIP(hipGetLastError());
+    if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) || (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s)))
+        return rc;
+    hipLaunchKernelGGL(blkp_swiglu, dim3((unsigned)div_ceil(nf, 256)), dim3(256), 0, s, g, u, g, nf);
+    QBK_HIP(hipGetLastError());
+    if ((rc = blkp_proj(B->down, n, g, true, oo, ws, s))) return rc;
+    hipLaunchKernelGGL(blkp_add, dim3((unsigned)div_ceil(nd, 256)), dim3(256), 0, s, oo, h1, h, nd);
+    QBK_HIP(hipGetLastError());
+    B->filled = n;
+    B->tokens = 0;  // the decode attention state rebuilds its codes from the cache
     return QBK_OK;
 }
 

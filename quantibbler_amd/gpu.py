@@ -367,6 +367,22 @@ class DecoderBlock:
         check(_lib.load().qbk_block_decode_dev(self.ctx.handle, self._h, _ptr(h), int(pos),
                                                _stream(stream)))
 
+    def prefill_workspace_size(self, n_tokens: int) -> int:
+        return int(_lib.load().qbk_block_prefill_workspace_size(self._h, int(n_tokens)))
+
+    def prefill_dev(self, h, n_tokens: int, workspace, workspace_size: int, stream=None):
+        """A new sequence's first n_tokens positions in one pass: h device f32
+        [n_tokens][d_model] rows, replaced by the block's outputs; decoding
+        continues at position n_tokens."""
+        if hasattr(h, "is_cuda"):
+            if not h.is_cuda or str(h.dtype) != "torch.float32" or not h.is_contiguous() \
+                    or h.numel() != self.d_model * int(n_tokens):
+                raise _lib.KernelError(
+                    f"prefill input must be a contiguous float32 device tensor of {n_tokens} x {self.d_model} "
+                    f"values; got {h.dtype} of {h.numel()} on {h.device}")
+        check(_lib.load().qbk_block_prefill_dev(self.ctx.handle, self._h, _ptr(h), int(n_tokens), _ptr(workspace),
+                                                int(workspace_size), _stream(stream)))
+
     def reset(self):
         check(_lib.load().qbk_block_reset(self._h))
 

@@ -255,6 +255,31 @@ class DeviceModel:
             b.reset()
         self.pos = 0
 
+    def prefill(self, tokens, stream=None):
+        """forward_prefill (engine/mod.rs:811-822) of a new sequence in one
+        pass per block: the tokens' embedding rows through every block's
+        prefill (batched projections, causal block-scaled SageAttention), then
+        the final norm and logits of the last position -- the logits a
+        token-at-a-time prefill ends with.  Returns them (a device tensor,
+        overwritten by the next call); decoding continues with step()."""
+        import torch
+
+        from .gpu import embed, rms_norm_dev
+
+        md = self.md
+        ids = [int(t) for t in tokens]
+        n = len(ids)
+        h = torch.empty((n, md.d_model), dtype=torch.float32, device="cuda")
+        embed(self.ctx, self.embedding, md.vocab_size, md.d_model, ids, h, stream)
+        need = max(b.prefill_workspace_size(n) for b in self.blocks)
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        for b in self.blocks:
+            b.prefill_dev(h, n, ws, need, stream)
+        rms_norm_dev(self.ctx, h[n - 1], 1, md.d_model, self.final_norm, md.rms_norm_eps, self.hn, stream)
+        self.head.logits_dev(self.hn, 1, self.logits, stream)
+        self.pos = n
+        return self.logits
+
     def step(self, token: int, stream=None):
         """The next position's logits (a device tensor, overwritten by the
         next step) for a host token id."""

@@ -120,3 +120,55 @@ def test_decoder_block_validation(ctx, orc):
     torch.cuda.synchronize()
     assert bool(torch.isfinite(h).all())
     block.close()
+
+
+@pytest.mark.parametrize("n", [5, 150])
+def test_block_prefill_then_decode(ctx, orc, n):
+    """A new sequence's n tokens in one prefill pass (projections at batch n:
+    the decode GEMV for n <= 8, the GEMM beyond; causal block-scaled
+    SageAttention over the n tokens; q/k norms; cache rows 0 .. n - 1), then
+    decode steps at positions n, n + 1, ... on the cache it filled: each row
+    against the oracle's restatement of the same arithmetic, to the block's
+    tolerance."""
+    from quantibbler_amd import DecoderBlock, FactorLayer
+
+    d, H, Hk, hd, ffn, cap, blk = 256, 4, 2, 128, 512, 200, 64
+    theta, eps = 500000.0, 1e-5
+    rng = np.random.default_rng(300 + n)
+    shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
+              (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    bfv = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a.astype(np.float32)))
+    norms = {"input": bfv(1.0 + 0.1 * rng.standard_normal(d)), "post_attention": bfv(1.0 + 0.1 * rng.standard_normal(d)),
+             "q_norm": bfv(1.0 + 0.2 * rng.standard_normal(hd)), "k_norm": bfv(1.0 + 0.2 * rng.standard_normal(hd))}
+    block = DecoderBlock(ctx, devs, norms["input"], norms["post_attention"], H, Hk, hd, theta, eps, cap, blk,
+                         norms["q_norm"], norms["k_norm"])
+    h = rng.standard_normal((n, d)).astype(np.float32)
+    hdv = torch.from_numpy(h).cuda()
+    wn = block.prefill_workspace_size(n)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream()
+    block.prefill_dev(hdv, n, ws, wn, st)
+    torch.cuda.synchronize()
+    kc = np.zeros((cap, Hk * hd), np.float32)
+    vc = np.zeros((cap, Hk * hd), np.float32)
+    want = orc.block_prefill(layers, norms, h, kc, vc, H, Hk, hd, theta, eps)
+    got = hdv.cpu().numpy()
+    worst = (1.0, 0.0)
+    for t in range(n):
+        cos, rel = metrics(got[t], want[t])
+        worst = (min(worst[0], cos), max(worst[1], rel))
+    print(f"prefill n={n}: worst cos {worst[0]:.7f} rel {worst[1]:.2e}", flush=True)
+    assert worst[0] >= COS_MIN and worst[1] <= REL_MAX, worst
+    for pos in range(n, n + 4):
+        x = rng.standard_normal(d).astype(np.float32)
+        xd = torch.from_numpy(x).cuda()
+        block.decode_dev(xd, pos, st)
+        torch.cuda.synchronize()
+        w2 = orc.block_step(layers, norms, x, pos, kc, vc, H, Hk, hd, theta, eps, "bf16", "sage", blk)
+        cos, rel = metrics(xd.cpu().numpy(), w2)
+        print(f"decode after prefill, pos {pos}: cos {cos:.7f} rel {rel:.2e}", flush=True)
+        assert cos >= COS_MIN and rel <= REL_MAX, (pos, cos, rel)
+    block.close()

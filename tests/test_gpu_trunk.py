@@ -153,3 +153,77 @@ def test_device_trunk_parity_tiny_goldens(ctx, orc, md):
     ref0 = orc.Trunk(md, serving="bf16", attention="sage", capacity=16).step(ids[0])
     assert np.abs(again - ref0).max() <= 2e-3
     m.close()
+
+
+def _qpk1_v2(orc, rng, dout, din, r):
+    """A random v2 qpk1 layer stream (f16 scales and bias), as the reference's
+    writer lays it out (container bitstreams, element (i, j) at bit i r + j)."""
+    ubs = rng.choice([0, 1], (dout, r)).astype(np.uint8)
+    vbs = rng.choice([0, 1], (din, r)).astype(np.uint8)
+    s1 = (np.exp(0.3 * rng.standard_normal(dout)) / np.sqrt(r * din)).astype(np.float16)
+    s2 = np.exp(0.3 * rng.standard_normal(din)).astype(np.float16)
+    bias = (0.05 * rng.standard_normal(dout)).astype(np.float16)
+    head = b"QPK1" + b"".join(int(v).to_bytes(4, "little") for v in (2, 1, dout, din, r))
+    return (head + s1.tobytes() + s2.tobytes() + bias.tobytes()
+            + np.packbits(ubs.ravel(), bitorder="little").tobytes()
+            + np.packbits(vbs.ravel(), bitorder="little").tobytes())
+
+
+def synthetic_model(orc, seed, vocab=300, d=256, n_layers=2, H=4, Hk=2, hd=128, ffn=512):
+    from quantibbler_amd.model import ModelDir
+
+    rng = np.random.default_rng(seed)
+    streams, names = {}, []
+    for b in range(n_layers):
+        for suffix, (m, k, r) in (("self_attn.q_proj", (H * hd, d, 48)), ("self_attn.k_proj", (Hk * hd, d, 32)),
+                                  ("self_attn.v_proj", (Hk * hd, d, 32)), ("self_attn.o_proj", (d, H * hd, 48)),
+                                  ("mlp.gate_proj", (ffn, d, 64)), ("mlp.up_proj", (ffn, d, 64)),
+                                  ("mlp.down_proj", (d, ffn, 64))):
+            name = f"layers.{b}.inner.{suffix}"
+            names.append(name)
+            streams[name] = _qpk1_v2(orc, rng, m, k, r)
+    per_block = 2 * d + 2 * hd
+    norms = (1 + 0.1 * rng.standard_normal(per_block * n_layers + d)).astype(np.float32)
+    return ModelDir(path="<synthetic>", vocab_size=vocab, d_model=d, n_layers=n_layers, n_heads=H, n_kv_heads=Hk,
+                    head_dim=hd, rms_norm_eps=1e-6, rope_theta=10000.0,
+                    norm_slots=["input", "post_attention", "q_norm", "k_norm"], remainder_dtype="f32",
+                    layer_names=names, streams=streams,
+                    embedding=rng.standard_normal((vocab, d)).astype(np.float32),
+                    lm_head=(0.1 * rng.standard_normal((vocab, d))).astype(np.float32), norms=norms)
+
+
+def test_device_trunk_prefill_then_decode(ctx, orc):
+    """DeviceModel.prefill (every block's one-pass prefill: batched
+    projections, causal block-scaled SageAttention) and then greedy decode
+    steps, against the oracle composing the same arithmetic block by block
+    (block_prefill, then block_step on the caches it filled)."""
+    from quantibbler_amd.model import DeviceModel, _bf16_values
+
+    say("device trunk prefill + decode")
+    md = synthetic_model(orc, 808)
+    n = 70
+    rng = np.random.default_rng(809)
+    tokens = rng.integers(0, md.vocab_size, n).tolist()
+    m = DeviceModel(ctx, md, capacity=128)
+    got = m.prefill(tokens, torch.cuda.current_stream()).cpu().numpy()
+    # oracle: the same per-block arithmetic
+    ref = orc.Trunk(md, serving="bf16", attention="sage", capacity=128)
+    h = ref.embedding[np.array(tokens)].copy()
+    for b, (layers, norms) in enumerate(ref.blocks):
+        h = orc.block_prefill(layers, norms, h, ref.kc[b], ref.vc[b], md.n_heads, md.n_kv_heads, md.head_dim,
+                              md.rope_theta, md.rms_norm_eps)
+    ref.pos = n
+    hn = orc.norm_apply(h[-1], ref.final_norm, md.rms_norm_eps, "bf16")
+    want = orc.head_logits(ref.head, hn)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    say(f"  prefill logits rel {rel:.2e}")
+    assert rel <= 1e-2
+    assert int(np.argmax(got)) == int(np.argmax(want)) or np.sort(want)[-1] - np.sort(want)[-2] < 1e-2
+    for _ in range(3):
+        tok = int(np.argmax(want))
+        got = m.step(tok, torch.cuda.current_stream()).cpu().numpy()
+        want = ref.step(tok)
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        say(f"  decode logits rel {rel:.2e}")
+        assert rel <= 1e-2
+    m.close()
