@@ -21,8 +21,9 @@ Extras (same JSON line): single-layer decode latency; prefill GEMM TFLOP/s at
 B in {16, 128, 512, 2048}; block-scaled SageAttention prefill at
 B=1, H=32, S=4096, d=128, causal; the reference scheme's decode
 attention step at 4096 cached tokens (from scratch and on a kept state); the
-lm_head at 128256 x 4096; one decoder block at config 3's shapes, and a decode
-token through 32 such blocks and the lm_head; config 3's
+lm_head at 128256 x 4096; one decoder block at config 3's shapes; config 5 at
+batch 1 (a 2048-token prefill, then 256 greedy decode steps through 32 such
+blocks, the final norm, the lm_head and argmax); config 3's
 seven projections over 32 decoder layers (decode and prefill); and the CPU
 baselines, each a bounded sample on the job's host CPUs (up to the 16-CPU
 share of a one-GPU box): the headline's, the reference's bf16 serving
@@ -31,7 +32,7 @@ reference fast face (fast.rs, f64x4, OpenMP over 64-row blocks) in the fp32
 composite; the reference SageAttention scheme in f32 on two heads of config 4.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--layers 512]
-    python bench.py --only gemm|sage|cfg3|sage_decode|head|block|token
+    python bench.py --only gemm|sage|cfg3|sage_decode|head|block|model
 """
 import argparse
 import json
@@ -366,14 +367,18 @@ def bench_block(qa, ctx, torch, np, ctx_tokens=2048, steps=50):
             "shape": "d 4096, 32/8 heads x 128, ffn 14336, config-3 ranks; bf16 serving, sage decode attention"}
 
 
-def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab=128256):
-    """Greedy decode tokens of config 5 at batch 1, all on the device: the
-    embedding row of the previous token, 32 config-3-shaped DecoderBlocks
-    (each its own layers, 480 MB of signs in all, and its own cache), the
-    final norm, the lm_head logits and the greedy argmax that picks the next
-    token (engine/mod.rs:802-806, sampler.rs:4-15).  The caches are filled
-    one position a token to ctx_tokens before the timed tokens."""
-    from quantibbler_amd.gpu import argmax_dev, embed_dev, rms_norm_dev
+def bench_model(qa, ctx, torch, np, n_blocks=32, prompt=2048, steps=256, vocab=128256):
+    """Config 5 at batch 1, all on the device: a random-init 32-block
+    Llama-3-8B-shaped model at config 3's ranks (each block its own layers,
+    480 MB of signs in all, and its own KV cache), an embedding of 128256
+    rows, fp16-valued norms, and a 128256 x 4096 bf16 lm_head.  Workload:
+    the prefill of `prompt` random token ids (every block's one-pass
+    prefill: projections on the GEMM at batch `prompt`, causal block-scaled
+    SageAttention), its last position's logits and greedy token, then `steps`
+    greedy decode steps (embedding row, 32 DecoderBlocks on the sage decode
+    attention, final norm, logits, argmax -- engine/mod.rs:802-822,
+    sampler.rs:4-15), the next token fed back on the device."""
+    from quantibbler_amd.gpu import argmax_dev, embed, embed_dev, rms_norm_dev
 
     rng = np.random.default_rng(55)
     d = 4096
@@ -381,14 +386,15 @@ def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab
     for bi in range(n_blocks):
         layers = []
         for name, m, n, r in CFG3:
-            s1 = (np.exp(0.3 * rng.standard_normal(m)) / np.sqrt(r * n)).astype(np.float32)
-            s2 = np.exp(0.3 * rng.standard_normal(n)).astype(np.float32)
+            s1 = (np.exp(0.3 * rng.standard_normal(m)) / np.sqrt(r * n)).astype(np.float16).astype(np.float32)
+            s2 = np.exp(0.3 * rng.standard_normal(n)).astype(np.float16).astype(np.float32)
             layers.append(qa.FactorLayer.from_rows(ctx, m, n, r, random_rows(np, rng, m, r),
                                                    random_rows(np, rng, r, n), s1, s2, None))
-        w = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
-        blocks.append(qa.DecoderBlock(ctx, layers, w, w, 32, 8, 128, 500000.0, 1e-5,
-                                      ctx_tokens + steps + 64, 64))
+        w = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float16).astype(np.float32)
+        blocks.append(qa.DecoderBlock(ctx, layers, w, w, 32, 8, 128, 500000.0, 1e-5, prompt + steps + 64, 64))
         keep.append(layers)
+        if (bi + 1) % 8 == 0:
+            log(f"  config 5: built {bi + 1}/{n_blocks} blocks")
     g = torch.Generator(device="cuda").manual_seed(56)
     rows = (0.02 * torch.randn((vocab, d), device="cuda", generator=g)).to(torch.bfloat16).to(torch.float32)
     head = qa.LmHead.from_rows_dev(ctx, rows, vocab, d)
@@ -398,8 +404,21 @@ def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab
     logits = torch.empty(vocab, dtype=torch.float32, device="cuda")
     h = torch.empty(d, dtype=torch.float32, device="cuda")
     hn = torch.empty(d, dtype=torch.float32, device="cuda")
-    tok = torch.tensor([1], dtype=torch.int32, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream()
+    ids = rng.integers(0, vocab, prompt).astype(np.int32)
+    hp = torch.empty((prompt, d), dtype=torch.float32, device="cuda")
+    wn = max(B.prefill_workspace_size(prompt) for B in blocks)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+
+    def prefill():
+        embed(ctx, table, vocab, d, ids, hp, st)
+        for B in blocks:
+            B.reset()
+            B.prefill_dev(hp, prompt, ws, wn, st)
+        rms_norm_dev(ctx, hp[prompt - 1], 1, d, w_final, 1e-5, hn, st)
+        head.logits_dev(hn, 1, logits, st)
+        argmax_dev(ctx, logits, 1, vocab, tok, st)
 
     def token(pos):
         embed_dev(ctx, table, vocab, d, tok, 1, h, st)
@@ -409,26 +428,29 @@ def bench_token(qa, ctx, torch, np, n_blocks=32, ctx_tokens=512, steps=20, vocab
         head.logits_dev(hn, 1, logits, st)
         argmax_dev(ctx, logits, 1, vocab, tok, st)
 
-    for pos in range(ctx_tokens):
-        token(pos)
+    prefill()           # warm-up pass (first launches, allocator)
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
     a.record(st)
-    for pos in range(ctx_tokens, ctx_tokens + steps):
-        token(pos)
+    prefill()
     b.record(st)
+    for i in range(steps):
+        token(prompt + i)
+    c.record(st)
     torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / steps
+    pre_ms, dec_ms = a.elapsed_time(b), b.elapsed_time(c) / steps
     finite = bool(torch.isfinite(logits).all())
     for B in blocks:
         B.close()
     head.close()
-    log(f"  greedy decode token (embedding, 32 blocks, final norm, lm_head, argmax) at {ctx_tokens} "
-        f"cached tokens: {ms:.3f} ms")
-    return {"ms_per_token": round(ms, 3), "tokens_per_s": round(1e3 / ms, 1), "cached_tokens": ctx_tokens,
-            "logits_finite": finite,
-            "shape": "embedding 128256 x 4096, 32 config-3 blocks (bf16 serving, sage decode attention), "
-                     "final norm, lm_head 128256 x 4096 bf16, greedy argmax"}
+    log(f"  config 5 (B=1): prefill of {prompt} tokens {pre_ms:.2f} ms, then {steps} greedy steps at "
+        f"{dec_ms:.3f} ms/token")
+    return {"prefill_ms": round(pre_ms, 2), "prefill_tokens_per_s": round(prompt / pre_ms * 1e3, 1),
+            "decode_ms_per_token": round(dec_ms, 3), "decode_tokens_per_s": round(1e3 / dec_ms, 1),
+            "prompt_tokens": prompt, "decode_steps": steps, "logits_finite": finite,
+            "shape": "32 blocks (d 4096, 32/8 heads x 128, ffn 14336, config-3 ranks, fp16-valued scales), "
+                     "embedding and lm_head 128256 x 4096, bf16 serving; prefill on the GEMM and the "
+                     "block-scaled SageAttention, decode on the GEMV and the sage decode attention"}
 
 
 def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
@@ -626,7 +648,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=512)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head", "block", "token"],
+    ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head", "block", "model"],
                     help="run one secondary workload alone and print its figures (for profiling); "
                          "no headline line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -657,8 +679,8 @@ def main():
             res = bench_head(qa, ctx, torch, np)
         elif args.only == "block":
             res = bench_block(qa, ctx, torch, np)
-        elif args.only == "token":
-            res = bench_token(qa, ctx, torch, np)
+        elif args.only == "model":
+            res = bench_model(qa, ctx, torch, np)
         else:
             res = bench_cfg3(qa, ctx, torch, np)
         print(json.dumps({"only": args.only, "result": res}), flush=True)
@@ -701,8 +723,8 @@ def main():
         log("lm_head ...")
         extra["lm_head"] = bench_head(qa, ctx, torch, np)
         extra["decoder_block"] = bench_block(qa, ctx, torch, np)
-        log("decode token (32 blocks + lm_head) ...")
-        extra["decode_token"] = bench_token(qa, ctx, torch, np)
+        log("config 5: prefill + greedy decode (32 blocks + lm_head) ...")
+        extra["config5_b1"] = bench_model(qa, ctx, torch, np)
         log("config 3 (8B decoder layer projections) ...")
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")
