@@ -69,6 +69,15 @@ int qbk_validate_packed(size_t packed_len, size_t n_rows, size_t n_bits, size_t 
 /* core.rs sign_estimate: x >= 0 (incl. -0.0) -> +1, else -1. */
 void qbk_sign_estimate(const double *x, size_t n, int8_t *out);
 
+/* core.rs:318-424 joint_itq (the compressor's alternating Procrustes; host
+ * code, as the reference's): u_hat (dout x rank), v_hat (din x rank) f64
+ * row-major -> u_t, v_t +-1 int8 of the same shapes, the iteration count and
+ * whether ||R_new - R||_F <= tol stopped it (tol == 0 runs max_iter).  The
+ * reference's defaults are max_iter 50, tol 1e-12, seed 0. */
+int qbk_joint_itq(const double *u_hat, size_t u_len, const double *v_hat, size_t v_len, size_t dout,
+                  size_t din, size_t rank, size_t max_iter, double tol, uint64_t seed, int8_t *u_t,
+                  int8_t *v_t, size_t *n_iter, int *converged);
+
 /* ---- device context (gpu.rs:76-189 GpuContext) --------------------------- */
 
 /* gpu.rs:85-101 GpuContext::init_at(device_index); failure -> QBK_ERR_INIT

@@ -43,6 +43,8 @@ _SIGS = {
     "qbk_unpack_bits": (_I, [_P, _Z, _Z, _Z, _P]),
     "qbk_validate_packed": (_I, [_Z, _Z, _Z, C.POINTER(C.c_size_t)]),
     "qbk_sign_estimate": (None, [_P, _Z, _P]),
+    "qbk_joint_itq": (_I, [_P, _Z, _P, _Z, _Z, _Z, _Z, _Z, C.c_double, C.c_uint64, _P, _P, C.POINTER(_Z),
+                           C.POINTER(_I)]),
     "qbk_ctx_create": (_I, [_I, C.POINTER(_P)]),
     "qbk_ctx_destroy": (None, [_P]),
     "qbk_gpu_available": (_I, []),

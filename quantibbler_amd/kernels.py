@@ -10,9 +10,8 @@ name and ``hasattr``) runs unchanged when this module is importable as
     sys.modules["quantibbler_kernels"] = k
 
 The packed products run on the GPU (a process-wide GpuContext on device 0);
-pack_bits / unpack_bits / sign_estimate run in libqbk's host code, as the
-reference's do.  ``joint_itq`` (an off-path compressor solver) is not
-provided; the dispatcher's ``hasattr`` check routes it to NumPy.
+pack_bits / unpack_bits / sign_estimate and joint_itq (the compressor's
+alternating Procrustes) run in libqbk's host code, as the reference's do.
 Errors raise ValueError subclasses (lib.rs:34-36 maps KernelError to
 ValueError).
 """
@@ -28,7 +27,7 @@ from ._lib import KernelError, check
 
 __all__ = [
     "backend_version", "pack_bits", "unpack_bits", "sign_estimate", "packed_matvec",
-    "packed_matmul", "packed_matvec_dtype", "packed_matmul_dtype",
+    "packed_matmul", "packed_matvec_dtype", "packed_matmul_dtype", "joint_itq",
 ]
 
 _ctx = None
@@ -145,3 +144,22 @@ def packed_matvec_dtype(packed, n_bits: int, vec, dtype: str) -> np.ndarray:
 def packed_matmul_dtype(packed, n_bits: int, mat, dtype: str) -> np.ndarray:
     """lib.rs:326-382."""
     return _matmul(packed, n_bits, mat, _dtype_tag(dtype))
+
+
+def joint_itq(u_hat, v_hat, *, max_iter=None, tol=None, seed=None):
+    """lib.rs:197-235: joint_itq over Z = [u_hat; v_hat] (core.rs:318-424)
+    -> (u_t int8 (dout, r), v_t int8 (din, r), n_iter, converged)."""
+    u = np.ascontiguousarray(u_hat, dtype=np.float64)
+    v = np.ascontiguousarray(v_hat, dtype=np.float64)
+    dout, rank = _rows_cols(u.shape)
+    din, rank_v = _rows_cols(v.shape)
+    if rank != rank_v:
+        raise KernelError(f"joint_itq rank mismatch: u_hat r={rank}, v_hat r={rank_v}")
+    ut = np.zeros((dout, rank), np.int8)
+    vt = np.zeros((din, rank), np.int8)
+    n_iter, conv = C.c_size_t(), C.c_int()
+    check(_lib.load().qbk_joint_itq(u.ctypes.data, u.size, v.ctypes.data, v.size, dout, din, rank,
+                                    50 if max_iter is None else int(max_iter),
+                                    1e-12 if tol is None else float(tol), 0 if seed is None else int(seed),
+                                    ut.ctypes.data, vt.ctypes.data, C.byref(n_iter), C.byref(conv)))
+    return ut, vt, int(n_iter.value), bool(conv.value)

@@ -188,3 +188,20 @@ def test_init_fails_closed_without_device(lib):
     assert gpu_available() is False
     with pytest.raises(InitError, match="no usable HIP/ROCm device"):
         GpuContext(0)
+
+
+def test_rust_binding_declares_only_exported_symbols(lib):
+    """quantibbler_amd/rust/qbk-sys declares the C ABI for the reference's
+    Rust side (no cargo here to build it): every function it binds is
+    declared in include/qbk.h and exported by libqbk.so, and its struct
+    mirror of AttentionShape has the header's field order."""
+    src = open(os.path.join(ROOT, "quantibbler_amd", "rust", "qbk-sys", "src", "lib.rs")).read()
+    bound = set(re.findall(r"pub fn (qbk_[a-z0-9_]+)\(", src))
+    assert len(bound) >= 20
+    declared = set(declared_symbols())
+    for n in sorted(bound):
+        assert n in declared, f"{n} is not declared in include/qbk.h"
+        assert hasattr(lib, n), f"{n} is not exported"
+    fields = re.search(r"pub struct AttentionShape \{(.*?)\}", src, re.S).group(1)
+    assert re.findall(r"pub (\w+): usize", fields) == ["batch", "n_heads", "n_kv_heads", "seq_q", "seq_kv",
+                                                       "head_dim", "val_dim"]
