@@ -367,21 +367,25 @@ def bench_block(qa, ctx, torch, np, ctx_tokens=2048, steps=50):
             "shape": "d 4096, 32/8 heads x 128, ffn 14336, config-3 ranks; bf16 serving, sage decode attention"}
 
 
-def bench_model(qa, ctx, torch, np, n_blocks=32, prompt=2048, steps=256, vocab=128256):
-    """Config 5 at batch 1, all on the device: a random-init 32-block
-    Llama-3-8B-shaped model at config 3's ranks (each block its own layers,
-    480 MB of signs in all, and its own KV cache), an embedding of 128256
-    rows, fp16-valued norms, and a 128256 x 4096 bf16 lm_head.  Workload:
-    the prefill of `prompt` random token ids (every block's one-pass
-    prefill: projections on the GEMM at batch `prompt`, causal block-scaled
-    SageAttention), its last position's logits and greedy token, then `steps`
-    greedy decode steps (embedding row, 32 DecoderBlocks on the sage decode
-    attention, final norm, logits, argmax -- engine/mod.rs:802-822,
-    sampler.rs:4-15), the next token fed back on the device."""
+def bench_model(qa, ctx, torch, np, n_blocks=32, prompt=2048, steps=256, vocab=128256, batches=(1, 32)):
+    """Config 5, all on the device: a random-init 32-block Llama-3-8B-shaped
+    model at config 3's ranks (each block its own layers, 480 MB of signs in
+    all, and per sequence its own KV cache), an embedding of 128256 rows,
+    fp16-valued norms, and a 128256 x 4096 bf16 lm_head.  Workload per batch
+    size b: the prefill of `prompt` random token ids into each of b sequences
+    (every block's one-pass prefill: projections on the GEMM at batch
+    `prompt`, causal block-scaled SageAttention), the last positions' logits
+    and greedy tokens, then `steps` greedy decode steps of all b sequences
+    together (embedding rows, 32 DecoderBlocks -- projections at batch b, the
+    sage decode attention stepping each sequence's kept state -- final norm,
+    logits, argmax; engine/mod.rs:802-822, :1377-1476, sampler.rs:4-15), the
+    next tokens fed back on the device."""
     from quantibbler_amd.gpu import argmax_dev, embed, embed_dev, rms_norm_dev
 
     rng = np.random.default_rng(55)
     d = 4096
+    nseq = max(batches)
+    cap = prompt + steps + 64
     blocks, keep = [], []
     for bi in range(n_blocks):
         layers = []
@@ -391,66 +395,81 @@ def bench_model(qa, ctx, torch, np, n_blocks=32, prompt=2048, steps=256, vocab=1
             layers.append(qa.FactorLayer.from_rows(ctx, m, n, r, random_rows(np, rng, m, r),
                                                    random_rows(np, rng, r, n), s1, s2, None))
         w = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float16).astype(np.float32)
-        blocks.append(qa.DecoderBlock(ctx, layers, w, w, 32, 8, 128, 500000.0, 1e-5, prompt + steps + 64, 64))
+        blocks.append(qa.DecoderBlock(ctx, layers, w, w, 32, 8, 128, 500000.0, 1e-5, cap, 64, n_seqs=nseq))
         keep.append(layers)
         if (bi + 1) % 8 == 0:
-            log(f"  config 5: built {bi + 1}/{n_blocks} blocks")
+            log(f"  config 5: built {bi + 1}/{n_blocks} blocks ({nseq} sequences' caches each)")
     g = torch.Generator(device="cuda").manual_seed(56)
     rows = (0.02 * torch.randn((vocab, d), device="cuda", generator=g)).to(torch.bfloat16).to(torch.float32)
     head = qa.LmHead.from_rows_dev(ctx, rows, vocab, d)
     del rows
     table = torch.randn((vocab, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
     w_final = torch.ones(d, dtype=torch.float32, device="cuda")
-    logits = torch.empty(vocab, dtype=torch.float32, device="cuda")
-    h = torch.empty(d, dtype=torch.float32, device="cuda")
-    hn = torch.empty(d, dtype=torch.float32, device="cuda")
-    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    logits = torch.empty((nseq, vocab), dtype=torch.float32, device="cuda")
+    h = torch.empty((nseq, d), dtype=torch.float32, device="cuda")
+    hn = torch.empty((nseq, d), dtype=torch.float32, device="cuda")
+    tok = torch.zeros(nseq, dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream()
-    ids = rng.integers(0, vocab, prompt).astype(np.int32)
+    ids = rng.integers(0, vocab, (nseq, prompt)).astype(np.int32)
     hp = torch.empty((prompt, d), dtype=torch.float32, device="cuda")
     wn = max(B.prefill_workspace_size(prompt) for B in blocks)
-    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    wd = max(B.decode_batch_workspace_size(b) for B in blocks for b in batches)
+    ws = torch.empty(max(wn, wd), dtype=torch.uint8, device="cuda")
 
-    def prefill():
-        embed(ctx, table, vocab, d, ids, hp, st)
+    def prefill(b):
         for B in blocks:
             B.reset()
-            B.prefill_dev(hp, prompt, ws, wn, st)
-        rms_norm_dev(ctx, hp[prompt - 1], 1, d, w_final, 1e-5, hn, st)
-        head.logits_dev(hn, 1, logits, st)
-        argmax_dev(ctx, logits, 1, vocab, tok, st)
+        for sq in range(b):
+            embed(ctx, table, vocab, d, ids[sq], hp, st)
+            for B in blocks:
+                B.prefill_seq_dev(sq, hp, prompt, ws, wn, st)
+            rms_norm_dev(ctx, hp[prompt - 1], 1, d, w_final, 1e-5, hn[sq], st)
+        head.logits_dev(hn, b, logits, st)
+        argmax_dev(ctx, logits, b, vocab, tok, st)
 
-    def token(pos):
-        embed_dev(ctx, table, vocab, d, tok, 1, h, st)
-        for B in blocks:
-            B.decode_dev(h, pos, st)
-        rms_norm_dev(ctx, h, 1, d, w_final, 1e-5, hn, st)
-        head.logits_dev(hn, 1, logits, st)
-        argmax_dev(ctx, logits, 1, vocab, tok, st)
+    def token(b, pos):
+        embed_dev(ctx, table, vocab, d, tok, b, h, st)
+        if b == 1:
+            for B in blocks:
+                B.decode_dev(h[0], pos, st)
+        else:
+            p = [pos] * b
+            for B in blocks:
+                B.decode_batch_dev(h, p, ws, wd, st)
+        rms_norm_dev(ctx, h, b, d, w_final, 1e-5, hn, st)
+        head.logits_dev(hn, b, logits, st)
+        argmax_dev(ctx, logits, b, vocab, tok, st)
 
-    prefill()           # warm-up pass (first launches, allocator)
+    out = {}
+    prefill(1)          # warm-up pass (first launches, allocator)
+    token(1, prompt)
     torch.cuda.synchronize()
-    a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-    a.record(st)
-    prefill()
-    b.record(st)
-    for i in range(steps):
-        token(prompt + i)
-    c.record(st)
-    torch.cuda.synchronize()
-    pre_ms, dec_ms = a.elapsed_time(b), b.elapsed_time(c) / steps
-    finite = bool(torch.isfinite(logits).all())
+    for b in batches:
+        a, e1, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        a.record(st)
+        prefill(b)
+        e1.record(st)
+        for i in range(steps):
+            token(b, prompt + i)
+        c.record(st)
+        torch.cuda.synchronize()
+        pre_ms, dec_ms = a.elapsed_time(e1), e1.elapsed_time(c) / steps
+        finite = bool(torch.isfinite(logits[:b]).all())
+        log(f"  config 5 (B={b}): prefill of {b} x {prompt} tokens {pre_ms:.2f} ms, then {steps} greedy steps "
+            f"at {dec_ms:.3f} ms/step ({b * 1e3 / dec_ms:.1f} tokens/s)")
+        out[f"b{b}"] = {"batch": b, "prefill_ms": round(pre_ms, 2),
+                        "prefill_tokens_per_s": round(b * prompt / pre_ms * 1e3, 1),
+                        "decode_ms_per_step": round(dec_ms, 3),
+                        "decode_tokens_per_s": round(b * 1e3 / dec_ms, 1),
+                        "prompt_tokens": prompt, "decode_steps": steps, "logits_finite": finite}
     for B in blocks:
         B.close()
     head.close()
-    log(f"  config 5 (B=1): prefill of {prompt} tokens {pre_ms:.2f} ms, then {steps} greedy steps at "
-        f"{dec_ms:.3f} ms/token")
-    return {"prefill_ms": round(pre_ms, 2), "prefill_tokens_per_s": round(prompt / pre_ms * 1e3, 1),
-            "decode_ms_per_token": round(dec_ms, 3), "decode_tokens_per_s": round(1e3 / dec_ms, 1),
-            "prompt_tokens": prompt, "decode_steps": steps, "logits_finite": finite,
-            "shape": "32 blocks (d 4096, 32/8 heads x 128, ffn 14336, config-3 ranks, fp16-valued scales), "
-                     "embedding and lm_head 128256 x 4096, bf16 serving; prefill on the GEMM and the "
-                     "block-scaled SageAttention, decode on the GEMV and the sage decode attention"}
+    out["shape"] = ("32 blocks (d 4096, 32/8 heads x 128, ffn 14336, config-3 ranks, fp16-valued scales), "
+                    "embedding and lm_head 128256 x 4096, bf16 serving; prefill on the GEMM and the "
+                    "block-scaled SageAttention, decode on the GEMV (batch 1) or the GEMM (batch 32) and "
+                    "the sage decode attention")
+    return out
 
 
 def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
@@ -724,7 +743,7 @@ def main():
         extra["lm_head"] = bench_head(qa, ctx, torch, np)
         extra["decoder_block"] = bench_block(qa, ctx, torch, np)
         log("config 5: prefill + greedy decode (32 blocks + lm_head) ...")
-        extra["config5_b1"] = bench_model(qa, ctx, torch, np)
+        extra["config5"] = bench_model(qa, ctx, torch, np)
         log("config 3 (8B decoder layer projections) ...")
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")

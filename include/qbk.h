@@ -223,10 +223,35 @@ int qbk_block_reset(qbk_block *block);
 size_t qbk_block_prefill_workspace_size(const qbk_block *block, size_t n_tokens);
 int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *block, float *h, size_t n_tokens, void *workspace,
                           size_t workspace_size, void *stream);
-/* The block's KV cache (device, f32 [capacity][n_kv_heads * head_dim] each).
- * Rows written through these pointers are not seen by the attention state
- * until qbk_block_reset. */
+/* The block's KV cache (device, f32 [n_seqs][capacity][n_kv_heads * head_dim]
+ * each; sequence 0 first).  Rows written through these pointers are not seen
+ * by the attention state until qbk_block_reset. */
 int qbk_block_cache(const qbk_block *block, float **k_cache, float **v_cache);
+
+/* Batched serving (engine/mod.rs:1377-1476 steps a batch of sequences through
+ * the trunk; each sequence keeps its own cache): a block holding n_seqs
+ * (1 .. 64) independent sequences, each with a KV cache of `capacity` rows
+ * and its own attention state.  qbk_block_create is this with n_seqs = 1,
+ * and qbk_block_decode_dev / qbk_block_prefill_dev act on sequence 0. */
+int qbk_block_create_seqs(qbk_ctx *ctx, const qbk_factor *const *layers, const float *input_norm,
+                          size_t input_norm_len, const float *post_norm, size_t post_norm_len,
+                          const float *q_norm, const float *k_norm, size_t qk_norm_len, size_t n_heads,
+                          size_t n_kv_heads, size_t head_dim, double rope_theta, double rms_norm_eps,
+                          size_t capacity, size_t block_size, size_t n_seqs, qbk_block **out);
+/* qbk_block_prefill_dev for sequence `seq`. */
+int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *block, size_t seq, float *h, size_t n_tokens,
+                              void *workspace, size_t workspace_size, void *stream);
+/* One decode position of each of sequences 0 .. n - 1 (n <= n_seqs):
+ * h f32 [n][d_model] on the device (row i is sequence i's token), replaced
+ * by the block's outputs; pos (host, n entries) as qbk_block_decode_dev's
+ * pos per sequence.  The projections run at batch n (the decode GEMV up to
+ * batch 8, the bf16-MFMA GEMM beyond) and the attention steps every
+ * sequence's kept state in one set of launches.  `workspace` of at least
+ * qbk_block_decode_batch_workspace_size(block, n) bytes; nothing is
+ * allocated. */
+size_t qbk_block_decode_batch_workspace_size(const qbk_block *block, size_t n);
+int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *block, float *h, const size_t *pos, size_t n,
+                               void *workspace, size_t workspace_size, void *stream);
 
 /* ---- trunk pieces around the blocks (engine/mod.rs:763-800, 943) ---------- */
 

@@ -84,6 +84,11 @@ _SIGS = {
     "qbk_block_prefill_workspace_size": (_Z, [_P, _Z]),
     "qbk_block_prefill_dev": (_I, [_P, _P, _P, _Z, _P, _Z, _P]),
     "qbk_block_cache": (_I, [_P, _P, _P]),
+    "qbk_block_create_seqs": (_I, [_P, _P, _P, _Z, _P, _Z, _P, _P, _Z, _Z, _Z, _Z, C.c_double, C.c_double, _Z,
+                                   _Z, _Z, _P]),
+    "qbk_block_prefill_seq_dev": (_I, [_P, _P, _Z, _P, _Z, _P, _Z, _P]),
+    "qbk_block_decode_batch_workspace_size": (_Z, [_P, _Z]),
+    "qbk_block_decode_batch_dev": (_I, [_P, _P, _P, _P, _Z, _P, _Z, _P]),
     "qbk_attention_sage_decode_step_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _Z, _P, _P, _Z, _Z,
                                                 _Z, _P]),
     "qbk_head_create": (_I, [_P, _P, _Z, _Z, _Z, C.POINTER(_P)]),

@@ -43,11 +43,12 @@ struct qbk_block {
     float *w_in, *w_post;     // d each
     float *w_q, *w_k;         // head_dim each, or null (no per-head q/k norms)
     float2 *rope;             // [cap][hd / 2] (cos, sin) in f32, from f64
-    float *kc, *vc;           // [cap][Hk * hd] the block's KV cache
-    void *state;              // the attention's kept decode state
+    float *kc, *vc;           // [nseq][cap][Hk * hd] the block's KV caches
+    void *state;              // [nseq] the attention's kept decode states
     size_t state_bytes;
-    size_t tokens;            // cache rows the attention state's codes cover
-    size_t filled;            // cache rows holding this sequence's keys and values
+    size_t nseq;              // independent sequences: caches and states, sequence s at offset s
+    std::vector<size_t> tokens;  // per sequence: cache rows the attention state's codes cover
+    std::vector<size_t> filled;  // per sequence: cache rows holding its keys and values
     // per-call buffers
     uint16_t *xcat;           // bf16 [3 d] (q, k, v inputs), then [2 d] (gate, up)
     float *ycat;              // f32 [(H + 2 Hk) hd], then [2 ffn]
@@ -316,6 +317,87 @@ static BlkpPlan blkp_plan(const qbk_block *B, const qbk_factor *const L[7], size
     return p;
 }
 
+// ---- batched decode (one position of each of n sequences) -----------------
+
+#define BLKB_MAXSEQ QBK_DEC_MAXSEQ
+struct BlkbPos {
+    uint32_t p[BLKB_MAXSEQ];
+};
+
+// Row t (sequence t): per-head q/k norm and RoPE at pos.p[t] as blkd_qk_rope;
+// q to qr [n][H hd], k and v to row pos.p[t] of sequence t's cache.
+__global__ void __launch_bounds__(64) blkb_qk_rope(const float *q, const float *k, const float *v, const float2 *rope,
+                                                   BlkbPos pos, const float *wq, const float *wk, float eps, float *kc,
+                                                   float *vc, size_t kvs, float *qr, int H, int Hk, int hd) {
+    const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, half = hd / 2;
+    const size_t p = pos.p[t];
+    const bool is_q = head < H;
+    const int hh = is_q ? head : head - H;
+    const float *src = is_q ? q + ((size_t)t * H + hh) * hd : k + ((size_t)t * Hk + hh) * hd;
+    float *dst = is_q ? qr + ((size_t)t * H + hh) * hd : kc + t * kvs + (p * Hk + hh) * hd;
+    const float *w = is_q ? wq : wk;
+    float inv = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int j = lane; j < hd; j += 64) {
+            const float b = bf16_to_f32(f32_to_bf16(src[j]));
+            ss += b * b;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    }
+    const float2 *cs = rope + p * (size_t)half;
+    for (int j = lane; j < half; j += 64) {
+        float a = src[j], b = src[j + half];
+        if (w) {
+            a = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(a)) * inv * w[j]));
+            b = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(b)) * inv * w[j + half]));
+        }
+        const float2 c = cs[j];
+        dst[j] = a * c.x - b * c.y;
+        dst[j + half] = b * c.x + a * c.y;
+    }
+    if (!is_q) {
+        const float *vs = v + ((size_t)t * Hk + hh) * hd;
+        float *vr = vc + t * kvs + (p * Hk + hh) * hd;
+        for (int j = lane; j < hd; j += 64) vr[j] = vs[j];
+    }
+}
+
+struct BlkbPlan {
+    size_t o_x, o_q, o_k, o_v, o_qr, o_at, o_oo, o_h1, o_g, o_u, o_gemm, bytes;
+};
+
+static BlkbPlan blkb_plan(const qbk_block *B, size_t n) {
+    BlkbPlan p{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += round_up(bytes ? bytes : 4, 256);
+        return o;
+    };
+    const size_t d = B->d, qd = B->H * B->hd, kd = B->Hk * B->hd;
+    p.o_x = take(n * d * 2);
+    p.o_q = take(n * qd * 4);
+    p.o_k = take(n * kd * 4);
+    p.o_v = take(n * kd * 4);
+    p.o_qr = take(n * qd * 4);
+    p.o_at = take(n * qd * 4);
+    p.o_oo = take(n * d * 4);
+    p.o_h1 = take(n * d * 4);
+    p.o_g = take(n * B->ffn * 4);
+    p.o_u = take(n * B->ffn * 4);
+    size_t g = 0;
+    for (int i = 0; i < 7; i++) {
+        const size_t w = blkp_proj_ws(B->lay[i], n);
+        g = w > g ? w : g;
+    }
+    p.o_gemm = take(g);
+    p.bytes = off;
+    return p;
+}
+
 }  // namespace qbk
 
 using namespace qbk;
@@ -332,12 +414,14 @@ void qbk_block_destroy(qbk_block *B) {
     delete B;
 }
 
-int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float *input_norm,
-                     size_t input_norm_len, const float *post_norm, size_t post_norm_len, const float *q_norm,
-                     const float *k_norm, size_t qk_norm_len, size_t n_heads, size_t n_kv_heads,
-                     size_t head_dim, double rope_theta, double rms_norm_eps, size_t capacity,
-                     size_t block_size, qbk_block **out) {
+int qbk_block_create_seqs(qbk_ctx *ctx, const qbk_factor *const *layers, const float *input_norm,
+                          size_t input_norm_len, const float *post_norm, size_t post_norm_len, const float *q_norm,
+                          const float *k_norm, size_t qk_norm_len, size_t n_heads, size_t n_kv_heads,
+                          size_t head_dim, double rope_theta, double rms_norm_eps, size_t capacity,
+                          size_t block_size, size_t n_seqs, qbk_block **out) {
     int rc;
+    if (n_seqs == 0 || n_seqs > BLKB_MAXSEQ)
+        return fail(QBK_ERR_VALIDATION, fmt("decoder block holds 1 to %d sequences, got %zu", BLKB_MAXSEQ, n_seqs));
     if (!layers || !input_norm || !post_norm || !out) return fail(QBK_ERR_VALIDATION, "null argument");
     if (!q_norm != !k_norm)
         return fail(QBK_ERR_VALIDATION, "decoder block: q_norm and k_norm come together or not at all");
@@ -373,6 +457,9 @@ int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float 
     B->cap = capacity;
     B->block = block_size;
     B->eps = (float)rms_norm_eps;
+    B->nseq = n_seqs;
+    B->tokens.assign(n_seqs, 0);
+    B->filled.assign(n_seqs, 0);
     for (int i = 0; i < 7; i++) B->lay[i] = layers[i];
     B->o = layers[3];
     B->down = layers[6];
@@ -389,8 +476,8 @@ int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float 
     if ((rc = qbk_factor_set_create(ctx, qkv, 3, &B->qkv)) || (rc = qbk_factor_set_create(ctx, gu, 2, &B->gu)) ||
         (rc = alloc((void **)&B->w_in, d * 4)) || (rc = alloc((void **)&B->w_post, d * 4)) ||
         (q_norm && ((rc = alloc((void **)&B->w_q, hd * 4)) || (rc = alloc((void **)&B->w_k, hd * 4)))) ||
-        (rc = alloc((void **)&B->rope, capacity * (hd / 2) * 8)) || (rc = alloc((void **)&B->kc, kv)) ||
-        (rc = alloc((void **)&B->vc, kv)) || (rc = alloc(&B->state, B->state_bytes)) ||
+        (rc = alloc((void **)&B->rope, capacity * (hd / 2) * 8)) || (rc = alloc((void **)&B->kc, kv * n_seqs)) ||
+        (rc = alloc((void **)&B->vc, kv * n_seqs)) || (rc = alloc(&B->state, B->state_bytes * n_seqs)) ||
         (rc = alloc((void **)&B->xcat, 3 * d * 2)) ||
         (rc = alloc((void **)&B->ycat, ((H + 2 * Hk) * hd > 2 * ffn ? (H + 2 * Hk) * hd : 2 * ffn) * 4)) ||
         (rc = alloc((void **)&B->qrot, H * hd * 4)) || (rc = alloc((void **)&B->attn, H * hd * 4)) ||
@@ -429,6 +516,16 @@ int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float 
     return QBK_OK;
 }
 
+int qbk_block_create(qbk_ctx *ctx, const qbk_factor *const *layers, const float *input_norm,
+                     size_t input_norm_len, const float *post_norm, size_t post_norm_len, const float *q_norm,
+                     const float *k_norm, size_t qk_norm_len, size_t n_heads, size_t n_kv_heads,
+                     size_t head_dim, double rope_theta, double rms_norm_eps, size_t capacity,
+                     size_t block_size, qbk_block **out) {
+    return qbk_block_create_seqs(ctx, layers, input_norm, input_norm_len, post_norm, post_norm_len, q_norm, k_norm,
+                                 qk_norm_len, n_heads, n_kv_heads, head_dim, rope_theta, rms_norm_eps, capacity,
+                                 block_size, 1, out);
+}
+
 int qbk_block_cache(const qbk_block *B, float **k_cache, float **v_cache) {
     if (!B) return fail(QBK_ERR_VALIDATION, "null block");
     if (k_cache) *k_cache = B->kc;
@@ -441,9 +538,9 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     if (!B || !h) return fail(QBK_ERR_VALIDATION, "null argument");
     if (pos >= B->cap)
         return fail(QBK_ERR_VALIDATION, fmt("position %zu is past the block's cache capacity of %zu", pos, B->cap));
-    if (pos > B->filled)
+    if (pos > B->filled[0])
         return fail(QBK_ERR_VALIDATION,
-                    fmt("position %zu skips cache rows: the block holds %zu positions", pos, B->filled));
+                    fmt("position %zu skips cache rows: the block holds %zu positions", pos, B->filled[0]));
     if ((rc = bind(ctx))) return rc;
     if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
     hipStream_t s = (hipStream_t)stream;
@@ -457,12 +554,12 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
                        B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
     QBK_HIP(hipGetLastError());
     const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos + 1, B->hd, B->hd};
-    const size_t cached = B->tokens <= pos ? B->tokens : 0;
+    const size_t cached = B->tokens[0] <= pos ? B->tokens[0] : 0;
     if ((rc = qbk_attention_sage_decode_step_dev(ctx, &sh, B->qrot, B->kc, B->vc, B->block, B->attn, B->state,
                                                  B->state_bytes, B->cap, cached, stream)))
         return rc;
-    B->tokens = pos + 1;
-    B->filled = pos + 1;
+    B->tokens[0] = pos + 1;
+    B->filled[0] = pos + 1;
     if ((rc = q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s))) return rc;
     // MLP sublayer: h1 = o + h, then its norm
     hipLaunchKernelGGL(blkd_norm, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
@@ -479,8 +576,7 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
 
 int qbk_block_reset(qbk_block *B) {
     if (!B) return fail(QBK_ERR_VALIDATION, "null block");
-    B->tokens = 0;
-    B->filled = 0;
+    for (size_t i = 0; i < B->nseq; i++) B->tokens[i] = B->filled[i] = 0;
     return QBK_OK;
 }
 
@@ -489,10 +585,12 @@ size_t qbk_block_prefill_workspace_size(const qbk_block *B, size_t n_tokens) {
     return blkp_plan(B, B->lay, n_tokens).bytes;
 }
 
-int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t n, void *workspace, size_t workspace_size,
-                          void *stream) {
+int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *B, size_t seq, float *h, size_t n, void *workspace,
+                              size_t workspace_size, void *stream) {
     int rc;
     if (!B || !h) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (seq >= B->nseq)
+        return fail(QBK_ERR_VALIDATION, fmt("sequence %zu of a block holding %zu", seq, B->nseq));
     if (n == 0) return fail(QBK_ERR_VALIDATION, "prefill needs at least one token");
     if (n > B->cap)
         return fail(QBK_ERR_VALIDATION, fmt("prefill of %zu tokens exceeds the block's cache capacity of %zu", n, B->cap));
@@ -522,8 +620,9 @@ int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t n, void *
     if ((rc = blkp_proj(B->lay[0], n, x, false, q, ws, s)) || (rc = blkp_proj(B->lay[1], n, x, false, k, ws, s)) ||
         (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s)))
         return rc;
+    const size_t kvs = B->cap * B->Hk * B->hd;  // one sequence's cache floats
     hipLaunchKernelGGL(blkp_qk_rope, dim3(H + Hk, (unsigned)n), dim3(64), 0, s, q, k, v, B->rope, B->w_q, B->w_k,
-                       B->eps, B->kc, B->vc, qb, kb, vb, H, Hk, hd, (int)n);
+                       B->eps, B->kc + seq * kvs, B->vc + seq * kvs, qb, kb, vb, H, Hk, hd, (int)n);
     QBK_HIP(hipGetLastError());
     // causal block-scaled SageAttention over the n tokens
     const qbk_attn_shape sh{1, B->H, B->Hk, n, n, B->hd, B->hd};
@@ -545,8 +644,98 @@ int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t n, void *
     if ((rc = blkp_proj(B->down, n, g, true, oo, ws, s))) return rc;
     hipLaunchKernelGGL(blkp_add, dim3((unsigned)div_ceil(nd, 256)), dim3(256), 0, s, oo, h1, h, nd);
     QBK_HIP(hipGetLastError());
-    B->filled = n;
-    B->tokens = 0;  // the decode attention state rebuilds its codes from the cache
+    B->filled[seq] = n;
+    B->tokens[seq] = 0;  // the decode attention state rebuilds its codes from the cache
+    return QBK_OK;
+}
+
+int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t n, void *workspace, size_t workspace_size,
+                          void *stream) {
+    return qbk_block_prefill_seq_dev(ctx, B, 0, h, n, workspace, workspace_size, stream);
+}
+
+size_t qbk_block_decode_batch_workspace_size(const qbk_block *B, size_t n) {
+    if (!B || n == 0) return 0;
+    return blkb_plan(B, n).bytes;
+}
+
+// One position of each of sequences 0 .. n - 1 (sequence i at pos[i]): the
+// projections batched over the n rows (the GEMV at n <= 8, the GEMM beyond),
+// RoPE and the cache append per sequence, the sage decode attention per
+// sequence on its own kept state.
+int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_t *pos, size_t n, void *workspace,
+                               size_t workspace_size, void *stream) {
+    int rc;
+    if (!B || !h || !pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (n == 0 || n > B->nseq)
+        return fail(QBK_ERR_VALIDATION, fmt("batch of %zu sequences on a block holding %zu", n, B->nseq));
+    for (size_t i = 0; i < n; i++) {
+        if (pos[i] >= B->cap)
+            return fail(QBK_ERR_VALIDATION,
+                        fmt("position %zu is past the block's cache capacity of %zu", pos[i], B->cap));
+        if (pos[i] > B->filled[i])
+            return fail(QBK_ERR_VALIDATION, fmt("sequence %zu: position %zu skips cache rows: the block holds %zu "
+                                                "positions", i, pos[i], B->filled[i]));
+    }
+    const BlkbPlan P = blkb_plan(B, n);
+    if (!workspace || workspace_size < P.bytes)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("workspace of %zu bytes is smaller than the %zu this step needs", workspace_size, P.bytes));
+    if ((rc = bind(ctx))) return rc;
+    if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
+    hipStream_t s = (hipStream_t)stream;
+    char *w = (char *)workspace;
+    uint16_t *x = (uint16_t *)(w + P.o_x);
+    float *q = (float *)(w + P.o_q), *k = (float *)(w + P.o_k), *v = (float *)(w + P.o_v),
+          *qr = (float *)(w + P.o_qr), *at = (float *)(w + P.o_at), *oo = (float *)(w + P.o_oo),
+          *h1 = (float *)(w + P.o_h1), *g = (float *)(w + P.o_g), *u = (float *)(w + P.o_u);
+    void *ws = w + P.o_gemm;
+    const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk;
+    const size_t nd = n * B->d, nf = n * B->ffn, kvs = B->cap * B->Hk * B->hd;
+    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, h, (const float *)nullptr, (float *)nullptr,
+                       B->w_in, B->eps, x, d);
+    QBK_HIP(hipGetLastError());
+    if ((rc = blkp_proj(B->lay[0], n, x, false, q, ws, s)) || (rc = blkp_proj(B->lay[1], n, x, false, k, ws, s)) ||
+        (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s)))
+        return rc;
+    BlkbPos bp{};
+    for (size_t i = 0; i < n; i++) bp.p[i] = (uint32_t)pos[i];
+    hipLaunchKernelGGL(blkb_qk_rope, dim3(H + Hk, (unsigned)n), dim3(64), 0, s, q, k, v, B->rope, bp, B->w_q, B->w_k,
+                       B->eps, B->kc, B->vc, kvs, qr, H, Hk, hd);
+    QBK_HIP(hipGetLastError());
+    const qbk_attn_shape one{1, B->H, B->Hk, 1, B->cap, B->hd, B->hd};
+    const size_t qs = B->H * B->hd;
+    if (sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs)) {
+        size_t skv[BLKB_MAXSEQ], kept[BLKB_MAXSEQ];
+        for (size_t i = 0; i < n; i++) {
+            skv[i] = pos[i] + 1;
+            kept[i] = B->tokens[i] <= pos[i] ? B->tokens[i] : 0;
+        }
+        if ((rc = sage_decode_batch(&one, qr, qs, B->kc, B->vc, kvs, B->block, at, qs, B->state, B->state_bytes,
+                                    B->cap, skv, kept, n, s)))
+            return rc;
+    } else {
+        for (size_t i = 0; i < n; i++) {
+            const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos[i] + 1, B->hd, B->hd};
+            const size_t cached = B->tokens[i] <= pos[i] ? B->tokens[i] : 0;
+            if ((rc = qbk_attention_sage_decode_step_dev(ctx, &sh, qr + i * qs, B->kc + i * kvs, B->vc + i * kvs,
+                                                         B->block, at + i * qs,
+                                                         (char *)B->state + i * B->state_bytes, B->state_bytes,
+                                                         B->cap, cached, stream)))
+                return rc;
+        }
+    }
+    for (size_t i = 0; i < n; i++) B->tokens[i] = B->filled[i] = pos[i] + 1;
+    if ((rc = blkp_proj(B->o, n, at, true, oo, ws, s))) return rc;
+    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, oo, (const float *)h, h1, B->w_post, B->eps, x, d);
+    QBK_HIP(hipGetLastError());
+    if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) || (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s)))
+        return rc;
+    hipLaunchKernelGGL(blkp_swiglu, dim3((unsigned)div_ceil(nf, 256)), dim3(256), 0, s, g, u, g, nf);
+    QBK_HIP(hipGetLastError());
+    if ((rc = blkp_proj(B->down, n, g, true, oo, ws, s))) return rc;
+    hipLaunchKernelGGL(blkp_add, dim3((unsigned)div_ceil(nd, 256)), dim3(256), 0, s, oo, h1, h, nd);
+    QBK_HIP(hipGetLastError());
     return QBK_OK;
 }
 

@@ -83,6 +83,19 @@ int validate_packed(size_t packed_len, size_t n_rows, size_t n_bits, size_t *n_w
 static inline size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
 static inline size_t round_up(size_t a, size_t b) { return div_ceil(a, b) * b; }
 
+// Decode steps of up to QBK_DEC_MAXSEQ sequences in one set of launches
+// (sage.hip), for shapes where sage_decode_batchable holds: sequence i has
+// seq_kv[i] cache rows, the state's codes of its first cached[i] of them
+// kept from its last step; its query, caches, output and state sit i times
+// q_stride, kv_stride, o_stride (floats) and st_stride (bytes) past
+// sequence 0's.  `one` gives the heads and dims (its seq_kv is ignored).
+#define QBK_DEC_MAXSEQ 64
+bool sage_decode_batchable(const qbk_attn_shape *one, size_t block, size_t cap, const float *k, const float *v,
+                           size_t kv_stride);
+int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride, const float *k, const float *v,
+                      size_t kv_stride, size_t block, float *out, size_t o_stride, void *state, size_t st_stride,
+                      size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st);
+
 // ---- device helpers -------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {

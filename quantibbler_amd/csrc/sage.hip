@@ -661,6 +661,53 @@ struct DecArgs {
     float *mprev;                        // [H][nkb] running max before each block, or null
 };
 
+// Several sequences' decode steps in one set of launches: sequence s has
+// S[s] cached tokens, the codes of its first kb0[s] key blocks kept from its
+// last step, its query, output, caches and state at s times the strides
+// past those of sequence 0.  n == 0: a launch for the one sequence its
+// arguments describe.
+struct DecSeqTab {
+    uint32_t n;
+    uint32_t S[QBK_DEC_MAXSEQ], kb0[QBK_DEC_MAXSEQ];
+    size_t q_stride, o_stride, kv_stride;  // floats
+    size_t st_stride;                      // bytes
+};
+
+template <class T>
+__device__ __forceinline__ T *dec_shift(T *p, size_t bytes) {
+    return p ? (T *)((char *)p + bytes) : p;
+}
+
+__device__ __forceinline__ void dec_seq_ref(RefArgs &a, const DecSeqTab &t, uint32_t s) {
+    a.S = t.S[s];
+    a.nkb = (a.S + a.block - 1) / a.block;
+    a.kb0 = t.kb0[s];
+    a.q += s * t.q_stride;
+    a.out += s * t.o_stride;
+    a.k += s * t.kv_stride;
+    a.v += s * t.kv_stride;
+    const size_t b = s * t.st_stride;
+    a.kmean = dec_shift(a.kmean, b);
+    a.kdelta = dec_shift(a.kdelta, b);
+    a.khat = dec_shift(a.khat, b);
+    a.vd = dec_shift(a.vd, b);
+    a.vhat = dec_shift(a.vhat, b);
+}
+
+__device__ __forceinline__ void dec_seq(DecArgs &da, const DecSeqTab &t, uint32_t s) {
+    dec_seq_ref(da.r, t, s);
+    const size_t b = s * t.st_stride;
+    da.sc = dec_shift(da.sc, b);
+    da.bmax = dec_shift(da.bmax, b);
+    da.balpha = dec_shift(da.balpha, b);
+    da.besum = dec_shift(da.besum, b);
+    da.blive = dec_shift(da.blive, b);
+    da.pvt = dec_shift(da.pvt, b);
+    da.qsw = dec_shift(da.qsw, b);
+    da.qdl = dec_shift(da.qdl, b);
+    da.mprev = dec_shift(da.mprev, b);
+}
+
 // max over the workgroup (blockDim.x a multiple of 64, <= 1024)
 __device__ __forceinline__ float dec_wg_max(float v, float *red) {
 #pragma unroll
@@ -748,17 +795,28 @@ __device__ void dec_query_codes(const RefArgs &a, uint32_t bk, uint32_t *qsw, fl
 }
 
 // grid (max(nkb - kb0, 1), Hk, DPREP_KS + DPREP_VS + 1): the last slice
-// forms the query's codes (once per kv head, when qsw is given)
-__global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uint32_t *qsw, float *qdl) {
+// forms the query's codes (once per kv head, when qsw is given).  Batched
+// (t.n > 0): y runs over (sequence, kv head), x over the largest count of
+// blocks to quantise.
+__global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uint32_t *qsw, float *qdl,
+                                                     DecSeqTab t) {
     extern __shared__ __attribute__((aligned(16))) float tile[];  // [kj][row of this workgroup]
     __shared__ __attribute__((aligned(16))) float km[REF_MAXD];  // K means, then V scales
     __shared__ float kdl[256];                                    // deltas of this workgroup's tokens
     const uint32_t tid = threadIdx.x, z = blockIdx.z;
+    uint32_t bky = blockIdx.y;
+    if (t.n) {
+        const uint32_t sq = blockIdx.y / (uint32_t)a.Hk;
+        bky = blockIdx.y % (uint32_t)a.Hk;
+        dec_seq_ref(a, t, sq);
+        qsw = dec_shift(qsw, sq * t.st_stride);
+        qdl = dec_shift(qdl, sq * t.st_stride);
+    }
     if (z == DPREP_KS + DPREP_VS) {
-        if (blockIdx.x == 0 && qsw) dec_query_codes(a, blockIdx.y, qsw, qdl);
+        if (blockIdx.x == 0 && qsw) dec_query_codes(a, bky, qsw, qdl);
         return;
     }
-    const uint32_t kb = (uint32_t)a.kb0 + blockIdx.x, bk = blockIdx.y;
+    const uint32_t kb = (uint32_t)a.kb0 + blockIdx.x, bk = bky;
     if (kb >= a.nkb) return;
     const uint32_t j0 = kb * (uint32_t)a.block;
     const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
@@ -1052,8 +1110,9 @@ __global__ void __launch_bounds__(256) sage_dec_scores(DecArgs da) {
 // itself would read O(nkb^2) values): mprev[kb] = max(MASKED, bmax[0..kb-1]),
 // a max, so a parallel scan gives the reference's sequential value.  One
 // workgroup per head, 8 blocks a thread, 2048 blocks a pass.
-__global__ void __launch_bounds__(256) sage_dec_runmax(DecArgs da) {
+__global__ void __launch_bounds__(256) sage_dec_runmax(DecArgs da, DecSeqTab t) {
     __shared__ float wm[4];
+    if (t.n) dec_seq(da, t, blockIdx.y);
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t h = blockIdx.x, nkb = da.r.nkb;
     const float *bm = da.bmax + h * nkb;
@@ -1225,7 +1284,8 @@ __global__ void __launch_bounds__(256) sage_dec_pv(DecArgs da) {
 // the code is kept short: a launch this small is bound by its serial
 // instruction stream, fetches included.
 #define DEC_CB 32
-__global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da) {
+__global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da, DecSeqTab t) {
+    if (t.n) dec_seq(da, t, blockIdx.y);
     const RefArgs &a = da.r;
     __shared__ float sa[DEC_CB], se[DEC_CB];
     __shared__ int sl[DEC_CB];
@@ -1280,8 +1340,10 @@ __global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da) {
 #define DEC_KMAX 256
 #define DEC_PMAX 512
 
-__global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da) {
+__global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da, DecSeqTab t) {
+    if (t.n) dec_seq(da, t, blockIdx.z);
     const RefArgs &a = da.r;
+    if (blockIdx.x >= a.nkb) return;  // a batched launch covers the longest sequence's blocks
     __shared__ uint32_t qs[DEC_GMAX * (REF_MAXD / 4)];
     __shared__ float qd[DEC_GMAX];
     __shared__ float kms[REF_MAXD];
@@ -1364,8 +1426,10 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da) {
     }
 }
 
-__global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da) {
+__global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
+    if (t.n) dec_seq(da, t, blockIdx.z);
     const RefArgs &a = da.r;
+    if (blockIdx.x >= a.nkb) return;
     __shared__ __attribute__((aligned(16))) float pf[DEC_GMAX * DEC_KMAX];
     __shared__ __attribute__((aligned(16))) uint8_t ph[DEC_GMAX * DEC_KMAX];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1564,19 +1628,11 @@ static int validate_decode(const qbk_attn_shape *s, size_t block_size, const siz
     return QBK_OK;
 }
 
-// One step over seq_kv cached tokens with a workspace laid out for cap; the
-// products of the key blocks that were complete at cached tokens are taken
-// as they are (the caller guarantees that those cache rows are the ones the
-// workspace's earlier step quantised) and the rest are quantised again.
-static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, const float *v,
-                      size_t block, float *out, void *ws, size_t cap, size_t cached, hipStream_t st) {
-    DecPlan P = dec_plan(s, block, cap);
-    DecArgs da = P.da;
+static const DecSeqTab kNoSeqs{};
+
+// Binds a decode plan's workspace pointers to ws.
+static void dec_bind(const DecPlan &P, DecArgs &da, void *ws) {
     RefArgs &a = da.r;
-    a.q = q;
-    a.k = k;
-    a.v = v;
-    a.out = out;
     char *w = (char *)ws;
     a.kmean = (float *)(w + P.o_kmean);
     a.kdelta = (float *)(w + P.o_kdelta);
@@ -1592,6 +1648,23 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     da.qsw = (uint32_t *)(w + P.o_qsw);
     da.qdl = (float *)(w + P.o_qdl);
     da.mprev = nullptr;
+}
+
+// One step over seq_kv cached tokens with a workspace laid out for cap; the
+// products of the key blocks that were complete at cached tokens are taken
+// as they are (the caller guarantees that those cache rows are the ones the
+// workspace's earlier step quantised) and the rest are quantised again.
+static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, const float *v,
+                      size_t block, float *out, void *ws, size_t cap, size_t cached, hipStream_t st) {
+    DecPlan P = dec_plan(s, block, cap);
+    DecArgs da = P.da;
+    RefArgs &a = da.r;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    char *w = (char *)ws;
+    dec_bind(P, da, ws);
     const unsigned nkb = (unsigned)a.nkb, H = (unsigned)a.H;
     a.kb0 = cached / block;
     const DPrepGeom g = dprep_geom(a, k, v);
@@ -1600,7 +1673,8 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     if (g.ok && (a.kb0 < a.nkb || grouped)) {
         const unsigned nx = (unsigned)(a.kb0 < a.nkb ? a.nkb - a.kb0 : 1);
         hipLaunchKernelGGL(sage_dec_prep, dim3(nx, (unsigned)a.Hk, DPREP_KS + DPREP_VS + (grouped ? 1 : 0)),
-                           dim3(256), g.lds, st, a, g, grouped ? da.qsw : nullptr, grouped ? da.qdl : nullptr);
+                           dim3(256), g.lds, st, a, g, grouped ? da.qsw : nullptr, grouped ? da.qdl : nullptr,
+                           kNoSeqs);
         QBK_HIP(hipGetLastError());
     } else if (a.kb0 < a.nkb) {
         hipLaunchKernelGGL(sage_ref_prep, dim3((unsigned)(a.nkb - a.kb0), (unsigned)a.Hk), dim3(256),
@@ -1608,16 +1682,16 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
         QBK_HIP(hipGetLastError());
     }
     if (grouped) {
-        hipLaunchKernelGGL(sage_dec_scores_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da);
+        hipLaunchKernelGGL(sage_dec_scores_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da, kNoSeqs);
         QBK_HIP(hipGetLastError());
         if (a.nkb > DEC_PMAX) {
             da.mprev = (float *)(w + P.o_mprev);
-            hipLaunchKernelGGL(sage_dec_runmax, dim3(H), dim3(256), 0, st, da);
+            hipLaunchKernelGGL(sage_dec_runmax, dim3(H), dim3(256), 0, st, da, kNoSeqs);
             QBK_HIP(hipGetLastError());
         }
-        hipLaunchKernelGGL(sage_dec_pv_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da);
+        hipLaunchKernelGGL(sage_dec_pv_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da, kNoSeqs);
         QBK_HIP(hipGetLastError());
-        hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da);
+        hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da, kNoSeqs);
         QBK_HIP(hipGetLastError());
         return QBK_OK;
     }
@@ -1625,12 +1699,82 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     QBK_HIP(hipGetLastError());
     if (a.nkb > DEC_PMAX) {
         da.mprev = (float *)(w + P.o_mprev);
-        hipLaunchKernelGGL(sage_dec_runmax, dim3(H), dim3(256), 0, st, da);
+        hipLaunchKernelGGL(sage_dec_runmax, dim3(H), dim3(256), 0, st, da, kNoSeqs);
         QBK_HIP(hipGetLastError());
     }
     hipLaunchKernelGGL(sage_dec_pv, dim3(nkb, H), dim3(256), 0, st, da);
     QBK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da);
+    hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da, kNoSeqs);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+// The grouped kernels' batched form (sequences along the grid's last
+// dimension) fits a shape when its widest block does: the geometry at
+// seq_kv = cap bounds every sequence's.
+static bool dec_batch_plan(const qbk_attn_shape *one, size_t block, size_t cap, const float *k, const float *v,
+                           size_t kv_stride, DecPlan &P, DPrepGeom &g) {
+    qbk_attn_shape sh = *one;
+    sh.seq_kv = cap;
+    P = dec_plan(&sh, block, cap);
+    const RefArgs &a = P.da.r;
+    g = dprep_geom(a, k, v);
+    const size_t G = a.H / a.Hk, kjm = block < cap ? block : cap;
+    return g.ok && G <= DEC_GMAX && kjm <= DEC_KMAX && a.d % 16 == 0 && a.blk4 % 4 == 0 && kv_stride % 4 == 0;
+}
+
+bool sage_decode_batchable(const qbk_attn_shape *one, size_t block, size_t cap, const float *k, const float *v,
+                           size_t kv_stride) {
+    DecPlan P;
+    DPrepGeom g;
+    return one && block && cap && dec_batch_plan(one, block, cap, k, v, kv_stride, P, g);
+}
+
+int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride, const float *k, const float *v,
+                      size_t kv_stride, size_t block, float *out, size_t o_stride, void *state, size_t st_stride,
+                      size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st) {
+    DecPlan P;
+    DPrepGeom g;
+    if (n == 0 || n > QBK_DEC_MAXSEQ || !dec_batch_plan(one, block, cap, k, v, kv_stride, P, g))
+        return fail(QBK_ERR_VALIDATION, "sage decode: no batched form for this shape");
+    DecArgs da = P.da;
+    RefArgs &a = da.r;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    dec_bind(P, da, state);
+    DecSeqTab t{};
+    t.n = (uint32_t)n;
+    t.q_stride = q_stride;
+    t.o_stride = o_stride;
+    t.kv_stride = kv_stride;
+    t.st_stride = st_stride;
+    size_t mkb = 0, mx = 1;
+    for (size_t i = 0; i < n; i++) {
+        if (seq_kv[i] == 0 || seq_kv[i] > cap || cached[i] > seq_kv[i])
+            return fail(QBK_ERR_VALIDATION, fmt("sage decode: sequence %zu holds %zu tokens (%zu kept) in a "
+                                                "capacity of %zu", i, seq_kv[i], cached[i], cap));
+        const size_t nkb = div_ceil(seq_kv[i], block), kb0 = cached[i] / block;
+        t.S[i] = (uint32_t)seq_kv[i];
+        t.kb0[i] = (uint32_t)kb0;
+        mkb = nkb > mkb ? nkb : mkb;
+        mx = nkb - kb0 > mx ? nkb - kb0 : mx;
+    }
+    const unsigned Hk = (unsigned)a.Hk, H = (unsigned)a.H, ns = (unsigned)n;
+    hipLaunchKernelGGL(sage_dec_prep, dim3((unsigned)mx, Hk * ns, DPREP_KS + DPREP_VS + 1), dim3(256), g.lds, st, a,
+                       g, da.qsw, da.qdl, t);
+    QBK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(sage_dec_scores_g, dim3((unsigned)mkb, Hk, ns), dim3(256), 0, st, da, t);
+    QBK_HIP(hipGetLastError());
+    if (mkb > DEC_PMAX) {
+        da.mprev = (float *)((char *)state + P.o_mprev);
+        hipLaunchKernelGGL(sage_dec_runmax, dim3(H, ns), dim3(256), 0, st, da, t);
+        QBK_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(sage_dec_pv_g, dim3((unsigned)mkb, Hk, ns), dim3(256), 0, st, da, t);
+    QBK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(sage_dec_combine, dim3(H, ns), dim3(256), 0, st, da, t);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

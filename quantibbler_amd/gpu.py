@@ -330,7 +330,7 @@ class DecoderBlock:
 
     def __init__(self, ctx: GpuContext, layers, input_norm, post_norm, n_heads: int,
                  n_kv_heads: int, head_dim: int, rope_theta: float, rms_norm_eps: float,
-                 capacity: int, block_size: int = 64, q_norm=None, k_norm=None):
+                 capacity: int, block_size: int = 64, q_norm=None, k_norm=None, n_seqs: int = 1):
         if len(layers) != 7:
             raise _lib.KernelError("a decoder block takes 7 layers: q, k, v, o, gate, up, down")
         self.ctx = ctx
@@ -345,12 +345,14 @@ class DecoderBlock:
         if wq is not None and wk is not None and wk.size != wq.size:
             raise _lib.KernelError(f"decoder block: q/k norm weights of {wq.size} and {wk.size} floats differ")
         out = C.c_void_p()
-        check(_lib.load().qbk_block_create(ctx.handle, arr, _ptr(w_in), w_in.size, _ptr(w_post), w_post.size,
-                                           _ptr(wq), _ptr(wk), qk_len, int(n_heads), int(n_kv_heads),
-                                           int(head_dim), float(rope_theta), float(rms_norm_eps),
-                                           int(capacity), int(block_size), C.byref(out)))
+        check(_lib.load().qbk_block_create_seqs(ctx.handle, arr, _ptr(w_in), w_in.size, _ptr(w_post),
+                                                w_post.size, _ptr(wq), _ptr(wk), qk_len, int(n_heads),
+                                                int(n_kv_heads), int(head_dim), float(rope_theta),
+                                                float(rms_norm_eps), int(capacity), int(block_size), int(n_seqs),
+                                                C.byref(out)))
         self._h = out
         self.capacity = int(capacity)
+        self.n_seqs = int(n_seqs)
 
     def decode_dev(self, h, pos: int, stream=None):
         """h: device f32 [d_model] (a contiguous torch tensor, or a raw device
@@ -382,6 +384,36 @@ class DecoderBlock:
                     f"values; got {h.dtype} of {h.numel()} on {h.device}")
         check(_lib.load().qbk_block_prefill_dev(self.ctx.handle, self._h, _ptr(h), int(n_tokens), _ptr(workspace),
                                                 int(workspace_size), _stream(stream)))
+
+    def prefill_seq_dev(self, seq: int, h, n_tokens: int, workspace, workspace_size: int, stream=None):
+        """prefill_dev for sequence ``seq`` of a block holding several."""
+        self._check_rows(h, int(n_tokens), "prefill input")
+        check(_lib.load().qbk_block_prefill_seq_dev(self.ctx.handle, self._h, int(seq), _ptr(h), int(n_tokens),
+                                                    _ptr(workspace), int(workspace_size), _stream(stream)))
+
+    def decode_batch_workspace_size(self, n: int) -> int:
+        return int(_lib.load().qbk_block_decode_batch_workspace_size(self._h, int(n)))
+
+    def decode_batch_dev(self, h, positions, workspace, workspace_size: int, stream=None):
+        """One position of each of sequences 0 .. n - 1: h device f32
+        [n][d_model], row i sequence i's token, replaced by the block's
+        outputs; positions[i] as decode_dev's pos for sequence i."""
+        pos = np.ascontiguousarray(positions, np.uint64).ravel()
+        n = pos.size
+        self._check_rows(h, n, "batched decode input")
+        check(_lib.load().qbk_block_decode_batch_dev(self.ctx.handle, self._h, _ptr(h),
+                                                     _ptr(pos), n, _ptr(workspace),
+                                                     int(workspace_size), _stream(stream)))
+
+    def _check_rows(self, h, n: int, what: str):
+        if hasattr(h, "is_cuda"):
+            if not h.is_cuda or str(h.dtype) != "torch.float32" or not h.is_contiguous() \
+                    or h.numel() != self.d_model * n:
+                raise _lib.KernelError(
+                    f"{what} must be a contiguous float32 device tensor of {n} x {self.d_model} "
+                    f"values; got {h.dtype} of {h.numel()} on {h.device}")
+        elif not isinstance(h, int):
+            raise _lib.KernelError(f"{what} must be a device tensor or a device address")
 
     def reset(self):
         check(_lib.load().qbk_block_reset(self._h))

@@ -227,12 +227,12 @@ class DeviceModel:
     from a ModelDir; torch supplies the device buffers (plumbing only -- every
     step runs in libqbk)."""
 
-    def __init__(self, ctx, md: ModelDir, capacity: int, block_size: int = 64):
+    def __init__(self, ctx, md: ModelDir, capacity: int, block_size: int = 64, n_seqs: int = 1):
         import torch
 
         from .gpu import DecoderBlock, FactorLayer, LmHead
 
-        self.ctx, self.md, self.capacity = ctx, md, int(capacity)
+        self.ctx, self.md, self.capacity, self.n_seqs = ctx, md, int(capacity), int(n_seqs)
         dev = torch.device("cuda")
         self.layers, self.blocks = [], []
         for b in range(md.n_layers):
@@ -241,27 +241,32 @@ class DeviceModel:
             norms = {k: _bf16_values(v) for k, v in md.block_norms(b).items()}
             self.blocks.append(DecoderBlock(ctx, layers, norms["input"], norms["post_attention"], md.n_heads,
                                             md.n_kv_heads, md.head_dim, md.rope_theta, md.rms_norm_eps,
-                                            capacity, block_size, norms.get("q_norm"), norms.get("k_norm")))
+                                            capacity, block_size, norms.get("q_norm"), norms.get("k_norm"),
+                                            n_seqs=self.n_seqs))
         self.embedding = torch.from_numpy(_bf16_values(md.embedding)).to(dev)
         self.final_norm = torch.from_numpy(_bf16_values(md.final_norm())).to(dev)
         self.head = LmHead.from_rows(ctx, _bf16_values(md.head_rows()))
         self.h = torch.empty(md.d_model, dtype=torch.float32, device=dev)
         self.hn = torch.empty(md.d_model, dtype=torch.float32, device=dev)
         self.logits = torch.empty(md.vocab_size, dtype=torch.float32, device=dev)
-        self.pos = 0
+        self.pos = 0                        # sequence 0's, the one step() serves
+        self.positions = [0] * self.n_seqs  # every sequence's
+        self._batch = {}                    # n -> (h, hn, logits, workspace) of step_batch
 
     def reset(self):
         for b in self.blocks:
             b.reset()
         self.pos = 0
+        self.positions = [0] * self.n_seqs
 
-    def prefill(self, tokens, stream=None):
-        """forward_prefill (engine/mod.rs:811-822) of a new sequence in one
-        pass per block: the tokens' embedding rows through every block's
-        prefill (batched projections, causal block-scaled SageAttention), then
-        the final norm and logits of the last position -- the logits a
-        token-at-a-time prefill ends with.  Returns them (a device tensor,
-        overwritten by the next call); decoding continues with step()."""
+    def prefill(self, tokens, stream=None, seq: int = 0):
+        """forward_prefill (engine/mod.rs:811-822) of a new sequence (held as
+        sequence ``seq``) in one pass per block: the tokens' embedding rows
+        through every block's prefill (batched projections, causal
+        block-scaled SageAttention), then the final norm and logits of the
+        last position -- the logits a token-at-a-time prefill ends with.
+        Returns them (a device tensor, overwritten by the next call);
+        decoding continues with step() (sequence 0) or step_batch()."""
         import torch
 
         from .gpu import embed, rms_norm_dev
@@ -274,11 +279,49 @@ class DeviceModel:
         need = max(b.prefill_workspace_size(n) for b in self.blocks)
         ws = torch.empty(need, dtype=torch.uint8, device="cuda")
         for b in self.blocks:
-            b.prefill_dev(h, n, ws, need, stream)
+            b.prefill_seq_dev(int(seq), h, n, ws, need, stream)
         rms_norm_dev(self.ctx, h[n - 1], 1, md.d_model, self.final_norm, md.rms_norm_eps, self.hn, stream)
         self.head.logits_dev(self.hn, 1, self.logits, stream)
-        self.pos = n
+        self.positions[int(seq)] = n
+        if int(seq) == 0:
+            self.pos = n
         return self.logits
+
+    def step_batch(self, tokens, stream=None):
+        """One position of each of sequences 0 .. n - 1 (the batched decode of
+        engine/mod.rs:1377-1476): ``tokens`` n host ids, or a device int32
+        tensor of n ids (a greedy loop's argmax output, fed back without a
+        host round trip).  Returns the logits [n][vocab] (a device tensor,
+        overwritten by the next call of the same n)."""
+        import torch
+
+        from .gpu import embed, embed_dev, rms_norm_dev
+
+        md = self.md
+        dev_ids = hasattr(tokens, "is_cuda")
+        n = int(tokens.numel()) if dev_ids else len(tokens)
+        if n == 0 or n > self.n_seqs:
+            raise ValueError(f"a batch of {n} sequences on a model holding {self.n_seqs}")
+        if n not in self._batch:
+            wn = max(b.decode_batch_workspace_size(n) for b in self.blocks)
+            self._batch[n] = (torch.empty((n, md.d_model), dtype=torch.float32, device="cuda"),
+                              torch.empty((n, md.d_model), dtype=torch.float32, device="cuda"),
+                              torch.empty((n, md.vocab_size), dtype=torch.float32, device="cuda"),
+                              torch.empty(wn, dtype=torch.uint8, device="cuda"), wn)
+        h, hn, logits, ws, wn = self._batch[n]
+        if dev_ids:
+            embed_dev(self.ctx, self.embedding, md.vocab_size, md.d_model, tokens, n, h, stream)
+        else:
+            embed(self.ctx, self.embedding, md.vocab_size, md.d_model, [int(t) for t in tokens], h, stream)
+        pos = self.positions[:n]
+        for b in self.blocks:
+            b.decode_batch_dev(h, pos, ws, wn, stream)
+        rms_norm_dev(self.ctx, h, n, md.d_model, self.final_norm, md.rms_norm_eps, hn, stream)
+        self.head.logits_dev(hn, n, logits, stream)
+        for i in range(n):
+            self.positions[i] += 1
+        self.pos = self.positions[0]
+        return logits
 
     def step(self, token: int, stream=None):
         """The next position's logits (a device tensor, overwritten by the
@@ -292,6 +335,7 @@ class DeviceModel:
         rms_norm_dev(self.ctx, self.h, 1, md.d_model, self.final_norm, md.rms_norm_eps, self.hn, stream)
         self.head.logits_dev(self.hn, 1, self.logits, stream)
         self.pos += 1
+        self.positions[0] = self.pos
         return self.logits
 
     def close(self):

@@ -172,3 +172,77 @@ def test_block_prefill_then_decode(ctx, orc, n):
         print(f"decode after prefill, pos {pos}: cos {cos:.7f} rel {rel:.2e}", flush=True)
         assert cos >= COS_MIN and rel <= REL_MAX, (pos, cos, rel)
     block.close()
+
+
+def test_block_batched_decode(ctx, orc):
+    """A block holding ten sequences: each prefilled to its own length (0 ..
+    130 tokens, sequence by sequence), then decode steps of all ten at once
+    (projections at batch 10 on the GEMM, the attention stepping every
+    sequence's kept state in one set of launches), then a step of the first
+    three only (batch 3, the GEMV): every row against the oracle's block
+    arithmetic on that sequence's own cache, to the block's tolerance."""
+    from quantibbler_amd import DecoderBlock, FactorLayer
+
+    d, H, Hk, hd, ffn, cap, blk = 256, 4, 2, 128, 512, 160, 64
+    theta, eps = 500000.0, 1e-5
+    lens = [0, 5, 70, 130, 1, 64, 0, 9, 33, 128]
+    ns = len(lens)
+    rng = np.random.default_rng(901)
+    shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
+              (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    bfv = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a.astype(np.float32)))
+    norms = {"input": bfv(1.0 + 0.1 * rng.standard_normal(d)), "post_attention": bfv(1.0 + 0.1 * rng.standard_normal(d)),
+             "q_norm": bfv(1.0 + 0.2 * rng.standard_normal(hd)), "k_norm": bfv(1.0 + 0.2 * rng.standard_normal(hd))}
+    block = DecoderBlock(ctx, devs, norms["input"], norms["post_attention"], H, Hk, hd, theta, eps, cap, blk,
+                         norms["q_norm"], norms["k_norm"], n_seqs=ns)
+    st = torch.cuda.current_stream()
+    kcs = [np.zeros((cap, Hk * hd), np.float32) for _ in range(ns)]
+    vcs = [np.zeros((cap, Hk * hd), np.float32) for _ in range(ns)]
+    for s, n in enumerate(lens):
+        if n == 0:
+            continue
+        h = rng.standard_normal((n, d)).astype(np.float32)
+        hdv = torch.from_numpy(h).cuda()
+        wn = block.prefill_workspace_size(n)
+        ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+        block.prefill_seq_dev(s, hdv, n, ws, wn, st)
+        torch.cuda.synchronize()
+        want = orc.block_prefill(layers, norms, h, kcs[s], vcs[s], H, Hk, hd, theta, eps)
+        cos, rel = metrics(hdv.cpu().numpy(), want)
+        assert cos >= COS_MIN and rel <= REL_MAX, (s, cos, rel)
+    pos = list(lens)
+    for n in (ns, ns, 3):
+        x = rng.standard_normal((n, d)).astype(np.float32)
+        xd = torch.from_numpy(x).cuda()
+        wn = block.decode_batch_workspace_size(n)
+        ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+        block.decode_batch_dev(xd, pos[:n], ws, wn, st)
+        torch.cuda.synchronize()
+        got = xd.cpu().numpy()
+        for s in range(n):
+            want = orc.block_step(layers, norms, x[s], pos[s], kcs[s], vcs[s], H, Hk, hd, theta, eps, "bf16",
+                                  "sage", blk)
+            cos, rel = metrics(got[s], want)
+            print(f"batch {n}: sequence {s} at pos {pos[s]}: cos {cos:.7f} rel {rel:.2e}", flush=True)
+            assert cos >= COS_MIN and rel <= REL_MAX, (n, s, pos[s], cos, rel)
+        for s in range(n):
+            pos[s] += 1
+    # validation of the batched step
+    from quantibbler_amd import KernelError
+
+    h = torch.zeros((ns + 1) * d, dtype=torch.float32, device="cuda")
+    ws = torch.empty(block.decode_batch_workspace_size(ns), dtype=torch.uint8, device="cuda")
+    with pytest.raises(KernelError, match="batch of 11 sequences on a block holding 10"):
+        block.decode_batch_dev(h, [0] * (ns + 1), ws, ws.numel(), st)
+    with pytest.raises(KernelError, match=r"sequence 1: position 9 skips cache rows: the block holds 8 positions"):
+        block.decode_batch_dev(h[:2 * d], [0, 9], ws, ws.numel(), st)
+    with pytest.raises(KernelError, match="position 160 is past the block's cache capacity of 160"):
+        block.decode_batch_dev(h[:d], [160], ws, ws.numel(), st)
+    with pytest.raises(KernelError, match="workspace of 16 bytes is smaller"):
+        block.decode_batch_dev(h[:d], [0], ws, 16, st)
+    with pytest.raises(KernelError, match="sequence 10 of a block holding 10"):
+        block.prefill_seq_dev(10, h[:d], 1, ws, ws.numel(), st)
+    block.close()

@@ -227,3 +227,68 @@ def test_device_trunk_prefill_then_decode(ctx, orc):
         say(f"  decode logits rel {rel:.2e}")
         assert rel <= 1e-2
     m.close()
+
+
+def _oracle_prefill(orc, md, tokens, capacity):
+    """The oracle trunk of one sequence after its prefill: the per-block
+    arithmetic DeviceModel.prefill runs (block_prefill over the tokens'
+    embedding rows), and the last position's logits."""
+    ref = orc.Trunk(md, serving="bf16", attention="sage", capacity=capacity)
+    h = ref.embedding[np.array(tokens)].copy()
+    for b, (layers, norms) in enumerate(ref.blocks):
+        h = orc.block_prefill(layers, norms, h, ref.kc[b], ref.vc[b], md.n_heads, md.n_kv_heads, md.head_dim,
+                              md.rope_theta, md.rms_norm_eps)
+    ref.pos = len(tokens)
+    hn = orc.norm_apply(h[-1], ref.final_norm, md.rms_norm_eps, "bf16")
+    return ref, orc.head_logits(ref.head, hn)
+
+
+def test_device_trunk_batched_greedy(ctx, orc):
+    """Batched serving: ten sequences, each prefilled to its own length, then
+    greedy steps of all ten together (DeviceModel.step_batch: projections at
+    batch 10 on the GEMM, every sequence's attention on its own cache), the
+    ids once from the host and once as a device tensor, then a step of the
+    first three (batch 3, the GEMV): each sequence's logits against its own
+    oracle trunk, which takes the same greedy ids.
+
+    The budget is the one the single-sequence trunk tests hold each row to
+    (1e-2 relative on the logits), here on the mean over the 47 rows, with
+    each row within twice it: a bf16 rounding or an int8 code of the sage
+    attention that lands on the other side of a tie moves one row's logits
+    by up to about 1e-2, and over many rows one of them does."""
+    from quantibbler_amd.model import DeviceModel
+
+    say("device trunk batched greedy decode")
+    md = synthetic_model(orc, 818)
+    lens = [70, 3, 1, 20, 64, 65, 9, 2, 33, 5]
+    ns, cap = len(lens), 96
+    rng = np.random.default_rng(819)
+    m = DeviceModel(ctx, md, capacity=cap, n_seqs=ns)
+    st = torch.cuda.current_stream()
+    refs, nxt, rels = [], [], []
+    for s, n in enumerate(lens):
+        tokens = rng.integers(0, md.vocab_size, n).tolist()
+        got = m.prefill(tokens, st, seq=s).cpu().numpy()
+        ref, want = _oracle_prefill(orc, md, tokens, cap)
+        rels.append(float(np.linalg.norm(got - want) / np.linalg.norm(want)))
+        refs.append(ref)
+        nxt.append(int(np.argmax(want)))
+    say(f"  prefill logits rel per sequence: {' '.join(f'{r:.1e}' for r in rels)}")
+    assert m.positions == lens
+    for step, n in enumerate((ns, ns, 3)):
+        ids = nxt[:n] if step != 1 else torch.tensor(nxt[:n], dtype=torch.int32, device="cuda")
+        got = m.step_batch(ids, st).cpu().numpy()
+        assert got.shape == (n, md.vocab_size)
+        row = []
+        for s in range(n):
+            want = refs[s].step(nxt[s])
+            row.append(float(np.linalg.norm(got[s] - want) / np.linalg.norm(want)))
+            nxt[s] = int(np.argmax(want))
+        say(f"  batch {n}: logits rel per sequence: {' '.join(f'{r:.1e}' for r in row)}")
+        rels += row
+    say(f"  mean {np.mean(rels):.2e}, max {np.max(rels):.2e} over {len(rels)} rows")
+    assert np.mean(rels) <= 1e-2 and np.max(rels) <= 2e-2, (np.mean(rels), np.max(rels))
+    assert m.positions == [p + 3 for p in lens[:3]] + [p + 2 for p in lens[3:]]
+    with pytest.raises(ValueError, match="a batch of 11 sequences on a model holding 10"):
+        m.step_batch([0] * 11, st)
+    m.close()
