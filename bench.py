@@ -670,6 +670,8 @@ def main():
     ap.add_argument("--only", choices=["gemm", "sage", "cfg3", "sage_decode", "head", "block", "model"],
                     help="run one secondary workload alone and print its figures (for profiling); "
                          "no headline line")
+    ap.add_argument("--model-steps", type=int, default=256, help="config 5's greedy decode steps")
+    ap.add_argument("--model-batches", default="1,32", help="config 5's batch sizes, comma-separated")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-traffic", action="store_true",
                     help="first run an elementwise kernel of known traffic (256 MiB read, 256 MiB "
@@ -699,7 +701,8 @@ def main():
         elif args.only == "block":
             res = bench_block(qa, ctx, torch, np)
         elif args.only == "model":
-            res = bench_model(qa, ctx, torch, np)
+            res = bench_model(qa, ctx, torch, np, steps=args.model_steps,
+                              batches=tuple(int(b) for b in args.model_batches.split(",")))
         else:
             res = bench_cfg3(qa, ctx, torch, np)
         print(json.dumps({"only": args.only, "result": res}), flush=True)
@@ -743,7 +746,8 @@ def main():
         extra["lm_head"] = bench_head(qa, ctx, torch, np)
         extra["decoder_block"] = bench_block(qa, ctx, torch, np)
         log("config 5: prefill + greedy decode (32 blocks + lm_head) ...")
-        extra["config5"] = bench_model(qa, ctx, torch, np)
+        extra["config5"] = bench_model(qa, ctx, torch, np, steps=args.model_steps,
+                                       batches=tuple(int(b) for b in args.model_batches.split(",")))
         log("config 3 (8B decoder layer projections) ...")
         extra["cfg3_8b_layer"] = bench_cfg3(qa, ctx, torch, np)
     log("cpu baseline ...")

@@ -161,9 +161,10 @@ __global__ void blkd_add(const float *a, const float *b, float *out, int n) {
 
 // Per row of d: hsum = a (+ r), optionally stored to hout; x = bf16 of the
 // RMS-normalised bf16(hsum) times w (the decode's blkd_norm, a row per
-// workgroup).
+// workgroup), written nrep times: copy k of the n rows at x + k n d (the
+// input of a layer set whose layers share x).
 __global__ void __launch_bounds__(256) blkp_norm(const float *a, const float *r, float *hout, const float *w,
-                                                 float eps, uint16_t *x, int d) {
+                                                 float eps, uint16_t *x, int d, int nrep = 1) {
     __shared__ float red[4];
     const size_t off = (size_t)blockIdx.x * d;
     const int tid = threadIdx.x;
@@ -185,7 +186,8 @@ __global__ void __launch_bounds__(256) blkp_norm(const float *a, const float *r,
         float v = a[off + i];
         if (r) v = v + r[off + i];
         const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
-        x[off + i] = blkd_bf16(b * inv * w[i]);
+        const uint16_t o = blkd_bf16(b * inv * w[i]);
+        for (int k = 0; k < nrep; k++) x[k * (size_t)gridDim.x * d + off + i] = o;  // copy k: [n][d] at k n d
     }
 }
 
@@ -365,12 +367,18 @@ __global__ void __launch_bounds__(64) blkb_qk_rope(const float *q, const float *
     }
 }
 
+// Up to Q4_MAXB_KERNEL sequences the projections run on the fp4 decode
+// GEMV, q/k/v and gate/up as the block's layer sets (one launch per stage
+// for each set, x written once per layer of the set); beyond, layer by
+// layer on the prefill GEMM.
 struct BlkbPlan {
-    size_t o_x, o_q, o_k, o_v, o_qr, o_at, o_oo, o_h1, o_g, o_u, o_gemm, bytes;
+    bool sets;
+    size_t o_x, o_qkv, o_qr, o_at, o_oo, o_h1, o_gu, o_gemm, bytes;
 };
 
 static BlkbPlan blkb_plan(const qbk_block *B, size_t n) {
     BlkbPlan p{};
+    p.sets = n <= Q4_MAXB_KERNEL;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -378,20 +386,23 @@ static BlkbPlan blkb_plan(const qbk_block *B, size_t n) {
         return o;
     };
     const size_t d = B->d, qd = B->H * B->hd, kd = B->Hk * B->hd;
-    p.o_x = take(n * d * 2);
-    p.o_q = take(n * qd * 4);
-    p.o_k = take(n * kd * 4);
-    p.o_v = take(n * kd * 4);
+    p.o_x = take(3 * n * d * 2);
+    p.o_qkv = take(n * (qd + 2 * kd) * 4);  // q [n][qd], then k and v [n][kd]
     p.o_qr = take(n * qd * 4);
     p.o_at = take(n * qd * 4);
     p.o_oo = take(n * d * 4);
     p.o_h1 = take(n * d * 4);
-    p.o_g = take(n * B->ffn * 4);
-    p.o_u = take(n * B->ffn * 4);
+    p.o_gu = take(2 * n * B->ffn * 4);      // g [n][ffn], then u
     size_t g = 0;
-    for (int i = 0; i < 7; i++) {
-        const size_t w = blkp_proj_ws(B->lay[i], n);
-        g = w > g ? w : g;
+    if (p.sets) {
+        const size_t w[4] = {q4_set_workspace_batch(B->qkv, n), q4_set_workspace_batch(B->gu, n),
+                             q4_workspace(B->o, n), q4_workspace(B->down, n)};
+        for (int i = 0; i < 4; i++) g = w[i] > g ? w[i] : g;
+    } else {
+        for (int i = 0; i < 7; i++) {
+            const size_t w = blkp_proj_ws(B->lay[i], n);
+            g = w > g ? w : g;
+        }
     }
     p.o_gemm = take(g);
     p.bytes = off;
@@ -660,9 +671,9 @@ size_t qbk_block_decode_batch_workspace_size(const qbk_block *B, size_t n) {
 }
 
 // One position of each of sequences 0 .. n - 1 (sequence i at pos[i]): the
-// projections batched over the n rows (the GEMV at n <= 8, the GEMM beyond),
-// RoPE and the cache append per sequence, the sage decode attention per
-// sequence on its own kept state.
+// projections batched over the n rows (the GEMV up to batch 32, the GEMM
+// beyond), RoPE and the cache append per sequence, the sage decode
+// attention stepping every sequence's kept state.
 int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_t *pos, size_t n, void *workspace,
                                size_t workspace_size, void *stream) {
     int rc;
@@ -686,18 +697,23 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
     hipStream_t s = (hipStream_t)stream;
     char *w = (char *)workspace;
     uint16_t *x = (uint16_t *)(w + P.o_x);
-    float *q = (float *)(w + P.o_q), *k = (float *)(w + P.o_k), *v = (float *)(w + P.o_v),
-          *qr = (float *)(w + P.o_qr), *at = (float *)(w + P.o_at), *oo = (float *)(w + P.o_oo),
-          *h1 = (float *)(w + P.o_h1), *g = (float *)(w + P.o_g), *u = (float *)(w + P.o_u);
+    const size_t qd = B->H * B->hd, kd = B->Hk * B->hd;
+    float *q = (float *)(w + P.o_qkv), *k = q + n * qd, *v = k + n * kd, *qr = (float *)(w + P.o_qr),
+          *at = (float *)(w + P.o_at), *oo = (float *)(w + P.o_oo), *h1 = (float *)(w + P.o_h1),
+          *g = (float *)(w + P.o_gu), *u = g + n * B->ffn;
     void *ws = w + P.o_gemm;
     const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk;
     const size_t nd = n * B->d, nf = n * B->ffn, kvs = B->cap * B->Hk * B->hd;
     hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, h, (const float *)nullptr, (float *)nullptr,
-                       B->w_in, B->eps, x, d);
+                       B->w_in, B->eps, x, d, P.sets ? 3 : 1);
     QBK_HIP(hipGetLastError());
-    if ((rc = blkp_proj(B->lay[0], n, x, false, q, ws, s)) || (rc = blkp_proj(B->lay[1], n, x, false, k, ws, s)) ||
-        (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s)))
+    if (P.sets) {
+        if ((rc = q4_set_run_batch(B->qkv, n, x, false, q, false, ws, s))) return rc;
+    } else if ((rc = blkp_proj(B->lay[0], n, x, false, q, ws, s)) ||
+               (rc = blkp_proj(B->lay[1], n, x, false, k, ws, s)) ||
+               (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s))) {
         return rc;
+    }
     BlkbPos bp{};
     for (size_t i = 0; i < n; i++) bp.p[i] = (uint32_t)pos[i];
     hipLaunchKernelGGL(blkb_qk_rope, dim3(H + Hk, (unsigned)n), dim3(64), 0, s, q, k, v, B->rope, bp, B->w_q, B->w_k,
@@ -726,14 +742,21 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
         }
     }
     for (size_t i = 0; i < n; i++) B->tokens[i] = B->filled[i] = pos[i] + 1;
-    if ((rc = blkp_proj(B->o, n, at, true, oo, ws, s))) return rc;
-    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, oo, (const float *)h, h1, B->w_post, B->eps, x, d);
-    QBK_HIP(hipGetLastError());
-    if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) || (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s)))
+    if ((rc = P.sets ? q4_run(B->o, n, at, true, oo, false, ws, s) : blkp_proj(B->o, n, at, true, oo, ws, s)))
         return rc;
+    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, oo, (const float *)h, h1, B->w_post, B->eps, x,
+                       d, P.sets ? 2 : 1);
+    QBK_HIP(hipGetLastError());
+    if (P.sets) {
+        if ((rc = q4_set_run_batch(B->gu, n, x, false, g, false, ws, s))) return rc;
+    } else if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) ||
+               (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s))) {
+        return rc;
+    }
     hipLaunchKernelGGL(blkp_swiglu, dim3((unsigned)div_ceil(nf, 256)), dim3(256), 0, s, g, u, g, nf);
     QBK_HIP(hipGetLastError());
-    if ((rc = blkp_proj(B->down, n, g, true, oo, ws, s))) return rc;
+    if ((rc = P.sets ? q4_run(B->down, n, g, true, oo, false, ws, s) : blkp_proj(B->down, n, g, true, oo, ws, s)))
+        return rc;
     hipLaunchKernelGGL(blkp_add, dim3((unsigned)div_ceil(nd, 256)), dim3(256), 0, s, oo, h1, h, nd);
     QBK_HIP(hipGetLastError());
     return QBK_OK;

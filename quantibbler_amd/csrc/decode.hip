@@ -1,4 +1,4 @@
-// decode.hip -- the factor linear's decode GEMV (batch 1..8) on gfx950.
+// decode.hip -- the factor linear's decode GEMV (batch 1..32) on gfx950.
 //
 //   t = bf16(Vb^T z), z = bf16(s2 * x);  y = bf16(Ub t) * s1 + bias
 //                                        (engine/mod.rs:449-460, apply_bf16)
@@ -9,7 +9,9 @@
 // lo*2^e_lo, one E8M0 scale per 32-element block and column (a bf16 value
 // has 8 significant bits: hi keeps the top 4, lo the rest).  Token b of a
 // decode batch uses columns 2b, 2b+1.  Each 128-k slice of a 16-row tile is
-// one MFMA over 256 bytes of packed signs.
+// one MFMA over 256 bytes of packed signs per 16 columns (8 tokens): batches
+// beyond 8 run column groups of 16 against the same sign registers, so the
+// signs are still read once.
 //
 // A launch covers any set of layers (any shapes): each stage reads a device
 // table of Q4Layer entries (factor_internal.h) and finds its layer from the
@@ -181,7 +183,7 @@ __global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a) {
 #pragma unroll
     for (int e = 0; e < 16; e++) z[e] = 0.0f;
     if (live) {
-        const size_t off = L.act0 + (size_t)b * L.k_valid;
+        const size_t off = L.act0 * (size_t)a.batch + (size_t)b * L.k_valid;
         const uint16_t *src = (const uint16_t *)a.act + off;
         const float *srcf = (const float *)a.act + off;
         const float *s2 = L.s_in;
@@ -322,6 +324,33 @@ __device__ __forceinline__ void q4_step(f32x4_t acc[4], const uint4 &w4u, uint32
                                                                   Q4_SCALE_A, 0, bs);
 }
 
+// Slice j against NCG column groups (batch > 8): the four row tiles' signs
+// are built once and each group's fp8 operand read from global memory (L2);
+// columns past the batch's read nothing and use a zero operand.
+template <int NCG>
+__device__ __forceinline__ void q4_step_g(f32x4_t acc[NCG][4], const uint4 &w4u, uint32_t j, const uint8_t *gb,
+                                          const uint8_t *gs, int g, int ncol, int col, uint32_t c7) {
+    const i32x8_t s0 = q4_signs(w4u.x, c7), s1 = q4_signs(w4u.y, c7), s2 = q4_signs(w4u.z, c7),
+                  s3 = q4_signs(w4u.w, c7);
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++) {
+        const int c = 16 * cg + col;
+        i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
+        int bs = 127;
+        if (c < ncol) {
+            const size_t slot = ((size_t)j * 4 + g) * ncol + c;
+            const uint4 *bq = (const uint4 *)(gb + slot * 32);
+            const uint4 b0 = bq[0], b1 = bq[1];
+            bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+            bs = gs[slot];
+        }
+        acc[cg][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s0, bv, acc[cg][0], 4, 0, 0, Q4_SCALE_A, 0, bs);
+        acc[cg][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s1, bv, acc[cg][1], 4, 0, 0, Q4_SCALE_A, 0, bs);
+        acc[cg][2] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s2, bv, acc[cg][2], 4, 0, 0, Q4_SCALE_A, 0, bs);
+        acc[cg][3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s3, bv, acc[cg][3], 4, 0, 0, Q4_SCALE_A, 0, bs);
+    }
+}
+
 // Epilogue of one 64-row group, one row per lane: the accumulators are
 // transposed through the wave's LDS region T [ncol][64] (lane (col, g) holds
 // rows 16rt + 4g + i of column col), then lane l finishes row rg*64 + l of
@@ -335,25 +364,30 @@ __device__ __forceinline__ void q4_step(f32x4_t acc[4], const uint4 &w4u, uint32
 // (l & 15), hi to column 2b and lo to 2b + 1.
 //
 // Stage 2 writes y = bf16(v) * s1 + bias (so / bi: this lane's row).
+//
+// acc holds columns c0 .. c0 + 15 (tokens c0 / 2 on): a column group of a
+// batch beyond 8 (c0 = 16 cg), or the whole batch (c0 = 0).
 template <int STAGE>
 __device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, const Q4Args &a,
                                             const Q4Layer &L, int ncol, size_t rg, int lane, float so,
-                                            float bi) {
+                                            float bi, int c0 = 0) {
     const int col = lane & 15, g = lane >> 4;
-    if (col < ncol) {
+    const int nc = ncol - c0 < 16 ? ncol - c0 : 16;
+    if (col < nc) {
 #pragma unroll
         for (int rt = 0; rt < 4; rt++) *(f32x4_t *)(T + col * 64 + 16 * rt + 4 * g) = acc[rt];
     }
     __builtin_amdgcn_wave_barrier();
     const size_t row = rg * 64 + lane;
     const bool valid = row < L.rows_valid;
-    for (int b = 0; b < (ncol >> 1); b++) {
-        const float v = (T[(2 * b) * 64 + lane] + T[(2 * b + 1) * 64 + lane]) / 1.5f;
+    for (int bb = 0; bb < (nc >> 1); bb++) {
+        const int b = (c0 >> 1) + bb;
+        const float v = (T[(2 * bb) * 64 + lane] + T[(2 * bb + 1) * 64 + lane]) / 1.5f;
         const float t = valid ? bf16_to_f32(f32_to_bf16(v)) : 0.0f;
         if (STAGE == 2) {
             if (valid) {
                 const float y = t * so + bi;
-                const size_t o = L.out0 + (size_t)b * L.rows_valid + row;
+                const size_t o = L.out0 * (size_t)a.batch + (size_t)b * L.rows_valid + row;
                 if (a.y_bf16)
                     ((uint16_t *)a.out)[o] = f32_to_bf16(y);
                 else
@@ -417,8 +451,9 @@ __host__ __device__ constexpr uint32_t q4_wave_lds(int ncol) {
 // XCD-aware 1-D grid: workgroup i runs on XCD i % 8; XCD x takes the
 // contiguous range [x*per_x, (x+1)*per_x) of the (layer, row group) work, so
 // that one layer's operand is fetched into one L2.
-template <int STAGE, int KSPLIT, int NCOL>
+template <int STAGE, int KSPLIT, int NCOL, int NCG = 1>
 __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
+    static_assert(NCG == 1 || NCOL == 0, "column groups read their operand from global memory");
     extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
@@ -479,9 +514,11 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
     const size_t sdead = L.k_valid > kmin ? (L.k_valid - kmin + 127) / 128 : 0;  // first slice all past K
     const uint32_t dead_off = (uint32_t)(lane & 48);
     const bool rows_dead = rgc * 64 >= L.rows_valid;
-    f32x4_t acc[4];
+    f32x4_t acc[NCG][4];
 #pragma unroll
-    for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
+    for (int cg = 0; cg < NCG; cg++)
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) acc[cg][rt] = f32x4_t{0, 0, 0, 0};
     for (size_t sb = s0; sb < (rows_dead ? s0 : s1); sb += Q4_U) {
         const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
         // a step's operand: Q4_U slices x 4 lane groups x NCOL columns x 32 B,
@@ -518,33 +555,53 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
             __builtin_amdgcn_wave_barrier();
         }
         const uint8_t *gbs = gb + sb * 4 * ncol * 32, *gss = gs + sb * 4 * ncol;
-        if (nsl == Q4_U) {
+        if (NCG > 1) {
+            if (nsl == Q4_U) {
+#pragma unroll
+                for (int u = 0; u < Q4_U; u++) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
+            } else {
+#pragma unroll
+                for (int u = 0; u < Q4_U; u++)
+                    if (u < (int)nsl) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
+            }
+        } else if (nsl == Q4_U) {
 #pragma unroll
             for (int u = 0; u < Q4_U; u++)
-                q4_step<NCOL>(acc, w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
+                q4_step<NCOL>(acc[0], w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
         } else {
 #pragma unroll
             for (int u = 0; u < Q4_U; u++)
                 if (u < (int)nsl)
-                    q4_step<NCOL>(acc, w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
+                    q4_step<NCOL>(acc[0], w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
         }
         if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
     }
     if (KSPLIT > 1) {
-        f32x4_t *red = (f32x4_t *)(q4_lds + 4 * wreg);  // [4 waves][4 tiles][64 lanes]
+        // one column group at a time through [4 waves][4 tiles][64 lanes]
+        f32x4_t *red = (f32x4_t *)(q4_lds + 4 * wreg);
 #pragma unroll
-        for (int rt = 0; rt < 4; rt++) red[(wave * 4 + rt) * 64 + lane] = acc[rt];
-        __syncthreads();
-        if (ks != 0) return;
+        for (int cg = 0; cg < NCG; cg++) {
+            if (cg) __syncthreads();  // the last group's sums are read
 #pragma unroll
-        for (int rt = 0; rt < 4; rt++) {
-            f32x4_t v = red[(wave * 4 + rt) * 64 + lane];
-            for (int q = 1; q < KSPLIT; q++) v += red[((wave + q) * 4 + rt) * 64 + lane];
-            acc[rt] = v;
+            for (int rt = 0; rt < 4; rt++) red[(wave * 4 + rt) * 64 + lane] = acc[cg][rt];
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int rt = 0; rt < 4; rt++) {
+                    f32x4_t v = red[(wave * 4 + rt) * 64 + lane];
+                    for (int q = 1; q < KSPLIT; q++) v += red[((wave + q) * 4 + rt) * 64 + lane];
+                    acc[cg][rt] = v;
+                }
+            }
         }
+        if (ks != 0) return;
     }
     if (!live) return;
-    q4_epilogue<STAGE>(acc, (float *)wl, a, L, ncol, rg, lane, so, bi);
+#pragma unroll
+    for (int cg = 0; cg < NCG; cg++) {
+        if (cg) __builtin_amdgcn_wave_barrier();  // the last group's transpose is read
+        q4_epilogue<STAGE>(acc[cg], (float *)wl, a, L, ncol, rg, lane, so, bi, 16 * cg);
+    }
 }
 
 // ------------------------------------------------------------------------
@@ -578,8 +635,9 @@ struct Q4Geom {
 };
 
 // Fill stage-1 / stage-2 entries (tab[i], tab[n + i]) for layers[0..n) and
-// the launch geometry; x and y of layer i start at the running sums of
-// batch * din and batch * dout.
+// the launch geometry; x and y of layer i start at batch times the running
+// sums of din and dout (the entries hold the sums, so one table serves
+// every batch).
 static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, int num_cus,
                      Q4Layer *tab, Q4Geom &G) {
     G = Q4Geom{};
@@ -640,8 +698,8 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
         s2 += ns2;
         wg1 += div_ceil(L->r_p / 64, rpw1);
         wg2 += div_ceil(L->dout_p / 64, rpw2);
-        act += batch * L->din;
-        out += batch * L->dout;
+        act += L->din;
+        out += L->dout;
     }
     G.ns1_tot = s1;
     G.ns2_tot = s2;
@@ -714,11 +772,15 @@ static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32
     }
     const int ksplit = phase == 2 ? G.ks1 : G.ks2;
     const int ncol_t = G.batch <= 2 ? (int)G.ncol : 0;  // staged operand at batch 1-2
+    const int ncg = (int)div_ceil(G.ncol, 16);           // column groups (batch > 8)
     const size_t lds = q4_gemv_lds(ncol_t, ksplit);
     dim3 g((unsigned)round_up((size_t)a.n_wg, 8));  // a multiple of the 8 XCDs
-#define Q4_LAUNCH(ST, KS)                                                                        \
-    if (ncol_t == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 2>), g, dim3(256), lds, s, a);  \
-    else if (ncol_t == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 4>), g, dim3(256), lds, s, a); \
+#define Q4_LAUNCH(ST, KS)                                                                             \
+    if (ncol_t == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 2>), g, dim3(256), lds, s, a);       \
+    else if (ncol_t == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 4>), g, dim3(256), lds, s, a);  \
+    else if (ncg == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0, 4>), g, dim3(256), lds, s, a);  \
+    else if (ncg == 3) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0, 3>), g, dim3(256), lds, s, a);  \
+    else if (ncg == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0, 2>), g, dim3(256), lds, s, a);  \
     else hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0>), g, dim3(256), lds, s, a);
 #define Q4_LAUNCH_KS(ST)                                                                         \
     if (ksplit == 4) { Q4_LAUNCH(ST, 4) }                                                        \
@@ -766,7 +828,7 @@ using namespace qbk;
 
 // A decode set: layers of any shapes, one table, three launches.
 struct qbk_factor_set {
-    int device;
+    int device, num_cus;
     size_t n;
     Q4Layer *tab;          // device: [0, n) stage 1, [n, 2n) stage 2; then the
     uint32_t *wg1, *wg2;   // per-workgroup layer tables (same allocation)
@@ -789,6 +851,31 @@ int q4_set_run(const qbk_factor_set *S, const void *x, bool xf32, void *y, bool 
 
 size_t q4_set_workspace(const qbk_factor_set *S) { return S->geom.bytes; }
 
+// The set at a batch of n tokens: the device tables are the batch-1 ones
+// (their offsets are per token); the geometry is the batch's.
+static void q4_set_geom(const qbk_factor_set *S, size_t n, Q4Geom &G) {
+    std::vector<Q4Layer> h(2 * S->n);
+    q4_build(S->layers.data(), S->n, n, S->num_cus, h.data(), G);
+}
+
+size_t q4_set_workspace_batch(const qbk_factor_set *S, size_t n) {
+    Q4Geom G;
+    q4_set_geom(S, n, G);
+    return G.bytes;
+}
+
+int q4_set_run_batch(const qbk_factor_set *S, size_t n, const void *x, bool xf32, void *y, bool ybf16, void *ws,
+                     hipStream_t s) {
+    if (n == 1) return q4_set_run(S, x, xf32, y, ybf16, ws, s);
+    Q4Geom G;
+    q4_set_geom(S, n, G);
+    for (int ph = 1; ph <= Q4_PHASES; ph++) {
+        int rc = q4_phase(ph, G, S->tab, S->wg1, S->wg2, nullptr, x, xf32, y, ybf16, ws, s);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
+
 }  // namespace qbk
 
 extern "C" {
@@ -807,6 +894,7 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
     std::vector<Q4Layer> h(2 * n);
     qbk_factor_set *S = new qbk_factor_set();
     S->device = ctx->device;
+    S->num_cus = ctx->num_cus;
     S->n = n;
     S->layers.assign(layers, layers + n);
     q4_build(layers, n, 1, ctx->num_cus, h.data(), S->geom);
@@ -877,6 +965,27 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, c
                                             workspace_size, S->geom.bytes));
     return q4_phase(stage, S->geom, S->tab, S->wg1, S->wg2, S->s2cat, x, false, y, true, workspace,
                     (hipStream_t)stream);
+}
+
+size_t qbk_factor_set_workspace_size_batch(const qbk_factor_set *S, size_t n) {
+    if (!S || n == 0 || n > Q4_MAXB_KERNEL) return 0;
+    return q4_set_workspace_batch(S, n);
+}
+
+int qbk_factor_set_decode_batch_dev(qbk_ctx *ctx, const qbk_factor_set *S, size_t n, const uint16_t *x,
+                                    uint16_t *y, void *workspace, size_t workspace_size, void *stream) {
+    int rc;
+    if (!S) return fail(QBK_ERR_VALIDATION, "null layer set");
+    if (n == 0 || n > Q4_MAXB_KERNEL)
+        return fail(QBK_ERR_VALIDATION, fmt("batched set decode takes 1 to %zu tokens, got %zu", Q4_MAXB_KERNEL, n));
+    if (!x || !y) return fail(QBK_ERR_VALIDATION, "null buffer");
+    if ((rc = bind(ctx))) return rc;
+    if (S->device != ctx->device) return fail(QBK_ERR_VALIDATION, "layer set lives on another device");
+    const size_t need = q4_set_workspace_batch(S, n);
+    if (!workspace || workspace_size < need)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("workspace of %zu bytes is smaller than the %zu this call needs", workspace_size, need));
+    return q4_set_run_batch(S, n, x, false, y, true, workspace, (hipStream_t)stream);
 }
 
 int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *S, const uint16_t *x, uint16_t *y,

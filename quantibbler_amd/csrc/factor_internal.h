@@ -46,13 +46,16 @@ struct qbk_factor {
 
 namespace qbk {
 
-// decode.hip: the largest batch the fp4 decode GEMV serves.
+// decode.hip: the largest batch the factor linear's decode face routes to the
+// fp4 GEMV (beyond, the prefill GEMM), and the largest the GEMV serves at all
+// (the decoder block's batched decode steps use it up to there).
 constexpr size_t Q4_MAXB = 8;
+constexpr size_t Q4_MAXB_KERNEL = 32;
 
 // The two table entries of one layer decoded alone (offsets 0).
 void q4_layer_entries(const qbk_factor *L, Q4Layer out[2]);
 
-// Workspace bytes of a single-layer decode at `batch` (<= Q4_MAXB).
+// Workspace bytes of a single-layer decode at `batch` (<= Q4_MAXB_KERNEL).
 size_t q4_workspace(const qbk_factor *L, size_t batch);
 
 // Single-layer decode: x [batch][din] (bf16, or f32 when xf32) ->
@@ -64,6 +67,11 @@ int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y,
 // workspace bytes.
 int q4_set_run(const qbk_factor_set *S, const void *x, bool xf32, void *y, bool ybf16, void *ws, hipStream_t s);
 size_t q4_set_workspace(const qbk_factor_set *S);
+// The set at a batch of n <= Q4_MAXB_KERNEL tokens: x [layer][n][din],
+// y [layer][n][dout].
+size_t q4_set_workspace_batch(const qbk_factor_set *S, size_t n);
+int q4_set_run_batch(const qbk_factor_set *S, size_t n, const void *x, bool xf32, void *y, bool ybf16, void *ws,
+                     hipStream_t s);
 
 // prefill.hip: the sign layout of the prefill GEMM (rows_p a multiple of
 // 128, bits_p of 64), its workspace, and the two-stage GEMM for N tokens:

@@ -596,6 +596,15 @@ class FactorSet:
                                                     _ptr(workspace), int(workspace_size),
                                                     _stream(stream)))
 
+    def workspace_size_batch(self, n: int) -> int:
+        return int(_lib.load().qbk_factor_set_workspace_size_batch(self._h, int(n)))
+
+    def decode_batch_dev(self, n: int, x, y, workspace, workspace_size: int, stream=None):
+        """Every layer at a batch of n tokens (1 .. 32): x bf16 [layer][n][din],
+        y bf16 [layer][n][dout], device pointers or tensors."""
+        check(_lib.load().qbk_factor_set_decode_batch_dev(self.ctx.handle, self._h, int(n), _ptr(x), _ptr(y),
+                                                          _ptr(workspace), int(workspace_size), _stream(stream)))
+
     def stage_dev(self, stage: int, x, y, workspace, workspace_size: int, stream=None):
         check(_lib.load().qbk_factor_set_stage_dev(self.ctx.handle, self._h, int(stage), _ptr(x),
                                                    _ptr(y), _ptr(workspace), int(workspace_size),

@@ -88,6 +88,72 @@ def test_config3_set_decode_bit_identical(ctx, orc, cfg3_layers):
     S.close()
 
 
+@pytest.mark.parametrize("n", [9, 16, 24, 32])
+def test_config3_set_decode_batch_bit_identical(ctx, orc, cfg3_layers, n):
+    """The set at a batch of n tokens (column groups of 16 operand columns
+    against the same sign registers): integer-exact inputs, every row of
+    every layer bit-identical to the oracle's composite."""
+    from quantibbler_amd import FactorSet
+
+    host, dev = cfg3_layers
+    rng = np.random.default_rng(40 + n)
+    S = FactorSet(ctx, dev)
+    xs = [orc.f32_to_bf16_fast(rng.integers(-2, 3, (n, L["din"])).astype(np.float32)) for L in host]
+    xd = torch.from_numpy(np.concatenate([x.ravel() for x in xs]).view(np.int16)).cuda()
+    yd = torch.empty(n * sum(L["dout"] for L in host), dtype=torch.int16, device="cuda")
+    wn = S.workspace_size_batch(n)
+    ws = torch.zeros(wn, dtype=torch.uint8, device="cuda")
+    say(f"config-3 set decode at batch {n}")
+    S.decode_batch_dev(n, xd, yd, ws, wn, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    y = yd.cpu().numpy().view(np.uint16)
+    off = 0
+    for L, xi in zip(host, xs):
+        want = orc.factor_apply_bf16_batch(L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                           L["bias"], xi)
+        same(y[off:off + n * L["dout"]].reshape(n, L["dout"]), orc.f32_to_bf16_fast(want),
+             f"config-3 set decode at batch {n}, layer {L['name']}")
+        off += n * L["dout"]
+    S.close()
+
+
+def test_config3_set_decode_batch_rows_match_batch1(ctx, orc, cfg3_layers):
+    """General bf16 inputs (N(0,1) rounded to bf16; these layers have s2 = 1):
+    row b of a batch-32 set decode is bit-identical to the set decoding row b
+    alone -- each operand column's sum is the same MFMA sequence whatever the
+    other columns hold."""
+    from quantibbler_amd import FactorSet
+
+    host, dev = cfg3_layers
+    n = 32
+    rng = np.random.default_rng(77)
+    S = FactorSet(ctx, dev)
+    xs = [orc.f32_to_bf16_fast(rng.standard_normal((n, L["din"])).astype(np.float32)) for L in host]
+    xd = torch.from_numpy(np.concatenate([x.ravel() for x in xs]).view(np.int16)).cuda()
+    yd = torch.empty(n * sum(L["dout"] for L in host), dtype=torch.int16, device="cuda")
+    wn = S.workspace_size_batch(n)
+    ws = torch.zeros(max(wn, S.workspace_size()), dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream()
+    S.decode_batch_dev(n, xd, yd, ws, wn, st)
+    torch.cuda.synchronize()
+    y = yd.cpu().numpy().view(np.uint16)
+    y1 = torch.empty(sum(L["dout"] for L in host), dtype=torch.int16, device="cuda")
+    for b in (0, 7, 8, 15, 31):
+        x1 = torch.from_numpy(np.concatenate([x[b] for x in xs]).view(np.int16)).cuda()
+        S.decode_dev(x1, y1, ws, ws.numel(), st)
+        torch.cuda.synchronize()
+        got1 = y1.cpu().numpy().view(np.uint16)
+        off, off1 = 0, 0
+        for L in host:
+            same(y[off + b * L["dout"]:off + (b + 1) * L["dout"]], got1[off1:off1 + L["dout"]],
+                 f"batch-32 row {b} vs batch 1, layer {L['name']}")
+            off += n * L["dout"]
+            off1 += L["dout"]
+    with pytest.raises(Exception, match="batched set decode takes 1 to 32 tokens, got 33"):
+        S.decode_batch_dev(33, xd, yd, ws, wn, st)
+    S.close()
+
+
 @pytest.mark.parametrize("which", [c[0] for c in CFG3])
 def test_config3_prefill_b2048_integer_exact(ctx, orc, cfg3_layers, which):
     host, dev = cfg3_layers
