@@ -283,18 +283,19 @@ def bench_sage_decode(qa, ctx, torch, np, seq=4096, iters=20):
 def bench_head(qa, ctx, torch, np, vocab=128256, d=4096, iters=20):
     """The language-model head of config 5 (engine/mod.rs:781-800): one
     decode step's logits over a bf16-valued 128256 x 4096 head (1.05 GB
-    stored as bf16, the bytes that dominate a batch-1 decode step), and a
-    batch of 8 positions."""
+    stored as bf16, the bytes that dominate a batch-1 decode step), and
+    batches of 8 and 32 positions (config 5's batch; bit-exact sequential
+    sums, so bound by the vector ALU: 2 * 32 * 128256 * 4096 f32 operations).
     g = torch.Generator(device="cuda").manual_seed(11)
     rows = torch.randn((vocab, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
     H = qa.LmHead.from_rows_dev(ctx, rows, vocab, d)
     del rows
     torch.cuda.empty_cache()
-    hid = torch.randn((8, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
-    out = torch.empty((8, vocab), dtype=torch.float32, device="cuda")
+    hid = torch.randn((32, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
+    out = torch.empty((32, vocab), dtype=torch.float32, device="cuda")
     st = torch.cuda.current_stream()
     res = {"vocab": vocab, "d_model": d, "stored_bf16": H.bf16, "head_bytes": vocab * d * 2}
-    for b in (1, 8):
+    for b in (1, 8, 32):
         for _ in range(3):
             H.logits_dev(hid, b, out, st)
         torch.cuda.synchronize()

@@ -182,7 +182,9 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *set, int stage,
  * (layer i's n rows start after layers 0..i-1's), y bf16 [layer][n][dout_i]
  * likewise.  The signs are read once for the batch: 16 operand columns (8
  * tokens) per fp4 MFMA, the column groups against the same sign registers.
- * Row b of y_i is bit-identical to the layer applied to row b alone. */
+ * Row b of y_i is bit-identical to the layer applied to row b alone.  Beyond
+ * batch 8 the column groups hold 280-510 VGPRs a wave (one or two waves a
+ * SIMD), so past batch ~12 the prefill GEMM of each layer is faster. */
 size_t qbk_factor_set_workspace_size_batch(const qbk_factor_set *set, size_t n);
 int qbk_factor_set_decode_batch_dev(qbk_ctx *ctx, const qbk_factor_set *set, size_t n, const uint16_t *x,
                                     uint16_t *y, void *workspace, size_t workspace_size, void *stream);
@@ -254,7 +256,7 @@ int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *block, size_t seq, float 
  * h f32 [n][d_model] on the device (row i is sequence i's token), replaced
  * by the block's outputs; pos (host, n entries) as qbk_block_decode_dev's
  * pos per sequence.  The projections run at batch n (the fp4 decode GEMV up
- * to batch 32, the bf16-MFMA GEMM beyond) and the attention steps every
+ * to batch 8, the bf16-MFMA GEMM beyond) and the attention steps every
  * sequence's kept state in one set of launches.  `workspace` of at least
  * qbk_block_decode_batch_workspace_size(block, n) bytes; nothing is
  * allocated. */

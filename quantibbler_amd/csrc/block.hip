@@ -367,10 +367,11 @@ __global__ void __launch_bounds__(64) blkb_qk_rope(const float *q, const float *
     }
 }
 
-// Up to Q4_MAXB_KERNEL sequences the projections run on the fp4 decode
-// GEMV, q/k/v and gate/up as the block's layer sets (one launch per stage
-// for each set, x written once per layer of the set); beyond, layer by
-// layer on the prefill GEMM.
+// Up to Q4_MAXB sequences the projections run on the fp4 decode GEMV, q/k/v
+// and gate/up as the block's layer sets (one launch per stage for each set,
+// x written once per layer of the set); beyond, layer by layer on the
+// prefill GEMM, which is the faster of the two there (at config 3's q shape:
+// 20-21 us a layer at batch 9-32 against the GEMV's 19-40 us).
 struct BlkbPlan {
     bool sets;
     size_t o_x, o_qkv, o_qr, o_at, o_oo, o_h1, o_gu, o_gemm, bytes;
@@ -378,7 +379,7 @@ struct BlkbPlan {
 
 static BlkbPlan blkb_plan(const qbk_block *B, size_t n) {
     BlkbPlan p{};
-    p.sets = n <= Q4_MAXB_KERNEL;
+    p.sets = n <= Q4_MAXB;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -671,7 +672,7 @@ size_t qbk_block_decode_batch_workspace_size(const qbk_block *B, size_t n) {
 }
 
 // One position of each of sequences 0 .. n - 1 (sequence i at pos[i]): the
-// projections batched over the n rows (the GEMV up to batch 32, the GEMM
+// projections batched over the n rows (the GEMV up to batch 8, the GEMM
 // beyond), RoPE and the cache append per sequence, the sage decode
 // attention stepping every sequence's kept state.
 int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_t *pos, size_t n, void *workspace,

@@ -55,7 +55,7 @@ static inline size_t head_rows_per_wg(int bf16) { return (HEAD_THREADS / 64) * h
 // rows += hidden[b][t] * w (bf16: the word's low half is row 2c, high half
 // row 2c + 1)
 template <bool BF16, int NB, int CH>
-__device__ __forceinline__ void head_chunk(float acc[NB][2], const uint32_t W[CH], const cf32_t *h, size_t d,
+__device__ __forceinline__ void head_chunk(float acc[NB][2], const uint32_t W[CH], const cf32_t *const h[NB],
                                            size_t t0) {
     float w0[CH], w1[CH];
 #pragma unroll
@@ -69,7 +69,7 @@ __device__ __forceinline__ void head_chunk(float acc[NB][2], const uint32_t W[CH
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int u = 0; u < CH; u++) {
-            const float hv = h[(size_t)b * d + t0 + u];
+            const float hv = h[b][t0 + u];
             acc[b][0] = acc[b][0] + hv * w0[u];
             if (BF16) acc[b][1] = acc[b][1] + hv * w1[u];
         }
@@ -92,17 +92,29 @@ __device__ __forceinline__ void head_load(uint32_t W[CH], const uint32_t *col, s
     }
 }
 
-// logits[b][v] for NB hidden rows.  w: the per-wave blocked layout, bf16
-// (dwords of two rows) or f32; lane l of wave block wb reads dword
-// ((wb * d_p / 4 + t / 4) * 64 + l) * 4 + t % 4 at step t.
+// logits[b][v] for up to NB hidden rows a wave.  w: the per-wave blocked
+// layout, bf16 (dwords of two rows) or f32; lane l of wave block wb reads
+// dword ((wb * d_p / 4 + t / 4) * 64 + l) * 4 + t % 4 at step t.  The four
+// waves of a workgroup cover 4 / chunks wave blocks; the waves of one block
+// take consecutive chunks of NB of the batch rows (the last chunk may hold
+// fewer) -- the same head words, fetched once from memory and re-read from
+// the CU's cache, so a batch of up to 4 NB rows keeps four waves a SIMD
+// busy where one wave of 4 NB accumulators would run alone.
 template <bool BF16, int NB>
 __global__ void __launch_bounds__(HEAD_THREADS) head_logits_kernel(const uint32_t *w, size_t vocab_p, size_t vocab,
-                                                                  size_t d, const float *hidden, float *logits) {
-    const size_t wb = (size_t)blockIdx.x * (HEAD_THREADS / 64) + (threadIdx.x >> 6);
+                                                                  size_t d, const float *hidden, float *logits,
+                                                                  int chunks, int batch) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ci = wave % chunks;  // wave-uniform
+    const size_t wb = (size_t)blockIdx.x * (HEAD_THREADS / 64 / chunks) + wave / chunks;
     const size_t lane = threadIdx.x & 63;
     const size_t dq = (d + 3) / 4;  // four-step groups
     const uint32_t *col = w + wb * dq * 256 + lane * 4;
-    const cf32_t *h = (const cf32_t *)hidden;
+    const int nb = batch - ci * NB < NB ? batch - ci * NB : NB;  // rows of this wave's chunk (>= 1)
+    hidden += (size_t)ci * NB * d;
+    logits += (size_t)ci * NB * vocab;
+    const cf32_t *h[NB];  // the chunk's rows; rows past nb repeat the last (not stored)
+#pragma unroll
+    for (int b = 0; b < NB; b++) h[b] = (const cf32_t *)hidden + (size_t)(b < nb ? b : nb - 1) * d;
     float acc[NB][2];
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[b][0] = acc[b][1] = 0.0f;
@@ -113,9 +125,9 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_logits_kernel(const uint32_
         head_load<CH>(A, col, 0, dq - 1);
         for (size_t t0 = 0; t0 < dmain; t0 += 2 * CH) {
             head_load<CH>(Bw, col, t0 + CH, dq - 1);
-            head_chunk<BF16, NB, CH>(acc, A, h, d, t0);
+            head_chunk<BF16, NB, CH>(acc, A, h, t0);
             head_load<CH>(A, col, t0 + 2 * CH, dq - 1);
-            head_chunk<BF16, NB, CH>(acc, Bw, h, d, t0 + CH);
+            head_chunk<BF16, NB, CH>(acc, Bw, h, t0 + CH);
         }
     }
     for (size_t t = dmain; t < d; t++) {  // the last d % (2 CH) steps, in order
@@ -124,7 +136,7 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_logits_kernel(const uint32_
         const float w1 = BF16 ? __uint_as_float(wv & 0xffff0000u) : 0.0f;
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const float hv = h[(size_t)b * d + t];
+            const float hv = h[b][t];
             acc[b][0] = acc[b][0] + hv * w0;
             if (BF16) acc[b][1] = acc[b][1] + hv * w1;
         }
@@ -132,6 +144,7 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_logits_kernel(const uint32_
     const size_t v0 = wb * head_rows_per_wave(BF16) + (BF16 ? 2 * lane : lane);
 #pragma unroll
     for (int b = 0; b < NB; b++) {
+        if (b >= nb) break;
         if (v0 < vocab) logits[(size_t)b * vocab + v0] = acc[b][0];
         if (BF16 && v0 + 1 < vocab) logits[(size_t)b * vocab + v0 + 1] = acc[b][1];
     }
@@ -212,17 +225,21 @@ static int head_build(qbk_ctx *ctx, const float *src_dev, size_t vocab, size_t d
     return QBK_OK;
 }
 
+// Up to 4 HEAD_MAXB rows a launch: 1, 2 or 4 chunks of at most HEAD_MAXB
+// rows, a wave each, over the same head words.
 static int head_run(const qbk_head *H, const float *hidden, size_t batch, float *logits, hipStream_t s) {
     const size_t rpw = head_rows_per_wg(H->bf16);
-    const dim3 g((unsigned)(H->vocab_p / rpw));
-    for (size_t b0 = 0; b0 < batch; b0 += HEAD_MAXB) {
-        const size_t nb = batch - b0 < HEAD_MAXB ? batch - b0 : HEAD_MAXB;
+    for (size_t b0 = 0; b0 < batch; b0 += 4 * HEAD_MAXB) {
+        const size_t rows = batch - b0 < 4 * HEAD_MAXB ? batch - b0 : 4 * HEAD_MAXB;
+        const int chunks = rows <= HEAD_MAXB ? 1 : rows <= 2 * HEAD_MAXB ? 2 : 4;
+        const size_t nb = div_ceil(rows, (size_t)chunks);
+        const dim3 g((unsigned)(H->vocab_p / (rpw / chunks)));
         const float *hb = hidden + b0 * H->d_model;
         float *lb = logits + b0 * H->vocab;
         const uint32_t *w = (const uint32_t *)H->w;
 #define HEAD_LAUNCH(BF, NB)                                                                                   \
     hipLaunchKernelGGL((head_logits_kernel<BF, NB>), g, dim3(HEAD_THREADS), 0, s, w, H->vocab_p, H->vocab,     \
-                       H->d_model, hb, lb)
+                       H->d_model, hb, lb, chunks, (int)rows)
 #define HEAD_BATCH(BF)                                                                                        \
     switch (nb) {                                                                                             \
         case 1: HEAD_LAUNCH(BF, 1); break;                                                                    \

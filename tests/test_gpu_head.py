@@ -2,7 +2,8 @@
 through the C ABI -- bit-identical to the oracle's sequential f32 sums, for
 bf16-valued heads (stored as bf16) and f32 heads (stored as f32), ragged
 vocabularies, d_model not a multiple of the 64-step load chunks, batches of
-1-11 rows (split into launches of up to 8), and the device-pointer form."""
+1-70 rows (a launch takes up to 32, in 1, 2 or 4 wave chunks of up to 8 with
+a shorter last chunk), and the device-pointer form."""
 import numpy as np
 import pytest
 
@@ -27,6 +28,9 @@ def say(*a):
     (1000, 64, True, 1), (777, 100, True, 3), (1537, 256, False, 2), (513, 4096, True, 11), (300, 7, False, 8),
     # whole 128-step chunks and a ragged tail that ends inside a four-step group
     (650, 262, True, 2), (130, 262, False, 1),
+    # two chunks (9-16 rows), four (17-32), and several launches
+    (1000, 300, True, 9), (700, 128, False, 16), (1500, 200, True, 17), (513, 520, True, 32),
+    (300, 100, False, 30), (1100, 96, True, 70),
 ])
 def test_head_logits_bit_identical(ctx, orc, vocab, d, bf16, batch):
     from quantibbler_amd import LmHead
