@@ -285,7 +285,7 @@ def bench_head(qa, ctx, torch, np, vocab=128256, d=4096, iters=20):
     decode step's logits over a bf16-valued 128256 x 4096 head (1.05 GB
     stored as bf16, the bytes that dominate a batch-1 decode step), and
     batches of 8 and 32 positions (config 5's batch; bit-exact sequential
-    sums, so bound by the vector ALU: 2 * 32 * 128256 * 4096 f32 operations).
+    sums, so bound by the vector ALU: 2 * 32 * 128256 * 4096 f32 operations)."""
     g = torch.Generator(device="cuda").manual_seed(11)
     rows = torch.randn((vocab, d), device="cuda", generator=g).to(torch.bfloat16).to(torch.float32)
     H = qa.LmHead.from_rows_dev(ctx, rows, vocab, d)

@@ -205,3 +205,14 @@ def test_rust_binding_declares_only_exported_symbols(lib):
     fields = re.search(r"pub struct AttentionShape \{(.*?)\}", src, re.S).group(1)
     assert re.findall(r"pub (\w+): usize", fields) == ["batch", "n_heads", "n_kv_heads", "seq_q", "seq_kv",
                                                        "head_dim", "val_dim"]
+
+
+def test_driver_scripts_compile():
+    """bench.py and __graft_entry__.py, which the driver runs on the GPU box,
+    at least compile here."""
+    import os
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for name in ("bench.py", "__graft_entry__.py"):
+        with open(os.path.join(root, name)) as f:
+            compile(f.read(), name, "exec")
