@@ -163,13 +163,14 @@ __global__ void blkd_add(const float *a, const float *b, float *out, int n) {
 // RMS-normalised bf16(hsum) times w (the decode's blkd_norm, a row per
 // workgroup), written nrep times: copy k of the n rows at x + k n d (the
 // input of a layer set whose layers share x).
-__global__ void __launch_bounds__(256) blkp_norm(const float *a, const float *r, float *hout, const float *w,
-                                                 float eps, uint16_t *x, int d, int nrep = 1) {
-    __shared__ float red[4];
+template <int NT>
+__global__ void __launch_bounds__(NT) blkp_norm(const float *a, const float *r, float *hout, const float *w,
+                                                float eps, uint16_t *x, int d, int nrep) {
+    __shared__ float red[NT / 64];
     const size_t off = (size_t)blockIdx.x * d;
     const int tid = threadIdx.x;
     float ss = 0.0f;
-    for (int i = tid; i < d; i += 256) {
+    for (int i = tid; i < d; i += NT) {
         float v = a[off + i];
         if (r) v = v + r[off + i];
         if (hout) hout[off + i] = v;
@@ -180,15 +181,28 @@ __global__ void __launch_bounds__(256) blkp_norm(const float *a, const float *r,
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NT / 64; i++) tot += red[i];
     const float inv = 1.0f / sqrtf(tot / (float)d + eps);
-    for (int i = tid; i < d; i += 256) {
+    for (int i = tid; i < d; i += NT) {
         float v = a[off + i];
         if (r) v = v + r[off + i];
         const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
         const uint16_t o = blkd_bf16(b * inv * w[i]);
         for (int k = 0; k < nrep; k++) x[k * (size_t)gridDim.x * d + off + i] = o;  // copy k: [n][d] at k n d
     }
+}
+
+// blkp_norm over n rows: 1024 threads a row for a few rows (a batched decode
+// step: the row's latency is the step's), 256 for many (a prefill).
+static void blkp_norm_launch(size_t n, const float *a, const float *r, float *hout, const float *w, float eps,
+                             uint16_t *x, int d, int nrep, hipStream_t s) {
+    if (n <= 64)
+        hipLaunchKernelGGL(blkp_norm<BLKD_NORM_THREADS>, dim3((unsigned)n), dim3(BLKD_NORM_THREADS), 0, s, a, r,
+                           hout, w, eps, x, d, nrep);
+    else
+        hipLaunchKernelGGL(blkp_norm<256>, dim3((unsigned)n), dim3(256), 0, s, a, r, hout, w, eps, x, d, nrep);
 }
 
 // Row t's q, k, v (token-major f32, as the projections wrote them): per-head
@@ -626,8 +640,7 @@ int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *B, size_t seq, float *h, 
     const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk;
     const size_t nd = n * B->d, nf = n * B->ffn;
     // attention sublayer: norm, q/k/v at batch n, q/k norms + RoPE + cache
-    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, h, (const float *)nullptr, (float *)nullptr,
-                       B->w_in, B->eps, x, d);
+    blkp_norm_launch(n, h, nullptr, nullptr, B->w_in, B->eps, x, d, 1, s);
     QBK_HIP(hipGetLastError());
     if ((rc = blkp_proj(B->lay[0], n, x, false, q, ws, s)) || (rc = blkp_proj(B->lay[1], n, x, false, k, ws, s)) ||
         (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s)))
@@ -647,7 +660,7 @@ int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *B, size_t seq, float *h, 
     }
     // o + residual, norm, gate / up, SwiGLU, down + residual
     if ((rc = blkp_proj(B->o, n, arow, false, oo, ws, s))) return rc;
-    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, oo, (const float *)h, h1, B->w_post, B->eps, x, d);
+    blkp_norm_launch(n, oo, h, h1, B->w_post, B->eps, x, d, 1, s);
     QBK_HIP(hipGetLastError());
     if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) || (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s)))
         return rc;
@@ -705,8 +718,7 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
     void *ws = w + P.o_gemm;
     const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk;
     const size_t nd = n * B->d, nf = n * B->ffn, kvs = B->cap * B->Hk * B->hd;
-    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, h, (const float *)nullptr, (float *)nullptr,
-                       B->w_in, B->eps, x, d, P.sets ? 3 : 1);
+    blkp_norm_launch(n, h, nullptr, nullptr, B->w_in, B->eps, x, d, P.sets ? 3 : 1, s);
     QBK_HIP(hipGetLastError());
     if (P.sets) {
         if ((rc = q4_set_run_batch(B->qkv, n, x, false, q, false, ws, s))) return rc;
@@ -745,8 +757,7 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
     for (size_t i = 0; i < n; i++) B->tokens[i] = B->filled[i] = pos[i] + 1;
     if ((rc = P.sets ? q4_run(B->o, n, at, true, oo, false, ws, s) : blkp_proj(B->o, n, at, true, oo, ws, s)))
         return rc;
-    hipLaunchKernelGGL(blkp_norm, dim3((unsigned)n), dim3(256), 0, s, oo, (const float *)h, h1, B->w_post, B->eps, x,
-                       d, P.sets ? 2 : 1);
+    blkp_norm_launch(n, oo, h, h1, B->w_post, B->eps, x, d, P.sets ? 2 : 1, s);
     QBK_HIP(hipGetLastError());
     if (P.sets) {
         if ((rc = q4_set_run_batch(B->gu, n, x, false, g, false, ws, s))) return rc;
