@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "factor_internal.h"
+#include "q4_operand.h"
 
 #pragma clang fp contract(off)
 
@@ -155,6 +156,126 @@ __global__ void blkd_swiglu(const float *gu, float *hid, int ffn) {
 __global__ void blkd_add(const float *a, const float *b, float *out, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = a[i] + b[i];
+}
+
+// blkd_norm writing, in place of x, the batch-1 stage-1 operand of the layer
+// set that x feeds (nrep layers each reading x: every din == d, d a multiple
+// of 128; q4_operand.h's flat runs over nrep copies of x, the bytes
+// q4_prep_flat_kernel writes from them).  The row, the residual, w and the
+// first runs' s2 are loaded up front (one memory round trip before the
+// reduction), the sums run in blkd_norm's order, x goes through LDS.
+#define BLKD_OP_PER 8  // row elements a thread holds: d <= 8192
+__global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm_op(const float *a, const float *r, float *hout,
+                                                                 const float *w, float eps, int d, int nrep,
+                                                                 const float *s2cat, uint8_t *op, uint8_t *sc) {
+    __shared__ float red[BLKD_NORM_THREADS / 64];
+    __shared__ __attribute__((aligned(16))) uint16_t xs[BLKD_NORM_THREADS * BLKD_OP_PER];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t n_runs = (uint32_t)(nrep * d / 16), rpl = (uint32_t)(d / 16);
+    // a run past the end shadows one of the last slice (n_runs is a multiple
+    // of 8, so its shuffle partner at lane distance 2 does too)
+    auto run_of = [&](uint32_t tt) { return tt < n_runs ? tt : n_runs - 8 + (tt & 7); };
+    u32x4_t sr[4];
+    {
+        const u32x4_t *ss = (const u32x4_t *)(s2cat + (size_t)run_of((uint32_t)tid) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) sr[q] = ss[q];
+    }
+    float va[BLKD_OP_PER], wv[BLKD_OP_PER];
+#pragma unroll
+    for (int k = 0; k < BLKD_OP_PER; k++) {
+        const int i = tid + k * BLKD_NORM_THREADS;
+        va[k] = 0.0f;
+        wv[k] = 0.0f;
+        if (i < d) {
+            float v = a[i];
+            if (r) v = v + r[i];
+            va[k] = v;
+            wv[k] = w[i];
+        }
+    }
+    float ss2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < BLKD_OP_PER; k++) {
+        const int i = tid + k * BLKD_NORM_THREADS;
+        if (i < d) {
+            if (hout) hout[i] = va[k];
+            const float b = __uint_as_float((uint32_t)blkd_bf16(va[k]) << 16);
+            ss2 += b * b;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss2 += __shfl_xor(ss2, o, 64);
+    if (lane == 0) red[wave] = ss2;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < BLKD_NORM_THREADS / 64; i++) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+#pragma unroll
+    for (int k = 0; k < BLKD_OP_PER; k++) {
+        const int i = tid + k * BLKD_NORM_THREADS;
+        if (i < d) {
+            const float b = __uint_as_float((uint32_t)blkd_bf16(va[k]) << 16);
+            xs[i] = blkd_bf16(b * inv * wv[k]);
+        }
+    }
+    __syncthreads();
+    for (uint32_t t0 = 0; t0 < n_runs; t0 += BLKD_NORM_THREADS) {  // uniform: every lane shuffles
+        const uint32_t tt = t0 + (uint32_t)tid, t = run_of(tt);
+        if (t0 > 0) {
+            const u32x4_t *ss = (const u32x4_t *)(s2cat + (size_t)t * 16);
+#pragma unroll
+            for (int q = 0; q < 4; q++) sr[q] = ss[q];
+        }
+        const uint32_t e0 = (t % rpl) * 16;
+        const u32x4_t xr[2] = {*(const u32x4_t *)(xs + e0), *(const u32x4_t *)(xs + e0 + 8)};
+        float z[16];
+        q4_run_z(xr, sr, z);
+        uint32_t hw[4], lw[4];
+        int e_hi, e_lo;
+        q4_run_operand(z, hw, lw, e_hi, e_lo);
+        if (tt >= n_runs) continue;
+        const int rr = (int)(t & 7);
+        const size_t slot = q4_run_slot(t >> 3, rr, 2, 0), byte = 16 * (rr & 1);
+        *(uint4 *)(op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *(uint4 *)(op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        if ((rr & 2) == 0)
+            *(uint16_t *)(sc + q4_run_scale(t >> 3, rr, 2, 0)) = (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
+    }
+}
+
+// blkd_swiglu written as the batch-1 stage-1 operand of the layer it feeds
+// (din = ffn, a multiple of 128): a thread per run of 16, hid as
+// blkd_swiglu forms it, z = bf16(s2 hid) as q4_prep_kernel's f32 path.
+__global__ void __launch_bounds__(256) blkd_swiglu_op(const float *gu, int ffn, const float *s2, uint8_t *op,
+                                                      uint8_t *sc) {
+    const uint32_t n_runs = (uint32_t)ffn / 16;
+    const uint32_t tt = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = tt < n_runs ? tt : n_runs - 8 + (tt & 7);
+    const size_t k0 = (size_t)t * 16;
+    float z[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 g4 = *(const float4 *)(gu + k0 + 4 * q), u4 = *(const float4 *)(gu + ffn + k0 + 4 * q);
+        const float4 s4 = *(const float4 *)(s2 + k0 + 4 * q);
+        const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w},
+                    sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float hid = g[e] * u[e] / (1.0f + expf(0.0f - g[e]));
+            z[4 * q + e] = bf16_to_f32(f32_to_bf16(sv[e] * hid));
+        }
+    }
+    uint32_t hw[4], lw[4];
+    int e_hi, e_lo;
+    q4_run_operand(z, hw, lw, e_hi, e_lo);
+    if (tt >= n_runs) return;
+    const int rr = (int)(t & 7);
+    const size_t slot = q4_run_slot(t >> 3, rr, 2, 0), byte = 16 * (rr & 1);
+    *(uint4 *)(op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if ((rr & 2) == 0)
+        *(uint16_t *)(sc + q4_run_scale(t >> 3, rr, 2, 0)) = (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
 }
 
 // ---- prefill (n tokens at positions 0 .. n - 1) ---------------------------
@@ -571,11 +692,23 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
     hipStream_t s = (hipStream_t)stream;
     const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk, ffn = (int)B->ffn;
+    // the norms and SwiGLU write the operand of the projections they feed
+    // when those have the flat batch-1 layout (every din a multiple of 128)
+    const bool fits = d <= BLKD_NORM_THREADS * BLKD_OP_PER;
+    uint8_t *op, *sc;
+    const float *s2c;
     // attention sublayer
-    hipLaunchKernelGGL(blkd_norm, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, h, (const float *)nullptr,
-                       (float *)nullptr, B->w_in, B->eps, B->xcat, 3, d);
-    QBK_HIP(hipGetLastError());
-    if ((rc = q4_set_run(B->qkv, B->xcat, false, B->ycat, false, B->ws, s))) return rc;
+    if (fits && q4_set_flat_operand(B->qkv, B->ws, &op, &sc, &s2c)) {
+        hipLaunchKernelGGL(blkd_norm_op, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, h, (const float *)nullptr,
+                           (float *)nullptr, B->w_in, B->eps, d, 3, s2c, op, sc);
+        QBK_HIP(hipGetLastError());
+        if ((rc = q4_set_run_staged(B->qkv, B->ycat, false, B->ws, s))) return rc;
+    } else {
+        hipLaunchKernelGGL(blkd_norm, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, h, (const float *)nullptr,
+                           (float *)nullptr, B->w_in, B->eps, B->xcat, 3, d);
+        QBK_HIP(hipGetLastError());
+        if ((rc = q4_set_run(B->qkv, B->xcat, false, B->ycat, false, B->ws, s))) return rc;
+    }
     hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, B->w_q, B->w_k,
                        B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
     QBK_HIP(hipGetLastError());
@@ -588,10 +721,25 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     B->filled[0] = pos + 1;
     if ((rc = q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s))) return rc;
     // MLP sublayer: h1 = o + h, then its norm
-    hipLaunchKernelGGL(blkd_norm, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
-                       B->w_post, B->eps, B->xcat, 2, d);
-    QBK_HIP(hipGetLastError());
-    if ((rc = q4_set_run(B->gu, B->xcat, false, B->ycat, false, B->ws, s))) return rc;
+    if (fits && q4_set_flat_operand(B->gu, B->ws, &op, &sc, &s2c)) {
+        hipLaunchKernelGGL(blkd_norm_op, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
+                           B->w_post, B->eps, d, 2, s2c, op, sc);
+        QBK_HIP(hipGetLastError());
+        if ((rc = q4_set_run_staged(B->gu, B->ycat, false, B->ws, s))) return rc;
+    } else {
+        hipLaunchKernelGGL(blkd_norm, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
+                           B->w_post, B->eps, B->xcat, 2, d);
+        QBK_HIP(hipGetLastError());
+        if ((rc = q4_set_run(B->gu, B->xcat, false, B->ycat, false, B->ws, s))) return rc;
+    }
+    // h' = down(SwiGLU) + h1: the residual added in the down projection's
+    // epilogue when it runs from a flat operand
+    if (q4_flat_operand(B->down, B->ws, &op, &sc)) {
+        hipLaunchKernelGGL(blkd_swiglu_op, dim3((unsigned)div_ceil((size_t)ffn / 16, 256)), dim3(256), 0, s,
+                           B->ycat, ffn, B->down->s2, op, sc);
+        QBK_HIP(hipGetLastError());
+        return q4_run_staged(B->down, h, false, B->h1, B->ws, s);
+    }
     hipLaunchKernelGGL(blkd_swiglu, dim3((ffn + 255) / 256), dim3(256), 0, s, B->ycat, B->hid, ffn);
     QBK_HIP(hipGetLastError());
     if ((rc = q4_run(B->down, 1, B->hid, true, B->dout, false, B->ws, s))) return rc;

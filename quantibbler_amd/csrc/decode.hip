@@ -26,12 +26,12 @@
 #include <vector>
 
 #include "factor_internal.h"
+#include "q4_operand.h"
 
 namespace qbk {
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // Pointers read from a layer table are generic to the compiler; loading
 // through an address_space(1) pointer keeps them global loads (flat loads
 // count against both vmcnt and lgkmcnt and defeat per-load waits).
@@ -57,6 +57,7 @@ struct Q4Args {
     uint8_t *tb_op, *tb_sc;      // stage 1: stage 2's operand and scales
     int y_bf16, vec_ok;          // vec_ok: x rows allow 16-element vector loads
     uint32_t c7;                 // 0x77777777 (fp4 sign build)
+    const float *resid;          // stage 2, f32 y: added to y (y = (t s1 + bias) + resid), or null
 };
 
 // The table entry of layer li (scalar loads).
@@ -86,83 +87,6 @@ __device__ __forceinline__ Q4Layer q4_entry(const Q4Args &a, uint32_t li) {
 __device__ __forceinline__ uint32_t q4_layer_of(const Q4Args &a, uint32_t wgi) {
     if (a.n_layers == 1) return 0;
     return ((__attribute__((address_space(4))) const uint32_t *)a.wg_layer)[wgi];
-}
-
-__device__ __forceinline__ int e8m0_of(float amax) {
-    // exponent so that amax * 2^-e lies in [128, 256): e = floor(log2 amax) - 7
-    int ex = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
-    int e = ex - 7;
-    return e < -126 ? -126 : (e > 126 ? 126 : e);
-}
-
-__device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
-
-// One run of 16 activations z = bf16(s2 * x) as stage 1's fp8 operand:
-// z splits exactly into hi + lo, each fp8 e4m3 part keeping 4 significant
-// bits relative to its block's E8M0 exponent (e_hi from the block max of z,
-// e_lo from the block max of the residual).  The E8M0 scale given by MFMA
-// lane group G covers the activations k = 128s + kq4(G, e) (measured on
-// gfx950): the two runs 16(G>>1) + 64(G&1) + {0, 32}, i.e. runs r and r^2, so
-// the block max is one shuffle away -- the calling lanes must hold runs r
-// and r^2 of a slice at lane distance 2.
-__device__ __forceinline__ void q4_run_operand(float z[16], uint32_t hw[4], uint32_t lw[4], int &e_hi,
-                                               int &e_lo) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(z[e]));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
-    const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
-    float rmax = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
-        hw[q] = (uint32_t)w;
-        z[4 * q] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
-        z[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
-        z[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
-        z[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
-#pragma unroll
-        for (int u = 0; u < 4; u++) rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
-    }
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
-    e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
-    const float inv_lo = pow2f(-e_lo);
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
-        lw[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
-    }
-}
-
-// z = bf16(s2 * x) of 16 bf16 activations (two 16-byte words) and their s2.
-__device__ __forceinline__ void q4_run_z(const u32x4_t xr[2], const u32x4_t sr[4], float z[16]) {
-#pragma unroll
-    for (int q = 0; q < 2; q++) {
-#pragma unroll
-        for (int h = 0; h < 4; h++) {
-            z[8 * q + 2 * h] = bf16_to_f32(xr[q][h] & 0xffff);
-            z[8 * q + 2 * h + 1] = bf16_to_f32(xr[q][h] >> 16);
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-            z[4 * q + u] = bf16_to_f32(f32_to_bf16(__uint_as_float(sr[q][u]) * z[4 * q + u]));
-    }
-}
-
-// Where run r (of slice u, token b) of a step's operand lives in the layout
-// [slice][4 lane groups][ncol][32 B]: lane group 2(r>>2) + ((r>>1)&1), byte
-// offset 16(r&1); hi in column 2b, lo in 2b + 1.  Its two scale bytes (hi,
-// lo) sit in [slice][4][ncol] at group 2(r&1) + (r>>2) when r & 2 == 0.
-__device__ __forceinline__ size_t q4_run_slot(size_t slice, int r, int ncol, int b) {
-    return (slice * 4 + 2 * (r >> 2) + ((r >> 1) & 1)) * ncol + 2 * b;
-}
-__device__ __forceinline__ size_t q4_run_scale(size_t slice, int r, int ncol, int b) {
-    return (slice * 4 + 2 * (r & 1) + (r >> 2)) * ncol + 2 * b;
 }
 
 // x -> stage 1's fp8 operand.  Workgroup (x, layer); one thread per run of
@@ -386,8 +310,9 @@ __device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, cons
         const float t = valid ? bf16_to_f32(f32_to_bf16(v)) : 0.0f;
         if (STAGE == 2) {
             if (valid) {
-                const float y = t * so + bi;
+                float y = t * so + bi;
                 const size_t o = L.out0 * (size_t)a.batch + (size_t)b * L.rows_valid + row;
+                if (a.resid) y = y + a.resid[o];
                 if (a.y_bf16)
                     ((uint16_t *)a.out)[o] = f32_to_bf16(y);
                 else
@@ -725,7 +650,7 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
 // the layers' s2 concatenated (null when some din is not a multiple of 128).
 static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32_t *wg1,
                     const uint32_t *wg2, const float *s2cat, const void *x, bool xf32, void *y, bool ybf16,
-                    void *ws, hipStream_t s) {
+                    void *ws, hipStream_t s, const float *resid = nullptr) {
     char *w = (char *)ws;
     Q4Args a{};
     a.c7 = 0x77777777u;
@@ -747,6 +672,7 @@ static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32
         a.op = (uint8_t *)(w + G.o_op2);
         a.sc = (uint8_t *)(w + G.o_sc2);
         a.out = y;
+        a.resid = ybf16 ? nullptr : resid;
         a.n_wg = G.n_wg2;
         a.wg_layer = wg2;
     }
@@ -822,6 +748,27 @@ int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y,
     return QBK_OK;
 }
 
+bool q4_flat_operand(const qbk_factor *L, void *ws, uint8_t **op, uint8_t **sc) {
+    Q4Layer tab[2];
+    Q4Geom G;
+    q4_build(&L, 1, 1, L->num_cus, tab, G);
+    if (!G.din_mult128) return false;
+    *op = (uint8_t *)ws + G.o_op1;
+    *sc = (uint8_t *)ws + G.o_sc1;
+    return true;
+}
+
+int q4_run_staged(const qbk_factor *L, void *y, bool ybf16, const float *resid, void *ws, hipStream_t s) {
+    Q4Layer tab[2];
+    Q4Geom G;
+    q4_build(&L, 1, 1, L->num_cus, tab, G);
+    for (int ph = 2; ph <= Q4_PHASES; ph++) {
+        int rc = q4_phase(ph, G, L->q4_tab, nullptr, nullptr, nullptr, nullptr, false, y, ybf16, ws, s, resid);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
+
 }  // namespace qbk
 
 using namespace qbk;
@@ -850,6 +797,22 @@ int q4_set_run(const qbk_factor_set *S, const void *x, bool xf32, void *y, bool 
 }
 
 size_t q4_set_workspace(const qbk_factor_set *S) { return S->geom.bytes; }
+
+bool q4_set_flat_operand(const qbk_factor_set *S, void *ws, uint8_t **op, uint8_t **sc, const float **s2cat) {
+    if (!S->s2cat || !S->geom.din_mult128) return false;
+    *op = (uint8_t *)ws + S->geom.o_op1;
+    *sc = (uint8_t *)ws + S->geom.o_sc1;
+    *s2cat = S->s2cat;
+    return true;
+}
+
+int q4_set_run_staged(const qbk_factor_set *S, void *y, bool ybf16, void *ws, hipStream_t s) {
+    for (int ph = 2; ph <= Q4_PHASES; ph++) {
+        int rc = q4_phase(ph, S->geom, S->tab, S->wg1, S->wg2, nullptr, nullptr, false, y, ybf16, ws, s);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
 
 // The set at a batch of n tokens: the device tables are the batch-1 ones
 // (their offsets are per token); the geometry is the batch's.

@@ -73,6 +73,17 @@ size_t q4_set_workspace_batch(const qbk_factor_set *S, size_t n);
 int q4_set_run_batch(const qbk_factor_set *S, size_t n, const void *x, bool xf32, void *y, bool ybf16, void *ws,
                      hipStream_t s);
 
+// A batch-1 decode whose stage-1 operand a caller's kernel writes itself
+// (q4_operand.h's runs, flat over the concatenated x: run t covers k = 16t
+// .. 16t + 15 at global slice t / 8, two columns): where the operand and its
+// scales go in the workspace ws (and, for a set, the layers' s2
+// concatenated).  False when some din is not a multiple of 128 (no flat
+// layout).  Then the two GEMV launches; resid (f32 y only) is added to y.
+bool q4_flat_operand(const qbk_factor *L, void *ws, uint8_t **op, uint8_t **sc);
+bool q4_set_flat_operand(const qbk_factor_set *S, void *ws, uint8_t **op, uint8_t **sc, const float **s2cat);
+int q4_run_staged(const qbk_factor *L, void *y, bool ybf16, const float *resid, void *ws, hipStream_t s);
+int q4_set_run_staged(const qbk_factor_set *S, void *y, bool ybf16, void *ws, hipStream_t s);
+
 // prefill.hip: the sign layout of the prefill GEMM (rows_p a multiple of
 // 128, bits_p of 64), its workspace, and the two-stage GEMM for N tokens:
 // x [N][din] (bf16, or f32 when xf32) -> y [N][dout].

@@ -1,0 +1,95 @@
+// q4_operand.h -- the decode GEMV's stage-1 operand: activations z =
+// bf16(s2 * x) as two fp8 e4m3 columns (hi, lo) with E8M0 block scales, in
+// the layout the fp4 x fp8 scaled MFMA reads.  Shared by the decode's prep
+// kernels (decode.hip) and the decoder block's kernels that write the
+// operand of the projection they feed directly (block.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qbk_internal.h"
+
+namespace qbk {
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int e8m0_of(float amax) {
+    // exponent so that amax * 2^-e lies in [128, 256): e = floor(log2 amax) - 7
+    int ex = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
+    int e = ex - 7;
+    return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+__device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+// One run of 16 activations z = bf16(s2 * x) as stage 1's fp8 operand:
+// z splits exactly into hi + lo, each fp8 e4m3 part keeping 4 significant
+// bits relative to its block's E8M0 exponent (e_hi from the block max of z,
+// e_lo from the block max of the residual).  The E8M0 scale given by MFMA
+// lane group G covers the activations k = 128s + kq4(G, e) (measured on
+// gfx950): the two runs 16(G>>1) + 64(G&1) + {0, 32}, i.e. runs r and r^2, so
+// the block max is one shuffle away -- the calling lanes must hold runs r
+// and r^2 of a slice at lane distance 2.
+__device__ __forceinline__ void q4_run_operand(float z[16], uint32_t hw[4], uint32_t lw[4], int &e_hi,
+                                               int &e_lo) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(z[e]));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+    const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+    float rmax = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
+        hw[q] = (uint32_t)w;
+        z[4 * q] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
+        z[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
+        z[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
+        z[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+#pragma unroll
+        for (int u = 0; u < 4; u++) rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
+    }
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
+    e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+    const float inv_lo = pow2f(-e_lo);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
+        lw[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
+    }
+}
+
+// z = bf16(s2 * x) of 16 bf16 activations (two 16-byte words) and their s2.
+__device__ __forceinline__ void q4_run_z(const u32x4_t xr[2], const u32x4_t sr[4], float z[16]) {
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            z[8 * q + 2 * h] = bf16_to_f32(xr[q][h] & 0xffff);
+            z[8 * q + 2 * h + 1] = bf16_to_f32(xr[q][h] >> 16);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            z[4 * q + u] = bf16_to_f32(f32_to_bf16(__uint_as_float(sr[q][u]) * z[4 * q + u]));
+    }
+}
+
+// Where run r (of slice u, token b) of a step's operand lives in the layout
+// [slice][4 lane groups][ncol][32 B]: lane group 2(r>>2) + ((r>>1)&1), byte
+// offset 16(r&1); hi in column 2b, lo in 2b + 1.  Its two scale bytes (hi,
+// lo) sit in [slice][4][ncol] at group 2(r&1) + (r>>2) when r & 2 == 0.
+__device__ __forceinline__ size_t q4_run_slot(size_t slice, int r, int ncol, int b) {
+    return (slice * 4 + 2 * (r >> 2) + ((r >> 1) & 1)) * ncol + 2 * b;
+}
+__device__ __forceinline__ size_t q4_run_scale(size_t slice, int r, int ncol, int b) {
+    return (slice * 4 + 2 * (r & 1) + (r >> 2)) * ncol + 2 * b;
+}
+
+}  // namespace qbk

@@ -65,29 +65,56 @@ __device__ __forceinline__ void amax_merge(float &bv, uint32_t &bi, float v, uin
     }
 }
 
-__global__ void __launch_bounds__(TRUNK_THREADS) trunk_argmax(const float *logits, size_t vocab, int32_t *out) {
-    __shared__ float sv[TRUNK_THREADS / 64];
-    __shared__ uint32_t si[TRUNK_THREADS / 64];
+// A row per workgroup of ARGMAX_THREADS: a scalar head up to a 16-byte
+// boundary, the body in 16-byte loads four a thread in flight (a vocabulary
+// row is ~0.5 MB: one load at a time per thread left the kernel latency
+// bound at 156 us), a scalar tail.  amax_merge is a total order, so the
+// merge order does not change the winner.
+#define ARGMAX_THREADS 1024
+typedef float tr_f32x4_t __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(ARGMAX_THREADS) trunk_argmax(const float *logits, size_t vocab, int32_t *out) {
+    __shared__ float sv[ARGMAX_THREADS / 64];
+    __shared__ uint32_t si[ARGMAX_THREADS / 64];
     const float *row = logits + (size_t)blockIdx.x * vocab;
+    const uint32_t tid = threadIdx.x;
     float bv = -INFINITY;
     uint32_t bi = 0;
-    for (size_t i = threadIdx.x; i < vocab; i += TRUNK_THREADS) {
-        const float v = row[i];
-        amax_merge(bv, bi, v != v ? -INFINITY : v, (uint32_t)i);
+    auto take = [&](float v, size_t i) { amax_merge(bv, bi, v != v ? -INFINITY : v, (uint32_t)i); };
+    size_t head = (4 - (((uintptr_t)row >> 2) & 3)) & 3;
+    head = head < vocab ? head : vocab;
+    if (tid < head) take(row[tid], tid);
+    const size_t nb = (vocab - head) / 4;
+    const tr_f32x4_t *b4 = (const tr_f32x4_t *)(row + head);
+    size_t j = tid;
+    for (; j + 3 * ARGMAX_THREADS < nb; j += 4 * ARGMAX_THREADS) {
+        tr_f32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = b4[j + u * ARGMAX_THREADS];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) take(v[u][e], head + 4 * (j + u * ARGMAX_THREADS) + e);
     }
+    for (; j < nb; j += ARGMAX_THREADS) {
+        const tr_f32x4_t v = b4[j];
+#pragma unroll
+        for (int e = 0; e < 4; e++) take(v[e], head + 4 * j + e);
+    }
+    for (size_t i = head + 4 * nb + tid; i < vocab; i += ARGMAX_THREADS) take(row[i], i);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float v = __shfl_xor(bv, o, 64);
         const uint32_t i = (uint32_t)__shfl_xor((int)bi, o, 64);
         amax_merge(bv, bi, v, i);
     }
-    if ((threadIdx.x & 63) == 0) {
-        sv[threadIdx.x >> 6] = bv;
-        si[threadIdx.x >> 6] = bi;
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < TRUNK_THREADS / 64; w++) amax_merge(bv, bi, sv[w], si[w]);
+    if (tid == 0) {
+        for (int w = 1; w < ARGMAX_THREADS / 64; w++) amax_merge(bv, bi, sv[w], si[w]);
         out[blockIdx.x] = (int32_t)bi;
     }
 }
@@ -149,7 +176,7 @@ int qbk_argmax_dev(qbk_ctx *ctx, const float *logits, size_t rows, size_t vocab,
     if (vocab == 0 || vocab > 0xFFFFFFFFu) return fail(QBK_ERR_VALIDATION, "argmax needs 1 <= vocab < 2^32");
     if (rows == 0) return QBK_OK;
     if ((rc = bind(ctx))) return rc;
-    hipLaunchKernelGGL(trunk_argmax, dim3((unsigned)rows), dim3(TRUNK_THREADS), 0, (hipStream_t)stream, logits,
+    hipLaunchKernelGGL(trunk_argmax, dim3((unsigned)rows), dim3(ARGMAX_THREADS), 0, (hipStream_t)stream, logits,
                        vocab, out);
     QBK_HIP(hipGetLastError());
     return QBK_OK;

@@ -18,6 +18,10 @@ COS_MIN = 0.9999
 REL_MAX = 0.01
 
 
+def say(*a):
+    print(*a, flush=True)
+
+
 @pytest.fixture(scope="module")
 def ctx():
     from quantibbler_amd import GpuContext
@@ -246,3 +250,40 @@ def test_block_batched_decode(ctx, orc):
     with pytest.raises(KernelError, match="sequence 10 of a block holding 10"):
         block.prefill_seq_dev(10, h[:d], 1, ws, ws.numel(), st)
     block.close()
+
+
+@pytest.mark.parametrize("d,ffn", [(256, 512), (6144, 1024)])
+def test_block_decode_fused_operands_bit_identical(ctx, orc, d, ffn):
+    """The one-sequence step writes the projections' fp8 operands from its
+    norm and SwiGLU kernels and adds the residual in the down projection's
+    epilogue; the batched step at batch 1 runs the same arithmetic through
+    separate prep and add kernels.  Two blocks of the same weights fed the
+    same inputs stay bit-identical over 70 positions (a key-block boundary
+    crossed); at d 6144 the set of three layers has 1152 operand runs, more
+    than the norm's 1024 threads."""
+    from quantibbler_amd import DecoderBlock, FactorLayer
+
+    H, Hk, hd, cap, blk = 4, 2, 128, 80, 64
+    theta, eps = 500000.0, 1e-5
+    say(f"block fused operands d={d} ffn={ffn}")
+    rng = np.random.default_rng(d + ffn)
+    shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
+              (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    bfv = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a.astype(np.float32)))
+    norms = [bfv(1.0 + 0.1 * rng.standard_normal(d)), bfv(1.0 + 0.1 * rng.standard_normal(d))]
+    qk = [bfv(1.0 + 0.2 * rng.standard_normal(hd)), bfv(1.0 + 0.2 * rng.standard_normal(hd))]
+    one = DecoderBlock(ctx, devs, *norms, H, Hk, hd, theta, eps, cap, blk, *qk)
+    bat = DecoderBlock(ctx, devs, *norms, H, Hk, hd, theta, eps, cap, blk, *qk, n_seqs=1)
+    st = torch.cuda.current_stream()
+    wn = bat.decode_batch_workspace_size(1)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    for pos in range(70):
+        x = torch.from_numpy(rng.standard_normal(d).astype(np.float32)).cuda()
+        ha, hb = x.clone(), x.clone()
+        one.decode_dev(ha, pos, st)
+        bat.decode_batch_dev(hb, [pos], ws, wn, st)
+        torch.cuda.synchronize()
+        assert torch.equal(ha, hb), (pos, float((ha - hb).abs().max()))

@@ -118,6 +118,36 @@ def test_argmax_first_max_rule(ctx):
     assert out.cpu().numpy().tolist() == [greedy(row) for row in rows]
 
 
+@pytest.mark.parametrize("vocab", [1, 3, 7, 128256, 128259])
+def test_argmax_wide_rows(ctx, vocab):
+    """Rows of odd length start off the 16-byte grid (the kernel's scalar
+    head), long rows take the vector body and a scalar tail; the winner is
+    placed in each part, with ties between the parts."""
+    from quantibbler_amd.gpu import argmax_dev
+
+    say(f"trunk argmax wide rows vocab={vocab}")
+    rng = np.random.default_rng(vocab)
+    rows = []
+    for pos in sorted({0, 1, 2, vocab // 2, vocab - 2, vocab - 1}):
+        if not 0 <= pos < vocab:
+            continue
+        r = rng.standard_normal(vocab).astype(np.float32)
+        r[pos] = 9.0
+        rows.append(r)
+        t = r.copy()
+        t[vocab - 1 - pos] = 9.0                                  # a tie: the first index wins
+        rows.append(t)
+    r = np.full(vocab, np.nan, np.float32)
+    r[-1] = -1.0
+    rows.append(r)
+    x = np.stack(rows)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty(len(rows), dtype=torch.int32, device="cuda")
+    argmax_dev(ctx, xd, len(rows), vocab, out, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert out.cpu().numpy().tolist() == [int(np.argmax(np.nan_to_num(row, nan=-np.inf))) for row in rows]
+
+
 @pytest.fixture(scope="module")
 def md():
     from quantibbler_amd.model import ModelDir
