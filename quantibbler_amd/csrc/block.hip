@@ -714,12 +714,17 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     QBK_HIP(hipGetLastError());
     const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos + 1, B->hd, B->hd};
     const size_t cached = B->tokens[0] <= pos ? B->tokens[0] : 0;
-    if ((rc = qbk_attention_sage_decode_step_dev(ctx, &sh, B->qrot, B->kc, B->vc, B->block, B->attn, B->state,
-                                                 B->state_bytes, B->cap, cached, stream)))
+    // the attention's combine writes the o projection's operand directly
+    DecOpSink sink{B->o->s2, nullptr, nullptr};
+    const bool osink = B->hd % 128 == 0 && q4_flat_operand(B->o, B->ws, &sink.op, &sink.sc);
+    if ((rc = sage_decode_step_sink(ctx, &sh, B->qrot, B->kc, B->vc, B->block, B->attn, B->state, B->state_bytes,
+                                    B->cap, cached, osink ? &sink : nullptr, stream)))
         return rc;
     B->tokens[0] = pos + 1;
     B->filled[0] = pos + 1;
-    if ((rc = q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s))) return rc;
+    if ((rc = osink ? q4_run_staged(B->o, B->oout, false, nullptr, B->ws, s)
+                    : q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s)))
+        return rc;
     // MLP sublayer: h1 = o + h, then its norm
     if (fits && q4_set_flat_operand(B->gu, B->ws, &op, &sc, &s2c)) {
         hipLaunchKernelGGL(blkd_norm_op, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,

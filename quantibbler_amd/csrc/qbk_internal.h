@@ -96,6 +96,18 @@ int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride
                       size_t kv_stride, size_t block, float *out, size_t o_stride, void *state, size_t st_stride,
                       size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st);
 
+// A decode step (qbk_attention_sage_decode_step_dev's contract) whose
+// combine also writes its output [n_heads][val_dim] as the batch-1 stage-1
+// fp8 operand of the factor layer it feeds (q4_operand.h's flat runs; val_dim
+// a multiple of 128): that layer's s2, operand and scale bytes.
+struct DecOpSink {
+    const float *s2;
+    uint8_t *op, *sc;
+};
+int sage_decode_step_sink(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
+                          const float *v, size_t block_size, float *out, void *state, size_t state_size,
+                          size_t capacity, size_t cached_tokens, const DecOpSink *sink, void *stream);
+
 // ---- device helpers -------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {

@@ -28,6 +28,7 @@
 #include <string>
 
 #include "qbk_internal.h"
+#include "q4_operand.h"
 
 namespace qbk {
 
@@ -659,6 +660,8 @@ struct DecArgs {
     uint32_t *qsw;                       // [H][d4] the query's codes (grouped kernels)
     float *qdl;                          // [H] and its delta
     float *mprev;                        // [H][nkb] running max before each block, or null
+    const float *op_s2;                  // combine: the next layer's s2, and where its operand goes
+    uint8_t *op, *op_sc;                 //   (DecOpSink), or null
 };
 
 // Several sequences' decode steps in one set of launches: sequence s has
@@ -1324,7 +1327,36 @@ __global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da, DecSeqTab t)
             }
         }
     }
-    if (act) a.out[(size_t)h * dv + c] = o / ell;
+    const float val = act ? o / ell : 0.0f;
+    if (act) a.out[(size_t)h * dv + c] = val;
+    if (da.op) {
+        // the output as the next layer's operand: a run of 16 channels a
+        // lane of wave 0 (dv a multiple of 128: the head's runs fill whole
+        // slices, lanes past them shadow the last slice's)
+        __shared__ float ov[REF_MAXD];
+        if (act) ov[c] = val;
+        __syncthreads();
+        if (tid < 64) {
+            const uint32_t nr = dv / 16, rl = tid < nr ? tid : nr - 8 + (tid & 7);
+            const float *s2 = da.op_s2 + (size_t)h * dv + 16 * rl;
+            float z[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) z[e] = bf16_to_f32(f32_to_bf16(s2[e] * ov[16 * rl + e]));
+            uint32_t hw[4], lw[4];
+            int e_hi, e_lo;
+            q4_run_operand(z, hw, lw, e_hi, e_lo);
+            if (tid < nr) {
+                const size_t t = (size_t)h * nr + rl;
+                const int r = (int)(t & 7);
+                const size_t slot = q4_run_slot(t >> 3, r, 2, 0), byte = 16 * (r & 1);
+                *(uint4 *)(da.op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                *(uint4 *)(da.op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+                if ((r & 2) == 0)
+                    *(uint16_t *)(da.op_sc + q4_run_scale(t >> 3, r, 2, 0)) =
+                        (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
+            }
+        }
+    }
 }
 
 // Grouped form of sage_dec_scores and sage_dec_pv: one workgroup per (key
@@ -1648,6 +1680,8 @@ static void dec_bind(const DecPlan &P, DecArgs &da, void *ws) {
     da.qsw = (uint32_t *)(w + P.o_qsw);
     da.qdl = (float *)(w + P.o_qdl);
     da.mprev = nullptr;
+    da.op_s2 = nullptr;
+    da.op = da.op_sc = nullptr;
 }
 
 // One step over seq_kv cached tokens with a workspace laid out for cap; the
@@ -1655,7 +1689,8 @@ static void dec_bind(const DecPlan &P, DecArgs &da, void *ws) {
 // as they are (the caller guarantees that those cache rows are the ones the
 // workspace's earlier step quantised) and the rest are quantised again.
 static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, const float *v,
-                      size_t block, float *out, void *ws, size_t cap, size_t cached, hipStream_t st) {
+                      size_t block, float *out, void *ws, size_t cap, size_t cached, hipStream_t st,
+                      const DecOpSink *sink = nullptr) {
     DecPlan P = dec_plan(s, block, cap);
     DecArgs da = P.da;
     RefArgs &a = da.r;
@@ -1665,6 +1700,11 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     a.out = out;
     char *w = (char *)ws;
     dec_bind(P, da, ws);
+    if (sink) {
+        da.op_s2 = sink->s2;
+        da.op = sink->op;
+        da.op_sc = sink->sc;
+    }
     const unsigned nkb = (unsigned)a.nkb, H = (unsigned)a.H;
     a.kb0 = cached / block;
     const DPrepGeom g = dprep_geom(a, k, v);
@@ -2457,6 +2497,15 @@ int qbk_attention_sage_decode_step_dev(qbk_ctx *ctx, const qbk_attn_shape *shape
                                        const float *k, const float *v, size_t block_size, float *out,
                                        void *state, size_t state_size, size_t capacity, size_t cached_tokens,
                                        void *stream) {
+    return sage_decode_step_sink(ctx, shape, q, k, v, block_size, out, state, state_size, capacity,
+                                 cached_tokens, nullptr, stream);
+}
+
+}  // extern "C"
+
+int qbk::sage_decode_step_sink(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
+                               const float *v, size_t block_size, float *out, void *state, size_t state_size,
+                               size_t capacity, size_t cached_tokens, const DecOpSink *sink, void *stream) {
     int rc;
     if ((rc = validate_decode(shape, block_size, nullptr))) return rc;
     if (shape->seq_kv > capacity)
@@ -2474,8 +2523,12 @@ int qbk_attention_sage_decode_step_dev(qbk_ctx *ctx, const qbk_attn_shape *shape
                                             state_size, need, capacity));
     if (!q || !k || !v || !out || !state) return fail(QBK_ERR_VALIDATION, "null buffer");
     if ((rc = bind(ctx))) return rc;
-    return run_decode(shape, q, k, v, block_size, out, state, capacity, cached_tokens, (hipStream_t)stream);
+    if (sink && (shape->val_dim % 128 != 0 || !sink->s2 || !sink->op || !sink->sc))
+        return fail(QBK_ERR_VALIDATION, "an operand sink needs val_dim a multiple of 128 and its three buffers");
+    return run_decode(shape, q, k, v, block_size, out, state, capacity, cached_tokens, (hipStream_t)stream, sink);
 }
+
+extern "C" {
 
 size_t qbk_sage_blk_workspace_size(const qbk_attn_shape *shape) {
     if (!shape) return 0;
