@@ -73,11 +73,11 @@ struct G32Args {
     const void *x;         // stage 1, XM 1 / 2: x [N][din] bf16 / f32, s2 [din]; din % 8 == 0
     const float *s2;
     size_t din;
-    // stage 1
-    float *part;           // [split][N][M_p] f32 (split > 1)
-    uint16_t *t_out;       // [N][M_p] bf16 (split == 1), zero for rows >= M_valid
+    float *part;           // [split][N][M_p] f32 (split > 1, either stage)
     size_t k_per_split;
     int split;
+    // stage 1
+    uint16_t *t_out;       // [N][M_p] bf16 (split == 1), zero for rows >= M_valid
     // stage 2
     void *y;               // [N][M_valid] bf16 or f32
     const float *s1, *bias;
@@ -126,7 +126,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     const int wr = wave % WM, wc = wave / WM;  // 64-row block, 32 NT-token block
     const size_t n0 = (size_t)blockIdx.x * BN, m0 = (size_t)blockIdx.y * BM;
     size_t kb = 0, ke = a.K_p;
-    if (STAGE == 1) {
+    if (STAGE == 1 || a.split > 1) {
         kb = (size_t)blockIdx.z * a.k_per_split;
         ke = kb + a.k_per_split < a.K_p ? kb + a.k_per_split : a.K_p;
     }
@@ -288,7 +288,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     const size_t row0 = m0 + 64 * wr;  // this wave's first row
     // stage 2: s1 and bias of rows 8c .. 8c + 7 of the wave (c = lane % 8)
     float s1v[8], biv[8];
-    if (STAGE == 2 && gvalid) {
+    if (STAGE == 2 && gvalid && a.split == 1) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const size_t rr = row0 + 8 * (lane & 7) + e;
@@ -308,7 +308,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
         __builtin_amdgcn_wave_barrier();
         const size_t nb = n0 + wc * 32 * NT + nt * 32;  // first token of the n-tile
         if (gvalid) {
-            if (STAGE == 1 && a.split > 1) {
+            if (a.split > 1) {
                 // f32 partials: 16 lanes per token (4 rows each), four tokens per store
 #pragma unroll 4
                 for (int k = 0; k < 8; k++) {
@@ -422,6 +422,54 @@ __global__ void __launch_bounds__(256) g32_reduce_kernel(const float *__restrict
     *(uint4 *)(t + e0) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Stage 2 split over K: y = bf16(sum of the split partials in split order)
+// * s1 + bias for rows < dout (the stage-2 epilogue's arithmetic on the whole
+// sum); eight rows per thread over [N][M_p].
+__global__ void __launch_bounds__(256) g32_reduce_y_kernel(const float *__restrict__ part, int split,
+                                                            size_t stride, size_t ld, size_t dout,
+                                                            const float *__restrict__ s1,
+                                                            const float *__restrict__ bias, void *y, int y_bf16,
+                                                            int vec_y, size_t chunks) {
+    const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const size_t e0 = c * 8, n = e0 / ld, r0 = e0 % ld;
+    if (r0 >= dout) return;
+    float v[8];
+    const float4 *p0 = (const float4 *)(part + e0);
+    const float4 a0 = p0[0], a1 = p0[1];
+    v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+    v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+    for (int s = 1; s < split; s++) {
+        const float4 *ps = (const float4 *)(part + (size_t)s * stride + e0);
+        const float4 c0 = ps[0], c1 = ps[1];
+        v[0] += c0.x; v[1] += c0.y; v[2] += c0.z; v[3] += c0.w;
+        v[4] += c1.x; v[5] += c1.y; v[6] += c1.z; v[7] += c1.w;
+    }
+    float yv[8];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint32_t u = f32x2_to_bf16x2(v[2 * p], v[2 * p + 1]);
+        const size_t ra = r0 + 2 * p < dout ? r0 + 2 * p : 0, rb = r0 + 2 * p + 1 < dout ? r0 + 2 * p + 1 : 0;
+        yv[2 * p] = __uint_as_float(u << 16) * s1[ra] + bias[ra];
+        yv[2 * p + 1] = __uint_as_float(u & 0xffff0000u) * s1[rb] + bias[rb];
+    }
+    if (y_bf16 && vec_y && r0 + 8 <= dout) {
+        uint32_t w[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) w[p] = f32x2_to_bf16x2(yv[2 * p], yv[2 * p + 1]);
+        *(uint4 *)((uint16_t *)y + n * dout + r0) = make_uint4(w[0], w[1], w[2], w[3]);
+        return;
+    }
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        if (r0 + p >= dout) continue;
+        if (y_bf16)
+            ((uint16_t *)y)[n * dout + r0 + p] = f32_to_bf16(yv[p]);
+        else
+            ((float *)y)[n * dout + r0 + p] = yv[p];
+    }
+}
+
 // ------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------
@@ -456,16 +504,30 @@ static int g32_split(const qbk_factor *L, size_t N) {
     return s;
 }
 
+// Stage-2 K split, by the same rule, where the stage's own tiles (one row
+// block a workgroup, no split of its own) leave CUs idle: a decode batch
+// of 9-64 tokens gives q/o 32 workgroups of 18 64-k stages each, a chain of
+// dependent stages per workgroup, without it.
+static int g32_split2(const qbk_factor *L, size_t N) {
+    if (g32_big(L->dout_p, N, L->num_cus)) return 1;
+    const size_t tiles = div_ceil(N, G32Small::BN) * div_ceil(L->dout_p, G32Small::BM);
+    int s = 1;
+    while (tiles * s < (size_t)L->num_cus && s < 8 && L->r_p / (G_BK * 2 * s) >= 4) s *= 2;
+    return s;
+}
+
 // Workspace: z bf16 [N][din_p] (written only when stage 1 cannot form z from x
-// itself) | partials f32 [split][N][r_p] | t bf16 [N][r_p].
+// itself) | partials f32 [split][N][r_p] | t bf16 [N][r_p] | stage 2's
+// partials f32 [split2][N][dout_p].
 struct G32Plan {
-    int split;
-    size_t o_z, o_part, o_t, bytes;
+    int split, split2;
+    size_t o_z, o_part, o_t, o_part2, bytes;
 };
 
 static G32Plan g32_plan(const qbk_factor *L, size_t N) {
     G32Plan p{};
     p.split = g32_split(L, N);
+    p.split2 = g32_split2(L, N);
     size_t off = 0;
     auto take = [&](size_t n) {
         size_t o = off;
@@ -475,6 +537,7 @@ static G32Plan g32_plan(const qbk_factor *L, size_t N) {
     p.o_z = take(N * L->din_p * 2);
     p.o_part = take(p.split > 1 ? (size_t)p.split * N * L->r_p * 4 : 0);
     p.o_t = take(N * L->r_p * 2);
+    p.o_part2 = take(p.split2 > 1 ? (size_t)p.split2 * N * L->dout_p * 4 : 0);
     p.bytes = off;
     return p;
 }
@@ -574,8 +637,18 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     b.vec_y = L->dout % 8 == 0 && (uintptr_t)y % 16 == 0;
     b.sign_mask = 0x80008000u;
     b.one_pair = 0x3F803F80u;
-    g32_launch_any<2, 0>(b, L->dout_p, 1, g32_big(L->dout_p, N, L->num_cus), s);
+    b.split = p.split2;
+    b.part = (float *)(w + p.o_part2);
+    b.k_per_split = round_up(div_ceil(L->r_p, p.split2), G_BK);
+    g32_launch_any<2, 0>(b, L->dout_p, p.split2, g32_big(L->dout_p, N, L->num_cus), s);
     QBK_HIP(hipGetLastError());
+    if (p.split2 > 1) {
+        const size_t chunks = N * L->dout_p / 8;
+        hipLaunchKernelGGL(g32_reduce_y_kernel, dim3((unsigned)div_ceil(chunks, 256)), dim3(256), 0, s,
+                           (const float *)b.part, p.split2, N * L->dout_p, L->dout_p, L->dout, L->s1, L->bias, y,
+                           ybf16 ? 1 : 0, b.vec_y, chunks);
+        QBK_HIP(hipGetLastError());
+    }
     return QBK_OK;
 }
 

@@ -154,13 +154,17 @@ def gpu_t(layer, ws, batch):
         assert not tb[:, r:].any()
         return tb[:, :r]
     # prefill GEMM: [z bf16 [batch][din_p] | f32 partials [split][batch][r_p]
-    # (split > 1) | t bf16 [batch][r_p]]
+    # (split > 1) | t bf16 [batch][r_p] | stage 2's f32 partials
+    # [split2][batch][dout_p] (split2 > 1)]
     from oracle import oracle as orc
 
     zb = rnd(batch * (-(-layer.din // 64) * 64) * 2)
-    for s in (1, 2, 4, 8):
+    dp = -(-layer.dout // 128) * 128
+    sizes = {(s, s2) for s in (1, 2, 4, 8) for s2 in (1, 2, 4, 8)}
+    for s, s2 in sorted(sizes):
         pb = rnd(s * batch * rp * 4) if s > 1 else 0
-        if zb + pb + rnd(batch * rp * 2) == ws.size:
+        p2 = rnd(s2 * batch * dp * 4) if s2 > 1 else 0
+        if zb + pb + rnd(batch * rp * 2) + p2 == ws.size:
             t = ws[zb + pb: zb + pb + batch * rp * 2].view(np.uint16).reshape(batch, rp)
             assert not t[:, r:].any()
             if s > 1:
