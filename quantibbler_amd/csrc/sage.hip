@@ -1372,14 +1372,18 @@ __global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da, DecSeqTab t)
 #define DEC_KMAX 256
 #define DEC_PMAX 512
 
+// GM, DM: the largest group and head_dim a kernel serves (register and LDS
+// arrays sized by them: the config-5 shape's 4 and 128 leave room for twice
+// the waves of the general 16 and 256).
+template <int GM, int DM>
 __global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da, DecSeqTab t) {
     if (t.n) dec_seq(da, t, blockIdx.z);
     const RefArgs &a = da.r;
     if (blockIdx.x >= a.nkb) return;  // a batched launch covers the longest sequence's blocks
-    __shared__ uint32_t qs[DEC_GMAX * (REF_MAXD / 4)];
-    __shared__ float qd[DEC_GMAX];
-    __shared__ float kms[REF_MAXD];
-    __shared__ __attribute__((aligned(16))) float term[DEC_GMAX * REF_MAXD];
+    __shared__ uint32_t qs[GM * (DM / 4)];
+    __shared__ float qd[GM];
+    __shared__ float kms[DM];
+    __shared__ __attribute__((aligned(16))) float term[GM * DM];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kb = blockIdx.x, bk = blockIdx.y, G = (uint32_t)(a.H / a.Hk);
     const uint32_t d = (uint32_t)a.d, d4 = d / 4, n4 = d4 / 4;
@@ -1392,9 +1396,9 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da, DecSeqTab t
     if (tid < d) kms[tid] = a.kmean[((size_t)bk * a.pnkb + kb) * d + tid];
     const uint32_t jl = lane < kj ? lane : kj - 1;
     const u32x4_t *krow = (const u32x4_t *)(a.khat + ((size_t)bk * a.pst + j0 + jl) * d4);
-    u32x4_t kv[REF_MAXD / 16];
+    u32x4_t kv[DM / 16];
 #pragma unroll
-    for (uint32_t u = 0; u < REF_MAXD / 16; u++)
+    for (uint32_t u = 0; u < DM / 16; u++)
         if (u < n4) kv[u] = krow[u];
     const float kd0 = a.kdelta[(size_t)bk * a.pst + j0 + jl];
     __syncthreads();
@@ -1429,7 +1433,7 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da, DecSeqTab t
             float kdl;
             if (j == lane) {
 #pragma unroll
-                for (uint32_t u = 0; u < REF_MAXD / 16; u++)
+                for (uint32_t u = 0; u < DM / 16; u++)
                     if (u < n4)
 #pragma unroll
                         for (int e = 0; e < 4; e++)
@@ -1458,12 +1462,14 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da, DecSeqTab t
     }
 }
 
+// GM, KM: the largest group and key block a kernel serves.
+template <int GM, int KM>
 __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     if (t.n) dec_seq(da, t, blockIdx.z);
     const RefArgs &a = da.r;
     if (blockIdx.x >= a.nkb) return;
-    __shared__ __attribute__((aligned(16))) float pf[DEC_GMAX * DEC_KMAX];
-    __shared__ __attribute__((aligned(16))) uint8_t ph[DEC_GMAX * DEC_KMAX];
+    __shared__ __attribute__((aligned(16))) float pf[GM * KM];
+    __shared__ __attribute__((aligned(16))) uint8_t ph[GM * KM];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kb = blockIdx.x, bk = blockIdx.y, G = (uint32_t)(a.H / a.Hk), nkb = (uint32_t)a.nkb;
     const uint32_t dv = (uint32_t)a.dv;
@@ -1475,9 +1481,9 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     const uint32_t hstep = 256 / dv, c = tid % dv, hs = tid / dv;
     const size_t vb = ((size_t)bk * a.pnkb + kb) * dv + c;
     const u32x4_t *vrow = (const u32x4_t *)(a.vhat + vb * a.blk4);
-    u32x4_t vv[DEC_KMAX / 16];
+    u32x4_t vv[KM / 16];
 #pragma unroll
-    for (uint32_t u = 0; u < DEC_KMAX / 16; u++)
+    for (uint32_t u = 0; u < KM / 16; u++)
         if (u < vn4) vv[u] = vrow[u];
     const float vdc = a.vd[vb];
     // and the scores of this wave's first head at this lane's first key
@@ -1516,8 +1522,8 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
                 pr = pr < 0.0f ? 0.0f : pr;
                 pc = (int)pr;
             }
-            pf[hg * DEC_KMAX + j] = p;
-            ph[hg * DEC_KMAX + j] = (uint8_t)pc;
+            pf[hg * KM + j] = p;
+            ph[hg * KM + j] = (uint8_t)pc;
         }
         if (lane == 0) {
             da.blive[h * nkb + kb] = live;
@@ -1528,7 +1534,7 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     // esum: p summed in key order (:315), by lane 0 of the head's wave
     for (uint32_t hg = wave; hg < G; hg += 4)
         if (lane == 0) {
-            const float *pp = pf + hg * DEC_KMAX;
+            const float *pp = pf + hg * KM;
             float esum = 0.0f;
             uint32_t t = 0;
 #pragma unroll 4
@@ -1545,16 +1551,35 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     // P^.V^ per (head, channel) (:317-341)
     if (hs < hstep)
         for (uint32_t hg = hs; hg < G; hg += hstep) {
-            const uint32_t *pw = (const uint32_t *)(ph + hg * DEC_KMAX);
+            const uint32_t *pw = (const uint32_t *)(ph + hg * KM);
             int pv = 0;
 #pragma unroll
-            for (uint32_t u = 0; u < DEC_KMAX / 16; u++)
+            for (uint32_t u = 0; u < KM / 16; u++)
                 if (u < vn4)
 #pragma unroll
                     for (int e = 0; e < 4; e++)
                         if (4 * u + e < tw) pv = __builtin_amdgcn_sdot4((int)pw[4 * u + e], (int)vv[u][e], pv, false);
             da.pvt[(((size_t)bk * G + hg) * nkb + kb) * dv + c] = (float)pv * (1.0f / 127.0f) * vdc;
         }
+}
+
+
+// The grouped kernels' instances: the config-5 shape's (group 4, head_dim
+// 128, 64-key blocks) and the general bounds.
+static void dec_launch_scores(dim3 g, const DecArgs &da, const DecSeqTab &t, hipStream_t st) {
+    const RefArgs &a = da.r;
+    if (a.H / a.Hk <= 4 && a.d <= 128)
+        hipLaunchKernelGGL((sage_dec_scores_g<4, 128>), g, dim3(256), 0, st, da, t);
+    else
+        hipLaunchKernelGGL((sage_dec_scores_g<DEC_GMAX, REF_MAXD>), g, dim3(256), 0, st, da, t);
+}
+
+static void dec_launch_pv(dim3 g, const DecArgs &da, const DecSeqTab &t, hipStream_t st) {
+    const RefArgs &a = da.r;
+    if (a.H / a.Hk <= 4 && a.block <= 64)
+        hipLaunchKernelGGL((sage_dec_pv_g<4, 64>), g, dim3(256), 0, st, da, t);
+    else
+        hipLaunchKernelGGL((sage_dec_pv_g<DEC_GMAX, DEC_KMAX>), g, dim3(256), 0, st, da, t);
 }
 
 struct DecPlan {
@@ -1722,14 +1747,14 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
         QBK_HIP(hipGetLastError());
     }
     if (grouped) {
-        hipLaunchKernelGGL(sage_dec_scores_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da, kNoSeqs);
+        dec_launch_scores(dim3(nkb, (unsigned)a.Hk), da, kNoSeqs, st);
         QBK_HIP(hipGetLastError());
         if (a.nkb > DEC_PMAX) {
             da.mprev = (float *)(w + P.o_mprev);
             hipLaunchKernelGGL(sage_dec_runmax, dim3(H), dim3(256), 0, st, da, kNoSeqs);
             QBK_HIP(hipGetLastError());
         }
-        hipLaunchKernelGGL(sage_dec_pv_g, dim3(nkb, (unsigned)a.Hk), dim3(256), 0, st, da, kNoSeqs);
+        dec_launch_pv(dim3(nkb, (unsigned)a.Hk), da, kNoSeqs, st);
         QBK_HIP(hipGetLastError());
         hipLaunchKernelGGL(sage_dec_combine, dim3(H), dim3(256), 0, st, da, kNoSeqs);
         QBK_HIP(hipGetLastError());
@@ -1805,14 +1830,14 @@ int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride
     hipLaunchKernelGGL(sage_dec_prep, dim3((unsigned)mx, Hk * ns, DPREP_KS + DPREP_VS + 1), dim3(256), g.lds, st, a,
                        g, da.qsw, da.qdl, t);
     QBK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(sage_dec_scores_g, dim3((unsigned)mkb, Hk, ns), dim3(256), 0, st, da, t);
+    dec_launch_scores(dim3((unsigned)mkb, Hk, ns), da, t, st);
     QBK_HIP(hipGetLastError());
     if (mkb > DEC_PMAX) {
         da.mprev = (float *)((char *)state + P.o_mprev);
         hipLaunchKernelGGL(sage_dec_runmax, dim3(H, ns), dim3(256), 0, st, da, t);
         QBK_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(sage_dec_pv_g, dim3((unsigned)mkb, Hk, ns), dim3(256), 0, st, da, t);
+    dec_launch_pv(dim3((unsigned)mkb, Hk, ns), da, t, st);
     QBK_HIP(hipGetLastError());
     hipLaunchKernelGGL(sage_dec_combine, dim3(H, ns), dim3(256), 0, st, da, t);
     QBK_HIP(hipGetLastError());
