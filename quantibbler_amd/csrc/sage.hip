@@ -728,36 +728,42 @@ __device__ __forceinline__ float dec_wg_max(float v, float *red) {
 }
 
 // Pre-pass of a decode step, for blocks that fit in LDS: the (key block, kv
-// head) work of sage_ref_prep (the same f32 operations) spread over
-// DPREP_KS workgroups for K -- each forms the block's channel means (the
-// first writes them) and then the deltas and codes of its share of the
-// tokens -- and DPREP_VS for V, each a share of the channels.  Each
-// workgroup issues all of its loads at once (up to DPREP_U 16-byte loads a
-// thread), so a step's pre-pass costs about one trip to memory and a short
-// serial tail instead of one workgroup's whole sequence.
+// head) work of sage_ref_prep (the same f32 operations) spread over ks
+// workgroups for K -- each forms the block's channel means (the first
+// writes them) and then the deltas and codes of its share of the tokens --
+// and vs for V, each a share of the channels (DPREP_KS and DPREP_VS for one
+// sequence; one each when many sequences' (kv head, block) pairs fill the
+// chip already).  Each workgroup issues all of its loads at once (up to
+// DPREP_U 16-byte loads a thread), so a step's pre-pass costs about one trip
+// to memory and a short serial tail instead of one workgroup's whole
+// sequence.
 #define DPREP_KS 4
 #define DPREP_VS 4
 #define DPREP_U 16
 #define DPREP_LDS 61440
 
 struct DPrepGeom {
+    uint32_t ks, vs;                // workgroups per (kv head, block) for K / V
     uint32_t kq, kstep, vq, vstep;  // 16-byte columns and rows per pass of a K / V load
     size_t lds;
     bool ok;
 };
 
-static DPrepGeom dprep_geom(const RefArgs &a, const void *k, const void *v) {
+static DPrepGeom dprep_geom(const RefArgs &a, const void *k, const void *v, uint32_t ks = DPREP_KS,
+                            uint32_t vs = DPREP_VS) {
     DPrepGeom g{};
+    g.ks = ks;
+    g.vs = vs;
     const size_t kj = a.block < a.S ? a.block : a.S;
     if (a.d % 4 || a.dv % 4 || ((uintptr_t)k & 15) || ((uintptr_t)v & 15)) return g;
     g.kq = (uint32_t)(a.d / 4);
     g.kstep = 256 / g.kq;
-    g.vq = (uint32_t)div_ceil(a.dv / 4, DPREP_VS);
+    g.vq = (uint32_t)div_ceil(a.dv / 4, vs);
     g.vstep = 256 / g.vq;
     const size_t kjp = 4 * div_ceil(kj, 4);  // V is staged channel-major with rows of kjp tokens
     g.lds = 4 * (kj * a.d > 4 * (size_t)g.vq * kjp ? kj * a.d : 4 * (size_t)g.vq * kjp);
     g.ok = g.kstep > 0 && g.vstep > 0 && kj <= (size_t)DPREP_U * g.kstep && kj <= (size_t)DPREP_U * g.vstep &&
-           g.lds <= DPREP_LDS && div_ceil(kj, DPREP_KS) <= 256;
+           g.lds <= DPREP_LDS && div_ceil(kj, ks) <= 256;
     return g;
 }
 
@@ -797,7 +803,7 @@ __device__ void dec_query_codes(const RefArgs &a, uint32_t bk, uint32_t *qsw, fl
     }
 }
 
-// grid (max(nkb - kb0, 1), Hk, DPREP_KS + DPREP_VS + 1): the last slice
+// grid (max(nkb - kb0, 1), Hk, ks + vs + 1): the last slice
 // forms the query's codes (once per kv head, when qsw is given).  Batched
 // (t.n > 0): y runs over (sequence, kv head), x over the largest count of
 // blocks to quantise.
@@ -815,7 +821,7 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
         qsw = dec_shift(qsw, sq * t.st_stride);
         qdl = dec_shift(qdl, sq * t.st_stride);
     }
-    if (z == DPREP_KS + DPREP_VS) {
+    if (z == g.ks + g.vs) {
         if (blockIdx.x == 0 && qsw) dec_query_codes(a, bky, qsw, qdl);
         return;
     }
@@ -825,7 +831,7 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
     const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
     const uint32_t d = (uint32_t)a.d, d4 = d / 4;
     f32x4_t r[DPREP_U];
-    if (z < DPREP_KS) {
+    if (z < g.ks) {
         const float *K = a.k + bk * a.k_head + (size_t)j0 * a.k_tok;
         const uint32_t q = tid % g.kq, r0 = tid / g.kq;
         const bool lane_ok = r0 < g.kstep;
@@ -851,7 +857,7 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
         }
         __syncthreads();
         // this workgroup's tokens
-        const uint32_t per = (kj + DPREP_KS - 1) / DPREP_KS, t0 = z * per;
+        const uint32_t per = (kj + g.ks - 1) / g.ks, t0 = z * per;
         const uint32_t t1 = t0 + per < kj ? t0 + per : kj;
         if (t0 >= t1) return;
         const uint32_t nt = t1 - t0;
@@ -921,7 +927,7 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
     } else {
         // V: channels 4 * c4_0 .. of this workgroup, all of the block's
         // tokens, staged channel-major ([cw][kjp], kjp = kj rounded up to 4)
-        const uint32_t dv4 = (uint32_t)a.dv / 4, c4_0 = (z - DPREP_KS) * g.vq;
+        const uint32_t dv4 = (uint32_t)a.dv / 4, c4_0 = (z - g.ks) * g.vq;
         if (c4_0 >= dv4) return;
         const uint32_t cq = dv4 - c4_0 < g.vq ? dv4 - c4_0 : g.vq, cw = 4 * cq;
         const uint32_t step = 256 / cq, tw = (kj + 3) / 4, kjp = 4 * tw;
@@ -1737,7 +1743,7 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     const bool grouped = g.ok && G <= DEC_GMAX && kjm <= DEC_KMAX && a.d % 16 == 0 && a.blk4 % 4 == 0;
     if (g.ok && (a.kb0 < a.nkb || grouped)) {
         const unsigned nx = (unsigned)(a.kb0 < a.nkb ? a.nkb - a.kb0 : 1);
-        hipLaunchKernelGGL(sage_dec_prep, dim3(nx, (unsigned)a.Hk, DPREP_KS + DPREP_VS + (grouped ? 1 : 0)),
+        hipLaunchKernelGGL(sage_dec_prep, dim3(nx, (unsigned)a.Hk, g.ks + g.vs + (grouped ? 1 : 0)),
                            dim3(256), g.lds, st, a, g, grouped ? da.qsw : nullptr, grouped ? da.qdl : nullptr,
                            kNoSeqs);
         QBK_HIP(hipGetLastError());
@@ -1827,7 +1833,13 @@ int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride
         mx = nkb - kb0 > mx ? nkb - kb0 : mx;
     }
     const unsigned Hk = (unsigned)a.Hk, H = (unsigned)a.H, ns = (unsigned)n;
-    hipLaunchKernelGGL(sage_dec_prep, dim3((unsigned)mx, Hk * ns, DPREP_KS + DPREP_VS + 1), dim3(256), g.lds, st, a,
+    // one workgroup each for K and V per (sequence, kv head, block) once the
+    // pairs alone fill the chip (the split only shortens one sequence's step)
+    if (Hk * ns >= 64) {
+        const DPrepGeom g1 = dprep_geom(a, k, v, 1, 1);
+        if (g1.ok) g = g1;
+    }
+    hipLaunchKernelGGL(sage_dec_prep, dim3((unsigned)mx, Hk * ns, g.ks + g.vs + 1), dim3(256), g.lds, st, a,
                        g, da.qsw, da.qdl, t);
     QBK_HIP(hipGetLastError());
     dec_launch_scores(dim3((unsigned)mkb, Hk, ns), da, t, st);

@@ -287,3 +287,59 @@ def test_block_decode_fused_operands_bit_identical(ctx, orc, d, ffn):
         bat.decode_batch_dev(hb, [pos], ws, wn, st)
         torch.cuda.synchronize()
         assert torch.equal(ha, hb), (pos, float((ha - hb).abs().max()))
+
+
+def test_block_batched_decode_many_sequences(ctx, orc):
+    """32 sequences of 2 kv heads (64 (sequence, kv head) pairs: the
+    attention pre-pass then runs one workgroup for K and one for V per pair
+    and key block instead of splitting each four ways), prefilled to lengths
+    across key-block boundaries, two batched steps: every row against the
+    oracle's block arithmetic on that sequence's own cache."""
+    from quantibbler_amd import DecoderBlock, FactorLayer
+
+    d, H, Hk, hd, ffn, cap, blk = 256, 4, 2, 128, 512, 160, 64
+    theta, eps = 500000.0, 1e-5
+    ns = 32
+    say(f"block batched decode, {ns} sequences")
+    rng = np.random.default_rng(4242)
+    lens = rng.integers(1, 140, ns).tolist()
+    lens[:4] = [1, 63, 64, 128]
+    shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
+              (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    bfv = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a.astype(np.float32)))
+    norms = {"input": bfv(1.0 + 0.1 * rng.standard_normal(d)), "post_attention": bfv(1.0 + 0.1 * rng.standard_normal(d)),
+             "q_norm": bfv(1.0 + 0.2 * rng.standard_normal(hd)), "k_norm": bfv(1.0 + 0.2 * rng.standard_normal(hd))}
+    block = DecoderBlock(ctx, devs, norms["input"], norms["post_attention"], H, Hk, hd, theta, eps, cap, blk,
+                         norms["q_norm"], norms["k_norm"], n_seqs=ns)
+    st = torch.cuda.current_stream()
+    kcs = [np.zeros((cap, Hk * hd), np.float32) for _ in range(ns)]
+    vcs = [np.zeros((cap, Hk * hd), np.float32) for _ in range(ns)]
+    for s, n in enumerate(lens):
+        h = rng.standard_normal((n, d)).astype(np.float32)
+        hdv = torch.from_numpy(h).cuda()
+        wn = block.prefill_workspace_size(n)
+        ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+        block.prefill_seq_dev(s, hdv, n, ws, wn, st)
+        torch.cuda.synchronize()
+        orc.block_prefill(layers, norms, h, kcs[s], vcs[s], H, Hk, hd, theta, eps)
+    pos = list(lens)
+    wn = block.decode_batch_workspace_size(ns)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    for step in range(2):
+        x = rng.standard_normal((ns, d)).astype(np.float32)
+        xd = torch.from_numpy(x).cuda()
+        block.decode_batch_dev(xd, pos, ws, wn, st)
+        torch.cuda.synchronize()
+        got = xd.cpu().numpy()
+        worst = (1.0, 0.0)
+        for s in range(ns):
+            want = orc.block_step(layers, norms, x[s], pos[s], kcs[s], vcs[s], H, Hk, hd, theta, eps, "bf16",
+                                  "sage", blk)
+            cos, rel = metrics(got[s], want)
+            worst = (min(worst[0], cos), max(worst[1], rel))
+            assert cos >= COS_MIN and rel <= REL_MAX, (step, s, pos[s], cos, rel)
+        say(f"step {step}: worst cos {worst[0]:.7f} rel {worst[1]:.2e}")
+        pos = [p + 1 for p in pos]
