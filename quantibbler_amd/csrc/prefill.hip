@@ -479,6 +479,7 @@ __global__ void __launch_bounds__(256) g32_reduce_y_kernel(const float *__restri
 // workgroup.
 typedef G32Shape<4, 2, 2> G32Big;
 typedef G32Shape<2, 2, 1> G32Small;
+typedef G32Shape<2, 1, 1> G32Tiny;  // 128 x 32 tiles (2 waves): batches of up to 32 tokens
 
 static bool g32_big(size_t M_p, size_t N, int num_cus) {
     return div_ceil(N, G32Big::BN) * div_ceil(M_p, G32Big::BM) >= (size_t)num_cus;
@@ -552,6 +553,8 @@ template <int STAGE, int XM>
 static void g32_launch_any(const G32Args &a, size_t M_p, int split, bool big, hipStream_t s) {
     if (big)
         g32_launch<STAGE, XM, G32Big, 4, 2, 2>(a, M_p, split, s);
+    else if (a.N <= (size_t)G32Tiny::BN)
+        g32_launch<STAGE, XM, G32Tiny, 2, 1, 1>(a, M_p, split, s);
     else
         g32_launch<STAGE, XM, G32Small, 2, 2, 1>(a, M_p, split, s);
 }
