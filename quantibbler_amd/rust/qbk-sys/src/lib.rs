@@ -40,6 +40,14 @@ pub struct QbkFactor {
 pub struct QbkHead {
     _p: [u8; 0],
 }
+#[repr(C)]
+pub struct QbkFactorSet {
+    _p: [u8; 0],
+}
+#[repr(C)]
+pub struct QbkBlock {
+    _p: [u8; 0],
+}
 
 /// gpu_attention.rs:402-411 AttentionShape, field for field.
 #[repr(C)]
@@ -92,6 +100,95 @@ extern "C" {
     pub fn qbk_head_destroy(head: *mut QbkHead);
     pub fn qbk_head_logits(ctx: *mut QbkCtx, head: *const QbkHead, hidden: *const f32, hidden_len: usize,
                            logits: *mut f32, logits_len: usize) -> c_int;
+}
+
+// The device-pointer faces (`_dev`: device buffers in and out, work queued
+// on the caller's HIP stream, no copies), layer sets, the decoder block, the
+// trunk pieces and the remaining host helpers -- the rest of include/qbk.h.
+extern "C" {
+    pub fn qbk_dtype_from_name(name: *const c_char, dtype_out: *mut c_int) -> c_int;
+    pub fn qbk_validate_packed(packed_len: usize, n_rows: usize, n_bits: usize, n_words: *mut usize) -> c_int;
+    pub fn qbk_sign_estimate(x: *const f64, n: usize, out: *mut i8);
+    pub fn qbk_packed_matvec_dev(ctx: *mut QbkCtx, dtype: c_int, packed: *const u8, n_rows: usize, n_bits: usize,
+                                 vec: *const c_void, out: *mut c_void, stream: *mut c_void) -> c_int;
+    pub fn qbk_packed_matmul_dev(ctx: *mut QbkCtx, dtype: c_int, packed: *const u8, n_rows: usize, n_bits: usize,
+                                 mat: *const c_void, k_cols: usize, n_cols: usize, out: *mut c_void,
+                                 stream: *mut c_void) -> c_int;
+    pub fn qbk_factor_from_rows(ctx: *mut QbkCtx, dout: usize, din: usize, r: usize, ub_rows: *const u8,
+                                vb_t_rows: *const u8, s1: *const f32, s2: *const f32, bias: *const f32,
+                                out: *mut *mut QbkFactor) -> c_int;
+    pub fn qbk_factor_linear_noalloc_dev(ctx: *mut QbkCtx, layer: *const QbkFactor, x: *const u16, batch: usize,
+                                         y: *mut c_void, y_dtype: c_int, stream: *mut c_void) -> c_int;
+    pub fn qbk_factor_set_create(ctx: *mut QbkCtx, layers: *const *const QbkFactor, n_layers: usize,
+                                 out: *mut *mut QbkFactorSet) -> c_int;
+    pub fn qbk_factor_set_destroy(set: *mut QbkFactorSet);
+    pub fn qbk_factor_set_workspace_size(set: *const QbkFactorSet) -> usize;
+    pub fn qbk_factor_set_decode_dev(ctx: *mut QbkCtx, set: *const QbkFactorSet, x: *const u16, y: *mut u16,
+                                     workspace: *mut c_void, workspace_size: usize, stream: *mut c_void) -> c_int;
+    pub fn qbk_factor_set_stage_dev(ctx: *mut QbkCtx, set: *const QbkFactorSet, stage: c_int, x: *const u16,
+                                    y: *mut u16, workspace: *mut c_void, workspace_size: usize,
+                                    stream: *mut c_void) -> c_int;
+    pub fn qbk_factor_set_workspace_size_batch(set: *const QbkFactorSet, n: usize) -> usize;
+    pub fn qbk_factor_set_decode_batch_dev(ctx: *mut QbkCtx, set: *const QbkFactorSet, n: usize, x: *const u16,
+                                           y: *mut u16, workspace: *mut c_void, workspace_size: usize,
+                                           stream: *mut c_void) -> c_int;
+    pub fn qbk_block_create(ctx: *mut QbkCtx, layers: *const *const QbkFactor, input_norm: *const f32,
+                            input_norm_len: usize, post_norm: *const f32, post_norm_len: usize, q_norm: *const f32,
+                            k_norm: *const f32, qk_norm_len: usize, n_heads: usize, n_kv_heads: usize,
+                            head_dim: usize, rope_theta: f64, rms_norm_eps: f64, capacity: usize, block_size: usize,
+                            out: *mut *mut QbkBlock) -> c_int;
+    pub fn qbk_block_destroy(block: *mut QbkBlock);
+    pub fn qbk_block_decode_dev(ctx: *mut QbkCtx, block: *mut QbkBlock, h: *mut f32, pos: usize,
+                                stream: *mut c_void) -> c_int;
+    pub fn qbk_block_reset(block: *mut QbkBlock) -> c_int;
+    pub fn qbk_block_prefill_workspace_size(block: *const QbkBlock, n_tokens: usize) -> usize;
+    pub fn qbk_block_prefill_dev(ctx: *mut QbkCtx, block: *mut QbkBlock, h: *mut f32, n_tokens: usize,
+                                 workspace: *mut c_void, workspace_size: usize, stream: *mut c_void) -> c_int;
+    pub fn qbk_block_cache(block: *const QbkBlock, k_cache: *mut *mut f32, v_cache: *mut *mut f32) -> c_int;
+    pub fn qbk_block_create_seqs(ctx: *mut QbkCtx, layers: *const *const QbkFactor, input_norm: *const f32,
+                                 input_norm_len: usize, post_norm: *const f32, post_norm_len: usize,
+                                 q_norm: *const f32, k_norm: *const f32, qk_norm_len: usize, n_heads: usize,
+                                 n_kv_heads: usize, head_dim: usize, rope_theta: f64, rms_norm_eps: f64,
+                                 capacity: usize, block_size: usize, n_seqs: usize, out: *mut *mut QbkBlock) -> c_int;
+    pub fn qbk_block_prefill_seq_dev(ctx: *mut QbkCtx, block: *mut QbkBlock, seq: usize, h: *mut f32, n_tokens: usize,
+                                     workspace: *mut c_void, workspace_size: usize, stream: *mut c_void) -> c_int;
+    pub fn qbk_block_decode_batch_workspace_size(block: *const QbkBlock, n: usize) -> usize;
+    pub fn qbk_block_decode_batch_dev(ctx: *mut QbkCtx, block: *mut QbkBlock, h: *mut f32, pos: *const usize,
+                                      n: usize, workspace: *mut c_void, workspace_size: usize,
+                                      stream: *mut c_void) -> c_int;
+    pub fn qbk_embed(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32, n: usize,
+                     out: *mut f32, stream: *mut c_void) -> c_int;
+    pub fn qbk_embed_dev(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32,
+                         n: usize, out: *mut f32, stream: *mut c_void) -> c_int;
+    pub fn qbk_rms_norm_dev(ctx: *mut QbkCtx, x: *const f32, rows: usize, d: usize, w: *const f32, eps: f64,
+                            out: *mut f32, stream: *mut c_void) -> c_int;
+    pub fn qbk_argmax_dev(ctx: *mut QbkCtx, logits: *const f32, rows: usize, vocab: usize, out: *mut i32,
+                          stream: *mut c_void) -> c_int;
+    pub fn qbk_attention_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const f32, k: *const f32,
+                             v: *const f32, causal: c_int, out: *mut f32, stream: *mut c_void) -> c_int;
+    pub fn qbk_attention_sage_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const f32, k: *const f32,
+                                  v: *const f32, causal: c_int, block_size: usize, out: *mut f32,
+                                  stream: *mut c_void) -> c_int;
+    pub fn qbk_sage_decode_workspace_size(shape: *const AttentionShape, block_size: usize) -> usize;
+    pub fn qbk_attention_sage_decode_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const f32, k: *const f32,
+                                         v: *const f32, block_size: usize, out: *mut f32, workspace: *mut c_void,
+                                         workspace_size: usize, stream: *mut c_void) -> c_int;
+    pub fn qbk_attention_sage_decode_step_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const f32,
+                                              k: *const f32, v: *const f32, block_size: usize, out: *mut f32,
+                                              state: *mut c_void, state_size: usize, capacity: usize,
+                                              cached_tokens: usize, stream: *mut c_void) -> c_int;
+    pub fn qbk_sage_blk_workspace_size(shape: *const AttentionShape) -> usize;
+    pub fn qbk_attention_sage_blk_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const u16, k: *const u16,
+                                      v: *const u16, causal: c_int, out: *mut u16, workspace: *mut c_void,
+                                      workspace_size: usize, stream: *mut c_void) -> c_int;
+    pub fn qbk_sage_blk_quantize_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const u16, k: *const u16,
+                                     v: *const u16, qhat: *mut i8, qscale: *mut f32, khat: *mut i8, kscale: *mut f32,
+                                     kmean: *mut f32, vh: *mut u16, stream: *mut c_void) -> c_int;
+    pub fn qbk_head_create_dev(ctx: *mut QbkCtx, head: *const f32, vocab: usize, d_model: usize,
+                               out: *mut *mut QbkHead) -> c_int;
+    pub fn qbk_head_info(head: *const QbkHead, vocab: *mut usize, d_model: *mut usize, bf16: *mut c_int) -> c_int;
+    pub fn qbk_head_logits_dev(ctx: *mut QbkCtx, head: *const QbkHead, hidden: *const f32, batch: usize,
+                               logits: *mut f32, stream: *mut c_void) -> c_int;
 }
 
 /// core.rs:31 KernelError: the reference's message text.

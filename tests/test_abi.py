@@ -190,18 +190,30 @@ def test_init_fails_closed_without_device(lib):
         GpuContext(0)
 
 
+def header_arities():
+    """Each function include/qbk.h declares and its parameter count."""
+    text = open(os.path.join(ROOT, "include", "qbk.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for name, args in re.findall(r"\b(qbk_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        args = args.strip()
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
 def test_rust_binding_declares_only_exported_symbols(lib):
     """quantibbler_amd/rust/qbk-sys declares the C ABI for the reference's
-    Rust side (no cargo here to build it): every function it binds is
-    declared in include/qbk.h and exported by libqbk.so, and its struct
-    mirror of AttentionShape has the header's field order."""
+    Rust side (no cargo here to build it): it binds every function
+    include/qbk.h declares, each with the header's parameter count, all
+    exported by libqbk.so, and its struct mirror of AttentionShape has the
+    header's field order."""
     src = open(os.path.join(ROOT, "quantibbler_amd", "rust", "qbk-sys", "src", "lib.rs")).read()
-    bound = set(re.findall(r"pub fn (qbk_[a-z0-9_]+)\(", src))
-    assert len(bound) >= 20
-    declared = set(declared_symbols())
-    for n in sorted(bound):
-        assert n in declared, f"{n} is not declared in include/qbk.h"
+    bound = dict(re.findall(r"pub fn (qbk_[a-z0-9_]+)\(([^)]*)\)", src))
+    declared = header_arities()
+    assert set(bound) == set(declared), sorted(set(bound) ^ set(declared))
+    for n, args in sorted(bound.items()):
         assert hasattr(lib, n), f"{n} is not exported"
+        assert (args.count(":") if args.strip() else 0) == declared[n], f"{n}: parameter count differs from qbk.h"
     fields = re.search(r"pub struct AttentionShape \{(.*?)\}", src, re.S).group(1)
     assert re.findall(r"pub (\w+): usize", fields) == ["batch", "n_heads", "n_kv_heads", "seq_q", "seq_kv",
                                                        "head_dim", "val_dim"]

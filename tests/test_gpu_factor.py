@@ -70,10 +70,20 @@ SHAPES = [(256, 512, 128), (300, 200, 37), (1024, 4096, 1102), (4096, 4096, 1024
 
 
 @pytest.mark.parametrize("dout,din,r", SHAPES)
-@pytest.mark.parametrize("batch", [1, 2, 8, 9, 16, 33, 128])
+@pytest.mark.parametrize("batch", [1, 2, 8, 9, 16, 32, 33, 128])
 def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
     if dout * r > 2_000_000 and batch not in (1, 8, 16, 128):
         pytest.skip("covered by the smaller shapes")
+    integer_exact_case(ctx, orc, dout, din, r, batch)
+
+
+def test_integer_exact_config2_batch512(ctx, orc):
+    """Config 2's shape at B = 512 (the K-split stage 1 on 128 x 64 tiles, stage
+    2 on its own 256 tiles)."""
+    integer_exact_case(ctx, orc, 4096, 4096, 1024, 512)
+
+
+def integer_exact_case(ctx, orc, dout, din, r, batch):
     say("factor integer-exact", dout, din, r, "batch", batch)
     rng = np.random.default_rng(dout + din + r + batch)
     L = make_layer(orc, rng, dout, din, r, integer=True)
