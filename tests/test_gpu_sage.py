@@ -74,6 +74,7 @@ def padded_decode_call(ctx, qh, kc, vc, block):
     (2, 1, 32, 48, 150, 100), (8, 8, 128, 128, 333, 64), (4, 2, 64, 64, 90, 256),
     (2, 1, 6, 10, 45, 16),   # channels not a multiple of 4: the general pre-pass
     (32, 2, 128, 128, 129, 64),   # 16 heads a kv head
+    (8, 2, 128, 128, 75, 16), (4, 1, 32, 32, 70, 64),   # four heads a kv head: short blocks, short heads
     # more than 512 blocks: the running max scanned first (per-head kernels;
     # two scan passes past 2048 blocks; grouped kernels)
     (2, 1, 16, 16, 1100, 2), (2, 1, 16, 16, 4200, 2), (4, 2, 64, 64, 8400, 16),
