@@ -539,6 +539,11 @@ static BlkbPlan blkb_plan(const qbk_block *B, size_t n) {
             const size_t w = blkp_proj_ws(B->lay[i], n);
             g = w > g ? w : g;
         }
+        for (const qbk_factor_set *S : {B->qkv, B->gu})
+            if (q4_set_gemm_fits(S, n)) {
+                const size_t w = q4_set_gemm_workspace(S, n);
+                g = w > g ? w : g;
+            }
     }
     p.o_gemm = take(g);
     p.bytes = off;
@@ -875,6 +880,9 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
     QBK_HIP(hipGetLastError());
     if (P.sets) {
         if ((rc = q4_set_run_batch(B->qkv, n, x, false, q, false, ws, s))) return rc;
+    } else if (q4_set_gemm_fits(B->qkv, n)) {
+        // q, k, v as one set on the GEMM (y [layer][n][dout]: q, then k, v)
+        if ((rc = q4_set_gemm_run(B->qkv, n, x, false, q, false, ws, s))) return rc;
     } else if ((rc = blkp_proj(B->lay[0], n, x, false, q, ws, s)) ||
                (rc = blkp_proj(B->lay[1], n, x, false, k, ws, s)) ||
                (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s))) {
@@ -914,6 +922,8 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
     QBK_HIP(hipGetLastError());
     if (P.sets) {
         if ((rc = q4_set_run_batch(B->gu, n, x, false, g, false, ws, s))) return rc;
+    } else if (q4_set_gemm_fits(B->gu, n)) {
+        if ((rc = q4_set_gemm_run(B->gu, n, x, false, g, false, ws, s))) return rc;
     } else if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) ||
                (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s))) {
         return rc;

@@ -780,6 +780,7 @@ struct qbk_factor_set {
     Q4Layer *tab;          // device: [0, n) stage 1, [n, 2n) stage 2; then the
     uint32_t *wg1, *wg2;   // per-workgroup layer tables (same allocation)
     float *s2cat;          // device: the layers' s2 concatenated (every din % 128 == 0), else null
+    G32SetLayer *g32tab;   // device: the set on the prefill GEMM, [n] stage 1 then [n] stage 2
     Q4Geom geom;           // batch 1
     std::vector<const qbk_factor *> layers;
 };
@@ -797,6 +798,17 @@ int q4_set_run(const qbk_factor_set *S, const void *x, bool xf32, void *y, bool 
 }
 
 size_t q4_set_workspace(const qbk_factor_set *S) { return S->geom.bytes; }
+
+bool q4_set_gemm_fits(const qbk_factor_set *S, size_t N) { return g32_set_fits(S->layers.data(), S->n, N); }
+
+size_t q4_set_gemm_workspace(const qbk_factor_set *S, size_t N) {
+    return g32_set_workspace(S->layers.data(), S->n, N);
+}
+
+int q4_set_gemm_run(const qbk_factor_set *S, size_t N, const void *x, bool xf32, void *y, bool ybf16, void *ws,
+                    hipStream_t s) {
+    return g32_set_run(S->layers.data(), S->n, S->g32tab, S->g32tab + S->n, N, x, xf32, y, ybf16, ws, s);
+}
 
 bool q4_set_flat_operand(const qbk_factor_set *S, void *ws, uint8_t **op, uint8_t **sc, const float **s2cat) {
     if (!S->s2cat || !S->geom.din_mult128) return false;
@@ -893,9 +905,19 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
         for (size_t i = 0, o = 0; e1 == hipSuccess && i < n; o += layers[i]->din, i++)
             e1 = hipMemcpy(S->s2cat + o, layers[i]->s2, layers[i]->din * sizeof(float), hipMemcpyDeviceToDevice);
     }
+    S->g32tab = nullptr;
+    if (e1 == hipSuccess) {
+        std::vector<G32SetLayer> gt(2 * n);
+        g32_set_tables(layers, n, gt.data(), gt.data() + n);
+        e1 = hipMalloc((void **)&S->g32tab, gt.size() * sizeof(G32SetLayer));
+        if (e1 != hipSuccess) S->g32tab = nullptr;
+        if (e1 == hipSuccess)
+            e1 = hipMemcpy(S->g32tab, gt.data(), gt.size() * sizeof(G32SetLayer), hipMemcpyHostToDevice);
+    }
     if (e1 != hipSuccess) {
         (void)hipFree(S->tab);
         if (S->s2cat) (void)hipFree(S->s2cat);
+        if (S->g32tab) (void)hipFree(S->g32tab);
         delete S;
         return fail(QBK_ERR_DEVICE, fmt("hipMemcpy failed: %s", hipGetErrorString(e1)));
     }
@@ -910,6 +932,7 @@ void qbk_factor_set_destroy(qbk_factor_set *S) {
     (void)hipSetDevice(S->device);
     (void)hipFree(S->tab);
     if (S->s2cat) (void)hipFree(S->s2cat);
+    if (S->g32tab) (void)hipFree(S->g32tab);
     (void)hipSetDevice(cur);
     delete S;
 }

@@ -12,6 +12,19 @@
 
 namespace qbk {
 
+// One layer of a layer set in a prefill-GEMM launch (a device table built
+// when the set is made): the stage's signs and scales, its dims, its first
+// 128-row tile in the launch, and where its rows (stage 1: in the
+// concatenated partials / t) or its activation columns (stage 2: in t) and
+// its y block (stage 2: y0 rows of N tokens before it) sit.
+struct G32SetLayer {
+    const uint32_t *sg;
+    const float *s2, *s1, *bias;
+    size_t M_p, M_valid, K_p;
+    uint32_t tile0;
+    size_t col0, y0;
+};
+
 // One stage of one layer in a decode launch: an entry of a device-side
 // table, so that one launch covers any number of layers of any shapes.
 // Offsets count slices (128 k) and elements, so they do not depend on the
@@ -79,10 +92,28 @@ int q4_set_run_batch(const qbk_factor_set *S, size_t n, const void *x, bool xf32
 // scales go in the workspace ws (and, for a set, the layers' s2
 // concatenated).  False when some din is not a multiple of 128 (no flat
 // layout).  Then the two GEMV launches; resid (f32 y only) is added to y.
+// A set's layers on the prefill GEMM for a batch of N tokens (x
+// [N][din], the layers' shared input; y [layer][N][dout]) when
+// q4_set_gemm_fits: three launches for the set.
+bool q4_set_gemm_fits(const qbk_factor_set *S, size_t N);
+size_t q4_set_gemm_workspace(const qbk_factor_set *S, size_t N);
+int q4_set_gemm_run(const qbk_factor_set *S, size_t N, const void *x, bool xf32, void *y, bool ybf16, void *ws,
+                    hipStream_t s);
+
 bool q4_flat_operand(const qbk_factor *L, void *ws, uint8_t **op, uint8_t **sc);
 bool q4_set_flat_operand(const qbk_factor_set *S, void *ws, uint8_t **op, uint8_t **sc, const float **s2cat);
 int q4_run_staged(const qbk_factor *L, void *y, bool ybf16, const float *resid, void *ws, hipStream_t s);
 int q4_set_run_staged(const qbk_factor_set *S, void *y, bool ybf16, void *ws, hipStream_t s);
+
+// prefill.hip: a layer set on the prefill GEMM for a decode step's batch of
+// N <= 64 tokens (layers sharing x, din % 8 == 0): the per-layer device
+// tables (stage 1, stage 2), the workspace, and the three launches; y is
+// [layer][N][dout].
+void g32_set_tables(const qbk_factor *const *L, size_t n, G32SetLayer *t1, G32SetLayer *t2);
+bool g32_set_fits(const qbk_factor *const *L, size_t n, size_t N);
+size_t g32_set_workspace(const qbk_factor *const *L, size_t n, size_t N);
+int g32_set_run(const qbk_factor *const *L, size_t n, const G32SetLayer *tab1, const G32SetLayer *tab2, size_t N,
+                const void *x, bool xf32, void *y, bool ybf16, void *ws, hipStream_t s);
 
 // prefill.hip: the sign layout of the prefill GEMM (rows_p a multiple of
 // 128, bits_p of 64), its workspace, and the two-stage GEMM for N tokens:

@@ -73,9 +73,15 @@ struct G32Args {
     const void *x;         // stage 1, XM 1 / 2: x [N][din] bf16 / f32, s2 [din]; din % 8 == 0
     const float *s2;
     size_t din;
-    float *part;           // [split][N][M_p] f32 (split > 1, either stage)
+    float *part;           // [split][N][ld_out] f32 (split > 1, either stage)
     size_t k_per_split;
     int split;
+    size_t ld_out, ld_act; // row strides of part / t_out and of the activation (XM 0)
+    // a layer set (null for one layer): the layers of this stage, found by
+    // row tile (128-row tiles), each at its own rows of the concatenated
+    // partials / t (stage 1) or columns of t and block of y (stage 2)
+    const G32SetLayer *set;
+    uint32_t n_set;
     // stage 1
     uint16_t *t_out;       // [N][M_p] bf16 (split == 1), zero for rows >= M_valid
     // stage 2
@@ -114,8 +120,31 @@ struct G32Shape {
 };
 
 template <int STAGE, int XM, int WM, int WN, int NT>
-__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 2))) g32_kernel(G32Args a) {
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(1, 2))) g32_kernel(G32Args a0) {
     using SH = G32Shape<WM, WN, NT>;
+    G32Args a = a0;
+    size_t by = blockIdx.y, col0 = 0;
+    if (a.set) {
+        // this workgroup's layer: the last whose first tile is at or before it
+        const __attribute__((address_space(4))) G32SetLayer *ls =
+            (const __attribute__((address_space(4))) G32SetLayer *)a.set;
+        uint32_t li = 0;
+        for (uint32_t i = 1; i < a.n_set; i++)
+            if (by >= ls[i].tile0) li = i;
+        by -= ls[li].tile0;
+        a.sg = ls[li].sg;
+        a.M_p = ls[li].M_p;
+        a.M_valid = ls[li].M_valid;
+        a.K_p = ls[li].K_p;
+        a.s2 = ls[li].s2;
+        a.s1 = ls[li].s1;
+        a.bias = ls[li].bias;
+        col0 = ls[li].col0;
+        if (STAGE == 2) {
+            a.act += col0;
+            a.y = (char *)a.y + ls[li].y0 * a.N * (a.y_bf16 ? 2 : 4);
+        }
+    }
     constexpr int BN = SH::BN, BM = SH::BM, TPB8 = SH::THREADS / 8;
     // [2 tile buffers of BN x G_PITCH bf16] during the loop; [waves][32 x
     // G_TPITCH f32] in the epilogue
@@ -124,7 +153,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = wave % WM, wc = wave / WM;  // 64-row block, 32 NT-token block
-    const size_t n0 = (size_t)blockIdx.x * BN, m0 = (size_t)blockIdx.y * BM;
+    const size_t n0 = (size_t)blockIdx.x * BN, m0 = by * BM;
     size_t kb = 0, ke = a.K_p;
     if (STAGE == 1 || a.split > 1) {
         kb = (size_t)blockIdx.z * a.k_per_split;
@@ -146,7 +175,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
     // output columns the epilogue does not store; with XM, chunks past din
     // read chunk 0 and store zeros -- so that the wait for the prefetch can
     // be a counted one at the LDS store.
-    const size_t kc = (tid & 7) * 8, ld = XM ? a.din : a.K_p;
+    const size_t kc = (tid & 7) * 8, ld = XM ? a.din : a.ld_act;
     const char *brow[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -314,8 +343,13 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
                 for (int k = 0; k < 8; k++) {
                     const int tt = 4 * k + (lane >> 4), c = lane & 15;
                     const size_t n = nb + tt;
-                    const float4 v = *(const float4 *)&T[tt * G_TPITCH + 4 * c];
-                    if (n < a.N) *(float4 *)(a.part + ((size_t)blockIdx.z * a.N + n) * a.M_p + row0 + 4 * c) = v;
+                    float4 v = *(const float4 *)&T[tt * G_TPITCH + 4 * c];
+                    const size_t rv = row0 + 4 * c;  // rows past the valid ones contribute zeros
+                    if (rv >= a.M_valid) v.x = 0.0f;
+                    if (rv + 1 >= a.M_valid) v.y = 0.0f;
+                    if (rv + 2 >= a.M_valid) v.z = 0.0f;
+                    if (rv + 3 >= a.M_valid) v.w = 0.0f;
+                    if (n < a.N) *(float4 *)(a.part + ((size_t)blockIdx.z * a.N + n) * a.ld_out + col0 + rv) = v;
                 }
             } else {
                 // bf16 rows: 8 lanes per token (8 rows each), eight tokens per store
@@ -337,7 +371,7 @@ __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_
                             if (rb + 2 * p >= a.M_valid) w[p] &= 0xffff0000u;
                             if (rb + 2 * p + 1 >= a.M_valid) w[p] &= 0x0000ffffu;
                         }
-                        *(uint4 *)(a.t_out + n * a.M_p + rb) = make_uint4(w[0], w[1], w[2], w[3]);
+                        *(uint4 *)(a.t_out + n * a.ld_out + col0 + rb) = make_uint4(w[0], w[1], w[2], w[3]);
                     } else {
                         float y[8];
 #pragma unroll
@@ -561,6 +595,118 @@ static void g32_launch_any(const G32Args &a, size_t M_p, int split, bool big, hi
 
 size_t g32_workspace(const qbk_factor *L, size_t N) { return g32_plan(L, N).bytes; }
 
+// ---- layer sets (a decode step's batch beyond the GEMV) -----------------
+//
+// The layers of a set share x (so din); one launch per stage covers them
+// all: stage 1's row tiles of every layer in one grid, K split as one layer
+// would be, the partials and t of the layers side by side ([.][N][sum r_p],
+// rows past a layer's r written as zeros); stage 2's row tiles of every
+// layer in one grid, each reading its own columns of t, no K split.  Three
+// launches for the set where the layers alone take three or four each.
+
+void g32_set_tables(const qbk_factor *const *L, size_t n, G32SetLayer *t1, G32SetLayer *t2) {
+    size_t tile1 = 0, tile2 = 0, rcol = 0, ycol = 0;
+    for (size_t i = 0; i < n; i++) {
+        t1[i] = G32SetLayer{L[i]->vt_g32, L[i]->s2, nullptr, nullptr, L[i]->r_p, L[i]->r, L[i]->din_p,
+                            (uint32_t)tile1, rcol, 0};
+        t2[i] = G32SetLayer{L[i]->u_g32, nullptr, L[i]->s1, L[i]->bias, L[i]->dout_p, L[i]->dout, L[i]->r_p,
+                            (uint32_t)tile2, rcol, ycol};
+        tile1 += L[i]->r_p / 128;
+        tile2 += L[i]->dout_p / 128;
+        rcol += L[i]->r_p;
+        ycol += L[i]->dout;
+    }
+}
+
+bool g32_set_fits(const qbk_factor *const *L, size_t n, size_t N) {
+    if (N == 0 || N > (size_t)G32Small::BN) return false;
+    for (size_t i = 0; i < n; i++)
+        if (L[i]->din != L[0]->din || L[i]->din % 8 != 0) return false;
+    return true;
+}
+
+struct G32SetPlan {
+    int split;
+    size_t rtot, tiles1, tiles2, o_part, o_t, bytes;
+};
+
+static G32SetPlan g32_set_plan(const qbk_factor *const *L, size_t n, size_t N) {
+    G32SetPlan p{};
+    for (size_t i = 0; i < n; i++) {
+        p.rtot += L[i]->r_p;
+        p.tiles2 += L[i]->dout_p / 128;
+    }
+    p.tiles1 = p.rtot / 128;
+    const size_t bn = N <= (size_t)G32Tiny::BN ? G32Tiny::BN : G32Small::BN;
+    const size_t tiles = div_ceil(N, bn) * p.tiles1;
+    p.split = 1;
+    while (tiles * p.split < (size_t)L[0]->num_cus && p.split < 8 && L[0]->din_p / (G_BK * 2 * p.split) >= 4)
+        p.split *= 2;
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        const size_t o = off;
+        off += round_up(b ? b : 4, 256);
+        return o;
+    };
+    p.o_part = take(p.split > 1 ? (size_t)p.split * N * p.rtot * 4 : 0);
+    p.o_t = take(N * p.rtot * 2);
+    p.bytes = off;
+    return p;
+}
+
+size_t g32_set_workspace(const qbk_factor *const *L, size_t n, size_t N) { return g32_set_plan(L, n, N).bytes; }
+
+int g32_set_run(const qbk_factor *const *L, size_t n, const G32SetLayer *tab1, const G32SetLayer *tab2, size_t N,
+                const void *x, bool xf32, void *y, bool ybf16, void *ws, hipStream_t s) {
+    const G32SetPlan p = g32_set_plan(L, n, N);
+    char *w = (char *)ws;
+    float *part = (float *)(w + p.o_part);
+    uint16_t *t = (uint16_t *)(w + p.o_t);
+    G32Args a{};
+    a.K_p = L[0]->din_p;
+    a.N = N;
+    a.x = x;
+    a.din = L[0]->din;
+    a.split = p.split;
+    a.part = part;
+    a.t_out = t;
+    a.k_per_split = round_up(div_ceil(L[0]->din_p, p.split), G_BK);
+    a.ld_out = p.rtot;
+    a.ld_act = L[0]->din_p;
+    a.set = tab1;
+    a.n_set = (uint32_t)n;
+    a.sign_mask = 0x80008000u;
+    a.one_pair = 0x3F803F80u;
+    if (xf32)
+        g32_launch_any<1, 2>(a, p.tiles1 * 128, p.split, false, s);
+    else
+        g32_launch_any<1, 1>(a, p.tiles1 * 128, p.split, false, s);
+    QBK_HIP(hipGetLastError());
+    if (p.split > 1) {
+        const size_t chunks = N * p.rtot / 8;
+        hipLaunchKernelGGL(g32_reduce_kernel, dim3((unsigned)div_ceil(chunks, 256)), dim3(256), 0, s,
+                           (const float *)part, p.split, N * p.rtot, p.rtot, p.rtot, t, chunks);
+        QBK_HIP(hipGetLastError());
+    }
+    bool vec = (uintptr_t)y % 16 == 0;
+    for (size_t i = 0; i < n; i++) vec = vec && L[i]->dout % 8 == 0;
+    G32Args b{};
+    b.N = N;
+    b.act = t;
+    b.y = y;
+    b.y_bf16 = ybf16;
+    b.vec_y = vec;
+    b.split = 1;
+    b.ld_act = p.rtot;
+    b.set = tab2;
+    b.n_set = (uint32_t)n;
+    b.sign_mask = 0x80008000u;
+    b.one_pair = 0x3F803F80u;
+    g32_launch_any<2, 0>(b, p.tiles2 * 128, 1, false, s);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
 int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
             hipStream_t s) {
     const G32Plan p = g32_plan(L, N);
@@ -609,6 +755,8 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.split = p.split;
     a.part = part;
     a.t_out = t;
+    a.ld_out = L->r_p;
+    a.ld_act = L->din_p;
     a.k_per_split = round_up(div_ceil(L->din_p, p.split), G_BK);
     a.sign_mask = 0x80008000u;
     a.one_pair = 0x3F803F80u;
@@ -642,6 +790,8 @@ int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     b.one_pair = 0x3F803F80u;
     b.split = p.split2;
     b.part = (float *)(w + p.o_part2);
+    b.ld_out = L->dout_p;
+    b.ld_act = L->r_p;
     b.k_per_split = round_up(div_ceil(L->r_p, p.split2), G_BK);
     g32_launch_any<2, 0>(b, L->dout_p, p.split2, g32_big(L->dout_p, N, L->num_cus), s);
     QBK_HIP(hipGetLastError());
