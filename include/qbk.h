@@ -188,6 +188,17 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *set, int stage,
 size_t qbk_factor_set_workspace_size_batch(const qbk_factor_set *set, size_t n);
 int qbk_factor_set_decode_batch_dev(qbk_ctx *ctx, const qbk_factor_set *set, size_t n, const uint16_t *x,
                                     uint16_t *y, void *workspace, size_t workspace_size, void *stream);
+/* A set whose layers read the same input (q/k/v, gate/up: engine/mod.rs:
+ * 901-906, :928-929) at a batch of n tokens (1 .. 64) on the prefill GEMM,
+ * one launch per stage for the whole set: x bf16 [n][din] (every layer's
+ * din equal and a multiple of 8), y bf16 [layer][n][dout_i].  Sums in MFMA
+ * order (bit-identical to the reference on integer-exact inputs, within the
+ * stage bounds otherwise); the decoder block's batched step runs its q/k/v
+ * and gate/up this way beyond batch 8.  No counterpart in the reference (it
+ * applies each layer to one token at a time). */
+size_t qbk_factor_set_shared_workspace_size(const qbk_factor_set *set, size_t n);
+int qbk_factor_set_shared_dev(qbk_ctx *ctx, const qbk_factor_set *set, size_t n, const uint16_t *x, uint16_t *y,
+                              void *workspace, size_t workspace_size, void *stream);
 
 
 /* ---- decoder block (engine/mod.rs:878-945) --------------------------------- */

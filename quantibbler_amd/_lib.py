@@ -66,6 +66,8 @@ _SIGS = {
     "qbk_factor_set_decode_dev": (_I, [_P, _P, _P, _P, _P, _Z, _P]),
     "qbk_factor_set_workspace_size_batch": (_Z, [_P, _Z]),
     "qbk_factor_set_decode_batch_dev": (_I, [_P, _P, _Z, _P, _P, _P, _Z, _P]),
+    "qbk_factor_set_shared_workspace_size": (_Z, [_P, _Z]),
+    "qbk_factor_set_shared_dev": (_I, [_P, _P, _Z, _P, _P, _P, _Z, _P]),
     "qbk_factor_set_stage_dev": (_I, [_P, _P, _I, _P, _P, _P, _Z, _P]),
     "qbk_attention": (_I, [_P, C.POINTER(AttnShape), _P, _Z, _P, _Z, _P, _Z, _I, _P]),
     "qbk_attention_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _I, _P, _P]),

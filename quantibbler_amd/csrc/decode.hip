@@ -974,6 +974,30 @@ int qbk_factor_set_decode_batch_dev(qbk_ctx *ctx, const qbk_factor_set *S, size_
     return q4_set_run_batch(S, n, x, false, y, true, workspace, (hipStream_t)stream);
 }
 
+size_t qbk_factor_set_shared_workspace_size(const qbk_factor_set *S, size_t n) {
+    if (!S || !q4_set_gemm_fits(S, n)) return 0;
+    return q4_set_gemm_workspace(S, n);
+}
+
+int qbk_factor_set_shared_dev(qbk_ctx *ctx, const qbk_factor_set *S, size_t n, const uint16_t *x, uint16_t *y,
+                              void *workspace, size_t workspace_size, void *stream) {
+    int rc;
+    if (!S) return fail(QBK_ERR_VALIDATION, "null layer set");
+    if (n == 0 || n > 64)
+        return fail(QBK_ERR_VALIDATION, fmt("shared-input set on the GEMM takes 1 to 64 tokens, got %zu", n));
+    if (!q4_set_gemm_fits(S, n))
+        return fail(QBK_ERR_VALIDATION, "shared-input set: every layer's din must be equal and a multiple of 8");
+    if (!x || !y) return fail(QBK_ERR_VALIDATION, "null buffer");
+    if ((uintptr_t)x % 16 != 0) return fail(QBK_ERR_VALIDATION, "shared-input set: x must be 16-byte aligned");
+    if ((rc = bind(ctx))) return rc;
+    if (S->device != ctx->device) return fail(QBK_ERR_VALIDATION, "layer set lives on another device");
+    const size_t need = q4_set_gemm_workspace(S, n);
+    if (!workspace || workspace_size < need)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("workspace of %zu bytes is smaller than the %zu this call needs", workspace_size, need));
+    return q4_set_gemm_run(S, n, x, false, y, true, workspace, (hipStream_t)stream);
+}
+
 int qbk_factor_set_decode_dev(qbk_ctx *ctx, const qbk_factor_set *S, const uint16_t *x, uint16_t *y,
                               void *workspace, size_t workspace_size, void *stream) {
     for (int ph = 1; ph <= Q4_PHASES; ph++) {

@@ -605,6 +605,16 @@ class FactorSet:
         check(_lib.load().qbk_factor_set_decode_batch_dev(self.ctx.handle, self._h, int(n), _ptr(x), _ptr(y),
                                                           _ptr(workspace), int(workspace_size), _stream(stream)))
 
+    def shared_workspace_size(self, n: int) -> int:
+        return int(_lib.load().qbk_factor_set_shared_workspace_size(self._h, int(n)))
+
+    def shared_dev(self, n: int, x, y, workspace, workspace_size: int, stream=None):
+        """Layers that read the same input (q/k/v, gate/up) at a batch of n
+        tokens (1 .. 64) on the prefill GEMM: x bf16 [n][din], y bf16
+        [layer][n][dout]."""
+        check(_lib.load().qbk_factor_set_shared_dev(self.ctx.handle, self._h, int(n), _ptr(x), _ptr(y),
+                                                    _ptr(workspace), int(workspace_size), _stream(stream)))
+
     def stage_dev(self, stage: int, x, y, workspace, workspace_size: int, stream=None):
         check(_lib.load().qbk_factor_set_stage_dev(self.ctx.handle, self._h, int(stage), _ptr(x),
                                                    _ptr(y), _ptr(workspace), int(workspace_size),

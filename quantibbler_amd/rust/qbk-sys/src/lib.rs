@@ -129,6 +129,10 @@ extern "C" {
                                     y: *mut u16, workspace: *mut c_void, workspace_size: usize,
                                     stream: *mut c_void) -> c_int;
     pub fn qbk_factor_set_workspace_size_batch(set: *const QbkFactorSet, n: usize) -> usize;
+    pub fn qbk_factor_set_shared_workspace_size(set: *const QbkFactorSet, n: usize) -> usize;
+    pub fn qbk_factor_set_shared_dev(ctx: *mut QbkCtx, set: *const QbkFactorSet, n: usize, x: *const u16,
+                                     y: *mut u16, workspace: *mut c_void, workspace_size: usize,
+                                     stream: *mut c_void) -> c_int;
     pub fn qbk_factor_set_decode_batch_dev(ctx: *mut QbkCtx, set: *const QbkFactorSet, n: usize, x: *const u16,
                                            y: *mut u16, workspace: *mut c_void, workspace_size: usize,
                                            stream: *mut c_void) -> c_int;

@@ -117,6 +117,47 @@ def test_config3_set_decode_batch_bit_identical(ctx, orc, cfg3_layers, n):
     S.close()
 
 
+@pytest.mark.parametrize("group,n", [("qkv", 9), ("qkv", 32), ("qkv", 64), ("gu", 32)])
+def test_config3_shared_set_gemm_bit_identical(ctx, orc, cfg3_layers, group, n):
+    """q/k/v (or gate/up) as one shared-input set on the prefill GEMM at a
+    decode batch (the decoder block's batched step beyond batch 8): one x
+    [n][4096] of integer-exact values, every row of every layer bit-identical
+    to the oracle's composite."""
+    from quantibbler_amd import FactorSet
+
+    host, dev = cfg3_layers
+    idx = [0, 1, 2] if group == "qkv" else [4, 5]
+    rng = np.random.default_rng(50 + n + len(idx))
+    S = FactorSet(ctx, [dev[i] for i in idx])
+    x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (n, 4096)).astype(np.float32))
+    xd = torch.from_numpy(x.view(np.int16)).cuda()
+    yd = torch.empty(n * sum(host[i]["dout"] for i in idx), dtype=torch.int16, device="cuda")
+    wn = S.shared_workspace_size(n)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    say(f"config-3 shared set {group} on the GEMM at batch {n}")
+    S.shared_dev(n, xd, yd, ws, wn, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    y = yd.cpu().numpy().view(np.uint16)
+    off = 0
+    for i in idx:
+        L = host[i]
+        want = orc.factor_apply_bf16_batch(L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                           L["bias"], x)
+        same(y[off:off + n * L["dout"]].reshape(n, L["dout"]), orc.f32_to_bf16_fast(want),
+             f"shared set {group} at batch {n}, layer {L['name']}")
+        off += n * L["dout"]
+    from quantibbler_amd import KernelError
+
+    with pytest.raises(KernelError, match="takes 1 to 64 tokens, got 65"):
+        S.shared_dev(65, xd, yd, ws, wn, torch.cuda.current_stream())
+    S.close()
+    mixed = FactorSet(ctx, [dev[0], dev[6]])
+    assert mixed.shared_workspace_size(n) == 0
+    with pytest.raises(KernelError, match="every layer's din must be equal"):
+        mixed.shared_dev(n, xd, yd, ws, wn, torch.cuda.current_stream())
+    mixed.close()
+
+
 def test_config3_set_decode_batch_rows_match_batch1(ctx, orc, cfg3_layers):
     """General bf16 inputs (N(0,1) rounded to bf16; these layers have s2 = 1):
     row b of a batch-32 set decode is bit-identical to the set decoding row b
