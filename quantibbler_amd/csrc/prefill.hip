@@ -535,7 +535,11 @@ static int g32_split(const qbk_factor *L, size_t N) {
     const size_t tiles = big ? div_ceil(N, G32Big::BN) * div_ceil(L->r_p, G32Big::BM)
                              : div_ceil(N, G32Small::BN) * div_ceil(L->r_p, G32Small::BM);
     int s = 1;
-    while (tiles * s < (size_t)L->num_cus && s < 8 && L->din_p / (G_BK * 2 * s) >= 4) s *= 2;
+    // up to 8 splits of at least four 64-k stages; a long K (the down
+    // projection's 224 stages) up to 16 of at least twelve
+    const size_t st = L->din_p / G_BK;
+    while (tiles * s < (size_t)L->num_cus && ((s < 8 && st / (2 * s) >= 4) || (s < 16 && st / (2 * s) >= 12)))
+        s *= 2;
     return s;
 }
 
