@@ -1483,14 +1483,24 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
     const uint32_t tw = (kj + 3) / 4, vn4 = (tw + 3) / 4;
     // first, this thread's channel's V codes and scale (256 / dv threads a
-    // channel, each for every (256 / dv)-th head of the group)
+    // channel, each for every (256 / dv)-th head of the group).  A group of
+    // four at dv 128 and blocks of at most 64 keys: the two threads of a
+    // channel take half of its code words each, for all four heads, so the
+    // codes are fetched once per workgroup (their integer sums added after).
+    const bool halves = GM == 4 && KM == 64 && G == 4 && dv == 128;
     const uint32_t hstep = 256 / dv, c = tid % dv, hs = tid / dv;
     const size_t vb = ((size_t)bk * a.pnkb + kb) * dv + c;
     const u32x4_t *vrow = (const u32x4_t *)(a.vhat + vb * a.blk4);
     u32x4_t vv[KM / 16];
+    if (halves) {
 #pragma unroll
-    for (uint32_t u = 0; u < KM / 16; u++)
-        if (u < vn4) vv[u] = vrow[u];
+        for (uint32_t u = 0; u < 2; u++)
+            if (2 * hs + u < vn4) vv[u] = vrow[2 * hs + u];
+    } else {
+#pragma unroll
+        for (uint32_t u = 0; u < KM / 16; u++)
+            if (u < vn4) vv[u] = vrow[u];
+    }
     const float vdc = a.vd[vb];
     // and the scores of this wave's first head at this lane's first key
     const float sc0 = wave < G && lane < kj ? da.sc[((size_t)bk * G + wave) * a.S + j0 + lane] : 0.0f;
@@ -1555,6 +1565,29 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
             da.besum[((size_t)bk * G + hg) * nkb + kb] = esum;
         }
     // P^.V^ per (head, channel) (:317-341)
+    if (halves) {
+        __shared__ int red[2][4][128];
+#pragma unroll
+        for (uint32_t hg = 0; hg < 4; hg++) {
+            const uint32_t *pw = (const uint32_t *)(ph + hg * KM);
+            int pv = 0;
+#pragma unroll
+            for (uint32_t u = 0; u < 2; u++)
+                if (2 * hs + u < vn4)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (4 * (2 * hs + u) + e < tw)
+                            pv = __builtin_amdgcn_sdot4((int)pw[4 * (2 * hs + u) + e], (int)vv[u][e], pv, false);
+            red[hs][hg][c] = pv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t hg = hs; hg < 4; hg += 2) {
+            const int pv = red[0][hg][c] + red[1][hg][c];
+            da.pvt[(((size_t)bk * G + hg) * nkb + kb) * dv + c] = (float)pv * (1.0f / 127.0f) * vdc;
+        }
+        return;
+    }
     if (hs < hstep)
         for (uint32_t hg = hs; hg < G; hg += hstep) {
             const uint32_t *pw = (const uint32_t *)(ph + hg * KM);
