@@ -1604,28 +1604,35 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
 
 
 // sage_dec_scores_g for groups of exactly four heads, head_dim <= 128 and
-// key blocks of at most 64: a lane per (head, key) -- 16 keys a wave, all
-// four heads -- so that a block's key codes are fetched once per workgroup
-// (the four lanes of a key read the same words) instead of once per head
-// wave; the same f32 operations in the same order (each shift summed
-// sequentially by its own lane, the scores' products as above).
+// key blocks of at most 64: two key blocks a workgroup (two waves each), a
+// lane per key for two heads of the group -- so that a block's key codes are
+// fetched once per workgroup (the two lanes of a key read the same words),
+// and a batched step's grid holds half the workgroups, each no longer; the
+// same f32 operations in the same order (each shift summed sequentially by
+// its own lane, the scores' products as above).
 __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab t) {
     if (t.n) dec_seq(da, t, blockIdx.z);
     const RefArgs &a = da.r;
-    if (blockIdx.x >= a.nkb) return;  // a batched launch covers the longest sequence's blocks
+    const uint32_t kbA = 2 * blockIdx.x;
+    if (kbA >= a.nkb) return;  // a batched launch covers the longest sequence's blocks
     __shared__ uint32_t qs[4 * 32];
-    __shared__ float qd[4], shs[4], wmax[4][4];
-    __shared__ float kms[128];
-    __shared__ __attribute__((aligned(16))) float term[4 * 128];
+    __shared__ float qd[4], shs[2][4], wmax[4][4];
+    __shared__ float kms[2][128];
+    __shared__ __attribute__((aligned(16))) float term[2][4 * 128];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kb = blockIdx.x, bk = blockIdx.y;
+    const uint32_t bk = blockIdx.y, bi = wave >> 1, kb = kbA + bi;
+    const bool bval = kb < (uint32_t)a.nkb;  // the workgroup's second block may be past the end
     const uint32_t d = (uint32_t)a.d, d4 = d / 4, n4 = d4 / 4;
-    const uint32_t j0 = kb * (uint32_t)a.block;
+    const uint32_t kbc = bval ? kb : kbA;
+    const uint32_t j0 = kbc * (uint32_t)a.block;
     const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
-    const uint32_t hg = lane >> 4, kk = 16 * wave + (lane & 15);
+    const uint32_t hp = lane >> 5, kk = 32 * (wave & 1) + (lane & 31);  // heads hp, hp + 2; key kk
     for (uint32_t i = tid; i < 4 * d4; i += 256) qs[i] = da.qsw[(size_t)bk * 4 * d4 + i];
     if (tid < 4) qd[tid] = da.qdl[bk * 4 + tid];
-    if (tid < d) kms[tid] = a.kmean[((size_t)bk * a.pnkb + kb) * d + tid];
+    if (tid < 2 * d) {
+        const uint32_t b2 = tid / d, c = tid % d, kb2 = kbA + b2 < (uint32_t)a.nkb ? kbA + b2 : kbA;
+        kms[b2][c] = a.kmean[((size_t)bk * a.pnkb + kb2) * d + c];
+    }
     const uint32_t jl = kk < kj ? kk : kj - 1;
     const u32x4_t *krow = (const u32x4_t *)(a.khat + ((size_t)bk * a.pst + j0 + jl) * d4);
     u32x4_t kv[8];
@@ -1634,16 +1641,16 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab 
         if (u < n4) kv[u] = krow[u];
     const float kdl = a.kdelta[(size_t)bk * a.pst + j0 + jl];
     __syncthreads();
-    // the shift's terms (q^_c * dq) * kmean_c, every (head, channel) at once
-    for (uint32_t i = tid; i < 4 * d; i += 256) {
-        const uint32_t h4 = i / d, c = i % d;
+    // the shift's terms (q^_c * dq) * kmean_c, every (block, head, channel)
+    for (uint32_t i = tid; i < 8 * d; i += 256) {
+        const uint32_t b2 = i / (4 * d), r = i % (4 * d), h4 = r / d, c = r % d;
         const int qc = (int)(int8_t)(qs[h4 * d4 + c / 4] >> (8 * (c % 4)));
-        term[i] = ((float)qc * qd[h4]) * kms[c];
+        term[b2][r] = ((float)qc * qd[h4]) * kms[b2][c];
     }
     __syncthreads();
-    // each head's shift: its terms summed in channel order (:253), four lanes
-    if (tid < 4) {
-        const float *tt = term + tid * d;
+    // each (block, head)'s shift: its terms summed in channel order (:253)
+    if (tid < 8) {
+        const float *tt = term[tid >> 2] + (tid & 3) * d;
         float shift = 0.0f;
 #pragma unroll 4
         for (uint32_t c = 0; c < d; c += 4) {
@@ -1653,33 +1660,37 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab 
             shift += t4[2];
             shift += t4[3];
         }
-        shs[tid] = shift;
+        shs[tid >> 2][tid & 3] = shift;
     }
     __syncthreads();
-    const uint32_t *qh = qs + hg * d4;
-    int acc = 0;
+    const bool ok = bval && kk < kj;
 #pragma unroll
-    for (uint32_t u = 0; u < 8; u++)
-        if (u < n4)
+    for (uint32_t e2 = 0; e2 < 2; e2++) {
+        const uint32_t hg = hp + 2 * e2;
+        const uint32_t *qh = qs + hg * d4;
+        int acc = 0;
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc = __builtin_amdgcn_sdot4((int)qh[4 * u + e], (int)kv[u][e], acc, false);
-    const float sv = (float)acc * qd[hg] * kdl + shs[hg];
-    const bool ok = kk < kj;
-    if (ok) da.sc[((size_t)bk * 4 + hg) * a.S + j0 + kk] = sv;
-    // the block max of each head: over the wave's 16 keys, then the waves
-    float rm = ok ? sv : MASKED;
+        for (uint32_t u = 0; u < 8; u++)
+            if (u < n4)
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        const float w = __shfl_xor(rm, o, 64);
-        rm = w > rm ? w : rm;
+                for (int e = 0; e < 4; e++)
+                    acc = __builtin_amdgcn_sdot4((int)qh[4 * u + e], (int)kv[u][e], acc, false);
+        const float sv = (float)acc * qd[hg] * kdl + shs[bi][hg];
+        if (ok) da.sc[((size_t)bk * 4 + hg) * a.S + j0 + kk] = sv;
+        // the block max of the head: over the wave's 32 keys, then its two waves
+        float rm = ok ? sv : MASKED;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) {
+            const float w = __shfl_xor(rm, o, 64);
+            rm = w > rm ? w : rm;
+        }
+        if ((lane & 31) == 0) wmax[wave][hg] = rm;
     }
-    if ((lane & 15) == 0) wmax[wave][hg] = rm;
     __syncthreads();
-    if (tid < 4) {
-        float m = wmax[0][tid];
-#pragma unroll
-        for (int w = 1; w < 4; w++) m = wmax[w][tid] > m ? wmax[w][tid] : m;
-        da.bmax[((size_t)bk * 4 + tid) * a.nkb + kb] = m;
+    if (tid < 8) {
+        const uint32_t b2 = tid >> 2, hg = tid & 3;
+        const float m0 = wmax[2 * b2][hg], m1 = wmax[2 * b2 + 1][hg];
+        if (kbA + b2 < (uint32_t)a.nkb) da.bmax[((size_t)bk * 4 + hg) * a.nkb + kbA + b2] = m1 > m0 ? m1 : m0;
     }
 }
 
@@ -1688,7 +1699,7 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab 
 static void dec_launch_scores(dim3 g, const DecArgs &da, const DecSeqTab &t, hipStream_t st) {
     const RefArgs &a = da.r;
     if (a.H / a.Hk == 4 && a.d <= 128 && a.block <= 64)
-        hipLaunchKernelGGL(sage_dec_scores_g4, g, dim3(256), 0, st, da, t);
+        hipLaunchKernelGGL(sage_dec_scores_g4, dim3((g.x + 1) / 2, g.y, g.z), dim3(256), 0, st, da, t);
     else if (a.H / a.Hk <= 4 && a.d <= 128)
         hipLaunchKernelGGL((sage_dec_scores_g<4, 128>), g, dim3(256), 0, st, da, t);
     else
