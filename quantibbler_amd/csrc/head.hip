@@ -20,11 +20,16 @@
 // so, engine/mod.rs:695-706) it is stored as bf16 -- 1.05 GB instead of 2.1
 // for 128256 x 4096 -- and widened exactly on use; otherwise as f32.
 //
-// The dot product is HBM-bound (one pass over the head per call; the
-// hidden rows ride in SGPRs through scalar loads).  A lane covers two rows
-// (bf16: one dword holds both) or one (f32), reads a dword per step, and
-// keeps two chunks of loads in flight (alternating register sets, so no
-// in-flight register is ever copied).
+// At one hidden row the dot product is HBM-bound (one pass over the head
+// per call; the row rides in SGPRs through scalar loads).  From two rows a
+// wave on, the rows' values come through LDS (head_logits_lds_kernel), and
+// beyond eight rows two or four waves share each block of head words (the
+// block fetched once from memory), so that a batch's products (two VALU ops
+// a term: the reference rounds the product and the sum separately) spread
+// over more SIMDs.  A lane covers two vocabulary rows (bf16: one dword
+// holds both) or one (f32), reads a dword per step, and keeps two chunks
+// of loads in flight (alternating register sets, so no in-flight register
+// is ever copied).
 #include <string.h>
 
 #include "qbk_internal.h"
@@ -43,6 +48,7 @@ namespace qbk {
 #define HEAD_THREADS 256
 #define HEAD_CHUNK 64   // steps per load chunk
 #define HEAD_MAXB 8     // hidden rows per launch
+#define HEAD_LDS_CH 32  // steps per load chunk of the LDS-fed kernel (16: 3-5 % slower at 8-32 rows)
 
 typedef __attribute__((address_space(1))) const uint32_t g32_t;
 typedef __attribute__((address_space(4))) const float cf32_t;
@@ -150,6 +156,131 @@ __global__ void __launch_bounds__(HEAD_THREADS) head_logits_kernel(const uint32_
     }
 }
 
+// The same logits for NB >= 2 hidden rows a wave, the rows' values read
+// from LDS instead of scalar loads: each wave stages its rows' next CH steps
+// ([step][8] floats, lane u loading step u of every row) one chunk ahead,
+// and the products run step by step, a step's row values two broadcast
+// reads (all lanes one address).  Each (row, vocabulary row) sum still runs
+// over t in order.  (With the rows in SGPRs, eight rows a wave waited on a
+// scalar memory round trip every sixteen values and ran at a third of the
+// VALU rate the products need.)
+typedef __attribute__((address_space(1))) const float gf32h_t;
+
+template <bool BF16, int NB, int CH>
+__global__ void __launch_bounds__(HEAD_THREADS) head_logits_lds_kernel(const uint32_t *w, size_t vocab_p,
+                                                                      size_t vocab, size_t d, const float *hidden,
+                                                                      float *logits, int chunks, int batch) {
+    static_assert(NB >= 2 && NB <= 8 && CH <= 64 && CH % 4 == 0, "rows and chunk");
+    __shared__ __attribute__((aligned(16))) float hs[HEAD_THREADS / 64][2][CH][8];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ci = wave % chunks;  // wave-uniform
+    const size_t wb = (size_t)blockIdx.x * (HEAD_THREADS / 64 / chunks) + wave / chunks;
+    const size_t lane = threadIdx.x & 63;
+    const size_t dq = (d + 3) / 4;
+    const uint32_t *col = w + wb * dq * 256 + lane * 4;
+    const int nb = batch - ci * NB < NB ? batch - ci * NB : NB;  // rows of this wave's chunk (>= 1)
+    hidden += (size_t)ci * NB * d;
+    logits += (size_t)ci * NB * vocab;
+    const gf32h_t *hr[NB];  // rows past nb repeat the last (not stored)
+#pragma unroll
+    for (int b = 0; b < NB; b++) hr[b] = (const gf32h_t *)hidden + (size_t)(b < nb ? b : nb - 1) * d;
+    float acc[NB][2];
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[b][0] = acc[b][1] = 0.0f;
+    float(*hw)[CH][8] = hs[wave];
+    const size_t dmain = d / (2 * CH) * (2 * CH);
+    const size_t us = lane % CH;  // the step this lane stages (lanes past CH repeat it, not stored)
+    auto hload = [&](float H[NB], size_t t0) {
+        size_t t = t0 + us;
+        t = t < d ? t : d - 1;
+#pragma unroll
+        for (int b = 0; b < NB; b++) H[b] = hr[b][t];
+    };
+    auto hstore = [&](const float H[NB], int buf) {
+        if (lane < CH) {
+            float v[8];
+#pragma unroll
+            for (int b = 0; b < 8; b++) v[b] = b < NB ? H[b] : 0.0f;
+            *(float4 *)&hw[buf][us][0] = make_float4(v[0], v[1], v[2], v[3]);
+            if (NB > 4) *(float4 *)&hw[buf][us][4] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+    // a chunk in groups of HG steps: the next group's row values are read
+    // while this group's products run (the empty asm statements, which take
+    // the sums and fence memory, keep the compiler from hoisting every read
+    // of the chunk ahead of the products, which held a register per value)
+    constexpr int HG = 4;
+    auto hread = [&](float4 R[HG][2], int buf, int u0) {
+#pragma unroll
+        for (int i = 0; i < HG; i++) {
+            R[i][0] = *(const float4 *)&hw[buf][u0 + i][0];
+            if (NB > 4) R[i][1] = *(const float4 *)&hw[buf][u0 + i][4];
+        }
+    };
+    auto chunk = [&](const uint32_t W[CH], int buf) {
+        float4 R[2][HG][2];
+        hread(R[0], buf, 0);
+#pragma unroll
+        for (int g = 0; g < CH / HG; g++) {
+            if (g + 1 < CH / HG) hread(R[(g + 1) & 1], buf, (g + 1) * HG);
+#pragma unroll
+            for (int i = 0; i < HG; i++) {
+                const int u = g * HG + i;
+                const float4 h0 = R[g & 1][i][0], h1 = R[g & 1][i][1];
+                const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+                const float w0 = BF16 ? __uint_as_float(W[u] << 16) : __uint_as_float(W[u]);
+                const float w1 = BF16 ? __uint_as_float(W[u] & 0xffff0000u) : 0.0f;
+#pragma unroll
+                for (int b = 0; b < NB; b++) {
+                    acc[b][0] = acc[b][0] + hv[b] * w0;
+                    if (BF16) acc[b][1] = acc[b][1] + hv[b] * w1;
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                __asm__ volatile("" : "+v"(acc[b][0]));
+                if (BF16) __asm__ volatile("" : "+v"(acc[b][1]));
+            }
+            __asm__ volatile("" ::: "memory");
+        }
+    };
+    uint32_t A[CH], Bw[CH];
+    float HA[NB], HB[NB];
+    if (dmain) {
+        head_load<CH>(A, col, 0, dq - 1);
+        hload(HA, 0);
+#pragma unroll 1
+        for (size_t t0 = 0; t0 < dmain; t0 += 2 * CH) {
+            head_load<CH>(Bw, col, t0 + CH, dq - 1);
+            hstore(HA, 0);
+            hload(HB, t0 + CH);
+            chunk(A, 0);
+            head_load<CH>(A, col, t0 + 2 * CH, dq - 1);
+            hstore(HB, 1);
+            hload(HA, t0 + 2 * CH);
+            chunk(Bw, 1);
+        }
+    }
+    for (size_t t = dmain; t < d; t++) {  // the last d % (2 CH) steps, in order
+        const uint32_t wv = col[(t / 4) * 256 + t % 4];
+        const float w0 = BF16 ? __uint_as_float(wv << 16) : __uint_as_float(wv);
+        const float w1 = BF16 ? __uint_as_float(wv & 0xffff0000u) : 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float hv = hr[b][t];
+            acc[b][0] = acc[b][0] + hv * w0;
+            if (BF16) acc[b][1] = acc[b][1] + hv * w1;
+        }
+    }
+    const size_t v0 = wb * head_rows_per_wave(BF16) + (BF16 ? 2 * lane : lane);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        if (b >= nb) break;
+        if (v0 < vocab) logits[(size_t)b * vocab + v0] = acc[b][0];
+        if (BF16 && v0 + 1 < vocab) logits[(size_t)b * vocab + v0 + 1] = acc[b][1];
+    }
+}
+
 // any element of src (f32, n of them) not a bf16 value -> *flag = 1
 __global__ void head_bf16_check(const float *src, size_t n, uint32_t *flag) {
     uint32_t bad = 0;
@@ -231,6 +362,9 @@ static int head_run(const qbk_head *H, const float *hidden, size_t batch, float 
     const size_t rpw = head_rows_per_wg(H->bf16);
     for (size_t b0 = 0; b0 < batch; b0 += 4 * HEAD_MAXB) {
         const size_t rows = batch - b0 < 4 * HEAD_MAXB ? batch - b0 : 4 * HEAD_MAXB;
+        // (four waves of two rows each for a batch of 8 took 452 us against
+        // 338 for one wave of eight: the waves sharing a block re-read its
+        // words from the caches, and at two rows a wave that traffic bounds)
         const int chunks = rows <= HEAD_MAXB ? 1 : rows <= 2 * HEAD_MAXB ? 2 : 4;
         const size_t nb = div_ceil(rows, (size_t)chunks);
         const dim3 g((unsigned)(H->vocab_p / (rpw / chunks)));
@@ -238,8 +372,12 @@ static int head_run(const qbk_head *H, const float *hidden, size_t batch, float 
         float *lb = logits + b0 * H->vocab;
         const uint32_t *w = (const uint32_t *)H->w;
 #define HEAD_LAUNCH(BF, NB)                                                                                   \
-    hipLaunchKernelGGL((head_logits_kernel<BF, NB>), g, dim3(HEAD_THREADS), 0, s, w, H->vocab_p, H->vocab,     \
-                       H->d_model, hb, lb, chunks, (int)rows)
+    if (NB == 1)                                                                                              \
+        hipLaunchKernelGGL((head_logits_kernel<BF, 1>), g, dim3(HEAD_THREADS), 0, s, w, H->vocab_p, H->vocab,  \
+                           H->d_model, hb, lb, chunks, (int)rows);                                            \
+    else                                                                                                      \
+        hipLaunchKernelGGL((head_logits_lds_kernel<BF, (NB > 1 ? NB : 2), HEAD_LDS_CH>), g, dim3(HEAD_THREADS), \
+                           0, s, w, H->vocab_p, H->vocab, H->d_model, hb, lb, chunks, (int)rows)
 #define HEAD_BATCH(BF)                                                                                        \
     switch (nb) {                                                                                             \
         case 1: HEAD_LAUNCH(BF, 1); break;                                                                    \
