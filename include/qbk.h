@@ -275,6 +275,27 @@ size_t qbk_block_decode_batch_workspace_size(const qbk_block *block, size_t n);
 int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *block, float *h, const size_t *pos, size_t n,
                                void *workspace, size_t workspace_size, void *stream);
 
+/* Decode steps whose positions live in device memory, so that a step
+ * captured once in a HIP graph serves every later position (the reference
+ * steps its engine from the host, engine/mod.rs:1377-1476; these take the
+ * host out of the loop).  pos: device uint32, one per sequence (n entries
+ * for the batched form), read when the step runs: the position the step
+ * writes (as qbk_block_decode_dev's pos).  The attention steps a kept state
+ * that must hold every complete key block before that position -- as after
+ * an eager step at pos - 1 -- and keeps the same arithmetic, so each step is
+ * bit-identical to the eager step at that position.  A position at or past
+ * the capacity skips the cache and attention (the step's output is then
+ * undefined).  Needs the grouped decode attention (head_dim a multiple of
+ * 16, up to 16 query heads a kv head, key blocks of up to 64 tokens; a
+ * validation error otherwise).  These steps do not update the block's host
+ * record of cached positions: qbk_block_set_positions sets it (sequence i
+ * holding pos[i] positions, its attention state stepped through them) before
+ * the next eager step. */
+int qbk_block_decode_pos_dev(qbk_ctx *ctx, qbk_block *block, float *h, const uint32_t *pos, void *stream);
+int qbk_block_decode_batch_pos_dev(qbk_ctx *ctx, qbk_block *block, float *h, const uint32_t *pos, size_t n,
+                                   void *workspace, size_t workspace_size, void *stream);
+int qbk_block_set_positions(qbk_block *block, const size_t *pos, size_t n);
+
 /* ---- trunk pieces around the blocks (engine/mod.rs:763-800, 943) ---------- */
 
 /* Engine::embed (engine/mod.rs:768-778): out[i] = table[tokens[i]], f32
@@ -295,6 +316,10 @@ int qbk_rms_norm_dev(qbk_ctx *ctx, const float *x, size_t rows, size_t d, const 
  * largest value (NaN never wins; 0 when nothing beats -inf). */
 int qbk_argmax_dev(qbk_ctx *ctx, const float *logits, size_t rows, size_t vocab, int32_t *out,
                    void *stream);
+/* pos[i] += 1 for i < n (device uint32): a greedy loop's positions after a
+ * device-position step (no reference counterpart: the reference's loop
+ * counts positions on the host). */
+int qbk_positions_advance_dev(qbk_ctx *ctx, uint32_t *pos, size_t n, void *stream);
 
 /* ---- attention (gpu_attention.rs) ----------------------------------------- */
 

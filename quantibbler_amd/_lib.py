@@ -93,6 +93,10 @@ _SIGS = {
     "qbk_block_prefill_seq_dev": (_I, [_P, _P, _Z, _P, _Z, _P, _Z, _P]),
     "qbk_block_decode_batch_workspace_size": (_Z, [_P, _Z]),
     "qbk_block_decode_batch_dev": (_I, [_P, _P, _P, _P, _Z, _P, _Z, _P]),
+    "qbk_block_decode_pos_dev": (_I, [_P, _P, _P, _P, _P]),
+    "qbk_block_decode_batch_pos_dev": (_I, [_P, _P, _P, _P, _Z, _P, _Z, _P]),
+    "qbk_block_set_positions": (_I, [_P, _P, _Z]),
+    "qbk_positions_advance_dev": (_I, [_P, _P, _Z, _P]),
     "qbk_attention_sage_decode_step_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _Z, _P, _P, _Z, _Z,
                                                 _Z, _P]),
     "qbk_head_create": (_I, [_P, _P, _Z, _Z, _Z, C.POINTER(_P)]),

@@ -107,9 +107,14 @@ __global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm(const float *a, c
 // head's values rounded to bf16, their mean square (a tree here), then
 // bf16(v * inv * w).  RoPE pairs (i, i + hd/2) (engine/mod.rs:1169-1187).
 __global__ void __launch_bounds__(64) blkd_qk_rope(const float *qkv, const float2 *rope, size_t pos,
-                                                   const float *wq, const float *wk, float eps, float *qrot,
-                                                   float *kc, float *vc, int H, int Hk, int hd) {
+                                                   const uint32_t *pos_dev, size_t cap, const float *wq,
+                                                   const float *wk, float eps, float *qrot, float *kc, float *vc,
+                                                   int H, int Hk, int hd) {
     const int head = blockIdx.x, lane = threadIdx.x, half = hd / 2;
+    if (pos_dev) {
+        pos = *(const __attribute__((address_space(4))) uint32_t *)pos_dev;
+        if (pos >= cap) return;  // past the cache: nothing is written
+    }
     const bool is_q = head < H;
     const int hh = is_q ? head : head - H;
     const float *src = is_q ? qkv + (size_t)hh * hd : qkv + (size_t)H * hd + (size_t)hh * hd;
@@ -464,10 +469,12 @@ struct BlkbPos {
 // Row t (sequence t): per-head q/k norm and RoPE at pos.p[t] as blkd_qk_rope;
 // q to qr [n][H hd], k and v to row pos.p[t] of sequence t's cache.
 __global__ void __launch_bounds__(64) blkb_qk_rope(const float *q, const float *k, const float *v, const float2 *rope,
-                                                   BlkbPos pos, const float *wq, const float *wk, float eps, float *kc,
-                                                   float *vc, size_t kvs, float *qr, int H, int Hk, int hd) {
+                                                   BlkbPos pos, const uint32_t *pos_dev, size_t cap, const float *wq,
+                                                   const float *wk, float eps, float *kc, float *vc, size_t kvs,
+                                                   float *qr, int H, int Hk, int hd) {
     const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, half = hd / 2;
-    const size_t p = pos.p[t];
+    const size_t p = pos_dev ? ((const __attribute__((address_space(4))) uint32_t *)pos_dev)[t] : pos.p[t];
+    if (p >= cap) return;  // a device position past the cache: nothing is written
     const bool is_q = head < H;
     const int hh = is_q ? head : head - H;
     const float *src = is_q ? q + ((size_t)t * H + hh) * hd : k + ((size_t)t * Hk + hh) * hd;
@@ -685,16 +692,28 @@ int qbk_block_cache(const qbk_block *B, float **k_cache, float **v_cache) {
     return QBK_OK;
 }
 
-int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void *stream) {
+}  // extern "C"
+
+// The decode of one position of sequence 0: at pos (host), or with pos_dev
+// at the position that device word holds when the step runs (the host
+// record of cached positions is then left to the caller).
+static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, const uint32_t *pos_dev,
+                            void *stream) {
     int rc;
     if (!B || !h) return fail(QBK_ERR_VALIDATION, "null argument");
-    if (pos >= B->cap)
+    if (!pos_dev && pos >= B->cap)
         return fail(QBK_ERR_VALIDATION, fmt("position %zu is past the block's cache capacity of %zu", pos, B->cap));
-    if (pos > B->filled[0])
+    if (!pos_dev && pos > B->filled[0])
         return fail(QBK_ERR_VALIDATION,
                     fmt("position %zu skips cache rows: the block holds %zu positions", pos, B->filled[0]));
     if ((rc = bind(ctx))) return rc;
     if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
+    const qbk_attn_shape one{1, B->H, B->Hk, 1, B->cap, B->hd, B->hd};
+    const size_t kvs = B->cap * B->Hk * B->hd;
+    if (pos_dev && !sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs))
+        return fail(QBK_ERR_VALIDATION, "a device-position step needs the grouped sage decode kernels "
+                                        "(head_dim a multiple of 16, groups of up to 16 heads, blocks of up to "
+                                        "64 tokens)");
     hipStream_t s = (hipStream_t)stream;
     const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk, ffn = (int)B->ffn;
     // the norms and SwiGLU write the operand of the projections they feed
@@ -714,19 +733,27 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
         QBK_HIP(hipGetLastError());
         if ((rc = q4_set_run(B->qkv, B->xcat, false, B->ycat, false, B->ws, s))) return rc;
     }
-    hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, B->w_q, B->w_k,
-                       B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
+    hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, pos_dev, B->cap, B->w_q,
+                       B->w_k, B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
     QBK_HIP(hipGetLastError());
-    const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos + 1, B->hd, B->hd};
-    const size_t cached = B->tokens[0] <= pos ? B->tokens[0] : 0;
     // the attention's combine writes the o projection's operand directly
     DecOpSink sink{B->o->s2, nullptr, nullptr};
     const bool osink = B->hd % 128 == 0 && q4_flat_operand(B->o, B->ws, &sink.op, &sink.sc);
-    if ((rc = sage_decode_step_sink(ctx, &sh, B->qrot, B->kc, B->vc, B->block, B->attn, B->state, B->state_bytes,
-                                    B->cap, cached, osink ? &sink : nullptr, stream)))
-        return rc;
-    B->tokens[0] = pos + 1;
-    B->filled[0] = pos + 1;
+    if (pos_dev) {
+        const size_t qs = B->H * B->hd;
+        if ((rc = sage_decode_batch(&one, B->qrot, qs, B->kc, B->vc, kvs, B->block, B->attn, qs, B->state,
+                                    B->state_bytes, B->cap, nullptr, nullptr, 1, s, pos_dev,
+                                    osink ? &sink : nullptr)))
+            return rc;
+    } else {
+        const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos + 1, B->hd, B->hd};
+        const size_t cached = B->tokens[0] <= pos ? B->tokens[0] : 0;
+        if ((rc = sage_decode_step_sink(ctx, &sh, B->qrot, B->kc, B->vc, B->block, B->attn, B->state,
+                                        B->state_bytes, B->cap, cached, osink ? &sink : nullptr, stream)))
+            return rc;
+        B->tokens[0] = pos + 1;
+        B->filled[0] = pos + 1;
+    }
     if ((rc = osink ? q4_run_staged(B->o, B->oout, false, nullptr, B->ws, s)
                     : q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s)))
         return rc;
@@ -755,6 +782,29 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     if ((rc = q4_run(B->down, 1, B->hid, true, B->dout, false, B->ws, s))) return rc;
     hipLaunchKernelGGL(blkd_add, dim3((d + 255) / 256), dim3(256), 0, s, B->dout, B->h1, h, d);
     QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+extern "C" {
+
+int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void *stream) {
+    return block_decode_one(ctx, B, h, pos, nullptr, stream);
+}
+
+int qbk_block_decode_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const uint32_t *pos, void *stream) {
+    if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    return block_decode_one(ctx, B, h, 0, pos, stream);
+}
+
+int qbk_block_set_positions(qbk_block *B, const size_t *pos, size_t n) {
+    if (!B || !pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (n == 0 || n > B->nseq)
+        return fail(QBK_ERR_VALIDATION, fmt("%zu sequences on a block holding %zu", n, B->nseq));
+    for (size_t i = 0; i < n; i++)
+        if (pos[i] > B->cap)
+            return fail(QBK_ERR_VALIDATION,
+                        fmt("sequence %zu: %zu positions exceed the block's cache capacity of %zu", i, pos[i], B->cap));
+    for (size_t i = 0; i < n; i++) B->tokens[i] = B->filled[i] = pos[i];
     return QBK_OK;
 }
 
@@ -846,13 +896,18 @@ size_t qbk_block_decode_batch_workspace_size(const qbk_block *B, size_t n) {
 // projections batched over the n rows (the GEMV up to batch 8, the GEMM
 // beyond), RoPE and the cache append per sequence, the sage decode
 // attention stepping every sequence's kept state.
-int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_t *pos, size_t n, void *workspace,
-                               size_t workspace_size, void *stream) {
+}  // extern "C"
+
+// With pos_dev (device, n entries) in place of pos: each sequence at the
+// position its word holds when the step runs; the host record of cached
+// positions is then left to the caller.
+static int block_decode_batch(qbk_ctx *ctx, qbk_block *B, float *h, const size_t *pos, const uint32_t *pos_dev,
+                              size_t n, void *workspace, size_t workspace_size, void *stream) {
     int rc;
-    if (!B || !h || !pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (!B || !h || (!pos && !pos_dev)) return fail(QBK_ERR_VALIDATION, "null argument");
     if (n == 0 || n > B->nseq)
         return fail(QBK_ERR_VALIDATION, fmt("batch of %zu sequences on a block holding %zu", n, B->nseq));
-    for (size_t i = 0; i < n; i++) {
+    for (size_t i = 0; !pos_dev && i < n; i++) {
         if (pos[i] >= B->cap)
             return fail(QBK_ERR_VALIDATION,
                         fmt("position %zu is past the block's cache capacity of %zu", pos[i], B->cap));
@@ -889,13 +944,17 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
         return rc;
     }
     BlkbPos bp{};
-    for (size_t i = 0; i < n; i++) bp.p[i] = (uint32_t)pos[i];
-    hipLaunchKernelGGL(blkb_qk_rope, dim3(H + Hk, (unsigned)n), dim3(64), 0, s, q, k, v, B->rope, bp, B->w_q, B->w_k,
-                       B->eps, B->kc, B->vc, kvs, qr, H, Hk, hd);
+    for (size_t i = 0; !pos_dev && i < n; i++) bp.p[i] = (uint32_t)pos[i];
+    hipLaunchKernelGGL(blkb_qk_rope, dim3(H + Hk, (unsigned)n), dim3(64), 0, s, q, k, v, B->rope, bp, pos_dev,
+                       B->cap, B->w_q, B->w_k, B->eps, B->kc, B->vc, kvs, qr, H, Hk, hd);
     QBK_HIP(hipGetLastError());
     const qbk_attn_shape one{1, B->H, B->Hk, 1, B->cap, B->hd, B->hd};
     const size_t qs = B->H * B->hd;
-    if (sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs)) {
+    if (pos_dev) {
+        if ((rc = sage_decode_batch(&one, qr, qs, B->kc, B->vc, kvs, B->block, at, qs, B->state, B->state_bytes,
+                                    B->cap, nullptr, nullptr, n, s, pos_dev)))
+            return rc;
+    } else if (sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs)) {
         size_t skv[BLKB_MAXSEQ], kept[BLKB_MAXSEQ];
         for (size_t i = 0; i < n; i++) {
             skv[i] = pos[i] + 1;
@@ -915,7 +974,7 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
                 return rc;
         }
     }
-    for (size_t i = 0; i < n; i++) B->tokens[i] = B->filled[i] = pos[i] + 1;
+    for (size_t i = 0; !pos_dev && i < n; i++) B->tokens[i] = B->filled[i] = pos[i] + 1;
     if ((rc = P.sets ? q4_run(B->o, n, at, true, oo, false, ws, s) : blkp_proj(B->o, n, at, true, oo, ws, s)))
         return rc;
     blkp_norm_launch(n, oo, h, h1, B->w_post, B->eps, x, d, P.sets ? 2 : 1, s);
@@ -935,6 +994,27 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
     hipLaunchKernelGGL(blkp_add, dim3((unsigned)div_ceil(nd, 256)), dim3(256), 0, s, oo, h1, h, nd);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
+}
+
+extern "C" {
+
+int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_t *pos, size_t n, void *workspace,
+                               size_t workspace_size, void *stream) {
+    if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    return block_decode_batch(ctx, B, h, pos, nullptr, n, workspace, workspace_size, stream);
+}
+
+int qbk_block_decode_batch_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const uint32_t *pos, size_t n,
+                                   void *workspace, size_t workspace_size, void *stream) {
+    if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (B && n && n <= B->nseq) {
+        const qbk_attn_shape one{1, B->H, B->Hk, 1, B->cap, B->hd, B->hd};
+        if (!sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, B->cap * B->Hk * B->hd))
+            return fail(QBK_ERR_VALIDATION, "a device-position step needs the grouped sage decode kernels "
+                                            "(head_dim a multiple of 16, groups of up to 16 heads, blocks of up "
+                                            "to 64 tokens)");
+    }
+    return block_decode_batch(ctx, B, h, nullptr, pos, n, workspace, workspace_size, stream);
 }
 
 }  // extern "C"

@@ -92,9 +92,18 @@ static inline size_t round_up(size_t a, size_t b) { return div_ceil(a, b) * b; }
 #define QBK_DEC_MAXSEQ 64
 bool sage_decode_batchable(const qbk_attn_shape *one, size_t block, size_t cap, const float *k, const float *v,
                            size_t kv_stride);
+struct DecOpSink;
 int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride, const float *k, const float *v,
                       size_t kv_stride, size_t block, float *out, size_t o_stride, void *state, size_t st_stride,
-                      size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st);
+                      size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st,
+                      const uint32_t *pos_dev = nullptr, const DecOpSink *sink = nullptr);
+// pos_dev (device, n entries): each sequence's position instead of seq_kv
+// and cached -- the step attends over pos + 1 cache rows and keeps the
+// codes of the pos / block complete key blocks before it (a state stepped
+// through pos - 1); the grids cover the capacity and the kernels read the
+// positions, so a captured graph of the step serves every position.  A
+// position at or past the capacity skips that sequence.  sink (n == 1):
+// the combine writes the o projection's batch-1 operand as well.
 
 // A decode step (qbk_attention_sage_decode_step_dev's contract) whose
 // combine also writes its output [n_heads][val_dim] as the batch-1 stage-1

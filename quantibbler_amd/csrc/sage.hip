@@ -674,7 +674,10 @@ struct DecSeqTab {
     uint32_t S[QBK_DEC_MAXSEQ], kb0[QBK_DEC_MAXSEQ];
     size_t q_stride, o_stride, kv_stride;  // floats
     size_t st_stride;                      // bytes
+    const uint32_t *pos;                   // device positions in place of S and kb0, or null
 };
+
+typedef __attribute__((address_space(4))) const uint32_t cu32_t;
 
 template <class T>
 __device__ __forceinline__ T *dec_shift(T *p, size_t bytes) {
@@ -682,9 +685,18 @@ __device__ __forceinline__ T *dec_shift(T *p, size_t bytes) {
 }
 
 __device__ __forceinline__ void dec_seq_ref(RefArgs &a, const DecSeqTab &t, uint32_t s) {
-    a.S = t.S[s];
+    if (t.pos) {
+        // written by an earlier kernel of the stream (scalar loads: the
+        // scalar cache starts each kernel invalidated)
+        const uint32_t p = ((cu32_t *)t.pos)[s];
+        const bool ok = p < a.pst;
+        a.S = ok ? p + 1 : 0;
+        a.kb0 = ok ? p / a.block : 0;
+    } else {
+        a.S = t.S[s];
+        a.kb0 = t.kb0[s];
+    }
     a.nkb = (a.S + a.block - 1) / a.block;
-    a.kb0 = t.kb0[s];
     a.q += s * t.q_stride;
     a.out += s * t.o_stride;
     a.k += s * t.kv_stride;
@@ -1929,11 +1941,13 @@ bool sage_decode_batchable(const qbk_attn_shape *one, size_t block, size_t cap, 
 
 int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride, const float *k, const float *v,
                       size_t kv_stride, size_t block, float *out, size_t o_stride, void *state, size_t st_stride,
-                      size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st) {
+                      size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st,
+                      const uint32_t *pos_dev, const DecOpSink *sink) {
     DecPlan P;
     DPrepGeom g;
     if (n == 0 || n > QBK_DEC_MAXSEQ || !dec_batch_plan(one, block, cap, k, v, kv_stride, P, g))
         return fail(QBK_ERR_VALIDATION, "sage decode: no batched form for this shape");
+    if (sink && n != 1) return fail(QBK_ERR_VALIDATION, "sage decode: an operand sink serves one sequence");
     DecArgs da = P.da;
     RefArgs &a = da.r;
     a.q = q;
@@ -1941,14 +1955,21 @@ int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride
     a.v = v;
     a.out = out;
     dec_bind(P, da, state);
+    if (sink) {
+        da.op_s2 = sink->s2;
+        da.op = sink->op;
+        da.op_sc = sink->sc;
+    }
     DecSeqTab t{};
     t.n = (uint32_t)n;
     t.q_stride = q_stride;
     t.o_stride = o_stride;
     t.kv_stride = kv_stride;
     t.st_stride = st_stride;
+    t.pos = pos_dev;
     size_t mkb = 0, mx = 1;
-    for (size_t i = 0; i < n; i++) {
+    if (pos_dev) mkb = a.pnkb;  // the capacity's blocks; one block (the position's) to quantise
+    for (size_t i = 0; !pos_dev && i < n; i++) {
         if (seq_kv[i] == 0 || seq_kv[i] > cap || cached[i] > seq_kv[i])
             return fail(QBK_ERR_VALIDATION, fmt("sage decode: sequence %zu holds %zu tokens (%zu kept) in a "
                                                 "capacity of %zu", i, seq_kv[i], cached[i], cap));

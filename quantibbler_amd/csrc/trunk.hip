@@ -119,6 +119,13 @@ __global__ void __launch_bounds__(ARGMAX_THREADS) trunk_argmax(const float *logi
     }
 }
 
+// pos[i] += 1 for the n sequences of a greedy loop's step (device-position
+// decode steps read them).
+__global__ void trunk_advance(uint32_t *pos, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) pos[i] = pos[i] + 1;
+}
+
 }  // namespace qbk
 
 using namespace qbk;
@@ -166,6 +173,16 @@ int qbk_rms_norm_dev(qbk_ctx *ctx, const float *x, size_t rows, size_t d, const 
     if ((rc = bind(ctx))) return rc;
     hipLaunchKernelGGL(trunk_rms_norm, dim3((unsigned)rows), dim3(TRUNK_THREADS), 0, (hipStream_t)stream, x, d, w,
                        (float)eps, out);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+int qbk_positions_advance_dev(qbk_ctx *ctx, uint32_t *pos, size_t n, void *stream) {
+    int rc;
+    if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (n == 0) return QBK_OK;
+    if ((rc = bind(ctx))) return rc;
+    hipLaunchKernelGGL(trunk_advance, dim3((unsigned)div_ceil(n, 256)), dim3(256), 0, (hipStream_t)stream, pos, n);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

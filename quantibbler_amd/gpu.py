@@ -265,6 +265,11 @@ def rms_norm_dev(ctx: GpuContext, x, rows: int, d: int, w, eps: float, out, stre
                                        _stream(stream)))
 
 
+def advance_positions_dev(ctx: GpuContext, pos, n: int, stream=None):
+    """pos[i] += 1 for the n device uint32 positions of a greedy loop."""
+    check(_lib.load().qbk_positions_advance_dev(ctx.handle, _ptr(pos), int(n), _stream(stream)))
+
+
 def argmax_dev(ctx: GpuContext, logits, rows: int, vocab: int, out, stream=None):
     """sampler.rs:4-15 greedy, per row (int32 ids into ``out``)."""
     check(_lib.load().qbk_argmax_dev(ctx.handle, _ptr(logits), int(rows), int(vocab), _ptr(out),
@@ -404,6 +409,40 @@ class DecoderBlock:
         check(_lib.load().qbk_block_decode_batch_dev(self.ctx.handle, self._h, _ptr(h),
                                                      _ptr(pos), n, _ptr(workspace),
                                                      int(workspace_size), _stream(stream)))
+
+    def decode_pos_dev(self, h, pos, stream=None):
+        """decode_dev at the position the device uint32 ``pos`` holds when
+        the step runs (a HIP graph of the step serves every position); the
+        kept attention state must be stepped through pos - 1.  The block's
+        host record of positions is left as it was (set_positions)."""
+        self._check_rows(h, 1, "decoder block input")
+        self._check_pos(pos, 1)
+        check(_lib.load().qbk_block_decode_pos_dev(self.ctx.handle, self._h, _ptr(h), _ptr(pos),
+                                                   _stream(stream)))
+
+    def decode_batch_pos_dev(self, h, pos, n: int, workspace, workspace_size: int, stream=None):
+        """decode_batch_dev with the n positions in the device uint32 tensor
+        ``pos``, read when the step runs."""
+        self._check_rows(h, int(n), "batched decode input")
+        self._check_pos(pos, int(n))
+        check(_lib.load().qbk_block_decode_batch_pos_dev(self.ctx.handle, self._h, _ptr(h), _ptr(pos), int(n),
+                                                         _ptr(workspace), int(workspace_size), _stream(stream)))
+
+    def set_positions(self, positions):
+        """The host record after device-position steps: sequence i holds
+        positions[i] positions, its attention state stepped through them."""
+        p = np.ascontiguousarray(positions, np.uint64).ravel()
+        check(_lib.load().qbk_block_set_positions(self._h, _ptr(p), p.size))
+
+    @staticmethod
+    def _check_pos(pos, n: int):
+        if hasattr(pos, "is_cuda"):
+            if not pos.is_cuda or str(pos.dtype) not in ("torch.int32", "torch.uint32") \
+                    or not pos.is_contiguous() or pos.numel() < n:
+                raise _lib.KernelError(f"positions must be a contiguous 32-bit device tensor of at least {n} "
+                                       f"entries; got {pos.dtype} of {pos.numel()} on {pos.device}")
+        elif not isinstance(pos, int):
+            raise _lib.KernelError("positions must be a device tensor or a device address")
 
     def _check_rows(self, h, n: int, what: str):
         if hasattr(h, "is_cuda"):

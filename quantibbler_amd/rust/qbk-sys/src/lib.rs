@@ -160,6 +160,12 @@ extern "C" {
     pub fn qbk_block_decode_batch_dev(ctx: *mut QbkCtx, block: *mut QbkBlock, h: *mut f32, pos: *const usize,
                                       n: usize, workspace: *mut c_void, workspace_size: usize,
                                       stream: *mut c_void) -> c_int;
+    pub fn qbk_block_decode_pos_dev(ctx: *mut QbkCtx, block: *mut QbkBlock, h: *mut f32, pos: *const u32,
+                                    stream: *mut c_void) -> c_int;
+    pub fn qbk_block_decode_batch_pos_dev(ctx: *mut QbkCtx, block: *mut QbkBlock, h: *mut f32, pos: *const u32,
+                                          n: usize, workspace: *mut c_void, workspace_size: usize,
+                                          stream: *mut c_void) -> c_int;
+    pub fn qbk_block_set_positions(block: *mut QbkBlock, pos: *const usize, n: usize) -> c_int;
     pub fn qbk_embed(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32, n: usize,
                      out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_embed_dev(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32,
@@ -168,6 +174,7 @@ extern "C" {
                             out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_argmax_dev(ctx: *mut QbkCtx, logits: *const f32, rows: usize, vocab: usize, out: *mut i32,
                           stream: *mut c_void) -> c_int;
+    pub fn qbk_positions_advance_dev(ctx: *mut QbkCtx, pos: *mut u32, n: usize, stream: *mut c_void) -> c_int;
     pub fn qbk_attention_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const f32, k: *const f32,
                              v: *const f32, causal: c_int, out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_attention_sage_dev(ctx: *mut QbkCtx, shape: *const AttentionShape, q: *const f32, k: *const f32,
