@@ -380,8 +380,12 @@ def bench_model(qa, ctx, torch, np, n_blocks=32, prompt=2048, steps=256, vocab=1
     together (embedding rows, 32 DecoderBlocks -- projections at batch b, the
     sage decode attention stepping each sequence's kept state -- final norm,
     logits, argmax; engine/mod.rs:802-822, :1377-1476, sampler.rs:4-15), the
-    next tokens fed back on the device."""
-    from quantibbler_amd.gpu import argmax_dev, embed, embed_dev, rms_norm_dev
+    next tokens fed back on the device.  Each batch size runs twice: with
+    the steps launched from the host, and (after a second prefill and one
+    host-launched step) with the step captured once in a HIP graph --
+    device positions, advanced on the device -- and replayed `steps` - 1
+    times."""
+    from quantibbler_amd.gpu import advance_positions_dev, argmax_dev, embed, embed_dev, rms_norm_dev
 
     rng = np.random.default_rng(55)
     d = 4096
@@ -441,6 +445,22 @@ def bench_model(qa, ctx, torch, np, n_blocks=32, prompt=2048, steps=256, vocab=1
         head.logits_dev(hn, b, logits, st)
         argmax_dev(ctx, logits, b, vocab, tok, st)
 
+    pos_dev = torch.zeros(nseq, dtype=torch.int32, device="cuda")
+
+    def token_dev(b, s):
+        # the same step with the positions in pos_dev, advanced at its end
+        embed_dev(ctx, table, vocab, d, tok, b, h, s)
+        if b == 1:
+            for B in blocks:
+                B.decode_pos_dev(h[0], pos_dev, s)
+        else:
+            for B in blocks:
+                B.decode_batch_pos_dev(h, pos_dev, b, ws, wd, s)
+        rms_norm_dev(ctx, h, b, d, w_final, 1e-5, hn, s)
+        head.logits_dev(hn, b, logits, s)
+        argmax_dev(ctx, logits, b, vocab, tok, s)
+        advance_positions_dev(ctx, pos_dev, b, s)
+
     out = {}
     prefill(1)          # warm-up pass (first launches, allocator)
     token(1, prompt)
@@ -458,10 +478,39 @@ def bench_model(qa, ctx, torch, np, n_blocks=32, prompt=2048, steps=256, vocab=1
         finite = bool(torch.isfinite(logits[:b]).all())
         log(f"  config 5 (B={b}): prefill of {b} x {prompt} tokens {pre_ms:.2f} ms, then {steps} greedy steps "
             f"at {dec_ms:.3f} ms/step ({b * 1e3 / dec_ms:.1f} tokens/s)")
+        eager_tok = tok[:b].clone()
+        # the graph-replayed loop: prefill again, one host-launched step
+        # (the attention states then hold every complete key block), the
+        # step captured once, then replayed for the remaining steps
+        prefill(b)
+        token(b, prompt)
+        pos_dev[:b] = prompt + 1
+        side = torch.cuda.Stream()
+        side.wait_stream(st)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            token_dev(b, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        a.record(st)
+        for i in range(steps - 1):
+            graph.replay()
+        c.record(st)
+        torch.cuda.synchronize()
+        graph_ms = a.elapsed_time(c) / (steps - 1)
+        same_tokens = bool(torch.equal(tok[:b], eager_tok))
+        del graph
+        for B in blocks:
+            B.set_positions([prompt + steps] * b)
+        log(f"  config 5 (B={b}): graph-replayed steps at {graph_ms:.3f} ms/step ({b * 1e3 / graph_ms:.1f} "
+            f"tokens/s), final tokens {'equal to' if same_tokens else 'DIFFERENT from'} the host-launched loop's")
         out[f"b{b}"] = {"batch": b, "prefill_ms": round(pre_ms, 2),
                         "prefill_tokens_per_s": round(b * prompt / pre_ms * 1e3, 1),
                         "decode_ms_per_step": round(dec_ms, 3),
                         "decode_tokens_per_s": round(b * 1e3 / dec_ms, 1),
+                        "graph_decode_ms_per_step": round(graph_ms, 3),
+                        "graph_decode_tokens_per_s": round(b * 1e3 / graph_ms, 1),
+                        "graph_tokens_equal": same_tokens,
                         "prompt_tokens": prompt, "decode_steps": steps, "logits_finite": finite}
     for B in blocks:
         B.close()
