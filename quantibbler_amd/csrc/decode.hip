@@ -43,6 +43,9 @@ typedef __attribute__((address_space(1))) const float gf32_t;
 typedef __attribute__((address_space(4))) const Q4Layer cq4layer_t;
 
 #define Q4_U 8       // slices whose sign loads a wave issues together
+// waves of a GEMV workgroup: four, or eight when eight waves split one row
+// group's K (a lone layer of long K at batch 1)
+#define Q4_NW(ks) ((ks) > 4 ? (ks) : 4)
 #define Q4_PHASES 3  // prep x, stage 1 (+ stage 2's operand), stage 2
 
 // One launch over a set of layers.
@@ -358,10 +361,11 @@ __host__ __device__ constexpr uint32_t q4_wave_lds(int ncol) {
     return ncol > 0 ? (uint32_t)(Q4_U * 4 * ncol * 32 + 256 + 48) : 16 * 64 * 4;
 }
 
-// Decode GEMV.  Workgroup = 4 waves; KSPLIT waves share a 64-row group and
-// split its slices (4/KSPLIT row groups per workgroup).  Lane l loads the 16
-// bytes of its four row tiles' sign words per slice (1 KiB per wave per
-// slice, contiguous over the slices); Q4_U slices are loaded per step.
+// Decode GEMV.  Workgroup = 4 waves (8 at KSPLIT 8); KSPLIT waves share a
+// 64-row group and split its slices (Q4_NW / KSPLIT row groups per
+// workgroup).  Lane l loads the 16 bytes of its four row tiles' sign words
+// per slice (1 KiB per wave per slice, contiguous over the slices); Q4_U
+// slices are loaded per step.
 //
 // NCOL > 0 (batch 1-2): each wave stages the fp8 operand of its own slices
 // through registers into its LDS region -- operand loads issued first, sign
@@ -377,7 +381,7 @@ __host__ __device__ constexpr uint32_t q4_wave_lds(int ncol) {
 // contiguous range [x*per_x, (x+1)*per_x) of the (layer, row group) work, so
 // that one layer's operand is fetched into one L2.
 template <int STAGE, int KSPLIT, int NCOL, int NCG = 1>
-__global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
+__global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     static_assert(NCG == 1 || NCOL == 0, "column groups read their operand from global memory");
     extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -388,7 +392,7 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
     if (wgi >= a.n_wg) return;  // padding workgroup (the whole group leaves)
     const uint32_t li = q4_layer_of(a, wgi);
     const Q4Layer L = q4_entry(a, li);
-    constexpr int RG_PER_WG = 4 / KSPLIT;
+    constexpr int RG_PER_WG = Q4_NW(KSPLIT) / KSPLIT;
     const size_t rg = (size_t)(wgi - L.wg0) * RG_PER_WG + wave / KSPLIT;
     const int ks = wave % KSPLIT;
     const size_t n_rg = L.rows_p / 64, ns = L.ns;
@@ -502,8 +506,8 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
         if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
     }
     if (KSPLIT > 1) {
-        // one column group at a time through [4 waves][4 tiles][64 lanes]
-        f32x4_t *red = (f32x4_t *)(q4_lds + 4 * wreg);
+        // one column group at a time through [waves][4 tiles][64 lanes]
+        f32x4_t *red = (f32x4_t *)(q4_lds + Q4_NW(KSPLIT) * wreg);
 #pragma unroll
         for (int cg = 0; cg < NCG; cg++) {
             if (cg) __syncthreads();  // the last group's sums are read
@@ -535,16 +539,22 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4Args a) {
 
 // LDS bytes of a q4_gemv_kernel workgroup.
 static size_t q4_gemv_lds(int ncol_t, int ksplit) {
-    return 4 * (size_t)q4_wave_lds(ncol_t) + (ksplit > 1 ? 4 * 4 * 64 * 16 : 0);
+    const size_t nw = Q4_NW(ksplit);
+    return nw * (size_t)q4_wave_lds(ncol_t) + (ksplit > 1 ? nw * 4 * 64 * 16 : 0);
 }
 
 // Waves that share a 64-row group split its slices: one load step (Q4_U
 // slices) per wave where the group has more, and further while the launch
 // is too small to fill the chip (a single layer).
-static int q4_ksplit(size_t max_ns, size_t min_ns, size_t n_rg_total, int num_cus) {
+static int q4_ksplit(size_t max_ns, size_t min_ns, size_t n_rg_total, int num_cus, size_t batch) {
     int k = 1;
     while (k < 4 && max_ns > (size_t)(2 * Q4_U * k)) k *= 2;
     while (k < 4 && min_ns >= (size_t)(2 * k) && n_rg_total * k < (size_t)num_cus * 8) k *= 2;
+    // eight waves a row group (one workgroup of 512 threads) where four
+    // would each run more than two load steps and the launch holds few row
+    // groups (a lone long-K layer at batch 1: config 3's down projection, 112
+    // slices over 28 row groups, 10.7 -> 8.4 us; sixteen waves, 8.6)
+    if (k == 4 && batch == 1 && min_ns > (size_t)(2 * Q4_U * 4) && n_rg_total * 8 <= (size_t)num_cus * 4) k = 8;
     return k;
 }
 
@@ -587,9 +597,9 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
         G.din_mult8 = G.din_mult8 && layers[i]->din % 8 == 0;
         G.din_mult128 = G.din_mult128 && layers[i]->din % 128 == 0;
     }
-    G.ks1 = q4_ksplit(max1, min1, rg1, num_cus);
-    G.ks2 = q4_ksplit(max2, min2, rg2, num_cus);
-    const size_t rpw1 = 4 / G.ks1, rpw2 = 4 / G.ks2;
+    G.ks1 = q4_ksplit(max1, min1, rg1, num_cus, batch);
+    G.ks2 = q4_ksplit(max2, min2, rg2, num_cus, batch);
+    const size_t rpw1 = Q4_NW(G.ks1) / G.ks1, rpw2 = Q4_NW(G.ks2) / G.ks2;
     size_t s1 = 0, s2 = 0, wg1 = 0, wg2 = 0, act = 0, out = 0;
     for (size_t i = 0; i < n; i++) {
         const qbk_factor *L = layers[i];
@@ -701,6 +711,14 @@ static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32
     const int ncg = (int)div_ceil(G.ncol, 16);           // column groups (batch > 8)
     const size_t lds = q4_gemv_lds(ncol_t, ksplit);
     dim3 g((unsigned)round_up((size_t)a.n_wg, 8));  // a multiple of the 8 XCDs
+    if (ksplit > 4) {  // batch 1 only (q4_ksplit)
+        if (phase == 2)
+            hipLaunchKernelGGL((q4_gemv_kernel<1, 8, 2>), g, dim3(512), lds, s, a);
+        else
+            hipLaunchKernelGGL((q4_gemv_kernel<2, 8, 2>), g, dim3(512), lds, s, a);
+        QBK_HIP(hipGetLastError());
+        return QBK_OK;
+    }
 #define Q4_LAUNCH(ST, KS)                                                                             \
     if (ncol_t == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 2>), g, dim3(256), lds, s, a);       \
     else if (ncol_t == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 4>), g, dim3(256), lds, s, a);  \

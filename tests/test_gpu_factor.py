@@ -77,6 +77,14 @@ def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
     integer_exact_case(ctx, orc, dout, din, r, batch)
 
 
+@pytest.mark.parametrize("dout,din,r", [(4096, 14336, 1733), (512, 9000, 200)])
+def test_integer_exact_long_k_batch1(ctx, orc, dout, din, r):
+    """A lone layer of long K at batch 1 (config 3's down projection, and a
+    K that is not a multiple of 128): stage 1 splits each row group's slices
+    over eight waves (512-thread workgroups) instead of four."""
+    integer_exact_case(ctx, orc, dout, din, r, 1)
+
+
 def test_integer_exact_config2_batch512(ctx, orc):
     """Config 2's shape at B = 512 (the K-split stage 1 on 128 x 64 tiles, stage
     2 on its own 256 tiles)."""
