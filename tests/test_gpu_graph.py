@@ -173,3 +173,38 @@ def test_block_graph_replay_bit_identical(ctx, orc, batched):
         blk.close()
     for L in devs:
         L.close()
+
+
+def test_block_device_position_past_capacity_skips(ctx, orc):
+    """A device position at the capacity writes no cache row and steps no
+    attention state (the kernels read the position and leave): after such a
+    step the block continues eagerly, bit-identical to its twin that never
+    took it."""
+    from quantibbler_amd.gpu import advance_positions_dev
+
+    say("device position at the capacity")
+    eag, dp, devs, rng = twin_blocks(ctx, orc, 4711, 4, 1, cap=80)
+    st = torch.cuda.current_stream()
+    d = eag.d_model
+    for pos in range(10):
+        x = torch.from_numpy(rng.standard_normal(d).astype(np.float32)).cuda()
+        ha, hb = x.clone(), x.clone()
+        eag.decode_dev(ha, pos, st)
+        dp.decode_dev(hb, pos, st)
+    pos_dev = torch.tensor([80], dtype=torch.int32, device="cuda")
+    junk = torch.from_numpy(rng.standard_normal(d).astype(np.float32)).cuda()
+    dp.decode_pos_dev(junk, pos_dev, st)
+    advance_positions_dev(ctx, pos_dev, 1, st)
+    torch.cuda.synchronize()
+    assert int(pos_dev.item()) == 81
+    for pos in range(10, 14):
+        x = torch.from_numpy(rng.standard_normal(d).astype(np.float32)).cuda()
+        ha, hb = x.clone(), x.clone()
+        eag.decode_dev(ha, pos, st)
+        dp.decode_dev(hb, pos, st)
+        torch.cuda.synchronize()
+        assert torch.equal(ha, hb), (pos, float((ha - hb).abs().max()))
+    for blk in (eag, dp):
+        blk.close()
+    for L in devs:
+        L.close()
