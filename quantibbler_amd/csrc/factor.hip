@@ -92,6 +92,27 @@ static void container_to_rows_transposed(const uint8_t *packed, size_t din, size
         }
 }
 
+// The reference's per-row bitplanes (bit k of row i at byte k/8, LSB first,
+// set for +1) rebuilt from the fp4 decode layout: one thread per row byte,
+// each of its bits read from the word and bit repack_q4 put it at (the
+// inverse of kq4: k % 128 = 64 (g & 1) + 32 (e >> 4) + 16 (g >> 1) + e % 16).
+__global__ void q4_to_rows(const uint32_t *q4, size_t n_rows, size_t n_bits, size_t bits_q, uint8_t *rows) {
+    const size_t rw = (n_bits + 7) / 8, idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_rows * rw) return;
+    const size_t i = idx / rw, j = idx % rw, ns = bits_q / 128;
+    const size_t rg = i / 64, rt = (i % 64) / 16, l15 = i % 16;
+    uint32_t byte = 0;
+    for (int b = 0; b < 8; b++) {
+        const size_t k = 8 * j + b;
+        if (k >= n_bits) break;
+        const uint32_t kk = (uint32_t)(k % 128), s = (uint32_t)(k / 128);
+        const uint32_t g = 2 * ((kk >> 4) & 1) + ((kk >> 6) & 1), e = 16 * ((kk >> 5) & 1) + (kk & 15);
+        const uint32_t w = q4[((rg * ns + s) * 64 + 16 * g + l15) * 4 + rt];
+        if (!((w >> (4 * (e & 7) + (e >> 3))) & 1)) byte |= 1u << b;
+    }
+    rows[idx] = (uint8_t)byte;
+}
+
 static int dev_upload(qbk_factor *L, void **dst, const void *src, size_t n) {
     void *p = nullptr;
     QBK_HIP(hipMalloc(&p, n ? n : 16));
@@ -150,8 +171,7 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
         return rc;                                                         \
     }                                                                      \
     L->field = (decltype(L->field))p;
-    UP(ub_rows, ub_rows, dout * div_ceil(r, 8));
-    UP(vbt_rows, vbt_rows, r * div_ceil(din, 8));
+    L->ub_rows = L->vbt_rows = nullptr;  // formed on the first f64-face call (q4_to_rows)
     UP(vt_g32, vf.data(), vf.size() * 4);
     UP(u_g32, uf.data(), uf.size() * 4);
     UP(vt_q4, vq.data(), vq.size() * 4);
@@ -381,7 +401,32 @@ int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *L, int serving, const float
     if ((rc = cs.create())) return rc;
     if (serving == QBK_F32) {
         // per token: z = f64(s2*x), the two f64 matvecs in element order,
-        // y = f32(u)*s1 + b -- all on the device
+        // y = f32(u)*s1 + b -- all on the device.  The matvecs read the
+        // reference's row layout, which the layer forms from its decode
+        // layout on the first such call (a third copy of the signs only for
+        // layers that use this face).
+        {
+            static std::mutex mu;
+            std::lock_guard<std::mutex> lock(mu);
+            if (!L->ub_rows) {
+                qbk_factor *M = const_cast<qbk_factor *>(L);
+                void *pu = nullptr, *pv = nullptr;
+                const size_t nu = L->dout * div_ceil(L->r, 8), nv = L->r * div_ceil(L->din, 8);
+                QBK_HIP(hipMalloc(&pu, nu));
+                M->allocs.push_back(pu);
+                QBK_HIP(hipMalloc(&pv, nv));
+                M->allocs.push_back(pv);
+                hipLaunchKernelGGL(q4_to_rows, dim3((unsigned)div_ceil(nu, 256)), dim3(256), 0, cs.s, L->u_q4, L->dout,
+                                   L->r, L->r_q, (uint8_t *)pu);
+                QBK_HIP(hipGetLastError());
+                hipLaunchKernelGGL(q4_to_rows, dim3((unsigned)div_ceil(nv, 256)), dim3(256), 0, cs.s, L->vt_q4, L->r,
+                                   L->din, L->din_q, (uint8_t *)pv);
+                QBK_HIP(hipGetLastError());
+                QBK_HIP(hipStreamSynchronize(cs.s));
+                M->vbt_rows = (uint8_t *)pv;
+                M->ub_rows = (uint8_t *)pu;
+            }
+        }
         DevBuf dx, dy, dz, dt, du;
         if ((rc = dx.alloc(batch * L->din * 4)) || (rc = dy.alloc(batch * L->dout * 4)) ||
             (rc = dz.alloc(L->din * 8)) || (rc = dt.alloc(L->r * 8)) || (rc = du.alloc(L->dout * 8)))

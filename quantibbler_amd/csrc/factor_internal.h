@@ -47,7 +47,8 @@ struct qbk_factor {
     int device, num_cus;
     size_t dout, din, r;
     size_t din_p, r_p, dout_p;  // padded for the MFMA tiles (64 / 128 / 128)
-    uint8_t *ub_rows, *vbt_rows;      // reference per-row bitplanes
+    uint8_t *ub_rows, *vbt_rows;      // reference per-row bitplanes, formed from the decode layout on the
+                                      // first f64-face call (null until then)
     uint32_t *vt_g32, *u_g32;         // prefill layout: [r_p/128][din_p/64][64][4], [dout_p/128][r_p/64][64][4]
     size_t din_q, r_q;                // K of the fp4 decode layout: multiples of 128
     uint32_t *vt_q4, *u_q4;           // [r_p/64][din_q/128][64][4], [dout_p/64][r_q/128][64][4]
