@@ -119,29 +119,7 @@ __global__ void __launch_bounds__(64) blkd_qk_rope(const float *qkv, const float
     const int hh = is_q ? head : head - H;
     const float *src = is_q ? qkv + (size_t)hh * hd : qkv + (size_t)H * hd + (size_t)hh * hd;
     float *dst = is_q ? qrot + (size_t)hh * hd : kc + pos * (size_t)Hk * hd + (size_t)hh * hd;
-    const float *w = is_q ? wq : wk;
-    float inv = 1.0f;
-    if (w) {
-        float ss = 0.0f;
-        for (int j = lane; j < hd; j += 64) {
-            const float b = bf16_to_f32(f32_to_bf16(src[j]));
-            ss += b * b;
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        inv = 1.0f / sqrtf(ss / (float)hd + eps);
-    }
-    const float2 *cs = rope + pos * (size_t)half;
-    for (int j = lane; j < half; j += 64) {
-        float a = src[j], b = src[j + half];
-        if (w) {
-            a = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(a)) * inv * w[j]));
-            b = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(b)) * inv * w[j + half]));
-        }
-        const float2 c = cs[j];
-        dst[j] = a * c.x - b * c.y;
-        dst[j + half] = b * c.x + a * c.y;
-    }
+    rope_head(src, is_q ? wq : wk, eps, rope + pos * (size_t)half, hd, lane, [&](int j, float v) { dst[j] = v; });
     if (!is_q) {
         const float *v = qkv + (size_t)(H + Hk) * hd + (size_t)hh * hd;
         float *vr = vc + pos * (size_t)Hk * hd + (size_t)hh * hd;
@@ -479,29 +457,7 @@ __global__ void __launch_bounds__(64) blkb_qk_rope(const float *q, const float *
     const int hh = is_q ? head : head - H;
     const float *src = is_q ? q + ((size_t)t * H + hh) * hd : k + ((size_t)t * Hk + hh) * hd;
     float *dst = is_q ? qr + ((size_t)t * H + hh) * hd : kc + t * kvs + (p * Hk + hh) * hd;
-    const float *w = is_q ? wq : wk;
-    float inv = 1.0f;
-    if (w) {
-        float ss = 0.0f;
-        for (int j = lane; j < hd; j += 64) {
-            const float b = bf16_to_f32(f32_to_bf16(src[j]));
-            ss += b * b;
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        inv = 1.0f / sqrtf(ss / (float)hd + eps);
-    }
-    const float2 *cs = rope + p * (size_t)half;
-    for (int j = lane; j < half; j += 64) {
-        float a = src[j], b = src[j + half];
-        if (w) {
-            a = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(a)) * inv * w[j]));
-            b = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(b)) * inv * w[j + half]));
-        }
-        const float2 c = cs[j];
-        dst[j] = a * c.x - b * c.y;
-        dst[j + half] = b * c.x + a * c.y;
-    }
+    rope_head(src, is_q ? wq : wk, eps, rope + p * (size_t)half, hd, lane, [&](int j, float x) { dst[j] = x; });
     if (!is_q) {
         const float *vs = v + ((size_t)t * Hk + hh) * hd;
         float *vr = vc + t * kvs + (p * Hk + hh) * hd;
@@ -733,9 +689,16 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
         QBK_HIP(hipGetLastError());
         if ((rc = q4_set_run(B->qkv, B->xcat, false, B->ycat, false, B->ws, s))) return rc;
     }
-    hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, pos_dev, B->cap, B->w_q,
-                       B->w_k, B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
-    QBK_HIP(hipGetLastError());
+    // the q/k norms, RoPE and the cache append run in the attention's
+    // pre-pass when the grouped decode kernels serve the shape (one launch
+    // fewer), else in a kernel of their own
+    const bool fold = sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs);
+    const DecRope rp{B->ycat, B->rope, B->w_q, B->w_k, B->eps, H};
+    if (!fold) {
+        hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, pos_dev, B->cap,
+                           B->w_q, B->w_k, B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
+        QBK_HIP(hipGetLastError());
+    }
     // the attention's combine writes the o projection's operand directly
     DecOpSink sink{B->o->s2, nullptr, nullptr};
     const bool osink = B->hd % 128 == 0 && q4_flat_operand(B->o, B->ws, &sink.op, &sink.sc);
@@ -743,13 +706,14 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
         const size_t qs = B->H * B->hd;
         if ((rc = sage_decode_batch(&one, B->qrot, qs, B->kc, B->vc, kvs, B->block, B->attn, qs, B->state,
                                     B->state_bytes, B->cap, nullptr, nullptr, 1, s, pos_dev,
-                                    osink ? &sink : nullptr)))
+                                    osink ? &sink : nullptr, fold ? &rp : nullptr)))
             return rc;
     } else {
         const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos + 1, B->hd, B->hd};
         const size_t cached = B->tokens[0] <= pos ? B->tokens[0] : 0;
         if ((rc = sage_decode_step_sink(ctx, &sh, B->qrot, B->kc, B->vc, B->block, B->attn, B->state,
-                                        B->state_bytes, B->cap, cached, osink ? &sink : nullptr, stream)))
+                                        B->state_bytes, B->cap, cached, osink ? &sink : nullptr, stream,
+                                        fold ? &rp : nullptr)))
             return rc;
         B->tokens[0] = pos + 1;
         B->filled[0] = pos + 1;

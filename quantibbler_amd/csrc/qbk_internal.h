@@ -93,17 +93,21 @@ static inline size_t round_up(size_t a, size_t b) { return div_ceil(a, b) * b; }
 bool sage_decode_batchable(const qbk_attn_shape *one, size_t block, size_t cap, const float *k, const float *v,
                            size_t kv_stride);
 struct DecOpSink;
+struct DecRope;
 int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride, const float *k, const float *v,
                       size_t kv_stride, size_t block, float *out, size_t o_stride, void *state, size_t st_stride,
                       size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st,
-                      const uint32_t *pos_dev = nullptr, const DecOpSink *sink = nullptr);
+                      const uint32_t *pos_dev = nullptr, const DecOpSink *sink = nullptr,
+                      const DecRope *rope = nullptr);
 // pos_dev (device, n entries): each sequence's position instead of seq_kv
 // and cached -- the step attends over pos + 1 cache rows and keeps the
 // codes of the pos / block complete key blocks before it (a state stepped
 // through pos - 1); the grids cover the capacity and the kernels read the
 // positions, so a captured graph of the step serves every position.  A
 // position at or past the capacity skips that sequence.  sink (n == 1):
-// the combine writes the o projection's batch-1 operand as well.
+// the combine writes the o projection's batch-1 operand as well.  rope
+// (n == 1): the step's q/k norm, RoPE and cache append run in the pre-pass
+// (the caches then take the new row from rope->qkv, not from the caller).
 
 // A decode step (qbk_attention_sage_decode_step_dev's contract) whose
 // combine also writes its output [n_heads][val_dim] as the batch-1 stage-1
@@ -115,7 +119,19 @@ struct DecOpSink {
 };
 int sage_decode_step_sink(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
                           const float *v, size_t block_size, float *out, void *state, size_t state_size,
-                          size_t capacity, size_t cached_tokens, const DecOpSink *sink, void *stream);
+                          size_t capacity, size_t cached_tokens, const DecOpSink *sink, void *stream,
+                          const DecRope *rope = nullptr);
+
+// The decode step's q/k norm and RoPE folded into the attention's pre-pass
+// (one sequence): the new token's k and v rows written into the cache and
+// its query rotated where the pre-pass forms the query's codes.
+struct DecRope {
+    const float *qkv;      // the step's projections: q (H heads), k (Hk), v (Hk), hd floats a head; null: no fold
+    const float2 *rope;    // (cos, sin) [capacity][hd / 2]
+    const float *wq, *wk;  // per-head norm weights, or null
+    float eps;
+    int H;
+};
 
 // ---- device helpers -------------------------------------------------------
 
@@ -129,6 +145,40 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
     if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
     uint32_t lsb = (u >> 16) & 1u;
     return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+
+// One head of a decode step's q/k norm (a per-head RMSNorm over bf16
+// operands when w is given, engine/mod.rs:909-912) and RoPE at the row cs of
+// (cos, sin) pairs (engine/mod.rs:878-945): a wave per head.  Each lane sums
+// the squares of its channels j = lane, lane + 64, ... in order, then an
+// xor-shuffle tree; out(j, value) receives rotated channel j.  The decode
+// kernels that rotate a head all call this, so their values agree bit for
+// bit.
+template <class OUT>
+__device__ __forceinline__ void rope_head(const float *src, const float *w, float eps, const float2 *cs, int hd,
+                                          int lane, OUT out) {
+    const int half = hd / 2;
+    float inv = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int j = lane; j < hd; j += 64) {
+            const float b = bf16_to_f32(f32_to_bf16(src[j]));
+            ss += b * b;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    }
+    for (int j = lane; j < half; j += 64) {
+        float a = src[j], b = src[j + half];
+        if (w) {
+            a = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(a)) * inv * w[j]));
+            b = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(b)) * inv * w[j + half]));
+        }
+        const float2 c = cs[j];
+        out(j, a * c.x - b * c.y);
+        out(j + half, b * c.x + a * c.y);
+    }
 }
 
 // The same rounding for a pair, packed (a in the low half), in one

@@ -782,12 +782,24 @@ static DPrepGeom dprep_geom(const RefArgs &a, const void *k, const void *v, uint
 // psi_Q of the step's query (gpu_attention.rs:113-159) for the heads of kv
 // head bk: a wave per head, lane l holding channels 4l .. 4l+3 (d <= 256);
 // the peak is a max, so a wave reduction gives the reference's value
-__device__ void dec_query_codes(const RefArgs &a, uint32_t bk, uint32_t *qsw, float *qdl) {
+//
+// With rp.qkv, the heads are rotated here first (rope_head at position p,
+// through the wave's lbuf region of d floats) instead of read from a.q.
+__device__ void dec_query_codes(const RefArgs &a, uint32_t bk, uint32_t *qsw, float *qdl, const DecRope &rp,
+                                uint32_t p, float *lbuf) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t G = (uint32_t)(a.H / a.Hk), d4 = (uint32_t)a.d / 4;
     for (uint32_t hg = wave; hg < G; hg += 4) {
         const uint32_t h = bk * G + hg;
         const float *qi = a.q + (size_t)h * a.d;
+        if (rp.qkv) {
+            float *lw = lbuf + wave * a.d;
+            __builtin_amdgcn_wave_barrier();  // the wave's last head is read
+            rope_head(rp.qkv + (size_t)h * a.d, rp.wq, rp.eps, rp.rope + (size_t)p * (a.d / 2), (int)a.d,
+                      (int)lane, [&](int j, float v) { lw[j] = v; });
+            __builtin_amdgcn_wave_barrier();
+            qi = lw;
+        }
         float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (lane < d4)
 #pragma unroll
@@ -820,7 +832,7 @@ __device__ void dec_query_codes(const RefArgs &a, uint32_t bk, uint32_t *qsw, fl
 // (t.n > 0): y runs over (sequence, kv head), x over the largest count of
 // blocks to quantise.
 __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uint32_t *qsw, float *qdl,
-                                                     DecSeqTab t) {
+                                                     DecSeqTab t, DecRope rp) {
     extern __shared__ __attribute__((aligned(16))) float tile[];  // [kj][row of this workgroup]
     __shared__ __attribute__((aligned(16))) float km[REF_MAXD];  // K means, then V scales
     __shared__ float kdl[256];                                    // deltas of this workgroup's tokens
@@ -833,8 +845,12 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
         qsw = dec_shift(qsw, sq * t.st_stride);
         qdl = dec_shift(qdl, sq * t.st_stride);
     }
+    // the step's position (one sequence): with rp.qkv its k and v rows are
+    // formed here -- row p of the block that holds it, in place of the cache
+    // row the loads bring, and written to the cache
+    const uint32_t p = a.S ? (uint32_t)a.S - 1 : 0;
     if (z == g.ks + g.vs) {
-        if (blockIdx.x == 0 && qsw) dec_query_codes(a, bky, qsw, qdl);
+        if (blockIdx.x == 0 && qsw && (a.S || !rp.qkv)) dec_query_codes(a, bky, qsw, qdl, rp, p, tile);
         return;
     }
     const uint32_t kb = (uint32_t)a.kb0 + blockIdx.x, bk = bky;
@@ -842,6 +858,7 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
     const uint32_t j0 = kb * (uint32_t)a.block;
     const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
     const uint32_t d = (uint32_t)a.d, d4 = d / 4;
+    const uint32_t prow = rp.qkv && p >= j0 && p - j0 < kj ? p - j0 : 0xffffffffu;
     f32x4_t r[DPREP_U];
     if (z < g.ks) {
         const float *K = a.k + bk * a.k_head + (size_t)j0 * a.k_tok;
@@ -855,7 +872,16 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
 #pragma unroll
         for (uint32_t u = 0; u < DPREP_U; u++) {
             const uint32_t row = r0 + u * g.kstep;
-            if (lane_ok && row < kj) *(f32x4_t *)&tile[row * d + 4 * q] = r[u];
+            if (lane_ok && row < kj && row != prow) *(f32x4_t *)&tile[row * d + 4 * q] = r[u];
+        }
+        if (prow != 0xffffffffu && tid < 64) {
+            float *crow = const_cast<float *>(K) + (size_t)prow * a.k_tok;
+            const bool w0 = z == 0;  // one workgroup appends the row
+            rope_head(rp.qkv + (size_t)(rp.H + bk) * d, rp.wk, rp.eps, rp.rope + (size_t)p * (d / 2), (int)d,
+                      (int)tid, [&](int j, float v) {
+                          tile[prow * d + j] = v;
+                          if (w0) crow[j] = v;
+                      });
         }
         __syncthreads();
         // the block's mean per channel, sequential over its tokens
@@ -954,9 +980,15 @@ __global__ void __launch_bounds__(256) sage_dec_prep(RefArgs a, DPrepGeom g, uin
 #pragma unroll
         for (uint32_t u = 0; u < DPREP_U; u++) {
             const uint32_t row = r0 + u * step;
-            if (lane_ok && row < kj)
+            if (lane_ok && row < kj && row != prow)
 #pragma unroll
                 for (int e = 0; e < 4; e++) tile[(4 * q + e) * kjp + row] = r[u][e];
+        }
+        if (prow != 0xffffffffu && tid < cw) {
+            // this workgroup's channels of the new v row (no rotation)
+            const float x = rp.qkv[(size_t)(rp.H + a.Hk + bk) * a.dv + 4 * c4_0 + tid];
+            tile[tid * kjp + prow] = x;
+            const_cast<float *>(V)[(size_t)prow * a.v_tok + tid] = x;
         }
         __syncthreads();
         uint32_t *vrow = a.vhat + ((size_t)bk * a.pnkb + kb) * a.dv * a.blk4;
@@ -1859,7 +1891,7 @@ static void dec_bind(const DecPlan &P, DecArgs &da, void *ws) {
 // workspace's earlier step quantised) and the rest are quantised again.
 static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, const float *v,
                       size_t block, float *out, void *ws, size_t cap, size_t cached, hipStream_t st,
-                      const DecOpSink *sink = nullptr) {
+                      const DecOpSink *sink = nullptr, const DecRope *rope = nullptr) {
     DecPlan P = dec_plan(s, block, cap);
     DecArgs da = P.da;
     RefArgs &a = da.r;
@@ -1879,11 +1911,14 @@ static int run_decode(const qbk_attn_shape *s, const float *q, const float *k, c
     const DPrepGeom g = dprep_geom(a, k, v);
     const size_t G = a.H / a.Hk, kjm = a.block < a.S ? a.block : a.S;
     const bool grouped = g.ok && G <= DEC_GMAX && kjm <= DEC_KMAX && a.d % 16 == 0 && a.blk4 % 4 == 0;
+    if (rope && !grouped)
+        return fail(QBK_ERR_VALIDATION, "sage decode: the RoPE fold needs the grouped decode kernels");
     if (g.ok && (a.kb0 < a.nkb || grouped)) {
         const unsigned nx = (unsigned)(a.kb0 < a.nkb ? a.nkb - a.kb0 : 1);
+        const size_t lds = rope && g.lds < 16 * a.d ? 16 * a.d : g.lds;  // the query's rotated heads
         hipLaunchKernelGGL(sage_dec_prep, dim3(nx, (unsigned)a.Hk, g.ks + g.vs + (grouped ? 1 : 0)),
-                           dim3(256), g.lds, st, a, g, grouped ? da.qsw : nullptr, grouped ? da.qdl : nullptr,
-                           kNoSeqs);
+                           dim3(256), lds, st, a, g, grouped ? da.qsw : nullptr, grouped ? da.qdl : nullptr,
+                           kNoSeqs, rope ? *rope : DecRope{});
         QBK_HIP(hipGetLastError());
     } else if (a.kb0 < a.nkb) {
         hipLaunchKernelGGL(sage_ref_prep, dim3((unsigned)(a.nkb - a.kb0), (unsigned)a.Hk), dim3(256),
@@ -1942,12 +1977,13 @@ bool sage_decode_batchable(const qbk_attn_shape *one, size_t block, size_t cap, 
 int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride, const float *k, const float *v,
                       size_t kv_stride, size_t block, float *out, size_t o_stride, void *state, size_t st_stride,
                       size_t cap, const size_t *seq_kv, const size_t *cached, size_t n, hipStream_t st,
-                      const uint32_t *pos_dev, const DecOpSink *sink) {
+                      const uint32_t *pos_dev, const DecOpSink *sink, const DecRope *rope) {
     DecPlan P;
     DPrepGeom g;
     if (n == 0 || n > QBK_DEC_MAXSEQ || !dec_batch_plan(one, block, cap, k, v, kv_stride, P, g))
         return fail(QBK_ERR_VALIDATION, "sage decode: no batched form for this shape");
-    if (sink && n != 1) return fail(QBK_ERR_VALIDATION, "sage decode: an operand sink serves one sequence");
+    if ((sink || rope) && n != 1)
+        return fail(QBK_ERR_VALIDATION, "sage decode: an operand sink or a RoPE fold serves one sequence");
     DecArgs da = P.da;
     RefArgs &a = da.r;
     a.q = q;
@@ -1986,8 +2022,9 @@ int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride
         const DPrepGeom g1 = dprep_geom(a, k, v, 1, 1);
         if (g1.ok) g = g1;
     }
-    hipLaunchKernelGGL(sage_dec_prep, dim3((unsigned)mx, Hk * ns, g.ks + g.vs + 1), dim3(256), g.lds, st, a,
-                       g, da.qsw, da.qdl, t);
+    const size_t lds = rope && g.lds < 16 * a.d ? 16 * a.d : g.lds;  // the query's rotated heads
+    hipLaunchKernelGGL(sage_dec_prep, dim3((unsigned)mx, Hk * ns, g.ks + g.vs + 1), dim3(256), lds, st, a, g,
+                       da.qsw, da.qdl, t, rope ? *rope : DecRope{});
     QBK_HIP(hipGetLastError());
     dec_launch_scores(dim3((unsigned)mkb, Hk, ns), da, t, st);
     QBK_HIP(hipGetLastError());
@@ -2689,7 +2726,8 @@ int qbk_attention_sage_decode_step_dev(qbk_ctx *ctx, const qbk_attn_shape *shape
 
 int qbk::sage_decode_step_sink(qbk_ctx *ctx, const qbk_attn_shape *shape, const float *q, const float *k,
                                const float *v, size_t block_size, float *out, void *state, size_t state_size,
-                               size_t capacity, size_t cached_tokens, const DecOpSink *sink, void *stream) {
+                               size_t capacity, size_t cached_tokens, const DecOpSink *sink, void *stream,
+                               const DecRope *rope) {
     int rc;
     if ((rc = validate_decode(shape, block_size, nullptr))) return rc;
     if (shape->seq_kv > capacity)
@@ -2709,7 +2747,8 @@ int qbk::sage_decode_step_sink(qbk_ctx *ctx, const qbk_attn_shape *shape, const 
     if ((rc = bind(ctx))) return rc;
     if (sink && (shape->val_dim % 128 != 0 || !sink->s2 || !sink->op || !sink->sc))
         return fail(QBK_ERR_VALIDATION, "an operand sink needs val_dim a multiple of 128 and its three buffers");
-    return run_decode(shape, q, k, v, block_size, out, state, capacity, cached_tokens, (hipStream_t)stream, sink);
+    return run_decode(shape, q, k, v, block_size, out, state, capacity, cached_tokens, (hipStream_t)stream, sink,
+                      rope);
 }
 
 extern "C" {
