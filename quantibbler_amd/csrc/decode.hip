@@ -484,20 +484,15 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
             __builtin_amdgcn_wave_barrier();
         }
         const uint8_t *gbs = gb + sb * 4 * ncol * 32, *gss = gs + sb * 4 * ncol;
+        // one form for whole and partial steps (a uniform branch per slice): a
+        // second, unguarded copy of the step kept its own accumulator
+        // registers -- 122 VGPRs a wave against 94 at batch 1 (four waves a
+        // SIMD instead of five), 256 against 140-238 for column groups
         if (NCG > 1) {
-            if (nsl == Q4_U) {
 #pragma unroll
-                for (int u = 0; u < Q4_U; u++) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
-            } else {
-#pragma unroll
-                for (int u = 0; u < Q4_U; u++)
-                    if (u < (int)nsl) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
-            }
+            for (int u = 0; u < Q4_U; u++)
+                if (u < (int)nsl) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
         } else {
-            // one form for whole and partial steps (a uniform branch per
-            // slice): a second, unguarded copy of the step kept its own
-            // accumulator registers, 122 VGPRs a wave against 94 -- four
-            // waves a SIMD instead of five
 #pragma unroll
             for (int u = 0; u < Q4_U; u++)
                 if (u < (int)nsl)
