@@ -374,8 +374,11 @@ __host__ __device__ constexpr uint32_t q4_wave_lds(int ncol) {
 // lanes read the operand of each slice from global memory (L2).
 //
 // Loads are unconditional (indices clamped into the layer; the MFMAs of
-// clamped slices are skipped) so that the compiler's wait counts stay exact:
-// each slice's MFMAs start as soon as its own load lands.
+// clamped slices are skipped) so that the compiler's wait counts stay
+// counted ones: a slice's MFMAs wait for the loads issued up to its own, not
+// for every load in flight (at batch 1-2 the compiler issues the operand's
+// loads behind six of the sign loads, so the first MFMA of a step waits for
+// those six).
 //
 // XCD-aware 1-D grid: workgroup i runs on XCD i % 8; XCD x takes the
 // contiguous range [x*per_x, (x+1)*per_x) of the (layer, row group) work, so
