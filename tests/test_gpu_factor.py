@@ -72,8 +72,6 @@ SHAPES = [(256, 512, 128), (300, 200, 37), (1024, 4096, 1102), (4096, 4096, 1024
 @pytest.mark.parametrize("dout,din,r", SHAPES)
 @pytest.mark.parametrize("batch", [1, 2, 8, 9, 16, 32, 33, 128])
 def test_integer_exact_bit_identical(ctx, orc, dout, din, r, batch):
-    if dout * r > 2_000_000 and batch not in (1, 8, 16, 128):
-        pytest.skip("covered by the smaller shapes")
     integer_exact_case(ctx, orc, dout, din, r, batch)
 
 
