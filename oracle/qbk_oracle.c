@@ -3,7 +3,8 @@
  *
  * TEST INFRASTRUCTURE ONLY (the checker, never the thing measured or shipped).
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
- * it.  Build: oracle/Makefile (gcc -O2 -ffp-contract=off -fopenmp).
+ * it.  Build: oracle/Makefile (gcc -O3 -march=x86-64-v3 -ffp-contract=off
+ * -fno-fast-math -fopenmp).
  *
  * Pinning (see tests/test_oracle_*.py):
  *   pack/unpack/validate   pack_bits.json, closed-form byte positions
@@ -17,9 +18,18 @@
  *   attention (exact)      attention_tiled.json, dense softmax closed form
  *   attention (sage, f64)  attention_sage.json quantized-reference.out
  *   attention (sage, f32)  attention_sage.json within the device gate (1e-4)
- *   block-scaled sage      parity with the reference UNPINNED (no reference
- *                          implementation exists); pinned by exact-attention
- *                          quality and by its quantizer invariants.
+ *   block-scaled sage      no reference implementation exists (the scheme
+ *                          is north_star's); pinned by what the mathematics
+ *                          fixes: Q's scale over exactly each 64-token
+ *                          window with RNE codes, identical keys giving the
+ *                          mean of V, a one-hot softmax giving that V row,
+ *                          fp16 P with an f32 row sum on two keys; plus
+ *                          exact-attention quality and the quantizer
+ *                          invariants
+ *   decoder block, trunk   the reference's parity-tiny HF goldens (logits of
+ *                          a 2-layer model, 1e-2 budget), planted composition
+ *                          mistakes that must fail them, RoPE / RMSNorm
+ *                          closed forms, a dense f64 block step
  */
 #include "qbk_oracle.h"
 
