@@ -387,73 +387,6 @@ def head_logits(head, hidden, threads=0):
     return out[0] if one else out
 
 
-# ---- one decoder block at one position (engine/mod.rs:878-945) --------------
-
-def rms_norm_bf16(x, w, eps) -> np.ndarray:
-    """engine/mod.rs:837-852 norm_apply at bf16 serving over rms_norm_into
-    (:1154-1166): the operand rounded to bf16, its sum of squares taken
-    sequentially in f32, / len, inv = 1 / sqrt(ss + eps) in f32, out =
-    v * inv * w, rounded to bf16."""
-    xb = bf16_to_f32(f32_to_bf16_fast(np.asarray(x, np.float32)))
-    ss = np.float32(0.0)
-    for v in xb:
-        ss = np.float32(ss + np.float32(v * v))
-    ss = np.float32(ss / np.float32(len(xb)))
-    inv = np.float32(np.float32(1.0) / np.sqrt(np.float32(ss + np.float32(eps))))
-    out = (xb * inv).astype(np.float32) * np.asarray(w, np.float32)
-    return bf16_to_f32(f32_to_bf16_fast(out.astype(np.float32)))
-
-
-def rope_rotate(v, head_dim, pos, theta) -> np.ndarray:
-    """engine/mod.rs:1169-1187: rotate_half pairs (i, i + hd/2) of every head
-    by pos * theta^(-2i/hd), the angle's sin and cos in f64, applied in f32."""
-    import math
-
-    v = np.array(v, np.float32)
-    half = head_dim // 2
-    for base in range(0, len(v), head_dim):
-        for i in range(half):
-            inv_freq = math.pow(theta, -(2.0 * i) / head_dim)
-            ang = pos * inv_freq
-            s, c = np.float32(math.sin(ang)), np.float32(math.cos(ang))
-            a, b = v[base + i], v[base + half + i]
-            v[base + i] = np.float32(np.float32(a * c) - np.float32(b * s))
-            v[base + half + i] = np.float32(np.float32(b * c) + np.float32(a * s))
-    return v
-
-
-def block_decode(layers, w_in, w_post, h, pos, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
-                 theta, eps, block) -> np.ndarray:
-    """engine/mod.rs:878-945, one block at position pos, bf16 serving and the
-    sage decode attention (the padded call of :984-1030, row 0).  layers: the
-    seven dicts q, k, v, o, gate, up, down with dout, din, r, ub, vt, s1, s2,
-    bias; k_cache / v_cache: f32 [capacity][n_kv_heads * head_dim], row pos
-    written here.  Returns the block's output h."""
-    def proj(L, x):
-        return factor_apply("bf16", L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
-                            L["bias"], x)
-
-    q_l, k_l, v_l, o_l, g_l, u_l, d_l = layers
-    h = np.asarray(h, np.float32)
-    x = rms_norm_bf16(h, w_in, eps)
-    q = rope_rotate(proj(q_l, x), head_dim, pos, theta)
-    k = rope_rotate(proj(k_l, x), head_dim, pos, theta)
-    v = proj(v_l, x)
-    k_cache[pos] = k
-    v_cache[pos] = v
-    seq = pos + 1
-    qp = np.zeros((1, n_heads, seq, head_dim), np.float32)
-    qp[0, :, 0, :] = q.reshape(n_heads, head_dim)
-    kp = np.ascontiguousarray(k_cache[:seq].reshape(seq, n_kv_heads, head_dim).transpose(1, 0, 2))[None]
-    vp = np.ascontiguousarray(v_cache[:seq].reshape(seq, n_kv_heads, head_dim).transpose(1, 0, 2))[None]
-    attn = attention_sage_dev(qp, kp, vp, False, block)[0, :, 0, :].reshape(-1)
-    h1 = (proj(o_l, attn) + h).astype(np.float32)
-    x2 = rms_norm_bf16(h1, w_post, eps)
-    g, u = proj(g_l, x2), proj(u_l, x2)
-    hid = ((g * u).astype(np.float32) / (np.float32(1.0) + np.exp(-g).astype(np.float32))).astype(np.float32)
-    return (proj(d_l, hid) + h1).astype(np.float32)
-
-
 # ---- the transformer trunk (engine/mod.rs:878-945, 763-800) ------------------
 
 def rms_norm_f32(x, w, eps) -> np.ndarray:
@@ -550,22 +483,39 @@ def block_step(layers, norms, h, pos, k_cache, v_cache, n_heads, n_kv_heads, hea
     return (proj(d_l, hid) + h1).astype(np.float32)
 
 
-def block_prefill(layers, norms, h_rows, k_cache, v_cache, n_heads, n_kv_heads, head_dim, theta, eps):
-    """The device block prefill's arithmetic at bf16 serving: every row of
-    engine/mod.rs:886-941 at positions 0 .. n - 1 (norms, apply_bf16
-    projections, q/k norms, RoPE, cache rows), with the attention of the n
-    tokens the block-scaled SageAttention (causal) over their bf16 q, k, v,
-    its output taken as bf16 for the o projection.  Returns the output rows;
-    fills cache rows 0 .. n - 1."""
+def bf16_round(x) -> np.ndarray:
+    """f32 values rounded to bf16 (RNE, half 2.7.1 from_f32) and widened back."""
+    return bf16_to_f32(f32_to_bf16(np.asarray(x, np.float32)))
+
+
+def heads_major(rows, n_heads, head_dim) -> np.ndarray:
+    """Token rows (n, n_heads * head_dim) -> the attention operand (1, n_heads,
+    n, head_dim): head h's slice of row t becomes [0, h, t]
+    (KvCache::head_major, engine/mod.rs:1236-1268)."""
+    rows = np.asarray(rows, np.float32)
+    n = rows.shape[0]
+    return np.ascontiguousarray(rows.reshape(n, n_heads, head_dim).transpose(1, 0, 2))[None]
+
+
+def token_rows(att) -> np.ndarray:
+    """The inverse of heads_major: (n_heads, n, dv) -> (n, n_heads * dv)."""
+    att = np.asarray(att, np.float32)
+    return np.ascontiguousarray(att.transpose(1, 0, 2)).reshape(att.shape[1], -1)
+
+
+def prefill_qkv(layers, norms, h_rows, k_cache, v_cache, head_dim, theta, eps):
+    """The first half of engine/mod.rs:886-921 for every row t of a prefill at
+    bf16 serving, position t: input norm, the q/k/v projections (apply_bf16),
+    per-head q/k norms when the block has them, RoPE at position t, cache rows
+    t written.  Returns the q, k, v rows (n, width) f32."""
     def proj(L, x):
         return factor_apply("bf16", L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
                             L["bias"], x)
 
-    q_l, k_l, v_l, o_l, g_l, u_l, d_l = layers
+    q_l, k_l, v_l = layers[:3]
     h_rows = np.asarray(h_rows, np.float32)
-    n = h_rows.shape[0]
     qs, ks, vs = [], [], []
-    for t in range(n):
+    for t in range(h_rows.shape[0]):
         x = norm_apply(h_rows[t], norms["input"], eps, "bf16")
         q, k, v = proj(q_l, x), proj(k_l, x), proj(v_l, x)
         if "q_norm" in norms and "k_norm" in norms:
@@ -576,18 +526,52 @@ def block_prefill(layers, norms, h_rows, k_cache, v_cache, n_heads, n_kv_heads, 
         qs.append(q)
         ks.append(k)
         vs.append(v)
-    qb = f32_to_bf16(np.stack(qs).reshape(n, n_heads, head_dim).transpose(1, 0, 2)[None].copy())
-    kb = f32_to_bf16(np.stack(ks).reshape(n, n_kv_heads, head_dim).transpose(1, 0, 2)[None].copy())
-    vb = f32_to_bf16(np.stack(vs).reshape(n, n_kv_heads, head_dim).transpose(1, 0, 2)[None].copy())
+    return np.stack(qs), np.stack(ks), np.stack(vs)
+
+
+def prefill_attention(q_rows, k_rows, v_rows, n_heads, n_kv_heads, head_dim):
+    """The prefill's attention (the step of engine/mod.rs:922-925 for every
+    row at once): the rows' bf16 q, k, v taken head-major, the causal
+    block-scaled SageAttention over the n tokens, the heads back to token rows
+    and rounded to bf16 -- the o projection's operand, as the device stores
+    it.  Returns (n, n_heads * head_dim) f32 holding bf16 values."""
+    qb = f32_to_bf16(heads_major(q_rows, n_heads, head_dim))
+    kb = f32_to_bf16(heads_major(k_rows, n_kv_heads, head_dim))
+    vb = f32_to_bf16(heads_major(v_rows, n_kv_heads, head_dim))
     att = attention_sage_blk(qb, kb, vb, causal=True)[0]                        # (H, n, hd) f32
-    att = bf16_to_f32(f32_to_bf16(att.transpose(1, 0, 2).reshape(n, -1).copy()))
+    return bf16_round(token_rows(att))
+
+
+def prefill_mlp(layers, norms, h_rows, att_rows, eps):
+    """The second half of engine/mod.rs:922-941 for every row: o projection +
+    residual, post-attention norm, gate/up, SwiGLU, down + residual, at bf16
+    serving.  Returns the block's output rows."""
+    def proj(L, x):
+        return factor_apply("bf16", L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                            L["bias"], x)
+
+    o_l, g_l, u_l, d_l = layers[3:]
+    h_rows = np.asarray(h_rows, np.float32)
     out = np.zeros_like(h_rows)
-    for t in range(n):
-        h1 = (proj(o_l, att[t]) + h_rows[t]).astype(np.float32)
+    for t in range(h_rows.shape[0]):
+        h1 = (proj(o_l, att_rows[t]) + h_rows[t]).astype(np.float32)
         x2 = norm_apply(h1, norms["post_attention"], eps, "bf16")
         hid = swiglu(proj(g_l, x2), proj(u_l, x2))
         out[t] = (proj(d_l, hid) + h1).astype(np.float32)
     return out
+
+
+def block_prefill(layers, norms, h_rows, k_cache, v_cache, n_heads, n_kv_heads, head_dim, theta, eps):
+    """The device block prefill's arithmetic at bf16 serving: every row of
+    engine/mod.rs:886-941 at positions 0 .. n - 1 (prefill_qkv), with the
+    attention of the n tokens the causal block-scaled SageAttention over their
+    bf16 q, k, v (prefill_attention), then the MLP half (prefill_mlp).  The
+    reference prefills by running this block token by token
+    (engine/mod.rs:1399-1402); the cache rows are the ones block_step writes.
+    Returns the output rows; fills cache rows 0 .. n - 1."""
+    q, k, v = prefill_qkv(layers, norms, h_rows, k_cache, v_cache, head_dim, theta, eps)
+    att = prefill_attention(q, k, v, n_heads, n_kv_heads, head_dim)
+    return prefill_mlp(layers, norms, h_rows, att, eps)
 
 
 class Trunk:
@@ -599,7 +583,7 @@ class Trunk:
 
     def __init__(self, md, serving="fp32", attention="scalar", capacity=None, block=64):
         self.md, self.serving, self.attention, self.block = md, serving, attention, block
-        q = (lambda a: bf16_to_f32(f32_to_bf16(np.asarray(a, np.float32)))) if serving == "bf16" else \
+        q = bf16_round if serving == "bf16" else \
             (lambda a: np.asarray(a, np.float32))
         self.embedding = q(md.embedding)
         self.head = q(md.head_rows())
