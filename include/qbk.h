@@ -92,7 +92,10 @@ int qbk_gpu_available(void);
 /* gpu.rs:116-185 GpuContext::packed_matvec generalised to the three dtypes of
  * dispatch.rs:81-92 packed_matvec_dyn.  out[i] = sum_k s(i,k) vec[k] in the
  * dtype's accumulator (f64, f32, f32 for bf16), summed in element order, so
- * results are bit-identical to core::packed_matvec. */
+ * results are bit-identical to core::packed_matvec.  At f64 (the reference's
+ * device face) a shape past the u32 index ceiling, n_rows * ceil(n_bits/8) or
+ * n_rows above 4294967295, is refused with gpu.rs:127-137's text before any
+ * device use. */
 int qbk_packed_matvec(qbk_ctx *ctx, int dtype, const uint8_t *packed, size_t packed_len,
                       size_t n_rows, size_t n_bits, const void *vec, size_t vec_len, void *out);
 /* dispatch.rs:95-109 packed_matmul_dyn / core.rs:288-317: output n_rows x k,

@@ -159,6 +159,14 @@ int qbk_packed_matvec(qbk_ctx *ctx, int dtype, const uint8_t *packed, size_t pac
     if (vec_len != n_bits)
         return fail(QBK_ERR_VALIDATION,
                     fmt("vec must have length %zu, got %zu", n_bits, vec_len));
+    // gpu.rs:127-137: the f64 device face's u32 index ceiling, after the
+    // shape checks and before any device use (checked without overflow:
+    // n_rows * w == packed_len already holds)
+    const size_t ceiling = 0xFFFFFFFFull;
+    if (dtype == QBK_F64 && (packed_len > ceiling || n_rows > ceiling))
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("packed shape %zu x %zu words exceeds the device u32 index ceiling (%zu); "
+                        "use the CPU rlib face", n_rows, w, ceiling));
     size_t es = dtype_size(dtype);
     if (n_rows == 0) return QBK_OK;
     if (n_bits == 0) {  // zero logical bits: every row's sum is empty

@@ -116,17 +116,11 @@ class GpuContext:
         code, npdt = _DTYPES[dtype]
         p = np.ascontiguousarray(packed, dtype=np.uint8).ravel()
         v = np.ascontiguousarray(vec, dtype=npdt).ravel()
-        if dtype == "float64":
-            # gpu.rs:116-137: after the shape and length checks, the reference
-            # device face's u32 index ceiling
-            nw = C.c_size_t()
-            check(_lib.load().qbk_validate_packed(p.size, int(n_rows), int(n_bits), C.byref(nw)))
-            if v.size != int(n_bits):
-                raise _lib.KernelError(f"vec must have length {n_bits}, got {v.size}")
-            if int(n_rows) * nw.value > 0xFFFFFFFF or int(n_rows) > 0xFFFFFFFF:
-                raise _lib.KernelError(f"packed shape {n_rows} x {nw.value} words exceeds the device u32 index "
-                                       f"ceiling (4294967295); use the CPU rlib face")
-        out = np.zeros(n_rows, dtype=npdt)
+        # the library refuses f64 shapes past the reference device face's u32
+        # index ceiling (gpu.rs:127-137) before any device use or write to out,
+        # so such a call is made without an output buffer
+        big = dtype == "float64" and max(p.size, int(n_rows)) > 0xFFFFFFFF
+        out = None if big else np.zeros(n_rows, dtype=npdt)
         check(_lib.load().qbk_packed_matvec(self._h, code, _ptr(p), p.size, n_rows, n_bits,
                                             _ptr(v), v.size, _ptr(out)))
         return out

@@ -97,6 +97,30 @@ def test_validation_precedes_device_use(lib):
         check(lib.qbk_attention_sage(None, C.byref(sh), None, 63, None, 32, None, 32, 1, 4, None))
 
 
+def test_packed_matvec_ceiling_precedes_device_use(lib):
+    # gpu.rs:116-137: after validate_packed and the vec length check, the f64
+    # device face refuses n_rows x words past the u32 index ceiling -- before
+    # any device use, so no context is needed and nothing is read
+    from quantibbler_amd import KernelError
+    from quantibbler_amd._lib import check
+
+    vec = (C.c_double * 8)()
+    rows = 1 << 32                      # 2^32 rows x 1 word: lengths match, past the ceiling
+    with pytest.raises(KernelError, match=r"^packed shape 4294967296 x 1 words exceeds the device u32 index "
+                                          r"ceiling \(4294967295\); use the CPU rlib face$"):
+        check(lib.qbk_packed_matvec(None, 0, None, rows, rows, 8, vec, 8, None))
+    rows = (1 << 30) + 1                # 2^30 + 1 rows x 4 words: the product passes it
+    with pytest.raises(KernelError, match=r"^packed shape 1073741825 x 4 words exceeds the device u32"):
+        check(lib.qbk_packed_matvec(None, 0, None, 4 * rows, rows, 32, (C.c_double * 32)(), 32, None))
+    # the shape checks come first, with their own texts
+    with pytest.raises(KernelError, match=r"^packed length 5 does not match 4294967296 rows x 1 bitplanes$"):
+        check(lib.qbk_packed_matvec(None, 0, None, 5, 1 << 32, 8, vec, 8, None))
+    with pytest.raises(KernelError, match=r"^vec must have length 8, got 7$"):
+        check(lib.qbk_packed_matvec(None, 0, None, 1 << 32, 1 << 32, 8, vec, 7, None))
+    # the ceiling is the f64 device face's: f32 / bf16 (core.rs's faces) have none,
+    # so at this shape they go on to the device (not called here)
+
+
 def test_exact_attention_validation_and_ceiling_precede_device_use(lib):
     # gpu_attention.rs:466-509: the exact face's messages, then its u32
     # index ceiling -- both before any device is touched
