@@ -249,9 +249,15 @@ size_t qbk_block_prefill_workspace_size(const qbk_block *block, size_t n_tokens)
 int qbk_block_prefill_dev(qbk_ctx *ctx, qbk_block *block, float *h, size_t n_tokens, void *workspace,
                           size_t workspace_size, void *stream);
 /* The block's KV cache (device, f32 [n_seqs][capacity][n_kv_heads * head_dim]
- * each; sequence 0 first).  Rows written through these pointers are not seen
- * by the attention state until qbk_block_reset. */
+ * each; sequence 0 first).  After writing rows 0 .. rows[i] - 1 of sequence i
+ * through these pointers, qbk_block_set_filled declares them: decoding then
+ * continues at position rows[i], and the attention state rebuilds its codes
+ * from the cache on that step (as after a prefill). */
 int qbk_block_cache(const qbk_block *block, float **k_cache, float **v_cache);
+/* Sequences 0 .. n - 1 hold rows[i] cache rows written by the caller; their
+ * attention state covers none of them yet.  No counterpart in the reference
+ * (its KvCache is filled only by its own steps, engine/mod.rs:1224-1268). */
+int qbk_block_set_filled(qbk_block *block, const size_t *rows, size_t n);
 
 /* Batched serving (engine/mod.rs:1377-1476 steps a batch of sequences through
  * the trunk; each sequence keeps its own cache): a block holding n_seqs
@@ -286,9 +292,11 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *block, float *h, const s
  * writes (as qbk_block_decode_dev's pos).  The attention steps a kept state
  * that must hold every complete key block before that position -- as after
  * an eager step at pos - 1 -- and keeps the same arithmetic, so each step is
- * bit-identical to the eager step at that position.  A position at or past
- * the capacity skips the cache and attention (the step's output is then
- * undefined).  Needs the grouped decode attention (head_dim a multiple of
+ * bit-identical to the eager step at that position; a state that does not
+ * cover the cached rows (right after a prefill or qbk_block_set_filled) is a
+ * validation error.  A position at or past the capacity skips the cache and
+ * attention (the attention output is then 0 and the step's output has no
+ * meaning).  Needs the grouped decode attention (head_dim a multiple of
  * 16, up to 16 query heads a kv head, key blocks of up to 64 tokens; a
  * validation error otherwise).  These steps do not update the block's host
  * record of cached positions: qbk_block_set_positions sets it (sequence i

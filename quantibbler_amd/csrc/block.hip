@@ -755,8 +755,27 @@ int qbk_block_decode_dev(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, void 
     return block_decode_one(ctx, B, h, pos, nullptr, stream);
 }
 
+}  // extern "C"
+
+// A device-position step reads the kept attention state for every complete
+// key block before its position, so each sequence's state must cover the
+// cached rows -- not so after a prefill or qbk_block_set_filled, whose state
+// is rebuilt by the next eager step.
+static int pos_state_ready(const qbk_block *B, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        if (B->tokens[i] < B->filled[i])
+            return fail(QBK_ERR_VALIDATION,
+                        fmt("sequence %zu: the attention state covers %zu of its %zu cached positions; a "
+                            "device-position step needs an eager step first", i, B->tokens[i], B->filled[i]));
+    return QBK_OK;
+}
+
+extern "C" {
+
 int qbk_block_decode_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const uint32_t *pos, void *stream) {
-    if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (!pos || !B) return fail(QBK_ERR_VALIDATION, "null argument");
+    int rc;
+    if ((rc = pos_state_ready(B, 1))) return rc;
     return block_decode_one(ctx, B, h, 0, pos, stream);
 }
 
@@ -769,6 +788,21 @@ int qbk_block_set_positions(qbk_block *B, const size_t *pos, size_t n) {
             return fail(QBK_ERR_VALIDATION,
                         fmt("sequence %zu: %zu positions exceed the block's cache capacity of %zu", i, pos[i], B->cap));
     for (size_t i = 0; i < n; i++) B->tokens[i] = B->filled[i] = pos[i];
+    return QBK_OK;
+}
+
+int qbk_block_set_filled(qbk_block *B, const size_t *rows, size_t n) {
+    if (!B || !rows) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (n == 0 || n > B->nseq)
+        return fail(QBK_ERR_VALIDATION, fmt("%zu sequences on a block holding %zu", n, B->nseq));
+    for (size_t i = 0; i < n; i++)
+        if (rows[i] > B->cap)
+            return fail(QBK_ERR_VALIDATION,
+                        fmt("sequence %zu: %zu rows exceed the block's cache capacity of %zu", i, rows[i], B->cap));
+    for (size_t i = 0; i < n; i++) {
+        B->filled[i] = rows[i];
+        B->tokens[i] = 0;  // the attention state rebuilds its codes from the cache
+    }
     return QBK_OK;
 }
 
@@ -972,6 +1006,8 @@ int qbk_block_decode_batch_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const u
                                    void *workspace, size_t workspace_size, void *stream) {
     if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
     if (B && n && n <= B->nseq) {
+        int rc;
+        if ((rc = pos_state_ready(B, n))) return rc;
         const qbk_attn_shape one{1, B->H, B->Hk, 1, B->cap, B->hd, B->hd};
         if (!sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, B->cap * B->Hk * B->hd))
             return fail(QBK_ERR_VALIDATION, "a device-position step needs the grouped sage decode kernels "

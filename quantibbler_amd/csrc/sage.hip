@@ -1377,7 +1377,8 @@ __global__ void __launch_bounds__(256) sage_dec_combine(DecArgs da, DecSeqTab t)
             }
         }
     }
-    const float val = act ? o / ell : 0.0f;
+    // no key block (a device position at or past the capacity): 0, not 0/0
+    const float val = act && nkb ? o / ell : 0.0f;
     if (act) a.out[(size_t)h * dv + c] = val;
     if (da.op) {
         // the output as the next layer's operand: a run of 16 channels a

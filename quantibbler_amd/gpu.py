@@ -428,6 +428,12 @@ class DecoderBlock:
         p = np.ascontiguousarray(positions, np.uint64).ravel()
         check(_lib.load().qbk_block_set_positions(self._h, _ptr(p), p.size))
 
+    def set_filled(self, rows):
+        """Sequence i holds rows[i] cache rows written through cache_ptrs();
+        its attention state is rebuilt from them on the next eager step."""
+        p = np.ascontiguousarray(rows, np.uint64).ravel()
+        check(_lib.load().qbk_block_set_filled(self._h, _ptr(p), p.size))
+
     @staticmethod
     def _check_pos(pos, n: int):
         if hasattr(pos, "is_cuda"):

@@ -166,6 +166,7 @@ extern "C" {
                                           n: usize, workspace: *mut c_void, workspace_size: usize,
                                           stream: *mut c_void) -> c_int;
     pub fn qbk_block_set_positions(block: *mut QbkBlock, pos: *const usize, n: usize) -> c_int;
+    pub fn qbk_block_set_filled(block: *mut QbkBlock, rows: *const usize, n: usize) -> c_int;
     pub fn qbk_embed(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32, n: usize,
                      out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_embed_dev(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32,

@@ -343,3 +343,74 @@ def test_block_batched_decode_many_sequences(ctx, orc):
             assert cos >= COS_MIN and rel <= REL_MAX, (step, s, pos[s], cos, rel)
         say(f"step {step}: worst cos {worst[0]:.7f} rel {worst[1]:.2e}")
         pos = [p + 1 for p in pos]
+
+
+def test_block_cache_written_by_the_caller(ctx, orc):
+    """Cache rows written through qbk_block_cache and declared with
+    qbk_block_set_filled: decoding continues at that position, the attention
+    state rebuilt from the cache, bit-identical to a twin block that filled
+    the same rows with its own prefill.  A device-position step is refused
+    until an eager step has rebuilt the state (after the prefill as after
+    set_filled), and accepted after it."""
+    from quantibbler_amd import DecoderBlock, FactorLayer, KernelError
+
+    d, H, Hk, hd, ffn, cap, blk = 256, 4, 2, 128, 512, 200, 64
+    n = 70
+    rng = np.random.default_rng(4711)
+    shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
+              (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    w_in = orc.bf16_round(1.0 + 0.1 * rng.standard_normal(d))
+    w_post = orc.bf16_round(1.0 + 0.1 * rng.standard_normal(d))
+    mk = lambda: DecoderBlock(ctx, devs, w_in, w_post, H, Hk, hd, 5e5, 1e-5, cap, blk)
+    twin, ext = mk(), mk()
+    st = torch.cuda.current_stream()
+    say("caller-written cache: prefill the twin,", n, "tokens")
+    h = torch.from_numpy(rng.standard_normal((n, d)).astype(np.float32)).cuda()
+    wn = twin.prefill_workspace_size(n)
+    ws = torch.empty(wn, dtype=torch.uint8, device="cuda")
+    twin.prefill_dev(h, n, ws, wn, st)
+    pos_dev = torch.tensor([n], dtype=torch.int32, device="cuda")
+    x = torch.zeros(d, dtype=torch.float32, device="cuda")
+    with pytest.raises(KernelError, match="sequence 0: the attention state covers 0 of its 70 cached positions; "
+                                          "a device-position step needs an eager step first"):
+        twin.decode_pos_dev(x, pos_dev, st)
+    # copy the twin's cache rows into the other block through the pointers
+    def rows(ptr):
+        # a torch view of the block's cache memory (the first n rows)
+        sto = torch._C._construct_storage_from_data_pointer(ptr, torch.device("cuda", 0), n * Hk * hd * 4)
+        return torch.empty(0, dtype=torch.float32, device="cuda").set_(sto, 0, (n, Hk * hd), (Hk * hd, 1))
+
+    kt, vt = twin.cache_ptrs()
+    ke, ve = ext.cache_ptrs()
+    for src, dst in ((kt, ke), (vt, ve)):
+        rows(dst).copy_(rows(src))
+    torch.cuda.synchronize()
+    with pytest.raises(KernelError, match=f"position {n} skips cache rows: the block holds 0 positions"):
+        ext.decode_dev(x, n, st)
+    ext.set_filled([n])
+    with pytest.raises(KernelError, match="the attention state covers 0 of its 70 cached positions"):
+        ext.decode_pos_dev(x, pos_dev, st)
+    with pytest.raises(KernelError, match="201 rows exceed the block's cache capacity of 200"):
+        ext.set_filled([cap + 1])
+    for pos in range(n, n + 3):
+        xin = rng.standard_normal(d).astype(np.float32)
+        a = torch.from_numpy(xin).cuda()
+        b = a.clone()
+        twin.decode_dev(a, pos, st)
+        ext.decode_dev(b, pos, st)
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(a).all())
+        assert torch.equal(a, b), f"position {pos}: caller-written cache differs from the twin's prefill"
+    # the states now cover the cache: a device-position step is accepted
+    pos_dev.fill_(n + 3)
+    a = torch.from_numpy(rng.standard_normal(d).astype(np.float32)).cuda()
+    b = a.clone()
+    twin.decode_pos_dev(a, pos_dev, st)
+    ext.decode_dev(b, n + 3, st)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    twin.close()
+    ext.close()

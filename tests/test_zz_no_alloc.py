@@ -2,7 +2,8 @@
 qbk_factor_linear_dev on the same layer and inputs: bit-identical outputs on
 two calls in a row, the second with a smaller input (its scratch array keeps
 the first call's contents), for the decode GEMV (batch <= 8) and the prefill
-GEMM; and the refusal of a call whose workspace exceeds the array."""
+GEMM; the call captured in a HIP graph and replayed with new inputs; and
+the refusal of a call whose workspace exceeds the array."""
 import numpy as np
 import pytest
 
@@ -82,4 +83,34 @@ def test_no_alloc_refuses_beyond_its_array(ctx, orc):
     y = torch.empty((batch, 4096), dtype=torch.float32, device="cuda")
     with pytest.raises(KernelError, match="the no-allocation entry point holds 33554432"):
         layer.linear_noalloc_dev(x, batch, y, "float32", torch.cuda.current_stream())
+    layer.close()
+
+
+@pytest.mark.parametrize("dout,din,r,batch", [(1024, 4096, 1102, 1), (512, 1024, 200, 300)])
+def test_no_alloc_under_graph_capture(ctx, orc, dout, din, r, batch):
+    """The no-allocation call captured in a HIP graph (torch's graph API) after
+    one eager call on the device (the scratch address is looked up there),
+    then replayed with new inputs written into the captured input buffer:
+    every replay bit-identical to qbk_factor_linear_dev on the same input,
+    with eager work and synchronisations between the replays."""
+    say("no-alloc factor linear under graph capture", dout, din, r, batch)
+    rng = np.random.default_rng(dout + batch + 1)
+    layer = _layer(ctx, orc, rng, dout, din, r)
+    x = torch.zeros((batch, din), dtype=torch.int16, device="cuda")
+    y = torch.zeros((batch, dout), dtype=torch.float32, device="cuda")
+    layer.linear_noalloc_dev(x, batch, y, "float32", torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer.linear_noalloc_dev(x, batch, y, "float32", torch.cuda.current_stream())
+    for rep in range(3):
+        xb = orc.f32_to_bf16_fast(rng.standard_normal((batch, din)).astype(np.float32))
+        x.copy_(torch.from_numpy(xb.view(np.int16)))
+        g.replay()
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        want = _with_workspace(layer, x, "float32")
+        torch.cuda.synchronize()
+        same(got, want.cpu().numpy(), f"replay {rep}")
+    del g
     layer.close()
