@@ -12,10 +12,10 @@ fp8 operand; stage 2, y = bf16(bf16(Ub t)*s1)).
 value = algorithmic bytes of all layers / step time, with config 1's
 per-layer count 1,097,728 B (U 512 KiB + V 512 KiB + x 8 KiB + y 8 KiB + s1,
 s2 32 KiB).  The timed region holds only the steps between two events.  The
-roofline's kernel duration: the dominant kernel's average over the same
-number of steps run again with an event between consecutive launches on the
-launch stream, so each kernel is timed inside the step it belongs to
-(rocprofv3 --kernel-trace --stats of the same command agrees; profiles/).
+roofline's kernel duration: the timed step split by the kernels' shares,
+which the same steps run again with an event between consecutive launches
+measure (rocprofv3 --kernel-trace of the same command gives the kernels'
+in-step durations; profiles/).
 
 Extras (same JSON line): single-layer decode latency; prefill GEMM TFLOP/s at
 B in {16, 128, 512, 2048}; block-scaled SageAttention prefill at
@@ -93,9 +93,9 @@ def make_layers(qa, ctx, np, count, seed):
 def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
     """The timed region: `steps` decodes of the whole set (three launches
     each), bracketed by two events and nothing else.  Then the same steps
-    again with an event between consecutive launches, all on the launch
-    stream, for each kernel's duration inside the step it belongs to (the
-    roofline's denominator: the dominant kernel's average launch)."""
+    again with an event between consecutive launches: each kernel's share of
+    the step, which splits the timed step into the kernels' average
+    durations (the roofline's denominator: the dominant kernel's)."""
     S = qa.FactorSet(ctx, layers)
     L = len(layers)
     rng = np.random.default_rng(7)
@@ -117,7 +117,10 @@ def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / steps
-    # in-step kernel durations: events e0 | prep | e1 | stage 1 | e2 | stage 2 | e3
+    # each kernel's share of the step: the same steps again with an event
+    # between consecutive launches on the launch stream; the shares split the
+    # unperturbed step time above (an event adds a dispatch gap to the kernel
+    # behind it, so the event intervals themselves run a few percent long)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     for i in range(steps):
         ev[i][0].record(st)
@@ -125,8 +128,9 @@ def bench_decode(qa, ctx, torch, np, layers, steps, warmup):
             S.stage_dev(ph, x, y, ws, ws_n, st)
             ev[i][ph].record(st)
     torch.cuda.synchronize()
-    phase_ms = [sum(ev[i][ph - 1].elapsed_time(ev[i][ph]) for i in range(steps)) / steps for ph in range(1, 4)]
-    return dict(ms_per_step=ms_step, phase_ms=phase_ms, wall_s=wall, set=S)
+    evt_ms = [sum(ev[i][ph - 1].elapsed_time(ev[i][ph]) for i in range(steps)) / steps for ph in range(1, 4)]
+    phase_ms = [ms_step * e / sum(evt_ms) for e in evt_ms]
+    return dict(ms_per_step=ms_step, phase_ms=phase_ms, evt_ms=evt_ms, wall_s=wall, set=S)
 
 
 def bench_single_latency(torch, np, layer, iters=200):
@@ -319,6 +323,10 @@ def bench_head(qa, ctx, torch, np, vocab=128256, d=4096, iters=20):
 CFG3 = [("q", 4096, 4096, 1102), ("k", 1024, 4096, 431), ("v", 1024, 4096, 431),
         ("o", 4096, 4096, 1102), ("gate", 14336, 4096, 1724), ("up", 14336, 4096, 1724),
         ("down", 4096, 14336, 1733)]
+# bytes of one decoder layer's seven v2 streams (qpk1 lib.rs:152-210): a
+# 24-byte header, fp16 s1 (dout), s2 (din) and bias (dout), then the two
+# continuous sign bitstreams -- 14,995,624 B
+CFG3_REF_LAYER_BYTES = sum(24 + 2 * (2 * m + n) + (m * r + 7) // 8 + (n * r + 7) // 8 for _, m, n, r in CFG3)
 
 
 def random_rows(np, rng, n_rows, n_bits):
@@ -565,10 +573,14 @@ def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / steps
     total = sign_bytes + act_bytes
-    out = {"decoder_layers": n_layers, "sign_bytes": sign_bytes, "bytes_per_token": total,
-           "ms_per_token": round(ms, 4), "GB/s": round(total / (ms * 1e-3) / 1e9, 1),
-           "frac_hbm_peak": round(total / (ms * 1e-3) / HBM_PEAK, 4),
-           "note": "f32 s1/s2 as stored here; the reference v2 stream (fp16 scales) counts 14,995,624 B per layer"}
+    ref = n_layers * CFG3_REF_LAYER_BYTES
+    out = {"decoder_layers": n_layers, "sign_bytes": sign_bytes, "ref_bytes_per_token": ref,
+           "ms_per_token": round(ms, 4), "GB/s": round(ref / (ms * 1e-3) / 1e9, 1),
+           "frac_hbm_peak": round(ref / (ms * 1e-3) / HBM_PEAK, 4),
+           "bytes_streamed_per_token": total,
+           "bytes_note": "frac and GB/s count the reference's v2 streams (signs + fp16 s1/s2/bias, "
+                         "14,995,624 B a decoder layer); bytes_streamed_per_token is what this "
+                         "build reads (signs, scales as stored, bf16 x and y)"}
     log(f"  cfg3 decode: {ms:.3f} ms/token over {n_layers} layers, {out['GB/s']} GB/s")
     # prefill: one decoder layer's seven projections at B = prefill_b
     flop = 0
@@ -781,8 +793,11 @@ def main():
     achieved = bytes_launch / (dom_ms * 1e-3) / 1e9
     log(f"  decode: {d['ms_per_step']:.3f} ms/step, {value:.1f} GB/s; phases (prep x, gemv 1 + "
         f"t operand, gemv 2) = {', '.join(f'{p:.4f}' for p in ph)} ms")
+    ev = d["evt_ms"]
     extra = {"decode_phase_ms": {"prep_x": round(ph[0], 4), "gemv_stage1": round(ph[1], 4),
-                                 "gemv_stage2": round(ph[2], 4)}}
+                                 "gemv_stage2": round(ph[2], 4)},
+             "decode_phase_event_interval_ms": {"prep_x": round(ev[0], 4), "gemv_stage1": round(ev[1], 4),
+                                                "gemv_stage2": round(ev[2], 4)}}
     if not args.no_extra:
         log("single-layer latency ...")
         extra["decode_single_layer_us"] = round(bench_single_latency(torch, np, layers[0]), 2)
@@ -832,7 +847,10 @@ def main():
             "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
             "kernel": f"q4_gemv_kernel<{dom},*,2> (decode stage {dom}, fp4 x fp8 scaled MFMA)",
             "bytes_per_launch": bytes_launch, "avg_launch_ms": round(dom_ms, 4),
-            "avg_launch_source": "HIP events between consecutive launches inside the timed steps",
+            "avg_launch_source": "the timed step (two HIP events on the launch stream) times the "
+                                 "kernel's share of the step, measured over the same steps run again "
+                                 "with an event between consecutive launches",
+            "event_interval_ms": round(d["evt_ms"][dom - 1], 4),
         },
         "cpu_baseline": cpu,
         "extra": extra,

@@ -39,6 +39,7 @@ CFLAGS = [
 ]
 EXTRA = {
     "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

@@ -389,10 +389,10 @@ __global__ void blkp_add(const float *a, const float *b, float *out, size_t coun
 // A projection of n rows: the decode GEMV up to its batch limit, the GEMM
 // beyond; y f32.
 static size_t blkp_proj_ws(const qbk_factor *L, size_t n) {
-    return n <= Q4_MAXB ? q4_workspace(L, n) : g32_workspace(L, n);
+    return n <= Q4_MAXB ? q4_workspace(L, n) : gemm_workspace(L, n);
 }
 static int blkp_proj(const qbk_factor *L, size_t n, const void *x, bool xf32, float *y, void *ws, hipStream_t s) {
-    return n <= Q4_MAXB ? q4_run(L, n, x, xf32, y, false, ws, s) : g32_run(L, x, xf32, n, y, false, ws, s);
+    return n <= Q4_MAXB ? q4_run(L, n, x, xf32, y, false, ws, s) : gemm_run(L, x, xf32, n, y, false, ws, s);
 }
 
 // Prefill workspace regions (256-byte aligned), for n rows.

@@ -309,7 +309,7 @@ __device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, cons
     const bool valid = row < L.rows_valid;
     for (int bb = 0; bb < (nc >> 1); bb++) {
         const int b = (c0 >> 1) + bb;
-        const float v = (T[(2 * bb) * 64 + lane] + T[(2 * bb + 1) * 64 + lane]) / 1.5f;
+        const float v = q4_unscale(T[(2 * bb) * 64 + lane] + T[(2 * bb + 1) * 64 + lane]);
         const float t = valid ? bf16_to_f32(f32_to_bf16(v)) : 0.0f;
         if (STAGE == 2) {
             if (valid) {

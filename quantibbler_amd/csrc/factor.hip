@@ -192,9 +192,10 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
 // ------------------------------------------------------------------------
 
 // batch <= Q4_MAXB: the fp4 decode's operand buffers (decode.hip).  Larger
-// batches: the prefill GEMM's z, split partials and t (prefill.hip).
+// batches: the fused GEMM's t (gemm.hip), or the two-stage GEMM's z, split
+// partials and t (prefill.hip).
 static size_t ws_bytes(const qbk_factor *L, size_t batch) {
-    return batch <= Q4_MAXB ? q4_workspace(L, batch) : g32_workspace(L, batch);
+    return batch <= Q4_MAXB ? q4_workspace(L, batch) : gemm_workspace(L, batch);
 }
 
 // ---- the no-allocation form of qbk_factor_linear_dev --------------------
@@ -355,7 +356,7 @@ int qbk_factor_linear_dev(qbk_ctx *ctx, const qbk_factor *L, const uint16_t *x, 
                         workspace_size, need));
     hipStream_t s = (hipStream_t)stream;
     if (batch <= Q4_MAXB) return q4_run(L, batch, x, false, y, y_dtype == QBK_BF16, workspace, s);
-    return g32_run(L, x, false, batch, y, y_dtype == QBK_BF16, workspace, s);
+    return gemm_run(L, x, false, batch, y, y_dtype == QBK_BF16, workspace, s);
 }
 
 int qbk_factor_linear_noalloc_dev(qbk_ctx *ctx, const qbk_factor *L, const uint16_t *x, size_t batch, void *y,
@@ -458,7 +459,7 @@ int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *L, int serving, const float
     if (batch <= Q4_MAXB)
         rc = q4_run(L, batch, dx.p, true, dy.p, false, dws.p, cs.s);
     else
-        rc = g32_run(L, dx.p, true, batch, dy.p, false, dws.p, cs.s);
+        rc = gemm_run(L, dx.p, true, batch, dy.p, false, dws.p, cs.s);
     if (rc) return rc;
     QBK_HIP(hipMemcpyAsync(y, dy.p, batch * L->dout * 4, hipMemcpyDeviceToHost, cs.s));
     QBK_HIP(hipStreamSynchronize(cs.s));

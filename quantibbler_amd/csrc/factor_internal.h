@@ -116,6 +116,22 @@ size_t g32_set_workspace(const qbk_factor *const *L, size_t n, size_t N);
 int g32_set_run(const qbk_factor *const *L, size_t n, const G32SetLayer *tab1, const G32SetLayer *tab2, size_t N,
                 const void *x, bool xf32, void *y, bool ybf16, void *ws, hipStream_t s);
 
+// gemm.hip: the prefill GEMM on the fp4 x fp8 MFMA, both stages in one
+// launch over the decode's sign layout, no workspace: x [N][din] (bf16, or
+// f32 when xf32) -> y [N][dout] (bf16 when ybf16, else f32), for layers of
+// rank up to 2048.
+// t_out (null, or [N][r_p] bf16): t as well, zero past r.
+bool q4g_fits(const qbk_factor *L, size_t N);
+int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, uint16_t *t_out,
+            hipStream_t s);
+// The factor linear past the decode GEMV's batches: the fused GEMM where it
+// applies (its workspace: t bf16 [N][r_p], left there), else the two-stage
+// GEMM below; gemm_workspace gives the bytes ws must hold.
+bool q4g_use(const qbk_factor *L, size_t N);
+size_t gemm_workspace(const qbk_factor *L, size_t N);
+int gemm_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
+             hipStream_t s);
+
 // prefill.hip: the sign layout of the prefill GEMM (rows_p a multiple of
 // 128, bits_p of 64), its workspace, and the two-stage GEMM for N tokens:
 // x [N][din] (bf16, or f32 when xf32) -> y [N][dout].

@@ -1,0 +1,555 @@
+// gemm.hip -- the factor linear's prefill GEMM on the fp4 x fp8 scaled MFMA,
+// both stages in one launch.
+//
+//   t = bf16(Vb^T z), z = bf16(s2 * x);  y = bf16(Ub t) * s1 + bias
+//                              (engine/mod.rs:449-460, apply_bf16, per token)
+//
+// The decode GEMV's arithmetic (decode.hip) at any number of tokens: the
+// +-1 signs are the fp4 A operand of v_mfma_scale_f32_16x16x128_f8f6f4, built
+// in registers from the decode's sign layout (four VALU ops per 32 weights);
+// the activations are the B operand, each split exactly into two fp8 e4m3
+// columns (hi, lo) with E8M0 scales per 32-element block -- token b of a
+// column group takes columns 2b, 2b + 1 of one MFMA, 8 tokens a group.
+//
+// One workgroup owns one column group (8 tokens) and all of the layer's rows:
+//   1. x of its tokens becomes stage 1's operand chunk by chunk (8 slices of
+//      128 k a chunk, double buffered in LDS): z = bf16(s2 * x) and its
+//      hi/lo split, formed once per token;
+//   2. stage 1: each wave takes 64-row groups of Vb^T (r) round robin and
+//      accumulates them over all chunks, two row groups sharing each B
+//      fragment;
+//   3. its epilogue forms t = bf16(acc) and writes it as stage 2's operand
+//      into LDS (the 32 rows of a scale block lie in one wave's row group, so
+//      the block maxima are two lane shuffles);
+//   4. stage 2: each wave takes 64-row groups of Ub (dout) round robin, two
+//      at a time, over t's slices in LDS, and writes y = bf16(acc) * s1 + bias.
+// Nothing between the stages leaves the CU: no operand prep launch, no split
+// K partials, no t round trip through memory.  Every workgroup reads all of
+// the layer's signs; they stay in the XCD's L2 (a config-2 layer is 1 MiB).
+// Sign words are loaded in units of four slices for two row groups, one unit
+// ahead of the MFMAs that use them.
+#include <mutex>
+
+#include "factor_internal.h"
+#include "q4_operand.h"
+
+namespace qbk {
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4_t gu4_t;
+
+#define Q4G_WAVES 8
+#define Q4G_CH 8          // slices of x per LDS chunk (1024 k)
+#define Q4G_SLICE 2112    // LDS bytes of one slice's operand: 2 KiB of fp8 + 64 scale bytes
+#define Q4G_SC 2048       // offset of the scale bytes within a slice
+#define Q4G_MAX_RG1 32    // stage-1 row groups (r_p / 64) the accumulators hold: 4 a wave
+#define Q4G_SCALE_A 125   // the fp4 signs' E8M0 scale 2^-2 (decode.hip's q4_signs)
+
+struct Q4GArgs {
+    const uint32_t *bits1, *bits2;  // Vb^T and Ub in the decode layout [rows_p/64][K/128][64][4]
+    const float *s2, *s1, *bias;
+    const void *x;                  // [N][din] bf16 or f32
+    void *y;                        // [N][dout] bf16 or f32
+    uint32_t N, din, ns1;           // tokens, din, stage-1 slices (din_q / 128)
+    uint32_t r, n_rg1, ns2;         // rank, stage-1 row groups (r_p / 64), stage-2 slices (r_q / 128)
+    uint32_t dout, n_rg2;           // dout, stage-2 row groups (dout_p / 64)
+    int vec_x, vec_y;               // x rows allow 16-byte loads; y rows allow 4-element stores
+    uint32_t c7;                    // 0x77777777
+    uint16_t *t_out;                // t bf16 [N][r_p] as well (zero past r), or null
+    uint32_t r_p;
+};
+
+__device__ __forceinline__ i32x8_t q4g_signs(uint32_t w, uint32_t c7) {
+    i32x8_t av;
+    av[0] = (int)((w << 3) | c7);
+    av[1] = (int)((w << 2) | c7);
+    av[2] = (int)((w << 1) | c7);
+    av[3] = (int)(w | c7);
+    av[4] = av[5] = av[6] = av[7] = 0;
+    return av;
+}
+
+// The B fragment and scale byte of lane (col, G) for one slice in LDS.
+__device__ __forceinline__ void q4g_bfrag(const uint8_t *slice, int lane, i32x8_t &bv, int &bs) {
+    const uint4 b0 = *(const uint4 *)(slice + lane * 16);
+    const uint4 b1 = *(const uint4 *)(slice + 1024 + lane * 16);
+    bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+    bs = slice[Q4G_SC + lane];
+}
+
+__device__ __forceinline__ void q4g_mfma4(f32x4_t acc[4], const u32x4_t &w, const i32x8_t &bv, int bs, uint32_t c7) {
+    acc[0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4g_signs(w.x, c7), bv, acc[0], 4, 0, 0, Q4G_SCALE_A, 0, bs);
+    acc[1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4g_signs(w.y, c7), bv, acc[1], 4, 0, 0, Q4G_SCALE_A, 0, bs);
+    acc[2] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4g_signs(w.z, c7), bv, acc[2], 4, 0, 0, Q4G_SCALE_A, 0, bs);
+    acc[3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(q4g_signs(w.w, c7), bv, acc[3], 4, 0, 0, Q4G_SCALE_A, 0, bs);
+}
+
+// One run of 16 activations of x in registers (the loads of a chunk are
+// issued a chunk ahead of their conversion).
+template <bool XF32>
+struct Q4GRun {
+    u32x4_t xr[XF32 ? 4 : 2];
+    u32x4_t sr[4];
+};
+
+template <bool XF32>
+__device__ __forceinline__ void q4g_load_run(const Q4GArgs &a, size_t n, size_t k0, Q4GRun<XF32> &R) {
+    if (n < a.N && a.vec_x && k0 + 16 <= a.din) {
+        const gu4_t *xs = (const gu4_t *)((const char *)a.x + (n * a.din + k0) * (XF32 ? 4 : 2));
+#pragma unroll
+        for (int q = 0; q < (XF32 ? 4 : 2); q++) {
+            R.xr[q] = xs[q];
+        }
+        const gu4_t *ss = (const gu4_t *)(a.s2 + k0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            R.sr[q] = ss[q];
+        }
+        return;
+    }
+    // the last run of a row, a token past N, or rows without 16-byte
+    // pieces: element by element, zero past din (x) and past N (token)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const size_t k = k0 + e;
+        const bool ok = n < a.N && k < a.din;
+        uint32_t xv = 0, sv = 0;
+        if (ok) {
+            xv = XF32 ? ((const uint32_t *)a.x)[n * a.din + k] : ((const uint16_t *)a.x)[n * a.din + k];
+            sv = __float_as_uint(a.s2[k]);
+        }
+        if constexpr (XF32)
+            R.xr[e >> 2][e & 3] = xv;
+        else if (e & 1)
+            R.xr[e >> 3][(e & 7) >> 1] |= xv << 16;
+        else
+            R.xr[e >> 3][(e & 7) >> 1] = xv;
+        R.sr[e >> 2][e & 3] = sv;
+    }
+}
+
+// Run (b, j, r) of a chunk -> the LDS operand: hi bytes to column 2b, lo to
+// 2b + 1 of B lane group r / 2, half r % 2; the scale pair of the run's
+// block from the runs with r & 2 == 0 (decode.hip's layout with 16 columns).
+template <bool XF32>
+__device__ __forceinline__ void q4g_store_run(const Q4GRun<XF32> &R, uint8_t *slice, int b, int r) {
+    float z[16];
+    if constexpr (XF32) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                z[4 * q + u] = bf16_to_f32(f32_to_bf16(__uint_as_float(R.sr[q][u]) * __uint_as_float(R.xr[q][u])));
+    } else {
+        q4_run_z(R.xr, R.sr, z);
+    }
+    uint32_t hw[4], lw[4];
+    int e_hi, e_lo;
+    q4_run_operand(z, hw, lw, e_hi, e_lo);
+    uint8_t *p = slice + (r & 1) * 1024 + ((r >> 1) * 16 + 2 * b) * 16;
+    *(uint4 *)p = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(p + 16) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if ((r & 2) == 0)
+        *(uint16_t *)(slice + Q4G_SC + (2 * (r & 1) + (r >> 2)) * 16 + 2 * b) =
+            (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
+}
+
+// The value of the lane's column partner (lane ^ 1: the other half of a
+// token's hi / lo pair) -- a DPP quad permutation, no LDS round trip.
+__device__ __forceinline__ float q4g_pair(float a) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));
+}
+
+// Stage 1's epilogue for row group g (acc: its four row tiles): t =
+// bf16((hi + lo) / 1.5), zero past r, written as stage 2's operand.  Lane
+// (col, G) of row tile rt holds rows 64g + 16rt + 4G + i of column col; both
+// lanes of a column pair form the same t.  Stage-2 slice g / 2, run 4(g & 1)
+// + rt, element 4G + i: lane (col, G) writes four consecutive bytes -- the hi
+// bytes from an even column, the lo bytes from an odd one.  Row tiles rt and
+// rt + 2 form one scale block (runs u, u ^ 2): its maxima are over the lane's
+// eight values and the lanes 16 and 32 apart.
+__device__ __forceinline__ void q4g_epilogue1(const f32x4_t acc[4], uint8_t *tbuf, size_t g, uint32_t r,
+                                              int lane, uint16_t *t_out, size_t n, uint32_t r_p) {
+    const int col = lane & 15, G = lane >> 4;
+    uint8_t *slice = tbuf + (g >> 1) * Q4G_SLICE;
+    const int half = (int)(g & 1);
+#pragma unroll
+    for (int pr = 0; pr < 2; pr++) {
+        float t[2][4];
+        uint32_t tw[2][2];
+        float amax = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const int rt = pr + 2 * tt;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = q4_unscale(acc[rt][i] + q4g_pair(acc[rt][i]));
+            const uint32_t row0 = (uint32_t)(64 * g) + 16 * rt + 4 * G;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                uint32_t w = f32x2_to_bf16x2(v[2 * h], v[2 * h + 1]);
+                if (row0 + 2 * h >= r) w &= 0xffff0000u;
+                if (row0 + 2 * h + 1 >= r) w &= 0x0000ffffu;
+                tw[tt][h] = w;
+                t[tt][2 * h] = __uint_as_float(w << 16);
+                t[tt][2 * h + 1] = __uint_as_float(w & 0xffff0000u);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) amax = fmaxf(amax, fabsf(t[tt][i]));
+        }
+        if (t_out && !(col & 1)) {
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+                *(uint2 *)(t_out + n * r_p + 64 * g + 16 * (pr + 2 * tt) + 4 * G) = make_uint2(tw[tt][0], tw[tt][1]);
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
+        const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+        uint32_t hw[2];
+        float rmax = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            int w = __builtin_amdgcn_cvt_pk_fp8_f32(t[tt][0] * inv_hi, t[tt][1] * inv_hi, 0, false);
+            w = __builtin_amdgcn_cvt_pk_fp8_f32(t[tt][2] * inv_hi, t[tt][3] * inv_hi, w, true);
+            hw[tt] = (uint32_t)w;
+            t[tt][0] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
+            t[tt][1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
+            t[tt][2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
+            t[tt][3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+#pragma unroll
+            for (int i = 0; i < 4; i++) rmax = fmaxf(rmax, fabsf(t[tt][i]));
+        }
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 16, 64));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
+        const float inv_lo = pow2f(-e_lo);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const int rt = pr + 2 * tt, u = 4 * half + rt;
+            uint32_t w = hw[tt];
+            if (col & 1) {
+                int lw = __builtin_amdgcn_cvt_pk_fp8_f32(t[tt][0] * inv_lo, t[tt][1] * inv_lo, 0, false);
+                w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[tt][2] * inv_lo, t[tt][3] * inv_lo, lw, true);
+            }
+            *(uint32_t *)(slice + (u & 1) * 1024 + ((u >> 1) * 16 + col) * 16 + 4 * G) = w;
+        }
+        if (G == 0) slice[Q4G_SC + (2 * pr + half) * 16 + col] = (uint8_t)((col & 1 ? e_lo : e_hi) + 127);
+    }
+}
+
+// Stage 2's epilogue for row group g: y = bf16((hi + lo) / 1.5) * s1 + bias,
+// s1 and bias of the group's 64 rows read from the wave's LDS region sb
+// ([64] s1 then [64] bias); the even lane of a column pair stores the four
+// rows it holds of token col / 2.
+__device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArgs &a, size_t g, const float *sb,
+                                              size_t n0, int lane, bool ybf16) {
+    const int col = lane & 15, G = lane >> 4;
+    const size_t n = n0 + (col >> 1);
+#pragma unroll
+    for (int rt = 0; rt < 4; rt++) {
+        const size_t row0 = 64 * g + 16 * rt + 4 * G;
+        const float4 s1v = *(const float4 *)(sb + 16 * rt + 4 * G);
+        const float4 biv = *(const float4 *)(sb + 64 + 16 * rt + 4 * G);
+        const float s1a[4] = {s1v.x, s1v.y, s1v.z, s1v.w}, bia[4] = {biv.x, biv.y, biv.z, biv.w};
+        float v[4], y[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = q4_unscale(acc[rt][i] + q4g_pair(acc[rt][i]));
+        const uint32_t u01 = f32x2_to_bf16x2(v[0], v[1]), u23 = f32x2_to_bf16x2(v[2], v[3]);
+        y[0] = __uint_as_float(u01 << 16) * s1a[0] + bia[0];
+        y[1] = __uint_as_float(u01 & 0xffff0000u) * s1a[1] + bia[1];
+        y[2] = __uint_as_float(u23 << 16) * s1a[2] + bia[2];
+        y[3] = __uint_as_float(u23 & 0xffff0000u) * s1a[3] + bia[3];
+        if ((col & 1) || n >= a.N || row0 >= a.dout) continue;
+        if (a.vec_y && row0 + 4 <= a.dout) {
+            if (ybf16)
+                *(uint2 *)((uint16_t *)a.y + n * a.dout + row0) =
+                    make_uint2(f32x2_to_bf16x2(y[0], y[1]), f32x2_to_bf16x2(y[2], y[3]));
+            else
+                *(float4 *)((float *)a.y + n * a.dout + row0) = make_float4(y[0], y[1], y[2], y[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (row0 + i >= a.dout) break;
+                if (ybf16)
+                    ((uint16_t *)a.y)[n * a.dout + row0 + i] = f32_to_bf16(y[i]);
+                else
+                    ((float *)a.y)[n * a.dout + row0 + i] = y[i];
+            }
+        }
+    }
+}
+
+// Sign words stream through a ring of Q4G_RING units per wave, all in
+// flight: a unit's loads are issued Q4G_RING units before its MFMAs.
+// Loads are unconditional (indices clamped into the layer) so that the
+// compiler's waits stay counted ones; only MFMAs sit under branches.
+#define Q4G_RING 4
+
+// NG1: stage-1 row groups a wave accumulates (2: r_p <= 1024, 4: r_p <=
+// 2048).  Stage 1's unit: one slice of the wave's NG1 row groups (their B
+// fragment read once); stage 2's unit: one slice of a pair of row groups.
+template <bool XF32, bool YBF16, int NG1>
+__global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t q4g_lds[];
+    uint8_t *xbuf = q4g_lds;                             // [2][Q4G_CH slices]
+    uint8_t *tbuf = q4g_lds + 2 * Q4G_CH * Q4G_SLICE;    // [ns2 slices]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const size_t n0 = (size_t)blockIdx.x * 8;
+    const uint32_t c7 = a.c7;
+    const gu4_t *b1 = (const gu4_t *)a.bits1, *b2 = (const gu4_t *)a.bits2;
+
+    // ---- stage 1 --------------------------------------------------------
+    // this wave's row groups: wave + 8q, q < NG1 (those past the rank padded
+    // to 128 load a clamped group and skip their MFMAs)
+    const uint32_t nrg1 = a.n_rg1, ns1 = a.ns1;
+    const int ng1 = wave < (int)nrg1 ? (int)((nrg1 - 1 - wave) / Q4G_WAVES) + 1 : 0;
+    const uint32_t nch = (ns1 + Q4G_CH - 1) / Q4G_CH, nu1 = nch * Q4G_CH;
+    // x conversion: thread (token b = wave, slice j, run r) of each chunk
+    const int xb = tid >> 6, xj = (tid >> 3) & 7, xr = tid & 7;
+    Q4GRun<XF32> run;
+    const gu4_t *g1p[NG1];
+#pragma unroll
+    for (int q = 0; q < NG1; q++) {
+        uint32_t g = (uint32_t)wave + Q4G_WAVES * q;
+        g = g < nrg1 ? g : nrg1 - 1;
+        g1p[q] = b1 + (size_t)g * ns1 * 64 + lane;
+    }
+    f32x4_t acc1[NG1][4];
+#pragma unroll
+    for (int q = 0; q < NG1; q++)
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) acc1[q][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4_t ring1[Q4G_RING][NG1];
+#define Q4G_ISSUE1(U, SLOT)                                                             \
+    {                                                                                   \
+        uint32_t s_ = (U);                                                              \
+        s_ = s_ < ns1 ? s_ : ns1 - 1;                                                   \
+        _Pragma("unroll") for (int q = 0; q < NG1; q++) ring1[SLOT][q] = g1p[q][(size_t)s_ * 64]; \
+    }
+
+    // chunk 0 into buffer 0; the first units' sign words in flight
+    q4g_load_run<XF32>(a, n0 + xb, 128 * xj + 16 * xr, run);
+#pragma unroll
+    for (int k = 0; k < Q4G_RING; k++) Q4G_ISSUE1((uint32_t)k, k)
+    q4g_store_run<XF32>(run, xbuf + xj * Q4G_SLICE, xb, xr);
+    __syncthreads();
+
+    for (uint32_t c = 0; c < nch; c++) {
+        const bool more = c + 1 < nch;
+        if (more) q4g_load_run<XF32>(a, n0 + xb, (size_t)(c + 1) * 1024 + 128 * xj + 16 * xr, run);
+        const uint8_t *xs = xbuf + (c & 1) * (Q4G_CH * Q4G_SLICE);
+        // B fragments one slice ahead (within the chunk: the next chunk's
+        // buffer is written behind the barrier that ends this one)
+        i32x8_t bvq[2];
+        int bsq[2];
+        q4g_bfrag(xs, lane, bvq[0], bsq[0]);
+#pragma unroll
+        for (int j = 0; j < Q4G_CH; j++) {
+            const int slot = j % Q4G_RING, cur = j & 1;
+            const uint32_t s = c * Q4G_CH + j;
+            if (j + 1 < Q4G_CH) q4g_bfrag(xs + (j + 1) * Q4G_SLICE, lane, bvq[cur ^ 1], bsq[cur ^ 1]);
+            if (s < ns1) {
+#pragma unroll
+                for (int q = 0; q < NG1; q++)
+                    if (q < ng1) q4g_mfma4(acc1[q], ring1[slot][q], bvq[cur], bsq[cur], c7);
+            }
+            Q4G_ISSUE1(s + Q4G_RING, slot)
+        }
+        if (more) q4g_store_run<XF32>(run, xbuf + ((c + 1) & 1) * (Q4G_CH * Q4G_SLICE) + xj * Q4G_SLICE, xb, xr);
+        __syncthreads();
+    }
+#undef Q4G_ISSUE1
+    (void)nu1;
+
+    // stage 1's epilogue: t -> stage 2's operand in LDS
+#pragma unroll
+    for (int q = 0; q < NG1; q++)
+        if (q < ng1) {
+            // tokens past N keep t to themselves
+            const size_t n = n0 + ((lane & 15) >> 1);
+            q4g_epilogue1(acc1[q], tbuf, (size_t)wave + Q4G_WAVES * q, a.r, lane, n < a.N ? a.t_out : nullptr, n,
+                          a.r_p);
+        }
+    __syncthreads();
+
+    // ---- stage 2 --------------------------------------------------------
+    // this wave's row groups wave + 8q, two at a time; units of one slice of
+    // a pair, flattened over the pairs (running counters: (p, s) of the unit
+    // computed, (pi, si) of the unit issued); s1 and bias of a pair's rows
+    // are loaded one pair ahead and staged through the wave's LDS region
+    const uint32_t nrg2 = a.n_rg2, ns2 = a.ns2, dout = a.dout;
+    const int ng2 = wave < (int)nrg2 ? (int)((nrg2 - 1 - wave) / Q4G_WAVES) + 1 : 0;
+    const uint32_t np2 = (uint32_t)(ng2 + 1) >> 1, total = np2 * ns2;
+    float *sb = (float *)(tbuf + ns2 * Q4G_SLICE) + wave * 256;  // [2 groups][s1 64 | bias 64]
+    f32x4_t acc2[2][4];
+    u32x4_t ring2[Q4G_RING][2];
+    uint32_t pi = 0, si = 0;
+#define Q4G_ISSUE2(SLOT)                                                                \
+    {                                                                                   \
+        const uint32_t p_ = pi < np2 ? pi : np2 - 1;                                    \
+        _Pragma("unroll") for (int w = 0; w < 2; w++) {                                 \
+            uint32_t g = (uint32_t)wave + Q4G_WAVES * (2 * p_ + w);                     \
+            g = g < nrg2 ? g : nrg2 - 1;                                                \
+            ring2[SLOT][w] = b2[((size_t)g * ns2 + si) * 64 + lane];                    \
+        }                                                                               \
+        if (++si == ns2) {                                                              \
+            si = 0;                                                                     \
+            ++pi;                                                                       \
+        }                                                                               \
+    }
+    // s1 and bias of lane l's row in pair P's two groups
+    float sv[2][2];
+#define Q4G_SCALES2(P)                                                                  \
+    _Pragma("unroll") for (int w = 0; w < 2; w++) {                                     \
+        size_t row = ((size_t)wave + Q4G_WAVES * (2 * (P) + w)) * 64 + lane;            \
+        row = row < dout ? row : dout - 1;                                              \
+        sv[w][0] = a.s1[row];                                                           \
+        sv[w][1] = a.bias[row];                                                         \
+    }
+    if (total > 0) {
+        Q4G_SCALES2(0u)
+#pragma unroll
+        for (int k = 0; k < Q4G_RING; k++) Q4G_ISSUE2(k)
+        uint32_t p = 0, s = 0;
+        i32x8_t bvq[2];
+        int bsq[2];
+        q4g_bfrag(tbuf, lane, bvq[0], bsq[0]);
+        for (uint32_t u0 = 0; u0 < total; u0 += Q4G_RING) {
+#pragma unroll
+            for (int k = 0; k < Q4G_RING; k++) {
+                const int cur = k & 1;
+                const uint32_t sn = s + 1 == ns2 ? 0 : s + 1;
+                q4g_bfrag(tbuf + sn * Q4G_SLICE, lane, bvq[cur ^ 1], bsq[cur ^ 1]);
+                if (u0 + k < total) {
+                    const bool two = 2 * p + 1 < (uint32_t)ng2;
+                    if (s == 0) {
+#pragma unroll
+                        for (int h = 0; h < 2; h++)
+#pragma unroll
+                            for (int rt = 0; rt < 4; rt++) acc2[h][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+                    q4g_mfma4(acc2[0], ring2[k][0], bvq[cur], bsq[cur], c7);
+                    if (two) q4g_mfma4(acc2[1], ring2[k][1], bvq[cur], bsq[cur], c7);
+                    if (sn == 0) {
+                        // the pair is complete: its scales through LDS, then the next pair's in flight
+#pragma unroll
+                        for (int w = 0; w < 2; w++) {
+                            sb[128 * w + lane] = sv[w][0];
+                            sb[128 * w + 64 + lane] = sv[w][1];
+                        }
+                        __builtin_amdgcn_wave_barrier();
+                        Q4G_SCALES2(p + 1 < np2 ? p + 1 : p)
+                        const size_t g0 = (size_t)wave + Q4G_WAVES * (2 * p);
+                        q4g_epilogue2(acc2[0], a, g0, sb, n0, lane, YBF16);
+                        if (two) q4g_epilogue2(acc2[1], a, g0 + Q4G_WAVES, sb + 128, n0, lane, YBF16);
+                        __builtin_amdgcn_wave_barrier();
+                    }
+                }
+                Q4G_ISSUE2(k)
+                s = sn;
+                p += sn == 0;
+            }
+        }
+    }
+#undef Q4G_ISSUE2
+#undef Q4G_SCALES2
+}
+
+// ------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------
+
+// x chunks, stage 2's operand, each wave's s1 / bias staging (1 KiB)
+static uint32_t q4g_lds_bytes(const qbk_factor *L) {
+    return (uint32_t)((2 * Q4G_CH + L->r_q / 128) * Q4G_SLICE + Q4G_WAVES * 1024);
+}
+
+bool q4g_fits(const qbk_factor *L, size_t N) {
+    return N > 0 && N <= 0x7fffffff && L->r > 0 && L->r_p / 64 <= Q4G_MAX_RG1 && L->din > 0 &&
+           L->din <= 0x7fffffff && L->dout > 0 && L->dout <= 0x7fffffff;
+}
+
+// The smallest batch the one-launch GEMM takes over from the two-stage one:
+// its workgroups (8 tokens each) each stream all of a layer's signs, so it
+// wins once they fill half the chip (measured at config 2: B = 512, 38 against
+// 31 us; B = 2048, 45 against 56 us); below, the two-stage GEMM splits each
+// stage over row tiles and K.
+#define Q4G_MIN_N 1024
+
+bool q4g_use(const qbk_factor *L, size_t N) { return N >= Q4G_MIN_N && q4g_fits(L, N); }
+
+size_t gemm_workspace(const qbk_factor *L, size_t N) {
+    return q4g_use(L, N) ? N * L->r_p * 2 : g32_workspace(L, N);
+}
+
+int gemm_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
+             hipStream_t s) {
+    if (q4g_use(L, N)) return q4g_run(L, x, xf32, N, y, ybf16, (uint16_t *)ws, s);
+    return g32_run(L, x, xf32, N, y, ybf16, ws, s);
+}
+
+int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, uint16_t *t_out,
+            hipStream_t s) {
+    const uint32_t lds = q4g_lds_bytes(L);
+    {
+        // up to 67.5 KiB of LDS, past the 64 KiB default: the attribute is
+        // per device, set once on each under a lock (callers may share a ctx)
+        static std::mutex mu;
+        static uint64_t done = 0;
+        int dev = 0;
+        QBK_HIP(hipGetDevice(&dev));
+        std::lock_guard<std::mutex> lock(mu);
+        if (dev < 64 && !((done >> dev) & 1)) {
+            const uint32_t most = (2 * Q4G_CH + Q4G_MAX_RG1 / 2) * Q4G_SLICE + Q4G_WAVES * 1024;
+            for (const void *k : {(const void *)q4g_kernel<false, false, 2>, (const void *)q4g_kernel<false, true, 2>,
+                                  (const void *)q4g_kernel<true, false, 2>, (const void *)q4g_kernel<true, true, 2>,
+                                  (const void *)q4g_kernel<false, false, 4>, (const void *)q4g_kernel<false, true, 4>,
+                                  (const void *)q4g_kernel<true, false, 4>, (const void *)q4g_kernel<true, true, 4>})
+                QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)most));
+            done |= 1ull << dev;
+        }
+    }
+    Q4GArgs a{};
+    a.bits1 = L->vt_q4;
+    a.bits2 = L->u_q4;
+    a.s2 = L->s2;
+    a.s1 = L->s1;
+    a.bias = L->bias;
+    a.x = x;
+    a.y = y;
+    a.N = (uint32_t)N;
+    a.din = (uint32_t)L->din;
+    a.ns1 = (uint32_t)(L->din_q / 128);
+    a.r = (uint32_t)L->r;
+    a.n_rg1 = (uint32_t)(L->r_p / 64);
+    a.ns2 = (uint32_t)(L->r_q / 128);
+    a.dout = (uint32_t)L->dout;
+    a.n_rg2 = (uint32_t)(L->dout_p / 64);
+    a.vec_x = L->din % (xf32 ? 4 : 8) == 0 && (uintptr_t)x % 16 == 0;
+    a.vec_y = L->dout % 4 == 0 && (uintptr_t)y % (ybf16 ? 8 : 16) == 0;
+    a.c7 = 0x77777777u;
+    a.t_out = t_out;
+    a.r_p = (uint32_t)L->r_p;
+    const dim3 grid((unsigned)div_ceil(N, 8)), block(64 * Q4G_WAVES);
+#define Q4G_LAUNCH(XF, YB, NG) hipLaunchKernelGGL((q4g_kernel<XF, YB, NG>), grid, block, lds, s, a)
+    const bool small = a.n_rg1 <= 2 * Q4G_WAVES;
+    if (small) {
+        if (xf32 && ybf16) Q4G_LAUNCH(true, true, 2);
+        else if (xf32) Q4G_LAUNCH(true, false, 2);
+        else if (ybf16) Q4G_LAUNCH(false, true, 2);
+        else Q4G_LAUNCH(false, false, 2);
+    } else {
+        if (xf32 && ybf16) Q4G_LAUNCH(true, true, 4);
+        else if (xf32) Q4G_LAUNCH(true, false, 4);
+        else if (ybf16) Q4G_LAUNCH(false, true, 4);
+        else Q4G_LAUNCH(false, false, 4);
+    }
+#undef Q4G_LAUNCH
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+}  // namespace qbk

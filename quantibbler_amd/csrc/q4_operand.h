@@ -24,6 +24,14 @@ __device__ __forceinline__ int e8m0_of(float amax) {
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
+// The fp4 signs enter the MFMA as +-1.5 (e2m1 6 at E8M0 scale 2^-2), so a
+// sum s comes out as 1.5 s.  Multiplying by c = 11184811 * 2^-24, the float
+// nearest 2/3, undoes it: 1.5 c = 1 + 2^-25, so for any float s, (1.5 s) * c
+// = s (1 + 2^-25) rounds back to s exactly -- what a division by 1.5 gives,
+// in one multiply; a sum that is not 1.5 times a float lands within one ulp
+// of the division's quotient.
+__device__ __forceinline__ float q4_unscale(float v) { return v * 0.666666686534881591796875f; }
+
 // One run of 16 activations z = bf16(s2 * x) as stage 1's fp8 operand:
 // z splits exactly into hi + lo, each fp8 e4m3 part keeping 4 significant
 // bits relative to its block's E8M0 exponent (e_hi from the block max of z,
@@ -76,8 +84,12 @@ __device__ __forceinline__ void q4_run_z(const u32x4_t xr[2], const u32x4_t sr[4
 #pragma unroll
     for (int q = 0; q < 4; q++) {
 #pragma unroll
-        for (int u = 0; u < 4; u++)
-            z[4 * q + u] = bf16_to_f32(f32_to_bf16(__uint_as_float(sr[q][u]) * z[4 * q + u]));
+        for (int u = 0; u < 4; u += 2) {
+            const uint32_t w = f32x2_to_bf16x2(__uint_as_float(sr[q][u]) * z[4 * q + u],
+                                               __uint_as_float(sr[q][u + 1]) * z[4 * q + u + 1]);
+            z[4 * q + u] = __uint_as_float(w << 16);
+            z[4 * q + u + 1] = __uint_as_float(w & 0xffff0000u);
+        }
     }
 }
 

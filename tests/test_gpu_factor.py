@@ -83,6 +83,16 @@ def test_integer_exact_long_k_batch1(ctx, orc, dout, din, r):
     integer_exact_case(ctx, orc, dout, din, r, 1)
 
 
+@pytest.mark.parametrize("dout,din,r,batch", [(300, 200, 37, 1031), (256, 512, 128, 1024), (1024, 4096, 1102, 1024),
+                                              (512, 640, 2000, 1030)])
+def test_integer_exact_one_launch(ctx, orc, dout, din, r, batch):
+    """The one-launch GEMM (batches from 1024 on): ragged last token groups,
+    a din that is not a multiple of 128, ranks whose 64-row groups do not
+    split evenly over the eight waves (1102: 18 groups), and the largest rank
+    it takes (2000: 32 groups, four a wave)."""
+    integer_exact_case(ctx, orc, dout, din, r, batch)
+
+
 def test_integer_exact_config2_batch512(ctx, orc):
     """Config 2's shape at B = 512 (the K-split stage 1 on 128 x 64 tiles, stage
     2 on its own 256 tiles)."""
@@ -169,7 +179,12 @@ def gpu_t(layer, ws, batch):
         assert np.array_equal(orc.bf16_to_f32(tb).astype(np.float64), t), "operand is not a bf16 t"
         assert not tb[:, r:].any()
         return tb[:, :r]
-    # prefill GEMM: [z bf16 [batch][din_p] | f32 partials [split][batch][r_p]
+    if ws.size == batch * rp * 2:
+        # fused prefill GEMM (gemm.hip): t bf16 [batch][r_p], zero past r
+        t = ws.view(np.uint16).reshape(batch, rp)
+        assert not t[:, r:].any()
+        return t[:, :r]
+    # two-stage prefill GEMM (rank past 2048): [z bf16 [batch][din_p] | f32 partials [split][batch][r_p]
     # (split > 1) | t bf16 [batch][r_p] | stage 2's f32 partials
     # [split2][batch][dout_p] (split2 > 1)]
     from oracle import oracle as orc
@@ -193,8 +208,32 @@ def gpu_t(layer, ws, batch):
     raise AssertionError("unexpected workspace size")
 
 
-@pytest.mark.parametrize("dout,din,r", SHAPES)
-@pytest.mark.parametrize("batch", [1, 4, 16, 128])
+def mfma_window(v):
+    """Bound on what the fp4 x fp8 scaled MFMA's own summation can lose in a
+    stage fed v [batch][K]: the MFMA sums each 32-element scale block (the
+    runs kq4(g, .) of a 128-k slice) in a fixed-point window about 13 bits
+    below the block's largest product, truncating what falls below it (probed
+    on gfx950 with planted operands: one large product and small ones in the
+    same block lose bits, across blocks nothing is lost); measured losses stay
+    under 2^-10 of the block's largest product.  v's hi piece carries the
+    block maximum, its lo piece at most 2^-4 of it, and the epilogue divides
+    out the 1.5 of the fp4 signs: per token, 2^-10 (1 + 2^-4) times the sum
+    of the blocks' largest |v|."""
+    v = np.abs(np.asarray(v, np.float64))
+    K = v.shape[1]
+    kp = -(-K // 128) * 128
+    w = np.zeros((v.shape[0], kp))
+    w[:, :K] = v
+    k = np.arange(kp) % 128
+    grp = (np.arange(kp) // 128) * 4 + 2 * ((k >> 4) & 1) + ((k >> 6) & 1)
+    tot = np.zeros(v.shape[0])
+    for gi in np.unique(grp):
+        tot += w[:, grp == gi].max(axis=1)
+    return (2.0 ** -10 * (1 + 2.0 ** -4) * tot)[:, None]
+
+
+@pytest.mark.parametrize("dout,din,r,batch", [(d, n, r, b) for b in (1, 4, 16, 128) for d, n, r in SHAPES]
+                         + [(256, 512, 128, 1024), (300, 200, 37, 1031)])
 def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
     say("factor stage bounds", dout, din, r, "batch", batch)
     rng = np.random.default_rng(1000 + dout + r + batch)
@@ -213,7 +252,7 @@ def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
                                            L["bias"], x, want_t=True)
     tof = orc.bf16_to_f32(t_orc).astype(np.float64)
     ulp = np.spacing(np.abs(tof).astype(np.float32)).astype(np.float64) * 2 ** 16
-    assert np.all(np.abs(tf - tof) <= ulp + 1e-6 * np.abs(z).sum(axis=1, keepdims=True))
+    assert np.all(np.abs(tf - tof) <= ulp + 1e-6 * np.abs(z).sum(axis=1, keepdims=True) + mfma_window(z))
     # stage 2 from the device's own t
     u_exact = tf @ L["ubs"].T.astype(np.float64)
     y_exact = u_exact * L["s1"] + L["bias"]
@@ -223,13 +262,14 @@ def test_config_distribution_stage_bounds(ctx, orc, dout, din, r, batch):
     y_or = (u_or * L["s1"] + L["bias"]).astype(np.float32)
     # one bf16 ulp of u, plus the f32 reassociation term (the device sums in a
     # different order; under cancellation that can move u across several ulps)
+    # and the MFMA's summation window
     uulp = np.spacing(np.abs(u_or).astype(np.float32)) * 2 ** 16
-    reassoc = 1e-6 * np.abs(tf).sum(axis=1, keepdims=True)
+    reassoc = 1e-6 * np.abs(tf).sum(axis=1, keepdims=True) + mfma_window(tf)
     assert np.all(np.abs(y - y_or) <= np.abs(L["s1"]) * (uulp * 1.01 + reassoc) + 1e-6 * np.abs(y_or))
 
 
-def _rounding_layer(orc, rng, din):
-    L = make_layer(orc, rng, 64, din, 32)
+def _rounding_layer(orc, rng, din, r=32):
+    L = make_layer(orc, rng, 64, din, r)
     # scales that put a tie bit into the product's mantissa, overflow and underflow it
     picks = np.array([1 + 2.0 ** -8, 1.5 + 2.0 ** -9, 3.0, 2.0 ** 100, 2.0 ** -100, 1.0], np.float32)
     L["s2"] = np.where(rng.random(din) < 0.5, picks[rng.integers(0, picks.size, din)], L["s2"]).astype(np.float32)
@@ -237,13 +277,14 @@ def _rounding_layer(orc, rng, din):
 
 
 def test_prefill_activation_rounding_staged(ctx, orc):
-    """z = bf16(s2 * x) (engine/mod.rs:449-452), the prefill GEMM's first
-    product, for rows that are not 16-byte chunks (din 203): staged whole at
-    the head of the workspace and compared bit for bit with the oracle's
-    rounding over ties, overflow to infinity, denormals and NaN payloads."""
+    """z = bf16(s2 * x) (engine/mod.rs:449-452), the two-stage prefill GEMM's
+    first product (ranks past 2048 take that GEMM), for rows that are not
+    16-byte chunks (din 203): staged whole at the head of the workspace and
+    compared bit for bit with the oracle's rounding over ties, overflow to
+    infinity, denormals and NaN payloads."""
     rng = np.random.default_rng(210)
     batch, din = 16, 203
-    L = _rounding_layer(orc, rng, din)
+    L = _rounding_layer(orc, rng, din, r=2100)
     xb = rng.integers(0, 1 << 16, (batch, din)).astype(np.uint16)
     # every bf16 bit pattern class: NaNs with payloads, +-inf, denormals, zeros
     specials = np.array([0x7F81, 0x7FC0, 0xFFA5, 0x7F80, 0xFF80, 0x0001, 0x807F, 0x0000, 0x8000, 0x7F7F],
@@ -258,11 +299,11 @@ def test_prefill_activation_rounding_staged(ctx, orc):
     assert np.array_equal(z[:, :din], want), np.argwhere(z[:, :din] != want)[:5]
 
 
-def _one_hot(orc, rng, L, batch, din, finite):
+def _one_hot(orc, rng, L, batch, din, finite, zmax=np.inf):
     """x with one nonzero element per token, so that every sum of the two
     stages is exact: t = +-z of that element, u = (integer) * z.  Values are
-    kept where z is a nonzero normal (or +-inf unless finite): the MFMA's NaN
-    sign and denormal inputs are not IEEE-specified."""
+    kept where z is a nonzero normal below zmax (or +-inf unless finite): the
+    MFMA's NaN sign and denormal inputs are not IEEE-specified."""
     cols = rng.integers(0, din, batch)
     vals = np.zeros(batch, np.float32)
     for n in range(batch):
@@ -271,7 +312,7 @@ def _one_hot(orc, rng, L, batch, din, finite):
             if not finite and rng.random() < 0.2:
                 v = np.float32(rng.choice([-1, 1]) * 3.0e38)
             zf = orc.bf16_to_f32(orc.f32_to_bf16(np.float32(L["s2"][cols[n]] * orc.bf16_to_f32(orc.f32_to_bf16(v)))))
-            if (np.isinf(zf) and not finite) or (np.isfinite(zf) and abs(zf) >= 2.0 ** -126):
+            if (np.isinf(zf) and not finite) or (np.isfinite(zf) and 2.0 ** -126 <= abs(zf) < zmax):
                 vals[n] = v
                 break
     x = np.zeros((batch, din), np.float32)
@@ -280,13 +321,14 @@ def _one_hot(orc, rng, L, batch, din, finite):
 
 
 def test_prefill_activation_rounding_fused(ctx, orc):
-    """The same product formed inside the GEMM's activation staging (din % 8
-    == 0): bf16 x through the device entry point, where t read back from the
-    workspace must be exactly +-z, ties and overflow included; f32 x through
-    the host face, where y must be bit-identical to the oracle's."""
+    """The same product formed inside the two-stage GEMM's activation staging
+    (din % 8 == 0, rank past 2048): bf16 x through the device entry point,
+    where t read back from the workspace must be exactly +-z, ties and
+    overflow included; f32 x through the host face, where y must be
+    bit-identical to the oracle's."""
     rng = np.random.default_rng(200)
     batch, din = 16, 200
-    L = _rounding_layer(orc, rng, din)
+    L = _rounding_layer(orc, rng, din, r=2100)
     layer = upload(ctx, L)
     x, cols = _one_hot(orc, rng, L, batch, din, finite=False)
     xb = orc.f32_to_bf16(x)
@@ -301,6 +343,48 @@ def test_prefill_activation_rounding_fused(ctx, orc):
     want_y = np.stack([orc.factor_apply("bf16", L["dout"], din, L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
                                         L["bias"], x[i]) for i in range(batch)])
     same(got, want_y)
+
+
+@pytest.mark.parametrize("din", [200, 203])
+def test_prefill_activation_rounding_one_launch(ctx, orc, din):
+    """z = bf16(s2 * x) formed by the one-launch GEMM (gemm.hip) as it
+    stages x: rows of 16-byte pieces (din 200) and element by element (din
+    203).  One-hot tokens make every sum exact: t read back from the
+    workspace must be exactly +-z over the tie-making scales, and y through
+    the f32 host face bit-identical to the oracle's.  A token with an
+    infinite z (s2 * x overflowing) gives NaN in every output where the
+    reference's sequential composite does: its fp8 split turns inf into NaN,
+    where the reference's t keeps +-inf and its u sums infinities of both
+    signs.  The fp4 signs enter the MFMA as +-1.5 (divided out at the end),
+    so sums whose 1.5-fold passes the f32 range overflow where the
+    reference's stay finite: finite z are kept below 2^122 here (u sums r =
+    32 of them)."""
+    say("factor one-launch GEMM activation rounding", din)
+    rng = np.random.default_rng(200 + din)
+    batch = 1029  # the one-launch GEMM from 1024 tokens on; a ragged last group of 8
+    L = _rounding_layer(orc, rng, din)
+    layer = upload(ctx, L)
+    zmax = 2.0 ** 122
+    x, cols = _one_hot(orc, rng, L, batch, din, finite=True, zmax=zmax)
+    xb = orc.f32_to_bf16(x)
+    _, ws = run_dev(layer, xb)
+    t = gpu_t(layer, ws, batch)
+    z = orc.f32_to_bf16((L["s2"][cols] * orc.bf16_to_f32(xb[np.arange(batch), cols])).astype(np.float32))
+    want = z[:, None] ^ np.where(L["vts"][:, cols].T < 0, np.uint16(0x8000), np.uint16(0))
+    assert np.array_equal(t, want.astype(np.uint16)), np.argwhere(t != want)[:5]
+    x, _ = _one_hot(orc, rng, L, batch, din, finite=True, zmax=zmax)
+    got = layer.apply(x, "bfloat16")
+    want_y = np.stack([orc.factor_apply("bf16", L["dout"], din, L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                        L["bias"], x[i]) for i in range(batch)])
+    same(got, want_y)
+    x, _ = _one_hot(orc, rng, L, batch, din, finite=False, zmax=zmax)
+    xb = orc.f32_to_bf16(x)
+    want = orc.factor_apply_bf16_batch(L["dout"], din, L["r"], L["ub"], L["vt"], L["s1"], L["s2"], L["bias"], xb)
+    got, _ = run_dev(layer, xb)
+    assert np.isnan(want).any()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    same(got[fin], want[fin], "finite outputs")
 
 
 def set_decode(S, x, dout):

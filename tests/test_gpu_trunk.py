@@ -245,18 +245,27 @@ def test_device_trunk_prefill_then_decode(ctx, orc):
     ref.pos = n
     hn = orc.norm_apply(h[-1], ref.final_norm, md.rms_norm_eps, "bf16")
     want = orc.head_logits(ref.head, hn)
-    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
-    say(f"  prefill logits rel {rel:.2e}")
-    assert rel <= 1e-2
+    sage_gate(got, want, "prefill")
     assert int(np.argmax(got)) == int(np.argmax(want)) or np.sort(want)[-1] - np.sort(want)[-2] < 1e-2
     for _ in range(3):
         tok = int(np.argmax(want))
         got = m.step(tok, torch.cuda.current_stream()).cpu().numpy()
         want = ref.step(tok)
-        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
-        say(f"  decode logits rel {rel:.2e}")
-        assert rel <= 1e-2
+        sage_gate(got, want, "decode")
     m.close()
+
+
+def sage_gate(got, want, label):
+    """The reference's gate for final logits on the sage face
+    (crates/quantibbler-server/tests/cross_face_sage_identity.rs:84-86,
+    147-160): cosine >= 0.999 and relative L1 = sum|a - b| / sum|a| <= 0.02;
+    the relative L2 is reported beside them."""
+    g, w = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    cos = float(g @ w / (np.linalg.norm(g) * np.linalg.norm(w)))
+    rl1 = float(np.abs(g - w).sum() / np.abs(w).sum())
+    rel = float(np.linalg.norm(g - w) / np.linalg.norm(w))
+    say(f"  {label} logits cos {cos:.7f} relL1 {rl1:.2e} rel {rel:.2e}")
+    assert cos >= 0.999 and rl1 <= 0.02, (label, cos, rl1)
 
 
 def _oracle_prefill(orc, md, tokens, capacity):
@@ -281,11 +290,10 @@ def test_device_trunk_batched_greedy(ctx, orc):
     first three (batch 3, the GEMV): each sequence's logits against its own
     oracle trunk, which takes the same greedy ids.
 
-    The budget is the one the single-sequence trunk tests hold each row to
-    (1e-2 relative on the logits), here on the mean over the 47 rows, with
-    each row within twice it: a bf16 rounding or an int8 code of the sage
-    attention that lands on the other side of a tie moves one row's logits
-    by up to about 1e-2, and over many rows one of them does."""
+    Every row is held to the reference's sage-face gate on final logits
+    (cosine >= 0.999, relative L1 <= 0.02: cross_face_sage_identity.rs:84-86),
+    as the single-sequence trunk test holds its rows; the relative L2 of each
+    row is reported beside it."""
     from quantibbler_amd.model import DeviceModel
 
     say("device trunk batched greedy decode")
@@ -300,6 +308,7 @@ def test_device_trunk_batched_greedy(ctx, orc):
         tokens = rng.integers(0, md.vocab_size, n).tolist()
         got = m.prefill(tokens, st, seq=s).cpu().numpy()
         ref, want = _oracle_prefill(orc, md, tokens, cap)
+        sage_gate(got, want, f"prefill of sequence {s}")
         rels.append(float(np.linalg.norm(got - want) / np.linalg.norm(want)))
         refs.append(ref)
         nxt.append(int(np.argmax(want)))
@@ -312,12 +321,12 @@ def test_device_trunk_batched_greedy(ctx, orc):
         row = []
         for s in range(n):
             want = refs[s].step(nxt[s])
+            sage_gate(got[s], want, f"batch {n} step, sequence {s}")
             row.append(float(np.linalg.norm(got[s] - want) / np.linalg.norm(want)))
             nxt[s] = int(np.argmax(want))
         say(f"  batch {n}: logits rel per sequence: {' '.join(f'{r:.1e}' for r in row)}")
         rels += row
-    say(f"  mean {np.mean(rels):.2e}, max {np.max(rels):.2e} over {len(rels)} rows")
-    assert np.mean(rels) <= 1e-2 and np.max(rels) <= 2e-2, (np.mean(rels), np.max(rels))
+    say(f"  relative L2: mean {np.mean(rels):.2e}, max {np.max(rels):.2e} over {len(rels)} rows")
     assert m.positions == [p + 3 for p in lens[:3]] + [p + 2 for p in lens[3:]]
     with pytest.raises(ValueError, match="a batch of 11 sequences on a model holding 10"):
         m.step_batch([0] * 11, st)
