@@ -39,11 +39,11 @@ typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const u32x4_t gu4_t;
 
-#define Q4G_WAVES 8
-#define Q4G_CH 8          // slices of x per LDS chunk (1024 k)
+#define Q4G_WAVES 16
+#define Q4G_CH 16         // slices of x per LDS chunk (2048 k)
 #define Q4G_SLICE 2112    // LDS bytes of one slice's operand: 2 KiB of fp8 + 64 scale bytes
 #define Q4G_SC 2048       // offset of the scale bytes within a slice
-#define Q4G_MAX_RG1 32    // stage-1 row groups (r_p / 64) the accumulators hold: 4 a wave
+#define Q4G_MAX_RG1 32    // stage-1 row groups (r_p / 64) the accumulators hold: 2 a wave
 #define Q4G_SCALE_A 125   // the fp4 signs' E8M0 scale 2^-2 (decode.hip's q4_signs)
 
 struct Q4GArgs {
@@ -68,6 +68,15 @@ __device__ __forceinline__ i32x8_t q4g_signs(uint32_t w, uint32_t c7) {
     av[3] = (int)(w | c7);
     av[4] = av[5] = av[6] = av[7] = 0;
     return av;
+}
+
+// A workgroup barrier that orders LDS only: HIP's __syncthreads() also
+// fences global memory, which waits for every load in flight -- the sign
+// words the rings hold ahead -- at each barrier.
+__device__ __forceinline__ void q4g_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // The B fragment and scale byte of lane (col, G) for one slice in LDS.
@@ -161,6 +170,17 @@ __device__ __forceinline__ float q4g_pair(float a) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));
 }
 
+// max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups holding a
+// column) of non-negative values: v_permlane16/32_swap of a register with
+// itself hands each lane the other half's value in one of its two results,
+// in the VALU.
+__device__ __forceinline__ float q4g_max4(float v) {
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float a = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
 // Stage 1's epilogue for row group g (acc: its four row tiles): t =
 // bf16((hi + lo) / 1.5), zero past r, written as stage 2's operand.  Lane
 // (col, G) of row tile rt holds rows 64g + 16rt + 4G + i of column col; both
@@ -168,7 +188,7 @@ __device__ __forceinline__ float q4g_pair(float a) {
 // + rt, element 4G + i: lane (col, G) writes four consecutive bytes -- the hi
 // bytes from an even column, the lo bytes from an odd one.  Row tiles rt and
 // rt + 2 form one scale block (runs u, u ^ 2): its maxima are over the lane's
-// eight values and the lanes 16 and 32 apart.
+// eight values and the lanes 16, 32 and 48 apart (q4g_max4).
 __device__ __forceinline__ void q4g_epilogue1(const f32x4_t acc[4], uint8_t *tbuf, size_t g, uint32_t r,
                                               int lane, uint16_t *t_out, size_t n, uint32_t r_p) {
     const int col = lane & 15, G = lane >> 4;
@@ -203,8 +223,7 @@ __device__ __forceinline__ void q4g_epilogue1(const f32x4_t acc[4], uint8_t *tbu
             for (int tt = 0; tt < 2; tt++)
                 *(uint2 *)(t_out + n * r_p + 64 * g + 16 * (pr + 2 * tt) + 4 * G) = make_uint2(tw[tt][0], tw[tt][1]);
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        amax = q4g_max4(amax);
         const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
         const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
         uint32_t hw[2];
@@ -221,8 +240,7 @@ __device__ __forceinline__ void q4g_epilogue1(const f32x4_t acc[4], uint8_t *tbu
 #pragma unroll
             for (int i = 0; i < 4; i++) rmax = fmaxf(rmax, fabsf(t[tt][i]));
         }
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 16, 64));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        rmax = q4g_max4(rmax);
         const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
         const float inv_lo = pow2f(-e_lo);
 #pragma unroll
@@ -287,7 +305,7 @@ __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArg
 // compiler's waits stay counted ones; only MFMAs sit under branches.
 #define Q4G_RING 4
 
-// NG1: stage-1 row groups a wave accumulates (2: r_p <= 1024, 4: r_p <=
+// NG1: stage-1 row groups a wave accumulates (1: r_p <= 1024, 2: r_p <=
 // 2048).  Stage 1's unit: one slice of the wave's NG1 row groups (their B
 // fragment read once); stage 2's unit: one slice of a pair of row groups.
 template <bool XF32, bool YBF16, int NG1>
@@ -307,8 +325,8 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
     const uint32_t nrg1 = a.n_rg1, ns1 = a.ns1;
     const int ng1 = wave < (int)nrg1 ? (int)((nrg1 - 1 - wave) / Q4G_WAVES) + 1 : 0;
     const uint32_t nch = (ns1 + Q4G_CH - 1) / Q4G_CH, nu1 = nch * Q4G_CH;
-    // x conversion: thread (token b = wave, slice j, run r) of each chunk
-    const int xb = tid >> 6, xj = (tid >> 3) & 7, xr = tid & 7;
+    // x conversion: thread (token b, slice j, run r) of each chunk, two waves a token
+    const int xb = tid >> 7, xj = (tid >> 3) & 15, xr = tid & 7;
     Q4GRun<XF32> run;
     const gu4_t *g1p[NG1];
 #pragma unroll
@@ -322,7 +340,8 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
     for (int q = 0; q < NG1; q++)
 #pragma unroll
         for (int rt = 0; rt < 4; rt++) acc1[q][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4_t ring1[Q4G_RING][NG1];
+    constexpr int R1 = NG1 == 1 ? 8 : 4;  // stage 1's ring: eight slices ahead for one group a wave
+    u32x4_t ring1[R1][NG1];
 #define Q4G_ISSUE1(U, SLOT)                                                             \
     {                                                                                   \
         uint32_t s_ = (U);                                                              \
@@ -333,13 +352,13 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
     // chunk 0 into buffer 0; the first units' sign words in flight
     q4g_load_run<XF32>(a, n0 + xb, 128 * xj + 16 * xr, run);
 #pragma unroll
-    for (int k = 0; k < Q4G_RING; k++) Q4G_ISSUE1((uint32_t)k, k)
+    for (int k = 0; k < R1; k++) Q4G_ISSUE1((uint32_t)k, k)
     q4g_store_run<XF32>(run, xbuf + xj * Q4G_SLICE, xb, xr);
-    __syncthreads();
+    q4g_lds_barrier();
 
     for (uint32_t c = 0; c < nch; c++) {
         const bool more = c + 1 < nch;
-        if (more) q4g_load_run<XF32>(a, n0 + xb, (size_t)(c + 1) * 1024 + 128 * xj + 16 * xr, run);
+        if (more) q4g_load_run<XF32>(a, n0 + xb, (size_t)(c + 1) * (128 * Q4G_CH) + 128 * xj + 16 * xr, run);
         const uint8_t *xs = xbuf + (c & 1) * (Q4G_CH * Q4G_SLICE);
         // B fragments one slice ahead (within the chunk: the next chunk's
         // buffer is written behind the barrier that ends this one)
@@ -348,7 +367,7 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
         q4g_bfrag(xs, lane, bvq[0], bsq[0]);
 #pragma unroll
         for (int j = 0; j < Q4G_CH; j++) {
-            const int slot = j % Q4G_RING, cur = j & 1;
+            const int slot = j % R1, cur = j & 1;
             const uint32_t s = c * Q4G_CH + j;
             if (j + 1 < Q4G_CH) q4g_bfrag(xs + (j + 1) * Q4G_SLICE, lane, bvq[cur ^ 1], bsq[cur ^ 1]);
             if (s < ns1) {
@@ -356,24 +375,13 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
                 for (int q = 0; q < NG1; q++)
                     if (q < ng1) q4g_mfma4(acc1[q], ring1[slot][q], bvq[cur], bsq[cur], c7);
             }
-            Q4G_ISSUE1(s + Q4G_RING, slot)
+            Q4G_ISSUE1(s + R1, slot)
         }
         if (more) q4g_store_run<XF32>(run, xbuf + ((c + 1) & 1) * (Q4G_CH * Q4G_SLICE) + xj * Q4G_SLICE, xb, xr);
-        __syncthreads();
+        q4g_lds_barrier();
     }
 #undef Q4G_ISSUE1
     (void)nu1;
-
-    // stage 1's epilogue: t -> stage 2's operand in LDS
-#pragma unroll
-    for (int q = 0; q < NG1; q++)
-        if (q < ng1) {
-            // tokens past N keep t to themselves
-            const size_t n = n0 + ((lane & 15) >> 1);
-            q4g_epilogue1(acc1[q], tbuf, (size_t)wave + Q4G_WAVES * q, a.r, lane, n < a.N ? a.t_out : nullptr, n,
-                          a.r_p);
-        }
-    __syncthreads();
 
     // ---- stage 2 --------------------------------------------------------
     // this wave's row groups wave + 8q, two at a time; units of one slice of
@@ -409,10 +417,26 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
         sv[w][0] = a.s1[row];                                                           \
         sv[w][1] = a.bias[row];                                                         \
     }
+    // the first units' sign words and pair 0's scales in flight under
+    // stage 1's epilogue
     if (total > 0) {
         Q4G_SCALES2(0u)
 #pragma unroll
         for (int k = 0; k < Q4G_RING; k++) Q4G_ISSUE2(k)
+    }
+
+    // stage 1's epilogue: t -> stage 2's operand in LDS
+#pragma unroll
+    for (int q = 0; q < NG1; q++)
+        if (q < ng1) {
+            // tokens past N keep t to themselves
+            const size_t n = n0 + ((lane & 15) >> 1);
+            q4g_epilogue1(acc1[q], tbuf, (size_t)wave + Q4G_WAVES * q, a.r, lane, n < a.N ? a.t_out : nullptr, n,
+                          a.r_p);
+        }
+    q4g_lds_barrier();
+
+    if (total > 0) {
         uint32_t p = 0, s = 0;
         i32x8_t bvq[2];
         int bsq[2];
@@ -504,10 +528,10 @@ int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
         std::lock_guard<std::mutex> lock(mu);
         if (dev < 64 && !((done >> dev) & 1)) {
             const uint32_t most = (2 * Q4G_CH + Q4G_MAX_RG1 / 2) * Q4G_SLICE + Q4G_WAVES * 1024;
-            for (const void *k : {(const void *)q4g_kernel<false, false, 2>, (const void *)q4g_kernel<false, true, 2>,
-                                  (const void *)q4g_kernel<true, false, 2>, (const void *)q4g_kernel<true, true, 2>,
-                                  (const void *)q4g_kernel<false, false, 4>, (const void *)q4g_kernel<false, true, 4>,
-                                  (const void *)q4g_kernel<true, false, 4>, (const void *)q4g_kernel<true, true, 4>})
+            for (const void *k : {(const void *)q4g_kernel<false, false, 1>, (const void *)q4g_kernel<false, true, 1>,
+                                  (const void *)q4g_kernel<true, false, 1>, (const void *)q4g_kernel<true, true, 1>,
+                                  (const void *)q4g_kernel<false, false, 2>, (const void *)q4g_kernel<false, true, 2>,
+                                  (const void *)q4g_kernel<true, false, 2>, (const void *)q4g_kernel<true, true, 2>})
                 QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)most));
             done |= 1ull << dev;
         }
@@ -535,17 +559,17 @@ int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.r_p = (uint32_t)L->r_p;
     const dim3 grid((unsigned)div_ceil(N, 8)), block(64 * Q4G_WAVES);
 #define Q4G_LAUNCH(XF, YB, NG) hipLaunchKernelGGL((q4g_kernel<XF, YB, NG>), grid, block, lds, s, a)
-    const bool small = a.n_rg1 <= 2 * Q4G_WAVES;
+    const bool small = a.n_rg1 <= Q4G_WAVES;
     if (small) {
+        if (xf32 && ybf16) Q4G_LAUNCH(true, true, 1);
+        else if (xf32) Q4G_LAUNCH(true, false, 1);
+        else if (ybf16) Q4G_LAUNCH(false, true, 1);
+        else Q4G_LAUNCH(false, false, 1);
+    } else {
         if (xf32 && ybf16) Q4G_LAUNCH(true, true, 2);
         else if (xf32) Q4G_LAUNCH(true, false, 2);
         else if (ybf16) Q4G_LAUNCH(false, true, 2);
         else Q4G_LAUNCH(false, false, 2);
-    } else {
-        if (xf32 && ybf16) Q4G_LAUNCH(true, true, 4);
-        else if (xf32) Q4G_LAUNCH(true, false, 4);
-        else if (ybf16) Q4G_LAUNCH(false, true, 4);
-        else Q4G_LAUNCH(false, false, 4);
     }
 #undef Q4G_LAUNCH
     QBK_HIP(hipGetLastError());
