@@ -750,6 +750,13 @@ def main():
     import quantibbler_amd as qa
 
     ctx = qa.GpuContext(0)
+    if args.calibrate_traffic:
+        a = torch.ones(1 << 26, dtype=torch.int32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        del a, b
     if args.only:
         if args.only == "gemm":
             layers, _ = make_layers(qa, ctx, np, 1, seed=1)
@@ -769,13 +776,6 @@ def main():
             res = bench_cfg3(qa, ctx, torch, np)
         print(json.dumps({"only": args.only, "result": res}), flush=True)
         return
-    if args.calibrate_traffic:
-        a = torch.ones(1 << 26, dtype=torch.int32, device="cuda")
-        b = torch.empty_like(a)
-        for _ in range(3):
-            torch.neg(a, out=b)
-        torch.cuda.synchronize()
-        del a, b
     log(f"building {args.layers} config-1 layers ...")
     layers, host = make_layers(qa, ctx, np, args.layers, seed=1)
     log("decode sweep ...")
@@ -850,7 +850,7 @@ def main():
             "avg_launch_source": "the timed step (two HIP events on the launch stream) times the "
                                  "kernel's share of the step, measured over the same steps run again "
                                  "with an event between consecutive launches",
-            "event_interval_ms": round(d["evt_ms"][dom - 1], 4),
+            "event_interval_ms": round(d["evt_ms"][dom], 4),
         },
         "cpu_baseline": cpu,
         "extra": extra,
