@@ -540,13 +540,16 @@ def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
     sign_bytes = act_bytes = 0
     for li in range(n_layers):
         for name, m, n, r in CFG3:
+            # fp16 scales (configs[2]: "packed signs plus fp16 scales"), which the
+            # decode streams as fp16
             L = qa.FactorLayer.from_rows(ctx, m, n, r, random_rows(np, rng, m, r), random_rows(np, rng, r, n),
-                                         np.exp(0.5 * rng.standard_normal(m)).astype(np.float32),
-                                         np.exp(0.5 * rng.standard_normal(n)).astype(np.float32), None)
+                                         np.exp(0.5 * rng.standard_normal(m)).astype(np.float16).astype(np.float32),
+                                         np.exp(0.5 * rng.standard_normal(n)).astype(np.float16).astype(np.float32),
+                                         None)
             groups.setdefault((m, n, r), []).append(L)
             ordered.append(L)
             sign_bytes += (m * r + 7) // 8 + (n * r + 7) // 8
-            act_bytes += 2 * n + 2 * m + 4 * m + 4 * n  # x, y (bf16), s1, s2 (f32)
+            act_bytes += 2 * n + 2 * m + 2 * m + 2 * n  # x, y (bf16), s1, s2 (fp16)
         if (li + 1) % 8 == 0:
             log(f"  cfg3: uploaded {li + 1}/{n_layers} decoder layers")
     st = torch.cuda.current_stream()
@@ -580,7 +583,7 @@ def bench_cfg3(qa, ctx, torch, np, n_layers=32, steps=100, prefill_b=2048):
            "bytes_streamed_per_token": total,
            "bytes_note": "frac and GB/s count the reference's v2 streams (signs + fp16 s1/s2/bias, "
                          "14,995,624 B a decoder layer); bytes_streamed_per_token is what this "
-                         "build reads (signs, scales as stored, bf16 x and y)"}
+                         "build reads (signs, fp16 s1 and s2, bf16 x and y; the bias is zero and not read)"}
     log(f"  cfg3 decode: {ms:.3f} ms/token over {n_layers} layers, {out['GB/s']} GB/s")
     # prefill: one decoder layer's seven projections at B = prefill_b
     flop = 0

@@ -71,6 +71,8 @@ __device__ __forceinline__ Q4Layer q4_entry(const Q4Args &a, uint32_t li) {
     L.s_in = lp->s_in;
     L.s_out = lp->s_out;
     L.bias = lp->bias;
+    L.s_out_h = lp->s_out_h;
+    L.bias_h = lp->bias_h;
     L.rows_p = lp->rows_p;
     L.rows_valid = lp->rows_valid;
     L.ns = lp->ns;
@@ -162,7 +164,8 @@ __global__ void __launch_bounds__(256) q4_prep_kernel(Q4Args a) {
 // global slice t / 8, and s2cat holds the layers' s2 concatenated the same
 // way -- no per-layer table lookup ahead of the loads (one dependent memory
 // round trip instead of two).
-__global__ void __launch_bounds__(256) q4_prep_flat_kernel(const uint16_t *x, const float *s2cat, uint8_t *op,
+template <bool S2H>
+__global__ void __launch_bounds__(256) q4_prep_flat_kernel(const uint16_t *x, const void *s2cat, uint8_t *op,
                                                            uint8_t *sc, uint32_t n_runs) {
     const uint32_t t0 = blockIdx.x * 256 + threadIdx.x;
     const bool live = t0 < n_runs;
@@ -171,9 +174,24 @@ __global__ void __launch_bounds__(256) q4_prep_flat_kernel(const uint16_t *x, co
     const uint32_t t = live ? t0 : n_runs - 8 + (t0 & 7);
     const size_t k0 = (size_t)t * 16;
     const gu32x4_t *xs = (const gu32x4_t *)(x + k0);
-    const gu32x4_t *ss = (const gu32x4_t *)(s2cat + k0);
     const u32x4_t xr[2] = {xs[0], xs[1]};
-    const u32x4_t sr[4] = {ss[0], ss[1], ss[2], ss[3]};
+    u32x4_t sr[4];
+    if (S2H) {  // fp16 s2, widened exactly
+        const gu32x4_t *ss = (const gu32x4_t *)((const uint16_t *)s2cat + k0);
+        const u32x4_t h[2] = {ss[0], ss[1]};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t w0 = h[q >> 1][2 * (q & 1)], w1 = h[q >> 1][2 * (q & 1) + 1];
+            sr[q] = u32x4_t{__float_as_uint(h16_to_f32(w0 & 0xffff)), __float_as_uint(h16_to_f32(w0 >> 16)),
+                            __float_as_uint(h16_to_f32(w1 & 0xffff)), __float_as_uint(h16_to_f32(w1 >> 16))};
+        }
+    } else {
+        const gu32x4_t *ss = (const gu32x4_t *)((const float *)s2cat + k0);
+        sr[0] = ss[0];
+        sr[1] = ss[1];
+        sr[2] = ss[2];
+        sr[3] = ss[3];
+    }
     float z[16];
     q4_run_z(xr, sr, z);
     uint32_t hw[4], lw[4];
@@ -430,8 +448,13 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     if (STAGE == 2) {
         const size_t row = rgc * 64 + lane;
         const size_t rc = row < L.rows_valid ? row : L.rows_valid - 1;
-        so = ((gf32_t *)L.s_out)[rc];
-        if (L.bias) bi = ((gf32_t *)L.bias)[rc];
+        if (L.s_out_h) {  // fp16 scales (the layer's are fp16 values): half the bytes
+            so = h16_to_f32(((const __attribute__((address_space(1))) uint16_t *)L.s_out_h)[rc]);
+            if (L.bias_h) bi = h16_to_f32(((const __attribute__((address_space(1))) uint16_t *)L.bias_h)[rc]);
+        } else {
+            so = ((gf32_t *)L.s_out)[rc];
+            if (L.bias) bi = ((gf32_t *)L.bias)[rc];
+        }
     }
 
     // Padding is not streamed.  A row group wholly past the valid rows (the
@@ -620,6 +643,8 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
         b.bits = L->u_q4;
         b.s_out = L->s1;
         b.bias = L->bias_zero ? nullptr : L->bias;
+        b.s_out_h = L->scales_f16 ? L->s1h : nullptr;
+        b.bias_h = L->scales_f16 && !L->bias_zero ? L->biash : nullptr;
         b.rows_p = (uint32_t)L->dout_p;
         b.rows_valid = (uint32_t)L->dout;
         b.ns = (uint32_t)ns2;
@@ -658,7 +683,7 @@ static void q4_build(const qbk_factor *const *layers, size_t n, size_t batch, in
 // the layers' s2 concatenated (null when some din is not a multiple of 128).
 static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32_t *wg1,
                     const uint32_t *wg2, const float *s2cat, const void *x, bool xf32, void *y, bool ybf16,
-                    void *ws, hipStream_t s, const float *resid = nullptr) {
+                    void *ws, hipStream_t s, const float *resid = nullptr, const uint16_t *s2cat_h = nullptr) {
     char *w = (char *)ws;
     Q4Args a{};
     a.c7 = 0x77777777u;
@@ -687,8 +712,12 @@ static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32
     if (phase == 1) {
         if (s2cat && !xf32 && G.batch == 1 && G.din_mult128 && (uintptr_t)x % 16 == 0) {
             const uint32_t n_runs = (uint32_t)(G.ns1_tot * 8);
-            hipLaunchKernelGGL(q4_prep_flat_kernel, dim3((unsigned)div_ceil(n_runs, 256)), dim3(256), 0, s,
-                               (const uint16_t *)x, s2cat, a.op, a.sc, n_runs);
+            if (s2cat_h)
+                hipLaunchKernelGGL(q4_prep_flat_kernel<true>, dim3((unsigned)div_ceil(n_runs, 256)), dim3(256), 0,
+                                   s, (const uint16_t *)x, (const void *)s2cat_h, a.op, a.sc, n_runs);
+            else
+                hipLaunchKernelGGL(q4_prep_flat_kernel<false>, dim3((unsigned)div_ceil(n_runs, 256)), dim3(256), 0,
+                                   s, (const uint16_t *)x, (const void *)s2cat, a.op, a.sc, n_runs);
             QBK_HIP(hipGetLastError());
             return QBK_OK;
         }
@@ -758,7 +787,8 @@ int q4_run(const qbk_factor *L, size_t batch, const void *x, bool xf32, void *y,
     q4_build(&L, 1, batch, L->num_cus, tab, G);  // geometry; the device table is L->q4_tab
     const float *s2cat = G.din_mult128 ? L->s2 : nullptr;  // one layer: its own s2
     for (int ph = 1; ph <= Q4_PHASES; ph++) {
-        int rc = q4_phase(ph, G, L->q4_tab, nullptr, nullptr, s2cat, x, xf32, y, ybf16, ws, s);
+        int rc = q4_phase(ph, G, L->q4_tab, nullptr, nullptr, s2cat, x, xf32, y, ybf16, ws, s, nullptr,
+                          s2cat && L->scales_f16 ? L->s2h : nullptr);
         if (rc) return rc;
     }
     return QBK_OK;
@@ -796,6 +826,7 @@ struct qbk_factor_set {
     Q4Layer *tab;          // device: [0, n) stage 1, [n, 2n) stage 2; then the
     uint32_t *wg1, *wg2;   // per-workgroup layer tables (same allocation)
     float *s2cat;          // device: the layers' s2 concatenated (every din % 128 == 0), else null
+    uint16_t *s2cat_h;     // device: the same as fp16 when every layer's scales are fp16 values, else null
     G32SetLayer *g32tab;   // device: the set on the prefill GEMM, [n] stage 1 then [n] stage 2
     Q4Geom geom;           // batch 1
     std::vector<const qbk_factor *> layers;
@@ -807,7 +838,8 @@ namespace qbk {
 // form is bf16 in and out): x the concatenation of the layers' inputs.
 int q4_set_run(const qbk_factor_set *S, const void *x, bool xf32, void *y, bool ybf16, void *ws, hipStream_t s) {
     for (int ph = 1; ph <= Q4_PHASES; ph++) {
-        int rc = q4_phase(ph, S->geom, S->tab, S->wg1, S->wg2, S->s2cat, x, xf32, y, ybf16, ws, s);
+        int rc = q4_phase(ph, S->geom, S->tab, S->wg1, S->wg2, S->s2cat, x, xf32, y, ybf16, ws, s, nullptr,
+                          S->s2cat_h);
         if (rc) return rc;
     }
     return QBK_OK;
@@ -910,6 +942,7 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
     S->wg1 = (uint32_t *)((char *)S->tab + tab_bytes);
     S->wg2 = S->wg1 + S->geom.n_wg1;
     S->s2cat = nullptr;
+    S->s2cat_h = nullptr;
     e1 = hipMemcpy(S->tab, h.data(), tab_bytes, hipMemcpyHostToDevice);
     if (e1 == hipSuccess) e1 = hipMemcpy(S->wg1, wl.data(), wl.size() * 4, hipMemcpyHostToDevice);
     if (e1 == hipSuccess && S->geom.din_mult128) {
@@ -920,6 +953,16 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
         if (e1 != hipSuccess) S->s2cat = nullptr;
         for (size_t i = 0, o = 0; e1 == hipSuccess && i < n; o += layers[i]->din, i++)
             e1 = hipMemcpy(S->s2cat + o, layers[i]->s2, layers[i]->din * sizeof(float), hipMemcpyDeviceToDevice);
+        // and as fp16 when every layer's scales are fp16 values
+        bool f16 = true;
+        for (size_t i = 0; i < n; i++) f16 = f16 && layers[i]->scales_f16;
+        if (e1 == hipSuccess && f16) {
+            e1 = hipMalloc((void **)&S->s2cat_h, n_in * sizeof(uint16_t));
+            if (e1 != hipSuccess) S->s2cat_h = nullptr;
+            for (size_t i = 0, o = 0; e1 == hipSuccess && i < n; o += layers[i]->din, i++)
+                e1 = hipMemcpy(S->s2cat_h + o, layers[i]->s2h, layers[i]->din * sizeof(uint16_t),
+                               hipMemcpyDeviceToDevice);
+        }
     }
     S->g32tab = nullptr;
     if (e1 == hipSuccess) {
@@ -933,6 +976,7 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
     if (e1 != hipSuccess) {
         (void)hipFree(S->tab);
         if (S->s2cat) (void)hipFree(S->s2cat);
+        if (S->s2cat_h) (void)hipFree(S->s2cat_h);
         if (S->g32tab) (void)hipFree(S->g32tab);
         delete S;
         return fail(QBK_ERR_DEVICE, fmt("hipMemcpy failed: %s", hipGetErrorString(e1)));
@@ -948,6 +992,7 @@ void qbk_factor_set_destroy(qbk_factor_set *S) {
     (void)hipSetDevice(S->device);
     (void)hipFree(S->tab);
     if (S->s2cat) (void)hipFree(S->s2cat);
+    if (S->s2cat_h) (void)hipFree(S->s2cat_h);
     if (S->g32tab) (void)hipFree(S->g32tab);
     (void)hipSetDevice(cur);
     delete S;
@@ -966,7 +1011,7 @@ int qbk_factor_set_stage_dev(qbk_ctx *ctx, const qbk_factor_set *S, int stage, c
         return fail(QBK_ERR_VALIDATION, fmt("workspace of %zu bytes is smaller than the %zu this call needs",
                                             workspace_size, S->geom.bytes));
     return q4_phase(stage, S->geom, S->tab, S->wg1, S->wg2, S->s2cat, x, false, y, true, workspace,
-                    (hipStream_t)stream);
+                    (hipStream_t)stream, nullptr, S->s2cat_h);
 }
 
 size_t qbk_factor_set_workspace_size_batch(const qbk_factor_set *S, size_t n) {

@@ -113,6 +113,45 @@ __global__ void q4_to_rows(const uint32_t *q4, size_t n_rows, size_t n_bits, siz
     rows[idx] = (uint8_t)byte;
 }
 
+// v's fp16 bits when v is an fp16 value (zero, a normal or subnormal fp16
+// magnitude, or an infinity), else false.  The conversion is exact, so no
+// rounding is involved.
+static bool f32_to_f16_exact(float v, uint16_t *out) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u, ex = (u >> 23) & 0xff, man = u & 0x7fffffu;
+    if (ex == 0xff) {
+        if (man) return false;  // NaN: kept in f32
+        *out = (uint16_t)(sign | 0x7c00u);
+        return true;
+    }
+    if (ex == 0 && man == 0) {
+        *out = (uint16_t)sign;
+        return true;
+    }
+    if (ex == 0) return false;  // f32 subnormals lie below fp16's range
+    const int e = (int)ex - 127;
+    if (e > 15) return false;
+    if (e >= -14) {
+        if (man & 0x1fffu) return false;
+        *out = (uint16_t)(sign | (uint32_t)(e + 15) << 10 | (man >> 13));
+        return true;
+    }
+    if (e < -24) return false;
+    // fp16 subnormal: m * 2^-24 with the implicit bit shifted in
+    const uint32_t full = man | 0x800000u, shift = (uint32_t)(13 + (-14 - e));
+    if (full & ((1u << shift) - 1)) return false;
+    *out = (uint16_t)(sign | (full >> shift));
+    return true;
+}
+
+static bool f16_copy(const float *v, size_t n, std::vector<uint16_t> &h) {
+    h.resize(n);
+    for (size_t i = 0; i < n; i++)
+        if (!f32_to_f16_exact(v[i], &h[i])) return false;
+    return true;
+}
+
 static int dev_upload(qbk_factor *L, void **dst, const void *src, size_t n) {
     void *p = nullptr;
     QBK_HIP(hipMalloc(&p, n ? n : 16));
@@ -179,6 +218,19 @@ static int build_layer(qbk_ctx *ctx, size_t dout, size_t din, size_t r, const ui
     UP(s1, s1, dout * 4);
     UP(s2, s2, din * 4);
     UP(bias, bias ? bias : zb.data(), dout * 4);
+    // fp16 copies where the scales are fp16 values (v2 qpk1 streams): the
+    // decode GEMV then streams half the scale bytes
+    {
+        std::vector<uint16_t> h1, h2, hb;
+        L->scales_f16 = f16_copy(s1, dout, h1) && f16_copy(s2, din, h2) &&
+                        f16_copy(bias ? bias : zb.data(), dout, hb);
+        L->s1h = L->s2h = L->biash = nullptr;
+        if (L->scales_f16) {
+            UP(s1h, h1.data(), dout * 2);
+            UP(s2h, h2.data(), din * 2);
+            UP(biash, hb.data(), dout * 2);
+        }
+    }
     Q4Layer qtab[2];
     q4_layer_entries(L, qtab);
     UP(q4_tab, qtab, sizeof qtab);

@@ -33,6 +33,7 @@ struct Q4Layer {
     const uint32_t *bits;        // this stage's signs in the fp4 decode layout
     const float *s_in;           // stage 1: s2
     const float *s_out, *bias;   // stage 2: s1, bias
+    const uint16_t *s_out_h, *bias_h;  // stage 2: the same as fp16 when every value is one, else null
     uint32_t rows_p, rows_valid; // this stage's output rows: padded (to 128), valid
     uint32_t ns, k_valid;        // this stage's 128-k slices, valid K
     uint32_t slice0;             // slices of this stage held by the layers before this one
@@ -53,6 +54,8 @@ struct qbk_factor {
     size_t din_q, r_q;                // K of the fp4 decode layout: multiples of 128
     uint32_t *vt_q4, *u_q4;           // [r_p/64][din_q/128][64][4], [dout_p/64][r_q/128][64][4]
     float *s1, *s2, *bias;            // dout, din, dout (zeros when absent)
+    bool scales_f16;                  // every s1, s2 and bias value is an fp16 value (a v2 qpk1 stream's)
+    uint16_t *s1h, *s2h, *biash;      // then the same as fp16, the copies the decode GEMV streams (else null)
     bool bias_zero;                   // bias absent or all +0.0 (the decode skips its load)
     qbk::Q4Layer *q4_tab;             // device Q4Layer[2] of this layer alone: stage 1, stage 2
     std::vector<void *> allocs;

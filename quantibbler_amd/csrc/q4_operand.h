@@ -24,6 +24,9 @@ __device__ __forceinline__ int e8m0_of(float amax) {
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
+// fp16 bits (the low half of h) -> f32, exact.
+__device__ __forceinline__ float h16_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
 // The fp4 signs enter the MFMA as +-1.5 (e2m1 6 at E8M0 scale 2^-2), so a
 // sum s comes out as 1.5 s.  Multiplying by c = 11184811 * 2^-24, the float
 // nearest 2/3, undoes it: 1.5 c = 1 + 2^-25, so for any float s, (1.5 s) * c

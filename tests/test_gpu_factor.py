@@ -396,16 +396,23 @@ def set_decode(S, x, dout):
     return yd.cpu().numpy().view(np.uint16)
 
 
+@pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("dout,din,r,n", [(512, 1024, 200, 5), (300, 640, 200, 7), (96, 128, 64, 3)])
-def test_set_decode_matches_single_layers(ctx, orc, dout, din, r, n):
+def test_set_decode_matches_single_layers(ctx, orc, dout, din, r, n, f16):
     """Integer-exact set decode: bit-identical to the oracle and to the
     single-layer path (steps of fewer than 8 slices where din/128 or r_p/128
-    is small)."""
+    is small).  With s1, s2 and bias fp16 values (f16, as a v2 qpk1 stream
+    holds them) the decode streams the layers' fp16 copies: s2 in the
+    operand prep, s1 and bias in stage 2's epilogue."""
     from quantibbler_amd import FactorSet
 
-    say("factor set decode", dout, din, r, n)
+    say("factor set decode", dout, din, r, n, "fp16 scales" if f16 else "")
     rng = np.random.default_rng(77 + din)
     Ls = [make_layer(orc, rng, dout, din, r, integer=True) for _ in range(n)]
+    if f16:
+        for L in Ls:
+            for k in ("s1", "s2", "bias"):
+                L[k] = L[k].astype(np.float16).astype(np.float32)
     layers = [upload(ctx, L) for L in Ls]
     S = FactorSet(ctx, layers)
     x = orc.f32_to_bf16_fast(rng.integers(-2, 3, (n, din)).astype(np.float32))
