@@ -23,6 +23,7 @@
 //   3. q4_gemv_kernel<2>: y = bf16(Ub t) * s1 + bias.
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "factor_internal.h"
@@ -51,7 +52,7 @@ typedef __attribute__((address_space(4))) const Q4Layer cq4layer_t;
 // One launch over a set of layers.
 struct Q4Args {
     const Q4Layer *layers;       // this stage's table entries
-    const uint32_t *wg_layer;    // GEMV: layer of each workgroup (null for one layer)
+    const uint32_t *wg_layer;    // GEMV: (layer, first row group) of each workgroup (null for one layer)
     uint32_t n_layers, n_wg;     // layers; workgroups doing work (GEMV)
     int batch, ncol;             // ncol = 2 * batch
     const void *act;             // stage 1 prep: x (bf16, or f32)
@@ -86,12 +87,21 @@ __device__ __forceinline__ Q4Layer q4_entry(const Q4Args &a, uint32_t li) {
     return L;
 }
 
-// The layer of workgroup wgi: one scalar load from the per-workgroup table
-// (so that a workgroup's sign loads wait on two dependent scalar loads, not
-// on a search).
-__device__ __forceinline__ uint32_t q4_layer_of(const Q4Args &a, uint32_t wgi) {
-    if (a.n_layers == 1) return 0;
-    return ((__attribute__((address_space(4))) const uint32_t *)a.wg_layer)[wgi];
+// The layer and first row group of workgroup wgi: one scalar load from the
+// per-workgroup table (so that a workgroup's sign loads wait on two
+// dependent scalar loads, not on a search); one layer: its row groups in
+// order.
+__device__ __forceinline__ void q4_work_of(const Q4Args &a, uint32_t wgi, uint32_t rg_per_wg, uint32_t &li,
+                                           uint32_t &rg0) {
+    if (a.n_layers == 1) {
+        li = 0;
+        rg0 = wgi * rg_per_wg;
+        return;
+    }
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t e = ((__attribute__((address_space(4))) const u32x2_t *)a.wg_layer)[wgi];
+    li = e[0];
+    rg0 = e[1];
 }
 
 // x -> stage 1's fp8 operand.  Workgroup (x, layer); one thread per run of
@@ -296,6 +306,23 @@ __device__ __forceinline__ void q4_step_g(f32x4_t acc[NCG][4], const uint4 &w4u,
     }
 }
 
+// The maximum of v over the 32 lanes whose ids differ from this lane's only
+// in bits 0-3 and 5 (one scale block of stage 2's operand), with no LDS
+// round trip: the quad by two DPP quad permutations (l ^ 1, l ^ 2), the
+// 16-lane row by two DPP row rotations (by 4 and by 8 lanes, which between
+// them reach every quad of the row), and the lane 32 apart by
+// v_permlane32_swap.  Every lane of the wave must be active.
+#define Q4_DPP_MAX(v, ctrl) fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false)))
+__device__ __forceinline__ float q4_block_max32(float v) {
+    v = Q4_DPP_MAX(v, 0xB1);   // quad_perm [1, 0, 3, 2]
+    v = Q4_DPP_MAX(v, 0x4E);   // quad_perm [2, 3, 0, 1]
+    v = Q4_DPP_MAX(v, 0x124);  // row_ror 4
+    v = Q4_DPP_MAX(v, 0x128);  // row_ror 8
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+}
+#undef Q4_DPP_MAX
+
 // Epilogue of one 64-row group, one row per lane: the accumulators are
 // transposed through the wave's LDS region T [ncol][64] (lane (col, g) holds
 // rows 16rt + 4g + i of column col), then lane l finishes row rg*64 + l of
@@ -341,21 +368,11 @@ __device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, cons
             }
             continue;
         }
-        float amax = fabsf(t);
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 8, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        const float amax = q4_block_max32(fabsf(t));
         const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
         const int hw = __builtin_amdgcn_cvt_pk_fp8_f32(t * pow2f(-e_hi), 0.0f, 0, false);
         const float r = t - __builtin_amdgcn_cvt_f32_fp8(hw, 0) * pow2f(e_hi);  // exact residual
-        float rmax = fabsf(r);
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 64));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 4, 64));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 8, 64));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        const float rmax = q4_block_max32(fabsf(r));
         const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
         const int lw = __builtin_amdgcn_cvt_pk_fp8_f32(r * pow2f(-e_lo), 0.0f, 0, false);
         const int q = (lane >> 4) & 1, h = lane >> 5;
@@ -411,10 +428,11 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     const uint32_t xcd = blockIdx.x & 7, per_x = gridDim.x >> 3;
     const uint32_t wgi = xcd * per_x + (blockIdx.x >> 3);
     if (wgi >= a.n_wg) return;  // padding workgroup (the whole group leaves)
-    const uint32_t li = q4_layer_of(a, wgi);
-    const Q4Layer L = q4_entry(a, li);
     constexpr int RG_PER_WG = Q4_NW(KSPLIT) / KSPLIT;
-    const size_t rg = (size_t)(wgi - L.wg0) * RG_PER_WG + wave / KSPLIT;
+    uint32_t li, rg0;
+    q4_work_of(a, wgi, RG_PER_WG, li, rg0);
+    const Q4Layer L = q4_entry(a, li);
+    const size_t rg = (size_t)rg0 + wave / KSPLIT;
     const int ks = wave % KSPLIT;
     const size_t n_rg = L.rows_p / 64, ns = L.ns;
     const size_t per = (ns + KSPLIT - 1) / KSPLIT;
@@ -887,6 +905,42 @@ size_t q4_set_workspace_batch(const qbk_factor_set *S, size_t n) {
     return G.bytes;
 }
 
+// The per-workgroup table of a set's GEMV launch: (layer, first row group)
+// of each workgroup.  The kernel hands XCD x the contiguous workgroups [x
+// per_x, (x + 1) per_x) (per_x = the grid's eighth); inside each such range
+// the workgroups are ordered by the slices they stream, longest first (at
+// config 3 the down projection's row groups stream 112 slices, the others'
+// 32, and in layer order the last of them started when most of the launch
+// had ended), ties kept in layer order; row groups wholly past a layer's
+// valid rows stream nothing and go last.
+static void q4_wg_table(const Q4Layer *tab, size_t n, uint32_t n_wg, uint32_t rg_per_wg, uint32_t *out) {
+    struct Unit {
+        uint32_t li, rg0;
+        uint64_t cost;
+    };
+    std::vector<Unit> u(n_wg);
+    for (size_t i = 0; i < n; i++) {
+        const uint32_t e = i + 1 < n ? tab[i + 1].wg0 : n_wg;
+        for (uint32_t w = tab[i].wg0; w < e; w++) {
+            const uint32_t rg0 = (w - tab[i].wg0) * rg_per_wg;
+            uint64_t live = 0;
+            for (uint32_t r = rg0; r < rg0 + rg_per_wg && r < tab[i].rows_p / 64; r++)
+                live += (uint64_t)r * 64 < tab[i].rows_valid;
+            u[w] = Unit{(uint32_t)i, rg0, live * tab[i].ns};
+        }
+    }
+    const uint32_t per_x = (uint32_t)(round_up(n_wg, 8) / 8);
+    for (uint32_t x = 0; x < 8; x++) {
+        const uint32_t b = x * per_x, e = b + per_x < n_wg ? b + per_x : n_wg;
+        if (b < e)
+            std::stable_sort(u.begin() + b, u.begin() + e, [](const Unit &p, const Unit &q) { return p.cost > q.cost; });
+    }
+    for (uint32_t w = 0; w < n_wg; w++) {
+        out[2 * w] = u[w].li;
+        out[2 * w + 1] = u[w].rg0;
+    }
+}
+
 int q4_set_run_batch(const qbk_factor_set *S, size_t n, const void *x, bool xf32, void *y, bool ybf16, void *ws,
                      hipStream_t s) {
     if (n == 1) return q4_set_run(S, x, xf32, y, ybf16, ws, s);
@@ -925,14 +979,10 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
         delete S;
         return fail(QBK_ERR_VALIDATION, "layer set too large for one decode launch");
     }
-    // layer of every workgroup of the two GEMV launches
-    std::vector<uint32_t> wl(S->geom.n_wg1 + S->geom.n_wg2);
-    for (size_t i = 0; i < n; i++) {
-        const uint32_t e1 = i + 1 < n ? h[i + 1].wg0 : S->geom.n_wg1;
-        const uint32_t e2 = i + 1 < n ? h[n + i + 1].wg0 : S->geom.n_wg2;
-        for (uint32_t w = h[i].wg0; w < e1; w++) wl[w] = (uint32_t)i;
-        for (uint32_t w = h[n + i].wg0; w < e2; w++) wl[S->geom.n_wg1 + w] = (uint32_t)i;
-    }
+    // (layer, first row group) of every workgroup of the two GEMV launches
+    std::vector<uint32_t> wl(2 * (S->geom.n_wg1 + S->geom.n_wg2));
+    q4_wg_table(h.data(), n, S->geom.n_wg1, Q4_NW(S->geom.ks1) / S->geom.ks1, wl.data());
+    q4_wg_table(h.data() + n, n, S->geom.n_wg2, Q4_NW(S->geom.ks2) / S->geom.ks2, wl.data() + 2 * S->geom.n_wg1);
     const size_t tab_bytes = 2 * n * sizeof(Q4Layer);
     hipError_t e1 = hipMalloc((void **)&S->tab, tab_bytes + wl.size() * 4);
     if (e1 != hipSuccess) {
@@ -940,7 +990,7 @@ int qbk_factor_set_create(qbk_ctx *ctx, const qbk_factor *const *layers, size_t 
         return fail(QBK_ERR_DEVICE, fmt("hipMalloc failed: %s", hipGetErrorString(e1)));
     }
     S->wg1 = (uint32_t *)((char *)S->tab + tab_bytes);
-    S->wg2 = S->wg1 + S->geom.n_wg1;
+    S->wg2 = S->wg1 + 2 * S->geom.n_wg1;
     S->s2cat = nullptr;
     S->s2cat_h = nullptr;
     e1 = hipMemcpy(S->tab, h.data(), tab_bytes, hipMemcpyHostToDevice);
