@@ -225,6 +225,10 @@ __global__ void __launch_bounds__(256) q4_prep_flat_kernel(const uint16_t *x, co
 // divides by 1.5: exact whenever the f32 sum is (1.5 * sum then needs one
 // more significant bit).
 #define Q4_SCALE_A 125
+
+// sched_barrier mask: SALU, VALU, LDS and transcendental instructions may
+// cross; MFMAs and vector memory loads and stores may not.
+#define Q4_SCHED_PIN 0x486
 __device__ __forceinline__ i32x8_t q4_signs(uint32_t w, uint32_t c7) {
     i32x8_t av;
     av[0] = (int)((w << 3) | c7);
@@ -389,12 +393,14 @@ __device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, cons
     }
 }
 
-// LDS bytes of one wave's region: the staged operand of Q4_U slices (NCOL
-// columns), their scales (one dword per lane), a zero slot, and room for the
-// epilogue's transpose.
+// LDS bytes of one wave's region.  NCOL > 0: two buffers, each the staged
+// operand of Q4_U slices (NCOL columns) and their scales (one dword per
+// lane), then a zero slot; the epilogue's transpose and the K split's
+// partial sums (4 KiB a wave) reuse the buffers.  NCOL == 0: the transpose.
 __host__ __device__ constexpr uint32_t q4_wave_lds(int ncol) {
-    return ncol > 0 ? (uint32_t)(Q4_U * 4 * ncol * 32 + 256 + 48) : 16 * 64 * 4;
+    return ncol > 0 ? (uint32_t)(2 * (Q4_U * 4 * ncol * 32 + 256) + 48) : 16 * 64 * 4;
 }
+static_assert(q4_wave_lds(2) >= 4 * 64 * 16, "a wave's partial sums fit its region");
 
 // Decode GEMV.  Workgroup = 4 waves (8 at KSPLIT 8); KSPLIT waves share a
 // 64-row group and split its slices (Q4_NW / KSPLIT row groups per
@@ -448,9 +454,11 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     const uint8_t *gb = a.op + (size_t)L.slice0 * 4 * ncol * 32;  // this layer's operand
     const uint8_t *gs = a.sc + (size_t)L.slice0 * 4 * ncol;
 
-    // staged operand offsets within the wave's region (slice j of the step)
+    // staged operand offsets within the wave's region (slice j of the step;
+    // buffer b at b * RB)
     constexpr uint32_t OPB = NCOL > 0 ? Q4_U * 4 * NCOL * 32 : 0;
-    constexpr uint32_t ZS = OPB + 256;
+    constexpr uint32_t RB = OPB + 256;
+    constexpr uint32_t ZS = 2 * RB;
     const uint32_t slot0 = (uint32_t)(g * ncol + col);
     const uint32_t bo0 = bcol ? slot0 * 32 : ZS, bstep = bcol ? 4 * ncol * 32 : 0;
     const uint32_t so0 = bcol ? OPB + slot0 : ZS + 32, sstep = bcol ? 4 * ncol : 0;
@@ -492,72 +500,160 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     for (int cg = 0; cg < NCG; cg++)
 #pragma unroll
         for (int rt = 0; rt < 4; rt++) acc[cg][rt] = f32x4_t{0, 0, 0, 0};
-    for (size_t sb = s0; sb < (rows_dead ? s0 : s1); sb += Q4_U) {
-        const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
-        // a step's operand: Q4_U slices x 4 lane groups x NCOL columns x 32 B,
-        // SQ 16-byte words per lane
-        constexpr int SQ = NCOL > 0 ? Q4_U * NCOL / 8 : 1;
-        static_assert(NCOL == 0 || Q4_U * NCOL % 8 == 0, "whole 16-byte words per lane");
-        uint4 stg[SQ];
-        uint32_t stgs = 0;
-        if (NCOL > 0) {
-            // operand of slices sb..sb+nsl-1: SQ uint4 + one dword of scales per lane
+    if constexpr (NCOL == 2 && KSPLIT <= 4) {
+        // Batch 1, up to four waves a row group.  (At batch 2 the ring's
+        // registers went to scratch, and eight waves a group needed 124 VGPRs
+        // against 94: those keep the step loop below.)  A ring of Q4_U sign
+        // words a lane: the slot of slice j is refilled
+        // with slice j + Q4_U as soon as slice j's signs are expanded, so
+        // Q4_U - 1 to Q4_U sign loads stay in flight through the MFMAs.  The
+        // staged operand of group G (slices s0 + Q4_U G ...) sits in buffer
+        // G & 1: group G + 1's operand loads are issued at the start of group
+        // G and written to the other buffer at its end (the buffer group G - 1
+        // read; one wave's LDS operations complete in order).  The groups
+        // before the last issue their successors' loads unconditionally
+        // (clamped into the layer, as in a partial last group), so the
+        // compiler's wait counts stay exact counts; the last group issues
+        // none.
+        const size_t n = rows_dead ? 0 : s1 - s0;
+        const uint32_t n_grp = (uint32_t)((n + Q4_U - 1) / Q4_U);
+        constexpr int SQ = Q4_U * NCOL / 8;  // 16-byte operand words a lane per group
+        static_assert(Q4_U * NCOL % 8 == 0, "whole 16-byte words per lane");
+        struct Staged {
+            uint4 w[SQ];
+            uint32_t s;
+        };
+        auto op_load = [&](uint32_t grp) {
+            Staged st;
+            const size_t sb = s0 + (size_t)grp * Q4_U;
+            const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
             const uint32_t ob = nsl * 4 * NCOL * 32, os = nsl * 4 * NCOL;
             const uint8_t *gbs = gb + sb * 4 * NCOL * 32, *gss = gs + sb * 4 * NCOL;
 #pragma unroll
             for (int q = 0; q < SQ; q++) {
                 uint32_t o = (lane + 64 * q) * 16;
                 o = o < ob ? o : ob - 16;
-                stg[q] = *(const uint4 *)(gbs + o);
+                st.w[q] = *(const uint4 *)(gbs + o);
             }
             uint32_t o = lane * 4;
             o = o < os ? o : os - 4;
-            stgs = *(const uint32_t *)(gss + o);
-        }
-        uint4 w4[Q4_U];
+            st.s = *(const uint32_t *)(gss + o);
+            return st;
+        };
+        auto op_store = [&](uint32_t grp, const Staged &st) {
+            uint8_t *buf = wl + (grp & 1) * RB;
 #pragma unroll
-        for (int u = 0; u < Q4_U; u++) {
-            const size_t sl = sb + (u < (int)nsl ? u : nsl - 1);
-            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64 - (sl >= sdead ? dead_off : 0)));
-            w4[u] = make_uint4(q[0], q[1], q[2], q[3]);
-        }
-        if (NCOL > 0) {
-#pragma unroll
-            for (int q = 0; q < SQ; q++) *(uint4 *)(wl + (lane + 64 * q) * 16) = stg[q];
-            *(uint32_t *)(wl + OPB + lane * 4) = stgs;  // lanes past the scales fill the padding
+            for (int q = 0; q < SQ; q++) *(uint4 *)(buf + (lane + 64 * q) * 16) = st.w[q];
+            *(uint32_t *)(buf + OPB + lane * 4) = st.s;  // lanes past the scales fill the padding
             __builtin_amdgcn_wave_barrier();
-        }
-        const uint8_t *gbs = gb + sb * 4 * ncol * 32, *gss = gs + sb * 4 * ncol;
-        // one form for whole and partial steps (a uniform branch per slice): a
-        // second, unguarded copy of the step kept its own accumulator
-        // registers -- 122 VGPRs a wave against 94 at batch 1 (four waves a
-        // SIMD instead of five), 256 against 140-238 for column groups
-        if (NCG > 1) {
+        };
+        auto sign_load = [&](size_t j) {
+            const size_t sl = j < s1 ? j : s1 - 1;
+            const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64 - (sl >= sdead ? dead_off : 0)));
+            return make_uint4(q[0], q[1], q[2], q[3]);
+        };
+        if (n_grp > 0) {
+            uint4 w4[Q4_U];
+            const Staged st0 = op_load(0);
+#pragma unroll
+            for (int u = 0; u < Q4_U; u++) w4[u] = sign_load(s0 + u);
+            op_store(0, st0);
+            uint32_t grp = 0;
+            for (; grp + 1 < n_grp; grp++) {
+                const Staged st = op_load(grp + 1);
+                __builtin_amdgcn_sched_barrier(Q4_SCHED_PIN);
+                const size_t sb = s0 + (size_t)grp * Q4_U;
+                const uint32_t rb = bcol ? (grp & 1) * RB : 0;
+                // each refill stays behind its own slice's MFMAs and ahead of
+                // the next slice's (the scheduler would otherwise sink the
+                // loads below the group's MFMAs)
+#pragma unroll
+                for (int u = 0; u < Q4_U; u++) {
+                    q4_slice_lds(acc[0], w4[u], wl, bo0 + rb + u * bstep, so0 + rb + u * sstep, c7);
+                    w4[u] = sign_load(sb + Q4_U + u);
+                    __builtin_amdgcn_sched_barrier(Q4_SCHED_PIN);
+                }
+                op_store(grp + 1, st);
+            }
+            const size_t sb = s0 + (size_t)grp * Q4_U;
+            const uint32_t nsl = (uint32_t)(s1 - sb), rb = bcol ? (grp & 1) * RB : 0;
 #pragma unroll
             for (int u = 0; u < Q4_U; u++)
-                if (u < (int)nsl) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
-        } else {
-#pragma unroll
-            for (int u = 0; u < Q4_U; u++)
-                if (u < (int)nsl)
-                    q4_step<NCOL>(acc[0], w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
+                if (u < (int)nsl) q4_slice_lds(acc[0], w4[u], wl, bo0 + rb + u * bstep, so0 + rb + u * sstep, c7);
         }
-        if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
+    } else {
+        for (size_t sb = s0; sb < (rows_dead ? s0 : s1); sb += Q4_U) {
+            const uint32_t nsl = (uint32_t)(s1 - sb < Q4_U ? s1 - sb : Q4_U);
+            // a step's operand: Q4_U slices x 4 lane groups x NCOL columns x 32 B,
+            // SQ 16-byte words per lane
+            constexpr int SQ = NCOL > 0 ? Q4_U * NCOL / 8 : 1;
+            static_assert(NCOL == 0 || Q4_U * NCOL % 8 == 0, "whole 16-byte words per lane");
+            uint4 stg[SQ];
+            uint32_t stgs = 0;
+            if (NCOL > 0) {
+                // operand of slices sb..sb+nsl-1: SQ uint4 + one dword of scales per lane
+                const uint32_t ob = nsl * 4 * NCOL * 32, os = nsl * 4 * NCOL;
+                const uint8_t *gbs = gb + sb * 4 * NCOL * 32, *gss = gs + sb * 4 * NCOL;
+    #pragma unroll
+                for (int q = 0; q < SQ; q++) {
+                    uint32_t o = (lane + 64 * q) * 16;
+                    o = o < ob ? o : ob - 16;
+                    stg[q] = *(const uint4 *)(gbs + o);
+                }
+                uint32_t o = lane * 4;
+                o = o < os ? o : os - 4;
+                stgs = *(const uint32_t *)(gss + o);
+            }
+            uint4 w4[Q4_U];
+    #pragma unroll
+            for (int u = 0; u < Q4_U; u++) {
+                const size_t sl = sb + (u < (int)nsl ? u : nsl - 1);
+                const u32x4_t q = __builtin_nontemporal_load((gu32x4_t *)(wp + sl * 64 - (sl >= sdead ? dead_off : 0)));
+                w4[u] = make_uint4(q[0], q[1], q[2], q[3]);
+            }
+            if (NCOL > 0) {
+    #pragma unroll
+                for (int q = 0; q < SQ; q++) *(uint4 *)(wl + (lane + 64 * q) * 16) = stg[q];
+                *(uint32_t *)(wl + OPB + lane * 4) = stgs;  // lanes past the scales fill the padding
+                __builtin_amdgcn_wave_barrier();
+            }
+            const uint8_t *gbs = gb + sb * 4 * ncol * 32, *gss = gs + sb * 4 * ncol;
+            // one form for whole and partial steps (a uniform branch per slice): a
+            // second, unguarded copy of the step kept its own accumulator
+            // registers -- 122 VGPRs a wave against 94 at batch 1 (four waves a
+            // SIMD instead of five), 256 against 140-238 for column groups
+            if (NCG > 1) {
+    #pragma unroll
+                for (int u = 0; u < Q4_U; u++)
+                    if (u < (int)nsl) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
+            } else {
+    #pragma unroll
+                for (int u = 0; u < Q4_U; u++)
+                    if (u < (int)nsl)
+                        q4_step<NCOL>(acc[0], w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
+            }
+            if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
+        }
     }
     if (KSPLIT > 1) {
-        // one column group at a time through [waves][4 tiles][64 lanes]
-        f32x4_t *red = (f32x4_t *)(q4_lds + Q4_NW(KSPLIT) * wreg);
+        // one column group at a time through [4 tiles][64 lanes] a wave: in
+        // the wave's own region (NCOL > 0: no wave reads another's region
+        // before the barrier) or past the regions
+        auto red = [&](int w, int rt) {
+            return NCOL > 0 ? (f32x4_t *)(q4_lds + w * wreg) + rt * 64 + lane
+                            : (f32x4_t *)(q4_lds + Q4_NW(KSPLIT) * wreg) + (w * 4 + rt) * 64 + lane;
+        };
 #pragma unroll
         for (int cg = 0; cg < NCG; cg++) {
             if (cg) __syncthreads();  // the last group's sums are read
 #pragma unroll
-            for (int rt = 0; rt < 4; rt++) red[(wave * 4 + rt) * 64 + lane] = acc[cg][rt];
+            for (int rt = 0; rt < 4; rt++) *red(wave, rt) = acc[cg][rt];
             __syncthreads();
             if (ks == 0) {
 #pragma unroll
                 for (int rt = 0; rt < 4; rt++) {
-                    f32x4_t v = red[(wave * 4 + rt) * 64 + lane];
-                    for (int q = 1; q < KSPLIT; q++) v += red[((wave + q) * 4 + rt) * 64 + lane];
+                    f32x4_t v = *red(wave, rt);
+                    for (int q = 1; q < KSPLIT; q++) v += *red(wave + q, rt);
                     acc[cg][rt] = v;
                 }
             }
@@ -579,7 +675,7 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
 // LDS bytes of a q4_gemv_kernel workgroup.
 static size_t q4_gemv_lds(int ncol_t, int ksplit) {
     const size_t nw = Q4_NW(ksplit);
-    return nw * (size_t)q4_wave_lds(ncol_t) + (ksplit > 1 ? nw * 4 * 64 * 16 : 0);
+    return nw * (size_t)q4_wave_lds(ncol_t) + (ksplit > 1 && ncol_t == 0 ? nw * 4 * 64 * 16 : 0);
 }
 
 // Waves that share a 64-row group split its slices: one load step (Q4_U
