@@ -258,6 +258,19 @@ int qbk_block_cache(const qbk_block *block, float **k_cache, float **v_cache);
  * attention state covers none of them yet.  No counterpart in the reference
  * (its KvCache is filled only by its own steps, engine/mod.rs:1224-1268). */
 int qbk_block_set_filled(qbk_block *block, const size_t *rows, size_t n);
+/* engine/mod.rs:953-968 Engine::gqa_attention's face, chosen once when the
+ * engine loads (QUANTIBBLER_ATTN): QBK_ATTN_SAGE (the default) runs the
+ * reference-scheme sage decode attention (the gpu:sage face, :984-1030) on a
+ * kept state; QBK_ATTN_EXACT the exact f32 attention over cache rows
+ * 0 .. pos (the gpu:tiled face, :1041-1067, which the scalar default face
+ * computes too, :1073-1116), read in place in the row-major cache, and the o
+ * projection from its f32 output.  The exact face serves qbk_block_decode_dev
+ * and qbk_block_prefill_dev (sequence 0; its prefill runs forward_prefill's
+ * per-token loop, :811-822); the batched and device-position steps refuse
+ * it.  Switching keeps the cache: the sage state rebuilds the rows the exact
+ * face wrote on its next step. */
+enum { QBK_ATTN_SAGE = 0, QBK_ATTN_EXACT = 1 };
+int qbk_block_set_attention_face(qbk_block *block, int face);
 
 /* Batched serving (engine/mod.rs:1377-1476 steps a batch of sequences through
  * the trunk; each sequence keeps its own cache): a block holding n_seqs

@@ -97,6 +97,7 @@ _SIGS = {
     "qbk_block_decode_batch_pos_dev": (_I, [_P, _P, _P, _P, _Z, _P, _Z, _P]),
     "qbk_block_set_positions": (_I, [_P, _P, _Z]),
     "qbk_block_set_filled": (_I, [_P, _P, _Z]),
+    "qbk_block_set_attention_face": (_I, [_P, _I]),
     "qbk_positions_advance_dev": (_I, [_P, _P, _Z, _P]),
     "qbk_attention_sage_decode_step_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _Z, _P, _P, _Z, _Z,
                                                 _Z, _P]),

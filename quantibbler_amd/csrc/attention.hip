@@ -37,6 +37,10 @@ struct AttArgs {
     size_t H, Hk, Sq, Skv, d, dv;
     int causal;
     float scale;
+    // element strides of k and v: between consecutive keys of a kv head and
+    // between kv heads (head-major (B, Hkv, Skv, d): d and Skv d; a decoder
+    // block's row-major cache (rows, Hkv d): Hkv d and d)
+    size_t k_tok, k_head, v_tok, v_head;
 };
 
 __device__ __forceinline__ float att_block_max(float v, float *red) {
@@ -67,8 +71,8 @@ __global__ void __launch_bounds__(ATT_THREADS) att_exact(AttArgs a) {
     const size_t i = row % a.Sq, bh = row / a.Sq, b = bh / a.H, h = bh % a.H;
     const size_t bk = b * a.Hk + h / (a.H / a.Hk);
     const float *qr = a.q + row * a.d;
-    const float *kb = a.k + bk * a.Skv * a.d;
-    const float *vb = a.v + bk * a.Skv * a.dv;
+    const float *kb = a.k + bk * a.k_head;
+    const float *vb = a.v + bk * a.v_head;
     const int tid = threadIdx.x;
     for (size_t c = tid; c < a.d; c += ATT_THREADS) qs[c] = qr[c];
     // keys visible to query i: j < i + 1 + (Skv - Sq), i.e. j + Sq <= i + Skv
@@ -83,7 +87,7 @@ __global__ void __launch_bounds__(ATT_THREADS) att_exact(AttArgs a) {
         const size_t j1 = j0 + ATT_CHUNK < kend ? j0 + ATT_CHUNK : kend;
         float cmax = -INFINITY;
         for (size_t j = j0 + tid; j < j1; j += ATT_THREADS) {
-            const float *kr = kb + j * a.d;
+            const float *kr = kb + j * a.k_tok;
             float s = 0.0f;
             for (size_t c0 = 0; c0 < a.d; c0 += 16) {  // blocked: 16-term partials
                 float sp = 0.0f;
@@ -114,7 +118,7 @@ __global__ void __launch_bounds__(ATT_THREADS) att_exact(AttArgs a) {
             for (size_t jb = j0; jb < j1; jb += 32) {  // blocked: 32-term partials
                 float sp = 0.0f;
                 const size_t je = jb + 32 < j1 ? jb + 32 : j1;
-                for (size_t j = jb; j < je; j++) sp += ps[j - j0] * vb[j * a.dv + c];
+                for (size_t j = jb; j < je; j++) sp += ps[j - j0] * vb[j * a.v_tok + c];
                 sacc += sp;
             }
             acc[u] = acc[u] * alpha + sacc;
@@ -170,10 +174,25 @@ static int validate_exact(const qbk_attn_shape *s, const size_t *lens) {
 static int launch_exact(const qbk_attn_shape *s, const float *q, const float *k, const float *v, int causal,
                         float *out, hipStream_t st) {
     AttArgs a{q, k, v, out, s->n_heads, s->n_kv_heads, s->seq_q, s->seq_kv, s->head_dim, s->val_dim, causal ? 1 : 0,
-              1.0f / sqrtf((float)s->head_dim)};
+              1.0f / sqrtf((float)s->head_dim), s->head_dim, s->seq_kv * s->head_dim, s->val_dim,
+              s->seq_kv * s->val_dim};
     const size_t rows = s->batch * s->n_heads * s->seq_q;
     if (rows > 0x7FFFFFFFull) return fail(QBK_ERR_VALIDATION, "attention: too many query rows for one launch");
     hipLaunchKernelGGL(att_exact, dim3((unsigned)rows), dim3(ATT_THREADS), 0, st, a);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+// One query position of every head over rows 0 .. rows - 1 of a decoder
+// block's row-major cache (f32 [rows][Hk hd] keys and values): the engine's
+// tiled decode face (engine/mod.rs:1041-1067: seq_q = 1, so every cached key
+// is visible), reading the cache in place rather than gathered head-major.
+int attention_exact_cache(const float *q, const float *kc, const float *vc, size_t H, size_t Hk, size_t hd,
+                          size_t rows, float *out, hipStream_t st) {
+    if (rows == 0 || H == 0 || Hk == 0 || H % Hk != 0 || hd == 0 || hd > ATT_MAXD)
+        return fail(QBK_ERR_VALIDATION, "exact cache attention: bad shape");
+    AttArgs a{q, kc, vc, out, H, Hk, 1, rows, hd, hd, 0, 1.0f / sqrtf((float)hd), Hk * hd, hd, Hk * hd, hd};
+    hipLaunchKernelGGL(att_exact, dim3((unsigned)H), dim3(ATT_THREADS), 0, st, a);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

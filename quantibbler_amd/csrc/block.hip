@@ -50,6 +50,7 @@ struct qbk_block {
     size_t nseq;              // independent sequences: caches and states, sequence s at offset s
     std::vector<size_t> tokens;  // per sequence: cache rows the attention state's codes cover
     std::vector<size_t> filled;  // per sequence: cache rows holding its keys and values
+    int face;                    // QBK_ATTN_SAGE (the sage decode attention) or QBK_ATTN_EXACT
     // per-call buffers
     uint16_t *xcat;           // bf16 [3 d] (q, k, v inputs), then [2 d] (gate, up)
     float *ycat;              // f32 [(H + 2 Hk) hd], then [2 ffn]
@@ -573,6 +574,7 @@ int qbk_block_create_seqs(qbk_ctx *ctx, const qbk_factor *const *layers, const f
     B->block = block_size;
     B->eps = (float)rms_norm_eps;
     B->nseq = n_seqs;
+    B->face = QBK_ATTN_SAGE;
     B->tokens.assign(n_seqs, 0);
     B->filled.assign(n_seqs, 0);
     for (int i = 0; i < 7; i++) B->lay[i] = layers[i];
@@ -650,6 +652,12 @@ int qbk_block_cache(const qbk_block *B, float **k_cache, float **v_cache) {
 
 }  // extern "C"
 
+static int block_mlp_one(qbk_block *B, float *h, hipStream_t s);
+
+static const char *const kExactFaceOnly =
+    "the exact attention face serves one sequence at host positions (qbk_block_decode_dev, "
+    "qbk_block_prefill_dev); the batched and device-position steps run the sage face";
+
 // The decode of one position of sequence 0: at pos (host), or with pos_dev
 // at the position that device word holds when the step runs (the host
 // record of cached positions is then left to the caller).
@@ -664,6 +672,8 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
                     fmt("position %zu skips cache rows: the block holds %zu positions", pos, B->filled[0]));
     if ((rc = bind(ctx))) return rc;
     if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
+    const bool exact = B->face == QBK_ATTN_EXACT;
+    if (pos_dev && exact) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
     const qbk_attn_shape one{1, B->H, B->Hk, 1, B->cap, B->hd, B->hd};
     const size_t kvs = B->cap * B->Hk * B->hd;
     if (pos_dev && !sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs))
@@ -692,12 +702,22 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
     // the q/k norms, RoPE and the cache append run in the attention's
     // pre-pass when the grouped decode kernels serve the shape (one launch
     // fewer), else in a kernel of their own
-    const bool fold = sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs);
+    const bool fold = !exact && sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs);
     const DecRope rp{B->ycat, B->rope, B->w_q, B->w_k, B->eps, H};
     if (!fold) {
         hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, pos_dev, B->cap,
                            B->w_q, B->w_k, B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
         QBK_HIP(hipGetLastError());
+    }
+    // the exact face (engine/mod.rs:1041-1067 gqa_attention_tiled): f32
+    // attention of the rotated query over cache rows 0 .. pos, read in place;
+    // the o projection from its f32 output
+    if (exact) {
+        if ((rc = attention_exact_cache(B->qrot, B->kc, B->vc, B->H, B->Hk, B->hd, pos + 1, B->attn, s))) return rc;
+        if (B->tokens[0] > pos) B->tokens[0] = pos;  // the sage state covers the rows before pos at most
+        B->filled[0] = pos + 1;
+        if ((rc = q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s))) return rc;
+        return block_mlp_one(B, h, s);
     }
     // the attention's combine writes the o projection's operand directly
     DecOpSink sink{B->o->s2, nullptr, nullptr};
@@ -721,7 +741,17 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
     if ((rc = osink ? q4_run_staged(B->o, B->oout, false, nullptr, B->ws, s)
                     : q4_run(B->o, 1, B->attn, true, B->oout, false, B->ws, s)))
         return rc;
-    // MLP sublayer: h1 = o + h, then its norm
+    return block_mlp_one(B, h, s);
+}
+
+// The MLP sublayer of one position of sequence 0, from the o projection's
+// output B->oout: h1 = o + h, its norm, gate / up, SwiGLU, down + h1 -> h.
+static int block_mlp_one(qbk_block *B, float *h, hipStream_t s) {
+    int rc;
+    const int d = (int)B->d, ffn = (int)B->ffn;
+    const bool fits = d <= BLKD_NORM_THREADS * BLKD_OP_PER;
+    uint8_t *op, *sc;
+    const float *s2c;
     if (fits && q4_set_flat_operand(B->gu, B->ws, &op, &sc, &s2c)) {
         hipLaunchKernelGGL(blkd_norm_op, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
                            B->w_post, B->eps, d, 2, s2c, op, sc);
@@ -774,6 +804,7 @@ extern "C" {
 
 int qbk_block_decode_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const uint32_t *pos, void *stream) {
     if (!pos || !B) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (B->face == QBK_ATTN_EXACT) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
     int rc;
     if ((rc = pos_state_ready(B, 1))) return rc;
     return block_decode_one(ctx, B, h, 0, pos, stream);
@@ -806,6 +837,15 @@ int qbk_block_set_filled(qbk_block *B, const size_t *rows, size_t n) {
     return QBK_OK;
 }
 
+int qbk_block_set_attention_face(qbk_block *B, int face) {
+    if (!B) return fail(QBK_ERR_VALIDATION, "null block");
+    if (face != QBK_ATTN_SAGE && face != QBK_ATTN_EXACT)
+        return fail(QBK_ERR_VALIDATION,
+                    fmt("attention face must be QBK_ATTN_SAGE (0) or QBK_ATTN_EXACT (1), got %d", face));
+    B->face = face;
+    return QBK_OK;
+}
+
 int qbk_block_reset(qbk_block *B) {
     if (!B) return fail(QBK_ERR_VALIDATION, "null block");
     for (size_t i = 0; i < B->nseq; i++) B->tokens[i] = B->filled[i] = 0;
@@ -826,6 +866,14 @@ int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *B, size_t seq, float *h, 
     if (n == 0) return fail(QBK_ERR_VALIDATION, "prefill needs at least one token");
     if (n > B->cap)
         return fail(QBK_ERR_VALIDATION, fmt("prefill of %zu tokens exceeds the block's cache capacity of %zu", n, B->cap));
+    if (B->face == QBK_ATTN_EXACT) {
+        // forward_prefill's per-token loop (engine/mod.rs:811-822) on the
+        // exact face: row t through the decode step at position t
+        if (seq != 0) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
+        for (size_t t = 0; t < n; t++)
+            if ((rc = block_decode_one(ctx, B, h + t * B->d, t, nullptr, stream))) return rc;
+        return QBK_OK;
+    }
     if (B->hd != 128)
         return fail(QBK_ERR_VALIDATION,
                     fmt("block prefill runs the block-scaled SageAttention, which needs head_dim 128; got %zu", B->hd));
@@ -903,6 +951,7 @@ static int block_decode_batch(qbk_ctx *ctx, qbk_block *B, float *h, const size_t
                               size_t n, void *workspace, size_t workspace_size, void *stream) {
     int rc;
     if (!B || !h || (!pos && !pos_dev)) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (B->face == QBK_ATTN_EXACT) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
     if (n == 0 || n > B->nseq)
         return fail(QBK_ERR_VALIDATION, fmt("batch of %zu sequences on a block holding %zu", n, B->nseq));
     for (size_t i = 0; !pos_dev && i < n; i++) {
@@ -1005,6 +1054,7 @@ int qbk_block_decode_batch_dev(qbk_ctx *ctx, qbk_block *B, float *h, const size_
 int qbk_block_decode_batch_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const uint32_t *pos, size_t n,
                                    void *workspace, size_t workspace_size, void *stream) {
     if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (B && B->face == QBK_ATTN_EXACT) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
     if (B && n && n <= B->nseq) {
         int rc;
         if ((rc = pos_state_ready(B, n))) return rc;

@@ -109,6 +109,12 @@ int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride
 // (n == 1): the step's q/k norm, RoPE and cache append run in the pre-pass
 // (the caches then take the new row from rope->qkv, not from the caller).
 
+// Exact f32 attention of one query position (q [H][hd]) over rows
+// 0 .. rows - 1 of a decoder block's row-major cache ([rows][Hk hd] keys and
+// values) -> out [H][hd] (attention.hip; the engine's tiled decode face).
+int attention_exact_cache(const float *q, const float *kc, const float *vc, size_t H, size_t Hk, size_t hd,
+                          size_t rows, float *out, hipStream_t st);
+
 // A decode step (qbk_attention_sage_decode_step_dev's contract) whose
 // combine also writes its output [n_heads][val_dim] as the batch-1 stage-1
 // fp8 operand of the factor layer it feeds (q4_operand.h's flat runs; val_dim

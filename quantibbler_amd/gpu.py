@@ -352,6 +352,7 @@ class DecoderBlock:
         self._h = out
         self.capacity = int(capacity)
         self.n_seqs = int(n_seqs)
+        self.face = "sage"
 
     def decode_dev(self, h, pos: int, stream=None):
         """h: device f32 [d_model] (a contiguous torch tensor, or a raw device
@@ -453,6 +454,19 @@ class DecoderBlock:
                     f"values; got {h.dtype} of {h.numel()} on {h.device}")
         elif not isinstance(h, int):
             raise _lib.KernelError(f"{what} must be a device tensor or a device address")
+
+    ATTENTION_FACES = {"sage": 0, "exact": 1}
+
+    def set_attention_face(self, face: str):
+        """The attention face of the block's steps (engine/mod.rs:953-968):
+        "sage" (the default: the reference-scheme sage decode attention on a
+        kept state) or "exact" (f32 attention over the cached rows, the
+        gpu:tiled face; one sequence at host positions -- decode_dev and
+        prefill_dev, the latter token by token)."""
+        if face not in self.ATTENTION_FACES:
+            raise _lib.KernelError(f"attention face must be one of {sorted(self.ATTENTION_FACES)}, got {face!r}")
+        check(_lib.load().qbk_block_set_attention_face(self._h, self.ATTENTION_FACES[face]))
+        self.face = face
 
     def reset(self):
         check(_lib.load().qbk_block_reset(self._h))

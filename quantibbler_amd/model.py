@@ -223,11 +223,15 @@ class DeviceModel:
     """The transformer trunk on the device at bf16 serving (Engine::forward,
     engine/mod.rs:802-806, and forward_prefill's per-token loop, :811-822):
     embedding row -> every DecoderBlock over its KV cache -> final norm ->
-    lm_head logits, all device-resident; the sage decode attention.  Built
-    from a ModelDir; torch supplies the device buffers (plumbing only -- every
-    step runs in libqbk)."""
+    lm_head logits, all device-resident.  ``attention`` picks every block's
+    face once, as the engine does at load (engine/mod.rs:953-968): "sage"
+    (the sage decode attention; prefill on the block-scaled SageAttention)
+    or "exact" (f32 attention over the cache, one sequence, prefill token by
+    token).  Built from a ModelDir; torch supplies the device buffers
+    (plumbing only -- every step runs in libqbk)."""
 
-    def __init__(self, ctx, md: ModelDir, capacity: int, block_size: int = 64, n_seqs: int = 1):
+    def __init__(self, ctx, md: ModelDir, capacity: int, block_size: int = 64, n_seqs: int = 1,
+                 attention: str = "sage"):
         import torch
 
         from .gpu import DecoderBlock, FactorLayer, LmHead
@@ -243,6 +247,8 @@ class DeviceModel:
                                             md.n_kv_heads, md.head_dim, md.rope_theta, md.rms_norm_eps,
                                             capacity, block_size, norms.get("q_norm"), norms.get("k_norm"),
                                             n_seqs=self.n_seqs))
+            self.blocks[-1].set_attention_face(attention)
+        self.attention = attention
         self.embedding = torch.from_numpy(_bf16_values(md.embedding)).to(dev)
         self.final_norm = torch.from_numpy(_bf16_values(md.final_norm())).to(dev)
         self.head = LmHead.from_rows(ctx, _bf16_values(md.head_rows()))

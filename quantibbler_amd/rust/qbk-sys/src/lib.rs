@@ -27,6 +27,8 @@ pub const QBK_ERR_INIT: c_int = 3;
 pub const QBK_F64: c_int = 0;
 pub const QBK_F32: c_int = 1;
 pub const QBK_BF16: c_int = 2;
+pub const QBK_ATTN_SAGE: c_int = 0;
+pub const QBK_ATTN_EXACT: c_int = 1;
 
 #[repr(C)]
 pub struct QbkCtx {
@@ -167,6 +169,7 @@ extern "C" {
                                           stream: *mut c_void) -> c_int;
     pub fn qbk_block_set_positions(block: *mut QbkBlock, pos: *const usize, n: usize) -> c_int;
     pub fn qbk_block_set_filled(block: *mut QbkBlock, rows: *const usize, n: usize) -> c_int;
+    pub fn qbk_block_set_attention_face(block: *mut QbkBlock, face: c_int) -> c_int;
     pub fn qbk_embed(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32, n: usize,
                      out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_embed_dev(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32,

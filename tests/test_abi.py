@@ -97,6 +97,16 @@ def test_validation_precedes_device_use(lib):
         check(lib.qbk_attention_sage(None, C.byref(sh), None, 63, None, 32, None, 32, 1, 4, None))
 
 
+def test_block_attention_face_validation(lib):
+    # the face setter validates before it touches a block (engine/mod.rs:953-968
+    # knows three faces; the device block serves the sage and exact ones)
+    from quantibbler_amd import KernelError
+    from quantibbler_amd._lib import check
+
+    with pytest.raises(KernelError, match="null block"):
+        check(lib.qbk_block_set_attention_face(None, 1))
+
+
 def test_packed_matvec_ceiling_precedes_device_use(lib):
     # gpu.rs:116-137: after validate_packed and the vec length check, the f64
     # device face refuses n_rows x words past the u32 index ceiling -- before

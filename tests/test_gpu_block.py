@@ -86,6 +86,91 @@ def test_decoder_block_matches_oracle(ctx, orc, qk_norm):
     block.close()
 
 
+def _small_block(ctx, orc, seed, qk_norm, cap=40, blk=16):
+    from quantibbler_amd import DecoderBlock, FactorLayer
+
+    d, H, Hk, hd, ffn = 256, 4, 2, 64, 512
+    rng = np.random.default_rng(seed)
+    shapes = [(H * hd, d, 64), (Hk * hd, d, 32), (Hk * hd, d, 32), (d, H * hd, 64),
+              (ffn, d, 96), (ffn, d, 96), (d, ffn, 96)]
+    layers = [scaled_layer(orc, rng, *s) for s in shapes]
+    devs = [FactorLayer.from_rows(ctx, L["dout"], L["din"], L["r"], L["ub"], L["vt"], L["s1"], L["s2"],
+                                  L["bias"]) for L in layers]
+    bfv = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a.astype(np.float32)))
+    norms = {"input": bfv(1.0 + 0.1 * rng.standard_normal(d)),
+             "post_attention": bfv(1.0 + 0.1 * rng.standard_normal(d))}
+    if qk_norm:
+        norms["q_norm"] = bfv(1.0 + 0.2 * rng.standard_normal(hd))
+        norms["k_norm"] = bfv(1.0 + 0.2 * rng.standard_normal(hd))
+    block = DecoderBlock(ctx, devs, norms["input"], norms["post_attention"], H, Hk, hd, 500000.0, 1e-5, cap, blk,
+                         norms.get("q_norm"), norms.get("k_norm"))
+    return block, layers, norms, rng, dict(d=d, H=H, Hk=Hk, hd=hd, cap=cap, blk=blk)
+
+
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_decoder_block_exact_face_matches_oracle(ctx, orc, qk_norm):
+    """The exact attention face (engine/mod.rs:1041-1067, the f32 attention the
+    scalar default face also computes, :1073-1116) against the oracle's block
+    step on the scalar face; positions 8-15 switch the block to the sage face
+    and back (the oracle's sage face recomputes from the cache each step, so
+    the device's kept state must rebuild the rows the exact face wrote)."""
+    block, layers, norms, rng, g = _small_block(ctx, orc, 31 + qk_norm, qk_norm)
+    kc = np.zeros((g["cap"], g["Hk"] * g["hd"]), np.float32)
+    vc = np.zeros((g["cap"], g["Hk"] * g["hd"]), np.float32)
+    st = torch.cuda.current_stream()
+    worst = {"exact": (1.0, 0.0), "sage": (1.0, 0.0)}
+    for pos in range(24):
+        face = "sage" if 8 <= pos < 16 else "exact"
+        block.set_attention_face(face)
+        h = rng.standard_normal(g["d"]).astype(np.float32)
+        hd_dev = torch.from_numpy(h).cuda()
+        block.decode_dev(hd_dev, pos, st)
+        torch.cuda.synchronize()
+        want = orc.block_step(layers, norms, h, pos, kc, vc, g["H"], g["Hk"], g["hd"], 500000.0, 1e-5, "bf16",
+                              "scalar" if face == "exact" else "sage", g["blk"])
+        cos, rel = metrics(hd_dev.cpu().numpy(), want)
+        say(f"pos {pos} ({face}): out cos {cos:.8f} rel {rel:.2e}")
+        w = worst[face]
+        worst[face] = (min(w[0], cos), max(w[1], rel))
+        assert cos >= COS_MIN and rel <= REL_MAX, (pos, face, cos, rel)
+    say("worst", worst)
+    block.close()
+
+
+def test_decoder_block_exact_face_prefill_and_refusals(ctx, orc):
+    """On the exact face the prefill is forward_prefill's per-token loop
+    (engine/mod.rs:811-822): bit-identical to the same rows as decode steps;
+    the batched and device-position steps refuse the face."""
+    from quantibbler_amd import KernelError
+
+    block, layers, norms, rng, g = _small_block(ctx, orc, 41, True)
+    block.set_attention_face("exact")
+    st = torch.cuda.current_stream()
+    n = 21
+    rows = rng.standard_normal((n, g["d"])).astype(np.float32)
+    a = torch.from_numpy(rows).cuda()
+    need = block.prefill_workspace_size(n)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    block.prefill_dev(a, n, ws, need, st)
+    block.reset()
+    b = torch.from_numpy(rows).cuda()
+    for t in range(n):
+        block.decode_dev(b[t], t, st)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
+    h = torch.zeros(g["d"], dtype=torch.float32, device="cuda")
+    nb = block.decode_batch_workspace_size(1)
+    wsb = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    with pytest.raises(KernelError, match="the exact attention face serves one sequence at host positions"):
+        block.decode_batch_dev(h, [n], wsb, nb, st)
+    pos = torch.tensor([n], dtype=torch.int32, device="cuda")
+    with pytest.raises(KernelError, match="the exact attention face serves one sequence at host positions"):
+        block.decode_pos_dev(h, pos, st)
+    with pytest.raises(KernelError, match=r"attention face must be one of \['exact', 'sage'\], got 'tiled'"):
+        block.set_attention_face("tiled")
+    block.close()
+
+
 def test_decoder_block_validation(ctx, orc):
     from quantibbler_amd import DecoderBlock, FactorLayer, KernelError
 

@@ -185,6 +185,60 @@ def test_device_trunk_parity_tiny_goldens(ctx, orc, md):
     m.close()
 
 
+def test_device_trunk_exact_face(ctx, orc, md):
+    """The trunk on the exact attention face (DeviceModel(attention="exact"):
+    every block's engine/mod.rs:1041-1067 face) against the oracle on the
+    reference's default scalar face and the HF goldens; then the reference's
+    cross-face scenario (crates/quantibbler-server/tests/
+    cross_face_sage_identity.rs): greedy generation through the exact face and
+    through the sage face from the same prompt yields the same tokens, and the
+    final logits agree within the sage face's gate."""
+    from quantibbler_amd.model import DeviceModel
+
+    say("device trunk on parity-tiny, exact face")
+    with open(os.path.join(TINY, "goldens.json")) as f:
+        g = json.load(f)
+    ids = g["input_ids"]
+    cap = len(ids) + 8
+    m = DeviceModel(ctx, md, capacity=cap, attention="exact")
+    ref = orc.Trunk(md, serving="bf16", attention="scalar", capacity=cap)
+    worst_gold, worst_orc = 0.0, 0.0
+    st = torch.cuda.current_stream()
+    for pos, tok in enumerate(ids):
+        got = m.step(tok, st).cpu().numpy()
+        want = ref.step(tok)
+        gold = np.array(g["logits"][pos], np.float32)
+        worst_gold = max(worst_gold, float(np.abs(got - gold).max()))
+        rel_inf = float(np.abs(got - want).max() / np.abs(want).max())
+        worst_orc = max(worst_orc, rel_inf)
+        say(f"  pos {pos}: |device - HF| {np.abs(got - gold).max():.3g}  |device - oracle (scalar face)| "
+            f"{np.abs(got - want).max():.3g} (rel inf-norm {rel_inf:.3g})")
+    assert worst_gold <= 1e-2, worst_gold
+    # the exact faces' reassociation budget (cross_face_token_identity.rs:
+    # rel inf-norm <= 1e-5); measured 0 here
+    assert worst_orc <= 1e-5, worst_orc
+    # cross-face: the same prompt, then greedy steps, on each face
+    streams = {}
+    for face in ("exact", "sage"):
+        mf = m if face == "exact" else DeviceModel(ctx, md, capacity=cap, attention="sage")
+        mf.reset()
+        for t in ids[:4]:  # forward_prefill's per-token loop (engine/mod.rs:811-822)
+            logits = mf.step(t, st)
+        logits = logits.cpu().numpy().copy()
+        toks = []
+        for _ in range(6):
+            t = greedy(logits)
+            toks.append(t)
+            logits = mf.step(t, st).cpu().numpy().copy()
+        streams[face] = (toks, logits)
+        if mf is not m:
+            mf.close()
+    say(f"  greedy tokens: exact {streams['exact'][0]}, sage {streams['sage'][0]}")
+    assert streams["exact"][0] == streams["sage"][0]
+    sage_gate(streams["sage"][1], streams["exact"][1], "final logits, sage face vs exact face")
+    m.close()
+
+
 def _qpk1_v2(orc, rng, dout, din, r):
     """A random v2 qpk1 layer stream (f16 scales and bias), as the reference's
     writer lays it out (container bitstreams, element (i, j) at bit i r + j)."""
