@@ -271,6 +271,16 @@ int qbk_block_set_filled(qbk_block *block, const size_t *rows, size_t n);
  * face wrote on its next step. */
 enum { QBK_ATTN_SAGE = 0, QBK_ATTN_EXACT = 1 };
 int qbk_block_set_attention_face(qbk_block *block, int face);
+/* engine/mod.rs ServingDtype, chosen when the engine loads: QBK_BF16 (the
+ * default: apply_bf16 on the decode GEMV / prefill GEMM, bf16-rounded norms)
+ * or QBK_F32 -- apply's f64 products (z = f64(s2 x), Vb^T z and Ub t in
+ * element order, y = f32(u) s1 + b; :393-436), norm_apply and per_head_norm
+ * in f32 without bf16 roundings (:837-876), on either attention face.  The
+ * first QBK_F32 call forms the layers' row bitplanes and the block's f64
+ * scratch (the only allocations).  fp32 serving serves qbk_block_decode_dev
+ * and qbk_block_prefill_dev (sequence 0, the prefill token by token); the
+ * batched and device-position steps refuse it. */
+int qbk_block_set_serving(qbk_ctx *ctx, qbk_block *block, int serving);
 
 /* Batched serving (engine/mod.rs:1377-1476 steps a batch of sequences through
  * the trunk; each sequence keeps its own cache): a block holding n_seqs
@@ -336,6 +346,10 @@ int qbk_embed_dev(qbk_ctx *ctx, const float *table, size_t vocab, size_t d_model
  * (device pointers, rows x d). */
 int qbk_rms_norm_dev(qbk_ctx *ctx, const float *x, size_t rows, size_t d, const float *w, double eps,
                      float *out, void *stream);
+/* The same at fp32 serving (norm_apply's Fp32 arm, rms_norm_into as is):
+ * no bf16 roundings of the operand and the output. */
+int qbk_rms_norm_f32_dev(qbk_ctx *ctx, const float *x, size_t rows, size_t d, const float *w, double eps,
+                         float *out, void *stream);
 /* sampler.rs:4-15 greedy: per row of `vocab` logits, the first index of the
  * largest value (NaN never wins; 0 when nothing beats -inf). */
 int qbk_argmax_dev(qbk_ctx *ctx, const float *logits, size_t rows, size_t vocab, int32_t *out,

@@ -81,6 +81,7 @@ _SIGS = {
     "qbk_embed": (_I, [_P, _P, _Z, _Z, _P, _Z, _P, _P]),
     "qbk_embed_dev": (_I, [_P, _P, _Z, _Z, _P, _Z, _P, _P]),
     "qbk_rms_norm_dev": (_I, [_P, _P, _Z, _Z, _P, C.c_double, _P, _P]),
+    "qbk_rms_norm_f32_dev": (_I, [_P, _P, _Z, _Z, _P, C.c_double, _P, _P]),
     "qbk_argmax_dev": (_I, [_P, _P, _Z, _Z, _P, _P]),
     "qbk_block_destroy": (None, [_P]),
     "qbk_block_decode_dev": (_I, [_P, _P, _P, _Z, _P]),
@@ -98,6 +99,7 @@ _SIGS = {
     "qbk_block_set_positions": (_I, [_P, _P, _Z]),
     "qbk_block_set_filled": (_I, [_P, _P, _Z]),
     "qbk_block_set_attention_face": (_I, [_P, _I]),
+    "qbk_block_set_serving": (_I, [_P, _P, _I]),
     "qbk_positions_advance_dev": (_I, [_P, _P, _Z, _P]),
     "qbk_attention_sage_decode_step_dev": (_I, [_P, C.POINTER(AttnShape), _P, _P, _P, _Z, _P, _P, _Z, _Z,
                                                 _Z, _P]),

@@ -27,6 +27,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "factor_internal.h"
@@ -51,6 +52,9 @@ struct qbk_block {
     std::vector<size_t> tokens;  // per sequence: cache rows the attention state's codes cover
     std::vector<size_t> filled;  // per sequence: cache rows holding its keys and values
     int face;                    // QBK_ATTN_SAGE (the sage decode attention) or QBK_ATTN_EXACT
+    int serving;                 // QBK_BF16, or QBK_F32 (apply's f64 products, f32 norms)
+    float *xf;                   // fp32 serving: the normalised row, f32 [d] (null until set)
+    double *f64s;                // fp32 serving: the f64 products' scratch
     // per-call buffers
     uint16_t *xcat;           // bf16 [3 d] (q, k, v inputs), then [2 d] (gate, up)
     float *ycat;              // f32 [(H + 2 Hk) hd], then [2 ffn]
@@ -100,6 +104,33 @@ __global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm(const float *a, c
     }
 }
 
+// blkd_norm at fp32 serving (norm_apply's Fp32 arm, engine/mod.rs:837-852):
+// x = RMS-normalised hsum times w in f32, no bf16 roundings; x f32 [d].
+__global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm_f32(const float *a, const float *r, float *hout,
+                                                                  const float *w, float eps, float *x, int d) {
+    __shared__ float red[BLKD_NORM_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float ss = 0.0f;
+    for (int i = tid; i < d; i += BLKD_NORM_THREADS) {
+        float v = a[i];
+        if (r) v = v + r[i];
+        if (hout) hout[i] = v;
+        ss += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < BLKD_NORM_THREADS / 64; i++) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+    for (int i = tid; i < d; i += BLKD_NORM_THREADS) {
+        float v = a[i];
+        if (r) v = v + r[i];
+        x[i] = v * inv * w[i];
+    }
+}
+
 // Per-head RMSNorm (optional) and RoPE of q and k at position pos: one wave
 // per head, q heads first, then k heads (which also copy their v head to
 // the cache).  qkv = [q (H hd) | k (Hk hd) | v (Hk hd)] as the projections
@@ -107,6 +138,7 @@ __global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm(const float *a, c
 // norm_apply at bf16 serving over one head (engine/mod.rs:854-876): the
 // head's values rounded to bf16, their mean square (a tree here), then
 // bf16(v * inv * w).  RoPE pairs (i, i + hd/2) (engine/mod.rs:1169-1187).
+template <bool F32 = false>
 __global__ void __launch_bounds__(64) blkd_qk_rope(const float *qkv, const float2 *rope, size_t pos,
                                                    const uint32_t *pos_dev, size_t cap, const float *wq,
                                                    const float *wk, float eps, float *qrot, float *kc, float *vc,
@@ -120,7 +152,8 @@ __global__ void __launch_bounds__(64) blkd_qk_rope(const float *qkv, const float
     const int hh = is_q ? head : head - H;
     const float *src = is_q ? qkv + (size_t)hh * hd : qkv + (size_t)H * hd + (size_t)hh * hd;
     float *dst = is_q ? qrot + (size_t)hh * hd : kc + pos * (size_t)Hk * hd + (size_t)hh * hd;
-    rope_head(src, is_q ? wq : wk, eps, rope + pos * (size_t)half, hd, lane, [&](int j, float v) { dst[j] = v; });
+    auto put = [&](int j, float v) { dst[j] = v; };
+    rope_head<decltype(put), F32>(src, is_q ? wq : wk, eps, rope + pos * (size_t)half, hd, lane, put);
     if (!is_q) {
         const float *v = qkv + (size_t)(H + Hk) * hd + (size_t)hh * hd;
         float *vr = vc + pos * (size_t)Hk * hd + (size_t)hh * hd;
@@ -575,6 +608,9 @@ int qbk_block_create_seqs(qbk_ctx *ctx, const qbk_factor *const *layers, const f
     B->eps = (float)rms_norm_eps;
     B->nseq = n_seqs;
     B->face = QBK_ATTN_SAGE;
+    B->serving = QBK_BF16;
+    B->xf = nullptr;
+    B->f64s = nullptr;
     B->tokens.assign(n_seqs, 0);
     B->filled.assign(n_seqs, 0);
     for (int i = 0; i < 7; i++) B->lay[i] = layers[i];
@@ -657,6 +693,53 @@ static int block_mlp_one(qbk_block *B, float *h, hipStream_t s);
 static const char *const kExactFaceOnly =
     "the exact attention face serves one sequence at host positions (qbk_block_decode_dev, "
     "qbk_block_prefill_dev); the batched and device-position steps run the sage face";
+static const char *const kF32Only =
+    "fp32 serving runs one sequence at host positions (qbk_block_decode_dev, qbk_block_prefill_dev); the "
+    "batched and device-position steps serve bf16";
+
+// One position of sequence 0 at fp32 serving (engine/mod.rs:886-941 with
+// ServingDtype::Fp32): norms in f32 without bf16 roundings (:837-876), the
+// seven projections as apply's f64 products (:393-436), q/k norms and RoPE,
+// the cache append, the block's attention face over rows 0 .. pos, SwiGLU,
+// the residuals.  A parity face: a few launches a projection.
+static int block_decode_f32(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, hipStream_t s) {
+    int rc;
+    const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk, ffn = (int)B->ffn;
+    auto proj = [&](int li, const float *x, float *y) {
+        return factor_apply_f64_dev(ctx, B->lay[li], x, y, B->f64s, s);
+    };
+    hipLaunchKernelGGL(blkd_norm_f32, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, h, (const float *)nullptr,
+                       (float *)nullptr, B->w_in, B->eps, B->xf, d);
+    QBK_HIP(hipGetLastError());
+    float *q = B->ycat, *k = q + (size_t)H * hd, *v = k + (size_t)Hk * hd;
+    if ((rc = proj(0, B->xf, q)) || (rc = proj(1, B->xf, k)) || (rc = proj(2, B->xf, v))) return rc;
+    hipLaunchKernelGGL(blkd_qk_rope<true>, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos,
+                       (const uint32_t *)nullptr, B->cap, B->w_q, B->w_k, B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
+    QBK_HIP(hipGetLastError());
+    if (B->face == QBK_ATTN_EXACT) {
+        if ((rc = attention_exact_cache(B->qrot, B->kc, B->vc, B->H, B->Hk, B->hd, pos + 1, B->attn, s))) return rc;
+        if (B->tokens[0] > pos) B->tokens[0] = pos;
+    } else {
+        const qbk_attn_shape sh{1, B->H, B->Hk, 1, pos + 1, B->hd, B->hd};
+        const size_t cached = B->tokens[0] <= pos ? B->tokens[0] : 0;
+        if ((rc = sage_decode_step_sink(ctx, &sh, B->qrot, B->kc, B->vc, B->block, B->attn, B->state,
+                                        B->state_bytes, B->cap, cached, nullptr, s)))
+            return rc;
+        B->tokens[0] = pos + 1;
+    }
+    B->filled[0] = pos + 1;
+    if ((rc = proj(3, B->attn, B->oout))) return rc;
+    hipLaunchKernelGGL(blkd_norm_f32, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
+                       B->w_post, B->eps, B->xf, d);
+    QBK_HIP(hipGetLastError());
+    if ((rc = proj(4, B->xf, B->ycat)) || (rc = proj(5, B->xf, B->ycat + ffn))) return rc;
+    hipLaunchKernelGGL(blkd_swiglu, dim3((ffn + 255) / 256), dim3(256), 0, s, B->ycat, B->hid, ffn);
+    QBK_HIP(hipGetLastError());
+    if ((rc = proj(6, B->hid, B->dout))) return rc;
+    hipLaunchKernelGGL(blkd_add, dim3((d + 255) / 256), dim3(256), 0, s, B->dout, B->h1, h, d);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
 
 // The decode of one position of sequence 0: at pos (host), or with pos_dev
 // at the position that device word holds when the step runs (the host
@@ -674,6 +757,10 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
     if (B->device != ctx->device) return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
     const bool exact = B->face == QBK_ATTN_EXACT;
     if (pos_dev && exact) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
+    if (B->serving == QBK_F32) {
+        if (pos_dev) return fail(QBK_ERR_VALIDATION, kF32Only);
+        return block_decode_f32(ctx, B, h, pos, (hipStream_t)stream);
+    }
     const qbk_attn_shape one{1, B->H, B->Hk, 1, B->cap, B->hd, B->hd};
     const size_t kvs = B->cap * B->Hk * B->hd;
     if (pos_dev && !sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs))
@@ -705,7 +792,7 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
     const bool fold = !exact && sage_decode_batchable(&one, B->block, B->cap, B->kc, B->vc, kvs);
     const DecRope rp{B->ycat, B->rope, B->w_q, B->w_k, B->eps, H};
     if (!fold) {
-        hipLaunchKernelGGL(blkd_qk_rope, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, pos_dev, B->cap,
+        hipLaunchKernelGGL(blkd_qk_rope<false>, dim3(H + Hk), dim3(64), 0, s, B->ycat, B->rope, pos, pos_dev, B->cap,
                            B->w_q, B->w_k, B->eps, B->qrot, B->kc, B->vc, H, Hk, hd);
         QBK_HIP(hipGetLastError());
     }
@@ -805,6 +892,7 @@ extern "C" {
 int qbk_block_decode_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const uint32_t *pos, void *stream) {
     if (!pos || !B) return fail(QBK_ERR_VALIDATION, "null argument");
     if (B->face == QBK_ATTN_EXACT) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
+    if (B->serving == QBK_F32) return fail(QBK_ERR_VALIDATION, kF32Only);
     int rc;
     if ((rc = pos_state_ready(B, 1))) return rc;
     return block_decode_one(ctx, B, h, 0, pos, stream);
@@ -846,6 +934,31 @@ int qbk_block_set_attention_face(qbk_block *B, int face) {
     return QBK_OK;
 }
 
+int qbk_block_set_serving(qbk_ctx *ctx, qbk_block *B, int serving) {
+    int rc;
+    if (!B) return fail(QBK_ERR_VALIDATION, "null block");
+    if (serving != QBK_F32 && serving != QBK_BF16)
+        return fail(QBK_ERR_VALIDATION, "serving dtype must be QBK_F32 or QBK_BF16");
+    if (serving == QBK_F32 && !B->xf) {
+        if ((rc = bind(ctx))) return rc;
+        if (B->device != ctx->device)
+            return fail(QBK_ERR_VALIDATION, "block lives on another device than the context");
+        size_t nd = 0;
+        for (const qbk_factor *L : B->lay) nd = std::max(nd, L->din + L->r + L->dout);
+        void *xf = nullptr, *sc = nullptr;
+        QBK_HIP(hipMalloc(&xf, B->d * sizeof(float)));
+        B->allocs.push_back(xf);
+        QBK_HIP(hipMalloc(&sc, nd * sizeof(double)));
+        B->allocs.push_back(sc);
+        for (const qbk_factor *L : B->lay)
+            if ((rc = factor_rows_ready(L, nullptr))) return rc;
+        B->xf = (float *)xf;
+        B->f64s = (double *)sc;
+    }
+    B->serving = serving;
+    return QBK_OK;
+}
+
 int qbk_block_reset(qbk_block *B) {
     if (!B) return fail(QBK_ERR_VALIDATION, "null block");
     for (size_t i = 0; i < B->nseq; i++) B->tokens[i] = B->filled[i] = 0;
@@ -866,10 +979,11 @@ int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *B, size_t seq, float *h, 
     if (n == 0) return fail(QBK_ERR_VALIDATION, "prefill needs at least one token");
     if (n > B->cap)
         return fail(QBK_ERR_VALIDATION, fmt("prefill of %zu tokens exceeds the block's cache capacity of %zu", n, B->cap));
-    if (B->face == QBK_ATTN_EXACT) {
+    if (B->face == QBK_ATTN_EXACT || B->serving == QBK_F32) {
         // forward_prefill's per-token loop (engine/mod.rs:811-822) on the
-        // exact face: row t through the decode step at position t
-        if (seq != 0) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
+        // exact face or at fp32 serving: row t through the decode step at
+        // position t
+        if (seq != 0) return fail(QBK_ERR_VALIDATION, B->serving == QBK_F32 ? kF32Only : kExactFaceOnly);
         for (size_t t = 0; t < n; t++)
             if ((rc = block_decode_one(ctx, B, h + t * B->d, t, nullptr, stream))) return rc;
         return QBK_OK;
@@ -952,6 +1066,7 @@ static int block_decode_batch(qbk_ctx *ctx, qbk_block *B, float *h, const size_t
     int rc;
     if (!B || !h || (!pos && !pos_dev)) return fail(QBK_ERR_VALIDATION, "null argument");
     if (B->face == QBK_ATTN_EXACT) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
+    if (B->serving == QBK_F32) return fail(QBK_ERR_VALIDATION, kF32Only);
     if (n == 0 || n > B->nseq)
         return fail(QBK_ERR_VALIDATION, fmt("batch of %zu sequences on a block holding %zu", n, B->nseq));
     for (size_t i = 0; !pos_dev && i < n; i++) {
@@ -1055,6 +1170,7 @@ int qbk_block_decode_batch_pos_dev(qbk_ctx *ctx, qbk_block *B, float *h, const u
                                    void *workspace, size_t workspace_size, void *stream) {
     if (!pos) return fail(QBK_ERR_VALIDATION, "null argument");
     if (B && B->face == QBK_ATTN_EXACT) return fail(QBK_ERR_VALIDATION, kExactFaceOnly);
+    if (B && B->serving == QBK_F32) return fail(QBK_ERR_VALIDATION, kF32Only);
     if (B && n && n <= B->nseq) {
         int rc;
         if ((rc = pos_state_ready(B, n))) return rc;

@@ -441,6 +441,59 @@ __global__ void factor_f64_out(const double *u, const float *s1, const float *bi
     if (i < n) y[i] = ((float)u[i]) * s1[i] + bias[i];
 }
 
+}  // extern "C"
+
+namespace qbk {
+
+// The reference's row bitplanes of L (ub_rows, vbt_rows), formed from the
+// decode layout on first use and kept with the layer.
+int factor_rows_ready(const qbk_factor *L, hipStream_t s) {
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    if (L->ub_rows) return QBK_OK;
+    qbk_factor *M = const_cast<qbk_factor *>(L);
+    void *pu = nullptr, *pv = nullptr;
+    const size_t nu = L->dout * div_ceil(L->r, 8), nv = L->r * div_ceil(L->din, 8);
+    QBK_HIP(hipMalloc(&pu, nu));
+    M->allocs.push_back(pu);
+    QBK_HIP(hipMalloc(&pv, nv));
+    M->allocs.push_back(pv);
+    hipLaunchKernelGGL(q4_to_rows, dim3((unsigned)div_ceil(nu, 256)), dim3(256), 0, s, L->u_q4, L->dout, L->r,
+                       L->r_q, (uint8_t *)pu);
+    QBK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(q4_to_rows, dim3((unsigned)div_ceil(nv, 256)), dim3(256), 0, s, L->vt_q4, L->r, L->din,
+                       L->din_q, (uint8_t *)pv);
+    QBK_HIP(hipGetLastError());
+    QBK_HIP(hipStreamSynchronize(s));
+    M->vbt_rows = (uint8_t *)pv;
+    M->ub_rows = (uint8_t *)pu;
+    return QBK_OK;
+}
+
+// apply's fp32 serving (engine/mod.rs:393-436) of one token on the device:
+// z = f64(s2 x), t = Vb^T z and u = Ub t as f64 matvecs in element order
+// (the packed f64 product), y = f32(u) s1 + b.  x, y f32 device vectors;
+// scratch holds din + r + dout doubles; the rows must be formed
+// (factor_rows_ready).
+int factor_apply_f64_dev(qbk_ctx *ctx, const qbk_factor *L, const float *x, float *y, double *scratch,
+                         hipStream_t s) {
+    int rc;
+    double *z = scratch, *t = z + L->din, *u = t + L->r;
+    hipLaunchKernelGGL(factor_f64_in, dim3((unsigned)((L->din + 255) / 256)), dim3(256), 0, s, x,
+                       (const float *)L->s2, z, L->din);
+    QBK_HIP(hipGetLastError());
+    if ((rc = qbk_packed_matvec_dev(ctx, QBK_F64, L->vbt_rows, L->r, L->din, z, t, s))) return rc;
+    if ((rc = qbk_packed_matvec_dev(ctx, QBK_F64, L->ub_rows, L->dout, L->r, t, u, s))) return rc;
+    hipLaunchKernelGGL(factor_f64_out, dim3((unsigned)((L->dout + 255) / 256)), dim3(256), 0, s, (const double *)u,
+                       (const float *)L->s1, (const float *)L->bias, y, L->dout);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+}  // namespace qbk
+
+extern "C" {
+
 // engine/mod.rs:393-460 apply / apply_bf16 with host buffers.
 int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *L, int serving, const float *x, size_t batch,
                      float *y) {
@@ -458,47 +511,16 @@ int qbk_factor_apply(qbk_ctx *ctx, const qbk_factor *L, int serving, const float
         // reference's row layout, which the layer forms from its decode
         // layout on the first such call (a third copy of the signs only for
         // layers that use this face).
-        {
-            static std::mutex mu;
-            std::lock_guard<std::mutex> lock(mu);
-            if (!L->ub_rows) {
-                qbk_factor *M = const_cast<qbk_factor *>(L);
-                void *pu = nullptr, *pv = nullptr;
-                const size_t nu = L->dout * div_ceil(L->r, 8), nv = L->r * div_ceil(L->din, 8);
-                QBK_HIP(hipMalloc(&pu, nu));
-                M->allocs.push_back(pu);
-                QBK_HIP(hipMalloc(&pv, nv));
-                M->allocs.push_back(pv);
-                hipLaunchKernelGGL(q4_to_rows, dim3((unsigned)div_ceil(nu, 256)), dim3(256), 0, cs.s, L->u_q4, L->dout,
-                                   L->r, L->r_q, (uint8_t *)pu);
-                QBK_HIP(hipGetLastError());
-                hipLaunchKernelGGL(q4_to_rows, dim3((unsigned)div_ceil(nv, 256)), dim3(256), 0, cs.s, L->vt_q4, L->r,
-                                   L->din, L->din_q, (uint8_t *)pv);
-                QBK_HIP(hipGetLastError());
-                QBK_HIP(hipStreamSynchronize(cs.s));
-                M->vbt_rows = (uint8_t *)pv;
-                M->ub_rows = (uint8_t *)pu;
-            }
-        }
-        DevBuf dx, dy, dz, dt, du;
+        if ((rc = factor_rows_ready(L, cs.s))) return rc;
+        DevBuf dx, dy, dsc;
         if ((rc = dx.alloc(batch * L->din * 4)) || (rc = dy.alloc(batch * L->dout * 4)) ||
-            (rc = dz.alloc(L->din * 8)) || (rc = dt.alloc(L->r * 8)) || (rc = du.alloc(L->dout * 8)))
+            (rc = dsc.alloc((L->din + L->r + L->dout) * 8)))
             return rc;
         QBK_HIP(hipMemcpyAsync(dx.p, x, batch * L->din * 4, hipMemcpyHostToDevice, cs.s));
-        const unsigned gi = (unsigned)((L->din + 255) / 256), go = (unsigned)((L->dout + 255) / 256);
-        for (size_t bb = 0; bb < batch; bb++) {
-            hipLaunchKernelGGL(factor_f64_in, dim3(gi), dim3(256), 0, cs.s, (const float *)dx.p + bb * L->din,
-                               (const float *)L->s2, (double *)dz.p, L->din);
-            QBK_HIP(hipGetLastError());
-            if ((rc = qbk_packed_matvec_dev(ctx, QBK_F64, L->vbt_rows, L->r, L->din, dz.p, dt.p, cs.s)))
+        for (size_t bb = 0; bb < batch; bb++)
+            if ((rc = factor_apply_f64_dev(ctx, L, (const float *)dx.p + bb * L->din, (float *)dy.p + bb * L->dout,
+                                           (double *)dsc.p, cs.s)))
                 return rc;
-            if ((rc = qbk_packed_matvec_dev(ctx, QBK_F64, L->ub_rows, L->dout, L->r, dt.p, du.p, cs.s)))
-                return rc;
-            hipLaunchKernelGGL(factor_f64_out, dim3(go), dim3(256), 0, cs.s, (const double *)du.p,
-                               (const float *)L->s1, (const float *)L->bias, (float *)dy.p + bb * L->dout,
-                               L->dout);
-            QBK_HIP(hipGetLastError());
-        }
         QBK_HIP(hipMemcpyAsync(y, dy.p, batch * L->dout * 4, hipMemcpyDeviceToHost, cs.s));
         QBK_HIP(hipStreamSynchronize(cs.s));
         return QBK_OK;

@@ -144,4 +144,11 @@ size_t g32_workspace(const qbk_factor *L, size_t N);
 int g32_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, void *ws,
             hipStream_t s);
 
+// apply's fp32 serving on the device (factor.hip): the reference's row
+// bitplanes formed once, then one token's f64 product (scratch: din + r + dout
+// doubles).
+int factor_rows_ready(const qbk_factor *L, hipStream_t s);
+int factor_apply_f64_dev(qbk_ctx *ctx, const qbk_factor *L, const float *x, float *y, double *scratch,
+                         hipStream_t s);
+
 }  // namespace qbk

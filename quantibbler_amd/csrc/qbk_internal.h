@@ -160,15 +160,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
 // xor-shuffle tree; out(j, value) receives rotated channel j.  The decode
 // kernels that rotate a head all call this, so their values agree bit for
 // bit.
-template <class OUT>
+// F32 (fp32 serving, engine/mod.rs:854-876): the norm without the bf16
+// roundings of its input and output.
+template <class OUT, bool F32 = false>
 __device__ __forceinline__ void rope_head(const float *src, const float *w, float eps, const float2 *cs, int hd,
                                           int lane, OUT out) {
     const int half = hd / 2;
+    auto rd = [](float v) { return F32 ? v : bf16_to_f32(f32_to_bf16(v)); };
     float inv = 1.0f;
     if (w) {
         float ss = 0.0f;
         for (int j = lane; j < hd; j += 64) {
-            const float b = bf16_to_f32(f32_to_bf16(src[j]));
+            const float b = rd(src[j]);
             ss += b * b;
         }
 #pragma unroll
@@ -178,8 +181,8 @@ __device__ __forceinline__ void rope_head(const float *src, const float *w, floa
     for (int j = lane; j < half; j += 64) {
         float a = src[j], b = src[j + half];
         if (w) {
-            a = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(a)) * inv * w[j]));
-            b = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(b)) * inv * w[j + half]));
+            a = rd(rd(a) * inv * w[j]);
+            b = rd(rd(b) * inv * w[j + half]);
         }
         const float2 c = cs[j];
         out(j, a * c.x - b * c.y);

@@ -30,6 +30,9 @@ __global__ void __launch_bounds__(TRUNK_THREADS) trunk_embed(const float *table,
 // :1152-1160): the row rounded to bf16, its mean square in f32 (a tree over
 // the workgroup here; the reference's is one sequential fold), inv =
 // 1 / sqrt(ms + eps), out = bf16(b * inv * w) held as f32.
+// F32: norm_apply at fp32 serving (no bf16 roundings of the operand and
+// the output).
+template <bool F32>
 __global__ void __launch_bounds__(TRUNK_THREADS) trunk_rms_norm(const float *x, size_t d, const float *w,
                                                                float eps, float *out) {
     __shared__ float red[TRUNK_THREADS / 64];
@@ -37,7 +40,7 @@ __global__ void __launch_bounds__(TRUNK_THREADS) trunk_rms_norm(const float *x, 
     float *orow = out + (size_t)blockIdx.x * d;
     float ss = 0.0f;
     for (size_t i = threadIdx.x; i < d; i += TRUNK_THREADS) {
-        const float b = bf16_to_f32(f32_to_bf16(xr[i]));
+        const float b = F32 ? xr[i] : bf16_to_f32(f32_to_bf16(xr[i]));
         ss += b * b;
     }
 #pragma unroll
@@ -49,8 +52,8 @@ __global__ void __launch_bounds__(TRUNK_THREADS) trunk_rms_norm(const float *x, 
     for (int i = 0; i < TRUNK_THREADS / 64; i++) tot += red[i];
     const float inv = 1.0f / sqrtf(tot / (float)d + eps);
     for (size_t i = threadIdx.x; i < d; i += TRUNK_THREADS) {
-        const float b = bf16_to_f32(f32_to_bf16(xr[i]));
-        orow[i] = bf16_to_f32(f32_to_bf16(b * inv * w[i]));
+        const float b = F32 ? xr[i] : bf16_to_f32(f32_to_bf16(xr[i]));
+        orow[i] = F32 ? b * inv * w[i] : bf16_to_f32(f32_to_bf16(b * inv * w[i]));
     }
 }
 
@@ -171,8 +174,20 @@ int qbk_rms_norm_dev(qbk_ctx *ctx, const float *x, size_t rows, size_t d, const 
     if (!x || !w || !out) return fail(QBK_ERR_VALIDATION, "null argument");
     if (rows == 0 || d == 0) return QBK_OK;
     if ((rc = bind(ctx))) return rc;
-    hipLaunchKernelGGL(trunk_rms_norm, dim3((unsigned)rows), dim3(TRUNK_THREADS), 0, (hipStream_t)stream, x, d, w,
-                       (float)eps, out);
+    hipLaunchKernelGGL(trunk_rms_norm<false>, dim3((unsigned)rows), dim3(TRUNK_THREADS), 0, (hipStream_t)stream, x, d,
+                       w, (float)eps, out);
+    QBK_HIP(hipGetLastError());
+    return QBK_OK;
+}
+
+int qbk_rms_norm_f32_dev(qbk_ctx *ctx, const float *x, size_t rows, size_t d, const float *w, double eps,
+                         float *out, void *stream) {
+    int rc;
+    if (!x || !w || !out) return fail(QBK_ERR_VALIDATION, "null argument");
+    if (rows == 0 || d == 0) return QBK_OK;
+    if ((rc = bind(ctx))) return rc;
+    hipLaunchKernelGGL(trunk_rms_norm<true>, dim3((unsigned)rows), dim3(TRUNK_THREADS), 0, (hipStream_t)stream, x, d,
+                       w, (float)eps, out);
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

@@ -253,10 +253,11 @@ def embed_dev(ctx: GpuContext, table, vocab: int, d_model: int, tokens, n: int, 
                                     _ptr(out), _stream(stream)))
 
 
-def rms_norm_dev(ctx: GpuContext, x, rows: int, d: int, w, eps: float, out, stream=None):
-    """The final norm (engine/mod.rs:943) at bf16 serving, per row."""
-    check(_lib.load().qbk_rms_norm_dev(ctx.handle, _ptr(x), int(rows), int(d), _ptr(w), float(eps), _ptr(out),
-                                       _stream(stream)))
+def rms_norm_dev(ctx: GpuContext, x, rows: int, d: int, w, eps: float, out, stream=None, serving: str = "bf16"):
+    """The final norm (engine/mod.rs:943) per row at the serving dtype:
+    "bf16" (operand and output rounded to bf16) or "fp32" (as is)."""
+    fn = _lib.load().qbk_rms_norm_f32_dev if serving == "fp32" else _lib.load().qbk_rms_norm_dev
+    check(fn(ctx.handle, _ptr(x), int(rows), int(d), _ptr(w), float(eps), _ptr(out), _stream(stream)))
 
 
 def advance_positions_dev(ctx: GpuContext, pos, n: int, stream=None):
@@ -353,6 +354,7 @@ class DecoderBlock:
         self.capacity = int(capacity)
         self.n_seqs = int(n_seqs)
         self.face = "sage"
+        self.serving = "bf16"
 
     def decode_dev(self, h, pos: int, stream=None):
         """h: device f32 [d_model] (a contiguous torch tensor, or a raw device
@@ -467,6 +469,18 @@ class DecoderBlock:
             raise _lib.KernelError(f"attention face must be one of {sorted(self.ATTENTION_FACES)}, got {face!r}")
         check(_lib.load().qbk_block_set_attention_face(self._h, self.ATTENTION_FACES[face]))
         self.face = face
+
+    SERVING = {"fp32": 1, "bf16": 2}
+
+    def set_serving(self, serving: str):
+        """The block's serving dtype (engine/mod.rs ServingDtype): "bf16"
+        (the default) or "fp32" -- apply's f64 products and f32 norms, one
+        sequence at host positions (decode_dev, prefill_dev token by
+        token).  The first "fp32" call forms the layers' row bitplanes."""
+        if serving not in self.SERVING:
+            raise _lib.KernelError(f"serving must be one of {sorted(self.SERVING)}, got {serving!r}")
+        check(_lib.load().qbk_block_set_serving(self.ctx.handle, self._h, self.SERVING[serving]))
+        self.serving = serving
 
     def reset(self):
         check(_lib.load().qbk_block_reset(self._h))

@@ -227,31 +227,41 @@ class DeviceModel:
     face once, as the engine does at load (engine/mod.rs:953-968): "sage"
     (the sage decode attention; prefill on the block-scaled SageAttention)
     or "exact" (f32 attention over the cache, one sequence, prefill token by
-    token).  Built from a ModelDir; torch supplies the device buffers
-    (plumbing only -- every step runs in libqbk)."""
+    token).  ``serving`` is the engine's serving dtype: "bf16" (remainder
+    tensors rounded to bf16, the GEMV / GEMM projections) or "fp32" (the
+    tensors as stored, apply's f64 products, f32 norms; one sequence, prefill
+    token by token).  Built from a ModelDir; torch supplies the device
+    buffers (plumbing only -- every step runs in libqbk)."""
 
     def __init__(self, ctx, md: ModelDir, capacity: int, block_size: int = 64, n_seqs: int = 1,
-                 attention: str = "sage"):
+                 attention: str = "sage", serving: str = "bf16"):
         import torch
 
         from .gpu import DecoderBlock, FactorLayer, LmHead
 
         self.ctx, self.md, self.capacity, self.n_seqs = ctx, md, int(capacity), int(n_seqs)
+        if serving not in ("bf16", "fp32"):
+            raise ValueError(f"serving must be 'bf16' or 'fp32', got {serving!r}")
+        self.serving = serving
+        # bf16 serving rounds the remainder tensors to bf16 (engine/mod.rs:695-706)
+        rnd = _bf16_values if serving == "bf16" else (lambda a: np.ascontiguousarray(a, np.float32))
         dev = torch.device("cuda")
         self.layers, self.blocks = [], []
         for b in range(md.n_layers):
             layers = [FactorLayer.from_qpk1(ctx, s) for s in md.block_layers(b)]
             self.layers.append(layers)
-            norms = {k: _bf16_values(v) for k, v in md.block_norms(b).items()}
+            norms = {k: rnd(v) for k, v in md.block_norms(b).items()}
             self.blocks.append(DecoderBlock(ctx, layers, norms["input"], norms["post_attention"], md.n_heads,
                                             md.n_kv_heads, md.head_dim, md.rope_theta, md.rms_norm_eps,
                                             capacity, block_size, norms.get("q_norm"), norms.get("k_norm"),
                                             n_seqs=self.n_seqs))
             self.blocks[-1].set_attention_face(attention)
+            if serving == "fp32":
+                self.blocks[-1].set_serving("fp32")
         self.attention = attention
-        self.embedding = torch.from_numpy(_bf16_values(md.embedding)).to(dev)
-        self.final_norm = torch.from_numpy(_bf16_values(md.final_norm())).to(dev)
-        self.head = LmHead.from_rows(ctx, _bf16_values(md.head_rows()))
+        self.embedding = torch.from_numpy(rnd(md.embedding)).to(dev)
+        self.final_norm = torch.from_numpy(rnd(md.final_norm())).to(dev)
+        self.head = LmHead.from_rows(ctx, rnd(md.head_rows()))
         self.h = torch.empty(md.d_model, dtype=torch.float32, device=dev)
         self.hn = torch.empty(md.d_model, dtype=torch.float32, device=dev)
         self.logits = torch.empty(md.vocab_size, dtype=torch.float32, device=dev)
@@ -286,7 +296,8 @@ class DeviceModel:
         ws = torch.empty(need, dtype=torch.uint8, device="cuda")
         for b in self.blocks:
             b.prefill_seq_dev(int(seq), h, n, ws, need, stream)
-        rms_norm_dev(self.ctx, h[n - 1], 1, md.d_model, self.final_norm, md.rms_norm_eps, self.hn, stream)
+        rms_norm_dev(self.ctx, h[n - 1], 1, md.d_model, self.final_norm, md.rms_norm_eps, self.hn, stream,
+                     self.serving)
         self.head.logits_dev(self.hn, 1, self.logits, stream)
         self.positions[int(seq)] = n
         if int(seq) == 0:
@@ -338,7 +349,8 @@ class DeviceModel:
         embed(self.ctx, self.embedding, md.vocab_size, md.d_model, [int(token)], self.h, stream)
         for b in self.blocks:
             b.decode_dev(self.h, self.pos, stream)
-        rms_norm_dev(self.ctx, self.h, 1, md.d_model, self.final_norm, md.rms_norm_eps, self.hn, stream)
+        rms_norm_dev(self.ctx, self.h, 1, md.d_model, self.final_norm, md.rms_norm_eps, self.hn, stream,
+                     self.serving)
         self.head.logits_dev(self.hn, 1, self.logits, stream)
         self.pos += 1
         self.positions[0] = self.pos

@@ -170,12 +170,15 @@ extern "C" {
     pub fn qbk_block_set_positions(block: *mut QbkBlock, pos: *const usize, n: usize) -> c_int;
     pub fn qbk_block_set_filled(block: *mut QbkBlock, rows: *const usize, n: usize) -> c_int;
     pub fn qbk_block_set_attention_face(block: *mut QbkBlock, face: c_int) -> c_int;
+    pub fn qbk_block_set_serving(ctx: *mut QbkCtx, block: *mut QbkBlock, serving: c_int) -> c_int;
     pub fn qbk_embed(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32, n: usize,
                      out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_embed_dev(ctx: *mut QbkCtx, table: *const f32, vocab: usize, d_model: usize, tokens: *const i32,
                          n: usize, out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_rms_norm_dev(ctx: *mut QbkCtx, x: *const f32, rows: usize, d: usize, w: *const f32, eps: f64,
                             out: *mut f32, stream: *mut c_void) -> c_int;
+    pub fn qbk_rms_norm_f32_dev(ctx: *mut QbkCtx, x: *const f32, rows: usize, d: usize, w: *const f32, eps: f64,
+                                out: *mut f32, stream: *mut c_void) -> c_int;
     pub fn qbk_argmax_dev(ctx: *mut QbkCtx, logits: *const f32, rows: usize, vocab: usize, out: *mut i32,
                           stream: *mut c_void) -> c_int;
     pub fn qbk_positions_advance_dev(ctx: *mut QbkCtx, pos: *mut u32, n: usize, stream: *mut c_void) -> c_int;

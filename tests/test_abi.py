@@ -105,6 +105,8 @@ def test_block_attention_face_validation(lib):
 
     with pytest.raises(KernelError, match="null block"):
         check(lib.qbk_block_set_attention_face(None, 1))
+    with pytest.raises(KernelError, match="null block"):
+        check(lib.qbk_block_set_serving(None, None, 1))
 
 
 def test_packed_matvec_ceiling_precedes_device_use(lib):

@@ -16,6 +16,10 @@ torch = pytest.importorskip("torch")
 
 COS_MIN = 0.9999
 REL_MAX = 0.01
+# fp32 serving (f64 products): the block's tree-summed norms and device exps
+# against the reference's sequential sums and libm exps
+F32_COS_MIN = 0.9999999
+F32_REL_MAX = 1e-5  # the exact faces' budget (cross_face_token_identity.rs: rel <= 1e-5)
 
 
 def say(*a):
@@ -168,6 +172,57 @@ def test_decoder_block_exact_face_prefill_and_refusals(ctx, orc):
         block.decode_pos_dev(h, pos, st)
     with pytest.raises(KernelError, match=r"attention face must be one of \['exact', 'sage'\], got 'tiled'"):
         block.set_attention_face("tiled")
+    block.close()
+
+
+@pytest.mark.parametrize("face", ["exact", "sage"])
+def test_decoder_block_fp32_serving_matches_oracle(ctx, orc, face):
+    """fp32 serving (engine/mod.rs ServingDtype::Fp32: apply's f64 products,
+    f32 norms) on each attention face, against the oracle's block step at
+    fp32 serving.  The products are the reference's f64 row sums; the norms'
+    sums are trees and the exps the device's, hence a tolerance, far tighter
+    than bf16 serving's."""
+    block, layers, norms, rng, g = _small_block(ctx, orc, 51 + (face == "sage"), True)
+    block.set_serving("fp32")
+    block.set_attention_face(face)
+    kc = np.zeros((g["cap"], g["Hk"] * g["hd"]), np.float32)
+    vc = np.zeros((g["cap"], g["Hk"] * g["hd"]), np.float32)
+    st = torch.cuda.current_stream()
+    worst = (1.0, 0.0)
+    for pos in range(20):
+        h = rng.standard_normal(g["d"]).astype(np.float32)
+        hd_dev = torch.from_numpy(h).cuda()
+        block.decode_dev(hd_dev, pos, st)
+        torch.cuda.synchronize()
+        want = orc.block_step(layers, norms, h, pos, kc, vc, g["H"], g["Hk"], g["hd"], 500000.0, 1e-5, "fp32",
+                              "scalar" if face == "exact" else "sage", g["blk"])
+        cos, rel = metrics(hd_dev.cpu().numpy(), want)
+        say(f"fp32 pos {pos} ({face}): out cos {cos:.9f} rel {rel:.2e}")
+        worst = (min(worst[0], cos), max(worst[1], rel))
+        assert cos >= F32_COS_MIN and rel <= F32_REL_MAX, (pos, face, cos, rel)
+    say("fp32 worst", face, worst)
+    # the token-by-token prefill equals the same rows as decode steps; the
+    # batched step refuses fp32 serving
+    from quantibbler_amd import KernelError
+
+    n = 9
+    rows = rng.standard_normal((n, g["d"])).astype(np.float32)
+    a = torch.from_numpy(rows).cuda()
+    need = block.prefill_workspace_size(n)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    block.reset()
+    block.prefill_dev(a, n, ws, need, st)
+    block.reset()
+    b = torch.from_numpy(rows).cuda()
+    for t in range(n):
+        block.decode_dev(b[t], t, st)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
+    nb = block.decode_batch_workspace_size(1)
+    wsb = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    if face == "sage":
+        with pytest.raises(KernelError, match="fp32 serving runs one sequence at host positions"):
+            block.decode_batch_dev(b[0], [n], wsb, nb, st)
     block.close()
 
 

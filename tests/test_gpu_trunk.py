@@ -239,6 +239,38 @@ def test_device_trunk_exact_face(ctx, orc, md):
     m.close()
 
 
+@pytest.mark.parametrize("face", ["exact", "sage"])
+def test_device_trunk_fp32_serving(ctx, orc, md, face):
+    """The trunk at fp32 serving (engine/mod.rs ServingDtype::Fp32: apply's
+    f64 products, f32 norms, the remainder tensors as stored) on each
+    attention face, against the oracle's fp32 trunk on the same face within
+    the exact faces' budget (relative inf-norm <= 1e-5,
+    cross_face_token_identity.rs) and the HF goldens of parity-tiny (the
+    oracle reproduces them to 8.6e-5 at fp32 serving)."""
+    from quantibbler_amd.model import DeviceModel
+
+    say(f"device trunk on parity-tiny, fp32 serving, {face} face")
+    with open(os.path.join(TINY, "goldens.json")) as f:
+        g = json.load(f)
+    ids = g["input_ids"]
+    cap = len(ids) + 4
+    m = DeviceModel(ctx, md, capacity=cap, attention=face, serving="fp32")
+    ref = orc.Trunk(md, serving="fp32", attention="scalar" if face == "exact" else "sage", capacity=cap)
+    worst_gold, worst_orc = 0.0, 0.0
+    st = torch.cuda.current_stream()
+    for pos, tok in enumerate(ids):
+        got = m.step(tok, st).cpu().numpy()
+        want = ref.step(tok)
+        gold = np.array(g["logits"][pos], np.float32)
+        rel_inf = float(np.abs(got - want).max() / np.abs(want).max())
+        worst_gold = max(worst_gold, float(np.abs(got - gold).max()))
+        worst_orc = max(worst_orc, rel_inf)
+        say(f"  pos {pos}: |device - HF| {np.abs(got - gold).max():.3g}  rel inf-norm to the oracle {rel_inf:.3g}")
+    assert worst_orc <= 1e-5, worst_orc
+    assert worst_gold <= (1e-3 if face == "exact" else 1e-2), worst_gold
+    m.close()
+
+
 def _qpk1_v2(orc, rng, dout, din, r):
     """A random v2 qpk1 layer stream (f16 scales and bias), as the reference's
     writer lays it out (container bitstreams, element (i, j) at bit i r + j)."""
