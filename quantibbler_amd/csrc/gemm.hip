@@ -340,7 +340,12 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
     for (int q = 0; q < NG1; q++)
 #pragma unroll
         for (int rt = 0; rt < 4; rt++) acc1[q][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    constexpr int R1 = NG1 == 1 ? 8 : 4;  // stage 1's ring: eight slices ahead for one group a wave
+    // stage 1's ring: eight slices ahead for one group a wave, two for two
+    // groups (four slices ahead of two groups held 128 VGPRs and spilled
+    // 27 of them to scratch inside the chunk loop, 73 with f32 x; two
+    // slices spill none with bf16 x: config 3's prefill 0.539-0.541 ->
+    // 0.493-0.511 ms a decoder layer, three slices 0.506-0.507)
+    constexpr int R1 = NG1 == 1 ? 8 : 2;
     u32x4_t ring1[R1][NG1];
 #define Q4G_ISSUE1(U, SLOT)                                                             \
     {                                                                                   \
