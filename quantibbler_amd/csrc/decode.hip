@@ -374,11 +374,12 @@ __device__ __forceinline__ void q4_epilogue(const f32x4_t acc[4], float *T, cons
         }
         const float amax = q4_block_max32(fabsf(t));
         const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
-        const int hw = __builtin_amdgcn_cvt_pk_fp8_f32(t * pow2f(-e_hi), 0.0f, 0, false);
-        const float r = t - __builtin_amdgcn_cvt_f32_fp8(hw, 0) * pow2f(e_hi);  // exact residual
+        const float sc_hi = pow2f(e_hi);
+        const int hw = (int)q4_fp8x1(t, sc_hi);
+        const float r = t - q4_f32x1((uint32_t)hw, sc_hi);  // exact residual
         const float rmax = q4_block_max32(fabsf(r));
         const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
-        const int lw = __builtin_amdgcn_cvt_pk_fp8_f32(r * pow2f(-e_lo), 0.0f, 0, false);
+        const int lw = (int)q4_fp8x1(r, pow2f(e_lo));
         const int q = (lane >> 4) & 1, h = lane >> 5;
         const size_t base = ((size_t)L.tb_slice0 + (rg >> 1)) * 4;
         const size_t slot = (base + 2 * (rg & 1) + h) * ncol + 2 * b;  // hi column; lo = +1

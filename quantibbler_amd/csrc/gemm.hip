@@ -12,7 +12,7 @@
 // column group takes columns 2b, 2b + 1 of one MFMA, 8 tokens a group.
 //
 // One workgroup owns one column group (8 tokens) and all of the layer's rows:
-//   1. x of its tokens becomes stage 1's operand chunk by chunk (8 slices of
+//   1. x of its tokens becomes stage 1's operand chunk by chunk (16 slices of
 //      128 k a chunk, double buffered in LDS): z = bf16(s2 * x) and its
 //      hi/lo split, formed once per token;
 //   2. stage 1: each wave takes 64-row groups of Vb^T (r) round robin and
@@ -26,8 +26,17 @@
 // Nothing between the stages leaves the CU: no operand prep launch, no split
 // K partials, no t round trip through memory.  Every workgroup reads all of
 // the layer's signs; they stay in the XCD's L2 (a config-2 layer is 1 MiB).
-// Sign words are loaded in units of four slices for two row groups, one unit
-// ahead of the MFMAs that use them.
+// Sign words stream through per-wave register rings, several slices ahead
+// of the MFMAs that use them.
+//
+// Where the time goes (config 2, B = 2048, measured per wave): an MFMA of
+// this shape holds a SIMD 32 cycles, but the SIMD's VALU ops do not overlap
+// it freely -- each VALU op costs about 4 cycles on top past the first few
+// in an MFMA's shadow -- so the VALU work per MFMA (4 ops building the signs,
+// plus the operand conversion and the epilogues) sets the pace as much as
+// the MFMAs do.  Hence: scaled fp8 conversions (one op for multiply and
+// convert), pair sums folded into DPP adds, and wave priorities that keep the
+// waves of a SIMD level so that none is left to run alone at the end.
 #include <mutex>
 
 #include "factor_internal.h"
@@ -166,8 +175,11 @@ __device__ __forceinline__ void q4g_store_run(const Q4GRun<XF32> &R, uint8_t *sl
 
 // The value of the lane's column partner (lane ^ 1: the other half of a
 // token's hi / lo pair) -- a DPP quad permutation, no LDS round trip.
+// Every source lane of a quad permutation exists, so bound_ctrl changes
+// nothing here (all lanes are active where it is called); set, it lets the
+// compiler fold the move into the add that uses it (v_add_f32_dpp).
 __device__ __forceinline__ float q4g_pair(float a) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, true));
 }
 
 // max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups holding a
@@ -225,32 +237,28 @@ __device__ __forceinline__ void q4g_epilogue1(const f32x4_t acc[4], uint8_t *tbu
         }
         amax = q4g_max4(amax);
         const int e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
-        const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+        const float sc_hi = pow2f(e_hi);
         uint32_t hw[2];
         float rmax = 0.0f;
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
-            int w = __builtin_amdgcn_cvt_pk_fp8_f32(t[tt][0] * inv_hi, t[tt][1] * inv_hi, 0, false);
-            w = __builtin_amdgcn_cvt_pk_fp8_f32(t[tt][2] * inv_hi, t[tt][3] * inv_hi, w, true);
-            hw[tt] = (uint32_t)w;
-            t[tt][0] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
-            t[tt][1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
-            t[tt][2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
-            t[tt][3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+            hw[tt] = q4_fp8x4(t[tt][0], t[tt][1], t[tt][2], t[tt][3], sc_hi);
+            float b[4];
+            q4_f32x4(hw[tt], sc_hi, b);
 #pragma unroll
-            for (int i = 0; i < 4; i++) rmax = fmaxf(rmax, fabsf(t[tt][i]));
+            for (int i = 0; i < 4; i++) {
+                t[tt][i] -= b[i];  // exact residuals
+                rmax = fmaxf(rmax, fabsf(t[tt][i]));
+            }
         }
         rmax = q4g_max4(rmax);
         const int e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
-        const float inv_lo = pow2f(-e_lo);
+        const float sc_lo = pow2f(e_lo);
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
             const int rt = pr + 2 * tt, u = 4 * half + rt;
             uint32_t w = hw[tt];
-            if (col & 1) {
-                int lw = __builtin_amdgcn_cvt_pk_fp8_f32(t[tt][0] * inv_lo, t[tt][1] * inv_lo, 0, false);
-                w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[tt][2] * inv_lo, t[tt][3] * inv_lo, lw, true);
-            }
+            if (col & 1) w = q4_fp8x4(t[tt][0], t[tt][1], t[tt][2], t[tt][3], sc_lo);
             *(uint32_t *)(slice + (u & 1) * 1024 + ((u >> 1) * 16 + col) * 16 + 4 * G) = w;
         }
         if (G == 0) slice[Q4G_SC + (2 * pr + half) * 16 + col] = (uint8_t)((col & 1 ? e_lo : e_hi) + 127);
@@ -260,7 +268,15 @@ __device__ __forceinline__ void q4g_epilogue1(const f32x4_t acc[4], uint8_t *tbu
 // Stage 2's epilogue for row group g: y = bf16((hi + lo) / 1.5) * s1 + bias,
 // s1 and bias of the group's 64 rows read from the wave's LDS region sb
 // ([64] s1 then [64] bias); the even lane of a column pair stores the four
-// rows it holds of token col / 2.
+// rows it holds of token col / 2 (splitting the rows between the pair, two
+// each, cuts the VALU work by a third but measured 2 us slower at config 2,
+// B = 2048: 64 lanes of 4-byte stores against 32 of 8).  VECY: y rows take
+// 4-element stores (dout a multiple of 4, y aligned), so a lane's four rows
+// are all in or all out; otherwise element by element.  The two are
+// separate kernels: one store per row tile keeps the count of memory
+// operations in flight the same on every path, which the waits on the sign
+// ring rely on.
+template <bool VECY>
 __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArgs &a, size_t g, const float *sb,
                                               size_t n0, int lane, bool ybf16) {
     const int col = lane & 15, G = lane >> 4;
@@ -280,7 +296,7 @@ __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArg
         y[2] = __uint_as_float(u23 << 16) * s1a[2] + bia[2];
         y[3] = __uint_as_float(u23 & 0xffff0000u) * s1a[3] + bia[3];
         if ((col & 1) || n >= a.N || row0 >= a.dout) continue;
-        if (a.vec_y && row0 + 4 <= a.dout) {
+        if constexpr (VECY) {
             if (ybf16)
                 *(uint2 *)((uint16_t *)a.y + n * a.dout + row0) =
                     make_uint2(f32x2_to_bf16x2(y[0], y[1]), f32x2_to_bf16x2(y[2], y[3]));
@@ -299,6 +315,19 @@ __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArg
     }
 }
 
+// The wave's issue priority, 0 (lowest) to 3: lowered as a wave gets ahead
+// so that the SIMD's scheduler, which otherwise favours the oldest wave,
+// keeps the waves of a SIMD level and they finish together -- a wave left
+// alone at the end runs its MFMAs and VALU work with nothing to overlap.
+__device__ __forceinline__ void q4g_prio(uint32_t level) {
+    switch (level) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+    }
+}
+
 // Sign words stream through a ring of Q4G_RING units per wave, all in
 // flight: a unit's loads are issued Q4G_RING units before its MFMAs.
 // Loads are unconditional (indices clamped into the layer) so that the
@@ -308,7 +337,7 @@ __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArg
 // NG1: stage-1 row groups a wave accumulates (1: r_p <= 1024, 2: r_p <=
 // 2048).  Stage 1's unit: one slice of the wave's NG1 row groups (their B
 // fragment read once); stage 2's unit: one slice of a pair of row groups.
-template <bool XF32, bool YBF16, int NG1>
+template <bool XF32, bool YBF16, int NG1, bool VECY>
 __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t q4g_lds[];
     uint8_t *xbuf = q4g_lds;                             // [2][Q4G_CH slices]
@@ -374,6 +403,8 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
         for (int j = 0; j < Q4G_CH; j++) {
             const int slot = j % R1, cur = j & 1;
             const uint32_t s = c * Q4G_CH + j;
+            // the chunk ends at a barrier: keep the waves level up to it
+            if (j % (Q4G_CH / 4) == 0) q4g_prio(3 - j / (Q4G_CH / 4));
             if (j + 1 < Q4G_CH) q4g_bfrag(xs + (j + 1) * Q4G_SLICE, lane, bvq[cur ^ 1], bsq[cur ^ 1]);
             if (s < ns1) {
 #pragma unroll
@@ -389,13 +420,18 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
     (void)nu1;
 
     // ---- stage 2 --------------------------------------------------------
-    // this wave's row groups wave + 8q, two at a time; units of one slice of
-    // a pair, flattened over the pairs (running counters: (p, s) of the unit
-    // computed, (pi, si) of the unit issued); s1 and bias of a pair's rows
-    // are loaded one pair ahead and staged through the wave's LDS region
+    // this wave's row groups wave + 16q, two at a time; a pair's units are
+    // its slices, rounded up to the ring depth so that each unit's ring slot
+    // is fixed at compile time (units past ns2 load a clamped slice and skip
+    // their MFMAs).  The ring runs on across pairs: (pi, si) is the unit
+    // issued.  The epilogue, with the only stores and s1 / bias loads, sits
+    // between pairs, outside the unit loop, so the waits on the ring keep
+    // their counts.  s1 and bias of a pair's rows are loaded one pair ahead
+    // and staged through the wave's LDS region.
     const uint32_t nrg2 = a.n_rg2, ns2 = a.ns2, dout = a.dout;
     const int ng2 = wave < (int)nrg2 ? (int)((nrg2 - 1 - wave) / Q4G_WAVES) + 1 : 0;
-    const uint32_t np2 = (uint32_t)(ng2 + 1) >> 1, total = np2 * ns2;
+    const uint32_t np2 = (uint32_t)(ng2 + 1) >> 1;
+    const uint32_t nsr = (ns2 + Q4G_RING - 1) / Q4G_RING * Q4G_RING;
     float *sb = (float *)(tbuf + ns2 * Q4G_SLICE) + wave * 256;  // [2 groups][s1 64 | bias 64]
     f32x4_t acc2[2][4];
     u32x4_t ring2[Q4G_RING][2];
@@ -403,12 +439,13 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
 #define Q4G_ISSUE2(SLOT)                                                                \
     {                                                                                   \
         const uint32_t p_ = pi < np2 ? pi : np2 - 1;                                    \
+        const uint32_t s_ = si < ns2 ? si : ns2 - 1;                                    \
         _Pragma("unroll") for (int w = 0; w < 2; w++) {                                 \
             uint32_t g = (uint32_t)wave + Q4G_WAVES * (2 * p_ + w);                     \
             g = g < nrg2 ? g : nrg2 - 1;                                                \
-            ring2[SLOT][w] = b2[((size_t)g * ns2 + si) * 64 + lane];                    \
+            ring2[SLOT][w] = b2[((size_t)g * ns2 + s_) * 64 + lane];                    \
         }                                                                               \
-        if (++si == ns2) {                                                              \
+        if (++si == nsr) {                                                              \
             si = 0;                                                                     \
             ++pi;                                                                       \
         }                                                                               \
@@ -424,7 +461,7 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
     }
     // the first units' sign words and pair 0's scales in flight under
     // stage 1's epilogue
-    if (total > 0) {
+    if (np2 > 0) {
         Q4G_SCALES2(0u)
 #pragma unroll
         for (int k = 0; k < Q4G_RING; k++) Q4G_ISSUE2(k)
@@ -441,47 +478,41 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
         }
     q4g_lds_barrier();
 
-    if (total > 0) {
-        uint32_t p = 0, s = 0;
+    for (uint32_t p = 0; p < np2; p++) {
+        const bool two = 2 * p + 1 < (uint32_t)ng2;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int rt = 0; rt < 4; rt++) acc2[h][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
         i32x8_t bvq[2];
         int bsq[2];
         q4g_bfrag(tbuf, lane, bvq[0], bsq[0]);
-        for (uint32_t u0 = 0; u0 < total; u0 += Q4G_RING) {
+        for (uint32_t s0 = 0; s0 < nsr; s0 += Q4G_RING) {
+            q4g_prio(3 - 4 * (p * nsr + s0) / (np2 * nsr));
 #pragma unroll
             for (int k = 0; k < Q4G_RING; k++) {
                 const int cur = k & 1;
-                const uint32_t sn = s + 1 == ns2 ? 0 : s + 1;
+                const uint32_t s = s0 + k, sn = s + 1 < ns2 ? s + 1 : ns2 - 1;
                 q4g_bfrag(tbuf + sn * Q4G_SLICE, lane, bvq[cur ^ 1], bsq[cur ^ 1]);
-                if (u0 + k < total) {
-                    const bool two = 2 * p + 1 < (uint32_t)ng2;
-                    if (s == 0) {
-#pragma unroll
-                        for (int h = 0; h < 2; h++)
-#pragma unroll
-                            for (int rt = 0; rt < 4; rt++) acc2[h][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
+                if (s < ns2) {
                     q4g_mfma4(acc2[0], ring2[k][0], bvq[cur], bsq[cur], c7);
                     if (two) q4g_mfma4(acc2[1], ring2[k][1], bvq[cur], bsq[cur], c7);
-                    if (sn == 0) {
-                        // the pair is complete: its scales through LDS, then the next pair's in flight
-#pragma unroll
-                        for (int w = 0; w < 2; w++) {
-                            sb[128 * w + lane] = sv[w][0];
-                            sb[128 * w + 64 + lane] = sv[w][1];
-                        }
-                        __builtin_amdgcn_wave_barrier();
-                        Q4G_SCALES2(p + 1 < np2 ? p + 1 : p)
-                        const size_t g0 = (size_t)wave + Q4G_WAVES * (2 * p);
-                        q4g_epilogue2(acc2[0], a, g0, sb, n0, lane, YBF16);
-                        if (two) q4g_epilogue2(acc2[1], a, g0 + Q4G_WAVES, sb + 128, n0, lane, YBF16);
-                        __builtin_amdgcn_wave_barrier();
-                    }
                 }
                 Q4G_ISSUE2(k)
-                s = sn;
-                p += sn == 0;
             }
         }
+        // the pair is complete: its scales through LDS, then the next pair's in flight
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            sb[128 * w + lane] = sv[w][0];
+            sb[128 * w + 64 + lane] = sv[w][1];
+        }
+        __builtin_amdgcn_wave_barrier();
+        Q4G_SCALES2(p + 1 < np2 ? p + 1 : p)
+        const size_t g0 = (size_t)wave + Q4G_WAVES * (2 * p);
+        q4g_epilogue2<VECY>(acc2[0], a, g0, sb, n0, lane, YBF16);
+        if (two) q4g_epilogue2<VECY>(acc2[1], a, g0 + Q4G_WAVES, sb + 128, n0, lane, YBF16);
+        __builtin_amdgcn_wave_barrier();
     }
 #undef Q4G_ISSUE2
 #undef Q4G_SCALES2
@@ -490,6 +521,17 @@ __global__ void __launch_bounds__(64 * Q4G_WAVES) q4g_kernel(Q4GArgs a) {
 // ------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------
+
+// Every instantiation, indexed by xf32 << 3 | ybf16 << 2 | (NG1 == 2) << 1 | vecy.
+#define Q4G_K(XF, YB, NG, VY) (const void *)q4g_kernel<XF, YB, NG, VY>
+static const void *const q4g_kernels[16] = {
+    Q4G_K(false, false, 1, false), Q4G_K(false, false, 1, true), Q4G_K(false, false, 2, false),
+    Q4G_K(false, false, 2, true),  Q4G_K(false, true, 1, false), Q4G_K(false, true, 1, true),
+    Q4G_K(false, true, 2, false),  Q4G_K(false, true, 2, true),  Q4G_K(true, false, 1, false),
+    Q4G_K(true, false, 1, true),   Q4G_K(true, false, 2, false), Q4G_K(true, false, 2, true),
+    Q4G_K(true, true, 1, false),   Q4G_K(true, true, 1, true),   Q4G_K(true, true, 2, false),
+    Q4G_K(true, true, 2, true)};
+#undef Q4G_K
 
 // x chunks, stage 2's operand, each wave's s1 / bias staging (1 KiB)
 static uint32_t q4g_lds_bytes(const qbk_factor *L) {
@@ -533,10 +575,7 @@ int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
         std::lock_guard<std::mutex> lock(mu);
         if (dev < 64 && !((done >> dev) & 1)) {
             const uint32_t most = (2 * Q4G_CH + Q4G_MAX_RG1 / 2) * Q4G_SLICE + Q4G_WAVES * 1024;
-            for (const void *k : {(const void *)q4g_kernel<false, false, 1>, (const void *)q4g_kernel<false, true, 1>,
-                                  (const void *)q4g_kernel<true, false, 1>, (const void *)q4g_kernel<true, true, 1>,
-                                  (const void *)q4g_kernel<false, false, 2>, (const void *)q4g_kernel<false, true, 2>,
-                                  (const void *)q4g_kernel<true, false, 2>, (const void *)q4g_kernel<true, true, 2>})
+            for (const void *k : q4g_kernels)
                 QBK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)most));
             done |= 1ull << dev;
         }
@@ -563,20 +602,11 @@ int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.t_out = t_out;
     a.r_p = (uint32_t)L->r_p;
     const dim3 grid((unsigned)div_ceil(N, 8)), block(64 * Q4G_WAVES);
-#define Q4G_LAUNCH(XF, YB, NG) hipLaunchKernelGGL((q4g_kernel<XF, YB, NG>), grid, block, lds, s, a)
-    const bool small = a.n_rg1 <= Q4G_WAVES;
-    if (small) {
-        if (xf32 && ybf16) Q4G_LAUNCH(true, true, 1);
-        else if (xf32) Q4G_LAUNCH(true, false, 1);
-        else if (ybf16) Q4G_LAUNCH(false, true, 1);
-        else Q4G_LAUNCH(false, false, 1);
-    } else {
-        if (xf32 && ybf16) Q4G_LAUNCH(true, true, 2);
-        else if (xf32) Q4G_LAUNCH(true, false, 2);
-        else if (ybf16) Q4G_LAUNCH(false, true, 2);
-        else Q4G_LAUNCH(false, false, 2);
-    }
-#undef Q4G_LAUNCH
+    // one row group a wave in stage 1 up to 16 groups (r_p <= 1024), two up to 32
+    const bool two = a.n_rg1 > Q4G_WAVES;
+    const void *k = q4g_kernels[(xf32 ? 8 : 0) | (ybf16 ? 4 : 0) | (two ? 2 : 0) | (a.vec_y ? 1 : 0)];
+    void *args[] = {&a};
+    QBK_HIP(hipLaunchKernel(k, grid, block, args, lds, s));
     QBK_HIP(hipGetLastError());
     return QBK_OK;
 }

@@ -24,6 +24,38 @@ __device__ __forceinline__ int e8m0_of(float amax) {
 
 __device__ __forceinline__ float pow2f(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
+// fp8 e4m3 of a / sc, b / sc, c / sc, d / sc (sc a power of two), bytes 0-3,
+// round to nearest even, saturating: the scaled conversion divides by sc
+// exactly, in the one instruction -- bit for bit cvt_pk_fp8_f32(a * 2^-e,
+// ...) for sc = 2^e, e in [-126, 126] (checked on gfx950 over 2^20 values).
+typedef short q4_s16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t q4_fp8x4(float a, float b, float c, float d, float sc) {
+    q4_s16x2_t w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q4_s16x2_t{0, 0}, a, b, sc, false);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, c, d, sc, true);
+    return __builtin_bit_cast(uint32_t, w);
+}
+
+// fp8 e4m3 of a / sc in byte 0 (byte 1 zero), as q4_fp8x4.
+__device__ __forceinline__ uint32_t q4_fp8x1(float a, float sc) {
+    const q4_s16x2_t w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(q4_s16x2_t{0, 0}, a, 0.0f, sc, false);
+    return (uint32_t)(uint16_t)w[0];
+}
+
+// fp8 byte 0 of w times sc (a power of two): exact.
+__device__ __forceinline__ float q4_f32x1(uint32_t w, float sc) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, sc, false)[0];
+}
+
+// The four fp8 bytes of w times sc (a power of two): exact.
+__device__ __forceinline__ void q4_f32x4(uint32_t w, float sc, float out[4]) {
+    const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, sc, false);
+    const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, sc, true);
+    out[0] = lo[0];
+    out[1] = lo[1];
+    out[2] = hi[0];
+    out[3] = hi[1];
+}
+
 // fp16 bits (the low half of h) -> f32, exact.
 __device__ __forceinline__ float h16_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
@@ -50,28 +82,24 @@ __device__ __forceinline__ void q4_run_operand(float z[16], uint32_t hw[4], uint
     for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(z[e]));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
     e_hi = amax > 0.0f ? e8m0_of(amax) : 0;
-    const float inv_hi = pow2f(-e_hi), sc_hi = pow2f(e_hi);
+    const float sc_hi = pow2f(e_hi);
     float rmax = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_hi, z[4 * q + 1] * inv_hi, 0, false);
-        w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_hi, z[4 * q + 3] * inv_hi, w, true);
-        hw[q] = (uint32_t)w;
-        z[4 * q] -= __builtin_amdgcn_cvt_f32_fp8(w, 0) * sc_hi;  // exact residuals
-        z[4 * q + 1] -= __builtin_amdgcn_cvt_f32_fp8(w, 1) * sc_hi;
-        z[4 * q + 2] -= __builtin_amdgcn_cvt_f32_fp8(w, 2) * sc_hi;
-        z[4 * q + 3] -= __builtin_amdgcn_cvt_f32_fp8(w, 3) * sc_hi;
+        hw[q] = q4_fp8x4(z[4 * q], z[4 * q + 1], z[4 * q + 2], z[4 * q + 3], sc_hi);
+        float b[4];
+        q4_f32x4(hw[q], sc_hi, b);
 #pragma unroll
-        for (int u = 0; u < 4; u++) rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
+        for (int u = 0; u < 4; u++) {
+            z[4 * q + u] -= b[u];  // exact residuals
+            rmax = fmaxf(rmax, fabsf(z[4 * q + u]));
+        }
     }
     rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
     e_lo = rmax > 0.0f ? e8m0_of(rmax) : 0;
-    const float inv_lo = pow2f(-e_lo);
+    const float sc_lo = pow2f(e_lo);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q] * inv_lo, z[4 * q + 1] * inv_lo, 0, false);
-        lw[q] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(z[4 * q + 2] * inv_lo, z[4 * q + 3] * inv_lo, w, true);
-    }
+    for (int q = 0; q < 4; q++) lw[q] = q4_fp8x4(z[4 * q], z[4 * q + 1], z[4 * q + 2], z[4 * q + 3], sc_lo);
 }
 
 // z = bf16(s2 * x) of 16 bf16 activations (two 16-byte words) and their s2.
