@@ -267,49 +267,64 @@ __device__ __forceinline__ void q4g_epilogue1(const f32x4_t acc[4], uint8_t *tbu
 
 // Stage 2's epilogue for row group g: y = bf16((hi + lo) / 1.5) * s1 + bias,
 // s1 and bias of the group's 64 rows read from the wave's LDS region sb
-// ([64] s1 then [64] bias); the even lane of a column pair stores the four
-// rows it holds of token col / 2 (splitting the rows between the pair, two
-// each, cuts the VALU work by a third but measured 2 us slower at config 2,
-// B = 2048: 64 lanes of 4-byte stores against 32 of 8).  VECY: y rows take
-// 4-element stores (dout a multiple of 4, y aligned), so a lane's four rows
-// are all in or all out; otherwise element by element.  The two are
-// separate kernels: one store per row tile keeps the count of memory
-// operations in flight the same on every path, which the waits on the sign
-// ring rely on.
+// ([64] s1 then [64] bias).  Lane (col, G) of row tile rt holds rows 16rt +
+// 4G + i, i < 4, of column col.  The two lanes of a column pair split the
+// work: both form the four pair sums by DPP adds, the even lane finishes
+// rows 0, 1 and the odd lane rows 2, 3 of token col / 2; the odd lane then
+// hands its two results back and the even lane stores all four (stores from
+// all 64 lanes of two rows each measured 2 us slower at config 2, B = 2048).
+__device__ __forceinline__ void q4g_y2(const f32x4_t acc[4], int rt, bool odd, const float *sb, int r2, float y[2]) {
+    const float2 s1v = *(const float2 *)(sb + r2);
+    const float2 biv = *(const float2 *)(sb + 64 + r2);
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) x[i] = acc[rt][i] + q4g_pair(acc[rt][i]);
+    const float v0 = q4_unscale(odd ? x[2] : x[0]), v1 = q4_unscale(odd ? x[3] : x[1]);
+    const uint32_t u = f32x2_to_bf16x2(v0, v1);
+    y[0] = __uint_as_float(u << 16) * s1v.x + biv.x;
+    y[1] = __uint_as_float(u & 0xffff0000u) * s1v.y + biv.y;
+}
+
+__device__ __forceinline__ uint32_t q4g_pair_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true);
+}
+
+// VECY: y rows take 4-element stores (dout a multiple of 4, y aligned), so
+// a lane pair's four rows are all in or all out; otherwise element by
+// element.  The two are separate kernels: one store per row tile keeps the
+// count of memory operations in flight the same on every path, which the
+// waits on the sign ring rely on.
 template <bool VECY>
 __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArgs &a, size_t g, const float *sb,
                                               size_t n0, int lane, bool ybf16) {
-    const int col = lane & 15, G = lane >> 4;
+    const int col = lane & 15, G = lane >> 4, odd = col & 1;
     const size_t n = n0 + (col >> 1);
 #pragma unroll
     for (int rt = 0; rt < 4; rt++) {
-        const size_t row0 = 64 * g + 16 * rt + 4 * G;
-        const float4 s1v = *(const float4 *)(sb + 16 * rt + 4 * G);
-        const float4 biv = *(const float4 *)(sb + 64 + 16 * rt + 4 * G);
-        const float s1a[4] = {s1v.x, s1v.y, s1v.z, s1v.w}, bia[4] = {biv.x, biv.y, biv.z, biv.w};
-        float v[4], y[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = q4_unscale(acc[rt][i] + q4g_pair(acc[rt][i]));
-        const uint32_t u01 = f32x2_to_bf16x2(v[0], v[1]), u23 = f32x2_to_bf16x2(v[2], v[3]);
-        y[0] = __uint_as_float(u01 << 16) * s1a[0] + bia[0];
-        y[1] = __uint_as_float(u01 & 0xffff0000u) * s1a[1] + bia[1];
-        y[2] = __uint_as_float(u23 << 16) * s1a[2] + bia[2];
-        y[3] = __uint_as_float(u23 & 0xffff0000u) * s1a[3] + bia[3];
-        if ((col & 1) || n >= a.N || row0 >= a.dout) continue;
+        const int r2 = 16 * rt + 4 * G + 2 * odd;  // this lane's first row within the group
+        float y[2];
+        q4g_y2(acc, rt, odd != 0, sb, r2, y);
+        // the odd lane's rows 2, 3, handed to the even lane (all lanes active)
+        const uint32_t w = f32x2_to_bf16x2(y[0], y[1]);
+        const uint32_t wp = q4g_pair_u(w);
+        const float y2 = __uint_as_float(q4g_pair_u(__float_as_uint(y[0])));
+        const float y3 = __uint_as_float(q4g_pair_u(__float_as_uint(y[1])));
+        const size_t row0 = 64 * g + r2;
+        if (odd || n >= a.N || row0 >= a.dout) continue;
         if constexpr (VECY) {
             if (ybf16)
-                *(uint2 *)((uint16_t *)a.y + n * a.dout + row0) =
-                    make_uint2(f32x2_to_bf16x2(y[0], y[1]), f32x2_to_bf16x2(y[2], y[3]));
+                *(uint2 *)((uint16_t *)a.y + n * a.dout + row0) = make_uint2(w, wp);
             else
-                *(float4 *)((float *)a.y + n * a.dout + row0) = make_float4(y[0], y[1], y[2], y[3]);
+                *(float4 *)((float *)a.y + n * a.dout + row0) = make_float4(y[0], y[1], y2, y3);
         } else {
+            const float yy[4] = {y[0], y[1], y2, y3};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 if (row0 + i >= a.dout) break;
                 if (ybf16)
-                    ((uint16_t *)a.y)[n * a.dout + row0 + i] = f32_to_bf16(y[i]);
+                    ((uint16_t *)a.y)[n * a.dout + row0 + i] = f32_to_bf16(yy[i]);
                 else
-                    ((float *)a.y)[n * a.dout + row0 + i] = y[i];
+                    ((float *)a.y)[n * a.dout + row0 + i] = yy[i];
             }
         }
     }
