@@ -84,12 +84,13 @@ def test_integer_exact_long_k_batch1(ctx, orc, dout, din, r):
 
 
 @pytest.mark.parametrize("dout,din,r,batch", [(300, 200, 37, 1031), (256, 512, 128, 1024), (1024, 4096, 1102, 1024),
-                                              (512, 640, 2000, 1030)])
+                                              (512, 640, 2000, 1030), (301, 200, 37, 1031), (1030, 384, 100, 1024)])
 def test_integer_exact_one_launch(ctx, orc, dout, din, r, batch):
     """The one-launch GEMM (batches from 1024 on): ragged last token groups,
     a din that is not a multiple of 128, ranks whose 64-row groups do not
     split evenly over the eight waves (1102: 18 groups), and the largest rank
-    it takes (2000: 32 groups, four a wave)."""
+    it takes (2000: 32 groups, four a wave).  A dout that is not a multiple
+    of 4 (301, 1030) runs the element-wise y stores, a kernel of its own."""
     integer_exact_case(ctx, orc, dout, din, r, batch)
 
 
