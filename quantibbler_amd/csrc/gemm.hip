@@ -559,11 +559,13 @@ bool q4g_fits(const qbk_factor *L, size_t N) {
 }
 
 // The smallest batch the one-launch GEMM takes over from the two-stage one:
-// its workgroups (8 tokens each) each stream all of a layer's signs, so it
-// wins once they fill half the chip (measured at config 2: B = 512, 38 against
-// 31 us; B = 2048, 45 against 56 us); below, the two-stage GEMM splits each
-// stage over row tiles and K.
-#define Q4G_MIN_N 1024
+// its workgroups (8 tokens each) each stream all of a layer's signs, so its
+// time barely depends on the batch; the two-stage GEMM's grows with it
+// (measured at config 2, one-launch against two-stage: B = 256, 28.9 against
+// 33.0 us; 512, 29.8 against 31.1; 768, 30.8 against 40.1; 2048, 35.5
+// against 56); below, the two-stage GEMM splits each stage over row tiles
+// and K.
+#define Q4G_MIN_N 256
 
 bool q4g_use(const qbk_factor *L, size_t N) { return N >= Q4G_MIN_N && q4g_fits(L, N); }
 

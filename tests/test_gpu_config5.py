@@ -108,7 +108,7 @@ def sage_gate(got, want, label):
 def test_config5_prefill_against_decode_steps(model):
     st = torch.cuda.current_stream()
     rng = np.random.default_rng(5001)
-    n = 1100  # the one-launch GEMM from 1024 tokens; a ragged last group of 8
+    n = 1100  # the one-launch GEMM (from 256 tokens); a ragged last group of 8
     tokens = rng.integers(0, VOCAB, n).tolist()
     say(f"config 5 shape: prefill of {n} tokens")
     model.reset()

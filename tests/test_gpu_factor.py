@@ -86,7 +86,7 @@ def test_integer_exact_long_k_batch1(ctx, orc, dout, din, r):
 @pytest.mark.parametrize("dout,din,r,batch", [(300, 200, 37, 1031), (256, 512, 128, 1024), (1024, 4096, 1102, 1024),
                                               (512, 640, 2000, 1030), (301, 200, 37, 1031), (1030, 384, 100, 1024)])
 def test_integer_exact_one_launch(ctx, orc, dout, din, r, batch):
-    """The one-launch GEMM (batches from 1024 on): ragged last token groups,
+    """The one-launch GEMM (batches from 256 on): ragged last token groups,
     a din that is not a multiple of 128, ranks whose 64-row groups do not
     split evenly over the eight waves (1102: 18 groups), and the largest rank
     it takes (2000: 32 groups, four a wave).  A dout that is not a multiple
@@ -94,10 +94,12 @@ def test_integer_exact_one_launch(ctx, orc, dout, din, r, batch):
     integer_exact_case(ctx, orc, dout, din, r, batch)
 
 
-def test_integer_exact_config2_batch512(ctx, orc):
-    """Config 2's shape at B = 512 (the K-split stage 1 on 128 x 64 tiles, stage
-    2 on its own 256 tiles)."""
-    integer_exact_case(ctx, orc, 4096, 4096, 1024, 512)
+@pytest.mark.parametrize("batch", [255, 512])
+def test_integer_exact_config2_mid_batches(ctx, orc, batch):
+    """Config 2's shape at B = 255 (the two-stage GEMM's largest batch: the
+    K-split stage 1 on 128 x 64 tiles, stage 2 on its own 256 tiles) and B =
+    512 (the one-launch GEMM on 64 workgroups)."""
+    integer_exact_case(ctx, orc, 4096, 4096, 1024, batch)
 
 
 def integer_exact_case(ctx, orc, dout, din, r, batch):
@@ -362,7 +364,7 @@ def test_prefill_activation_rounding_one_launch(ctx, orc, din):
     32 of them)."""
     say("factor one-launch GEMM activation rounding", din)
     rng = np.random.default_rng(200 + din)
-    batch = 1029  # the one-launch GEMM from 1024 tokens on; a ragged last group of 8
+    batch = 1029  # the one-launch GEMM (from 256 tokens on); a ragged last group of 8
     L = _rounding_layer(orc, rng, din)
     layer = upload(ctx, L)
     zmax = 2.0 ** 122
