@@ -43,6 +43,7 @@ struct qbk_block {
     const qbk_factor *o, *down;
     qbk_factor_set *qkv, *gu;
     float *w_in, *w_post;     // d each
+    float *ones_ffn;          // ffn ones: the down projection's s2 once the prefill's SwiGLU has applied it
     float *w_q, *w_k;         // head_dim each, or null (no per-head q/k norms)
     float2 *rope;             // [cap][hd / 2] (cos, sin) in f32, from f64
     float *kc, *vc;           // [nseq][cap][Hk * hd] the block's KV caches
@@ -346,12 +347,16 @@ static void blkp_norm_launch(size_t n, const float *a, const float *r, float *ho
 // Row t's q, k, v (token-major f32, as the projections wrote them): per-head
 // q/k norm (optional) and RoPE at position t, as blkd_qk_rope; k and v also
 // to cache row t.  The attention operands go out head-major in bf16:
-// qb [H][n][hd], kb / vb [Hk][n][hd].  Grid (H + Hk, n), a wave per head.
-__global__ void __launch_bounds__(64) blkp_qk_rope(const float *q, const float *k, const float *v, const float2 *rope,
-                                                   const float *wq, const float *wk, float eps, float *kc, float *vc,
-                                                   uint16_t *qb, uint16_t *kb, uint16_t *vb, int H, int Hk, int hd,
-                                                   int n) {
-    const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, half = hd / 2;
+// qb [H][n][hd], kb / vb [Hk][n][hd].  Grid (ceil((H + Hk) / 4), n), a wave
+// per head (one-wave workgroups, 40 a token at config 5, measured 30 us a
+// 2048-token block: dispatch-bound).
+__global__ void __launch_bounds__(256) blkp_qk_rope(const float *q, const float *k, const float *v, const float2 *rope,
+                                                    const float *wq, const float *wk, float eps, float *kc, float *vc,
+                                                    uint16_t *qb, uint16_t *kb, uint16_t *vb, int H, int Hk, int hd,
+                                                    int n) {
+    const int head = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), t = blockIdx.y, lane = threadIdx.x & 63,
+              half = hd / 2;
+    if (head >= H + Hk) return;  // a wave of the last workgroup past the heads (no barrier follows)
     const bool is_q = head < H;
     const int hh = is_q ? head : head - H;
     const float *src = is_q ? q + ((size_t)t * H + hh) * hd : k + ((size_t)t * Hk + hh) * hd;
@@ -396,16 +401,6 @@ __global__ void __launch_bounds__(64) blkp_qk_rope(const float *q, const float *
     }
 }
 
-// Attention output, head-major bf16 [H][n][hd] -> token-major [n][H hd], the
-// o projection's rows.
-__global__ void blkp_heads_to_rows(const uint16_t *ao, uint16_t *rows, int H, int hd, int n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t total = (size_t)H * n * hd;
-    if (i >= total) return;
-    const size_t c = i % hd, t = (i / hd) % n, h = i / ((size_t)hd * n);
-    rows[(t * H + h) * hd + c] = ao[i];
-}
-
 // hidden = g u / (1 + exp(-g)), elementwise over n rows of ffn
 __global__ void blkp_swiglu(const float *g, const float *u, float *hid, size_t count) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -413,6 +408,27 @@ __global__ void blkp_swiglu(const float *g, const float *u, float *hid, size_t c
         const float gv = g[i], uv = u[i];
         hid[i] = gv * uv / (1.0f + expf(0.0f - gv));
     }
+}
+
+// blkp_swiglu followed by the down projection's z = bf16(s2 hid) (the
+// GEMM's f32-x conversion, the same f32 product and rounding), written as
+// bf16: the GEMM then reads it at s2 = 1, where bf16(1 * z) = z.  Half the
+// bytes of the f32 hidden row on both sides.  Four elements a thread (ffn a
+// multiple of 4).
+__global__ void blkp_swiglu_z(const float *g, const float *u, const float *s2, uint16_t *z, size_t count,
+                              uint32_t ffn) {
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= count) return;
+    const float4 gv = *(const float4 *)(g + i), uv = *(const float4 *)(u + i);
+    const float4 sv = *(const float4 *)(s2 + i % ffn);
+    const float ga[4] = {gv.x, gv.y, gv.z, gv.w}, ua[4] = {uv.x, uv.y, uv.z, uv.w}, sa[4] = {sv.x, sv.y, sv.z, sv.w};
+    uint16_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float hid = ga[e] * ua[e] / (1.0f + expf(0.0f - ga[e]));
+        o[e] = f32_to_bf16(sa[e] * hid);
+    }
+    *(uint2 *)(z + i) = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
 }
 
 __global__ void blkp_add(const float *a, const float *b, float *out, size_t count) {
@@ -431,7 +447,7 @@ static int blkp_proj(const qbk_factor *L, size_t n, const void *x, bool xf32, fl
 
 // Prefill workspace regions (256-byte aligned), for n rows.
 struct BlkpPlan {
-    size_t o_x, o_q, o_k, o_v, o_qb, o_kb, o_vb, o_sage, o_ao, o_arow, o_oo, o_h1, o_g, o_u, o_gemm, bytes;
+    size_t o_x, o_q, o_k, o_v, o_qb, o_kb, o_vb, o_sage, o_arow, o_oo, o_h1, o_g, o_u, o_z, o_gemm, bytes;
     size_t sage_bytes, gemm_bytes;
 };
 
@@ -454,12 +470,12 @@ static BlkpPlan blkp_plan(const qbk_block *B, const qbk_factor *const L[7], size
     const qbk_attn_shape sh{1, B->H, B->Hk, n, n, B->hd, B->hd};
     p.sage_bytes = qbk_sage_blk_workspace_size(&sh);
     p.o_sage = take(p.sage_bytes);
-    p.o_ao = take(n * qd * 2);
     p.o_arow = take(n * qd * 2);
     p.o_oo = take(n * d * 4);
     p.o_h1 = take(n * d * 4);
     p.o_g = take(n * B->ffn * 4);
     p.o_u = take(n * B->ffn * 4);
+    p.o_z = take(n * B->ffn * 2);
     size_t g = 0;
     for (int i = 0; i < 7; i++) {
         const size_t w = blkp_proj_ws(L[i], n);
@@ -635,7 +651,8 @@ int qbk_block_create_seqs(qbk_ctx *ctx, const qbk_factor *const *layers, const f
         (rc = alloc((void **)&B->ycat, ((H + 2 * Hk) * hd > 2 * ffn ? (H + 2 * Hk) * hd : 2 * ffn) * 4)) ||
         (rc = alloc((void **)&B->qrot, H * hd * 4)) || (rc = alloc((void **)&B->attn, H * hd * 4)) ||
         (rc = alloc((void **)&B->oout, d * 4)) || (rc = alloc((void **)&B->h1, d * 4)) ||
-        (rc = alloc((void **)&B->hid, ffn * 4)) || (rc = alloc((void **)&B->dout, d * 4))) {
+        (rc = alloc((void **)&B->hid, ffn * 4)) || (rc = alloc((void **)&B->dout, d * 4)) ||
+        (rc = alloc((void **)&B->ones_ffn, ffn * 4))) {
         qbk_block_destroy(B);
         return rc;
     }
@@ -659,6 +676,10 @@ int qbk_block_create_seqs(qbk_ctx *ctx, const qbk_factor *const *layers, const f
     hipError_t e = hipMemcpy(B->rope, tab.data(), tab.size() * 8, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(B->w_in, input_norm, d * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(B->w_post, post_norm, d * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        const std::vector<float> ones(ffn, 1.0f);
+        e = hipMemcpy(B->ones_ffn, ones.data(), ffn * 4, hipMemcpyHostToDevice);
+    }
     if (e == hipSuccess && q_norm) e = hipMemcpy(B->w_q, q_norm, hd * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess && k_norm) e = hipMemcpy(B->w_k, k_norm, hd * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -1000,7 +1021,7 @@ int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *B, size_t seq, float *h, 
     hipStream_t s = (hipStream_t)stream;
     char *w = (char *)workspace;
     uint16_t *x = (uint16_t *)(w + P.o_x), *qb = (uint16_t *)(w + P.o_qb), *kb = (uint16_t *)(w + P.o_kb),
-             *vb = (uint16_t *)(w + P.o_vb), *ao = (uint16_t *)(w + P.o_ao), *arow = (uint16_t *)(w + P.o_arow);
+             *vb = (uint16_t *)(w + P.o_vb), *arow = (uint16_t *)(w + P.o_arow);
     float *q = (float *)(w + P.o_q), *k = (float *)(w + P.o_k), *v = (float *)(w + P.o_v),
           *oo = (float *)(w + P.o_oo), *h1 = (float *)(w + P.o_h1), *g = (float *)(w + P.o_g),
           *u = (float *)(w + P.o_u);
@@ -1014,29 +1035,34 @@ int qbk_block_prefill_seq_dev(qbk_ctx *ctx, qbk_block *B, size_t seq, float *h, 
         (rc = blkp_proj(B->lay[2], n, x, false, v, ws, s)))
         return rc;
     const size_t kvs = B->cap * B->Hk * B->hd;  // one sequence's cache floats
-    hipLaunchKernelGGL(blkp_qk_rope, dim3(H + Hk, (unsigned)n), dim3(64), 0, s, q, k, v, B->rope, B->w_q, B->w_k,
+    hipLaunchKernelGGL(blkp_qk_rope, dim3((H + Hk + 3) / 4, (unsigned)n), dim3(256), 0, s, q, k, v, B->rope, B->w_q, B->w_k,
                        B->eps, B->kc + seq * kvs, B->vc + seq * kvs, qb, kb, vb, H, Hk, hd, (int)n);
     QBK_HIP(hipGetLastError());
     // causal block-scaled SageAttention over the n tokens
     const qbk_attn_shape sh{1, B->H, B->Hk, n, n, B->hd, B->hd};
-    if ((rc = qbk_attention_sage_blk_dev(ctx, &sh, qb, kb, vb, 1, ao, w + P.o_sage, P.sage_bytes, stream))) return rc;
-    {
-        const size_t tot = n * B->H * B->hd;
-        hipLaunchKernelGGL(blkp_heads_to_rows, dim3((unsigned)div_ceil(tot, 256)), dim3(256), 0, s, ao, arow, H, hd,
-                           (int)n);
-        QBK_HIP(hipGetLastError());
-    }
+    // written token-major: the o projection's rows
+    if ((rc = sage_blk_run(ctx, &sh, qb, kb, vb, 1, arow, true, w + P.o_sage, P.sage_bytes, stream))) return rc;
     // o + residual, norm, gate / up, SwiGLU, down + residual
     if ((rc = blkp_proj(B->o, n, arow, false, oo, ws, s))) return rc;
     blkp_norm_launch(n, oo, h, h1, B->w_post, B->eps, x, d, 1, s);
     QBK_HIP(hipGetLastError());
     if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) || (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s)))
         return rc;
-    hipLaunchKernelGGL(blkp_swiglu, dim3((unsigned)div_ceil(nf, 256)), dim3(256), 0, s, g, u, g, nf);
-    QBK_HIP(hipGetLastError());
-    if ((rc = blkp_proj(B->down, n, g, true, oo, ws, s))) return rc;
-    hipLaunchKernelGGL(blkp_add, dim3((unsigned)div_ceil(nd, 256)), dim3(256), 0, s, oo, h1, h, nd);
-    QBK_HIP(hipGetLastError());
+    if (n > Q4_MAXB && q4g_use(B->down, n) && B->ffn % 4 == 0) {
+        // SwiGLU writes the down projection's z in bf16 (read at s2 = 1), and
+        // h = down + h1, the residual added in the GEMM's epilogue
+        uint16_t *z = (uint16_t *)(w + P.o_z);
+        hipLaunchKernelGGL(blkp_swiglu_z, dim3((unsigned)div_ceil(nf / 4, 256)), dim3(256), 0, s, g, u,
+                           B->down->s2, z, nf, (uint32_t)B->ffn);
+        QBK_HIP(hipGetLastError());
+        if ((rc = q4g_run(B->down, z, false, n, h, false, (uint16_t *)ws, s, h1, B->ones_ffn))) return rc;
+    } else {
+        hipLaunchKernelGGL(blkp_swiglu, dim3((unsigned)div_ceil(nf, 256)), dim3(256), 0, s, g, u, g, nf);
+        QBK_HIP(hipGetLastError());
+        if ((rc = blkp_proj(B->down, n, g, true, oo, ws, s))) return rc;
+        hipLaunchKernelGGL(blkp_add, dim3((unsigned)div_ceil(nd, 256)), dim3(256), 0, s, oo, h1, h, nd);
+        QBK_HIP(hipGetLastError());
+    }
     B->filled[seq] = n;
     B->tokens[seq] = 0;  // the decode attention state rebuilds its codes from the cache
     return QBK_OK;

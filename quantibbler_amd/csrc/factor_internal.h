@@ -123,10 +123,13 @@ int g32_set_run(const qbk_factor *const *L, size_t n, const G32SetLayer *tab1, c
 // launch over the decode's sign layout, no workspace: x [N][din] (bf16, or
 // f32 when xf32) -> y [N][dout] (bf16 when ybf16, else f32), for layers of
 // rank up to 2048.
-// t_out (null, or [N][r_p] bf16): t as well, zero past r.
+// t_out (null, or [N][r_p] bf16): t as well, zero past r.  resid (null, or
+// f32 [N][dout], with f32 y only): y = resid added to the layer's output.
+// s2 (null, or [din]): in place of the layer's s2 (ones for an x that
+// already holds z = bf16(s2 x)).
 bool q4g_fits(const qbk_factor *L, size_t N);
 int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, uint16_t *t_out,
-            hipStream_t s);
+            hipStream_t s, const float *resid = nullptr, const float *s2 = nullptr);
 // The factor linear past the decode GEMV's batches: the fused GEMM where it
 // applies (its workspace: t bf16 [N][r_p], left there), else the two-stage
 // GEMM below; gemm_workspace gives the bytes ws must hold.

@@ -67,6 +67,7 @@ struct Q4GArgs {
     uint32_t c7;                    // 0x77777777
     uint16_t *t_out;                // t bf16 [N][r_p] as well (zero past r), or null
     uint32_t r_p;
+    const float *resid;             // f32 [N][dout] added to an f32 y (the block's residual), or null
 };
 
 __device__ __forceinline__ i32x8_t q4g_signs(uint32_t w, uint32_t c7) {
@@ -312,10 +313,16 @@ __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArg
         const size_t row0 = 64 * g + r2;
         if (odd || n >= a.N || row0 >= a.dout) continue;
         if constexpr (VECY) {
-            if (ybf16)
+            if (ybf16) {
                 *(uint2 *)((uint16_t *)a.y + n * a.dout + row0) = make_uint2(w, wp);
-            else
-                *(float4 *)((float *)a.y + n * a.dout + row0) = make_float4(y[0], y[1], y2, y3);
+            } else {
+                float4 o = make_float4(y[0], y[1], y2, y3);
+                if (a.resid) {
+                    const float4 rv = *(const float4 *)(a.resid + n * a.dout + row0);
+                    o = make_float4(o.x + rv.x, o.y + rv.y, o.z + rv.z, o.w + rv.w);
+                }
+                *(float4 *)((float *)a.y + n * a.dout + row0) = o;
+            }
         } else {
             const float yy[4] = {y[0], y[1], y2, y3};
 #pragma unroll
@@ -324,7 +331,8 @@ __device__ __forceinline__ void q4g_epilogue2(const f32x4_t acc[4], const Q4GArg
                 if (ybf16)
                     ((uint16_t *)a.y)[n * a.dout + row0 + i] = f32_to_bf16(yy[i]);
                 else
-                    ((float *)a.y)[n * a.dout + row0 + i] = yy[i];
+                    ((float *)a.y)[n * a.dout + row0 + i] =
+                        a.resid ? yy[i] + a.resid[n * a.dout + row0 + i] : yy[i];
             }
         }
     }
@@ -580,7 +588,8 @@ int gemm_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, b
 }
 
 int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bool ybf16, uint16_t *t_out,
-            hipStream_t s) {
+            hipStream_t s, const float *resid, const float *s2) {
+    if (resid && ybf16) return fail(QBK_ERR_VALIDATION, "the GEMM adds a residual to an f32 output only");
     const uint32_t lds = q4g_lds_bytes(L);
     {
         // up to 67.5 KiB of LDS, past the 64 KiB default: the attribute is
@@ -600,7 +609,7 @@ int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     Q4GArgs a{};
     a.bits1 = L->vt_q4;
     a.bits2 = L->u_q4;
-    a.s2 = L->s2;
+    a.s2 = s2 ? s2 : L->s2;
     a.s1 = L->s1;
     a.bias = L->bias;
     a.x = x;
@@ -618,6 +627,7 @@ int q4g_run(const qbk_factor *L, const void *x, bool xf32, size_t N, void *y, bo
     a.c7 = 0x77777777u;
     a.t_out = t_out;
     a.r_p = (uint32_t)L->r_p;
+    a.resid = resid;
     const dim3 grid((unsigned)div_ceil(N, 8)), block(64 * Q4G_WAVES);
     // one row group a wave in stage 1 up to 16 groups (r_p <= 1024), two up to 32
     const bool two = a.n_rg1 > Q4G_WAVES;

@@ -112,6 +112,12 @@ int sage_decode_batch(const qbk_attn_shape *one, const float *q, size_t q_stride
 // Exact f32 attention of one query position (q [H][hd]) over rows
 // 0 .. rows - 1 of a decoder block's row-major cache ([rows][Hk hd] keys and
 // values) -> out [H][hd] (attention.hip; the engine's tiled decode face).
+// qbk_attention_sage_blk_dev with the output either head-major [B][H][S][hd]
+// (out_rows false, the C ABI's layout) or token-major [B][S][H][hd] (the
+// rows of the o projection that reads it).
+int sage_blk_run(qbk_ctx *ctx, const qbk_attn_shape *shape, const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                 int causal, uint16_t *out, bool out_rows, void *workspace, size_t workspace_size, void *stream);
+
 int attention_exact_cache(const float *q, const float *kc, const float *vc, size_t H, size_t Hk, size_t hd,
                           size_t rows, float *out, hipStream_t st);
 

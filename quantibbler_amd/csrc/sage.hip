@@ -2068,6 +2068,7 @@ struct BlkArgs {
     int8_t *qhat_out; // quantize-only launch: Q codes [B*H][S][HD] and scales [B*H][nblk]
     float *qscale_out;
     int hpx;          // heads per XCD of the XCD-aware tile order (0: plain order)
+    int out_rows;     // 1: out token-major [B][S][H][HD] (the o projection's rows), 0: [B][H][S][HD]
 };
 
 // Key order of a V^T block: within each 32-key chunk, position 8g + e holds
@@ -2524,7 +2525,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) b
         const float inv = 1.0f / lt[qt][0];
         const size_t q = qw + 16 * qt + col;
         if (q >= a.S) continue;
-        uint16_t *dst = a.out + (bh * a.S + q) * HD;
+        uint16_t *dst = a.out + (a.out_rows ? ((b * a.S + q) * a.H + h) * HD : (bh * a.S + q) * HD);
 #pragma unroll
         for (int ct = 0; ct < 8; ct++) {
             const uint32_t w0 = f32x2_to_bf16x2(o[qt][ct][0] * inv, o[qt][ct][1] * inv);
@@ -2762,6 +2763,13 @@ size_t qbk_sage_blk_workspace_size(const qbk_attn_shape *shape) {
 int qbk_attention_sage_blk_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const uint16_t *q,
                                const uint16_t *k, const uint16_t *v, int causal, uint16_t *out,
                                void *workspace, size_t workspace_size, void *stream) {
+    return sage_blk_run(ctx, shape, q, k, v, causal, out, false, workspace, workspace_size, stream);
+}
+}  // extern "C"
+
+namespace qbk {
+int sage_blk_run(qbk_ctx *ctx, const qbk_attn_shape *shape, const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                 int causal, uint16_t *out, bool out_rows, void *workspace, size_t workspace_size, void *stream) {
     int rc;
     if ((rc = validate_blk(shape))) return rc;
     if ((rc = bind(ctx))) return rc;
@@ -2774,9 +2782,13 @@ int qbk_attention_sage_blk_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const 
     blk_bind(P, q, k, v, workspace);
     if ((rc = run_blk_prepass(P, st))) return rc;
     P.a.out = out;
+    P.a.out_rows = out_rows ? 1 : 0;
     P.a.causal = causal ? 1 : 0;
     return run_blk_attn(P, st);
 }
+}  // namespace qbk
+
+extern "C" {
 
 int qbk_sage_blk_quantize_dev(qbk_ctx *ctx, const qbk_attn_shape *shape, const uint16_t *q,
                               const uint16_t *k, const uint16_t *v, int8_t *qhat, float *qscale,
