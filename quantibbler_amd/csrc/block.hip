@@ -301,35 +301,88 @@ __global__ void __launch_bounds__(256) blkd_swiglu_op(const float *gu, int ffn, 
 // Per row of d: hsum = a (+ r), optionally stored to hout; x = bf16 of the
 // RMS-normalised bf16(hsum) times w (the decode's blkd_norm, a row per
 // workgroup), written nrep times: copy k of the n rows at x + k n d (the
-// input of a layer set whose layers share x).
-template <int NT>
-__global__ void __launch_bounds__(NT) blkp_norm(const float *a, const float *r, float *hout, const float *w,
-                                                float eps, uint16_t *x, int d, int nrep) {
+// input of a layer set whose layers share x).  Rows up to NT NE elements
+// are read once, all their loads issued before any store.
+template <int NT, int NE = 8192 / NT>
+__global__ void __launch_bounds__(NT) blkp_norm(const float *__restrict__ a, const float *__restrict__ r,
+                                                float *__restrict__ hout, const float *__restrict__ w, float eps,
+                                                uint16_t *__restrict__ x, int d, int nrep) {
     __shared__ float red[NT / 64];
     const size_t off = (size_t)blockIdx.x * d;
     const int tid = threadIdx.x;
+    if (d > NT * NE) {  // a longer row: two passes over it
+        float ss = 0.0f;
+        for (int i = tid; i < d; i += NT) {
+            float v = a[off + i];
+            if (r) v = v + r[off + i];
+            if (hout) hout[off + i] = v;
+            const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
+            ss += b * b;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NT / 64; i++) tot += red[i];
+        const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+        for (int i = tid; i < d; i += NT) {
+            float v = a[off + i];
+            if (r) v = v + r[off + i];
+            const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
+            const uint16_t o = blkd_bf16(b * inv * w[i]);
+            for (int c = 0; c < nrep; c++) x[c * (size_t)gridDim.x * d + off + i] = o;
+        }
+        return;
+    }
+    // the row once: every load first, then the sums, then the stores
+    float va[NE], wa[NE];
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+        const int i = tid + k * NT;
+        va[k] = i < d ? a[off + i] : 0.0f;
+        wa[k] = i < d ? w[i] : 0.0f;
+    }
+    if (r) {
+#pragma unroll
+        for (int k = 0; k < NE; k++) {
+            const int i = tid + k * NT;
+            if (i < d) va[k] = va[k] + r[off + i];
+        }
+    }
     float ss = 0.0f;
-    for (int i = tid; i < d; i += NT) {
-        float v = a[off + i];
-        if (r) v = v + r[off + i];
-        if (hout) hout[off + i] = v;
-        const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
-        ss += b * b;
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+        const int i = tid + k * NT;
+        if (i < d) {
+            const float b = __uint_as_float((uint32_t)blkd_bf16(va[k]) << 16);
+            ss += b * b;
+        }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
+    if (hout) {
+#pragma unroll
+        for (int k = 0; k < NE; k++) {
+            const int i = tid + k * NT;
+            if (i < d) hout[off + i] = va[k];
+        }
+    }
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
     for (int i = 0; i < NT / 64; i++) tot += red[i];
     const float inv = 1.0f / sqrtf(tot / (float)d + eps);
-    for (int i = tid; i < d; i += NT) {
-        float v = a[off + i];
-        if (r) v = v + r[off + i];
-        const float b = __uint_as_float((uint32_t)blkd_bf16(v) << 16);
-        const uint16_t o = blkd_bf16(b * inv * w[i]);
-        for (int k = 0; k < nrep; k++) x[k * (size_t)gridDim.x * d + off + i] = o;  // copy k: [n][d] at k n d
+#pragma unroll
+    for (int k = 0; k < NE; k++) {
+        const int i = tid + k * NT;
+        if (i < d) {
+            const float b = __uint_as_float((uint32_t)blkd_bf16(va[k]) << 16);
+            const uint16_t o = blkd_bf16(b * inv * wa[k]);
+            for (int c = 0; c < nrep; c++) x[c * (size_t)gridDim.x * d + off + i] = o;  // copy c: [n][d] at c n d
+        }
     }
 }
 
