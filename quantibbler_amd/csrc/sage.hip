@@ -651,6 +651,15 @@ static int run_ref(const qbk_attn_shape *s, const float *q, const float *k, cons
 
 #define DEC_CH 4096  // keys of a block whose p and codes sit in LDS at once
 
+// A workgroup barrier that orders LDS only: __syncthreads() also fences
+// global memory, which waits for every load in flight -- the key or value
+// codes a kernel issues ahead of the work that does not need them.
+__device__ __forceinline__ void dec_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 struct DecArgs {
     RefArgs r;                           // shape (S = seq_kv), pre-pass products
     float *sc;                           // [H][S] scores, then p
@@ -1513,8 +1522,9 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g(DecArgs da, DecSeqTab t
     }
 }
 
-// GM, KM: the largest group and key block a kernel serves.
-template <int GM, int KM>
+// GM, KM: the largest group and key block a kernel serves; HALVES: the
+// instance for groups of exactly four heads at dv 128 (below).
+template <int GM, int KM, bool HALVES = false>
 __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     if (t.n) dec_seq(da, t, blockIdx.z);
     const RefArgs &a = da.r;
@@ -1522,8 +1532,8 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     __shared__ __attribute__((aligned(16))) float pf[GM * KM];
     __shared__ __attribute__((aligned(16))) uint8_t ph[GM * KM];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kb = blockIdx.x, bk = blockIdx.y, G = (uint32_t)(a.H / a.Hk), nkb = (uint32_t)a.nkb;
-    const uint32_t dv = (uint32_t)a.dv;
+    const uint32_t kb = blockIdx.x, bk = blockIdx.y, nkb = (uint32_t)a.nkb;
+    const uint32_t G = HALVES ? 4u : (uint32_t)(a.H / a.Hk), dv = HALVES ? 128u : (uint32_t)a.dv;
     const uint32_t j0 = kb * (uint32_t)a.block;
     const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
     const uint32_t tw = (kj + 3) / 4, vn4 = (tw + 3) / 4;
@@ -1532,34 +1542,55 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
     // four at dv 128 and blocks of at most 64 keys: the two threads of a
     // channel take half of its code words each, for all four heads, so the
     // codes are fetched once per workgroup (their integer sums added after).
-    const bool halves = GM == 4 && KM == 64 && G == 4 && dv == 128;
+    constexpr bool halves = HALVES;  // the launch checks G == 4 and dv == 128
+    static_assert(!HALVES || (GM == 4 && KM == 64), "the halves instance serves groups of four, 64-key blocks");
     const uint32_t hstep = 256 / dv, c = tid % dv, hs = tid / dv;
     const size_t vb = ((size_t)bk * a.pnkb + kb) * dv + c;
     const u32x4_t *vrow = (const u32x4_t *)(a.vhat + vb * a.blk4);
+    // The L2-resident operands first -- the scores of this wave's first
+    // head at this lane's first key and (two halves: the wave's one head) the
+    // earlier blocks' maxima -- then the V codes from HBM, unconditional
+    // (indices clamped), so that the probabilities and their key-order sum
+    // below are formed while the codes are in flight (the barriers order LDS
+    // only).
+    float sc0, mp0 = MASKED, bx0 = MASKED;
+    if (halves) {  // four waves, a head each: every load unconditional, selected after
+        const size_t h = (size_t)bk * G + wave;
+        const float *bm = da.bmax + h * nkb;
+        const float scr = da.sc[h * a.S + j0 + (lane < kj ? lane : 0)];
+        // a global load (a pointer chosen between two reads as a flat load,
+        // which counts against both wait counters)
+        const float *mpa = da.mprev ? da.mprev + h * nkb + kb : bm + (lane < kb ? lane : kb);
+        const float mpr = *(const __attribute__((address_space(1))) float *)mpa;
+        bx0 = bm[kb];
+        sc0 = lane < kj ? scr : 0.0f;
+        mp0 = da.mprev || lane < kb ? mpr : MASKED;
+    } else {
+        sc0 = wave < G && lane < kj ? da.sc[((size_t)bk * G + wave) * a.S + j0 + lane] : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the value loads stay behind these
     u32x4_t vv[KM / 16];
     if (halves) {
 #pragma unroll
-        for (uint32_t u = 0; u < 2; u++)
-            if (2 * hs + u < vn4) vv[u] = vrow[2 * hs + u];
+        for (uint32_t u = 0; u < 2; u++) vv[u] = vrow[2 * hs + u < vn4 ? 2 * hs + u : vn4 - 1];
     } else {
 #pragma unroll
         for (uint32_t u = 0; u < KM / 16; u++)
             if (u < vn4) vv[u] = vrow[u];
     }
     const float vdc = a.vd[vb];
-    // and the scores of this wave's first head at this lane's first key
-    const float sc0 = wave < G && lane < kj ? da.sc[((size_t)bk * G + wave) * a.S + j0 + lane] : 0.0f;
     // a wave per head: the running max before and after this block (a max
     // of MASKED and the earlier blocks' maxima: the reference's scan and a
     // reduction give one value), its live flag and alpha, p and its codes
     for (uint32_t hg = wave; hg < G; hg += 4) {
         const size_t h = (size_t)bk * G + hg;
         const float *bm = da.bmax + h * nkb;
-        float pm = MASKED;
-        if (da.mprev) {
+        float pm = halves ? mp0 : MASKED;
+        if (halves && da.mprev) {
+        } else if (da.mprev) {
             pm = da.mprev[h * nkb + kb];
         } else {
-            for (uint32_t i = lane; i < kb; i += 64) {
+            for (uint32_t i = halves ? lane + 64 : lane; i < kb; i += 64) {  // halves: blocks past the first 64
                 const float x = bm[i];
                 pm = x > pm ? x : pm;
             }
@@ -1569,7 +1600,7 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
                 pm = w > pm ? w : pm;
             }
         }
-        const float bx = bm[kb];
+        const float bx = halves ? bx0 : bm[kb];
         const float m_new = bx > pm ? bx : pm;
         const int live = !(m_new < MASKED * 0.5f);
         for (uint32_t j = lane; j < 4 * tw; j += 64) {
@@ -1591,7 +1622,7 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
             da.balpha[h * nkb + kb] = live ? qbk_expf(pm - m_new) : 0.0f;
         }
     }
-    __syncthreads();
+    dec_lds_barrier();
     // esum: p summed in key order (:315), by lane 0 of the head's wave
     for (uint32_t hg = wave; hg < G; hg += 4)
         if (lane == 0) {
@@ -1625,7 +1656,7 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
                             pv = __builtin_amdgcn_sdot4((int)pw[4 * (2 * hs + u) + e], (int)vv[u][e], pv, false);
             red[hs][hg][c] = pv;
         }
-        __syncthreads();
+        dec_lds_barrier();
 #pragma unroll
         for (uint32_t hg = hs; hg < 4; hg += 2) {
             const int pv = red[0][hg][c] + red[1][hg][c];
@@ -1648,8 +1679,8 @@ __global__ void __launch_bounds__(256) sage_dec_pv_g(DecArgs da, DecSeqTab t) {
 }
 
 
-// sage_dec_scores_g for groups of exactly four heads, head_dim <= 128 and
-// key blocks of at most 64: two key blocks a workgroup (two waves each), a
+// sage_dec_scores_g for groups of exactly four heads, head_dim 128 and key
+// blocks of at most 64: two key blocks a workgroup (two waves each), a
 // lane per key for two heads of the group -- so that a block's key codes are
 // fetched once per workgroup (the two lanes of a key read the same words),
 // and a batched step's grid holds half the workgroups, each no longer; the
@@ -1667,32 +1698,41 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t bk = blockIdx.y, bi = wave >> 1, kb = kbA + bi;
     const bool bval = kb < (uint32_t)a.nkb;  // the workgroup's second block may be past the end
-    const uint32_t d = (uint32_t)a.d, d4 = d / 4, n4 = d4 / 4;
+    constexpr uint32_t d = 128, d4 = d / 4, n4 = d4 / 4;  // the launch checks head_dim == 128
     const uint32_t kbc = bval ? kb : kbA;
     const uint32_t j0 = kbc * (uint32_t)a.block;
     const uint32_t kj = (uint32_t)(a.block < a.S - j0 ? a.block : a.S - j0);
     const uint32_t hp = lane >> 5, kk = 32 * (wave & 1) + (lane & 31);  // heads hp, hp + 2; key kk
-    for (uint32_t i = tid; i < 4 * d4; i += 256) qs[i] = da.qsw[(size_t)bk * 4 * d4 + i];
-    if (tid < 4) qd[tid] = da.qdl[bk * 4 + tid];
-    if (tid < 2 * d) {
-        const uint32_t b2 = tid / d, c = tid % d, kb2 = kbA + b2 < (uint32_t)a.nkb ? kbA + b2 : kbA;
-        kms[b2][c] = a.kmean[((size_t)bk * a.pnkb + kb2) * d + c];
-    }
+    // The L2-resident operands first (the group's query codes and deltas,
+    // the blocks' means), then this lane's key codes and delta from HBM,
+    // every load unconditional (indices clamped) so that the wait before
+    // the LDS writes counts only the first ones: the shifts below are formed
+    // while the key codes are in flight, and the barriers order LDS only.
+    const uint32_t qv = da.qsw[(size_t)bk * 4 * d4 + (tid < 4 * d4 ? tid : 0)];
+    const float qdv = da.qdl[bk * 4 + (tid & 3)];
+    const uint32_t b2m = tid / d < 2 ? tid / d : 1, cm = tid % d;
+    const uint32_t kb2 = kbA + b2m < (uint32_t)a.nkb ? kbA + b2m : kbA;
+    const float kmv = a.kmean[((size_t)bk * a.pnkb + kb2) * d + cm];
+    __builtin_amdgcn_sched_barrier(0);  // the key loads stay behind these
     const uint32_t jl = kk < kj ? kk : kj - 1;
     const u32x4_t *krow = (const u32x4_t *)(a.khat + ((size_t)bk * a.pst + j0 + jl) * d4);
     u32x4_t kv[8];
 #pragma unroll
-    for (uint32_t u = 0; u < 8; u++)
-        if (u < n4) kv[u] = krow[u];
+    for (uint32_t u = 0; u < 8; u++) kv[u] = krow[u];
     const float kdl = a.kdelta[(size_t)bk * a.pst + j0 + jl];
-    __syncthreads();
+    if (tid < 4 * d4) qs[tid] = qv;
+    if (tid < 4) qd[tid] = qdv;
+    if (tid < 2 * d) kms[b2m][cm] = kmv;
+    dec_lds_barrier();
     // the shift's terms (q^_c * dq) * kmean_c, every (block, head, channel)
-    for (uint32_t i = tid; i < 8 * d; i += 256) {
+#pragma unroll
+    for (uint32_t k = 0; k < 8 * d / 256; k++) {
+        const uint32_t i = tid + 256 * k;
         const uint32_t b2 = i / (4 * d), r = i % (4 * d), h4 = r / d, c = r % d;
         const int qc = (int)(int8_t)(qs[h4 * d4 + c / 4] >> (8 * (c % 4)));
         term[b2][r] = ((float)qc * qd[h4]) * kms[b2][c];
     }
-    __syncthreads();
+    dec_lds_barrier();
     // each (block, head)'s shift: its terms summed in channel order (:253)
     if (tid < 8) {
         const float *tt = term[tid >> 2] + (tid & 3) * d;
@@ -1707,7 +1747,7 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab 
         }
         shs[tid >> 2][tid & 3] = shift;
     }
-    __syncthreads();
+    dec_lds_barrier();
     const bool ok = bval && kk < kj;
 #pragma unroll
     for (uint32_t e2 = 0; e2 < 2; e2++) {
@@ -1731,7 +1771,7 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab 
         }
         if ((lane & 31) == 0) wmax[wave][hg] = rm;
     }
-    __syncthreads();
+    dec_lds_barrier();
     if (tid < 8) {
         const uint32_t b2 = tid >> 2, hg = tid & 3;
         const float m0 = wmax[2 * b2][hg], m1 = wmax[2 * b2 + 1][hg];
@@ -1743,7 +1783,7 @@ __global__ void __launch_bounds__(256) sage_dec_scores_g4(DecArgs da, DecSeqTab 
 // 128, 64-key blocks) and the general bounds.
 static void dec_launch_scores(dim3 g, const DecArgs &da, const DecSeqTab &t, hipStream_t st) {
     const RefArgs &a = da.r;
-    if (a.H / a.Hk == 4 && a.d <= 128 && a.block <= 64)
+    if (a.H / a.Hk == 4 && a.d == 128 && a.block <= 64)
         hipLaunchKernelGGL(sage_dec_scores_g4, dim3((g.x + 1) / 2, g.y, g.z), dim3(256), 0, st, da, t);
     else if (a.H / a.Hk <= 4 && a.d <= 128)
         hipLaunchKernelGGL((sage_dec_scores_g<4, 128>), g, dim3(256), 0, st, da, t);
@@ -1753,7 +1793,9 @@ static void dec_launch_scores(dim3 g, const DecArgs &da, const DecSeqTab &t, hip
 
 static void dec_launch_pv(dim3 g, const DecArgs &da, const DecSeqTab &t, hipStream_t st) {
     const RefArgs &a = da.r;
-    if (a.H / a.Hk <= 4 && a.block <= 64)
+    if (a.H / a.Hk == 4 && a.dv == 128 && a.block <= 64)
+        hipLaunchKernelGGL((sage_dec_pv_g<4, 64, true>), g, dim3(256), 0, st, da, t);
+    else if (a.H / a.Hk <= 4 && a.block <= 64)
         hipLaunchKernelGGL((sage_dec_pv_g<4, 64>), g, dim3(256), 0, st, da, t);
     else
         hipLaunchKernelGGL((sage_dec_pv_g<DEC_GMAX, DEC_KMAX>), g, dim3(256), 0, st, da, t);
