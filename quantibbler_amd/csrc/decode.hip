@@ -446,7 +446,10 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     const size_t s0 = ks * per < ns ? ks * per : ns;
     const size_t s1 = s0 + per < ns ? s0 + per : ns;
     const int col = lane & 15, g = lane >> 4;
-    const bool bcol = col < ncol;
+    // NCOL == 0, one column group a workgroup (batches 9-32): the grid's y
+    // index picks the workgroup's 16 columns (8 tokens)
+    const int c0 = NCOL == 0 && NCG == 1 ? 16 * (int)blockIdx.y : 0;
+    const bool bcol = c0 + col < ncol;
     const bool live = rg < n_rg;
     const size_t rgc = live ? rg : n_rg - 1;
     const uint32_t c7 = a.c7;
@@ -631,7 +634,8 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     #pragma unroll
                 for (int u = 0; u < Q4_U; u++)
                     if (u < (int)nsl)
-                        q4_step<NCOL>(acc[0], w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, col, bcol, c7);
+                        q4_step<NCOL>(acc[0], w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, c0 + col, bcol,
+                                      c7);
             }
             if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
         }
@@ -665,7 +669,7 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
 #pragma unroll
     for (int cg = 0; cg < NCG; cg++) {
         if (cg) __builtin_amdgcn_wave_barrier();  // the last group's transpose is read
-        q4_epilogue<STAGE>(acc[cg], (float *)wl, a, L, ncol, rg, lane, so, bi, 16 * cg);
+        q4_epilogue<STAGE>(acc[cg], (float *)wl, a, L, ncol, rg, lane, so, bi, c0 + 16 * cg);
     }
 }
 
@@ -864,10 +868,7 @@ static int q4_phase(int phase, const Q4Geom &G, const Q4Layer *tab, const uint32
 #define Q4_LAUNCH(ST, KS)                                                                             \
     if (ncol_t == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 2>), g, dim3(256), lds, s, a);       \
     else if (ncol_t == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 4>), g, dim3(256), lds, s, a);  \
-    else if (ncg == 4) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0, 4>), g, dim3(256), lds, s, a);  \
-    else if (ncg == 3) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0, 3>), g, dim3(256), lds, s, a);  \
-    else if (ncg == 2) hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0, 2>), g, dim3(256), lds, s, a);  \
-    else hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0>), g, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((q4_gemv_kernel<ST, KS, 0>), dim3(g.x, (unsigned)ncg), dim3(256), lds, s, a);
 #define Q4_LAUNCH_KS(ST)                                                                         \
     if (ksplit == 4) { Q4_LAUNCH(ST, 4) }                                                        \
     else if (ksplit == 2) { Q4_LAUNCH(ST, 2) }                                                   \

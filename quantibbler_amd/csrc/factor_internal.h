@@ -63,10 +63,11 @@ struct qbk_factor {
 
 namespace qbk {
 
-// decode.hip: the largest batch the factor linear's decode face routes to the
-// fp4 GEMV (beyond, the prefill GEMM), and the largest the GEMV serves at all
-// (the decoder block's batched decode steps use it up to there).
-constexpr size_t Q4_MAXB = 8;
+// decode.hip: the largest batch the factor linear (and the decoder block's
+// batched decode step) routes to the fp4 GEMV -- beyond it, the prefill
+// GEMM -- and the largest the GEMV serves at all.  Past 8 tokens each
+// workgroup takes one 8-token column group.
+constexpr size_t Q4_MAXB = 32;
 constexpr size_t Q4_MAXB_KERNEL = 32;
 
 // The two table entries of one layer decoded alone (offsets 0).

@@ -269,7 +269,7 @@ def test_decoder_block_validation(ctx, orc):
 @pytest.mark.parametrize("n", [5, 150])
 def test_block_prefill_then_decode(ctx, orc, n):
     """A new sequence's n tokens in one prefill pass (projections at batch n:
-    the decode GEMV for n <= 8, the GEMM beyond; causal block-scaled
+    the decode GEMV for n <= 32, the GEMM beyond; causal block-scaled
     SageAttention over the n tokens; q/k norms; cache rows 0 .. n - 1), then
     decode steps at positions n, n + 1, ... on the cache it filled: each row
     against the oracle's restatement of the same arithmetic, to the block's

@@ -120,7 +120,7 @@ def test_config3_set_decode_batch_bit_identical(ctx, orc, cfg3_layers, n):
 @pytest.mark.parametrize("group,n", [("qkv", 9), ("qkv", 32), ("qkv", 64), ("gu", 32)])
 def test_config3_shared_set_gemm_bit_identical(ctx, orc, cfg3_layers, group, n):
     """q/k/v (or gate/up) as one shared-input set on the prefill GEMM at a
-    decode batch (the decoder block's batched step beyond batch 8): one x
+    decode batch (the decoder block's batched step beyond batch 32): one x
     [n][4096] of integer-exact values, every row of every layer bit-identical
     to the oracle's composite."""
     from quantibbler_amd import FactorSet

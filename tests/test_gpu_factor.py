@@ -161,8 +161,9 @@ def gpu_t(layer, ws, batch):
     """The device's t (bf16) read back from the documented workspace layout."""
     r, rp = layer.r, -(-layer.r // 128) * 128
     rnd = lambda n: -(-n // 256) * 256
-    if batch <= 8:
-        # fp4 decode: [op1 | sc1 | op2 [slice][4][ncol][32] | sc2 [slice][4][ncol]]:
+    if batch <= 32:
+        # fp4 decode (the factor linear's route up to 32 tokens):
+        # [op1 | sc1 | op2 [slice][4][ncol][32] | sc2 [slice][4][ncol]]:
         # t is stage 2's operand, hi (column 2b) + lo (2b+1), E8M0 scales
         ns1, ns2, ncol = -(-layer.din // 128), rp // 128, 2 * batch
         o2 = rnd(ns1 * 4 * ncol * 32) + rnd(ns1 * 4 * ncol)
@@ -286,7 +287,7 @@ def test_prefill_activation_rounding_staged(ctx, orc):
     compared bit for bit with the oracle's rounding over ties, overflow to
     infinity, denormals and NaN payloads."""
     rng = np.random.default_rng(210)
-    batch, din = 16, 203
+    batch, din = 40, 203  # past the decode GEMV's 32 tokens, below the one-launch GEMM's 256
     L = _rounding_layer(orc, rng, din, r=2100)
     xb = rng.integers(0, 1 << 16, (batch, din)).astype(np.uint16)
     # every bf16 bit pattern class: NaNs with payloads, +-inf, denormals, zeros
@@ -330,7 +331,7 @@ def test_prefill_activation_rounding_fused(ctx, orc):
     overflow included; f32 x through the host face, where y must be
     bit-identical to the oracle's."""
     rng = np.random.default_rng(200)
-    batch, din = 16, 200
+    batch, din = 40, 200  # past the decode GEMV's 32 tokens, below the one-launch GEMM's 256
     L = _rounding_layer(orc, rng, din, r=2100)
     layer = upload(ctx, L)
     x, cols = _one_hot(orc, rng, L, batch, din, finite=False)

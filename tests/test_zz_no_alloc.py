@@ -1,7 +1,7 @@
 """The no-allocation factor linear (qbk_factor_linear_noalloc_dev) against
 qbk_factor_linear_dev on the same layer and inputs: bit-identical outputs on
 two calls in a row, the second with a smaller input (its scratch array keeps
-the first call's contents), for the decode GEMV (batch <= 8) and the prefill
+the first call's contents), for the decode GEMV (batch <= 32) and the prefill
 GEMM; the call captured in a HIP graph and replayed with new inputs; and
 the refusal of a call whose workspace exceeds the array."""
 import numpy as np
