@@ -283,33 +283,6 @@ __device__ __forceinline__ void q4_step(f32x4_t acc[4], const uint4 &w4u, uint32
                                                                   Q4_SCALE_A, 0, bs);
 }
 
-// Slice j against NCG column groups (batch > 8): the four row tiles' signs
-// are built once and each group's fp8 operand read from global memory (L2);
-// columns past the batch's read nothing and use a zero operand.
-template <int NCG>
-__device__ __forceinline__ void q4_step_g(f32x4_t acc[NCG][4], const uint4 &w4u, uint32_t j, const uint8_t *gb,
-                                          const uint8_t *gs, int g, int ncol, int col, uint32_t c7) {
-    const i32x8_t s0 = q4_signs(w4u.x, c7), s1 = q4_signs(w4u.y, c7), s2 = q4_signs(w4u.z, c7),
-                  s3 = q4_signs(w4u.w, c7);
-#pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        const int c = 16 * cg + col;
-        i32x8_t bv = {0, 0, 0, 0, 0, 0, 0, 0};
-        int bs = 127;
-        if (c < ncol) {
-            const size_t slot = ((size_t)j * 4 + g) * ncol + c;
-            const uint4 *bq = (const uint4 *)(gb + slot * 32);
-            const uint4 b0 = bq[0], b1 = bq[1];
-            bv = i32x8_t{(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
-            bs = gs[slot];
-        }
-        acc[cg][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s0, bv, acc[cg][0], 4, 0, 0, Q4_SCALE_A, 0, bs);
-        acc[cg][1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s1, bv, acc[cg][1], 4, 0, 0, Q4_SCALE_A, 0, bs);
-        acc[cg][2] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s2, bv, acc[cg][2], 4, 0, 0, Q4_SCALE_A, 0, bs);
-        acc[cg][3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(s3, bv, acc[cg][3], 4, 0, 0, Q4_SCALE_A, 0, bs);
-    }
-}
-
 // The maximum of v over the 32 lanes whose ids differ from this lane's only
 // in bits 0-3 and 5 (one scale block of stage 2's operand), with no LDS
 // round trip: the quad by two DPP quad permutations (l ^ 1, l ^ 2), the
@@ -425,9 +398,8 @@ static_assert(q4_wave_lds(2) >= 4 * 64 * 16, "a wave's partial sums fit its regi
 // XCD-aware 1-D grid: workgroup i runs on XCD i % 8; XCD x takes the
 // contiguous range [x*per_x, (x+1)*per_x) of the (layer, row group) work, so
 // that one layer's operand is fetched into one L2.
-template <int STAGE, int KSPLIT, int NCOL, int NCG = 1>
+template <int STAGE, int KSPLIT, int NCOL>
 __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
-    static_assert(NCG == 1 || NCOL == 0, "column groups read their operand from global memory");
     extern __shared__ __attribute__((aligned(16))) uint8_t q4_lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
@@ -448,7 +420,7 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     const int col = lane & 15, g = lane >> 4;
     // NCOL == 0, one column group a workgroup (batches 9-32): the grid's y
     // index picks the workgroup's 16 columns (8 tokens)
-    const int c0 = NCOL == 0 && NCG == 1 ? 16 * (int)blockIdx.y : 0;
+    const int c0 = NCOL == 0 ? 16 * (int)blockIdx.y : 0;
     const bool bcol = c0 + col < ncol;
     const bool live = rg < n_rg;
     const size_t rgc = live ? rg : n_rg - 1;
@@ -499,11 +471,9 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
     const size_t sdead = L.k_valid > kmin ? (L.k_valid - kmin + 127) / 128 : 0;  // first slice all past K
     const uint32_t dead_off = (uint32_t)(lane & 48);
     const bool rows_dead = rgc * 64 >= L.rows_valid;
-    f32x4_t acc[NCG][4];
+    f32x4_t acc[4];
 #pragma unroll
-    for (int cg = 0; cg < NCG; cg++)
-#pragma unroll
-        for (int rt = 0; rt < 4; rt++) acc[cg][rt] = f32x4_t{0, 0, 0, 0};
+    for (int rt = 0; rt < 4; rt++) acc[rt] = f32x4_t{0, 0, 0, 0};
     if constexpr (NCOL == 2 && KSPLIT <= 4) {
         // Batch 1, up to four waves a row group.  (At batch 2 the ring's
         // registers went to scratch, and eight waves a group needed 124 VGPRs
@@ -573,7 +543,7 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
                 // loads below the group's MFMAs)
 #pragma unroll
                 for (int u = 0; u < Q4_U; u++) {
-                    q4_slice_lds(acc[0], w4[u], wl, bo0 + rb + u * bstep, so0 + rb + u * sstep, c7);
+                    q4_slice_lds(acc, w4[u], wl, bo0 + rb + u * bstep, so0 + rb + u * sstep, c7);
                     w4[u] = sign_load(sb + Q4_U + u);
                     __builtin_amdgcn_sched_barrier(Q4_SCHED_PIN);
                 }
@@ -583,7 +553,7 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
             const uint32_t nsl = (uint32_t)(s1 - sb), rb = bcol ? (grp & 1) * RB : 0;
 #pragma unroll
             for (int u = 0; u < Q4_U; u++)
-                if (u < (int)nsl) q4_slice_lds(acc[0], w4[u], wl, bo0 + rb + u * bstep, so0 + rb + u * sstep, c7);
+                if (u < (int)nsl) q4_slice_lds(acc, w4[u], wl, bo0 + rb + u * bstep, so0 + rb + u * sstep, c7);
         }
     } else {
         for (size_t sb = s0; sb < (rows_dead ? s0 : s1); sb += Q4_U) {
@@ -625,52 +595,35 @@ __global__ void __launch_bounds__(64 * Q4_NW(KSPLIT)) q4_gemv_kernel(Q4Args a) {
             // one form for whole and partial steps (a uniform branch per slice): a
             // second, unguarded copy of the step kept its own accumulator
             // registers -- 122 VGPRs a wave against 94 at batch 1 (four waves a
-            // SIMD instead of five), 256 against 140-238 for column groups
-            if (NCG > 1) {
+            // SIMD instead of five)
     #pragma unroll
-                for (int u = 0; u < Q4_U; u++)
-                    if (u < (int)nsl) q4_step_g<NCG>(acc, w4[u], u, gbs, gss, g, ncol, col, c7);
-            } else {
-    #pragma unroll
-                for (int u = 0; u < Q4_U; u++)
-                    if (u < (int)nsl)
-                        q4_step<NCOL>(acc[0], w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, c0 + col, bcol,
-                                      c7);
-            }
+            for (int u = 0; u < Q4_U; u++)
+                if (u < (int)nsl)
+                    q4_step<NCOL>(acc, w4[u], u, wl, bo0, bstep, so0, sstep, gbs, gss, g, ncol, c0 + col, bcol, c7);
             if (NCOL > 0) __builtin_amdgcn_wave_barrier();  // the next step overwrites the region
         }
     }
     if (KSPLIT > 1) {
-        // one column group at a time through [4 tiles][64 lanes] a wave: in
-        // the wave's own region (NCOL > 0: no wave reads another's region
-        // before the barrier) or past the regions
+        // the partial sums through [4 tiles][64 lanes] a wave: in the wave's
+        // own region (NCOL > 0: no wave reads another's region before the
+        // barrier) or past the regions
         auto red = [&](int w, int rt) {
             return NCOL > 0 ? (f32x4_t *)(q4_lds + w * wreg) + rt * 64 + lane
                             : (f32x4_t *)(q4_lds + Q4_NW(KSPLIT) * wreg) + (w * 4 + rt) * 64 + lane;
         };
 #pragma unroll
-        for (int cg = 0; cg < NCG; cg++) {
-            if (cg) __syncthreads();  // the last group's sums are read
-#pragma unroll
-            for (int rt = 0; rt < 4; rt++) *red(wave, rt) = acc[cg][rt];
-            __syncthreads();
-            if (ks == 0) {
-#pragma unroll
-                for (int rt = 0; rt < 4; rt++) {
-                    f32x4_t v = *red(wave, rt);
-                    for (int q = 1; q < KSPLIT; q++) v += *red(wave + q, rt);
-                    acc[cg][rt] = v;
-                }
-            }
-        }
+        for (int rt = 0; rt < 4; rt++) *red(wave, rt) = acc[rt];
+        __syncthreads();
         if (ks != 0) return;
+#pragma unroll
+        for (int rt = 0; rt < 4; rt++) {
+            f32x4_t v = *red(wave, rt);
+            for (int q = 1; q < KSPLIT; q++) v += *red(wave + q, rt);
+            acc[rt] = v;
+        }
     }
     if (!live) return;
-#pragma unroll
-    for (int cg = 0; cg < NCG; cg++) {
-        if (cg) __builtin_amdgcn_wave_barrier();  // the last group's transpose is read
-        q4_epilogue<STAGE>(acc[cg], (float *)wl, a, L, ncol, rg, lane, so, bi, c0 + 16 * cg);
-    }
+    q4_epilogue<STAGE>(acc, (float *)wl, a, L, ncol, rg, lane, so, bi, c0);
 }
 
 // ------------------------------------------------------------------------
