@@ -176,8 +176,8 @@ __global__ void blkd_add(const float *a, const float *b, float *out, int n) {
     if (i < n) out[i] = a[i] + b[i];
 }
 
-// blkd_norm writing, in place of x, the batch-1 stage-1 operand of the layer
-// set that x feeds (nrep layers each reading x: every din == d, d a multiple
+// blkd_norm writing, in place of x, the stage-1 operand of the layer set
+// that x feeds (a workgroup per token, ncol = 2 x the batch) (nrep layers each reading x: every din == d, d a multiple
 // of 128; q4_operand.h's flat runs over nrep copies of x, the bytes
 // q4_prep_flat_kernel writes from them).  The row, the residual, w and the
 // first runs' s2 are loaded up front (one memory round trip before the
@@ -185,10 +185,16 @@ __global__ void blkd_add(const float *a, const float *b, float *out, int n) {
 #define BLKD_OP_PER 8  // row elements a thread holds: d <= 8192
 __global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm_op(const float *a, const float *r, float *hout,
                                                                  const float *w, float eps, int d, int nrep,
-                                                                 const float *s2cat, uint8_t *op, uint8_t *sc) {
+                                                                 const float *s2cat, uint8_t *op, uint8_t *sc,
+                                                                 int ncol) {
     __shared__ float red[BLKD_NORM_THREADS / 64];
     __shared__ __attribute__((aligned(16))) uint16_t xs[BLKD_NORM_THREADS * BLKD_OP_PER];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // token tok = blockIdx.x of a batch: its row, and its columns 2 tok, 2 tok + 1 of the operand's ncol
+    const int tok = (int)blockIdx.x;
+    a += (size_t)tok * d;
+    if (r) r += (size_t)tok * d;
+    if (hout) hout += (size_t)tok * d;
     const uint32_t n_runs = (uint32_t)(nrep * d / 16), rpl = (uint32_t)(d / 16);
     // a run past the end shadows one of the last slice (n_runs is a multiple
     // of 8, so its shuffle partner at lane distance 2 does too)
@@ -254,27 +260,32 @@ __global__ void __launch_bounds__(BLKD_NORM_THREADS) blkd_norm_op(const float *a
         q4_run_operand(z, hw, lw, e_hi, e_lo);
         if (tt >= n_runs) continue;
         const int rr = (int)(t & 7);
-        const size_t slot = q4_run_slot(t >> 3, rr, 2, 0), byte = 16 * (rr & 1);
+        const size_t slot = q4_run_slot(t >> 3, rr, ncol, tok), byte = 16 * (rr & 1);
         *(uint4 *)(op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
         *(uint4 *)(op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
         if ((rr & 2) == 0)
-            *(uint16_t *)(sc + q4_run_scale(t >> 3, rr, 2, 0)) = (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
+            *(uint16_t *)(sc + q4_run_scale(t >> 3, rr, ncol, tok)) = (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
     }
 }
 
-// blkd_swiglu written as the batch-1 stage-1 operand of the layer it feeds
-// (din = ffn, a multiple of 128): a thread per run of 16, hid as
-// blkd_swiglu forms it, z = bf16(s2 hid) as q4_prep_kernel's f32 path.
-__global__ void __launch_bounds__(256) blkd_swiglu_op(const float *gu, int ffn, const float *s2, uint8_t *op,
-                                                      uint8_t *sc) {
+// blkd_swiglu written as the stage-1 operand of the layer it feeds (din =
+// ffn, a multiple of 128): a thread per run of 16, hid as blkd_swiglu forms
+// it, z = bf16(s2 hid) as q4_prep_kernel's f32 path.  Token tok =
+// blockIdx.y of a batch: rows gp + tok ffn, up + tok ffn, columns 2 tok,
+// 2 tok + 1 of the operand's ncol.
+__global__ void __launch_bounds__(256) blkd_swiglu_op(const float *gp, const float *up, int ffn, const float *s2,
+                                                      uint8_t *op, uint8_t *sc, int ncol) {
     const uint32_t n_runs = (uint32_t)ffn / 16;
     const uint32_t tt = blockIdx.x * 256 + threadIdx.x;
     const uint32_t t = tt < n_runs ? tt : n_runs - 8 + (tt & 7);
+    const int tok = (int)blockIdx.y;
+    gp += (size_t)tok * ffn;
+    up += (size_t)tok * ffn;
     const size_t k0 = (size_t)t * 16;
     float z[16];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        const float4 g4 = *(const float4 *)(gu + k0 + 4 * q), u4 = *(const float4 *)(gu + ffn + k0 + 4 * q);
+        const float4 g4 = *(const float4 *)(gp + k0 + 4 * q), u4 = *(const float4 *)(up + k0 + 4 * q);
         const float4 s4 = *(const float4 *)(s2 + k0 + 4 * q);
         const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w},
                     sv[4] = {s4.x, s4.y, s4.z, s4.w};
@@ -289,11 +300,11 @@ __global__ void __launch_bounds__(256) blkd_swiglu_op(const float *gu, int ffn, 
     q4_run_operand(z, hw, lw, e_hi, e_lo);
     if (tt >= n_runs) return;
     const int rr = (int)(t & 7);
-    const size_t slot = q4_run_slot(t >> 3, rr, 2, 0), byte = 16 * (rr & 1);
+    const size_t slot = q4_run_slot(t >> 3, rr, ncol, tok), byte = 16 * (rr & 1);
     *(uint4 *)(op + slot * 32 + byte) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     *(uint4 *)(op + (slot + 1) * 32 + byte) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     if ((rr & 2) == 0)
-        *(uint16_t *)(sc + q4_run_scale(t >> 3, rr, 2, 0)) = (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
+        *(uint16_t *)(sc + q4_run_scale(t >> 3, rr, ncol, tok)) = (uint16_t)((e_hi + 127) | ((e_lo + 127) << 8));
 }
 
 // ---- prefill (n tokens at positions 0 .. n - 1) ---------------------------
@@ -851,7 +862,7 @@ static int block_decode_one(qbk_ctx *ctx, qbk_block *B, float *h, size_t pos, co
     // attention sublayer
     if (fits && q4_set_flat_operand(B->qkv, B->ws, &op, &sc, &s2c)) {
         hipLaunchKernelGGL(blkd_norm_op, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, h, (const float *)nullptr,
-                           (float *)nullptr, B->w_in, B->eps, d, 3, s2c, op, sc);
+                           (float *)nullptr, B->w_in, B->eps, d, 3, s2c, op, sc, 2);
         QBK_HIP(hipGetLastError());
         if ((rc = q4_set_run_staged(B->qkv, B->ycat, false, B->ws, s))) return rc;
     } else {
@@ -915,7 +926,7 @@ static int block_mlp_one(qbk_block *B, float *h, hipStream_t s) {
     const float *s2c;
     if (fits && q4_set_flat_operand(B->gu, B->ws, &op, &sc, &s2c)) {
         hipLaunchKernelGGL(blkd_norm_op, dim3(1), dim3(BLKD_NORM_THREADS), 0, s, B->oout, (const float *)h, B->h1,
-                           B->w_post, B->eps, d, 2, s2c, op, sc);
+                           B->w_post, B->eps, d, 2, s2c, op, sc, 2);
         QBK_HIP(hipGetLastError());
         if ((rc = q4_set_run_staged(B->gu, B->ycat, false, B->ws, s))) return rc;
     } else {
@@ -928,7 +939,7 @@ static int block_mlp_one(qbk_block *B, float *h, hipStream_t s) {
     // epilogue when it runs from a flat operand
     if (q4_flat_operand(B->down, B->ws, &op, &sc)) {
         hipLaunchKernelGGL(blkd_swiglu_op, dim3((unsigned)div_ceil((size_t)ffn / 16, 256)), dim3(256), 0, s,
-                           B->ycat, ffn, B->down->s2, op, sc);
+                           (const float *)B->ycat, (const float *)B->ycat + ffn, ffn, B->down->s2, op, sc, 2);
         QBK_HIP(hipGetLastError());
         return q4_run_staged(B->down, h, false, B->h1, B->ws, s);
     }
@@ -1172,9 +1183,22 @@ static int block_decode_batch(qbk_ctx *ctx, qbk_block *B, float *h, const size_t
     void *ws = w + P.o_gemm;
     const int d = (int)B->d, hd = (int)B->hd, H = (int)B->H, Hk = (int)B->Hk;
     const size_t nd = n * B->d, nf = n * B->ffn, kvs = B->cap * B->Hk * B->hd;
-    blkp_norm_launch(n, h, nullptr, nullptr, B->w_in, B->eps, x, d, P.sets ? 3 : 1, s);
+    // From 2 tokens on the layer-set GEMV, the norms and SwiGLU write their
+    // projections' stage-1 operands themselves (no prep launch) and the down
+    // projection's epilogue adds the residual.
+    const bool fits = P.sets && n >= 2 && d <= BLKD_NORM_THREADS * BLKD_OP_PER;
+    uint8_t *op, *sc;
+    const float *s2c;
+    const bool qkv_op = fits && q4_set_flat_operand_batch(B->qkv, n, ws, &op, &sc, &s2c);
+    if (qkv_op)
+        hipLaunchKernelGGL(blkd_norm_op, dim3((unsigned)n), dim3(BLKD_NORM_THREADS), 0, s, h, (const float *)nullptr,
+                           (float *)nullptr, B->w_in, B->eps, d, 3, s2c, op, sc, (int)(2 * n));
+    else
+        blkp_norm_launch(n, h, nullptr, nullptr, B->w_in, B->eps, x, d, P.sets ? 3 : 1, s);
     QBK_HIP(hipGetLastError());
-    if (P.sets) {
+    if (qkv_op) {
+        if ((rc = q4_set_run_batch_staged(B->qkv, n, q, false, ws, s))) return rc;
+    } else if (P.sets) {
         if ((rc = q4_set_run_batch(B->qkv, n, x, false, q, false, ws, s))) return rc;
     } else if (q4_set_gemm_fits(B->qkv, n)) {
         // q, k, v as one set on the GEMM (y [layer][n][dout]: q, then k, v)
@@ -1218,15 +1242,28 @@ static int block_decode_batch(qbk_ctx *ctx, qbk_block *B, float *h, const size_t
     for (size_t i = 0; !pos_dev && i < n; i++) B->tokens[i] = B->filled[i] = pos[i] + 1;
     if ((rc = P.sets ? q4_run(B->o, n, at, true, oo, false, ws, s) : blkp_proj(B->o, n, at, true, oo, ws, s)))
         return rc;
-    blkp_norm_launch(n, oo, h, h1, B->w_post, B->eps, x, d, P.sets ? 2 : 1, s);
+    const bool gu_op = fits && q4_set_flat_operand_batch(B->gu, n, ws, &op, &sc, &s2c);
+    if (gu_op)
+        hipLaunchKernelGGL(blkd_norm_op, dim3((unsigned)n), dim3(BLKD_NORM_THREADS), 0, s, (const float *)oo,
+                           (const float *)h, h1, B->w_post, B->eps, d, 2, s2c, op, sc, (int)(2 * n));
+    else
+        blkp_norm_launch(n, oo, h, h1, B->w_post, B->eps, x, d, P.sets ? 2 : 1, s);
     QBK_HIP(hipGetLastError());
-    if (P.sets) {
+    if (gu_op) {
+        if ((rc = q4_set_run_batch_staged(B->gu, n, g, false, ws, s))) return rc;
+    } else if (P.sets) {
         if ((rc = q4_set_run_batch(B->gu, n, x, false, g, false, ws, s))) return rc;
     } else if (q4_set_gemm_fits(B->gu, n)) {
         if ((rc = q4_set_gemm_run(B->gu, n, x, false, g, false, ws, s))) return rc;
     } else if ((rc = blkp_proj(B->lay[4], n, x, false, g, ws, s)) ||
                (rc = blkp_proj(B->lay[5], n, x, false, u, ws, s))) {
         return rc;
+    }
+    if (fits && q4_flat_operand_batch(B->down, n, ws, &op, &sc)) {
+        hipLaunchKernelGGL(blkd_swiglu_op, dim3((unsigned)div_ceil(B->ffn / 16, 256), (unsigned)n), dim3(256), 0, s,
+                           (const float *)g, (const float *)u, (int)B->ffn, B->down->s2, op, sc, (int)(2 * n));
+        QBK_HIP(hipGetLastError());
+        return q4_run_staged_batch(B->down, n, h, false, h1, ws, s);  // h = down(hid) + h1
     }
     hipLaunchKernelGGL(blkp_swiglu, dim3((unsigned)div_ceil(nf, 256)), dim3(256), 0, s, g, u, g, nf);
     QBK_HIP(hipGetLastError());

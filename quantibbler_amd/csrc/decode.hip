@@ -873,6 +873,28 @@ bool q4_flat_operand(const qbk_factor *L, void *ws, uint8_t **op, uint8_t **sc) 
     return true;
 }
 
+bool q4_flat_operand_batch(const qbk_factor *L, size_t n, void *ws, uint8_t **op, uint8_t **sc) {
+    Q4Layer tab[2];
+    Q4Geom G;
+    q4_build(&L, 1, n, L->num_cus, tab, G);
+    if (!G.din_mult128) return false;
+    *op = (uint8_t *)ws + G.o_op1;
+    *sc = (uint8_t *)ws + G.o_sc1;
+    return true;
+}
+
+int q4_run_staged_batch(const qbk_factor *L, size_t n, void *y, bool ybf16, const float *resid, void *ws,
+                        hipStream_t s) {
+    Q4Layer tab[2];
+    Q4Geom G;
+    q4_build(&L, 1, n, L->num_cus, tab, G);
+    for (int ph = 2; ph <= Q4_PHASES; ph++) {
+        int rc = q4_phase(ph, G, L->q4_tab, nullptr, nullptr, nullptr, nullptr, false, y, ybf16, ws, s, resid);
+        if (rc) return rc;
+    }
+    return QBK_OK;
+}
+
 int q4_run_staged(const qbk_factor *L, void *y, bool ybf16, const float *resid, void *ws, hipStream_t s) {
     Q4Layer tab[2];
     Q4Geom G;
@@ -990,6 +1012,27 @@ static void q4_wg_table(const Q4Layer *tab, size_t n, uint32_t n_wg, uint32_t rg
         out[2 * w] = u[w].li;
         out[2 * w + 1] = u[w].rg0;
     }
+}
+
+bool q4_set_flat_operand_batch(const qbk_factor_set *S, size_t n, void *ws, uint8_t **op, uint8_t **sc,
+                               const float **s2cat) {
+    if (!S->s2cat || !S->geom.din_mult128) return false;
+    Q4Geom G;
+    q4_set_geom(S, n, G);
+    *op = (uint8_t *)ws + G.o_op1;
+    *sc = (uint8_t *)ws + G.o_sc1;
+    *s2cat = S->s2cat;
+    return true;
+}
+
+int q4_set_run_batch_staged(const qbk_factor_set *S, size_t n, void *y, bool ybf16, void *ws, hipStream_t s) {
+    Q4Geom G;
+    q4_set_geom(S, n, G);
+    for (int ph = 2; ph <= Q4_PHASES; ph++) {
+        int rc = q4_phase(ph, G, S->tab, S->wg1, S->wg2, nullptr, nullptr, false, y, ybf16, ws, s);
+        if (rc) return rc;
+    }
+    return QBK_OK;
 }
 
 int q4_set_run_batch(const qbk_factor_set *S, size_t n, const void *x, bool xf32, void *y, bool ybf16, void *ws,

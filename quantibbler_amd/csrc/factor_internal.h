@@ -109,6 +109,14 @@ bool q4_flat_operand(const qbk_factor *L, void *ws, uint8_t **op, uint8_t **sc);
 bool q4_set_flat_operand(const qbk_factor_set *S, void *ws, uint8_t **op, uint8_t **sc, const float **s2cat);
 int q4_run_staged(const qbk_factor *L, void *y, bool ybf16, const float *resid, void *ws, hipStream_t s);
 int q4_set_run_staged(const qbk_factor_set *S, void *y, bool ybf16, void *ws, hipStream_t s);
+// The same at a batch of n <= Q4_MAXB_KERNEL tokens: the operand holds 2n
+// columns, token b's hi and lo in columns 2b, 2b + 1 (q4_run_slot's b).
+bool q4_flat_operand_batch(const qbk_factor *L, size_t n, void *ws, uint8_t **op, uint8_t **sc);
+bool q4_set_flat_operand_batch(const qbk_factor_set *S, size_t n, void *ws, uint8_t **op, uint8_t **sc,
+                               const float **s2cat);
+int q4_run_staged_batch(const qbk_factor *L, size_t n, void *y, bool ybf16, const float *resid, void *ws,
+                        hipStream_t s);
+int q4_set_run_batch_staged(const qbk_factor_set *S, size_t n, void *y, bool ybf16, void *ws, hipStream_t s);
 
 // prefill.hip: a layer set on the prefill GEMM for a decode step's batch of
 // N <= 64 tokens (layers sharing x, din % 8 == 0): the per-layer device
